@@ -1,0 +1,193 @@
+/*
+ * libmx -- an MI355X (gfx950) device for ggml's quantized MUL_MAT, MUL_MAT_ID and GET_ROWS.
+ *
+ * The C ABI below is the drop-in boundary. speech.cpp reaches these ops through ggml's backend plugin interface
+ * (ggml-backend-impl.h: ggml_backend_reg_i / ggml_backend_device_i / ggml_backend_i / ggml_backend_buffer_type_i /
+ * ggml_backend_buffer_i); each entry point names the ggml hook it serves and the speech.cpp call site that reaches that
+ * hook. Plain C types only: device pointers, sizes and a ggml-shaped tensor descriptor.
+ *
+ * Conventions
+ *  - Status codes mirror ggml_status: 0 success, -1 failed, -2 allocation failed; -3 / -4 are invalid / unsupported
+ *    arguments, which a ggml adapter reports as GGML_STATUS_FAILED (src/common/graph.cpp:13-31 maps them to the
+ *    Device and OutOfMemory faults). No entry point aborts on bad input; the message is in mx_last_error().
+ *  - Tensors follow ggml order: ne[0] is the fastest axis, nb[] are byte strides.
+ *  - Quantized tensors (Q8_0, Q4_K, Q6_K) held by this library are stored in its own device layout: each tensor's
+ *    allocation is split into planes (quants, scales, super-block scales) so every plane is 256-byte aligned and every
+ *    row of quants is contiguous. mx_tensor_set / mx_tensor_get take and return ggml's own block bytes (GGUF layout),
+ *    at any byte offset and size, so ggml and GGUF never see the device layout. Float and integer tensors are plain.
+ *  - One mx_backend is driven by one thread at a time (include/speech.h:27-30: one request per model at a time).
+ *    Work is queued on the backend's stream; results are ready after mx_backend_synchronize().
+ */
+#ifndef MX_H
+#define MX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MX_API __attribute__((visibility("default")))
+
+/* ggml_status values plus argument errors. */
+enum {
+    MX_SUCCESS = 0,
+    MX_FAILED = -1,
+    MX_ALLOC_FAILED = -2,
+    MX_INVALID = -3,
+    MX_UNSUPPORTED = -4,
+};
+
+/* ggml_type values (ggml.h enum ggml_type). */
+enum {
+    MX_TYPE_F32 = 0,
+    MX_TYPE_F16 = 1,
+    MX_TYPE_Q8_0 = 8,
+    MX_TYPE_Q8_1 = 9,
+    MX_TYPE_Q4_K = 12,
+    MX_TYPE_Q6_K = 14,
+    MX_TYPE_Q8_K = 15,
+    MX_TYPE_I32 = 26,
+};
+
+/* The ops this device computes (the ggml adapter maps GGML_OP_GET_ROWS / GGML_OP_MUL_MAT / GGML_OP_MUL_MAT_ID). */
+enum {
+    MX_OP_GET_ROWS = 1,
+    MX_OP_MUL_MAT = 2,
+    MX_OP_MUL_MAT_ID = 3,
+};
+
+/* Rounding of the activation quantizers.
+ * MX_ROUND_REF: ggml-quants.c quantize_row_q8_{0,1}_ref (d = amax/127, q = roundf(x * (1/d))). The default.
+ * MX_ROUND_X86: ggml-cpu's x86 quantize_row_q8_0 / _q8_1 (q = round-half-even(x * (127/amax))).
+ * Q8_K (the activation type of Q4_K / Q6_K weights) has a single form, quantize_row_q8_K_ref. */
+enum {
+    MX_ROUND_REF = 0,
+    MX_ROUND_X86 = 1,
+};
+
+/* A ggml tensor as the backend sees it (ggml.h struct ggml_tensor: type, ne, nb, data). `data` is a device address
+ * inside a buffer from mx_buffer_alloc (or any device memory for float / int tensors). */
+typedef struct mx_tensor {
+    int32_t type;
+    int32_t pad_;
+    int64_t ne[4];
+    uint64_t nb[4];
+    void *data;
+} mx_tensor;
+
+typedef struct mx_backend mx_backend;
+typedef struct mx_graph mx_graph;
+typedef struct mx_event mx_event;
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Device and backend: ggml_backend_reg_i.get_device_count / ggml_backend_device_i.{get_name, get_description,
+ * get_memory, init_backend} and ggml_backend_i.{free, synchronize}. Called from src/common/backend.cpp:70-120
+ * (enumeration, find_device, start_device), src/api/speech.cpp:339 and src/engines/drama3-engine.cpp:57 (memory).
+ * ------------------------------------------------------------------------------------------------------------- */
+MX_API int mx_device_count(void);
+MX_API int mx_device_description(int device, char *buf, size_t len);
+MX_API int mx_device_memory(int device, size_t *free_bytes, size_t *total_bytes);
+MX_API mx_backend *mx_backend_init(int device);
+MX_API void mx_backend_free(mx_backend *be);
+/* The hipStream_t the backend queues its work on. */
+MX_API void *mx_backend_stream(mx_backend *be);
+/* Waits for the queued work. Reports an index out of range met by GET_ROWS / MUL_MAT_ID since the last call as
+ * MX_INVALID (ggml's CPU backend asserts on it, ggml-cpu.c get_rows / mul_mat_id; this device never aborts). */
+MX_API int mx_backend_synchronize(mx_backend *be);
+/* Activation rounding used by mx_mul_mat / mx_mul_mat_id from now on (MX_ROUND_REF by default). */
+MX_API int mx_backend_set_rounding(mx_backend *be, int rounding);
+/* The last error message of the calling thread ("" if none). */
+MX_API const char *mx_last_error(void);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Buffer type and buffers: ggml_backend_buffer_type_i.{get_alignment, get_max_size, get_alloc_size, alloc_buffer} and
+ * ggml_backend_buffer_i.{get_base, free_buffer, clear, set_tensor, get_tensor, memset_tensor, cpy_tensor}.
+ * Reached from src/common/model-file.cpp:222-268 (ggml_backend_alloc_ctx_tensors, set_usage WEIGHTS, tensor_set in
+ * 16 MB pieces at increasing offsets) and src/common/qwen3-decoder.cpp:160,204,225,250,282,442.
+ * ------------------------------------------------------------------------------------------------------------- */
+MX_API size_t mx_buft_alignment(void);
+MX_API size_t mx_buft_max_size(void);
+/* Bytes the tensor takes in this device's layout (>= ggml_nbytes). */
+MX_API size_t mx_tensor_alloc_size(const mx_tensor *t);
+MX_API int mx_buffer_alloc(mx_backend *be, size_t size, void **base);
+MX_API int mx_buffer_free(mx_backend *be, void *base);
+MX_API int mx_buffer_clear(mx_backend *be, void *base, size_t size, uint8_t value);
+/* Writes `size` bytes of the tensor's ggml-layout bytes starting at byte `offset` (any offset, any size). */
+MX_API int mx_tensor_set(mx_backend *be, const mx_tensor *t, const void *host, size_t offset, size_t size);
+/* Reads ggml-layout bytes [offset, offset + size) of the tensor into host memory. */
+MX_API int mx_tensor_get(mx_backend *be, const mx_tensor *t, void *host, size_t offset, size_t size);
+/* Sets ggml-layout bytes [offset, offset + size) of the tensor to `value`. */
+MX_API int mx_tensor_memset(mx_backend *be, const mx_tensor *t, uint8_t value, size_t offset, size_t size);
+/* Copies a whole tensor between two tensors of the same type and shape held by this device. */
+MX_API int mx_tensor_copy(mx_backend *be, const mx_tensor *src, const mx_tensor *dst);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Ops: ggml_backend_device_i.supports_op and the nodes ggml_backend_i.graph_compute runs.
+ *   GET_ROWS:    src/common/qwen3-decoder.cpp:464,483,499; src/families/qwen3-tts/talker.cpp:55,63,91;
+ *                src/families/drama3/text-model.cpp:253,255
+ *   MUL_MAT:     src/common/qwen3-decoder.cpp:362-364,403,406-407,410,426; src/common/graph.h:15-19
+ *   MUL_MAT_ID:  src/common/graph.h:21-26 from src/families/drama3/text-model.cpp:198-221
+ * Shapes follow ggml exactly:
+ *   mx_get_rows(src0 [K, R, A, B] quantized, ids [n, A, B] I32) -> dst [K, n, A, B] F32
+ *   mx_mul_mat(src0 [K, N, A, B] quantized, src1 [K, M, A*r2, B*r3] F32) -> dst [N, M, A*r2, B*r3] F32
+ *   mx_mul_mat_id(as [K, N, E] quantized, b [K, 1 or k, T] F32, ids [k, T] I32) -> dst [N, k, T] F32
+ * All products accumulate each block's integer sum exactly and sum across blocks in fp32, whatever the tensor's
+ * requested precision (ggml_prec_set_acc, src/common/graph.h:10-26).
+ * ------------------------------------------------------------------------------------------------------------- */
+MX_API int mx_supports_op(int op, const mx_tensor *src0, const mx_tensor *src1, const mx_tensor *src2,
+                          const mx_tensor *dst);
+MX_API int mx_get_rows(mx_backend *be, const mx_tensor *src0, const mx_tensor *ids, const mx_tensor *dst);
+MX_API int mx_mul_mat(mx_backend *be, const mx_tensor *src0, const mx_tensor *src1, const mx_tensor *dst);
+MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids,
+                         const mx_tensor *dst);
+/* Several MUL_MAT nodes that read the same src1 (q/k/v, or gate/up) in one launch, as a backend's graph_compute
+ * may fuse them. Each dst[i] = src0[i] x src1, exactly as n separate mx_mul_mat calls compute it. */
+MX_API int mx_mul_mat_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
+                            const mx_tensor *const *dst);
+
+/* The activation quantizer the products use, exposed on its own: `nrows` rows of `k` floats (row stride
+ * `x_row_stride` bytes, device memory) to ggml blocks of `type` (MX_TYPE_Q8_0, MX_TYPE_Q8_1 or MX_TYPE_Q8_K),
+ * row after row, at `out` (device memory). ggml-cpu's src1 conversion (type_traits_cpu[vec_dot_type].from_float). */
+MX_API int mx_quantize_act(mx_backend *be, int type, int rounding, const float *x, int64_t k, int64_t nrows,
+                           size_t x_row_stride, void *out);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Replay of a fixed sequence of ops with one launch (the role CUDA graphs play inside ggml-cuda's graph_compute;
+ * the kept decode-step graph of src/common/qwen3-decoder.cpp:187-208,462-490). Between mx_graph_begin and
+ * mx_graph_end the ops are recorded, not run; mx_graph_launch replays them on the backend's stream. Record after one
+ * eager run of the same ops so every scratch buffer has its final size.
+ * ------------------------------------------------------------------------------------------------------------- */
+MX_API int mx_graph_begin(mx_backend *be);
+MX_API int mx_graph_end(mx_backend *be, mx_graph **graph);
+MX_API int mx_graph_launch(mx_backend *be, mx_graph *graph);
+MX_API void mx_graph_free(mx_graph *graph);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Events on the backend's stream: ggml_backend_device_i.{event_new, event_free, event_synchronize} and
+ * ggml_backend_i.event_record, plus the elapsed time between two recorded events (for timing on that stream).
+ * ------------------------------------------------------------------------------------------------------------- */
+MX_API mx_event *mx_event_new(mx_backend *be);
+MX_API int mx_event_record(mx_backend *be, mx_event *ev);
+MX_API int mx_event_synchronize(mx_event *ev);
+MX_API int mx_event_elapsed_ms(mx_event *start, mx_event *end, float *ms);
+MX_API void mx_event_free(mx_event *ev);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Host-side weight quantization: ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row, imatrix = NULL), the
+ * `speech quantize` path (src/common/quantize.cpp:164-182). ggml block bytes out; returns bytes written, 0 on error.
+ * ------------------------------------------------------------------------------------------------------------- */
+MX_API size_t mx_quantize_chunk(int type, const float *src, void *dst, int64_t start, int64_t nrows,
+                                int64_t n_per_row);
+/* Seeded N(mean, stddev) rows (splitmix64 -> xoshiro256** -> Box-Muller in double), row r from its own stream, and
+ * the same rows quantized straight to `type` with `nthreads` threads: synthetic weights without a float copy. */
+MX_API void mx_fill_normal_rows(uint64_t seed, int64_t row0, int64_t nrows, int64_t n_per_row, float mean,
+                                float stddev, float *out);
+MX_API size_t mx_quantize_normal_rows(int type, uint64_t seed, int64_t row0, int64_t nrows, int64_t n_per_row,
+                                      float mean, float stddev, void *dst, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

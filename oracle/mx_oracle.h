@@ -1,0 +1,94 @@
+/*
+ * CPU oracle for the quantized MUL_MAT / MUL_MAT_ID / GET_ROWS path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker: tests, the smoke check and the CPU-baseline leg of the
+ * benchmark may call it; the product (libmx) never links or calls it.
+ *
+ * It restates, in plain C, the arithmetic of ggml's CPU backend that speech.cpp routes these ops to. ggml itself is an
+ * un-vendored submodule of the reference (`.gitmodules:1-4`, fork nyosegawa/ggml branch `speech.cpp` on upstream
+ * v0.27.0 per `docs/adr/ggml-comes-from-a-fork-...-speed-ups.md:5-7`), absent from the reference tree, so each function
+ * names the ggml source it restates (ggml/src/ggml-quants.c, ggml/src/ggml-cpu/quants.c, ggml/src/ggml-cpu/ggml-cpu.c,
+ * ggml/src/ggml-common.h) and the reference call site that reaches it.
+ *
+ * Data is in ggml's own block layout (array-of-blocks, little endian), exactly as GGUF stores it.
+ */
+#ifndef MX_ORACLE_H
+#define MX_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml_type numbering (ggml.h enum ggml_type). */
+enum {
+    ORC_TYPE_F32 = 0,
+    ORC_TYPE_F16 = 1,
+    ORC_TYPE_Q8_0 = 8,
+    ORC_TYPE_Q8_1 = 9,
+    ORC_TYPE_Q4_K = 12,
+    ORC_TYPE_Q6_K = 14,
+    ORC_TYPE_Q8_K = 15,
+    ORC_TYPE_I32 = 26,
+};
+
+/* Rounding variant of the 32-block activation quantizers:
+ * ORC_ROUND_REF: quantize_row_q8_{0,1}_ref  -- id = 1/(amax/127), roundf (half away from zero).
+ * ORC_ROUND_X86: ggml-cpu x86 AVX2 quantize_row_q8_{0,1} -- id = 127/amax, round half to even. */
+enum { ORC_ROUND_REF = 0, ORC_ROUND_X86 = 1 };
+
+/* fp16 <-> fp32, IEEE binary16 round-to-nearest-even with subnormals (ggml_compute_fp32_to_fp16 semantics). */
+uint16_t orc_fp32_to_fp16(float f);
+float orc_fp16_to_fp32(uint16_t h);
+
+/* Block geometry: elements per block and bytes per block (ggml-common.h). */
+int64_t orc_blck_size(int type);
+size_t orc_type_size(int type);
+size_t orc_row_size(int type, int64_t ne);
+/* The activation type the CPU backend pairs with a weight type (type_traits_cpu[].vec_dot_type). */
+int orc_vec_dot_type(int type);
+
+/* Quantizers. */
+void orc_quantize_row_q8_0(const float *x, void *y, int64_t k, int rounding);
+void orc_quantize_row_q8_1(const float *x, void *y, int64_t k, int rounding);
+void orc_quantize_row_q8_K(const float *x, void *y, int64_t k);
+void orc_quantize_row_q4_K(const float *x, void *y, int64_t k);
+void orc_quantize_row_q6_K(const float *x, void *y, int64_t k);
+/* ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row, imatrix = NULL); returns bytes written. */
+size_t orc_quantize_chunk(int type, const float *src, void *dst, int64_t start, int64_t nrows, int64_t n_per_row);
+
+/* Dequantizers (ggml type_traits[type].to_float). */
+int orc_dequantize_row(int type, const void *x, float *y, int64_t k);
+
+/* vec_dot of one weight row (type) with one activation row in orc_vec_dot_type(type); ggml generic C order. */
+float orc_vec_dot(int type, int64_t n, const void *x, const void *y);
+/* The same dot with every per-block integer sum exact and the cross-block sum taken in double. */
+double orc_vec_dot_exact(int type, int64_t n, const void *x, const void *y);
+
+/* A ggml-shaped tensor in host memory. */
+typedef struct orc_tensor {
+    int32_t type;
+    int64_t ne[4];
+    size_t nb[4];
+    void *data;
+} orc_tensor;
+
+/* ggml_compute_forward_mul_mat: dst[i0,i1,i2,i3] = vec_dot(src0 row i0 of matrix (i2/r2, i3/r3), quant(src1 row)). */
+int orc_mul_mat(const orc_tensor *src0, const orc_tensor *src1, orc_tensor *dst, int rounding, int exact);
+/* ggml_compute_forward_mul_mat_id: dst[:, s, t] = as[ids[s,t]] . quant(b[:, s % ne11, t]). */
+int orc_mul_mat_id(const orc_tensor *as, const orc_tensor *b, const orc_tensor *ids, orc_tensor *dst, int rounding,
+                   int exact);
+/* ggml_compute_forward_get_rows: dst[:, i10, i11, i12] = dequant(src0[:, ids[i10,i11,i12], i11, i12]). */
+int orc_get_rows(const orc_tensor *src0, const orc_tensor *ids, orc_tensor *dst);
+
+/* Seeded synthetic data: splitmix64 -> xoshiro256** -> Box-Muller in double -> float. Row r of a tensor draws from
+ * its own stream seeded by (seed, r), so rows can be generated in any order or in parallel. */
+void orc_fill_normal_rows(uint64_t seed, int64_t row0, int64_t nrows, int64_t n_per_row, float mean, float stddev,
+                          float *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

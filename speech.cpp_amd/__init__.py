@@ -1,0 +1,324 @@
+"""Python binding of libmx (include/mx.h) through ctypes.
+
+libmx is the product: C++ host code and hand-written gfx950 HIP kernels behind a C ABI. This module only binds that
+ABI for the tests and the benchmark, the way a ctypes stub would bind it for any Python caller. It never computes
+anything itself: if libmx.so is missing it raises, so nothing can pass on a fallback.
+
+Tensors follow ggml order (ne[0] fastest). Device memory comes from the library's own buffers (mx_buffer_alloc).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import subprocess
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "libmx.so"
+
+# ggml_type values
+F32, F16, Q8_0, Q8_1, Q4_K, Q6_K, Q8_K, I32 = 0, 1, 8, 9, 12, 14, 15, 26
+BLCK = {F32: 1, F16: 1, I32: 1, Q8_0: 32, Q8_1: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
+TSIZE = {F32: 4, F16: 2, I32: 4, Q8_0: 34, Q8_1: 36, Q4_K: 144, Q6_K: 210, Q8_K: 292}
+OP_GET_ROWS, OP_MUL_MAT, OP_MUL_MAT_ID = 1, 2, 3
+ROUND_REF, ROUND_X86 = 0, 1
+SUCCESS, FAILED, ALLOC_FAILED, INVALID, UNSUPPORTED = 0, -1, -2, -3, -4
+
+EXPORTS = [
+    "mx_device_count", "mx_device_description", "mx_device_memory", "mx_backend_init", "mx_backend_free",
+    "mx_backend_stream", "mx_backend_synchronize", "mx_backend_set_rounding", "mx_last_error", "mx_buft_alignment",
+    "mx_buft_max_size", "mx_tensor_alloc_size", "mx_buffer_alloc", "mx_buffer_free", "mx_buffer_clear",
+    "mx_tensor_set", "mx_tensor_get", "mx_tensor_memset", "mx_tensor_copy", "mx_supports_op", "mx_get_rows",
+    "mx_mul_mat", "mx_mul_mat_id", "mx_mul_mat_group", "mx_quantize_act", "mx_graph_begin", "mx_graph_end",
+    "mx_graph_launch", "mx_graph_free", "mx_event_new", "mx_event_record", "mx_event_synchronize",
+    "mx_event_elapsed_ms", "mx_event_free", "mx_quantize_chunk", "mx_fill_normal_rows", "mx_quantize_normal_rows",
+]
+
+
+def row_size(t: int, ne0: int) -> int:
+    return ne0 // BLCK[t] * TSIZE[t]
+
+
+class MxTensor(ctypes.Structure):
+    _fields_ = [("type", ctypes.c_int32), ("pad_", ctypes.c_int32), ("ne", ctypes.c_int64 * 4),
+                ("nb", ctypes.c_uint64 * 4), ("data", ctypes.c_void_p)]
+
+
+class MxError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"libmx status {code}: {msg}")
+        self.code = code
+
+
+def build(force: bool = True) -> None:
+    """Compile libmx.so in-tree with hipcc for gfx950."""
+    args = ["make", "-s", "-j8", "-C", str(HERE)]
+    if force:
+        args.insert(2, "-B")
+    subprocess.run(args, check=True)
+
+
+_lib = None
+
+
+def lib():
+    """The loaded libmx.so; raises if it has not been built (no fallback exists)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C {HERE}` (or __graft_entry__.build())")
+    L = ctypes.CDLL(str(LIB_PATH))
+    vp, i32, i64, u64, sz, f32 = (ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_size_t,
+                                  ctypes.c_float)
+    P = ctypes.POINTER(MxTensor)
+    sig = {
+        "mx_device_count": ([], i32),
+        "mx_device_description": ([i32, ctypes.c_char_p, sz], i32),
+        "mx_device_memory": ([i32, ctypes.POINTER(sz), ctypes.POINTER(sz)], i32),
+        "mx_backend_init": ([i32], vp),
+        "mx_backend_free": ([vp], None),
+        "mx_backend_stream": ([vp], vp),
+        "mx_backend_synchronize": ([vp], i32),
+        "mx_backend_set_rounding": ([vp, i32], i32),
+        "mx_last_error": ([], ctypes.c_char_p),
+        "mx_buft_alignment": ([], sz),
+        "mx_buft_max_size": ([], sz),
+        "mx_tensor_alloc_size": ([P], sz),
+        "mx_buffer_alloc": ([vp, sz, ctypes.POINTER(vp)], i32),
+        "mx_buffer_free": ([vp, vp], i32),
+        "mx_buffer_clear": ([vp, vp, sz, ctypes.c_uint8], i32),
+        "mx_tensor_set": ([vp, P, vp, sz, sz], i32),
+        "mx_tensor_get": ([vp, P, vp, sz, sz], i32),
+        "mx_tensor_memset": ([vp, P, ctypes.c_uint8, sz, sz], i32),
+        "mx_tensor_copy": ([vp, P, P], i32),
+        "mx_supports_op": ([i32, P, P, P, P], i32),
+        "mx_get_rows": ([vp, P, P, P], i32),
+        "mx_mul_mat": ([vp, P, P, P], i32),
+        "mx_mul_mat_id": ([vp, P, P, P, P], i32),
+        "mx_mul_mat_group": ([vp, i32, ctypes.POINTER(P), P, ctypes.POINTER(P)], i32),
+        "mx_quantize_act": ([vp, i32, i32, vp, i64, i64, sz, vp], i32),
+        "mx_graph_begin": ([vp], i32),
+        "mx_graph_end": ([vp, ctypes.POINTER(vp)], i32),
+        "mx_graph_launch": ([vp, vp], i32),
+        "mx_graph_free": ([vp], None),
+        "mx_event_new": ([vp], vp),
+        "mx_event_record": ([vp, vp], i32),
+        "mx_event_synchronize": ([vp], i32),
+        "mx_event_elapsed_ms": ([vp, vp, ctypes.POINTER(f32)], i32),
+        "mx_event_free": ([vp], None),
+        "mx_quantize_chunk": ([i32, vp, vp, i64, i64, i64], sz),
+        "mx_fill_normal_rows": ([u64, i64, i64, i64, f32, f32, vp], None),
+        "mx_quantize_normal_rows": ([i32, u64, i64, i64, i64, f32, f32, vp, i32], sz),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes, fn.restype = args, res
+    _lib = L
+    return L
+
+
+def check(rc: int) -> None:
+    if rc != SUCCESS:
+        raise MxError(rc, lib().mx_last_error().decode(errors="replace"))
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+# ------------------------------------------------------------------------------------------ host-side quantization
+def quantize_chunk(t: int, x: np.ndarray) -> np.ndarray:
+    """ggml_quantize_chunk over a 2-D float32 matrix [nrows, n_per_row] (the library's host quantizer)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nrows, npr = x.shape
+    out = np.zeros((nrows, row_size(t, npr)), dtype=np.uint8)
+    n = lib().mx_quantize_chunk(t, _p(x), _p(out), 0, nrows, npr)
+    if n != out.size:
+        raise ValueError("mx_quantize_chunk failed")
+    return out
+
+
+def fill_normal(seed: int, nrows: int, n_per_row: int, mean: float = 0.0, std: float = 1.0, row0: int = 0):
+    out = np.empty((nrows, n_per_row), dtype=np.float32)
+    lib().mx_fill_normal_rows(seed & (2**64 - 1), row0, nrows, n_per_row, mean, std, _p(out))
+    return out
+
+
+def quantize_normal(t: int, seed: int, nrows: int, n_per_row: int, std: float, nthreads: int | None = None,
+                    mean: float = 0.0, row0: int = 0) -> np.ndarray:
+    out = np.empty((nrows, row_size(t, n_per_row)), dtype=np.uint8)
+    nthreads = nthreads or max(1, len(os.sched_getaffinity(0)))
+    n = lib().mx_quantize_normal_rows(t, seed & (2**64 - 1), row0, nrows, n_per_row, mean, std, _p(out), nthreads)
+    if n != out.size:
+        raise ValueError("mx_quantize_normal_rows failed")
+    return out
+
+
+# ------------------------------------------------------------------------------------------------------ device side
+def contiguous_nb(t: int, ne) -> tuple:
+    nb0 = TSIZE[t]
+    nb1 = row_size(t, ne[0])
+    nb2 = nb1 * ne[1]
+    nb3 = nb2 * ne[2]
+    return (nb0, nb1, nb2, nb3)
+
+
+class Tensor:
+    """A ggml-shaped tensor in a buffer of its own on the device."""
+
+    def __init__(self, be: "Backend", t: int, ne, nb=None):
+        ne = tuple(int(v) for v in ne) + (1,) * (4 - len(ne))
+        self.be = be
+        self.type = t
+        self.ne = ne
+        self.desc = MxTensor()
+        self.desc.type = t
+        for i in range(4):
+            self.desc.ne[i] = ne[i]
+        nb = nb or contiguous_nb(t, ne)
+        for i in range(4):
+            self.desc.nb[i] = nb[i]
+        self.size = int(lib().mx_tensor_alloc_size(ctypes.byref(self.desc)))
+        base = ctypes.c_void_p()
+        check(lib().mx_buffer_alloc(be.h, max(self.size, 256), ctypes.byref(base)))
+        self.base = base.value
+        self.desc.data = self.base
+        self.nbytes = row_size(t, ne[0]) * ne[1] * ne[2] * ne[3]
+
+    def ref(self):
+        return ctypes.byref(self.desc)
+
+    def set(self, data: np.ndarray, offset: int = 0) -> "Tensor":
+        data = np.ascontiguousarray(data)
+        check(lib().mx_tensor_set(self.be.h, self.ref(), _p(data), offset, data.nbytes))
+        return self
+
+    def get_bytes(self, offset: int = 0, size: int | None = None) -> np.ndarray:
+        size = self.nbytes - offset if size is None else size
+        out = np.empty(size, dtype=np.uint8)
+        check(lib().mx_tensor_get(self.be.h, self.ref(), _p(out), offset, size))
+        return out
+
+    def numpy(self) -> np.ndarray:
+        """Contents in ggml order, shaped [ne3, ne2, ne1, ne0] (f32 / i32) or [.., row bytes] (quantized)."""
+        b = self.get_bytes()
+        shape = (self.ne[3], self.ne[2], self.ne[1])
+        if self.type == F32:
+            return b.view(np.float32).reshape(shape + (self.ne[0],))
+        if self.type == I32:
+            return b.view(np.int32).reshape(shape + (self.ne[0],))
+        return b.reshape(shape + (row_size(self.type, self.ne[0]),))
+
+    def free(self) -> None:
+        if self.base:
+            check(lib().mx_buffer_free(self.be.h, self.base))
+            self.base = None
+
+    def __del__(self):
+        try:
+            if self.base and self.be.h:
+                lib().mx_buffer_free(self.be.h, self.base)
+        except Exception:
+            pass
+
+
+class Backend:
+    """One device backend: a HIP stream, scratch and an error word (ggml_backend_t)."""
+
+    def __init__(self, device: int = 0):
+        L = lib()
+        self.h = L.mx_backend_init(device)
+        if not self.h:
+            raise MxError(FAILED, L.mx_last_error().decode())
+        self.device = device
+
+    def close(self) -> None:
+        if self.h:
+            lib().mx_backend_free(self.h)
+            self.h = None
+
+    def tensor(self, t: int, ne, data: np.ndarray | None = None) -> Tensor:
+        T = Tensor(self, t, ne)
+        if data is not None:
+            T.set(data)
+        return T
+
+    def sync(self) -> None:
+        check(lib().mx_backend_synchronize(self.h))
+
+    def set_rounding(self, r: int) -> None:
+        check(lib().mx_backend_set_rounding(self.h, r))
+
+    def get_rows(self, src0: Tensor, ids: Tensor, dst: Tensor) -> None:
+        check(lib().mx_get_rows(self.h, src0.ref(), ids.ref(), dst.ref()))
+
+    def mul_mat(self, src0: Tensor, src1: Tensor, dst: Tensor) -> None:
+        check(lib().mx_mul_mat(self.h, src0.ref(), src1.ref(), dst.ref()))
+
+    def mul_mat_group(self, src0s, src1: Tensor, dsts) -> None:
+        P = ctypes.POINTER(MxTensor)
+        a = (P * len(src0s))(*[ctypes.pointer(s.desc) for s in src0s])
+        d = (P * len(dsts))(*[ctypes.pointer(s.desc) for s in dsts])
+        check(lib().mx_mul_mat_group(self.h, len(src0s), a, src1.ref(), d))
+
+    def mul_mat_id(self, as_: Tensor, b: Tensor, ids: Tensor, dst: Tensor) -> None:
+        check(lib().mx_mul_mat_id(self.h, as_.ref(), b.ref(), ids.ref(), dst.ref()))
+
+    def quantize_act(self, t: int, rounding: int, x: Tensor, k: int, nrows: int) -> Tensor:
+        out = Tensor(self, F32, (row_size(t, k) * nrows // 4 + 1,))
+        check(lib().mx_quantize_act(self.h, t, rounding, ctypes.c_void_p(x.base), k, nrows, x.desc.nb[1],
+                                    ctypes.c_void_p(out.base)))
+        return out
+
+    def supports(self, op: int, src0: Tensor, src1: Tensor | None, src2: Tensor | None, dst: Tensor) -> bool:
+        r = lambda t: t.ref() if t is not None else None  # noqa: E731
+        return bool(lib().mx_supports_op(op, r(src0), r(src1), r(src2), r(dst)))
+
+    # graphs and events
+    def graph_begin(self) -> None:
+        check(lib().mx_graph_begin(self.h))
+
+    def graph_end(self):
+        g = ctypes.c_void_p()
+        check(lib().mx_graph_end(self.h, ctypes.byref(g)))
+        return g.value
+
+    def graph_launch(self, g) -> None:
+        check(lib().mx_graph_launch(self.h, ctypes.c_void_p(g)))
+
+    def graph_free(self, g) -> None:
+        lib().mx_graph_free(ctypes.c_void_p(g))
+
+    def event(self):
+        e = lib().mx_event_new(self.h)
+        if not e:
+            raise MxError(FAILED, lib().mx_last_error().decode())
+        return e
+
+    def record(self, e) -> None:
+        check(lib().mx_event_record(self.h, ctypes.c_void_p(e)))
+
+    @staticmethod
+    def elapsed_ms(e0, e1) -> float:
+        check(lib().mx_event_synchronize(ctypes.c_void_p(e1)))
+        ms = ctypes.c_float()
+        check(lib().mx_event_elapsed_ms(ctypes.c_void_p(e0), ctypes.c_void_p(e1), ctypes.byref(ms)))
+        return float(ms.value)
+
+    @staticmethod
+    def event_free(e) -> None:
+        lib().mx_event_free(ctypes.c_void_p(e))
+
+
+def device_count() -> int:
+    return int(lib().mx_device_count())
+
+
+def device_description(device: int = 0) -> str:
+    buf = ctypes.create_string_buffer(256)
+    check(lib().mx_device_description(device, buf, 256))
+    return buf.value.decode()

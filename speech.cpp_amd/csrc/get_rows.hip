@@ -1,0 +1,90 @@
+// GET_ROWS: dst[:, i10, i11, i12] = dequantize(src0[:, ids[i10, i11, i12], i11, i12]) from the planar layout, the
+// arithmetic of ggml-quants.c dequantize_row_{q8_0,q4_K,q6_K} (bit-exact: the same fp32 products in the same order,
+// with no product fused into a subtraction).
+#include "mx_common.h"
+#include "mx_device.h"
+
+namespace mx {
+
+// One workgroup per output row, four consecutive elements per thread and step.
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_get_rows(GetRowsArgs a) {
+    const int64_t i = blockIdx.x;  // flat (i10, i11, i12)
+    const int64_t i10 = i % a.n_ids0;
+    const int64_t i11 = (i / a.n_ids0) % a.n_ids1;
+    const int64_t i12 = i / (a.n_ids0 * a.n_ids1);
+    const int32_t r = *(const int32_t *)((const uint8_t *)a.ids + i10 * a.ids_nb0 + i11 * a.ids_nb1 + i12 * a.ids_nb2);
+    float *y = (float *)((uint8_t *)a.dst + i10 * a.dst_nb1 + i11 * a.dst_nb2 + i12 * a.dst_nb3);
+    if (r < 0 || r >= a.R) {
+        // ggml's CPU backend asserts here; this device records the error for mx_backend_synchronize and writes zeros.
+        if (threadIdx.x == 0) atomicOr(a.err, 1);
+        for (int64_t e = 4 * threadIdx.x; e < a.K; e += 1024) *(float4 *)(y + e) = make_float4(0.f, 0.f, 0.f, 0.f);
+        return;
+    }
+    const int64_t row = (int64_t)r + i11 * a.src_mat_rows1 + i12 * a.src_mat_rows2;
+    const int64_t K = a.K;
+    for (int64_t e = 4 * threadIdx.x; e < K; e += 1024) {
+        float o[4];
+        if (TYPE == MX_TYPE_Q8_0) {
+            const int q4 = *(const int *)(a.w.p0 + row * K + e);
+            const float d = h2f(*(const uint16_t *)(a.w.p1 + (row * (K / 32) + e / 32) * 2));
+#pragma unroll
+            for (int j = 0; j < 4; j++) o[j] = (float)(int8_t)(q4 >> (8 * j)) * d;
+        } else if (TYPE == MX_TYPE_Q4_K) {
+            const int64_t sb = row * (K / 256) + e / 256;
+            const int ie = (int)(e % 256);          // element within the super-block
+            const int sub = ie / 32;                // sub-block 0..7
+            const int byte = (ie / 64) * 32 + ie % 32;
+            const uint32_t q4 = *(const uint32_t *)(a.w.p0 + sb * 128 + byte);
+            const uint8_t *s = a.w.p1 + sb * 12;
+            uint8_t sc, m;
+            if (sub < 4) {
+                sc = s[sub] & 63;
+                m = s[sub + 4] & 63;
+            } else {
+                sc = (uint8_t)((s[sub + 4] & 0xF) | ((s[sub - 4] >> 6) << 4));
+                m = (uint8_t)((s[sub + 4] >> 4) | ((s[sub] >> 6) << 4));
+            }
+            const uint32_t dm = *(const uint32_t *)(a.w.p2 + sb * 4);
+            const float d1 = h2f((uint16_t)(dm & 0xFFFF)) * sc;
+            const float m1 = h2f((uint16_t)(dm >> 16)) * m;
+            const int shift = (ie % 64) < 32 ? 0 : 4;
+            {
+#pragma clang fp contract(off)
+#pragma unroll
+                for (int j = 0; j < 4; j++) o[j] = d1 * (float)((q4 >> (8 * j + shift)) & 0xF) - m1;
+            }
+        } else {
+            const int64_t sb = row * (K / 256) + e / 256;
+            const int ie = (int)(e % 256);
+            const int half = ie / 128, quarter = (ie % 128) / 32, l = ie % 32;
+            const uint32_t ql = *(const uint32_t *)(a.w.p0 + sb * 128 + half * 64 + (quarter & 1) * 32 + l);
+            const uint32_t qh = *(const uint32_t *)(a.w.p1 + sb * 64 + half * 32 + l);
+            const float d = h2f(*(const uint16_t *)(a.w.p3 + sb * 2));
+            const float dsc = d * (float)(int8_t)a.w.p2[sb * 16 + ie / 16];
+            const int lshift = quarter < 2 ? 0 : 4;
+            const int hshift = 2 * quarter;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int q = (int)(((ql >> (8 * j + lshift)) & 0xF) | (((qh >> (8 * j + hshift)) & 3) << 4)) - 32;
+                o[j] = dsc * (float)q;
+            }
+        }
+        *(float4 *)(y + e) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+hipError_t launch_get_rows(const GetRowsArgs &a, hipStream_t s) {
+    const int64_t n = a.n_ids0 * a.n_ids1 * a.n_ids2;
+    if (n == 0) return hipSuccess;
+    dim3 grid((unsigned)n);
+    switch (a.type) {
+        case MX_TYPE_Q8_0: hipLaunchKernelGGL(k_get_rows<MX_TYPE_Q8_0>, grid, dim3(256), 0, s, a); break;
+        case MX_TYPE_Q4_K: hipLaunchKernelGGL(k_get_rows<MX_TYPE_Q4_K>, grid, dim3(256), 0, s, a); break;
+        case MX_TYPE_Q6_K: hipLaunchKernelGGL(k_get_rows<MX_TYPE_Q6_K>, grid, dim3(256), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace mx

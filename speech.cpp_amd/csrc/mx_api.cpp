@@ -1,0 +1,641 @@
+// libmx C ABI: device, backend, buffers and the three ops. See include/mx.h for the contract of each entry point.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "mx_common.h"
+#include "mx_dot.h"
+
+struct mx_backend {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int rounding = MX_ROUND_REF;
+    int *err = nullptr;              // device word: bit 0 GET_ROWS index out of range, bit 1 MUL_MAT_ID expert out of range
+    void *scratch = nullptr;         // grows on demand outside graph capture
+    size_t scratch_size = 0;
+    uint8_t *staging = nullptr;      // device staging for ggml-layout uploads and downloads
+    size_t staging_size = 0;
+    bool capturing = false;
+};
+
+struct mx_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+struct mx_event {
+    int device = 0;
+    hipEvent_t ev = nullptr;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(e == hipErrorOutOfMemory ? MX_ALLOC_FAILED : MX_FAILED, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_OK(expr, what)                          \
+    do {                                            \
+        hipError_t e_ = (expr);                     \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+constexpr size_t kStagingPiece = 64ull << 20;  // bytes per upload / download piece
+constexpr size_t kMaxLds = 64 * 1024;         // LDS a product kernel may ask for
+
+int64_t blck(int type) {
+    switch (type) {
+        case MX_TYPE_Q8_0: case MX_TYPE_Q8_1: return 32;
+        case MX_TYPE_Q4_K: case MX_TYPE_Q6_K: case MX_TYPE_Q8_K: return 256;
+        case MX_TYPE_F32: case MX_TYPE_F16: case MX_TYPE_I32: return 1;
+        default: return 0;
+    }
+}
+size_t tsize(int type) {
+    switch (type) {
+        case MX_TYPE_F32: case MX_TYPE_I32: return 4;
+        case MX_TYPE_F16: return 2;
+        case MX_TYPE_Q8_0: return 34;
+        case MX_TYPE_Q8_1: return 36;
+        case MX_TYPE_Q4_K: return 144;
+        case MX_TYPE_Q6_K: return 210;
+        case MX_TYPE_Q8_K: return 292;
+        default: return 0;
+    }
+}
+
+int64_t nelements(const mx_tensor *t) { return t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3]; }
+
+// ggml_nbytes
+size_t nbytes(const mx_tensor *t) {
+    if (nelements(t) == 0) return 0;
+    const int64_t b = blck(t->type);
+    size_t n = b == 1 ? tsize(t->type) : (size_t)(t->ne[0] / b) * t->nb[0];
+    if (b == 1) {
+        for (int i = 0; i < 4; i++) n += (size_t)(t->ne[i] - 1) * t->nb[i];
+    } else {
+        for (int i = 1; i < 4; i++) n += (size_t)(t->ne[i] - 1) * t->nb[i];
+    }
+    return n;
+}
+
+bool contiguous(const mx_tensor *t) {
+    const int64_t b = blck(t->type);
+    if (b == 0 || t->ne[0] % b != 0) return false;
+    if (t->nb[0] != tsize(t->type)) return false;
+    const uint64_t row = (uint64_t)(t->ne[0] / b) * tsize(t->type);
+    return t->nb[1] == row && t->nb[2] == row * (uint64_t)t->ne[1] && t->nb[3] == t->nb[2] * (uint64_t)t->ne[2];
+}
+
+bool shape_ok(const mx_tensor *t) {
+    for (int i = 0; i < 4; i++)
+        if (t->ne[i] < 0) return false;
+    return true;
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// A quantized weight this device computes from: Q8_0 / Q4_K / Q6_K, whole blocks, contiguous (the planar layout is a
+// function of type and shape only).
+bool weight_ok(const mx_tensor *w) {
+    return w && mx::is_quantized(w->type) && shape_ok(w) && contiguous(w) && w->data && nelements(w) > 0;
+}
+
+// F32 activations read with 16-byte loads: contiguous rows, 16-byte aligned rows and slices.
+bool f32_rows_ok(const mx_tensor *x) {
+    return x && x->type == MX_TYPE_F32 && shape_ok(x) && x->nb[0] == 4 && x->nb[1] % 16 == 0 && x->nb[2] % 16 == 0 &&
+           x->nb[3] % 16 == 0 && aligned16(x->data) && x->ne[0] % 4 == 0;
+}
+
+int check_be(mx_backend *be) {
+    if (!be) return fail(MX_INVALID, "null backend");
+    if (hipSetDevice(be->device) != hipSuccess) return fail(MX_FAILED, "cannot select device %d", be->device);
+    return MX_SUCCESS;
+}
+
+int ensure_scratch(mx_backend *be, size_t bytes) {
+    if (bytes <= be->scratch_size) return MX_SUCCESS;
+    if (be->capturing)
+        return fail(MX_FAILED, "an op needs %zu bytes of scratch while a graph is recorded; run it once before recording",
+                    bytes);
+    HIP_OK(hipStreamSynchronize(be->stream), "synchronize before growing scratch");
+    if (be->scratch) HIP_OK(hipFree(be->scratch), "free scratch");
+    be->scratch = nullptr;
+    be->scratch_size = 0;
+    const size_t size = std::max<size_t>(mx::align_up(bytes + bytes / 2, 1 << 20), 1 << 20);
+    HIP_OK(hipMalloc(&be->scratch, size), "allocate scratch");
+    be->scratch_size = size;
+    return MX_SUCCESS;
+}
+
+int ensure_staging(mx_backend *be) {
+    if (be->staging) return MX_SUCCESS;
+    HIP_OK(hipMalloc(&be->staging, kStagingPiece), "allocate staging");
+    be->staging_size = kStagingPiece;
+    return MX_SUCCESS;
+}
+
+int no_capture(mx_backend *be, const char *what) {
+    if (be->capturing) return fail(MX_FAILED, "%s cannot be recorded in a graph", what);
+    return MX_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+MX_API const char *mx_last_error(void) { return g_error.c_str(); }
+
+MX_API int mx_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+MX_API int mx_device_description(int device, char *buf, size_t len) {
+    hipDeviceProp_t p;
+    HIP_OK(hipGetDeviceProperties(&p, device), "device properties");
+    if (buf && len) snprintf(buf, len, "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    return MX_SUCCESS;
+}
+
+MX_API int mx_device_memory(int device, size_t *free_bytes, size_t *total_bytes) {
+    HIP_OK(hipSetDevice(device), "select device");
+    size_t f = 0, t = 0;
+    HIP_OK(hipMemGetInfo(&f, &t), "memory info");
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return MX_SUCCESS;
+}
+
+MX_API mx_backend *mx_backend_init(int device) {
+    if (device < 0 || device >= mx_device_count()) {
+        fail(MX_INVALID, "no device %d", device);
+        return nullptr;
+    }
+    if (hipSetDevice(device) != hipSuccess) {
+        fail(MX_FAILED, "cannot select device %d", device);
+        return nullptr;
+    }
+    mx_backend *be = new mx_backend();
+    be->device = device;
+    if (hipStreamCreateWithFlags(&be->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipMalloc(&be->err, 256) != hipSuccess || hipMemset(be->err, 0, 256) != hipSuccess) {
+        fail(MX_FAILED, "cannot create the backend of device %d", device);
+        mx_backend_free(be);
+        return nullptr;
+    }
+    return be;
+}
+
+MX_API void mx_backend_free(mx_backend *be) {
+    if (!be) return;
+    // Teardown: errors here have no one to report to.
+    (void)hipSetDevice(be->device);
+    if (be->stream) (void)hipStreamSynchronize(be->stream);
+    if (be->scratch) (void)hipFree(be->scratch);
+    if (be->staging) (void)hipFree(be->staging);
+    if (be->err) (void)hipFree(be->err);
+    if (be->stream) (void)hipStreamDestroy(be->stream);
+    delete be;
+}
+
+MX_API void *mx_backend_stream(mx_backend *be) { return be ? (void *)be->stream : nullptr; }
+
+MX_API int mx_backend_set_rounding(mx_backend *be, int rounding) {
+    if (!be) return fail(MX_INVALID, "null backend");
+    if (rounding != MX_ROUND_REF && rounding != MX_ROUND_X86) return fail(MX_INVALID, "unknown rounding %d", rounding);
+    be->rounding = rounding;
+    return MX_SUCCESS;
+}
+
+MX_API int mx_backend_synchronize(mx_backend *be) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if ((rc = no_capture(be, "synchronize"))) return rc;
+    HIP_OK(hipStreamSynchronize(be->stream), "synchronize");
+    int flag = 0;
+    HIP_OK(hipMemcpy(&flag, be->err, sizeof flag, hipMemcpyDeviceToHost), "read error word");
+    if (flag) {
+        const int zero = 0;
+        HIP_OK(hipMemcpy(be->err, &zero, sizeof zero, hipMemcpyHostToDevice), "clear error word");
+        return fail(MX_INVALID, "%s%s", (flag & 1) ? "GET_ROWS met a row index out of range; its rows are zero. " : "",
+                    (flag & 2) ? "MUL_MAT_ID met an expert index out of range; its pairs were skipped." : "");
+    }
+    return MX_SUCCESS;
+}
+
+// ------------------------------------------------------------------------------------------------------ buffers
+MX_API size_t mx_buft_alignment(void) { return mx::PLANE_ALIGN; }
+MX_API size_t mx_buft_max_size(void) { return SIZE_MAX; }
+
+MX_API size_t mx_tensor_alloc_size(const mx_tensor *t) {
+    if (!t || !shape_ok(t)) return 0;
+    if (mx::is_quantized(t->type)) return mx::planes_of(t->type, nelements(t)).total;
+    return nbytes(t);
+}
+
+MX_API int mx_buffer_alloc(mx_backend *be, size_t size, void **base) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!base) return fail(MX_INVALID, "null base pointer");
+    *base = nullptr;
+    HIP_OK(hipMalloc(base, std::max<size_t>(size, 1)), "allocate buffer");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_buffer_free(mx_backend *be, void *base) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!base) return MX_SUCCESS;
+    HIP_OK(hipStreamSynchronize(be->stream), "synchronize before free");
+    HIP_OK(hipFree(base), "free buffer");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_buffer_clear(mx_backend *be, void *base, size_t size, uint8_t value) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if ((rc = no_capture(be, "buffer clear"))) return rc;
+    HIP_OK(hipMemsetAsync(base, value, size, be->stream), "clear buffer");
+    HIP_OK(hipStreamSynchronize(be->stream), "synchronize clear");
+    return MX_SUCCESS;
+}
+
+static int tensor_range_ok(const mx_tensor *t, size_t offset, size_t size) {
+    if (!t || !t->data || !shape_ok(t)) return fail(MX_INVALID, "invalid tensor");
+    if (mx::is_quantized(t->type) && !contiguous(t)) return fail(MX_UNSUPPORTED, "quantized tensors must be contiguous");
+    const size_t n = nbytes(t);
+    if (offset > n || size > n - offset) return fail(MX_INVALID, "bytes [%zu, %zu) lie outside the tensor's %zu", offset,
+                                                     offset + size, n);
+    return MX_SUCCESS;
+}
+
+MX_API int mx_tensor_set(mx_backend *be, const mx_tensor *t, const void *host, size_t offset, size_t size) {
+    int rc = check_be(be);
+    if (rc || (rc = no_capture(be, "tensor_set")) || (rc = tensor_range_ok(t, offset, size))) return rc;
+    if (size == 0) return MX_SUCCESS;
+    if (!host) return fail(MX_INVALID, "null host pointer");
+    if (!mx::is_quantized(t->type)) {
+        HIP_OK(hipMemcpyAsync((uint8_t *)t->data + offset, host, size, hipMemcpyHostToDevice, be->stream), "upload");
+        HIP_OK(hipStreamSynchronize(be->stream), "synchronize upload");
+        return MX_SUCCESS;
+    }
+    if ((rc = ensure_staging(be))) return rc;
+    const mx::Planes pl = mx::planes_of(t->type, nelements(t));
+    const mx::SegMap map = mx::segmap_of(t->type, pl);
+    for (size_t done = 0; done < size;) {
+        const size_t piece = std::min(size - done, be->staging_size);
+        HIP_OK(hipMemcpyAsync(be->staging, (const uint8_t *)host + done, piece, hipMemcpyHostToDevice, be->stream),
+               "upload piece");
+        HIP_OK(mx::launch_scatter(map, (uint8_t *)t->data, be->staging, offset + done, piece, be->stream), "scatter");
+        done += piece;
+    }
+    HIP_OK(hipStreamSynchronize(be->stream), "synchronize upload");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_tensor_get(mx_backend *be, const mx_tensor *t, void *host, size_t offset, size_t size) {
+    int rc = check_be(be);
+    if (rc || (rc = no_capture(be, "tensor_get")) || (rc = tensor_range_ok(t, offset, size))) return rc;
+    if (size == 0) return MX_SUCCESS;
+    if (!host) return fail(MX_INVALID, "null host pointer");
+    if (!mx::is_quantized(t->type)) {
+        HIP_OK(hipMemcpyAsync(host, (const uint8_t *)t->data + offset, size, hipMemcpyDeviceToHost, be->stream),
+               "download");
+        HIP_OK(hipStreamSynchronize(be->stream), "synchronize download");
+        return MX_SUCCESS;
+    }
+    if ((rc = ensure_staging(be))) return rc;
+    const mx::Planes pl = mx::planes_of(t->type, nelements(t));
+    const mx::SegMap map = mx::segmap_of(t->type, pl);
+    for (size_t done = 0; done < size;) {
+        const size_t piece = std::min(size - done, be->staging_size);
+        HIP_OK(mx::launch_gather(map, (const uint8_t *)t->data, be->staging, offset + done, piece, be->stream), "gather");
+        HIP_OK(hipMemcpyAsync((uint8_t *)host + done, be->staging, piece, hipMemcpyDeviceToHost, be->stream),
+               "download piece");
+        HIP_OK(hipStreamSynchronize(be->stream), "synchronize download");
+        done += piece;
+    }
+    return MX_SUCCESS;
+}
+
+MX_API int mx_tensor_memset(mx_backend *be, const mx_tensor *t, uint8_t value, size_t offset, size_t size) {
+    int rc = check_be(be);
+    if (rc || (rc = no_capture(be, "tensor_memset")) || (rc = tensor_range_ok(t, offset, size))) return rc;
+    if (size == 0) return MX_SUCCESS;
+    if (!mx::is_quantized(t->type)) {
+        HIP_OK(hipMemsetAsync((uint8_t *)t->data + offset, value, size, be->stream), "memset");
+    } else {
+        const mx::Planes pl = mx::planes_of(t->type, nelements(t));
+        const mx::SegMap map = mx::segmap_of(t->type, pl);
+        for (size_t done = 0; done < size;) {
+            const size_t piece = std::min<size_t>(size - done, 1ull << 30);
+            HIP_OK(mx::launch_fill(map, (uint8_t *)t->data, value, offset + done, piece, be->stream), "fill");
+            done += piece;
+        }
+    }
+    HIP_OK(hipStreamSynchronize(be->stream), "synchronize memset");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_tensor_copy(mx_backend *be, const mx_tensor *src, const mx_tensor *dst) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!src || !dst || !src->data || !dst->data) return fail(MX_INVALID, "invalid tensor");
+    if (src->type != dst->type || nelements(src) != nelements(dst)) return fail(MX_INVALID, "tensors differ");
+    if (mx::is_quantized(src->type) && (!contiguous(src) || !contiguous(dst)))
+        return fail(MX_UNSUPPORTED, "quantized tensors must be contiguous");
+    const size_t n = mx::is_quantized(src->type) ? mx::planes_of(src->type, nelements(src)).total : nbytes(src);
+    if (!mx::is_quantized(src->type) && (!contiguous(src) || !contiguous(dst)))
+        return fail(MX_UNSUPPORTED, "only contiguous copies");
+    HIP_OK(hipMemcpyAsync(dst->data, src->data, n, hipMemcpyDeviceToDevice, be->stream), "copy tensor");
+    return MX_SUCCESS;
+}
+
+// ---------------------------------------------------------------------------------------------------------- ops
+MX_API int mx_supports_op(int op, const mx_tensor *src0, const mx_tensor *src1, const mx_tensor *src2,
+                          const mx_tensor *dst) {
+    if (!weight_ok(src0) || !dst || dst->type != MX_TYPE_F32 || !shape_ok(dst) || dst->nb[0] != 4) return 0;
+    const int64_t K = src0->ne[0];
+    switch (op) {
+        case MX_OP_GET_ROWS: {
+            const mx_tensor *ids = src1;
+            if (!ids || ids->type != MX_TYPE_I32 || !shape_ok(ids) || ids->ne[3] != 1) return 0;
+            if (src0->ne[2] != ids->ne[1] || src0->ne[3] != ids->ne[2]) return 0;
+            if (dst->ne[0] != K || dst->ne[1] != ids->ne[0] || dst->ne[2] != ids->ne[1] || dst->ne[3] != ids->ne[2]) return 0;
+            return aligned16(dst->data) && dst->nb[1] % 16 == 0 && dst->nb[2] % 16 == 0 && dst->nb[3] % 16 == 0;
+        }
+        case MX_OP_MUL_MAT: {
+            if (!f32_rows_ok(src1) || src1->ne[0] != K) return 0;
+            if (src0->ne[2] == 0 || src0->ne[3] == 0) return 0;
+            if (src1->ne[2] % src0->ne[2] != 0 || src1->ne[3] % src0->ne[3] != 0) return 0;
+            if (dst->ne[0] != src0->ne[1] || dst->ne[1] != src1->ne[1] || dst->ne[2] != src1->ne[2] ||
+                dst->ne[3] != src1->ne[3])
+                return 0;
+            return mx::act_lds_bytes(src0->type, K, 1) <= kMaxLds;
+        }
+        case MX_OP_MUL_MAT_ID: {
+            const mx_tensor *b = src1, *ids = src2;
+            if (!f32_rows_ok(b) || !ids || ids->type != MX_TYPE_I32 || !shape_ok(ids)) return 0;
+            if (src0->ne[3] != 1 || b->ne[0] != K || b->ne[3] != 1 || ids->ne[2] != 1 || ids->ne[3] != 1) return 0;
+            const int64_t n_ids = ids->ne[0], T = ids->ne[1];
+            if (b->ne[2] != T || (b->ne[1] != 1 && b->ne[1] != n_ids)) return 0;
+            if (dst->ne[0] != src0->ne[1] || dst->ne[1] != n_ids || dst->ne[2] != T || dst->ne[3] != 1) return 0;
+            if (src0->ne[2] > 65536) return 0;
+            return mx::act_lds_bytes(src0->type, K, mx::MAX_COLS) <= kMaxLds;
+        }
+        default: return 0;
+    }
+}
+
+MX_API int mx_get_rows(mx_backend *be, const mx_tensor *src0, const mx_tensor *ids, const mx_tensor *dst) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!mx_supports_op(MX_OP_GET_ROWS, src0, ids, nullptr, dst))
+        return fail(MX_UNSUPPORTED, "GET_ROWS: unsupported types, shapes or strides");
+    const mx::Planes pl = mx::planes_of(src0->type, nelements(src0));
+    mx::GetRowsArgs a{};
+    a.type = src0->type;
+    a.w = mx::wplanes(src0->data, pl);
+    a.K = src0->ne[0];
+    a.R = src0->ne[1];
+    a.n_ids0 = ids->ne[0];
+    a.n_ids1 = ids->ne[1];
+    a.n_ids2 = ids->ne[2];
+    a.src_mat_rows1 = src0->ne[1];
+    a.src_mat_rows2 = src0->ne[1] * src0->ne[2];
+    a.ids = (const int32_t *)ids->data;
+    a.ids_nb0 = (int64_t)ids->nb[0];
+    a.ids_nb1 = (int64_t)ids->nb[1];
+    a.ids_nb2 = (int64_t)ids->nb[2];
+    a.dst = (float *)dst->data;
+    a.dst_nb1 = (int64_t)dst->nb[1];
+    a.dst_nb2 = (int64_t)dst->nb[2];
+    a.dst_nb3 = (int64_t)dst->nb[3];
+    a.err = be->err;
+    HIP_OK(mx::launch_get_rows(a, be->stream), "GET_ROWS launch");
+    return MX_SUCCESS;
+}
+
+static int max_cols(int type, int64_t K) {
+    int nc = mx::MAX_COLS;
+    while (nc > 1 && mx::act_lds_bytes(type, K, nc) > kMaxLds) nc--;
+    return nc;
+}
+
+// Products sharing src1: n problems (n <= 4) of the same type and K, each with its own rows and dst.
+static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
+                        const mx_tensor *const *dst) {
+    const mx_tensor *w0 = src0[0];
+    mx::MatvecArgs a{};
+    a.type = w0->type;
+    a.rounding = be->rounding;
+    a.K = w0->ne[0];
+    a.x_col_stride = (int64_t)(src1->nb[1] / 4);
+    a.y_col_stride = (int64_t)(dst[0]->nb[1] / 4);
+    a.ne12 = src1->ne[2];
+    a.ne13 = src1->ne[3];
+    a.ne02 = w0->ne[2];
+    a.r2 = src1->ne[2] / w0->ne[2];
+    a.r3 = src1->ne[3] / w0->ne[3];
+    a.x_b2 = (int64_t)(src1->nb[2] / 4);
+    a.x_b3 = (int64_t)(src1->nb[3] / 4);
+    a.y_b2 = (int64_t)(dst[0]->nb[2] / 4);
+    a.y_b3 = (int64_t)(dst[0]->nb[3] / 4);
+    a.nprob = n;
+    const int64_t M = src1->ne[1];
+    const int ncmax = max_cols(a.type, a.K);
+    for (int64_t m0 = 0; m0 < M; m0 += ncmax) {
+        a.ncols = (int)std::min<int64_t>(ncmax, M - m0);
+        a.x = (const float *)src1->data + m0 * a.x_col_stride;
+        for (int i = 0; i < n; i++) {
+            const mx::Planes pl = mx::planes_of(src0[i]->type, nelements(src0[i]));
+            a.prob[i].w = mx::wplanes(src0[i]->data, pl);
+            a.prob[i].N = src0[i]->ne[1];
+            a.prob[i].row0 = 0;
+            a.prob[i].y = (float *)dst[i]->data + m0 * a.y_col_stride;
+        }
+        HIP_OK(mx::launch_matvec(a, be->stream), "MUL_MAT launch");
+    }
+    return MX_SUCCESS;
+}
+
+MX_API int mx_mul_mat(mx_backend *be, const mx_tensor *src0, const mx_tensor *src1, const mx_tensor *dst) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!mx_supports_op(MX_OP_MUL_MAT, src0, src1, nullptr, dst))
+        return fail(MX_UNSUPPORTED, "MUL_MAT: unsupported types, shapes or strides");
+    if (nelements(dst) == 0) return MX_SUCCESS;
+    return matvec_group(be, 1, &src0, src1, &dst);
+}
+
+MX_API int mx_mul_mat_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
+                            const mx_tensor *const *dst) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (n <= 0 || !src0 || !dst) return fail(MX_INVALID, "empty group");
+    for (int i = 0; i < n; i++) {
+        if (!mx_supports_op(MX_OP_MUL_MAT, src0[i], src1, nullptr, dst[i]))
+            return fail(MX_UNSUPPORTED, "MUL_MAT group member %d: unsupported types, shapes or strides", i);
+        if (src0[i]->type != src0[0]->type || src0[i]->ne[2] != 1 || src0[i]->ne[3] != 1 || src1->ne[2] != 1 ||
+            src1->ne[3] != 1 || dst[i]->nb[1] != dst[0]->nb[1])
+            return fail(MX_UNSUPPORTED, "MUL_MAT group members must be 2-D products of one weight type");
+    }
+    for (int i0 = 0; i0 < n; i0 += 4) {
+        const int k = std::min(4, n - i0);
+        if ((rc = matvec_group(be, k, src0 + i0, src1, dst + i0))) return rc;
+    }
+    return MX_SUCCESS;
+}
+
+MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids,
+                         const mx_tensor *dst) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!mx_supports_op(MX_OP_MUL_MAT_ID, as, b, ids, dst))
+        return fail(MX_UNSUPPORTED, "MUL_MAT_ID: unsupported types, shapes or strides");
+    const mx::Planes pl = mx::planes_of(as->type, nelements(as));
+    mx::MulMatIdArgs a{};
+    a.type = as->type;
+    a.rounding = be->rounding;
+    a.w = mx::wplanes(as->data, pl);
+    a.K = as->ne[0];
+    a.N = as->ne[1];
+    a.E = as->ne[2];
+    a.n_ids = ids->ne[0];
+    a.T = ids->ne[1];
+    a.b = (const float *)b->data;
+    a.b_ne1 = b->ne[1];
+    a.b_nb1 = (int64_t)b->nb[1];
+    a.b_nb2 = (int64_t)b->nb[2];
+    a.ids = (const int32_t *)ids->data;
+    a.ids_nb0 = (int64_t)ids->nb[0];
+    a.ids_nb1 = (int64_t)ids->nb[1];
+    a.dst = (float *)dst->data;
+    a.dst_nb1 = (int64_t)dst->nb[1];
+    a.dst_nb2 = (int64_t)dst->nb[2];
+    if (a.n_ids * a.T == 0) return MX_SUCCESS;
+    const size_t need = mx::mul_mat_id_scratch(&a, nullptr);
+    if ((rc = ensure_scratch(be, need))) return rc;
+    mx::mul_mat_id_scratch(&a, be->scratch);
+    a.err = be->err;
+    HIP_OK(mx::launch_mul_mat_id(a, be->stream), "MUL_MAT_ID launch");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_quantize_act(mx_backend *be, int type, int rounding, const float *x, int64_t k, int64_t nrows,
+                           size_t x_row_stride, void *out) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (type != MX_TYPE_Q8_0 && type != MX_TYPE_Q8_1 && type != MX_TYPE_Q8_K)
+        return fail(MX_UNSUPPORTED, "activation type %d", type);
+    if (rounding != MX_ROUND_REF && rounding != MX_ROUND_X86) return fail(MX_INVALID, "unknown rounding %d", rounding);
+    if (k < 0 || nrows < 0 || k % blck(type) != 0) return fail(MX_INVALID, "k must be a multiple of the block size");
+    if (!aligned16(x) || x_row_stride % 16 != 0) return fail(MX_INVALID, "x rows must be 16-byte aligned");
+    if ((type == MX_TYPE_Q8_K) && ((uintptr_t)out & 3)) return fail(MX_INVALID, "Q8_K output must be 4-byte aligned");
+    HIP_OK(mx::launch_quantize_act(type, rounding, x, k, nrows, (int64_t)(x_row_stride / 4), out, be->stream),
+           "quantize launch");
+    return MX_SUCCESS;
+}
+
+// ------------------------------------------------------------------------------------------------------ graphs
+MX_API int mx_graph_begin(mx_backend *be) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (be->capturing) return fail(MX_FAILED, "a graph is already being recorded");
+    HIP_OK(hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal), "begin capture");
+    be->capturing = true;
+    return MX_SUCCESS;
+}
+
+MX_API int mx_graph_end(mx_backend *be, mx_graph **graph) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!be->capturing) return fail(MX_FAILED, "no graph is being recorded");
+    be->capturing = false;
+    hipGraph_t g = nullptr;
+    HIP_OK(hipStreamEndCapture(be->stream, &g), "end capture");
+    mx_graph *out = new mx_graph();
+    out->graph = g;
+    hipError_t e = hipGraphInstantiate(&out->exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        delete out;
+        return hip_fail(e, "instantiate graph");
+    }
+    *graph = out;
+    return MX_SUCCESS;
+}
+
+MX_API int mx_graph_launch(mx_backend *be, mx_graph *graph) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!graph) return fail(MX_INVALID, "null graph");
+    HIP_OK(hipGraphLaunch(graph->exec, be->stream), "launch graph");
+    return MX_SUCCESS;
+}
+
+MX_API void mx_graph_free(mx_graph *graph) {
+    if (!graph) return;
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    delete graph;
+}
+
+// ------------------------------------------------------------------------------------------------------ events
+MX_API mx_event *mx_event_new(mx_backend *be) {
+    if (check_be(be)) return nullptr;
+    mx_event *e = new mx_event();
+    e->device = be->device;
+    if (hipEventCreate(&e->ev) != hipSuccess) {
+        fail(MX_FAILED, "cannot create an event");
+        delete e;
+        return nullptr;
+    }
+    return e;
+}
+
+MX_API int mx_event_record(mx_backend *be, mx_event *ev) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!ev) return fail(MX_INVALID, "null event");
+    HIP_OK(hipEventRecord(ev->ev, be->stream), "record event");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_event_synchronize(mx_event *ev) {
+    if (!ev) return fail(MX_INVALID, "null event");
+    HIP_OK(hipEventSynchronize(ev->ev), "synchronize event");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_event_elapsed_ms(mx_event *start, mx_event *end, float *ms) {
+    if (!start || !end || !ms) return fail(MX_INVALID, "null argument");
+    HIP_OK(hipEventElapsedTime(ms, start->ev, end->ev), "elapsed time");
+    return MX_SUCCESS;
+}
+
+MX_API void mx_event_free(mx_event *ev) {
+    if (!ev) return;
+    (void)hipEventDestroy(ev->ev);
+    delete ev;
+}
+
+}  // extern "C"

@@ -1,0 +1,190 @@
+// Internal declarations shared by libmx's host code and its HIP kernels (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/mx.h"
+
+namespace mx {
+
+constexpr int QK8 = 32;    // elements of a Q8_0 / Q8_1 block
+constexpr int QKK = 256;   // elements of a K-quant super-block
+constexpr size_t PLANE_ALIGN = 256;
+
+// ------------------------------------------------------------------------------------------------------------------
+// Device layout of a quantized tensor.
+//
+// ggml stores a tensor as an array of blocks (ggml-common.h): block_q8_0 {d, qs[32]} (34 B), block_q4_K {d, dmin,
+// scales[12], qs[128]} (144 B), block_q6_K {ql[128], qh[64], scales[16], d} (210 B). On this device each field becomes a
+// plane of its own: plane p holds that field of block 0, block 1, ... back to back, and each plane starts on a
+// 256-byte boundary. Blocks are numbered in ggml order (row-major over all rows of all matrices), so a row's quants
+// are contiguous and 16-byte aligned, which is what wide coalesced loads and MFMA tiles want.
+//
+//   Q8_0: plane 0 qs (32 B/block), plane 1 d (2 B/block)
+//   Q4_K: plane 0 qs (128 B/block), plane 1 scales (12 B/block), plane 2 d,dmin (4 B/block)
+//   Q6_K: plane 0 ql (128 B/block), plane 1 qh (64 B/block), plane 2 scales (16 B/block), plane 3 d (2 B/block)
+//
+// The map from a byte of ggml's block to (plane, byte in plane) is a permutation, so a partial upload of ggml bytes at
+// any offset scatters into every plane without reading anything else.
+// ------------------------------------------------------------------------------------------------------------------
+struct Segment {
+    uint16_t begin;  // first byte of the field in ggml's block
+    uint16_t len;    // bytes of the field
+    uint8_t plane;   // plane it goes to
+};
+
+struct TypeInfo {
+    int type;
+    int blk_elems;   // elements per block
+    int blk_bytes;   // bytes per ggml block
+    int nseg;
+    Segment seg[4];  // ggml block fields in byte order
+};
+
+inline const TypeInfo *type_info(int type) {
+    // Field order within ggml's structs: block_q8_0 {d, qs}; block_q4_K {d, dmin, scales, qs}; block_q6_K {ql, qh,
+    // scales, d}.
+    static const TypeInfo q8_0 = {MX_TYPE_Q8_0, 32, 34, 2, {{0, 2, 1}, {2, 32, 0}, {0, 0, 0}, {0, 0, 0}}};
+    static const TypeInfo q4_k = {MX_TYPE_Q4_K, 256, 144, 3, {{0, 4, 2}, {4, 12, 1}, {16, 128, 0}, {0, 0, 0}}};
+    static const TypeInfo q6_k = {MX_TYPE_Q6_K, 256, 210, 4, {{0, 128, 0}, {128, 64, 1}, {192, 16, 2}, {208, 2, 3}}};
+    switch (type) {
+        case MX_TYPE_Q8_0: return &q8_0;
+        case MX_TYPE_Q4_K: return &q4_k;
+        case MX_TYPE_Q6_K: return &q6_k;
+        default: return nullptr;
+    }
+}
+
+inline bool is_quantized(int type) { return type == MX_TYPE_Q8_0 || type == MX_TYPE_Q4_K || type == MX_TYPE_Q6_K; }
+
+struct Planes {
+    int n = 0;
+    uint64_t off[4] = {0, 0, 0, 0};      // byte offset of each plane from the tensor's base
+    uint32_t per_blk[4] = {0, 0, 0, 0};  // bytes per block in each plane
+    int64_t nblocks = 0;
+    uint64_t total = 0;                   // allocation size
+};
+
+inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+
+inline Planes planes_of(int type, int64_t nelements) {
+    Planes p;
+    const TypeInfo *ti = type_info(type);
+    if (!ti) return p;
+    p.nblocks = nelements / ti->blk_elems;
+    p.n = ti->nseg;
+    for (int s = 0; s < ti->nseg; s++) p.per_blk[ti->seg[s].plane] = ti->seg[s].len;
+    uint64_t off = 0;
+    for (int i = 0; i < p.n; i++) {
+        p.off[i] = off;
+        off = align_up(off + (uint64_t)p.nblocks * p.per_blk[i], PLANE_ALIGN);
+    }
+    p.total = off;
+    return p;
+}
+
+// The planes of a quantized weight, as kernels take them.
+struct WPlanes {
+    const uint8_t *p0, *p1, *p2, *p3;
+};
+
+inline WPlanes wplanes(const void *base, const Planes &pl) {
+    const uint8_t *b = (const uint8_t *)base;
+    return {b + pl.off[0], b + pl.off[1], pl.n > 2 ? b + pl.off[2] : nullptr, pl.n > 3 ? b + pl.off[3] : nullptr};
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Kernel launchers (defined in the .hip files). All run on `s`. Return hipError_t of the launch.
+// ------------------------------------------------------------------------------------------------------------------
+// Scatter `n` ggml-layout bytes (from device staging `src`), which are bytes [offset, offset + n) of a tensor of
+// `type`, into the planes at `base`; gather is the inverse.
+// A tensor's byte permutation, passed to kernels by value.
+struct SegMap {
+    int blk_bytes;
+    int nseg;
+    Segment seg[4];
+    uint64_t plane_off[4];
+};
+SegMap segmap_of(int type, const Planes &pl);
+hipError_t launch_scatter(const SegMap &m, uint8_t *base, const uint8_t *src, uint64_t offset, uint64_t n,
+                          hipStream_t s);
+hipError_t launch_gather(const SegMap &m, const uint8_t *base, uint8_t *dst, uint64_t offset, uint64_t n,
+                         hipStream_t s);
+hipError_t launch_fill(const SegMap &m, uint8_t *base, uint8_t value, uint64_t offset, uint64_t n, hipStream_t s);
+
+// Activation quantization to ggml blocks (Q8_0, Q8_1 or Q8_K) in global memory.
+hipError_t launch_quantize_act(int type, int rounding, const float *x, int64_t k, int64_t nrows, int64_t x_stride,
+                               void *out, hipStream_t s);
+
+// GET_ROWS for one 2-D slice batch.
+struct GetRowsArgs {
+    int type;
+    WPlanes w;
+    int64_t K;            // elements per row
+    int64_t R;            // rows per matrix of src0 (bound for ids)
+    int64_t n_ids0, n_ids1, n_ids2;  // ids ne[0..2]
+    int64_t src_mat_rows1, src_mat_rows2;  // row offset of matrix (i11, i12): i11 * rows1 + i12 * rows2
+    const int32_t *ids;
+    int64_t ids_nb0, ids_nb1, ids_nb2;     // strides in bytes
+    float *dst;
+    int64_t dst_nb1, dst_nb2, dst_nb3;     // bytes
+    int *err;
+};
+hipError_t launch_get_rows(const GetRowsArgs &a, hipStream_t s);
+
+// Mat-vec / small-M products: up to MAX_COLS columns of src1 per launch, all batch slices in grid.z.
+constexpr int MAX_COLS = 8;
+struct MatvecProblem {
+    WPlanes w;
+    int64_t N;             // rows of the matrix (outputs)
+    int64_t row0;          // first row of the matrix within the tensor's planes
+    float *y;              // dst column 0 of this problem
+};
+struct MatvecArgs {
+    int type;
+    int ncols;             // columns of src1 in this launch (1..MAX_COLS)
+    int rounding;
+    int64_t K;
+    const float *x;        // src1 column 0 of batch slice (0, 0)
+    int64_t x_col_stride;  // floats between columns
+    int64_t y_col_stride;  // floats between dst columns
+    // batch slices (grid.z = ne12 * ne13): matrix (i12 / r2, i13 / r3) of src0 meets slice (i12, i13) of src1
+    int64_t ne12, ne13, ne02, r2, r3;
+    int64_t x_b2, x_b3, y_b2, y_b3;  // float strides of src1 / dst slices
+    // problems sharing x (grid.y picks the problem)
+    int nprob;
+    MatvecProblem prob[4];
+};
+hipError_t launch_matvec(const MatvecArgs &a, hipStream_t s);
+
+// MUL_MAT_ID.
+struct MulMatIdArgs {
+    int type;
+    int rounding;
+    WPlanes w;
+    int64_t K, N, E;
+    int64_t n_ids, T;
+    const float *b;
+    int64_t b_ne1;         // 1 (one row per token, broadcast to every slot) or n_ids
+    int64_t b_nb1, b_nb2;  // bytes
+    const int32_t *ids;
+    int64_t ids_nb0, ids_nb1;  // bytes
+    float *dst;
+    int64_t dst_nb1, dst_nb2;  // bytes
+    // scratch (mul_mat_id_scratch carves it)
+    int32_t *counts;       // [E] pairs per expert
+    int32_t *offsets;      // [E] first pair of each expert in `pairs`
+    int32_t *active;       // [E + 1]: active[0] = number of experts with pairs, then their ids
+    int32_t *pairs;        // [n_ids * T] flat pair index t * n_ids + s, grouped by expert
+    int8_t *xq;            // [T * b_ne1][K] quantized activation rows
+    float *xd;             // [T * b_ne1][K / blk] their scales
+    int32_t *xbs;          // [T * b_ne1][K / 16] their 16-element sums (K-quants)
+    int *err;
+};
+// Scratch bytes MUL_MAT_ID needs and the carving of `base` into the fields above.
+size_t mul_mat_id_scratch(MulMatIdArgs *a, void *base);
+hipError_t launch_mul_mat_id(const MulMatIdArgs &a, hipStream_t s);
+
+}  // namespace mx

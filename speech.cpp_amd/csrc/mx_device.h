@@ -1,0 +1,129 @@
+// Device-side helpers for libmx's gfx950 kernels: fp16 conversion, wave64 reductions and the activation quantizers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mx.h"
+
+namespace mx {
+
+// fp16 bits <-> fp32. v_cvt_f16_f32 rounds to nearest even and keeps binary16 subnormals (the default FP mode of a
+// HIP kernel), which is IEEE conversion as ggml_compute_fp32_to_fp16 performs it.
+__device__ __forceinline__ float h2f(uint16_t h) {
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float)v;
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+    _Float16 v = (_Float16)f;
+    uint16_t h;
+    __builtin_memcpy(&h, &v, 2);
+    return h;
+}
+
+template <int WIDTH>
+__device__ __forceinline__ float sum_lanes(float v) {
+#pragma unroll
+    for (int m = WIDTH / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+template <int WIDTH>
+__device__ __forceinline__ int isum_lanes(int v) {
+#pragma unroll
+    for (int m = WIDTH / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+__device__ __forceinline__ int pack4(int a, int b, int c, int d) {
+    return (a & 0xFF) | ((b & 0xFF) << 8) | ((c & 0xFF) << 16) | ((int)((unsigned)d << 24));
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// 32-block quantizer (Q8_0 / Q8_1 activations). Eight consecutive lanes hold one block, four floats each (lane j of
+// the eight holds elements 4j..4j+3).
+//   REF (ggml-quants.c quantize_row_q8_{0,1}_ref): d = amax/127, id = d ? 1/d : 0, q = roundf(x*id).
+//   X86 (ggml-cpu x86 quantize_row_q8_{0,1}):       d = amax/127, id = amax ? 127/amax : 0, q = rint(x*id).
+// The divisions are IEEE (HIP's default correctly rounded fp32 division), the products single roundings.
+// Returns the four quants packed in an int; *d gets fp32 d (unrounded), *sum the block's quant sum (all 8 lanes).
+// ------------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ int quant32_lane(float4 v, int rounding, float *d_out, int *sum_out) {
+    float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    a = fmaxf(a, __shfl_xor(a, 1));
+    a = fmaxf(a, __shfl_xor(a, 2));
+    a = fmaxf(a, __shfl_xor(a, 4));
+    const float d = a / 127.0f;
+    int q0, q1, q2, q3;
+    if (rounding == MX_ROUND_X86) {
+        const float id = a != 0.0f ? 127.0f / a : 0.0f;
+        q0 = (int)rintf(v.x * id);
+        q1 = (int)rintf(v.y * id);
+        q2 = (int)rintf(v.z * id);
+        q3 = (int)rintf(v.w * id);
+    } else {
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        q0 = (int)roundf(v.x * id);
+        q1 = (int)roundf(v.y * id);
+        q2 = (int)roundf(v.z * id);
+        q3 = (int)roundf(v.w * id);
+    }
+    int s = q0 + q1 + q2 + q3;
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 4);
+    *d_out = d;
+    *sum_out = s;
+    return pack4(q0, q1, q2, q3);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// 256-block quantizer (Q8_K activations of Q4_K / Q6_K weights), ggml-quants.c quantize_row_q8_K_ref. One wave holds
+// one block, four floats per lane (lane l holds elements 4l..4l+3).
+//   max = the element of largest |x|, the first one on ties; iscale = -127/max; q = min(127, rint(iscale*x));
+//   d = 1/iscale; bsums[j] = sum of q[16j..16j+15]. An all-zero block gives d = 0, q = 0 and bsums 0.
+// Returns packed quants; *d the block's d; *bsum the sum over this lane's group of four lanes (16 elements).
+// ------------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ int quant256_wave(float4 v, int lane, float *d_out, int *bsum_out) {
+    const float e[4] = {v.x, v.y, v.z, v.w};
+    uint32_t best_bits = __float_as_uint(fabsf(e[0]));
+    uint32_t best_idx = 4u * lane;
+#pragma unroll
+    for (int j = 1; j < 4; j++) {
+        const uint32_t b = __float_as_uint(fabsf(e[j]));
+        if (b > best_bits) { best_bits = b; best_idx = 4u * lane + j; }
+    }
+    // Largest |x| wins; among equal |x| the smallest index (the first one ggml's strict '>' scan keeps).
+    uint64_t key = ((uint64_t)best_bits << 32) | (uint64_t)(0xFFFFFFFFu - best_idx);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint32_t hi = __shfl_xor((uint32_t)(key >> 32), m);
+        const uint32_t lo = __shfl_xor((uint32_t)key, m);
+        const uint64_t other = ((uint64_t)hi << 32) | lo;
+        key = other > key ? other : key;
+    }
+    const uint32_t amax_bits = (uint32_t)(key >> 32);
+    const uint32_t idx = 0xFFFFFFFFu - (uint32_t)key;
+    const uint32_t c = idx & 3u;  // every lane picks component idx%4; lane idx/4's is the block's max
+    const float mine = c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
+    const float maxv = __shfl(mine, (int)(idx >> 2));
+    if (amax_bits == 0) {
+        *d_out = 0.0f;
+        *bsum_out = 0;
+        return 0;
+    }
+    const float iscale = -127.0f / maxv;
+    int q[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int t = (int)rintf(iscale * e[j]);
+        q[j] = t < 127 ? t : 127;
+    }
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += __shfl_xor(s, 1);
+    s += __shfl_xor(s, 2);
+    *d_out = 1.0f / iscale;
+    *bsum_out = s;
+    return pack4(q[0], q[1], q[2], q[3]);
+}
+
+}  // namespace mx

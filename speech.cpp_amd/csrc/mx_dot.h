@@ -1,0 +1,169 @@
+// Per-chunk dot products of one weight row (planar layout) with up to NC quantized activation columns held in LDS.
+//
+// The integer part of every product is exact (v_dot4 over int8, int32 sums); scales are applied in fp32 as ggml's
+// CPU dots apply them (ggml-cpu/quants.c ggml_vec_dot_q8_0_q8_0 / _q4_K_q8_K / _q6_K_q8_K): d_w * d_x formed in fp32,
+// then times the exact integer sum. Only the order of the fp32 cross-block sum differs from the CPU.
+//
+// Activations in LDS, column c:
+//   xq[c*K + k]     int8 quants
+//   xd[c*nsc + b]   fp32 scale of block b (the fp16-rounded d of Q8_0/Q8_1 for Q8_0 weights; Q8_K's fp32 d otherwise)
+//   xbs[c*K/16 + j] sum of quants 16j..16j+15 (K-quants only; Q8_K's bsums)
+#pragma once
+
+#include "mx_common.h"
+#include "mx_device.h"
+
+namespace mx {
+
+__device__ __forceinline__ int dot16(int4 a, int4 b, int acc) {
+    acc = __builtin_amdgcn_sdot4(a.x, b.x, acc, false);
+    acc = __builtin_amdgcn_sdot4(a.y, b.y, acc, false);
+    acc = __builtin_amdgcn_sdot4(a.z, b.z, acc, false);
+    acc = __builtin_amdgcn_sdot4(a.w, b.w, acc, false);
+    return acc;
+}
+
+// Chunks per row: a Q8_0 chunk is 16 quants (half a block); a K-quant chunk is 32 elements (16 bytes of qs / ql).
+template <int TYPE>
+__host__ __device__ constexpr int chunk_elems() { return TYPE == MX_TYPE_Q8_0 ? 16 : 32; }
+
+// Unpack the 6-bit scale and min of sub-blocks j and j+1 (j even) from Q4_K's 12 packed bytes held in three words
+// (ggml-quants.c get_scale_min_k4).
+__device__ __forceinline__ uint32_t byte_of(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
+    const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
+    return (w >> (8 * (i & 3))) & 0xFFu;
+}
+__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int &sc, int &m) {
+    if (j < 4) {
+        sc = (int)(byte_of(s0, s1, s2, j) & 63);
+        m = (int)(byte_of(s0, s1, s2, j + 4) & 63);
+    } else {
+        sc = (int)((byte_of(s0, s1, s2, j + 4) & 0xF) | ((byte_of(s0, s1, s2, j - 4) >> 6) << 4));
+        m = (int)((byte_of(s0, s1, s2, j + 4) >> 4) | ((byte_of(s0, s1, s2, j) >> 6) << 4));
+    }
+}
+
+// acc[col] += contribution of chunk c of weight row `grow` (global row index within the tensor's planes).
+template <int TYPE, int NC, bool GUARD>
+__device__ __forceinline__ void chunk_dot(const WPlanes &w, int64_t grow, int64_t K, int c, const int8_t *xq,
+                                          const float *xd, const int *xbs, int ncols, float *acc) {
+    if (TYPE == MX_TYPE_Q8_0) {
+        const int64_t nblk = K / 32;
+        const int4 wq = *(const int4 *)(w.p0 + grow * K + 16 * c);
+        const float dw = h2f(*(const uint16_t *)(w.p1 + (grow * nblk + (c >> 1)) * 2));
+#pragma unroll
+        for (int col = 0; col < NC; col++) {
+            if (GUARD && col >= ncols) break;
+            const int4 xv = *(const int4 *)(xq + col * K + 16 * c);
+            const int s = dot16(wq, xv, 0);
+            acc[col] += (float)s * (dw * xd[col * nblk + (c >> 1)]);
+        }
+    } else if (TYPE == MX_TYPE_Q4_K) {
+        const int64_t nsb = K / 256;
+        const int sb = c >> 3, t = c & 7;
+        const int64_t blk = grow * nsb + sb;
+        const int4 q = *(const int4 *)(w.p0 + blk * 128 + 16 * t);
+        const uint32_t *sp = (const uint32_t *)(w.p1 + blk * 12);
+        const uint32_t s0 = sp[0], s1 = sp[1], s2 = sp[2];
+        const uint32_t dm = *(const uint32_t *)(w.p2 + blk * 4);
+        const float d = h2f((uint16_t)(dm & 0xFFFF)), dmin = h2f((uint16_t)(dm >> 16));
+        const int jlo = 2 * (t >> 1);
+        int sc_lo, m_lo, sc_hi, m_hi;
+        q4k_scale_min(s0, s1, s2, jlo, sc_lo, m_lo);
+        q4k_scale_min(s0, s1, s2, jlo + 1, sc_hi, m_hi);
+        const int4 qlo = make_int4(q.x & 0x0F0F0F0F, q.y & 0x0F0F0F0F, q.z & 0x0F0F0F0F, q.w & 0x0F0F0F0F);
+        const int4 qhi = make_int4((q.x >> 4) & 0x0F0F0F0F, (q.y >> 4) & 0x0F0F0F0F, (q.z >> 4) & 0x0F0F0F0F,
+                                   (q.w >> 4) & 0x0F0F0F0F);
+        const int lo_off = sb * 256 + 64 * (t >> 1) + 16 * (t & 1);
+#pragma unroll
+        for (int col = 0; col < NC; col++) {
+            if (GUARD && col >= ncols) break;
+            const int8_t *xc = xq + col * K;
+            const int dlo = dot16(qlo, *(const int4 *)(xc + lo_off), 0);
+            const int dhi = dot16(qhi, *(const int4 *)(xc + lo_off + 32), 0);
+            const int *bs = xbs + col * (K / 16);
+            const int isum = sc_lo * dlo + sc_hi * dhi;
+            const int msum = m_lo * bs[lo_off >> 4] + m_hi * bs[(lo_off >> 4) + 2];
+            const float dx = xd[col * nsb + sb];
+            acc[col] += (d * dx) * (float)isum - (dmin * dx) * (float)msum;
+        }
+    } else {  // Q6_K
+        const int64_t nsb = K / 256;
+        const int sb = c >> 3, t = c & 7;
+        const int h = t >> 2, u = t & 3;
+        const int64_t blk = grow * nsb + sb;
+        const int4 ql = *(const int4 *)(w.p0 + blk * 128 + 64 * h + 16 * u);
+        const int4 qh = *(const int4 *)(w.p1 + blk * 64 + 32 * h + 16 * (u & 1));
+        const int sh = 2 * (u >> 1);
+        const int4 qlo = make_int4((ql.x & 0x0F0F0F0F) | (((qh.x >> sh) & 0x03030303) << 4),
+                                   (ql.y & 0x0F0F0F0F) | (((qh.y >> sh) & 0x03030303) << 4),
+                                   (ql.z & 0x0F0F0F0F) | (((qh.z >> sh) & 0x03030303) << 4),
+                                   (ql.w & 0x0F0F0F0F) | (((qh.w >> sh) & 0x03030303) << 4));
+        const int4 qhi = make_int4(((ql.x >> 4) & 0x0F0F0F0F) | (((qh.x >> (sh + 4)) & 0x03030303) << 4),
+                                   ((ql.y >> 4) & 0x0F0F0F0F) | (((qh.y >> (sh + 4)) & 0x03030303) << 4),
+                                   ((ql.z >> 4) & 0x0F0F0F0F) | (((qh.z >> (sh + 4)) & 0x03030303) << 4),
+                                   ((ql.w >> 4) & 0x0F0F0F0F) | (((qh.w >> (sh + 4)) & 0x03030303) << 4));
+        const int lo_in = 128 * h + 32 * (u >> 1) + 16 * (u & 1);  // element offset within the super-block
+        const int sc_lo = (int)(int8_t)w.p2[blk * 16 + (lo_in >> 4)];
+        const int sc_hi = (int)(int8_t)w.p2[blk * 16 + (lo_in >> 4) + 4];
+        const float d = h2f(*(const uint16_t *)(w.p3 + blk * 2));
+        const int lo_off = sb * 256 + lo_in;
+#pragma unroll
+        for (int col = 0; col < NC; col++) {
+            if (GUARD && col >= ncols) break;
+            const int8_t *xc = xq + col * K;
+            const int *bs = xbs + col * (K / 16);
+            // The codes are 0..63; (q - 32) . x = q . x - 32 * sum(x), and sum(x) over 16 elements is a Q8_K bsum.
+            const int dlo = dot16(qlo, *(const int4 *)(xc + lo_off), 0) - 32 * bs[lo_off >> 4];
+            const int dhi = dot16(qhi, *(const int4 *)(xc + lo_off + 64), 0) - 32 * bs[(lo_off >> 4) + 4];
+            const int isum = sc_lo * dlo + sc_hi * dhi;
+            acc[col] += (d * xd[col * nsb + sb]) * (float)isum;
+        }
+    }
+}
+
+// Quantize `ncols` columns of f32 activations into LDS with 256 threads. For Q8_0 weights: 32-blocks (d rounded to
+// fp16 and back, as the CPU dot reads it); for K-quants: Q8_K 256-blocks with bsums.
+template <int TYPE, int NC, bool GUARD>
+__device__ __forceinline__ void quantize_cols_to_lds(const float *x, int64_t x_col_stride, int64_t K, int ncols,
+                                                     int rounding, int8_t *xq, float *xd, int *xbs) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    for (int col = 0; col < NC; col++) {
+        if (GUARD && col >= ncols) break;
+        const float *xc = x + col * x_col_stride;
+        for (int64_t base = 0; base < K; base += 1024) {
+            const int64_t e = base + 4 * tid;
+            if (TYPE == MX_TYPE_Q8_0) {
+                const bool valid = e < K;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (valid) v = *(const float4 *)(xc + e);
+                float d;
+                int sum;
+                const int q = quant32_lane(v, rounding, &d, &sum);
+                if (valid) {
+                    *(int *)(xq + col * K + e) = q;
+                    if ((tid & 7) == 0) xd[col * (K / 32) + e / 32] = h2f(f2h(d));
+                }
+            } else {
+                if (base + 256 * (tid >> 6) < K) {  // a whole wave per super-block
+                    const float4 v = *(const float4 *)(xc + e);
+                    float d;
+                    int bs;
+                    const int q = quant256_wave(v, lane, &d, &bs);
+                    *(int *)(xq + col * K + e) = q;
+                    if (lane == 0) xd[col * (K / 256) + e / 256] = d;
+                    if ((lane & 3) == 0) xbs[col * (K / 16) + e / 16] = bs;
+                }
+            }
+        }
+    }
+}
+
+// LDS bytes the activations of `ncols` columns take.
+__host__ __device__ inline size_t act_lds_bytes(int type, int64_t K, int ncols) {
+    if (type == MX_TYPE_Q8_0) return (size_t)ncols * (size_t)K + (size_t)ncols * (size_t)(K / 32) * 4;
+    return (size_t)ncols * (size_t)K + (size_t)ncols * (size_t)(K / 256) * 4 + (size_t)ncols * (size_t)(K / 16) * 4;
+}
+
+}  // namespace mx

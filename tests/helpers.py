@@ -1,0 +1,24 @@
+"""Shared helpers of the parity tests."""
+import numpy as np
+
+
+def rel_err(y: np.ndarray, y_ref: np.ndarray) -> float:
+    """Largest |y - y_ref| of each output row over the largest |y_ref| of that row, maximised over rows.
+
+    A row is one src1 column's outputs (ne0 of dst). This is the 'max relative error' the parity bar is stated in."""
+    y = np.asarray(y, dtype=np.float64).reshape(-1, y_ref.shape[-1])
+    r = np.asarray(y_ref, dtype=np.float64).reshape(-1, y_ref.shape[-1])
+    scale = np.maximum(np.abs(r).max(axis=1), 1e-30)
+    return float((np.abs(y - r).max(axis=1) / scale).max())
+
+
+def l2_rel(y: np.ndarray, y_ref: np.ndarray) -> float:
+    """Row-relative L2 error, as speech.cpp's decoder check measures it (checks/common/qwen3-decoder-check.cpp:59-66)."""
+    y = np.asarray(y, dtype=np.float64).reshape(-1, y_ref.shape[-1])
+    r = np.asarray(y_ref, dtype=np.float64).reshape(-1, y_ref.shape[-1])
+    return float((np.linalg.norm(y - r, axis=1) / np.maximum(np.linalg.norm(r, axis=1), 1e-30)).max())
+
+
+def bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
+    return a.shape == b.shape and np.array_equal(np.ascontiguousarray(a).view(np.uint8),
+                                                 np.ascontiguousarray(b).view(np.uint8))

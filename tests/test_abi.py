@@ -1,0 +1,77 @@
+"""The C ABI: libmx.so loads, exports exactly what include/mx.h declares, and its host-side pieces behave (no GPU)."""
+import pathlib
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "mx.h").read_text()
+    return sorted(set(re.findall(r"MX_API\s+[\w\s\*]*?\b(mx_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_list(mx):
+    assert declared_symbols() == sorted(mx.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(mx):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(mx.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = sorted(l.split()[-1] for l in out.splitlines() if " T " in l)
+    assert exported == declared_symbols()
+    L = mx.lib()
+    for s in declared_symbols():
+        assert hasattr(L, s)
+
+
+def test_library_is_built_for_gfx950(mx):
+    out = subprocess.run(["strings", str(mx.LIB_PATH)], capture_output=True, text=True, check=True).stdout
+    assert "gfx950" in out
+
+
+def test_no_device_is_reported_cleanly_without_gpu(mx):
+    if mx.device_count() > 0:
+        pytest.skip("a GPU is visible")
+    L = mx.lib()
+    assert not L.mx_backend_init(0)
+    assert "no device" in L.mx_last_error().decode()
+
+
+def test_alloc_size_covers_every_plane(mx):
+    for t, K, N in [(mx.Q8_0, 1024, 3), (mx.Q4_K, 2048, 5), (mx.Q6_K, 6144, 7), (mx.Q6_K, 256, 1)]:
+        d = mx.MxTensor()
+        d.type = t
+        for i, v in enumerate((K, N, 1, 1)):
+            d.ne[i] = v
+        nb = mx.contiguous_nb(t, (K, N, 1, 1))
+        for i in range(4):
+            d.nb[i] = nb[i]
+        size = mx.lib().mx_tensor_alloc_size(d)
+        nbytes = mx.row_size(t, K) * N
+        assert nbytes <= size <= nbytes + 4 * 256
+        assert size % 256 == 0
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K])
+def test_host_quantizer_matches_oracle(mx, t):
+    rng = np.random.default_rng(7 + t)
+    for std in (0.02, 1.0, 3e-5):
+        w = (rng.standard_normal((64, 512)) * std).astype(np.float32)
+        w[1] = 0.0
+        w[2, :256] = 0.0
+        w[3] = np.abs(w[3])
+        w[4] = -np.abs(w[4])
+        assert np.array_equal(mx.quantize_chunk(t, w), O.quantize_chunk(t, w))
+
+
+def test_generator_matches_oracle(mx):
+    a = mx.fill_normal(0x5EED0010, 7, 1001, 0.0, 0.02)
+    assert np.array_equal(a, O.fill_normal(0x5EED0010, 7, 1001, 0.0, 0.02))
+    q = mx.quantize_normal(mx.Q6_K, 99, 16, 512, 0.02, nthreads=3)
+    assert np.array_equal(q, O.quantize_chunk(O.TYPE_Q6_K, O.fill_normal(99, 16, 512, 0.0, 0.02)))

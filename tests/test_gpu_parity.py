@@ -1,0 +1,304 @@
+"""Parity of libmx's HIP kernels with the CPU oracle, through the C ABI, on device 0.
+
+Bars: activation quantization and GET_ROWS bit-exact; products within max relative error 1e-3 of the oracle (largest
+|difference| of a dst row over the largest |output| of that row). The kernels sum the same exact per-block integers as
+the oracle and differ only in the order of the fp32 cross-block sum, so the observed error is ~1e-6; the test also
+holds them to 1e-5 to catch a dropped term long before the 1e-3 bar would.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import bits_equal, l2_rel, rel_err
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3         # the parity bar
+TIGHT = 2e-5       # what exact integer sums with an fp32 cross-block sum give
+QTYPES = [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K]
+NAMES = {O.TYPE_Q8_0: "q8_0", O.TYPE_Q4_K: "q4_K", O.TYPE_Q6_K: "q6_K"}
+
+
+def weights(t, N, K, seed, std=0.02):
+    return O.quantize_chunk(t, O.fill_normal(seed, N, K, 0.0, std))
+
+
+def acts(seed, M, K):
+    return O.fill_normal(seed, M, K, 0.0, 1.0)
+
+
+def special_rows(K):
+    """Rows that exercise the quantizers' edge cases."""
+    rows = []
+    rows.append(np.zeros(K, np.float32))                                   # all-zero blocks: d = 0, q = 0
+    rows.append(np.full(K, 0.75, np.float32))                              # constant blocks: q = +-127
+    r = np.zeros(K, np.float32)
+    r[0::32] = 127.0
+    r[1::32] = 2.5                                                         # REF rounds 2.5 -> 3, X86 -> 2
+    r[2::32] = -2.5
+    r[3::32] = 0.5
+    rows.append(r)
+    rows.append((np.arange(K, dtype=np.float32) % 7 - 3) * np.float32(1e-6))  # fp16-subnormal scales
+    t = np.zeros(K, np.float32)
+    t[5::256] = -3.0
+    t[9::256] = 3.0                                                        # Q8_K tie on |max|: the first (-3) wins
+    t[100::256] = 1.0
+    rows.append(t)
+    rows.append(-np.abs(acts(11, 1, K)[0]))                                # one-signed
+    return np.stack(rows).astype(np.float32)
+
+
+# --------------------------------------------------------------------------------------------- activation quantizers
+@pytest.mark.parametrize("qt", [O.TYPE_Q8_0, O.TYPE_Q8_1, O.TYPE_Q8_K])
+@pytest.mark.parametrize("rounding", [O.ROUND_REF, O.ROUND_X86])
+def test_quantize_act_bit_exact(mx, be, qt, rounding):
+    if qt == O.TYPE_Q8_K and rounding == O.ROUND_X86:
+        pytest.skip("Q8_K has a single rounding")
+    K = 4096
+    x = np.concatenate([acts(0xAC700001, 9, K), special_rows(K), acts(3, 2, K) * np.float32(1e4)])
+    tx = be.tensor(mx.F32, (K, x.shape[0]), x)
+    out = be.quantize_act(qt, rounding, tx, K, x.shape[0])
+    be.sync()
+    got = out.get_bytes()[: O.row_size(qt, K) * x.shape[0]].reshape(x.shape[0], -1)
+    want = O.quantize_rows(qt, x, rounding)
+    assert np.array_equal(got, want), f"rows differing: {np.nonzero((got != want).any(axis=1))[0]}"
+
+
+# ------------------------------------------------------------------------------------------------ device layout
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+def test_tensor_set_get_roundtrip(mx, be, t):
+    K, N = 512, 37
+    w = weights(t, N, K, 0x5EED0100 + t).reshape(-1)
+    T = be.tensor(t, (K, N))
+    cuts = [0, 1, 35, 36, 143, 500, 1000, 2049, len(w)]   # pieces at offsets that split blocks and fields
+    for a, b in zip(cuts[:-1], cuts[1:]):
+        T.set(w[a:b], offset=a)
+    assert np.array_equal(T.get_bytes(), w)
+    assert np.array_equal(T.get_bytes(offset=37, size=301), w[37:338])
+    T.set(np.zeros(50, np.uint8), offset=211)
+    ref = w.copy()
+    ref[211:261] = 0
+    assert np.array_equal(T.get_bytes(), ref)
+
+
+def test_tensor_set_out_of_range(mx, be):
+    T = be.tensor(mx.Q8_0, (64, 2))
+    with pytest.raises(mx.MxError) as e:
+        T.set(np.zeros(10, np.uint8), offset=T.nbytes - 5)
+    assert e.value.code == mx.INVALID
+
+
+# ---------------------------------------------------------------------------------------------------- GET_ROWS
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+def test_get_rows_bit_exact(mx, be, t):
+    K, R = 1024, 50
+    table = weights(t, R, K, 0x5EED0200 + t)
+    ids = np.array([0, 49, 7, 7, 23, 1], np.int32)
+    T = be.tensor(t, (K, R), table)
+    I = be.tensor(mx.I32, (len(ids),), ids)
+    D = be.tensor(mx.F32, (K, len(ids)))
+    be.get_rows(T, I, D)
+    be.sync()
+    got = D.numpy().reshape(len(ids), K)
+    assert bits_equal(got, O.get_rows(t, table, K, ids))
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+def test_get_rows_3d(mx, be, t):
+    # src0 [K, R, 3], ids [n, 3]: matrix i11 of the table for the ids of column i11 (ggml_get_rows broadcast rule)
+    K, R, B, n = 256, 10, 3, 4
+    table = weights(t, R * B, K, 0x5EED0300 + t)
+    ids = np.array([[0, 9, 3, 3], [1, 1, 2, 8], [9, 0, 5, 4]], np.int32)
+    T = be.tensor(t, (K, R, B), table)
+    I = be.tensor(mx.I32, (n, B), ids)
+    D = be.tensor(mx.F32, (K, n, B))
+    be.get_rows(T, I, D)
+    be.sync()
+    got = D.numpy().reshape(B, n, K)
+    for b in range(B):
+        want = O.get_rows(t, table[b * R:(b + 1) * R], K, ids[b])
+        assert bits_equal(got[b], want)
+
+
+def test_get_rows_index_out_of_range(mx, be):
+    K, R = 256, 8
+    T = be.tensor(mx.Q8_0, (K, R), weights(O.TYPE_Q8_0, R, K, 5))
+    I = be.tensor(mx.I32, (2,), np.array([3, R], np.int32))
+    D = be.tensor(mx.F32, (K, 2))
+    be.get_rows(T, I, D)
+    with pytest.raises(mx.MxError) as e:
+        be.sync()
+    assert e.value.code == mx.INVALID
+    assert np.all(D.numpy().reshape(2, K)[1] == 0)
+    be.sync()  # the error word was cleared
+
+
+# ------------------------------------------------------------------------------------------------------ MUL_MAT
+def run_mul_mat(mx, be, t, w, x, K, N):
+    M = x.shape[0]
+    W = be.tensor(t, (K, N), w)
+    X = be.tensor(mx.F32, (K, M), x)
+    Y = be.tensor(mx.F32, (N, M))
+    be.mul_mat(W, X, Y)
+    be.sync()
+    return Y.numpy().reshape(M, N)
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8, 11])
+def test_mul_mat_small_m(mx, be, t, M):
+    K = 1536 if t != O.TYPE_Q8_0 else 1056
+    N = 301
+    w = weights(t, N, K, 0x5EED0400 + t)
+    x = acts(0xAC700400 + M, M, K)
+    y = run_mul_mat(mx, be, t, w, x, K, N)
+    y_ref = O.mul_mat(t, w, x)
+    assert rel_err(y, y_ref) <= TIGHT
+    assert rel_err(y, O.mul_mat(t, w, x, exact=True)) <= TIGHT
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("K", [256, 2048, 6144])
+def test_mul_mat_matvec_k(mx, be, t, K):
+    N = 130
+    w = weights(t, N, K, 0x5EED0500 + K + t)
+    x = acts(0xAC700500 + K, 1, K)
+    assert rel_err(run_mul_mat(mx, be, t, w, x, K, N), O.mul_mat(t, w, x)) <= TIGHT
+
+
+def test_mul_mat_config1(mx, be):
+    """Single MUL_MAT, batch 1: W 3072 x 1024 from N(0, 0.02) quantized to Q8_0 by quantize_row_q8_0_ref; x 1 x 1024
+    from N(0, 1); y 1 x 3072."""
+    K, N = 1024, 3072
+    w = weights(O.TYPE_Q8_0, N, K, 0x5EED0010)
+    x = acts(0xAC700001, 1, K)
+    y = run_mul_mat(mx, be, O.TYPE_Q8_0, w, x, K, N)
+    y_ref = O.mul_mat(O.TYPE_Q8_0, w, x)
+    assert rel_err(y, y_ref) <= TIGHT
+    assert l2_rel(y, y_ref) <= TIGHT
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+def test_mul_mat_x86_rounding(mx, be, t):
+    K, N, M = 512, 64, 3
+    w = weights(t, N, K, 0x5EED0600 + t)
+    x = np.concatenate([acts(0xAC700600, M, K), special_rows(K)[2:3]])
+    be.set_rounding(mx.ROUND_X86)
+    try:
+        y = run_mul_mat(mx, be, t, w, x, K, N)
+    finally:
+        be.set_rounding(mx.ROUND_REF)
+    assert rel_err(y, O.mul_mat(t, w, x, rounding=O.ROUND_X86)) <= TIGHT
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+def test_mul_mat_batched_broadcast(mx, be, t):
+    # src0 [K, N, 2, 1], src1 [K, M, 4, 2]: r2 = 2, r3 = 2 (ggml broadcast of src0 over src1's batch axes)
+    K, N, M = 256, 40, 2
+    w = weights(t, N * 2, K, 0x5EED0700 + t)
+    x = acts(0xAC700700, M * 4 * 2, K).reshape(2, 4, M, K)
+    W = be.tensor(t, (K, N, 2, 1), w)
+    X = be.tensor(mx.F32, (K, M, 4, 2), x)
+    Y = be.tensor(mx.F32, (N, M, 4, 2))
+    be.mul_mat(W, X, Y)
+    be.sync()
+    y = Y.numpy()
+    for i3 in range(2):
+        for i2 in range(4):
+            wm = w[(i2 // 2) * N:(i2 // 2 + 1) * N]
+            assert rel_err(y[i3, i2], O.mul_mat(t, wm, x[i3, i2])) <= TIGHT
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+def test_mul_mat_group(mx, be, t):
+    # q / k / v of one layer share src1: one launch, three results
+    K, M = 1024, 2
+    Ns = [256, 128, 128]
+    ws = [weights(t, n, K, 0x5EED0800 + i + t) for i, n in enumerate(Ns)]
+    x = acts(0xAC700800, M, K)
+    W = [be.tensor(t, (K, n), w) for n, w in zip(Ns, ws)]
+    X = be.tensor(mx.F32, (K, M), x)
+    Y = [be.tensor(mx.F32, (n, M)) for n in Ns]
+    be.mul_mat_group(W, X, Y)
+    be.sync()
+    for n, w, yt in zip(Ns, ws, Y):
+        assert rel_err(yt.numpy().reshape(M, n), O.mul_mat(t, w, x)) <= TIGHT
+
+
+def test_supports_op(mx, be):
+    W = be.tensor(mx.Q4_K, (300 // 256 * 256 + 256, 4))
+    X = be.tensor(mx.F32, (W.ne[0], 1))
+    Y = be.tensor(mx.F32, (4, 1))
+    assert be.supports(mx.OP_MUL_MAT, W, X, None, Y)
+    Xbad = be.tensor(mx.F32, (W.ne[0] - 256, 1))
+    assert not be.supports(mx.OP_MUL_MAT, W, Xbad, None, Y)
+    F = be.tensor(mx.F32, (W.ne[0], 4))
+    assert not be.supports(mx.OP_MUL_MAT, F, X, None, Y)   # F32 weights stay on the CPU backend
+
+
+# --------------------------------------------------------------------------------------------------- MUL_MAT_ID
+def mmid_case(mx, be, t, E, K, N, n_ids, T, bcast, seed):
+    w = weights(t, E * N, K, seed).reshape(E, N, -1)
+    B = 1 if bcast else n_ids
+    x = acts(seed + 1, T * B, K).reshape(T, B, K)
+    rng = np.random.default_rng(seed)
+    logits = rng.standard_normal((T, E))
+    ids = np.argsort(-logits, axis=1)[:, :n_ids].astype(np.int32)
+    Wt = be.tensor(t, (K, N, E), w.reshape(E * N, -1))
+    Xt = be.tensor(mx.F32, (K, B, T), x)
+    It = be.tensor(mx.I32, (n_ids, T), ids)
+    Yt = be.tensor(mx.F32, (N, n_ids, T))
+    be.mul_mat_id(Wt, Xt, It, Yt)
+    be.sync()
+    y = Yt.numpy().reshape(T, n_ids, N)
+    return y, O.mul_mat_id(t, w, x, ids)
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("T", [1, 3, 16, 40])
+@pytest.mark.parametrize("bcast", [True, False], ids=["b_bcast", "b_per_slot"])
+def test_mul_mat_id(mx, be, t, T, bcast):
+    y, y_ref = mmid_case(mx, be, t, E=8, K=512, N=96, n_ids=2, T=T, bcast=bcast, seed=0x5EED0900 + T + t)
+    assert rel_err(y, y_ref) <= TIGHT
+
+
+def test_mul_mat_id_bad_expert(mx, be):
+    K, N, E = 256, 32, 4
+    Wt = be.tensor(mx.Q8_0, (K, N, E), weights(O.TYPE_Q8_0, E * N, K, 9))
+    Xt = be.tensor(mx.F32, (K, 1, 2), acts(10, 2, K))
+    It = be.tensor(mx.I32, (2, 2), np.array([[0, 1], [3, E]], np.int32))
+    Yt = be.tensor(mx.F32, (N, 2, 2))
+    be.mul_mat_id(Wt, Xt, It, Yt)
+    with pytest.raises(mx.MxError) as e:
+        be.sync()
+    assert e.value.code == mx.INVALID
+    be.sync()
+
+
+# ------------------------------------------------------------------------------------------------------- graphs
+def test_graph_replay_matches_eager(mx, be):
+    K, N, R = 1024, 512, 16
+    tab = weights(O.TYPE_Q8_0, R, K, 21)
+    w = weights(O.TYPE_Q8_0, N, K, 22)
+    T = be.tensor(mx.Q8_0, (K, R), tab)
+    W = be.tensor(mx.Q8_0, (K, N), w)
+    I = be.tensor(mx.I32, (1,), np.array([3], np.int32))
+    X = be.tensor(mx.F32, (K, 1))
+    Y = be.tensor(mx.F32, (N, 1))
+    be.get_rows(T, I, X)
+    be.mul_mat(W, X, Y)
+    be.sync()
+    be.graph_begin()
+    be.get_rows(T, I, X)
+    be.mul_mat(W, X, Y)
+    g = be.graph_end()
+    try:
+        for tok in [5, 0, 15, 5]:
+            I.set(np.array([tok], np.int32))
+            be.graph_launch(g)
+            be.sync()
+            x_ref = O.get_rows(O.TYPE_Q8_0, tab, K, np.array([tok], np.int32))
+            assert bits_equal(X.numpy().reshape(1, K), x_ref)
+            assert rel_err(Y.numpy().reshape(1, N), O.mul_mat(O.TYPE_Q8_0, w, x_ref)) <= TIGHT
+    finally:
+        be.graph_free(g)
