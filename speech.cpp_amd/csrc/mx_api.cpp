@@ -449,7 +449,6 @@ static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, con
     a.rounding = be->rounding;
     a.K = w0->ne[0];
     a.x_col_stride = (int64_t)(src1->nb[1] / 4);
-    a.y_col_stride = (int64_t)(dst[0]->nb[1] / 4);
     a.ne12 = src1->ne[2];
     a.ne13 = src1->ne[3];
     a.ne02 = w0->ne[2];
@@ -470,7 +469,8 @@ static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, con
             a.prob[i].w = mx::wplanes(src0[i]->data, pl);
             a.prob[i].N = src0[i]->ne[1];
             a.prob[i].row0 = 0;
-            a.prob[i].y = (float *)dst[i]->data + m0 * a.y_col_stride;
+            a.prob[i].y_col_stride = (int64_t)(dst[i]->nb[1] / 4);
+            a.prob[i].y = (float *)dst[i]->data + m0 * a.prob[i].y_col_stride;
         }
         HIP_OK(mx::launch_matvec(a, be->stream), "MUL_MAT launch");
     }
@@ -495,7 +495,7 @@ MX_API int mx_mul_mat_group(mx_backend *be, int n, const mx_tensor *const *src0,
         if (!mx_supports_op(MX_OP_MUL_MAT, src0[i], src1, nullptr, dst[i]))
             return fail(MX_UNSUPPORTED, "MUL_MAT group member %d: unsupported types, shapes or strides", i);
         if (src0[i]->type != src0[0]->type || src0[i]->ne[2] != 1 || src0[i]->ne[3] != 1 || src1->ne[2] != 1 ||
-            src1->ne[3] != 1 || dst[i]->nb[1] != dst[0]->nb[1])
+            src1->ne[3] != 1)
             return fail(MX_UNSUPPORTED, "MUL_MAT group members must be 2-D products of one weight type");
     }
     for (int i0 = 0; i0 < n; i0 += 4) {

@@ -141,6 +141,7 @@ struct MatvecProblem {
     int64_t N;             // rows of the matrix (outputs)
     int64_t row0;          // first row of the matrix within the tensor's planes
     float *y;              // dst column 0 of this problem
+    int64_t y_col_stride;  // floats between its dst columns
 };
 struct MatvecArgs {
     int type;
@@ -149,7 +150,6 @@ struct MatvecArgs {
     int64_t K;
     const float *x;        // src1 column 0 of batch slice (0, 0)
     int64_t x_col_stride;  // floats between columns
-    int64_t y_col_stride;  // floats between dst columns
     // batch slices (grid.z = ne12 * ne13): matrix (i12 / r2, i13 / r3) of src0 meets slice (i12, i13) of src1
     int64_t ne12, ne13, ne02, r2, r3;
     int64_t x_b2, x_b3, y_b2, y_b3;  // float strides of src1 / dst slices

@@ -43,34 +43,78 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t
     }
 }
 
-// acc[col] += contribution of chunk c of weight row `grow` (global row index within the tensor's planes).
+// The weight bytes of one chunk, loaded ahead of the arithmetic so the loads of several chunks (and of the activation
+// prologue) are in flight together.
+template <int TYPE>
+struct WChunk;
+template <>
+struct WChunk<MX_TYPE_Q8_0> {
+    int4 q;        // 16 quants
+    uint32_t d;    // fp16 scale of their block (low half)
+};
+template <>
+struct WChunk<MX_TYPE_Q4_K> {
+    int4 q;        // 32 nibbles: 16 of sub-block j, 16 of sub-block j + 1
+    uint32_t s0, s1, s2;  // the 12 packed scale / min bytes
+    uint32_t dm;   // fp16 d | fp16 dmin << 16
+};
+template <>
+struct WChunk<MX_TYPE_Q6_K> {
+    int4 ql, qh;
+    uint32_t sc;   // the two int8 sub-block scales in bytes 0 and 1
+    uint32_t d;    // fp16 d (low half)
+};
+
+template <int TYPE>
+__device__ __forceinline__ WChunk<TYPE> load_chunk(const WPlanes &w, int64_t grow, int64_t K, int c) {
+    WChunk<TYPE> r;
+    if constexpr (TYPE == MX_TYPE_Q8_0) {
+        r.q = *(const int4 *)(w.p0 + grow * K + 16 * c);
+        r.d = *(const uint16_t *)(w.p1 + (grow * (K / 32) + (c >> 1)) * 2);
+    } else if constexpr (TYPE == MX_TYPE_Q4_K) {
+        const int64_t blk = grow * (K / 256) + (c >> 3);
+        r.q = *(const int4 *)(w.p0 + blk * 128 + 16 * (c & 7));
+        const uint32_t *sp = (const uint32_t *)(w.p1 + blk * 12);
+        r.s0 = sp[0];
+        r.s1 = sp[1];
+        r.s2 = sp[2];
+        r.dm = *(const uint32_t *)(w.p2 + blk * 4);
+    } else {
+        const int64_t blk = grow * (K / 256) + (c >> 3);
+        const int t = c & 7, h = t >> 2, u = t & 3;
+        r.ql = *(const int4 *)(w.p0 + blk * 128 + 64 * h + 16 * u);
+        r.qh = *(const int4 *)(w.p1 + blk * 64 + 32 * h + 16 * (u & 1));
+        const int lo_sc = 8 * h + 2 * (u >> 1) + (u & 1);  // (128h + 32(u>>1) + 16(u&1)) / 16
+        const uint8_t *sp = w.p2 + blk * 16;
+        r.sc = (uint32_t)sp[lo_sc] | ((uint32_t)sp[lo_sc + 4] << 8);
+        r.d = *(const uint16_t *)(w.p3 + blk * 2);
+    }
+    return r;
+}
+
+// acc[col] += contribution of chunk c (whose bytes are in `wc`) against the activation columns in LDS.
 template <int TYPE, int NC, bool GUARD>
-__device__ __forceinline__ void chunk_dot(const WPlanes &w, int64_t grow, int64_t K, int c, const int8_t *xq,
+__device__ __forceinline__ void dot_chunk(const WChunk<TYPE> &wc, int64_t K, int c, const int8_t *xq,
                                           const float *xd, const int *xbs, int ncols, float *acc) {
-    if (TYPE == MX_TYPE_Q8_0) {
+    if constexpr (TYPE == MX_TYPE_Q8_0) {
         const int64_t nblk = K / 32;
-        const int4 wq = *(const int4 *)(w.p0 + grow * K + 16 * c);
-        const float dw = h2f(*(const uint16_t *)(w.p1 + (grow * nblk + (c >> 1)) * 2));
+        const float dw = h2f((uint16_t)wc.d);
 #pragma unroll
         for (int col = 0; col < NC; col++) {
             if (GUARD && col >= ncols) break;
             const int4 xv = *(const int4 *)(xq + col * K + 16 * c);
-            const int s = dot16(wq, xv, 0);
+            const int s = dot16(wc.q, xv, 0);
             acc[col] += (float)s * (dw * xd[col * nblk + (c >> 1)]);
         }
-    } else if (TYPE == MX_TYPE_Q4_K) {
+    } else if constexpr (TYPE == MX_TYPE_Q4_K) {
         const int64_t nsb = K / 256;
         const int sb = c >> 3, t = c & 7;
-        const int64_t blk = grow * nsb + sb;
-        const int4 q = *(const int4 *)(w.p0 + blk * 128 + 16 * t);
-        const uint32_t *sp = (const uint32_t *)(w.p1 + blk * 12);
-        const uint32_t s0 = sp[0], s1 = sp[1], s2 = sp[2];
-        const uint32_t dm = *(const uint32_t *)(w.p2 + blk * 4);
-        const float d = h2f((uint16_t)(dm & 0xFFFF)), dmin = h2f((uint16_t)(dm >> 16));
+        const float d = h2f((uint16_t)(wc.dm & 0xFFFF)), dmin = h2f((uint16_t)(wc.dm >> 16));
         const int jlo = 2 * (t >> 1);
         int sc_lo, m_lo, sc_hi, m_hi;
-        q4k_scale_min(s0, s1, s2, jlo, sc_lo, m_lo);
-        q4k_scale_min(s0, s1, s2, jlo + 1, sc_hi, m_hi);
+        q4k_scale_min(wc.s0, wc.s1, wc.s2, jlo, sc_lo, m_lo);
+        q4k_scale_min(wc.s0, wc.s1, wc.s2, jlo + 1, sc_hi, m_hi);
+        const int4 q = wc.q;
         const int4 qlo = make_int4(q.x & 0x0F0F0F0F, q.y & 0x0F0F0F0F, q.z & 0x0F0F0F0F, q.w & 0x0F0F0F0F);
         const int4 qhi = make_int4((q.x >> 4) & 0x0F0F0F0F, (q.y >> 4) & 0x0F0F0F0F, (q.z >> 4) & 0x0F0F0F0F,
                                    (q.w >> 4) & 0x0F0F0F0F);
@@ -91,10 +135,8 @@ __device__ __forceinline__ void chunk_dot(const WPlanes &w, int64_t grow, int64_
         const int64_t nsb = K / 256;
         const int sb = c >> 3, t = c & 7;
         const int h = t >> 2, u = t & 3;
-        const int64_t blk = grow * nsb + sb;
-        const int4 ql = *(const int4 *)(w.p0 + blk * 128 + 64 * h + 16 * u);
-        const int4 qh = *(const int4 *)(w.p1 + blk * 64 + 32 * h + 16 * (u & 1));
         const int sh = 2 * (u >> 1);
+        const int4 ql = wc.ql, qh = wc.qh;
         const int4 qlo = make_int4((ql.x & 0x0F0F0F0F) | (((qh.x >> sh) & 0x03030303) << 4),
                                    (ql.y & 0x0F0F0F0F) | (((qh.y >> sh) & 0x03030303) << 4),
                                    (ql.z & 0x0F0F0F0F) | (((qh.z >> sh) & 0x03030303) << 4),
@@ -103,11 +145,10 @@ __device__ __forceinline__ void chunk_dot(const WPlanes &w, int64_t grow, int64_
                                    ((ql.y >> 4) & 0x0F0F0F0F) | (((qh.y >> (sh + 4)) & 0x03030303) << 4),
                                    ((ql.z >> 4) & 0x0F0F0F0F) | (((qh.z >> (sh + 4)) & 0x03030303) << 4),
                                    ((ql.w >> 4) & 0x0F0F0F0F) | (((qh.w >> (sh + 4)) & 0x03030303) << 4));
-        const int lo_in = 128 * h + 32 * (u >> 1) + 16 * (u & 1);  // element offset within the super-block
-        const int sc_lo = (int)(int8_t)w.p2[blk * 16 + (lo_in >> 4)];
-        const int sc_hi = (int)(int8_t)w.p2[blk * 16 + (lo_in >> 4) + 4];
-        const float d = h2f(*(const uint16_t *)(w.p3 + blk * 2));
-        const int lo_off = sb * 256 + lo_in;
+        const int sc_lo = (int)(int8_t)(wc.sc & 0xFF);
+        const int sc_hi = (int)(int8_t)((wc.sc >> 8) & 0xFF);
+        const float d = h2f((uint16_t)wc.d);
+        const int lo_off = sb * 256 + 128 * h + 32 * (u >> 1) + 16 * (u & 1);
 #pragma unroll
         for (int col = 0; col < NC; col++) {
             if (GUARD && col >= ncols) break;
@@ -120,6 +161,13 @@ __device__ __forceinline__ void chunk_dot(const WPlanes &w, int64_t grow, int64_
             acc[col] += (d * xd[col * nsb + sb]) * (float)isum;
         }
     }
+}
+
+// acc[col] += contribution of chunk c of weight row `grow` (global row index within the tensor's planes).
+template <int TYPE, int NC, bool GUARD>
+__device__ __forceinline__ void chunk_dot(const WPlanes &w, int64_t grow, int64_t K, int c, const int8_t *xq,
+                                          const float *xd, const int *xbs, int ncols, float *acc) {
+    dot_chunk<TYPE, NC, GUARD>(load_chunk<TYPE>(w, grow, K, c), K, c, xq, xd, xbs, ncols, acc);
 }
 
 // Quantize `ncols` columns of f32 activations into LDS with 256 threads. For Q8_0 weights: 32-blocks (d rounded to

@@ -75,3 +75,17 @@ def test_generator_matches_oracle(mx):
     assert np.array_equal(a, O.fill_normal(0x5EED0010, 7, 1001, 0.0, 0.02))
     q = mx.quantize_normal(mx.Q6_K, 99, 16, 512, 0.02, nthreads=3)
     assert np.array_equal(q, O.quantize_chunk(O.TYPE_Q6_K, O.fill_normal(99, 16, 512, 0.0, 0.02)))
+
+
+@pytest.mark.parametrize("name,t", [("q4_K_grid.json", O.TYPE_Q4_K), ("q6_K_grid.json", O.TYPE_Q6_K)])
+def test_host_quantizer_known_answer_blocks(mx, name, t):
+    import json
+    f = json.loads((ROOT / "tests" / "golden" / name).read_text())
+    x = np.array(f["x"], np.float32)[None]
+    assert mx.quantize_chunk(t, x)[0].tobytes().hex() == f["block"]
+
+
+def test_host_q8_0_exact_blocks(mx):
+    import json
+    for c in json.loads((ROOT / "tests" / "golden" / "q8_0_exact.json").read_text()):
+        assert mx.quantize_chunk(mx.Q8_0, np.array(c["x"], np.float32)[None])[0].tobytes().hex() == c["block"]

@@ -1,0 +1,319 @@
+"""Pins of the CPU oracle (oracle/mx_oracle.c), each against something other than the oracle's own formula.
+
+ggml is not available to run (an empty submodule in the reference), and the reference's own tests of this path need
+model files and dumps that are not in its tree, so the oracle is pinned by:
+  * IEEE binary16 as numpy implements it (every fp16 value, every midpoint, the overflow edge);
+  * known-answer blocks whose bytes follow from the block layout and arithmetic alone (tests/golden/, written by
+    tests/golden/make_golden.py without the oracle);
+  * an independent numpy decoder of every block layout, compared bit for bit with the oracle's dequantizers;
+  * exact float64 brute force over independently decoded values for every dot, MUL_MAT, MUL_MAT_ID and GET_ROWS;
+  * invariants (bsums = sums of quants, quantize(dequantize(b)) == b for full-range Q8_0 blocks);
+  * mutation checks: a plausible mistake (swapped nibbles, a dropped min term, a wrong scale index) fails the checks.
+Parity unpinned: the candidate searches inside make_qkx2_quants / make_qx_quants on generic data (only an import of
+ggml could fix those bytes); the grid fixtures pin everything around them, and the kernels read whatever bytes the
+quantizer wrote, so their parity does not depend on it.
+"""
+import json
+import pathlib
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLD = pathlib.Path(__file__).resolve().parent / "golden"
+
+
+def gold(name):
+    return json.loads((GOLD / name).read_text())
+
+
+def h2f(bits):
+    return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+# ---------------------------------------------------------------------------------------------- independent decoders
+def decode(t, blocks: np.ndarray) -> np.ndarray:
+    """Exact values (float64) of ggml blocks, written from ggml-common.h's layout comments."""
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1, O.TSIZE[t])
+    if t == O.TYPE_Q8_0:
+        d = h2f(b[:, 0:2].copy().view(np.uint16)[:, 0]).astype(np.float64)
+        q = b[:, 2:34].view(np.int8).astype(np.float64)
+        return (d[:, None] * q).reshape(-1)
+    if t == O.TYPE_Q4_K:
+        d = h2f(b[:, 0:2].copy().view(np.uint16)[:, 0]).astype(np.float64)
+        dmin = h2f(b[:, 2:4].copy().view(np.uint16)[:, 0]).astype(np.float64)
+        s = b[:, 4:16].astype(np.int64)
+        sc = np.zeros((len(b), 8), np.int64)
+        mn = np.zeros((len(b), 8), np.int64)
+        sc[:, :4] = s[:, 0:4] & 63
+        mn[:, :4] = s[:, 4:8] & 63
+        sc[:, 4:] = (s[:, 8:12] & 0xF) | ((s[:, 0:4] >> 6) << 4)
+        mn[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+        qs = b[:, 16:144].astype(np.int64)
+        out = np.zeros((len(b), 256))
+        for e in range(256):
+            byte = qs[:, (e // 64) * 32 + e % 32]
+            q = (byte >> 4) if (e // 32) % 2 else (byte & 0xF)
+            out[:, e] = d * sc[:, e // 32] * q - dmin * mn[:, e // 32]
+        return out.reshape(-1)
+    if t == O.TYPE_Q6_K:
+        ql = b[:, 0:128].astype(np.int64)
+        qh = b[:, 128:192].astype(np.int64)
+        sc = b[:, 192:208].view(np.int8).astype(np.float64)
+        d = h2f(b[:, 208:210].copy().view(np.uint16)[:, 0]).astype(np.float64)
+        out = np.zeros((len(b), 256))
+        for e in range(256):
+            h, r = divmod(e, 128)
+            quarter, l = divmod(r, 32)
+            lb = ql[:, 64 * h + l + 32 * (quarter & 1)]
+            lo = (lb & 0xF) if quarter < 2 else (lb >> 4)
+            hb = (qh[:, 32 * h + l] >> (2 * quarter)) & 3
+            out[:, e] = d * sc[:, e // 16] * ((lo | (hb << 4)) - 32)
+        return out.reshape(-1)
+    if t == O.TYPE_Q8_K:
+        d = b[:, 0:4].copy().view(np.float32)[:, 0].astype(np.float64)
+        q = b[:, 4:260].view(np.int8).astype(np.float64)
+        return (d[:, None] * q).reshape(-1)
+    raise ValueError(t)
+
+
+# ------------------------------------------------------------------------------------------------------------- fp16
+def test_fp16_to_fp32_every_value():
+    L = O.lib()
+    for h in range(65536):
+        ref = np.array([h], np.uint16).view(np.float16).astype(np.float32)[0]
+        got = L.orc_fp16_to_fp32(h)
+        if np.isnan(ref):
+            assert np.isnan(got)
+        else:
+            assert np.float32(got).view(np.uint32) == ref.view(np.uint32), hex(h)
+
+
+def test_fp32_to_fp16_rne_against_numpy():
+    L = O.lib()
+    finite = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    vals = [finite, -finite]
+    # midpoints between consecutive fp16 values (ties go to even) and one fp32 ulp either side of them
+    mids = ((finite[:-1].astype(np.float64) + finite[1:].astype(np.float64)) / 2).astype(np.float32)
+    vals += [mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(0))]
+    vals.append(np.array([65504.0, 65519.996, 65520.0, 7e4, 1e-8, 2.9802322e-08, 2.9802326e-08, 5.9604645e-08,
+                          np.inf, 1e-40, 3e-38], np.float32))
+    rng = np.random.default_rng(0)
+    vals.append((rng.standard_normal(200000) * 10.0 ** rng.uniform(-9, 5, 200000)).astype(np.float32))
+    x = np.concatenate(vals).astype(np.float32)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    got = np.array([L.orc_fp32_to_fp16(float(v)) for v in x], np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ------------------------------------------------------------------------------------------------ golden fixtures
+def test_q8_0_exact_blocks():
+    for c in gold("q8_0_exact.json"):
+        x = np.array(c["x"], np.float32)[None]
+        for r in (O.ROUND_REF, O.ROUND_X86):
+            assert O.quantize_rows(O.TYPE_Q8_0, x, r)[0].tobytes().hex() == c["block"]
+        blk = np.frombuffer(bytes.fromhex(c["block"]), np.uint8)
+        assert np.array_equal(O.dequantize_rows(O.TYPE_Q8_0, blk[None], 32)[0], np.array(c["dequant"], np.float32))
+
+
+def test_q8_rounding_ties():
+    f = gold("q8_ties.json")
+    x = np.array(f["x"], np.float32)[None]
+    assert O.quantize_rows(O.TYPE_Q8_0, x, O.ROUND_REF)[0].tobytes().hex() == f["ref_block"]
+    assert O.quantize_rows(O.TYPE_Q8_0, x, O.ROUND_X86)[0].tobytes().hex() == f["x86_block"]
+    q81 = O.quantize_rows(O.TYPE_Q8_1, x, O.ROUND_REF)[0]
+    ref = bytes.fromhex(f["ref_block"])
+    assert q81[0:2].tobytes() == ref[0:2] and q81[4:].tobytes() == ref[2:]
+    s = int(np.frombuffer(ref[2:], np.int8).astype(np.int64).sum())
+    assert q81[2:4].view(np.uint16)[0] == np.float32(s * 1.0).astype(np.float16).view(np.uint16)  # s = d * sum, d = 1
+
+
+def test_q8_K_first_of_tied_maxima():
+    f = gold("q8_K_ties.json")
+    x = np.array(f["x"], np.float32)[None]
+    assert O.quantize_rows(O.TYPE_Q8_K, x)[0].tobytes().hex() == f["block"]
+    # mutation: letting the later +3 set the scale flips every sign, which the fixture rejects
+    flipped = O.quantize_rows(O.TYPE_Q8_K, -x)[0].tobytes().hex()
+    assert flipped != f["block"]
+
+
+@pytest.mark.parametrize("name,t", [("q4_K_grid.json", O.TYPE_Q4_K), ("q6_K_grid.json", O.TYPE_Q6_K)])
+def test_k_quant_grid_blocks(name, t):
+    f = gold(name)
+    x = np.array(f["x"], np.float32)[None]
+    blk = np.frombuffer(bytes.fromhex(f["block"]), np.uint8)
+    assert O.quantize_rows(t, x)[0].tobytes().hex() == f["block"]
+    assert O.quantize_chunk(t, x)[0].tobytes().hex() == f["block"]
+    deq = O.dequantize_rows(t, blk[None], 256)[0]
+    assert np.array_equal(deq, np.array(f["dequant"], np.float32))
+    assert np.array_equal(decode(t, blk), np.array(f["dequant"], np.float64))
+
+
+def test_grid_fixture_rejects_swapped_nibbles():
+    f = gold("q4_K_grid.json")
+    blk = bytearray.fromhex(f["block"])
+    for i in range(16, 144):
+        blk[i] = ((blk[i] & 0xF) << 4) | (blk[i] >> 4)
+    assert not np.array_equal(decode(O.TYPE_Q4_K, np.frombuffer(bytes(blk), np.uint8)), np.array(f["dequant"]))
+
+
+# ------------------------------------------------------------------------------------------ quantizer invariants
+def test_q8_K_bsums_and_range():
+    x = O.fill_normal(31, 8, 1024)
+    x[1] = 0.0
+    q = O.quantize_rows(O.TYPE_Q8_K, x).reshape(-1, 292)
+    qs = q[:, 4:260].view(np.int8).astype(np.int64)
+    bs = q[:, 260:292].copy().view(np.int16).astype(np.int64)
+    assert np.array_equal(qs.reshape(-1, 16, 16).sum(axis=2), bs)
+    assert qs.min() >= -128 and qs.max() <= 127
+    assert np.all(q[4:8, :4].view(np.float32) == 0)  # the zero row's four blocks have d = 0
+
+
+def test_q8_0_roundtrip_full_range_blocks():
+    rng = np.random.default_rng(8)
+    q = rng.integers(-127, 128, size=(64, 32))
+    q[:, 0] = 127
+    d = (2.0 ** rng.integers(-12, 2, size=64)).astype(np.float32)
+    blocks = np.concatenate([np.frombuffer(np.float16(di).tobytes(), np.uint8)[None].repeat(1, 0) for di in d])
+    raw = np.concatenate([blocks, q.astype(np.int8).view(np.uint8)], axis=1)
+    x = O.dequantize_rows(O.TYPE_Q8_0, raw.reshape(1, -1), 64 * 32)
+    assert np.array_equal(O.quantize_rows(O.TYPE_Q8_0, x).reshape(-1), raw.reshape(-1))
+
+
+def test_q8_matches_numpy_restatement():
+    """quantize_row_q8_0_ref / _q8_1_ref against vectorized numpy float32 arithmetic."""
+    x = np.concatenate([O.fill_normal(41, 16, 512), O.fill_normal(42, 2, 512) * np.float32(1e-5)])
+    xb = x.reshape(-1, 32)
+    amax = np.abs(xb).max(axis=1)
+    d = (amax / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idf = np.where(d != 0, np.float32(1) / d, np.float32(0)).astype(np.float32)
+        v = (xb * idf[:, None]).astype(np.float32)
+    q_ref = (np.sign(v) * np.floor(np.abs(v) + np.float32(0.5))).astype(np.int8)   # roundf: half away from zero
+    with np.errstate(divide="ignore"):
+        idx = np.where(amax != 0, np.float32(127) / amax, np.float32(0)).astype(np.float32)
+    q_x86 = np.rint((xb * idx[:, None]).astype(np.float32)).astype(np.int8)           # half to even
+    dh = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    for r, q in ((O.ROUND_REF, q_ref), (O.ROUND_X86, q_x86)):
+        want = np.concatenate([dh, q.view(np.uint8)], axis=1).reshape(-1)
+        assert np.array_equal(O.quantize_rows(O.TYPE_Q8_0, x, r).reshape(-1), want)
+        s = (q.astype(np.int64).sum(axis=1).astype(np.float32) * d).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        want1 = np.concatenate([dh, s, q.view(np.uint8)], axis=1).reshape(-1)
+        assert np.array_equal(O.quantize_rows(O.TYPE_Q8_1, x, r).reshape(-1), want1)
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K])
+def test_k_quant_weights_reconstruct(t):
+    """Validity of the weight quantizers on generic data: field ranges and a reconstruction error of a 4/6-bit fit."""
+    for std in (0.02, 1.0):
+        w = O.fill_normal(50 + t, 32, 1024, 0.0, std)
+        w[0] = 0.0
+        q = O.quantize_chunk(t, w)
+        deq = decode(t, q.reshape(-1))
+        assert np.all(deq[:1024] == 0)
+        err = np.sqrt(np.mean((deq - w.reshape(-1).astype(np.float64)) ** 2)) / std
+        assert err < (0.12 if t == O.TYPE_Q4_K else 0.03)
+        assert np.array_equal(O.dequantize_rows(t, q, 1024).reshape(-1), deq.astype(np.float32))
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K])
+def test_dequantizers_match_independent_decoder(t):
+    w = O.fill_normal(60 + t, 16, 512, 0.0, 0.02)
+    q = O.quantize_chunk(t, w)
+    assert np.array_equal(O.dequantize_rows(t, q, 512).reshape(-1), decode(t, q.reshape(-1)).astype(np.float32))
+
+
+def test_quantize_chunk_row_offsets():
+    w = O.fill_normal(70, 6, 512, 0.0, 0.02)
+    for t in (O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K):
+        full = O.quantize_chunk(t, w)
+        out = np.zeros_like(full)
+        L = O.lib()
+        rs = O.row_size(t, 512)
+        n = L.orc_quantize_chunk(t, w.ctypes.data, out.ctypes.data, 2 * 512, 3, 512)
+        assert n == 3 * rs
+        assert np.array_equal(out[2:5], full[2:5]) and not out[0].any() and not out[5].any()
+
+
+# ------------------------------------------------------------------------------------------- dots and ops, brute force
+def brute_dot(t, wq, aq):
+    return float(np.dot(decode(t, wq), decode(O.VEC_DOT_TYPE[t], aq)))
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K])
+def test_vec_dot_against_float64_brute_force(t):
+    K = 2048
+    w = O.quantize_chunk(t, O.fill_normal(80 + t, 8, K, 0.0, 0.02))
+    x = O.fill_normal(90, 4, K)
+    a = O.quantize_rows(O.VEC_DOT_TYPE[t], x)
+    for i in range(8):
+        for j in range(4):
+            exact = brute_dot(t, w[i], a[j])
+            scale = float(np.abs(decode(t, w[i])) @ np.abs(decode(O.VEC_DOT_TYPE[t], a[j])))
+            assert abs(O.vec_dot(t, K, w[i], a[j]) - exact) <= 1e-6 * scale
+            # scale products are fp32 in both variants (as ggml forms them): ~6e-8 relative per block
+            assert abs(O.vec_dot(t, K, w[i], a[j], exact=True) - exact) <= 2e-7 * scale
+
+
+def test_brute_force_catches_a_dropped_min_term():
+    """Mutation check: the Q4_K dot without its dmin term is far outside the bound the test above uses."""
+    K = 512
+    w = O.quantize_chunk(O.TYPE_Q4_K, O.fill_normal(81, 1, K, 0.0, 0.02))[0]
+    a = O.quantize_rows(O.TYPE_Q8_K, O.fill_normal(91, 1, K))[0]
+    wb = bytearray(w.tobytes())
+    wb[2:4] = b"\x00\x00"   # dmin = 0 in the first super-block drops its min term
+    scale = float(np.abs(decode(O.TYPE_Q4_K, w)) @ np.abs(decode(O.TYPE_Q8_K, a)))
+    assert abs(O.vec_dot(O.TYPE_Q4_K, K, np.frombuffer(bytes(wb), np.uint8), a) - brute_dot(O.TYPE_Q4_K, w, a)) > 1e-4 * scale
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K])
+def test_mul_mat_is_the_product_of_decoded_operands(t):
+    K, N, M = 512, 24, 5
+    w = O.quantize_chunk(t, O.fill_normal(100 + t, N, K, 0.0, 0.02))
+    x = O.fill_normal(101, M, K)
+    y = O.mul_mat(t, w, x)
+    W = decode(t, w.reshape(-1)).reshape(N, K)
+    X = decode(O.VEC_DOT_TYPE[t], O.quantize_rows(O.VEC_DOT_TYPE[t], x).reshape(-1)).reshape(M, K)
+    ref = X @ W.T
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("bcast", [True, False])
+def test_mul_mat_id_routes_each_pair(bcast):
+    t, K, N, E, k, T = O.TYPE_Q6_K, 256, 16, 5, 2, 4
+    w = O.quantize_chunk(t, O.fill_normal(110, E * N, K, 0.0, 0.02)).reshape(E, N, -1)
+    B = 1 if bcast else k
+    x = O.fill_normal(111, T * B, K).reshape(T, B, K)
+    ids = np.array([[4, 0], [1, 1], [2, 3], [0, 4]], np.int32)
+    y = O.mul_mat_id(t, w, x, ids)
+    for ti in range(T):
+        for s in range(k):
+            wi = decode(t, w[ids[ti, s]].reshape(-1)).reshape(N, K)
+            xi = decode(O.TYPE_Q8_K, O.quantize_rows(O.TYPE_Q8_K, x[ti, s % B][None]).reshape(-1))
+            ref = wi @ xi
+            assert np.abs(y[ti, s] - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K])
+def test_get_rows_is_the_decoded_row(t):
+    K, R = 512, 9
+    table = O.quantize_chunk(t, O.fill_normal(120 + t, R, K, 0.0, 0.02))
+    ids = np.array([8, 0, 3, 3], np.int32)
+    out = O.get_rows(t, table, K, ids)
+    for i, r in enumerate(ids):
+        assert np.array_equal(out[i], decode(t, table[r]).astype(np.float32))
+    with pytest.raises(ValueError):
+        O.get_rows(t, table, K, np.array([R], np.int32))
+
+
+def test_cpu_fast_port_agrees_with_oracle():
+    if not O.fast().cpf_have_avx2():
+        pytest.skip("no AVX2 on this host")
+    for t in (O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K):
+        w = O.quantize_chunk(t, O.fill_normal(130 + t, 70, 1024, 0.0, 0.02))
+        x = O.fill_normal(131, 3, 1024)
+        y = O.cpu_fast_mul_mat(t, w, x, 4)
+        ref = O.mul_mat(t, w, x, rounding=O.ROUND_X86)
+        assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
