@@ -159,6 +159,16 @@ struct MatvecArgs {
 };
 hipError_t launch_matvec(const MatvecArgs &a, hipStream_t s);
 
+// Prefill GEMM (M > 8): activations quantized once into scratch (gemm_act_bytes of quants, int8 or fp16 values by
+// gemm_mode(), plus M * K/32 fp32 block scales), then MFMA tiles.
+int gemm_mode();
+size_t gemm_act_bytes(int64_t M, int64_t K);
+hipError_t launch_gemm_quant(int type, int rounding, const float *x, int64_t x_stride, int64_t M, int64_t K,
+                             void *xq, float *xd, hipStream_t s);
+hipError_t launch_gemm(int type, const WPlanes &w, int64_t M, int64_t N, int64_t K, const void *xq, const float *xd,
+                       float *y, int64_t ldy, hipStream_t s);
+inline bool gemm_supported(int type, int64_t K) { return type == MX_TYPE_Q8_0 && K % 128 == 0; }
+
 // MUL_MAT_ID.
 struct MulMatIdArgs {
     int type;

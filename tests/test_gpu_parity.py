@@ -302,3 +302,29 @@ def test_graph_replay_matches_eager(mx, be):
             assert rel_err(Y.numpy().reshape(1, N), O.mul_mat(O.TYPE_Q8_0, w, x_ref)) <= TIGHT
     finally:
         be.graph_free(g)
+
+
+# ----------------------------------------------------------------------------------------------- MUL_MAT, M > 8
+@pytest.mark.parametrize("M,N,K", [(9, 100, 1024), (64, 256, 2048), (130, 333, 1024), (512, 2048, 2048),
+                                   (100, 64, 6144)])
+def test_mul_mat_gemm_q8_0(mx, be, M, N, K):
+    t = O.TYPE_Q8_0
+    w = weights(t, N, K, 0x5EED0A00 + M + N)
+    x = acts(0xAC700A00 + M, M, K)
+    y = run_mul_mat(mx, be, t, w, x, K, N)
+    assert rel_err(y, O.mul_mat(t, w, x)) <= TIGHT
+
+
+def test_mul_mat_gemm_batched(mx, be):
+    t, K, N, M = O.TYPE_Q8_0, 1024, 96, 40
+    w = weights(t, N * 2, K, 0x5EED0B00)
+    x = acts(0xAC700B00, M * 4, K).reshape(1, 4, M, K)
+    W = be.tensor(t, (K, N, 2, 1), w)
+    X = be.tensor(mx.F32, (K, M, 4, 1), x)
+    Y = be.tensor(mx.F32, (N, M, 4, 1))
+    be.mul_mat(W, X, Y)
+    be.sync()
+    y = Y.numpy()
+    for i2 in range(4):
+        wm = w[(i2 // 2) * N:(i2 // 2 + 1) * N]
+        assert rel_err(y[0, i2], O.mul_mat(t, wm, x[0, i2])) <= TIGHT
