@@ -115,31 +115,36 @@ class Model:
 
 def per_label_pass(be, launches, reps: int):
     """Mean kernel time (ms) per launch of each label: each label's launches (the 28 layers' instances, distinct
-    weights) are recorded as a graph of their own and replayed, so no event sits between two kernels."""
-    out = {}
+    weights) are recorded as a graph of their own and replayed, so no event sits between two kernels. All graphs are
+    recorded first and freed last."""
     labels = []
     for lab, _, _, _ in launches:
         if lab not in labels:
             labels.append(lab)
+    graphs = {}
+    for lab in labels:
+        be.graph_begin()
+        for l, _, _, fn in launches:
+            if l == lab:
+                fn()
+        graphs[lab] = be.graph_end()
+    out = {}
     e0, e1 = be.event(), be.event()
     for lab in labels:
-        fns = [fn for l, _, _, fn in launches if l == lab]
-        be.graph_begin()
-        for fn in fns:
-            fn()
-        g = be.graph_end()
+        count = sum(1 for l, _, _, _ in launches if l == lab)
         for _ in range(3):
-            be.graph_launch(g)
+            be.graph_launch(graphs[lab])
         be.sync()
         be.record(e0)
         for _ in range(reps):
-            be.graph_launch(g)
+            be.graph_launch(graphs[lab])
         be.record(e1)
         be.sync()
-        out[lab] = be.elapsed_ms(e0, e1) / (reps * len(fns))
-        be.graph_free(g)
+        out[lab] = be.elapsed_ms(e0, e1) / (reps * count)
     be.event_free(e0)
     be.event_free(e1)
+    for g in graphs.values():
+        be.graph_free(g)
     return out
 
 
@@ -175,6 +180,51 @@ def cpu_baseline(mx, model, seconds: float):
                       f"across {threads} threads"}
 
 
+COPY_BYTES = 256 << 20  # the plain copy the counters are calibrated on
+TRAFFIC_FILE = ROOT / "profiles" / "k_matvec_q8_0_qwen3-0.6b_decode.traffic.txt"
+
+
+def summarize_pmc(fetch_csv: str, write_csv: str) -> str:
+    """Per-dispatch HBM traffic of the step's mat-vecs from two rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE,
+    KiB per dispatch), each scaled by what the counter reads for the run's plain 256 MiB device copy."""
+    import csv
+    import statistics
+
+    def per_kernel(path, counter):
+        vals = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return vals
+
+    f = per_kernel(fetch_csv, "FETCH_SIZE")
+    w = per_kernel(write_csv, "WRITE_SIZE")
+    copy = [k for k in f if "copyBuffer" in k]
+    f_cal = max(max(f[k]) for k in copy) * 1024 / COPY_BYTES   # counter bytes per byte actually read
+    w_cal = max(max(w[k]) for k in copy if k in w) * 1024 / COPY_BYTES
+    mv = [k for k in f if "k_matvec" in k]
+    fetch = [v for k in mv for v in f[k]]
+    write = [v for k in mv for v in w.get(k, [])]
+    fb = statistics.mean(fetch) * 1024 / f_cal
+    wb = statistics.mean(write) * 1024 / w_cal if write else 0.0
+    lines = [f"kernel family: k_matvec<Q8_0,1,*> ({len(fetch)} dispatches)",
+             f"copy calibration: FETCH_SIZE reads {f_cal:.4f} x and WRITE_SIZE {w_cal:.4f} x the bytes of a "
+             f"{COPY_BYTES >> 20} MiB device copy",
+             f"fetch_bytes_per_launch: {fb:.0f}", f"write_bytes_per_launch: {wb:.0f}",
+             f"traffic_bytes_per_launch: {fb + wb:.0f}"]
+    return "\n".join(lines)
+
+
+def read_traffic():
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":")[1]))
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -182,7 +232,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 skips it)")
     ap.add_argument("--no-graph", action="store_true", help="replay the step eagerly instead of as a graph")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the traffic summary of two rocprofv3 --pmc runs of this benchmark and exit")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        print(summarize_pmc(*args.summarize_pmc))
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
         sys.exit(2)
@@ -212,6 +267,13 @@ def main():
         step_eager()
         graph = be.graph_end()
     step = (lambda: be.graph_launch(graph)) if graph else step_eager
+
+    # A plain device copy of known size: the reference the HBM traffic counters are calibrated on.
+    cp_src, cp_dst = be.tensor(mx.F32, (COPY_BYTES // 4,)), be.tensor(mx.F32, (COPY_BYTES // 4,))
+    mx.check(mx.lib().mx_tensor_copy(be.h, cp_src.ref(), cp_dst.ref()))
+    be.sync()
+    cp_src.free()
+    cp_dst.free()
 
     for _ in range(args.warmup):
         step()
@@ -250,13 +312,7 @@ def main():
     achieved = per_launch_bytes / (per_launch_ms * 1e-3) / 1e9
     dom = {"launches": mv_launches}
 
-    traffic = None
-    tfile = ROOT / "profiles" / "traffic.json"
-    if tfile.exists():
-        try:
-            traffic = json.loads(tfile.read_text()).get(dom_name)
-        except Exception:
-            traffic = None
+    traffic = read_traffic()
 
     tok_s = 1e3 / ms_per_step
     step_gbps = weight_bytes / (ms_per_step * 1e-3) / 1e9
