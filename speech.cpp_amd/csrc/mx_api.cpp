@@ -440,6 +440,18 @@ static int max_cols(int type, int64_t K) {
     return nc;
 }
 
+// The first planar row of matrix (i02, i03) of a weight, as plane pointers.
+static mx::WPlanes matrix_planes(const mx_tensor *w, int64_t mat) {
+    const mx::Planes pl = mx::planes_of(w->type, nelements(w));
+    mx::WPlanes p = mx::wplanes(w->data, pl);
+    const int64_t blocks = mat * w->ne[1] * (w->ne[0] / mx::type_info(w->type)->blk_elems);
+    p.p0 += blocks * pl.per_blk[0];
+    p.p1 += blocks * pl.per_blk[1];
+    if (p.p2) p.p2 += blocks * pl.per_blk[2];
+    if (p.p3) p.p3 += blocks * pl.per_blk[3];
+    return p;
+}
+
 // M > 8: quantize src1 once into scratch, then one MFMA GEMM per weight; batch slices one after another.
 static int gemm_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
                       const mx_tensor *const *dst) {
@@ -459,20 +471,35 @@ static int gemm_group(mx_backend *be, int n, const mx_tensor *const *src0, const
                                          be->stream),
                    "GEMM activation quantization");
             for (int i = 0; i < n; i++) {
-                const mx::Planes pl = mx::planes_of(src0[i]->type, nelements(src0[i]));
-                mx::WPlanes w = mx::wplanes(src0[i]->data, pl);
                 const int64_t N = src0[i]->ne[1];
-                const int64_t mat = i12 / r2 + (i13 / r3) * src0[i]->ne[2];
-                const int64_t rows0 = mat * N;  // first planar row of this matrix
-                const mx::TypeInfo *ti = mx::type_info(src0[i]->type);
-                const int64_t blk_per_row = K / ti->blk_elems;
-                w.p0 += rows0 * blk_per_row * pl.per_blk[0];
-                w.p1 += rows0 * blk_per_row * pl.per_blk[1];
-                if (w.p2) w.p2 += rows0 * blk_per_row * pl.per_blk[2];
-                if (w.p3) w.p3 += rows0 * blk_per_row * pl.per_blk[3];
+                const mx::WPlanes w = matrix_planes(src0[i], i12 / r2 + (i13 / r3) * src0[i]->ne[2]);
                 float *y = (float *)((uint8_t *)dst[i]->data + i12 * dst[i]->nb[2] + i13 * dst[i]->nb[3]);
                 HIP_OK(mx::launch_gemm(src0[i]->type, w, M, N, K, xq, xd, y, (int64_t)(dst[i]->nb[1] / 4), be->stream),
                        "GEMM launch");
+            }
+        }
+    return MX_SUCCESS;
+}
+
+// M > 8 on K-quant weights: per batch slice and weight, Q8_K activations into scratch and one MFMA GEMM.
+static int gemm_kq_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
+                         const mx_tensor *const *dst) {
+    const mx_tensor *w0 = src0[0];
+    const int64_t K = w0->ne[0], M = src1->ne[1];
+    int rc = ensure_scratch(be, mx::gemm_kq_act_bytes(M, K));
+    if (rc) return rc;
+    const int64_t r2 = src1->ne[2] / w0->ne[2], r3 = src1->ne[3] / w0->ne[3];
+    for (int64_t i13 = 0; i13 < src1->ne[3]; i13++)
+        for (int64_t i12 = 0; i12 < src1->ne[2]; i12++) {
+            const float *x = (const float *)((const uint8_t *)src1->data + i12 * src1->nb[2] + i13 * src1->nb[3]);
+            HIP_OK(mx::launch_gemm_kq_quant(x, (int64_t)(src1->nb[1] / 4), M, K, be->scratch, be->stream),
+                   "K-quant GEMM activation quantization");
+            for (int i = 0; i < n; i++) {
+                const int64_t mat = i12 / r2 + (i13 / r3) * src0[i]->ne[2];
+                float *y = (float *)((uint8_t *)dst[i]->data + i12 * dst[i]->nb[2] + i13 * dst[i]->nb[3]);
+                HIP_OK(mx::launch_gemm_kq(src0[i]->type, matrix_planes(src0[i], mat), M, src0[i]->ne[1], K, be->scratch,
+                                          y, (int64_t)(dst[i]->nb[1] / 4), be->stream),
+                       "K-quant GEMM launch");
             }
         }
     return MX_SUCCESS;
@@ -499,6 +526,7 @@ static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, con
     a.nprob = n;
     const int64_t M = src1->ne[1];
     if (M > mx::MAX_COLS && mx::gemm_supported(a.type, a.K)) return gemm_group(be, n, src0, src1, dst);
+    if (M > mx::MAX_COLS && mx::gemm_kq_supported(a.type, a.K)) return gemm_kq_group(be, n, src0, src1, dst);
     const int ncmax = max_cols(a.type, a.K);
     for (int64_t m0 = 0; m0 < M; m0 += ncmax) {
         a.ncols = (int)std::min<int64_t>(ncmax, M - m0);

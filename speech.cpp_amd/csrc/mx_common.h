@@ -169,6 +169,16 @@ hipError_t launch_gemm(int type, const WPlanes &w, int64_t M, int64_t N, int64_t
                        float *y, int64_t ldy, hipStream_t s);
 inline bool gemm_supported(int type, int64_t K) { return type == MX_TYPE_Q8_0 && K % 128 == 0; }
 
+// Prefill GEMM on Q4_K / Q6_K weights: launch_gemm_kq_quant writes x (M rows of K floats, row stride x_stride) as
+// Q8_K into `scratch` (gemm_kq_act_bytes), launch_gemm_kq multiplies it into y (row stride ldy).
+size_t gemm_kq_act_bytes(int64_t M, int64_t K);
+hipError_t launch_gemm_kq_quant(const float *x, int64_t x_stride, int64_t M, int64_t K, void *scratch, hipStream_t s);
+hipError_t launch_gemm_kq(int type, const WPlanes &w, int64_t M, int64_t N, int64_t K, const void *scratch, float *y,
+                          int64_t ldy, hipStream_t s);
+inline bool gemm_kq_supported(int type, int64_t K) {
+    return (type == MX_TYPE_Q4_K || type == MX_TYPE_Q6_K) && K % 256 == 0;
+}
+
 // MUL_MAT_ID.
 struct MulMatIdArgs {
     int type;

@@ -328,3 +328,56 @@ def test_mul_mat_gemm_batched(mx, be):
     for i2 in range(4):
         wm = w[(i2 // 2) * N:(i2 // 2 + 1) * N]
         assert rel_err(y[0, i2], O.mul_mat(t, wm, x[0, i2])) <= TIGHT
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("M,N,K", [(9, 100, 1024), (64, 256, 2048), (130, 333, 1536), (512, 1024, 3072),
+                                   (100, 64, 6144)])
+def test_mul_mat_gemm_kquant(mx, be, t, M, N, K):
+    w = weights(t, N, K, 0x5EED0C00 + M + N + t)
+    x = acts(0xAC700C00 + M, M, K)
+    y = run_mul_mat(mx, be, t, w, x, K, N)
+    assert rel_err(y, O.mul_mat(t, w, x)) <= TIGHT
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+def test_mul_mat_gemm_special_rows(mx, be, t):
+    """Zero, constant, tied and subnormal-scale activation rows through the M > 8 path."""
+    K, N = 1024, 160
+    w = weights(t, N, K, 0x5EED0D00 + t)
+    x = np.concatenate([special_rows(K), acts(0xAC700D00, 7, K)])
+    y = run_mul_mat(mx, be, t, w, x, K, N)
+    assert rel_err(y, O.mul_mat(t, w, x)) <= TIGHT
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
+def test_mul_mat_gemm_kquant_batched(mx, be, t):
+    """Broadcast batches: ne12 = 2 * ne02, each weight matrix serves two activation slices."""
+    K, N, M = 1536, 96, 33
+    w = weights(t, N * 2, K, 0x5EED0E00)
+    x = acts(0xAC700E00, M * 4, K).reshape(1, 4, M, K)
+    W = be.tensor(t, (K, N, 2, 1), w)
+    X = be.tensor(mx.F32, (K, M, 4, 1), x)
+    Y = be.tensor(mx.F32, (N, M, 4, 1))
+    be.mul_mat(W, X, Y)
+    be.sync()
+    y = Y.numpy()
+    for i2 in range(4):
+        wm = w[(i2 // 2) * N:(i2 // 2 + 1) * N]
+        assert rel_err(y[0, i2], O.mul_mat(t, wm, x[0, i2])) <= TIGHT
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
+def test_mul_mat_gemm_kquant_group(mx, be, t):
+    """Two weights sharing src1 (gate / up): one Q8_K quantization, two GEMMs."""
+    K, M = 2048, 70
+    Ns = (192, 130)
+    w = [weights(t, n, K, 0x5EED0F00 + n) for n in Ns]
+    x = acts(0xAC700F00, M, K)
+    W = [be.tensor(t, (K, n), wi) for n, wi in zip(Ns, w)]
+    X = be.tensor(mx.F32, (K, M), x)
+    Y = [be.tensor(mx.F32, (n, M)) for n in Ns]
+    be.mul_mat_group(W, X, Y)
+    be.sync()
+    for n, wi, Yi in zip(Ns, w, Y):
+        assert rel_err(Yi.numpy().reshape(M, n), O.mul_mat(t, wi, x)) <= TIGHT
