@@ -1,13 +1,21 @@
 #!/usr/bin/env python3
-"""Decode-step benchmark of libmx at the Qwen3-0.6B shape (one MI355X).
+"""Benchmarks of libmx's quantized products on one MI355X.
 
-A step is one decode token's pass of the hot path at the Qwen3-0.6B shape (the Qwen3-TTS 0.6B talker / Qwen3-ASR 0.6B
-text decoder): GET_ROWS of the token's row of the tied 151936 x 1024 Q8_0 embedding, then per layer (28) the q/k/v,
-attn_o, gate/up and down Q8_0 mat-vecs, then the 151936-row Q8_0 lm_head mat-vec -- 197 mat-vecs reading
+Default workload (`--workload decode`): the decode step at the Qwen3-0.6B shape (the Qwen3-TTS 0.6B talker / Qwen3-ASR
+0.6B text decoder). GET_ROWS of the token's row of the tied 151936 x 1024 Q8_0 embedding, then per layer (28) the
+q/k/v, attn_o, gate/up and down Q8_0 mat-vecs, then the 151936-row Q8_0 lm_head mat-vec -- 197 mat-vecs reading
 633,233,408 bytes of weights per token. Every weight tensor is distinct and lives in HBM; q/k/v and gate/up each run
 as one launch (they share their input). The ops between them (RMSNorm, RoPE, attention over the f16 KV cache, SwiGLU,
 argmax) stay on ggml's CPU backend in this design, so each mat-vec reads a synthetic N(0,1) activation vector resident
 in HBM. The step is recorded once as a graph and replayed.
+
+Other workloads (one JSON line each, same keys):
+  matvec       one Q8_0 MUL_MAT 3072 x 1024 at batch 1, rotated over 160 distinct copies of the weight (535 MB)
+  prefill-q4k  Qwen3-1.7B-shape talker prefill: 28 layers of Q4_K linears (Q6_K down), M = 512 rows
+  asr-1.7b     Qwen3-ASR-1.7B-shape Q8_0 prefill of 1564 rows in blocks {512, 512, 512, 28}, the head on the last
+               row, then 32 batch-1 decode tokens
+  moe          one Drama3-like MoE FFN layer (gate, up, down MUL_MAT_ID; 64 Q4_K experts, top-4 of a softmax router)
+               at token batches of 1, 16 and 256
 
 Prints one JSON line. --gpus N > 1 exits: this build runs on one GPU.
 """
@@ -26,10 +34,16 @@ import numpy as np
 ROOT = pathlib.Path(__file__).resolve().parent
 METRIC = "quant mat-vec weight GB/s (% HBM peak); decode tok/s at Qwen3-0.6B shape"
 HBM_PEAK_GBPS = 8000.0
+INT8_PEAK_TOPS = 5000.0   # dense int8 MFMA, MI355X
 
-# Qwen3-0.6B shape
-LAYERS, HIDDEN, FFN, NQ, NKV, HEAD_DIM, VOCAB = 28, 1024, 3072, 16, 8, 128, 151936
-Q8_0_ROW = lambda k: k // 32 * 34  # noqa: E731
+Q8_0, Q4_K, Q6_K = 8, 12, 14
+BLCK = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
+TSIZE = {Q8_0: 34, Q4_K: 144, Q6_K: 210}
+NAME = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+
+
+def row_bytes(t: int, k: int) -> int:
+    return k // BLCK[t] * TSIZE[t]
 
 
 def load_mx():
@@ -44,94 +58,52 @@ def load_mx():
     return mod
 
 
-def layer_shapes():
-    """(name, K, N) of one layer's linears, ggml order: W [K, N]."""
-    q, kv = NQ * HEAD_DIM, NKV * HEAD_DIM
-    return [("q", HIDDEN, q), ("k", HIDDEN, kv), ("v", HIDDEN, kv), ("o", q, HIDDEN), ("gate", HIDDEN, FFN),
-            ("up", HIDDEN, FFN), ("down", FFN, HIDDEN)]
-
-
-def weight_seed(layer: int, idx: int) -> int:
-    return 0x5EED0000 + 2 * 16 + layer * 16 + idx
+def load_oracle():
+    sys.path.insert(0, str(ROOT))
+    import oracle as O
+    return O
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-class Model:
-    """The decode step's tensors on the device, built from seeded synthetic weights."""
+def weight_seed(config: int, layer: int, idx: int) -> int:
+    return 0x5EED0000 + config * 16 + layer * 16 + idx
 
-    def __init__(self, mx, be, threads: int):
-        self.mx, self.be = mx, be
-        t0 = time.time()
-        self.host = {}
-        self.layers = []
-        for l in range(LAYERS):
-            ws = {}
-            for i, (name, K, N) in enumerate(layer_shapes()):
-                q = mx.quantize_normal(mx.Q8_0, weight_seed(l, i), N, K, 0.02, nthreads=threads)
-                ws[name] = be.tensor(mx.Q8_0, (K, N), q)
-                self.host[(l, name)] = q
-            self.layers.append(ws)
-        head = mx.quantize_normal(mx.Q8_0, weight_seed(LAYERS, 0), VOCAB, HIDDEN, 0.02, nthreads=threads)
-        self.embd = be.tensor(mx.Q8_0, (HIDDEN, VOCAB), head)
-        self.host["embd"] = head
-        log(f"weights generated and uploaded in {time.time() - t0:.1f} s")
-        # activations: the token id, its embedding row, and one synthetic input per mat-vec of every layer
-        self.ids = be.tensor(mx.I32, (1,), np.array([4242], np.int32))
-        self.x0 = be.tensor(mx.F32, (HIDDEN, 1))
-        self.acts = []
-        for l in range(LAYERS):
-            a = {}
-            for j, (name, K) in enumerate([("attn_out", NQ * HEAD_DIM), ("ffn_in", HIDDEN), ("ffn_act", FFN),
-                                           ("final", HIDDEN)]):
-                a[name] = be.tensor(mx.F32, (K, 1), mx.fill_normal(0xAC700002 + 16 * l + j, 1, K))
-            self.acts.append(a)
-        self.outs = []
-        for l in range(LAYERS):
-            self.outs.append({name: be.tensor(mx.F32, (N, 1)) for name, K, N in layer_shapes()})
-        self.logits = be.tensor(mx.F32, (VOCAB, 1))
 
-    def launches(self):
-        """The step as a list of (label, K, weight bytes, callable)."""
-        be, L = self.be, []
-        L.append(("get_rows", HIDDEN, Q8_0_ROW(HIDDEN), lambda: be.get_rows(self.embd, self.ids, self.x0)))
-        for l in range(LAYERS):
-            w, o, a = self.layers[l], self.outs[l], self.acts[l]
-            x_in = self.x0 if l == 0 else a["final"]  # layer 0 reads the embedding row GET_ROWS produced
-            L.append(("qkv", HIDDEN, sum(Q8_0_ROW(w[n].ne[0]) * w[n].ne[1] for n in ("q", "k", "v")),
-                      lambda w=w, o=o, x=x_in: be.mul_mat_group([w["q"], w["k"], w["v"]], x, [o["q"], o["k"], o["v"]])))
-            L.append(("attn_o", NQ * HEAD_DIM, Q8_0_ROW(w["o"].ne[0]) * w["o"].ne[1],
-                      lambda w=w, o=o, a=a: be.mul_mat(w["o"], a["attn_out"], o["o"])))
-            L.append(("gate_up", HIDDEN, sum(Q8_0_ROW(w[n].ne[0]) * w[n].ne[1] for n in ("gate", "up")),
-                      lambda w=w, o=o, a=a: be.mul_mat_group([w["gate"], w["up"]], a["ffn_in"], [o["gate"], o["up"]])))
-            L.append(("down", FFN, Q8_0_ROW(w["down"].ne[0]) * w["down"].ne[1],
-                      lambda w=w, o=o, a=a: be.mul_mat(w["down"], a["ffn_act"], o["down"])))
-        L.append(("lm_head", HIDDEN, Q8_0_ROW(HIDDEN) * VOCAB,
-                  lambda: be.mul_mat(self.embd, self.acts[LAYERS - 1]["final"], self.logits)))
-        return L
+class Launch:
+    """One call into libmx: a label (launches of one label share a kernel and a shape class), its algorithmic bytes
+    (weights + activations read + outputs written) and int8 ops, and the call."""
+
+    def __init__(self, label, nbytes, ops, fn, weight_bytes=None):
+        self.label, self.nbytes, self.ops, self.fn = label, nbytes, ops, fn
+        self.weight_bytes = nbytes if weight_bytes is None else weight_bytes
 
 
 def per_label_pass(be, launches, reps: int):
-    """Mean kernel time (ms) per launch of each label: each label's launches (the 28 layers' instances, distinct
-    weights) are recorded as a graph of their own and replayed, so no event sits between two kernels. All graphs are
-    recorded first and freed last."""
+    """Mean time (ms) per launch of each label: each label's launches are recorded as a graph of their own and
+    replayed, so no event sits between two kernels. A label of few small launches repeats them inside its graph (up to
+    32 launches), so the graph's own launch cost does not swamp them; launches of 16 MB and more are recorded once, as
+    a repeat would find them in the 256 MB last-level cache. All graphs are recorded first and freed last."""
     labels = []
-    for lab, _, _, _ in launches:
-        if lab not in labels:
-            labels.append(lab)
-    graphs = {}
+    for L in launches:
+        if L.label not in labels:
+            labels.append(L.label)
+    graphs, counts = {}, {}
     for lab in labels:
+        mine = [L for L in launches if L.label == lab]
+        rep = 1 if max(L.nbytes for L in mine) >= (16 << 20) else max(1, 32 // len(mine))
         be.graph_begin()
-        for l, _, _, fn in launches:
-            if l == lab:
-                fn()
+        for _ in range(rep):
+            for L in mine:
+                L.fn()
         graphs[lab] = be.graph_end()
+        counts[lab] = rep * len(mine)
     out = {}
     e0, e1 = be.event(), be.event()
     for lab in labels:
-        count = sum(1 for l, _, _, _ in launches if l == lab)
+        count = counts[lab]
         for _ in range(3):
             be.graph_launch(graphs[lab])
         be.sync()
@@ -148,40 +120,282 @@ def per_label_pass(be, launches, reps: int):
     return out
 
 
-def cpu_baseline(mx, model, seconds: float):
-    """The oracle's AVX2 multi-threaded port of ggml's CPU mul_mat on the same weights, one token at a time."""
-    sys.path.insert(0, str(ROOT))
-    import oracle as O
+def label_table(launches, per_ms):
+    """{label: (launches, bytes, ops, ms per launch)} and a log line per label."""
+    by = {}
+    for L in launches:
+        d = by.setdefault(L.label, [0, 0, 0])
+        d[0] += 1
+        d[1] += L.nbytes
+        d[2] += L.ops
+    out = {}
+    for lab, (n, b, ops) in by.items():
+        ms = per_ms[lab]
+        out[lab] = (n, b, ops, ms)
+        extra = f"  {ops / n / (ms * 1e-3) / 1e12:8.1f} TOP/s" if ops else ""
+        log(f"{lab:10s} {n:4d} launches  {ms * 1e3:9.2f} us each  {b / n / 1e6:9.2f} MB each  "
+            f"{b / n / (ms * 1e-3) / 1e9:8.1f} GB/s{extra}")
+    return out
 
-    threads = O.physical_cores()
-    x = {K: mx.fill_normal(0xAC700002 + K, 1, K) for K in (HIDDEN, NQ * HEAD_DIM, FFN)}
-    shapes = layer_shapes()
-    ids = np.array([4242], np.int32)
 
-    def token():
-        O.get_rows(O.TYPE_Q8_0, model.host["embd"][4242:4243], HIDDEN, np.array([0], np.int32))
-        for l in range(LAYERS):
-            for name, K, N in shapes:
-                O.cpu_fast_mul_mat(O.TYPE_Q8_0, model.host[(l, name)], x[K], threads)
-        O.cpu_fast_mul_mat(O.TYPE_Q8_0, model.host["embd"], x[HIDDEN], threads)
+def time_graph(be, launches, steps: int, warmup: int, use_graph: bool = True):
+    """Runs the launches once eagerly (sizes the scratch), records them as one graph, then times `steps` replays
+    between HIP events on the backend's stream after `warmup` untimed ones. Returns ms per step."""
+    def eager():
+        for L in launches:
+            L.fn()
 
-    del ids
-    token()  # first run excluded
+    eager()
+    be.sync()
+    graph = None
+    if use_graph:
+        be.graph_begin()
+        eager()
+        graph = be.graph_end()
+    step = (lambda: be.graph_launch(graph)) if graph else eager
+    for _ in range(warmup):
+        step()
+    be.sync()
+    e0, e1 = be.event(), be.event()
+    t0 = time.perf_counter()
+    be.record(e0)
+    for _ in range(steps):
+        step()
+    be.record(e1)
+    be.sync()
+    wall = time.perf_counter() - t0
+    ms = be.elapsed_ms(e0, e1)
+    log(f"timed {steps} steps: {ms:.2f} ms by events, {wall * 1e3:.2f} ms by wall clock")
+    be.event_free(e0)
+    be.event_free(e1)
+    if graph:
+        be.graph_free(graph)
+    return ms / steps
+
+
+def hbm_roofline(kernel, table, labels):
+    """Algorithmic bytes per launch over the labels' mean launch time."""
+    n = sum(table[l][0] for l in labels)
+    b = sum(table[l][1] for l in labels)
+    ms = sum(table[l][3] * table[l][0] for l in labels)
+    achieved = (b / n) / (ms / n * 1e-3) / 1e9
+    return {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "launches_per_step": n, "bytes_per_launch": int(b / n),
+            "us_per_launch": round(ms / n * 1e3, 3)}
+
+
+def step_hbm_roofline(kernel, launches, ms_step, ms_other=0.0):
+    """Algorithmic bytes per launch of `launches` over their mean duration inside the timed step: the step's time less
+    `ms_other` (the step's other kernels) split over the launches. The step streams more weights than the 256 MB
+    last-level cache holds, so no launch finds its weights there, and the gaps between kernels in the graph count as
+    part of each launch."""
+    n = len(launches)
+    b = sum(L.nbytes for L in launches)
+    ms = (ms_step - ms_other) / n
+    achieved = (b / n) / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4), "launches_per_step": n, "bytes_per_launch": int(b / n),
+            "us_per_launch": round(ms * 1e3, 3)}
+
+
+def mfma_roofline(kernel, table, labels):
+    n = sum(table[l][0] for l in labels)
+    ops = sum(table[l][2] for l in labels)
+    ms = sum(table[l][3] * table[l][0] for l in labels)
+    achieved = ops / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "kernel": kernel, "achieved": round(achieved, 1), "peak": INT8_PEAK_TOPS,
+            "unit": "TOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4), "launches_per_step": n,
+            "ops_per_launch": int(ops / n), "us_per_launch": round(ms / n * 1e3, 3)}
+
+
+def base_result(args, value, unit, ms_per_step, dtype, config, higher=True):
+    return {"metric": METRIC, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(ms_per_step, 5), "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
+            "dtype": dtype, "data": "synthetic (seeded N(0,0.02) weights quantized by ggml's reference quantizers; "
+                                    "N(0,1) activations)", "config": config}
+
+
+def timed_sample(fn, seconds: float):
+    """Runs fn once untimed, then repeatedly for about `seconds`; returns (runs, elapsed s)."""
+    fn()
     n, t0 = 0, time.perf_counter()
     while True:
-        token()
+        fn()
         n += 1
         el = time.perf_counter() - t0
         if el >= seconds:
-            break
-    return {"value": n / el, "unit": "tok/s", "cores": threads, "kind": "port",
+            return n, el
+
+
+# ---------------------------------------------------------------------------------------------- decoder shapes
+def decoder_shapes(hidden, ffn, nq, nkv, head_dim):
+    """(name, K, N) of one layer's linears, ggml order: W [K, N]."""
+    q, kv = nq * head_dim, nkv * head_dim
+    return [("q", hidden, q), ("k", hidden, kv), ("v", hidden, kv), ("o", q, hidden), ("gate", hidden, ffn),
+            ("up", hidden, ffn), ("down", ffn, hidden)]
+
+
+class Decoder:
+    """A decoder's linears on the device, built from seeded synthetic weights: per layer q, k, v, o, gate, up, down,
+    plus the tied embedding / lm_head table."""
+
+    def __init__(self, mx, be, config, layers, hidden, ffn, nq, nkv, head_dim, vocab, types, threads, keep_host):
+        self.mx, self.be = mx, be
+        self.layers_n, self.hidden, self.ffn, self.vocab = layers, hidden, ffn, vocab
+        self.shapes = decoder_shapes(hidden, ffn, nq, nkv, head_dim)
+        self.types = types  # name -> weight type
+        t0 = time.time()
+        self.host = {}
+        self.layers = []
+        for l in range(layers):
+            ws = {}
+            for i, (name, K, N) in enumerate(self.shapes):
+                t = types[name]
+                q = mx.quantize_normal(t, weight_seed(config, l, i), N, K, 0.02, nthreads=threads)
+                ws[name] = be.tensor(t, (K, N), q)
+                if keep_host:
+                    self.host[(l, name)] = q
+            self.layers.append(ws)
+        self.embd = None
+        if vocab:
+            head = mx.quantize_normal(Q8_0, weight_seed(config, layers, 0), vocab, hidden, 0.02, nthreads=threads)
+            self.embd = be.tensor(Q8_0, (hidden, vocab), head)
+            if keep_host:
+                self.host["embd"] = head
+        log(f"weights generated and uploaded in {time.time() - t0:.1f} s")
+
+    def wbytes(self, l, names):
+        return sum(row_bytes(self.layers[l][n].type, self.layers[l][n].ne[0]) * self.layers[l][n].ne[1] for n in names)
+
+    def layer_bytes(self):
+        return sum(self.wbytes(l, [n for n, _, _ in self.shapes]) for l in range(self.layers_n))
+
+    def head_bytes(self):
+        return row_bytes(Q8_0, self.hidden) * self.vocab if self.vocab else 0
+
+
+class DecodeActs:
+    """Per-layer synthetic activations and outputs of a batch-`M` pass (distinct tensors per layer when
+    `per_layer`, else one set shared by every layer)."""
+
+    def __init__(self, mx, be, dec, M, seed, per_layer):
+        q_dim = [K for n, K, _ in dec.shapes if n == "o"][0]
+        self.M = M
+        sets = dec.layers_n if per_layer else 1
+        self.acts, self.outs = [], []
+        for l in range(sets):
+            a = {}
+            for j, (name, K) in enumerate([("attn_out", q_dim), ("ffn_in", dec.hidden), ("ffn_act", dec.ffn),
+                                           ("final", dec.hidden)]):
+                a[name] = be.tensor(mx.F32, (K, M), mx.fill_normal(seed + 16 * l + j, M, K))
+            self.acts.append(a)
+            self.outs.append({name: be.tensor(mx.F32, (N, M)) for name, K, N in dec.shapes})
+        self.per_layer = per_layer
+
+    def at(self, l):
+        i = l if self.per_layer else 0
+        return self.acts[i], self.outs[i]
+
+
+def layer_launches(be, dec, acts, l, x_in, label_of):
+    """One layer's products as four launches: q/k/v (shared input), attn_o, gate/up (shared input), down."""
+    w = dec.layers[l]
+    a, o = acts.at(l)
+    M = acts.M
+    x_in = a["final"] if x_in is None else x_in
+    out = []
+
+    def mk(label, names, x, K):
+        b = dec.wbytes(l, names)
+        N = sum(w[n].ne[1] for n in names)
+        ops = 2 * M * K * N if M > 1 else 0
+        nbytes = b + 4 * M * (K + N)
+        if len(names) == 1:
+            fn = lambda: be.mul_mat(w[names[0]], x, o[names[0]])  # noqa: E731
+        else:
+            fn = lambda: be.mul_mat_group([w[n] for n in names], x, [o[n] for n in names])  # noqa: E731
+        out.append(Launch(label_of(label, w[names[0]].type), nbytes, ops, fn, weight_bytes=b))
+
+    mk("qkv", ["q", "k", "v"], x_in, dec.hidden)
+    mk("attn_o", ["o"], a["attn_out"], w["o"].ne[0])
+    mk("gate_up", ["gate", "up"], a["ffn_in"], dec.hidden)
+    mk("down", ["down"], a["ffn_act"], dec.ffn)
+    return out
+
+
+# ---------------------------------------------------------------------------------------------- decode (default)
+QWEN3_06B = dict(layers=28, hidden=1024, ffn=3072, nq=16, nkv=8, head_dim=128, vocab=151936)
+COPY_BYTES = 256 << 20  # the plain copy the counters are calibrated on
+TRAFFIC_FILE = ROOT / "profiles" / "k_matvec_q8_0_qwen3-0.6b_decode.traffic.txt"
+
+
+def decode_token_launches(be, mx, dec, acts, ids, x0, logits):
+    L = [Launch("get_rows", row_bytes(Q8_0, dec.hidden) + 4 + 4 * dec.hidden, 0,
+                lambda: be.get_rows(dec.embd, ids, x0))]
+    for l in range(dec.layers_n):
+        L += layer_launches(be, dec, acts, l, x0 if l == 0 else None, lambda lab, t: lab)
+    final = acts.at(dec.layers_n - 1)[0]["final"]
+    L.append(Launch("lm_head", dec.head_bytes() + 4 * (dec.hidden + dec.vocab), 0,
+                    lambda: be.mul_mat(dec.embd, final, logits), weight_bytes=dec.head_bytes()))
+    return L
+
+
+def run_decode(args, mx, be, threads):
+    S = QWEN3_06B
+    dec = Decoder(mx, be, 2, S["layers"], S["hidden"], S["ffn"], S["nq"], S["nkv"], S["head_dim"], S["vocab"],
+                  {n: Q8_0 for n, _, _ in decoder_shapes(S["hidden"], S["ffn"], S["nq"], S["nkv"], S["head_dim"])},
+                  threads, keep_host=True)
+    acts = DecodeActs(mx, be, dec, 1, 0xAC700002, per_layer=True)
+    ids = be.tensor(mx.I32, (1,), np.array([4242], np.int32))
+    x0 = be.tensor(mx.F32, (S["hidden"], 1))
+    logits = be.tensor(mx.F32, (S["vocab"], 1))
+    launches = decode_token_launches(be, mx, dec, acts, ids, x0, logits)
+    weight_bytes = sum(L.weight_bytes for L in launches)
+
+    # A plain device copy of known size: the reference the HBM traffic counters are calibrated on.
+    cp_src, cp_dst = be.tensor(mx.F32, (COPY_BYTES // 4,)), be.tensor(mx.F32, (COPY_BYTES // 4,))
+    mx.check(mx.lib().mx_tensor_copy(be.h, cp_src.ref(), cp_dst.ref()))
+    be.sync()
+    cp_src.free()
+    cp_dst.free()
+
+    ms_per_step = time_graph(be, launches, args.steps, args.warmup, not args.no_graph)
+    # Roofline of the dominant kernel: k_matvec over Q8_0 at batch 1 (every launch of the step but the one GET_ROWS;
+    # the template is instantiated per lanes-per-row, all the same code), timed inside the step.
+    table = label_table(launches, per_label_pass(be, launches, reps=20))
+    roof = step_hbm_roofline("k_matvec<Q8_0, NC=1>", [L for L in launches if L.label != "get_rows"], ms_per_step,
+                             ms_other=table["get_rows"][3])
+    roof["traffic"] = read_traffic()
+    tok_s = 1e3 / ms_per_step
+    step_gbps = weight_bytes / (ms_per_step * 1e-3) / 1e9
+    result = base_result(args, round(tok_s, 2), "tok/s", ms_per_step, "int8", {
+        "workload": "qwen3-0.6b-shape decode step, batch 1", **S, "weights": "Q8_0",
+        "ops_per_step": "1 GET_ROWS + 197 MUL_MAT in 114 launches", "graph": not args.no_graph})
+    result.update({"weight_bytes_per_step": weight_bytes, "weight_GBps": round(step_gbps, 1),
+                   "hbm_frac_step": round(step_gbps / HBM_PEAK_GBPS, 4), "roofline": roof})
+    if args.cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_decode(dec, args.cpu_seconds)
+    return result
+
+
+def cpu_decode(dec, seconds):
+    """The oracle's AVX2 multi-threaded port of ggml's CPU mul_mat on the same weights, one token at a time."""
+    O = load_oracle()
+    threads = O.physical_cores()
+    x = {K: O.fill_normal(0xAC700002 + K, 1, K) for K in {K for _, K, _ in dec.shapes}}
+
+    def token():
+        O.get_rows(O.TYPE_Q8_0, dec.host["embd"][4242:4243], dec.hidden, np.array([0], np.int32))
+        for l in range(dec.layers_n):
+            for name, K, N in dec.shapes:
+                O.cpu_fast_mul_mat(dec.types[name], dec.host[(l, name)], x[K], threads)
+        O.cpu_fast_mul_mat(O.TYPE_Q8_0, dec.host["embd"], x[dec.hidden], threads)
+
+    n, el = timed_sample(token, seconds)
+    return {"value": round(n / el, 2), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{n} full decode tokens (1 GET_ROWS + 197 Q8_0 mat-vecs, 633 MB of weights each) after one "
                       f"untimed token, {el:.1f} s, AVX2 int8 dots, src1 quantized once per product, rows split "
                       f"across {threads} threads"}
-
-
-COPY_BYTES = 256 << 20  # the plain copy the counters are calibrated on
-TRAFFIC_FILE = ROOT / "profiles" / "k_matvec_q8_0_qwen3-0.6b_decode.traffic.txt"
 
 
 def summarize_pmc(fetch_csv: str, write_csv: str) -> str:
@@ -225,15 +439,269 @@ def read_traffic():
     return None
 
 
+# ---------------------------------------------------------------------------------------------- matvec
+MATVEC_COPIES = 160  # 160 x 3,342,336 B = 535 MB of distinct weight copies, larger than the 256 MB last-level cache
+
+
+def run_matvec(args, mx, be, threads):
+    K, N = 1024, 3072
+    w = mx.quantize_normal(Q8_0, weight_seed(1, 0, 0), N, K, 0.02, nthreads=threads)
+    x = mx.fill_normal(0xAC700001, 1, K)
+    W = [be.tensor(Q8_0, (K, N), w) for _ in range(MATVEC_COPIES)]
+    X = be.tensor(mx.F32, (K, 1), x)
+    Y = be.tensor(mx.F32, (N, 1))
+    nbytes = row_bytes(Q8_0, K) * N + 4 * K + 4 * N
+    launches = [Launch("matvec", nbytes, 0, lambda Wi=Wi: be.mul_mat(Wi, X, Y)) for Wi in W]
+    ms_per_step = time_graph(be, launches, args.steps, args.warmup, not args.no_graph)
+    roof = step_hbm_roofline("k_matvec<Q8_0, NC=1>", launches, ms_per_step)
+    roof["traffic"] = None
+    gbps = nbytes * MATVEC_COPIES / (ms_per_step * 1e-3) / 1e9
+    result = base_result(args, round(gbps, 1), "GB/s", ms_per_step, "int8", {
+        "workload": "single Q8_0 MUL_MAT 3072x1024 at batch 1, rotated over 160 weight copies",
+        "K": K, "N": N, "copies": MATVEC_COPIES, "bytes_per_product": nbytes, "graph": not args.no_graph})
+    result.update({"hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "us_per_product":
+                   round(ms_per_step / MATVEC_COPIES * 1e3, 3), "roofline": roof})
+    if args.cpu_seconds > 0:
+        O = load_oracle()
+        cores = O.physical_cores()
+        host = np.ascontiguousarray(np.broadcast_to(w, (MATVEC_COPIES,) + w.shape))
+        i = [0]
+
+        def one():
+            O.cpu_fast_mul_mat(O.TYPE_Q8_0, host[i[0] % MATVEC_COPIES], x, cores)
+            i[0] += 1
+
+        n, el = timed_sample(one, args.cpu_seconds)
+        result["cpu_baseline"] = {"value": round(n * nbytes / el / 1e9, 2), "unit": "GB/s", "cores": cores,
+                                  "kind": "port", "sample": f"{n} products over {MATVEC_COPIES} rotated host copies, "
+                                                            f"{el:.1f} s, AVX2, {cores} threads"}
+    return result
+
+
+# ---------------------------------------------------------------------------------------------- prefill
+QWEN3_17B = dict(layers=28, hidden=2048, ffn=6144, nq=16, nkv=8, head_dim=128)
+
+
+def prefill_launches(be, dec, acts, label_of):
+    L = []
+    for l in range(dec.layers_n):
+        L += layer_launches(be, dec, acts, l, None, label_of)
+    return L
+
+
+def cpu_prefill(dec, M, seconds, types):
+    """The AVX2 port of ggml's CPU mul_mat on the same weights at M rows, layer by layer, bounded by `seconds`."""
+    O = load_oracle()
+    cores = O.physical_cores()
+    x = {K: O.fill_normal(0xAC700300 + K, M, K) for K in {K for _, K, _ in dec.shapes}}
+    state = {"l": 0, "ops": 0}
+
+    def layer():
+        l = state["l"] % dec.layers_n
+        for name, K, N in dec.shapes:
+            O.cpu_fast_mul_mat(types[name], dec.host[(l, name)], x[K], cores)
+            state["ops"] += 2 * M * K * N
+        state["l"] += 1
+
+    layer()
+    state["ops"] = 0
+    n, t0 = 0, time.perf_counter()
+    while True:
+        layer()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": round(state["ops"] / el / 1e12, 4), "unit": "TOP/s", "cores": cores, "kind": "port",
+            "sample": f"{n} layers' 7 products at M = {M} after one untimed layer, {el:.1f} s, AVX2 int8 dots, "
+                      f"{cores} threads"}
+
+
+def run_prefill_q4k(args, mx, be, threads):
+    S = QWEN3_17B
+    M = 512
+    types = {n: (Q6_K if n == "down" else Q4_K) for n, _, _ in
+             decoder_shapes(S["hidden"], S["ffn"], S["nq"], S["nkv"], S["head_dim"])}
+    dec = Decoder(mx, be, 3, S["layers"], S["hidden"], S["ffn"], S["nq"], S["nkv"], S["head_dim"], 0, types, threads,
+                  keep_host=args.cpu_seconds > 0)
+    acts = DecodeActs(mx, be, dec, M, 0xAC700003, per_layer=False)
+    launches = prefill_launches(be, dec, acts, lambda lab, t: f"{lab}:{NAME[t]}")
+    ops = sum(L.ops for L in launches)
+    ms_per_step = time_graph(be, launches, args.steps, args.warmup, not args.no_graph)
+    table = label_table(launches, per_label_pass(be, launches, reps=5))
+    roof = mfma_roofline("k_gemm_kq<Q4_K> (with its Q8_K activation pass)", table,
+                         [l for l in table if l.endswith(":Q4_K")])
+    roof["traffic"] = None
+    tops = ops / (ms_per_step * 1e-3) / 1e12
+    result = base_result(args, round(tops, 2), "TOP/s", ms_per_step, "int8", {
+        "workload": "qwen3-1.7b-shape talker prefill, M = 512", **S, "M": M, "weights": "Q4_K, Q6_K down",
+        "graph": not args.no_graph})
+    wb = dec.layer_bytes()
+    result.update({"int8_frac": round(tops / INT8_PEAK_TOPS, 4), "ops_per_step": ops, "weight_bytes": wb,
+                   "tok_s": round(M / (ms_per_step * 1e-3), 1), "roofline": roof,
+                   "q6_k_down": mfma_roofline("k_gemm_kq<Q6_K>", table, ["down:Q6_K"])})
+    if args.cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_prefill(dec, M, args.cpu_seconds, types)
+    return result
+
+
+ASR_BLOCKS = (512, 512, 512, 28)   # 1500 audio rows + 64 text rows, in speech.cpp's 512-row prefill blocks
+ASR_DECODE_TOKENS = 32
+
+
+def run_asr(args, mx, be, threads):
+    S = dict(QWEN3_17B, vocab=151936)
+    types = {n: Q8_0 for n, _, _ in decoder_shapes(S["hidden"], S["ffn"], S["nq"], S["nkv"], S["head_dim"])}
+    dec = Decoder(mx, be, 4, S["layers"], S["hidden"], S["ffn"], S["nq"], S["nkv"], S["head_dim"], S["vocab"], types,
+                  threads, keep_host=args.cpu_seconds > 0)
+    acts = {M: DecodeActs(mx, be, dec, M, 0xAC700004 + M * 256, per_layer=False) for M in sorted(set(ASR_BLOCKS))}
+    dacts = DecodeActs(mx, be, dec, 1, 0xAC700004, per_layer=True)
+    logits = be.tensor(mx.F32, (S["vocab"], 1))
+    ids = be.tensor(mx.I32, (1,), np.array([4242], np.int32))
+    x0 = be.tensor(mx.F32, (S["hidden"], 1))
+    pre = []
+    for M in ASR_BLOCKS:
+        pre += prefill_launches(be, dec, acts[M], lambda lab, t, M=M: f"prefill_M{M}")
+    last = acts[ASR_BLOCKS[-1]].acts[0]["final"]
+    head_x = be.tensor(mx.F32, (S["hidden"], 1), last.numpy().reshape(ASR_BLOCKS[-1], S["hidden"])[-1:])
+    pre.append(Launch("head_last_row", dec.head_bytes(), 0, lambda: be.mul_mat(dec.embd, head_x, logits)))
+    tok = decode_token_launches(be, mx, dec, dacts, ids, x0, logits)
+    pre_ops = sum(L.ops for L in pre)
+    ms_pre = time_graph(be, pre, max(1, args.steps), args.warmup, not args.no_graph)
+    ms_tok = time_graph(be, tok, max(1, args.steps) * ASR_DECODE_TOKENS, args.warmup, not args.no_graph)
+    ms_step = ms_pre + ASR_DECODE_TOKENS * ms_tok
+    table = label_table(pre + tok, per_label_pass(be, pre + tok, reps=3))
+    roof = mfma_roofline("k_gemm_q8_0_i8 (with its activation pass)", table,
+                         [l for l in table if l.startswith("prefill_M512")])
+    roof["traffic"] = None
+    tops = pre_ops / (ms_pre * 1e-3) / 1e12
+    tok_w = sum(L.weight_bytes for L in tok)
+    result = base_result(args, round(tops, 2), "TOP/s", ms_step, "int8", {
+        "workload": "qwen3-asr-1.7b-shape Q8_0 prefill of 1564 rows + 32 decode tokens", **S,
+        "blocks": list(ASR_BLOCKS), "decode_tokens": ASR_DECODE_TOKENS, "weights": "Q8_0", "graph": not args.no_graph})
+    result.update({"int8_frac": round(tops / INT8_PEAK_TOPS, 4), "prefill_ms": round(ms_pre, 4),
+                   "prefill_ops": pre_ops, "decode_ms_per_token": round(ms_tok, 5),
+                   "decode_tok_s": round(1e3 / ms_tok, 2), "decode_weight_bytes_per_token": tok_w,
+                   "decode_hbm_frac": round(tok_w / (ms_tok * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "roofline": roof,
+                   "decode_roofline": step_hbm_roofline("k_matvec<Q8_0, NC=1>",
+                                                        [L for L in tok if L.label != "get_rows"], ms_tok,
+                                                        ms_other=table["get_rows"][3])})
+    if args.cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_prefill(dec, 512, args.cpu_seconds, types)
+    return result
+
+
+# ---------------------------------------------------------------------------------------------- moe
+MOE_E, MOE_K, MOE_H, MOE_F = 64, 4, 2048, 1536
+MOE_BATCHES = (1, 16, 256)
+MOE_LAYERS = 16  # distinct copies of the expert tensors: 5.4 GB, so no layer finds its experts in the 256 MB cache
+
+
+def router_ids(T, seed):
+    """top-4 of softmax(N(0,1) logits) per token (softmax is monotone, so the top-4 of the logits)."""
+    mx = load_mx()
+    logits = mx.fill_normal(seed, T, MOE_E).astype(np.float64)
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    return np.argsort(-p, axis=1, kind="stable")[:, :MOE_K].astype(np.int32)
+
+
+def run_moe(args, mx, be, threads):
+    t0 = time.time()
+    specs = [("gate", MOE_H, MOE_F), ("up", MOE_H, MOE_F), ("down", MOE_F, MOE_H)]
+    host = {}
+    for i, (name, K, N) in enumerate(specs):
+        host[name] = mx.quantize_normal(Q4_K, weight_seed(5, 0, i), MOE_E * N, K, 0.02, nthreads=threads)
+    layers = [{name: be.tensor(Q4_K, (K, N, MOE_E), host[name]) for name, K, N in specs} for _ in range(MOE_LAYERS)]
+    log(f"expert weights generated and uploaded ({MOE_LAYERS} layer copies) in {time.time() - t0:.1f} s")
+    per_expert = sum(row_bytes(Q4_K, K) * N for _, K, N in specs)
+    per_batch, all_launches, ms_total = [], [], 0.0
+    for T in MOE_BATCHES:
+        launches, wbytes, distinct = [], 0, []
+        xb = be.tensor(mx.F32, (MOE_H, 1, T), mx.fill_normal(0xAC700005 + T, T, MOE_H))
+        xa = be.tensor(mx.F32, (MOE_F, MOE_K, T), mx.fill_normal(0xAC700105 + T, T * MOE_K, MOE_F))
+        yg = be.tensor(mx.F32, (MOE_F, MOE_K, T))
+        yu = be.tensor(mx.F32, (MOE_F, MOE_K, T))
+        yd = be.tensor(mx.F32, (MOE_H, MOE_K, T))
+        for l, E in enumerate(layers):
+            ids = router_ids(T, 0x70E70005 + 1000 * T + l)
+            d = len(np.unique(ids))
+            distinct.append(d)
+            I = be.tensor(mx.I32, (MOE_K, T), ids)
+            wgu = d * row_bytes(Q4_K, MOE_H) * MOE_F
+            wdn = d * row_bytes(Q4_K, MOE_F) * MOE_H
+            ops = 2 * T * MOE_K * MOE_H * MOE_F
+            gu_bytes = wgu + 4 * T * (MOE_H + MOE_K * MOE_F + MOE_K)
+            launches.append(Launch(f"T{T}", gu_bytes, ops, lambda E=E, I=I: be.mul_mat_id(E["gate"], xb, I, yg),
+                                   weight_bytes=wgu))
+            launches.append(Launch(f"T{T}", gu_bytes, ops, lambda E=E, I=I: be.mul_mat_id(E["up"], xb, I, yu),
+                                   weight_bytes=wgu))
+            launches.append(Launch(f"T{T}", wdn + 4 * T * (MOE_K * MOE_F + MOE_K * MOE_H + MOE_K), ops,
+                                   lambda E=E, I=I: be.mul_mat_id(E["down"], xa, I, yd), weight_bytes=wdn))
+            wbytes += d * per_expert
+        log(f"T = {T}: distinct experts per layer {min(distinct)}..{max(distinct)} (mean {np.mean(distinct):.1f})")
+        ms = time_graph(be, launches, args.steps, args.warmup, not args.no_graph)
+        ms_total += ms
+        b = sum(L.nbytes for L in launches)
+        per_batch.append({"T": T, "distinct_experts_mean": round(float(np.mean(distinct)), 2),
+                          "weight_bytes_per_layer": int(wbytes / MOE_LAYERS),
+                          "us_per_layer": round(ms / MOE_LAYERS * 1e3, 2), "GBps": round(b / (ms * 1e-3) / 1e9, 1),
+                          "hbm_frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                          "TOPs": round(sum(L.ops for L in launches) / (ms * 1e-3) / 1e12, 2)})
+        all_launches.append((T, launches, ms))
+    total_b = sum(L.nbytes for _, ls, _ in all_launches for L in ls)
+    gbps = total_b / (ms_total * 1e-3) / 1e9
+    T_dom, l_dom, ms_dom = all_launches[-1]
+    roof = step_hbm_roofline(f"k_mmid_experts<Q4_K> at T = {T_dom} (with its bucket and Q8_K passes)", l_dom, ms_dom)
+    roof["traffic"] = None
+    result = base_result(args, round(gbps, 1), "GB/s", ms_total, "int8", {
+        "workload": "drama3-like MoE FFN layer via MUL_MAT_ID, token batches 1, 16, 256", "experts": MOE_E,
+        "top_k": MOE_K, "hidden": MOE_H, "expert_ffn": MOE_F, "weights": "Q4_K", "layer_copies": MOE_LAYERS,
+        "graph": not args.no_graph})
+    result.update({"hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "per_batch": per_batch, "roofline": roof})
+    if args.cpu_seconds > 0:
+        O = load_oracle()
+        cores = O.physical_cores()
+        T = 16
+        ids = router_ids(T, 0x70E70005 + 1000 * T)
+        xb = O.fill_normal(0xAC700005 + T, T, MOE_H)
+        xa = O.fill_normal(0xAC700105 + T, T * MOE_K, MOE_F).reshape(T, MOE_K, MOE_F)
+        hw = {name: host[name].reshape(MOE_E, N, -1) for name, _, N in specs}
+
+        def layer():
+            for name in ("gate", "up"):
+                for e in np.unique(ids):
+                    rows = np.nonzero((ids == e).any(axis=1))[0]
+                    O.cpu_fast_mul_mat(O.TYPE_Q4_K, hw[name][e], xb[rows], cores)
+            for e in np.unique(ids):
+                t_idx, s_idx = np.nonzero(ids == e)
+                O.cpu_fast_mul_mat(O.TYPE_Q4_K, hw["down"][e], xa[t_idx, s_idx], cores)
+
+        n, el = timed_sample(layer, args.cpu_seconds)
+        wb = len(np.unique(ids)) * per_expert
+        result["cpu_baseline"] = {"value": round(n * wb / el / 1e9, 2), "unit": "GB/s", "cores": cores,
+                                  "kind": "port",
+                                  "sample": f"{n} MoE layers at T = {T} ({len(np.unique(ids))} distinct experts), "
+                                            f"per-expert AVX2 products over the routed rows, {el:.1f} s, {cores} "
+                                            f"threads"}
+    return result
+
+
+WORKLOADS = {"decode": run_decode, "matvec": run_matvec, "prefill-q4k": run_prefill_q4k, "asr-1.7b": run_asr,
+             "moe": run_moe}
+DEFAULT_STEPS = {"decode": (300, 20), "matvec": (50, 5), "prefill-q4k": (20, 3), "asr-1.7b": (3, 1), "moe": (20, 3)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=300)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="decode")
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 skips it)")
     ap.add_argument("--no-graph", action="store_true", help="replay the step eagerly instead of as a graph")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help="print the traffic summary of two rocprofv3 --pmc runs of this benchmark and exit")
+                    help="print the traffic summary of two rocprofv3 --pmc runs of the decode benchmark and exit")
     args = ap.parse_args()
     if args.summarize_pmc:
         print(summarize_pmc(*args.summarize_pmc))
@@ -241,7 +709,12 @@ def main():
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
         sys.exit(2)
+    steps, warmup = DEFAULT_STEPS[args.workload]
+    args.steps = steps if args.steps is None else args.steps
+    args.warmup = warmup if args.warmup is None else args.warmup
     rank = int(os.environ.get("RANK", "0"))
+    if rank != 0:
+        args.cpu_seconds = 0
 
     mx = load_mx()
     if mx.device_count() < 1:
@@ -249,105 +722,7 @@ def main():
         sys.exit(1)
     be = mx.Backend(0)
     threads = max(1, len(os.sched_getaffinity(0)))
-    model = Model(mx, be, threads)
-    launches = model.launches()
-    weight_bytes = sum(b for _, _, b, _ in launches)
-    act_bytes = (HIDDEN * 4 + LAYERS * 4 * (HIDDEN + NQ * HEAD_DIM + HIDDEN + FFN) +
-                 4 * (LAYERS * sum(N for _, _, N in layer_shapes()) + VOCAB + HIDDEN))
-
-    def step_eager():
-        for _, _, _, fn in launches:
-            fn()
-
-    step_eager()
-    be.sync()
-    graph = None
-    if not args.no_graph:
-        be.graph_begin()
-        step_eager()
-        graph = be.graph_end()
-    step = (lambda: be.graph_launch(graph)) if graph else step_eager
-
-    # A plain device copy of known size: the reference the HBM traffic counters are calibrated on.
-    cp_src, cp_dst = be.tensor(mx.F32, (COPY_BYTES // 4,)), be.tensor(mx.F32, (COPY_BYTES // 4,))
-    mx.check(mx.lib().mx_tensor_copy(be.h, cp_src.ref(), cp_dst.ref()))
-    be.sync()
-    cp_src.free()
-    cp_dst.free()
-
-    for _ in range(args.warmup):
-        step()
-    be.sync()
-    e0, e1 = be.event(), be.event()
-    t0 = time.perf_counter()
-    be.record(e0)
-    for _ in range(args.steps):
-        step()
-    be.record(e1)
-    be.sync()
-    wall = time.perf_counter() - t0
-    ms_events = be.elapsed_ms(e0, e1)
-    ms_per_step = ms_events / args.steps
-    log(f"timed {args.steps} steps: {ms_events:.2f} ms by events, {wall * 1e3:.2f} ms by wall clock")
-
-    # Roofline of the dominant kernel: k_matvec over Q8_0 at batch 1 (every launch of the step but the one GET_ROWS;
-    # the template is instantiated per lanes-per-row, all the same code).
-    per_ms = per_label_pass(be, launches, reps=20)
-    by_label = {}
-    for label, K, b, _ in launches:
-        d = by_label.setdefault(label, [0, 0])
-        d[0] += 1
-        d[1] += b
-    for label, (n, b) in by_label.items():
-        ms = per_ms[label]
-        log(f"{label:8s} {n:3d} launches  {ms * 1e3:8.2f} us each  {b / n / 1e6:8.2f} MB each  "
-            f"{b / n / (ms * 1e-3) / 1e9:8.1f} GB/s")
-    mv = [lab for lab in by_label if lab != "get_rows"]
-    mv_launches = sum(by_label[lab][0] for lab in mv)
-    mv_bytes = sum(by_label[lab][1] for lab in mv)
-    mv_ms = sum(per_ms[lab] * by_label[lab][0] for lab in mv)
-    dom_name = "k_matvec<Q8_0, NC=1>"
-    per_launch_bytes = mv_bytes / mv_launches
-    per_launch_ms = mv_ms / mv_launches
-    achieved = per_launch_bytes / (per_launch_ms * 1e-3) / 1e9
-    dom = {"launches": mv_launches}
-
-    traffic = read_traffic()
-
-    tok_s = 1e3 / ms_per_step
-    step_gbps = weight_bytes / (ms_per_step * 1e-3) / 1e9
-    result = {
-        "metric": METRIC,
-        "value": round(tok_s, 2),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic (seeded N(0,0.02) weights quantized by quantize_row_q8_0_ref; N(0,1) activations)",
-        "config": {"workload": "qwen3-0.6b-shape decode step, batch 1", "layers": LAYERS, "hidden": HIDDEN,
-                   "ffn": FFN, "q_heads": NQ, "kv_heads": NKV, "head_dim": HEAD_DIM, "vocab": VOCAB,
-                   "weights": "Q8_0", "ops_per_step": "1 GET_ROWS + 197 MUL_MAT in 114 launches",
-                   "graph": graph is not None},
-        "weight_bytes_per_step": weight_bytes,
-        "weight_GBps": round(step_gbps, 1),
-        "hbm_frac_step": round(step_gbps / HBM_PEAK_GBPS, 4),
-        "roofline": {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "launches_per_step": dom["launches"], "bytes_per_launch": int(per_launch_bytes),
-                     "us_per_launch": round(per_launch_ms * 1e3, 3)},
-    }
-    del act_bytes
-    if graph:
-        be.graph_free(graph)
-    be.event_free(e0)
-    be.event_free(e1)
-    if rank == 0 and args.cpu_seconds > 0:
-        result["cpu_baseline"] = cpu_baseline(mx, model, args.cpu_seconds)
+    result = WORKLOADS[args.workload](args, mx, be, threads)
     be.close()
     if rank == 0:
         print(json.dumps(result), flush=True)

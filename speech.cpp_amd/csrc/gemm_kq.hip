@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void k_gemm_quant_q8k(const float *x, int64_t 
     float d;
     int bs16;
     const int q = quant256_wave(v, lane, &d, &bs16);
-    const int bs32 = bs16 + __shfl_xor(bs16, 4);  // lanes 8j..8j+7 hold sub-block j
+    const int bs32 = bs16 + dpp_i<dpp::HALF_MIRROR>(0, bs16);  // lanes 8j..8j+7 hold sub-block j
     *(int *)(xq + m * K + sb * 256 + 4 * lane) = q;
     if (lane == 0) xd[m * (K / 256) + sb] = d;
     if ((lane & 7) == 0) xs32[m * (K / 32) + sb * 8 + (lane >> 3)] = (float)bs32;

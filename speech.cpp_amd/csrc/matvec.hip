@@ -20,22 +20,77 @@ __device__ __forceinline__ MatvecProblem pick_problem(const MatvecArgs &a, int i
 // overlaps the load and quantization of x instead of following it.
 constexpr int PRELOAD = 4;
 
+// float4s of each activation column every thread loads ahead of the weights (elements 1024 i + 4 tid, i < XPRE).
+template <int NC>
+__host__ __device__ constexpr int xpre() { return NC == 1 ? 4 : (NC == 2 ? 2 : 1); }
+
+// Quantizes the 1024-element piece at `base` of one activation column (v = elements base + 4 tid .. + 3) into LDS:
+// Q8_0 weights take 32-blocks (d rounded to fp16 and back, as the CPU dot reads it), K-quants Q8_K 256-blocks with
+// their 16-element sums. Every wave of the workgroup calls it with the same `base`.
+template <int TYPE>
+__device__ __forceinline__ void quantize_piece(float4 v, int base, int K, int rounding, int8_t *xq, float *xd,
+                                               int *xbs) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int e = base + 4 * tid;
+    if constexpr (TYPE == MX_TYPE_Q8_0) {
+        float d;
+        int sum;
+        const int q = quant32_lane(v, rounding, &d, &sum);
+        if (e < K) {  // K % 32 == 0: the eight lanes of a block agree
+            *(int *)(xq + e) = q;
+            if ((tid & 7) == 0) xd[e / 32] = h2f(f2h(d));
+        }
+    } else {
+        if (base + 256 * (tid >> 6) < K) {  // a whole wave per super-block
+            float d;
+            int bs;
+            const int q = quant256_wave(v, lane, &d, &bs);
+            *(int *)(xq + e) = q;
+            if (lane == 0) xd[e / 256] = d;
+            if ((lane & 3) == 0) xbs[e / 16] = bs;
+        }
+    }
+}
+
+__device__ __forceinline__ float4 load_x4(const float *xc, int e, int K) {
+    const float4 v = *(const float4 *)(xc + (e < K ? e : K - 4));
+    return e < K ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
 template <int TYPE, int NC, int LPR>
 __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int64_t K = a.K;
-    const int64_t z = blockIdx.z;
-    const int64_t i12 = z % a.ne12, i13 = z / a.ne12;
+    const int K = (int)a.K;
+    const int tid = threadIdx.x;
+    // Batch slice; a single slice (decode) takes no division.
+    int i12 = 0, i13 = 0, mat = 0;
+    if (a.nbatch > 1) {
+        const unsigned z = blockIdx.z;
+        i12 = (int)(z % (unsigned)a.ne12);
+        i13 = (int)(z / (unsigned)a.ne12);
+        mat = (int)((unsigned)i12 / (unsigned)a.r2) + (int)((unsigned)i13 / (unsigned)a.r3) * a.ne02;
+    }
+    const float *x = a.x + i12 * a.x_b2 + i13 * a.x_b3;
+
+    // The activation loads go first: x -> quantization -> LDS is the prologue's critical path, and the memory counter
+    // retires loads in order, so waiting for x then does not wait for the weight loads issued after it.
+    constexpr int XP = xpre<NC>();
+    float4 xr[NC][XP];
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+#pragma unroll
+        for (int i = 0; i < XP; i++) xr[c][i] = load_x4(x + c * a.x_col_stride, 1024 * i + 4 * tid, K);
+
     const MatvecProblem p = pick_problem(a, (int)blockIdx.y);
     constexpr int G = 64 / LPR;  // rows in flight per wave
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = tid & 63, wave = tid >> 6;
     const int sub = lane % LPR, grp = lane / LPR;
     const int64_t row = (int64_t)blockIdx.x * (4 * G) + wave * G + grp;
     const bool has_row = row < p.N;
     // Rows past the end load (and then ignore) the last row, chunks past the end the last chunk: the preloads carry no
-    // branch, so they issue back to back.
-    const int64_t grow = p.row0 + (i12 / a.r2 + (i13 / a.r3) * a.ne02) * p.N + (has_row ? row : p.N - 1);
-    const int nchunks = (int)(K / chunk_elems<TYPE>());
+    // lane-dependent branch, so they issue back to back.
+    const int64_t grow = p.row0 + (int64_t)mat * p.N + (has_row ? row : p.N - 1);
+    const int nchunks = K / chunk_elems<TYPE>();
 
     WChunk<TYPE> pre[PRELOAD];
 #pragma unroll
@@ -44,11 +99,21 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
         pre[i] = load_chunk<TYPE>(p.w, grow, K, c < nchunks ? c : nchunks - 1);
     }
 
-    const float *x = a.x + i12 * a.x_b2 + i13 * a.x_b3;
     int8_t *xq = (int8_t *)smem;
     float *xd = (float *)(smem + (size_t)NC * K);
-    int *xbs = (int *)(xd + NC * (TYPE == MX_TYPE_Q8_0 ? K / 32 : K / 256));
-    quantize_cols_to_lds<TYPE, NC, false>(x, a.x_col_stride, K, NC, a.rounding, xq, xd, xbs);
+    constexpr int XDB = TYPE == MX_TYPE_Q8_0 ? 32 : 256;
+    int *xbs = (int *)(xd + NC * (K / XDB));
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const float *xc = x + c * a.x_col_stride;
+#pragma unroll
+        for (int i = 0; i < XP; i++)
+            if (1024 * i < K) quantize_piece<TYPE>(xr[c][i], 1024 * i, K, a.rounding, xq + c * K, xd + c * (K / XDB),
+                                                   xbs + c * (K / 16));
+        for (int base = 1024 * XP; base < K; base += 1024)
+            quantize_piece<TYPE>(load_x4(xc, base + 4 * tid, K), base, K, a.rounding, xq + c * K, xd + c * (K / XDB),
+                                 xbs + c * (K / 16));
+    }
     __syncthreads();
     if (!has_row) return;  // whole LPR-lane groups leave together; no barrier follows
 
@@ -65,7 +130,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
         chunk_dot<TYPE, NC, false>(p.w, grow, K, c, xq, xd, xbs, NC, acc);
 #pragma unroll
     for (int c = 0; c < NC; c++) acc[c] = sum_lanes<LPR>(acc[c]);
-    if (sub == 0) {
+    if (sub == LPR - 1) {  // the lane holding the group's sum
         float *y = p.y + i12 * a.y_b2 + i13 * a.y_b3 + row;
 #pragma unroll
         for (int c = 0; c < NC; c++) y[c * p.y_col_stride] = acc[c];
@@ -75,33 +140,29 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
 template <int TYPE, int NC, int LPR>
 static hipError_t launch_one(const MatvecArgs &a, int64_t maxN, size_t lds, hipStream_t s) {
     constexpr int G = 64 / LPR;
-    dim3 grid((unsigned)((maxN + 4 * G - 1) / (4 * G)), (unsigned)a.nprob, (unsigned)(a.ne12 * a.ne13));
+    dim3 grid((unsigned)((maxN + 4 * G - 1) / (4 * G)), (unsigned)a.nprob, (unsigned)a.nbatch);
     hipLaunchKernelGGL((k_matvec<TYPE, NC, LPR>), grid, dim3(256), lds, s, a);
     return hipGetLastError();
 }
 
-// Lanes per row: the fewest lanes (longest per-lane streams) that still give the launch enough workgroups to cover
-// the chip twice; small matrices get more lanes per row and so more, shorter workgroups. MX_MATVEC_LPR overrides it.
-static int pick_lpr(int64_t nchunks, int64_t maxN, int nprob, int64_t batches) {
+// Lanes per row: the fewest (16, 32 or 64) whose chunks per lane all fit the preload, so every weight byte of a lane
+// is requested before the activation prologue; rows longer than that take 64 lanes. Measured on the decode shapes
+// (K 1024..3072): one full preload beats more workgroups with shorter streams. MX_MATVEC_LPR overrides it.
+static int pick_lpr(int64_t nchunks) {
     static const int forced = [] {
         const char *e = getenv("MX_MATVEC_LPR");
         return e ? atoi(e) : 0;
     }();
     if (forced == 16 || forced == 32 || forced == 64) return forced;
-    const int64_t target = 512;
-    for (int lpr = 16; lpr <= 64; lpr *= 2) {
-        if (lpr > 16 && nchunks < lpr) return lpr / 2;
-        const int64_t rows_per_wg = 4 * (64 / lpr);
-        const int64_t wgs = (maxN + rows_per_wg - 1) / rows_per_wg * nprob * batches;
-        if (wgs >= target) return lpr;
-    }
-    return nchunks >= 64 ? 64 : (nchunks >= 32 ? 32 : 16);
+    int lpr = 16;
+    while (lpr < 64 && nchunks > (int64_t)PRELOAD * lpr) lpr *= 2;
+    return lpr;
 }
 
 template <int TYPE, int NC>
 static hipError_t launch_nc(const MatvecArgs &a, int64_t maxN, size_t lds, hipStream_t s) {
     const int64_t nchunks = a.K / chunk_elems<TYPE>();
-    switch (pick_lpr(nchunks, maxN, a.nprob, a.ne12 * a.ne13)) {
+    switch (pick_lpr(nchunks)) {
         case 16: return launch_one<TYPE, NC, 16>(a, maxN, lds, s);
         case 32: return launch_one<TYPE, NC, 32>(a, maxN, lds, s);
         default: return launch_one<TYPE, NC, 64>(a, maxN, lds, s);

@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) void k_mmid_experts(MulMatIdArgs a) {
             for (int c = sub; c < nchunks; c += LPR) chunk_dot<TYPE, NC, true>(a.w, grow, K, c, xq, xd, xbs, ng, acc);
 #pragma unroll
             for (int c = 0; c < NC; c++) acc[c] = sum_lanes<LPR>(acc[c]);
-            if (sub == 0) {
+            if (sub == LPR - 1) {  // the lane holding the group's sum
 #pragma unroll
                 for (int col = 0; col < NC; col++) {
                     if (col < ng) {

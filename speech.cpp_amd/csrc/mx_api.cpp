@@ -386,6 +386,7 @@ MX_API int mx_supports_op(int op, const mx_tensor *src0, const mx_tensor *src1, 
             if (!f32_rows_ok(src1) || src1->ne[0] != K) return 0;
             if (src0->ne[2] == 0 || src0->ne[3] == 0) return 0;
             if (src1->ne[2] % src0->ne[2] != 0 || src1->ne[3] % src0->ne[3] != 0) return 0;
+            if (src1->ne[2] * src1->ne[3] > mx::MAX_BATCH) return 0;
             if (dst->ne[0] != src0->ne[1] || dst->ne[1] != src1->ne[1] || dst->ne[2] != src1->ne[2] ||
                 dst->ne[3] != src1->ne[3])
                 return 0;
@@ -514,11 +515,11 @@ static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, con
     a.rounding = be->rounding;
     a.K = w0->ne[0];
     a.x_col_stride = (int64_t)(src1->nb[1] / 4);
-    a.ne12 = src1->ne[2];
-    a.ne13 = src1->ne[3];
-    a.ne02 = w0->ne[2];
-    a.r2 = src1->ne[2] / w0->ne[2];
-    a.r3 = src1->ne[3] / w0->ne[3];
+    a.nbatch = (int)(src1->ne[2] * src1->ne[3]);
+    a.ne12 = (int)src1->ne[2];
+    a.ne02 = (int)w0->ne[2];
+    a.r2 = (int)(src1->ne[2] / w0->ne[2]);
+    a.r3 = (int)(src1->ne[3] / w0->ne[3]);
     a.x_b2 = (int64_t)(src1->nb[2] / 4);
     a.x_b3 = (int64_t)(src1->nb[3] / 4);
     a.y_b2 = (int64_t)(dst[0]->nb[2] / 4);

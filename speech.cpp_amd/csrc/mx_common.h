@@ -136,6 +136,7 @@ hipError_t launch_get_rows(const GetRowsArgs &a, hipStream_t s);
 
 // Mat-vec / small-M products: up to MAX_COLS columns of src1 per launch, all batch slices in grid.z.
 constexpr int MAX_COLS = 8;
+constexpr int64_t MAX_BATCH = 65535;  // batch slices of one mat-vec launch (grid.z)
 struct MatvecProblem {
     WPlanes w;
     int64_t N;             // rows of the matrix (outputs)
@@ -150,8 +151,9 @@ struct MatvecArgs {
     int64_t K;
     const float *x;        // src1 column 0 of batch slice (0, 0)
     int64_t x_col_stride;  // floats between columns
-    // batch slices (grid.z = ne12 * ne13): matrix (i12 / r2, i13 / r3) of src0 meets slice (i12, i13) of src1
-    int64_t ne12, ne13, ne02, r2, r3;
+    // batch slices (grid.z = nbatch = ne12 * ne13 <= MAX_BATCH): matrix (i12 / r2, i13 / r3) of src0 meets slice
+    // (i12, i13) of src1
+    int nbatch, ne12, ne02, r2, r3;
     int64_t x_b2, x_b3, y_b2, y_b3;  // float strides of src1 / dst slices
     // problems sharing x (grid.y picks the problem)
     int nprob;

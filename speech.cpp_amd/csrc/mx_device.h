@@ -22,16 +22,34 @@ __device__ __forceinline__ uint16_t f2h(float f) {
     return h;
 }
 
+// Cross-lane exchanges on DPP (a modifier of the consuming VALU op: no LDS round trip). Each control reads, for lane
+// i: XOR1 / XOR2 lane i^1 / i^2 of its quad; HALF_MIRROR lane 7-i of its eight; MIRROR lane 15-i of its row of 16;
+// BCAST15 lane 15 of the row below (written into rows 1 and 3 with row mask 0xA); BCAST31 lane 31 (rows 2 and 3, row
+// mask 0xC). Lanes of rows outside the row mask get `old`.
+namespace dpp {
+constexpr int XOR1 = 0xB1, XOR2 = 0x4E, HALF_MIRROR = 0x141, MIRROR = 0x140, BCAST15 = 0x142, BCAST31 = 0x143;
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_i(int old, int v) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xF,
+                                                      false));
+}
+
+// Sum over aligned groups of WIDTH lanes (16, 32 or 64). Exact in the group's last lane (lane % WIDTH == WIDTH - 1);
+// for WIDTH 16 in every lane.
 template <int WIDTH>
 __device__ __forceinline__ float sum_lanes(float v) {
-#pragma unroll
-    for (int m = WIDTH / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-    return v;
-}
-template <int WIDTH>
-__device__ __forceinline__ int isum_lanes(int v) {
-#pragma unroll
-    for (int m = WIDTH / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    static_assert(WIDTH == 16 || WIDTH == 32 || WIDTH == 64, "group of 16, 32 or 64 lanes");
+    v += dpp_f<dpp::XOR1>(0.0f, v);
+    v += dpp_f<dpp::XOR2>(0.0f, v);
+    v += dpp_f<dpp::HALF_MIRROR>(0.0f, v);
+    v += dpp_f<dpp::MIRROR>(0.0f, v);
+    if (WIDTH >= 32) v += dpp_f<dpp::BCAST15, 0xA>(0.0f, v);
+    if (WIDTH >= 64) v += dpp_f<dpp::BCAST31, 0xC>(0.0f, v);
     return v;
 }
 
@@ -49,9 +67,9 @@ __device__ __forceinline__ int pack4(int a, int b, int c, int d) {
 // ------------------------------------------------------------------------------------------------------------------
 __device__ __forceinline__ int quant32_lane(float4 v, int rounding, float *d_out, int *sum_out) {
     float a = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    a = fmaxf(a, __shfl_xor(a, 1));
-    a = fmaxf(a, __shfl_xor(a, 2));
-    a = fmaxf(a, __shfl_xor(a, 4));
+    a = fmaxf(a, dpp_f<dpp::XOR1>(0.0f, a));
+    a = fmaxf(a, dpp_f<dpp::XOR2>(0.0f, a));
+    a = fmaxf(a, dpp_f<dpp::HALF_MIRROR>(0.0f, a));  // every lane of the eight now holds the block's amax
     const float d = a / 127.0f;
     int q0, q1, q2, q3;
     if (rounding == MX_ROUND_X86) {
@@ -68,9 +86,9 @@ __device__ __forceinline__ int quant32_lane(float4 v, int rounding, float *d_out
         q3 = (int)roundf(v.w * id);
     }
     int s = q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
-    s += __shfl_xor(s, 4);
+    s += dpp_i<dpp::XOR1>(0, s);
+    s += dpp_i<dpp::XOR2>(0, s);
+    s += dpp_i<dpp::HALF_MIRROR>(0, s);
     *d_out = d;
     *sum_out = s;
     return pack4(q0, q1, q2, q3);
@@ -92,20 +110,25 @@ __device__ __forceinline__ int quant256_wave(float4 v, int lane, float *d_out, i
         const uint32_t b = __float_as_uint(fabsf(e[j]));
         if (b > best_bits) { best_bits = b; best_idx = 4u * lane + j; }
     }
-    // Largest |x| wins; among equal |x| the smallest index (the first one ggml's strict '>' scan keeps).
-    uint64_t key = ((uint64_t)best_bits << 32) | (uint64_t)(0xFFFFFFFFu - best_idx);
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const uint32_t hi = __shfl_xor((uint32_t)(key >> 32), m);
-        const uint32_t lo = __shfl_xor((uint32_t)key, m);
-        const uint64_t other = ((uint64_t)hi << 32) | lo;
-        key = other > key ? other : key;
-    }
-    const uint32_t amax_bits = (uint32_t)(key >> 32);
-    const uint32_t idx = 0xFFFFFFFFu - (uint32_t)key;
+    // Largest |x| wins; among equal |x| the smallest index (the first one ggml's strict '>' scan keeps): the key
+    // (|x| bits, ~index) is maximal exactly there. Reduced within rows of 16, then across rows into lane 63.
+    uint32_t khi = best_bits, klo = 0xFFFFFFFFu - best_idx;
+    auto take = [&](uint32_t ohi, uint32_t olo) {
+        const bool gt = ohi > khi || (ohi == khi && olo > klo);
+        khi = gt ? ohi : khi;
+        klo = gt ? olo : klo;
+    };
+    take(dpp_i<dpp::XOR1>(0, khi), dpp_i<dpp::XOR1>(0, klo));
+    take(dpp_i<dpp::XOR2>(0, khi), dpp_i<dpp::XOR2>(0, klo));
+    take(dpp_i<dpp::HALF_MIRROR>(0, khi), dpp_i<dpp::HALF_MIRROR>(0, klo));
+    take(dpp_i<dpp::MIRROR>(0, khi), dpp_i<dpp::MIRROR>(0, klo));
+    take(dpp_i<dpp::BCAST15, 0xA>(0, khi), dpp_i<dpp::BCAST15, 0xA>(0, klo));
+    take(dpp_i<dpp::BCAST31, 0xC>(0, khi), dpp_i<dpp::BCAST31, 0xC>(0, klo));
+    const uint32_t amax_bits = (uint32_t)__builtin_amdgcn_readlane((int)khi, 63);
+    const uint32_t idx = 0xFFFFFFFFu - (uint32_t)__builtin_amdgcn_readlane((int)klo, 63);
     const uint32_t c = idx & 3u;  // every lane picks component idx%4; lane idx/4's is the block's max
     const float mine = c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
-    const float maxv = __shfl(mine, (int)(idx >> 2));
+    const float maxv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), (int)(idx >> 2)));
     if (amax_bits == 0) {
         *d_out = 0.0f;
         *bsum_out = 0;
@@ -119,8 +142,8 @@ __device__ __forceinline__ int quant256_wave(float4 v, int lane, float *d_out, i
         q[j] = t < 127 ? t : 127;
     }
     int s = q[0] + q[1] + q[2] + q[3];
-    s += __shfl_xor(s, 1);
-    s += __shfl_xor(s, 2);
+    s += dpp_i<dpp::XOR1>(0, s);
+    s += dpp_i<dpp::XOR2>(0, s);
     *d_out = 1.0f / iscale;
     *bsum_out = s;
     return pack4(q[0], q[1], q[2], q[3]);

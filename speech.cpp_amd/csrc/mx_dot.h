@@ -170,44 +170,6 @@ __device__ __forceinline__ void chunk_dot(const WPlanes &w, int64_t grow, int64_
     dot_chunk<TYPE, NC, GUARD>(load_chunk<TYPE>(w, grow, K, c), K, c, xq, xd, xbs, ncols, acc);
 }
 
-// Quantize `ncols` columns of f32 activations into LDS with 256 threads. For Q8_0 weights: 32-blocks (d rounded to
-// fp16 and back, as the CPU dot reads it); for K-quants: Q8_K 256-blocks with bsums.
-template <int TYPE, int NC, bool GUARD>
-__device__ __forceinline__ void quantize_cols_to_lds(const float *x, int64_t x_col_stride, int64_t K, int ncols,
-                                                     int rounding, int8_t *xq, float *xd, int *xbs) {
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    for (int col = 0; col < NC; col++) {
-        if (GUARD && col >= ncols) break;
-        const float *xc = x + col * x_col_stride;
-        for (int64_t base = 0; base < K; base += 1024) {
-            const int64_t e = base + 4 * tid;
-            if (TYPE == MX_TYPE_Q8_0) {
-                const bool valid = e < K;
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (valid) v = *(const float4 *)(xc + e);
-                float d;
-                int sum;
-                const int q = quant32_lane(v, rounding, &d, &sum);
-                if (valid) {
-                    *(int *)(xq + col * K + e) = q;
-                    if ((tid & 7) == 0) xd[col * (K / 32) + e / 32] = h2f(f2h(d));
-                }
-            } else {
-                if (base + 256 * (tid >> 6) < K) {  // a whole wave per super-block
-                    const float4 v = *(const float4 *)(xc + e);
-                    float d;
-                    int bs;
-                    const int q = quant256_wave(v, lane, &d, &bs);
-                    *(int *)(xq + col * K + e) = q;
-                    if (lane == 0) xd[col * (K / 256) + e / 256] = d;
-                    if ((lane & 3) == 0) xbs[col * (K / 16) + e / 16] = bs;
-                }
-            }
-        }
-    }
-}
-
 // LDS bytes the activations of `ncols` columns take.
 __host__ __device__ inline size_t act_lds_bytes(int type, int64_t K, int ncols) {
     if (type == MX_TYPE_Q8_0) return (size_t)ncols * (size_t)K + (size_t)ncols * (size_t)(K / 32) * 4;
