@@ -506,6 +506,43 @@ static int gemm_kq_group(mx_backend *be, int n, const mx_tensor *const *src0, co
     return MX_SUCCESS;
 }
 
+// MX_GEMM_Q4K=0 sends Q4_K prefill to the VALU-scaled kernel (k_gemm_kq) instead.
+static bool gemm_q4k_disabled() {
+    static const bool off = [] {
+        const char *e = getenv("MX_GEMM_Q4K");
+        return e && e[0] == '0';
+    }();
+    return off;
+}
+
+// M > 8 on Q4_K weights: per batch slice, activations quantized once, then one launch for the whole group.
+static int gemm_q4k_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
+                          const mx_tensor *const *dst) {
+    const mx_tensor *w0 = src0[0];
+    const int64_t K = w0->ne[0], M = src1->ne[1];
+    int rc = ensure_scratch(be, mx::gemm_q4k_act_bytes(M, K));
+    if (rc) return rc;
+    const int64_t r2 = src1->ne[2] / w0->ne[2], r3 = src1->ne[3] / w0->ne[3];
+    for (int64_t i13 = 0; i13 < src1->ne[3]; i13++)
+        for (int64_t i12 = 0; i12 < src1->ne[2]; i12++) {
+            const float *x = (const float *)((const uint8_t *)src1->data + i12 * src1->nb[2] + i13 * src1->nb[3]);
+            HIP_OK(mx::launch_gemm_q4k_quant(x, (int64_t)(src1->nb[1] / 4), M, K, be->scratch, be->stream),
+                   "Q4_K GEMM activation quantization");
+            mx::WPlanes w[4];
+            int64_t N[4], ldy[4];
+            float *y[4];
+            for (int i = 0; i < n; i++) {
+                w[i] = matrix_planes(src0[i], i12 / r2 + (i13 / r3) * src0[i]->ne[2]);
+                N[i] = src0[i]->ne[1];
+                y[i] = (float *)((uint8_t *)dst[i]->data + i12 * dst[i]->nb[2] + i13 * dst[i]->nb[3]);
+                ldy[i] = (int64_t)(dst[i]->nb[1] / 4);
+            }
+            HIP_OK(mx::launch_gemm_q4k(n, w, N, y, ldy, M, K, be->scratch, be->stream),
+                   "Q4_K GEMM launch");
+        }
+    return MX_SUCCESS;
+}
+
 // Products sharing src1: n problems (n <= 4) of the same type and K, each with its own rows and dst.
 static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
                         const mx_tensor *const *dst) {
@@ -527,6 +564,8 @@ static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, con
     a.nprob = n;
     const int64_t M = src1->ne[1];
     if (M > mx::MAX_COLS && mx::gemm_supported(a.type, a.K)) return gemm_group(be, n, src0, src1, dst);
+    if (M > mx::MAX_COLS && a.type == MX_TYPE_Q4_K && a.K % 256 == 0 && !gemm_q4k_disabled())
+        return gemm_q4k_group(be, n, src0, src1, dst);
     if (M > mx::MAX_COLS && mx::gemm_kq_supported(a.type, a.K)) return gemm_kq_group(be, n, src0, src1, dst);
     const int ncmax = max_cols(a.type, a.K);
     for (int64_t m0 = 0; m0 < M; m0 += ncmax) {

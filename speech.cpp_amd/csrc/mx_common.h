@@ -177,6 +177,13 @@ size_t gemm_kq_act_bytes(int64_t M, int64_t K);
 hipError_t launch_gemm_kq_quant(const float *x, int64_t x_stride, int64_t M, int64_t K, void *scratch, hipStream_t s);
 hipError_t launch_gemm_kq(int type, const WPlanes &w, int64_t M, int64_t N, int64_t K, const void *scratch, float *y,
                           int64_t ldy, hipStream_t s);
+// Q4_K prefill GEMM with the sub-block scales folded into the MFMA operands: launch_gemm_q4k_quant writes x as Q8_K
+// plus split sub-block sums into `scratch` (gemm_q4k_act_bytes); launch_gemm_q4k then runs up to four weights
+// (w[i], N[i] rows, into y[i] with row stride ldy[i]) sharing those activations in one launch.
+size_t gemm_q4k_act_bytes(int64_t M, int64_t K);
+hipError_t launch_gemm_q4k_quant(const float *x, int64_t x_stride, int64_t M, int64_t K, void *scratch, hipStream_t s);
+hipError_t launch_gemm_q4k(int nprob, const WPlanes *w, const int64_t *N, float *const *y, const int64_t *ldy,
+                           int64_t M, int64_t K, const void *scratch, hipStream_t s);
 inline bool gemm_kq_supported(int type, int64_t K) {
     return (type == MX_TYPE_Q4_K || type == MX_TYPE_Q6_K) && K % 256 == 0;
 }
