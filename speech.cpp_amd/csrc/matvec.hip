@@ -70,7 +70,16 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
         i13 = (int)(z / (unsigned)a.ne12);
         mat = (int)((unsigned)i12 / (unsigned)a.r2) + (int)((unsigned)i13 / (unsigned)a.r3) * a.ne02;
     }
-    const float *x = a.x + i12 * a.x_b2 + i13 * a.x_b3;
+    int xi12 = i12;
+    if (a.ids) {  // routed expert: the slice's matrix comes from ids (uniform over the workgroup)
+        mat = *(const int32_t *)((const uint8_t *)a.ids + i12 * a.ids_nb0 + i13 * a.ids_nb1);
+        if (mat < 0 || mat >= a.n_mats) {  // ggml-cpu asserts; this pair's output is left as it was and reported
+            if (tid == 0) atomicOr(a.err, 2);
+            return;
+        }
+        xi12 = (int)((unsigned)i12 % (unsigned)a.x_ne12);
+    }
+    const float *x = a.x + xi12 * a.x_b2 + i13 * a.x_b3;
 
     // The activation loads go first: x -> quantization -> LDS is the prologue's critical path, and the memory counter
     // retires loads in order, so waiting for x then does not wait for the weight loads issued after it.

@@ -1,0 +1,335 @@
+// MUL_MAT_ID on Q4_K experts as a grouped product: dst[:, s, t] = as[ids[s, t]] . quant(b[:, s % b_ne1, t]).
+//
+// The prep launch cuts each expert's (token, slot) pairs into chunks of up to 16, the rows of one 16x16 MFMA tile. A
+// workgroup takes one chunk and a few blocks of 64 of the expert's weight rows (dst columns); wave w owns columns
+// 16 w .. 16 w + 15 of each block and streams their super-blocks block after block.
+//
+// The weights stream through a ring of four stages per wave in LDS, filled by global_load_lds copies issued three
+// steps ahead (no registers held for them). The chunk's activation operands (K <= 2048) are loaded into LDS once per
+// workgroup and shared by its four waves and all its column blocks.
+//
+// Arithmetic per 256-element super-block, as ggml-cpu's vec_dot_q4_K_q8_K (and the Q4_K prefill GEMM):
+//   y += dx * (d * sum_j sc_j * S_j  -  dmin * sum_j mn_j * bsum_j)
+// In MFMA step q (q = 0..3) lane group g (lanes 16 g .. 16 g + 15) carries elements 64 q + 16 g .. + 15 of its column
+// and of its activation row: code bytes 32 q + 16 (g & 1) .. + 15, low nibbles for g < 2 (sub-block 2 q), high
+// nibbles for g >= 2 (sub-block 2 q + 1). So a step's activation loads are 64 contiguous bytes of each row, and A and B
+// agree on which element every (lane group, byte) slot carries. The codes are scaled by the 3-bit halves of their
+// own 6-bit scale (sc = 8 hi + lo; hi * q and lo * q are at most 105), so two MFMA chains give sum_j hi_j S_j and
+// sum_j lo_j S_j exactly. The min term is one v_mfma_f32_16x16x16_f16 on [64 h_j | l_j] (bsum_j = 64 h_j + l_j)
+// against the mins, exact.
+#include "mx_common.h"
+#include "mx_device.h"
+
+namespace mx {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+// Two u16 lanes of two codes each times (s, s): each byte's product stays below 256, so bytes do not interact.
+__device__ __forceinline__ int mq_pk_mul(int codes, uint32_t s2) {
+    int r;
+    asm("v_pk_mul_lo_u16 %0, %1, %2" : "=v"(r) : "v"(codes), "v"(s2));
+    return r;
+}
+
+// ggml-quants.c get_scale_min_k4 on the 12 packed scale bytes s0..s2, for sub-block j (0..7).
+__device__ __forceinline__ uint32_t mq_scale(uint32_t s0, uint32_t s2, int j) {
+    const int o = 8 * (j & 3);
+    const uint32_t lo = __builtin_amdgcn_ubfe(s0, o, 6);
+    const uint32_t up = __builtin_amdgcn_ubfe(s2, o, 4) | (__builtin_amdgcn_ubfe(s0, o + 6, 2) << 4);
+    return j < 4 ? lo : up;
+}
+__device__ __forceinline__ uint32_t mq_min(uint32_t s1, uint32_t s2, int j) {
+    const int o = 8 * (j & 3);
+    const uint32_t lo = __builtin_amdgcn_ubfe(s1, o, 6);
+    const uint32_t up = __builtin_amdgcn_ubfe(s2, o + 4, 4) | (__builtin_amdgcn_ubfe(s1, o + 6, 2) << 4);
+    return j < 4 ? lo : up;
+}
+
+constexpr int MQ_COLS = 64;  // dst columns per column block: 16 per wave
+static_assert(MMID_CHUNK == 16, "a chunk is one 16-row MFMA tile");
+
+constexpr int MQ_S = 4;         // ring stages per wave
+constexpr int MQ_STAGE = 2304;  // one stage: 16 columns x (128 code bytes + 12 scale bytes + d | dmin)
+
+typedef __attribute__((address_space(3))) void mq_lds;
+
+// Waits until at most n vector memory ops of this wave are outstanding. The memory clobber keeps the compiler from
+// moving loads and stores across it, so the LDS reads that follow see the copies it waited for.
+template <int n>
+__device__ __forceinline__ void mq_wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+}
+// Keeps the memory ops before it ahead of the ones after it (the wait counts depend on their issue order).
+__device__ __forceinline__ void mq_order() { asm volatile("" ::: "memory"); }
+
+// LDS of a workgroup: per wave a ring of MQ_S weight stages, then the chunk's activation operands for up to
+// MQ_KSEG super-blocks (one segment of K), laid out as the lanes read them:
+//   codes   [sb][q][grp][fr] x 16 bytes: row fr, elements 256 sb + 64 q + 16 grp .. + 15
+//   sums    [sb][fr] x 32 bytes: row fr's split sub-block sums [64 h_j | l_j] (fp16)
+//   scales  [sb][fr] floats: row fr's Q8_K scale
+constexpr int MQ_KSEG = 8;
+constexpr int MQ_RING = 4 * MQ_S * MQ_STAGE;
+constexpr int MQ_AQ = MQ_RING, MQ_A16 = MQ_AQ + MQ_KSEG * 4096, MQ_ADX = MQ_A16 + MQ_KSEG * 512;
+constexpr int MQ_LDS = MQ_ADX + MQ_KSEG * 64;
+
+// One wave's view of its work: the weight stream (ncb column blocks x nsb super-blocks).
+struct MqLane {
+    const uint8_t *qe, *se;  // the expert's code plane (+ 32 grp) and this lane's scale word source
+    int sstride;             // bytes between blocks of the scale source (12 or 4)
+    int col0, scol0;         // column of this lane's codes / of its scale word in column block 0
+    int nmax;                // last column
+    int nsb, nsteps, lane, fr, grp;
+    uint8_t *ring;           // this wave's ring (uniform)
+    uint32_t ring_lds, a_lds;  // LDS byte addresses of the ring and of the activation operands
+};
+
+// Segment `seg` of the chunk's activation operands, as this thread brings it to LDS: pieces of row t & 15 (arow: its
+// activation row). Loads past the segment repeat its last super-block; only the stores are conditional.
+struct MqSeg {
+    v4i codes[MQ_KSEG];  // thread t = (q, grp, fr): elements 64 q + 16 grp .. + 15 of each super-block
+    v4i sums;            // thread t = (sb, half, fr): 8 of the 16 split sums of super-block sb
+    float scale;         // thread t = (sb, fr): the Q8_K scale of super-block sb
+};
+__device__ __forceinline__ MqSeg mq_seg_load(const MulMatIdArgs &a, int arow, int seg, int nsb) {
+    const int t = threadIdx.x;
+    const int sb0 = MQ_KSEG * seg, last = min(MQ_KSEG, nsb - sb0) - 1;
+    MqSeg r;
+    const int8_t *xs = a.xq + arow * (int)a.K + sb0 * 256 + 64 * (t >> 6) + 16 * ((t >> 4) & 3);
+#pragma unroll
+    for (int i = 0; i < MQ_KSEG; i++) r.codes[i] = *(const v4i *)(xs + min(i, last) * 256);
+    r.sums = *(const v4i *)(a.x16 + (arow * nsb + sb0 + min(t >> 5, last)) * 16 + 8 * ((t >> 4) & 1));
+    r.scale = a.xd[arow * nsb + sb0 + min(t >> 4, last)];
+    return r;
+}
+// The stores go through inline assembly: the compiler would otherwise order them after every copy in flight into
+// the (disjoint) ring, since it cannot tell the two LDS regions apart.
+__device__ __forceinline__ void mq_seg_store(const MqSeg &r, uint8_t *smem, int seg, int nsb) {
+    const int t = threadIdx.x, fr = t & 15;
+    const int n = min(MQ_KSEG, nsb - MQ_KSEG * seg);
+    const uint32_t base = (uint32_t)(uintptr_t)(mq_lds *)smem;
+#pragma unroll
+    for (int i = 0; i < MQ_KSEG; i++)
+        if (i < n) asm volatile("ds_write_b128 %0, %1" ::"v"(base + MQ_AQ + i * 4096 + 16 * t), "v"(r.codes[i]) : "memory");
+    if ((t >> 5) < n)
+        asm volatile("ds_write_b128 %0, %1" ::"v"(base + MQ_A16 + (t >> 5) * 512 + fr * 32 + ((t >> 4) & 1) * 16),
+                     "v"(r.sums) : "memory");
+    if ((t >> 4) < n)
+        asm volatile("ds_write_b32 %0, %1" ::"v"(base + MQ_ADX + (t >> 4) * 64 + fr * 4), "v"(r.scale) : "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// Where the next copy comes from: column block cb (its per-lane sources at qcb / scb) and super-block sb.
+struct MqCursor {
+    const uint8_t *qcb, *scb;
+    int cb, sb;
+};
+__device__ __forceinline__ void mq_seek(const MqLane &c, MqCursor &k, int cb) {
+    const int64_t qcol = min(c.col0 + MQ_COLS * cb, c.nmax), scol = min(c.scol0 + MQ_COLS * cb, c.nmax);
+    k.qcb = c.qe + qcol * c.nsb * 128;
+    k.scb = c.se + scol * c.nsb * c.sstride;
+    k.cb = cb;
+}
+
+// Copies the cursor's super-block of the wave's 16 columns into ring stage SLOT (3 vector memory ops) and advances
+// the cursor; past the last step it stays on the last one, so the copies after the end repeat it.
+template <int SLOT>
+__device__ __forceinline__ void mq_copy(const MqLane &c, MqCursor &k, int ncb) {
+    uint8_t *st = c.ring + SLOT * MQ_STAGE;
+    __builtin_amdgcn_global_load_lds((const void *)(k.qcb + k.sb * 128), (mq_lds *)st, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void *)(k.qcb + k.sb * 128 + 16), (mq_lds *)(st + 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void *)(k.scb + k.sb * c.sstride), (mq_lds *)(st + 2048), 4, 0, 0);
+    if (k.sb + 1 < c.nsb) {
+        k.sb++;
+    } else if (k.cb + 1 < ncb) {
+        k.sb = 0;
+        mq_seek(c, k, k.cb + 1);
+    }
+}
+
+// Step of the wave's stream: super-block sb (sbl within the loaded segment) of its column block, weights in ring
+// stage SLOT. Each step issues the copies MQ_S - 1 steps ahead (3 ops) and then waits for its own, which were issued
+// MQ_S - 1 copies (9 ops) earlier. Operands are read from LDS in one block with the compiler kept out of it: it cannot
+// see that the copies waited for wrote there.
+template <int SLOT>
+__device__ __forceinline__ void mq_step(const MqLane &c, MqCursor &k, int ncb, int sbl, float (&acc)[4]) {
+    static_assert(MQ_S == 4, "the wait count assumes four stages");
+    mq_copy<(SLOT + MQ_S - 1) % MQ_S>(c, k, ncb);
+    mq_wait_vm<9>();
+    const uint32_t st = c.ring_lds + SLOT * MQ_STAGE;
+    const uint32_t aq = c.a_lds + MQ_AQ - MQ_RING + sbl * 4096 + 16 * c.lane;
+    const uint32_t a16 = c.a_lds + MQ_A16 - MQ_RING + sbl * 512 + 32 * c.fr + 8 * c.grp;
+    const uint32_t adx = c.a_lds + MQ_ADX - MQ_RING + sbl * 64 + 16 * c.grp;
+    v4i w[4];   // code bytes 32 q + 16 (grp & 1) .. + 15 of column fr
+    uint4 sv;   // its scale words 0..2, d | dmin
+    v4i xa[4];  // activation bytes 64 q + 16 grp .. + 15 of row fr
+    v4h s16;    // row fr's split sums 4 grp .. 4 grp + 3
+    v4f dxv;    // Q8_K scales of rows 4 grp .. 4 grp + 3
+    asm volatile(
+        "ds_read_b128 %0, %11\n"
+        "ds_read_b128 %1, %11 offset:256\n"
+        "ds_read_b128 %2, %11 offset:512\n"
+        "ds_read_b128 %3, %11 offset:768\n"
+        "ds_read_b128 %4, %12 offset:2048\n"
+        "ds_read_b128 %5, %13\n"
+        "ds_read_b128 %6, %13 offset:1024\n"
+        "ds_read_b128 %7, %13 offset:2048\n"
+        "ds_read_b128 %8, %13 offset:3072\n"
+        "ds_read_b64 %9, %14\n"
+        "ds_read_b128 %10, %15\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(sv), "=&v"(xa[0]), "=&v"(xa[1]), "=&v"(xa[2]),
+          "=&v"(xa[3]), "=&v"(s16), "=&v"(dxv)  // early clobber: no output may share a register with an address
+        : "v"(st + 1024 * (c.grp & 1) + 16 * c.fr), "v"(st + 16 * c.fr), "v"(aq), "v"(a16), "v"(adx)
+        : "memory");
+
+    const int grp = c.grp, hi = grp >> 1;
+    const v4i mask = {0x0F0F0F0F, 0x0F0F0F0F, 0x0F0F0F0F, 0x0F0F0F0F};
+    // mins of sub-blocks (4 grp + i) mod 8, matching the [64 h | l] halves this lane group carries
+    v4h b16;
+#pragma unroll
+    for (int i = 0; i < 4; i++) b16[i] = (_Float16)(float)mq_min(sv.y, sv.z, 4 * (grp & 1) + i);
+    const float d = h2f((uint16_t)(sv.w & 0xFFFF)), dmin = h2f((uint16_t)(sv.w >> 16));
+    v4i ih = {0, 0, 0, 0}, il = {0, 0, 0, 0};
+#pragma unroll
+    for (int q = 0; q < 4; q++) {  // codes scaled by the hi / lo halves of their sub-block's scale
+        const uint32_t sc = mq_scale(sv.x, sv.z, 2 * q + hi);
+        const uint32_t h = (sc >> 3) * 0x10001u, l = (sc & 7) * 0x10001u;
+        const v4i cq = (w[q] >> (4 * hi)) & mask;
+        const v4i bh = {mq_pk_mul(cq.x, h), mq_pk_mul(cq.y, h), mq_pk_mul(cq.z, h), mq_pk_mul(cq.w, h)};
+        const v4i bl = {mq_pk_mul(cq.x, l), mq_pk_mul(cq.y, l), mq_pk_mul(cq.z, l), mq_pk_mul(cq.w, l)};
+        ih = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[q], bh, ih, 0, 0, 0);
+        il = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[q], bl, il, 0, 0, 0);
+    }
+    const v4f mt = __builtin_amdgcn_mfma_f32_16x16x16f16(s16, b16, (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {  // output row 4 grp + i
+        const int v = (ih[i] << 3) + il[i];
+        acc[i] = fmaf(dxv[i], fmaf(-dmin, mt[i], d * (float)v), acc[i]);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // steps do not interleave: one step's operands live at a time
+}
+
+// Grid: x = groups of `cpb` column blocks of MQ_COLS, y = chunks (workgroups past the last chunk leave at once).
+// Wave w owns columns 16 w .. 16 w + 15 of each block and streams super-blocks 0 .. nsb - 1 (nsb <= MQ_KSEG) of
+// every block; a block's sums are written when its last super-block is done.
+__global__ __launch_bounds__(256) void k_mmid_q4k(MulMatIdArgs a, int cpb) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int chunk = blockIdx.y;
+    if (chunk >= a.ntiles[0]) return;  // uniform: fewer chunks than the grid allows
+    const int p0 = a.tiles[3 * chunk], cnt = a.tiles[3 * chunk + 1], e = a.tiles[3 * chunk + 2];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int N = (int)a.N;
+    const unsigned n_ids = (unsigned)a.n_ids;
+    const int nblk = (N + MQ_COLS - 1) / MQ_COLS;
+    const int cb0 = blockIdx.x * cpb, ncb = min(cpb, nblk - cb0);
+
+    MqLane c;
+    c.lane = threadIdx.x & 63;
+    c.fr = c.lane & 15;
+    c.grp = c.lane >> 4;
+    c.nsb = (int)(a.K / 256);
+    c.nsteps = ncb * c.nsb;
+    // row fr of the chunk is pair p0 + fr (rows past the chunk repeat its last pair; their sums are dropped)
+    const int pair = a.pairs[p0 + min(c.fr, cnt - 1)];
+    const unsigned pt = (unsigned)pair / n_ids, ps = (unsigned)pair - pt * n_ids;
+    const int arow = (int)(pt * (unsigned)a.b_ne1 + (a.b_ne1 == 1 ? 0u : ps));
+    // Copy sources: lane l brings code bytes 32 grp + 16 h (h = 0, 1) of column fr, and scale word l & 3 of column
+    // l >> 2 (words 0..2: the 12 scale bytes, word 3: d | dmin). They land at stage + 1024 h + 16 l and stage + 2048 +
+    // 4 l: bytes 32 q + 16 h of column fr sit at stage + 1024 h + 256 q + 16 fr, its scale words at stage + 2048 + 16 fr.
+    const int64_t eblk = (int64_t)e * N * c.nsb;
+    c.nmax = N - 1;
+    c.col0 = cb0 * MQ_COLS + wave * 16 + c.fr;
+    c.scol0 = cb0 * MQ_COLS + wave * 16 + (c.lane >> 2);
+    c.qe = a.w.p0 + eblk * 128 + 32 * c.grp;
+    const int sw = c.lane & 3;
+    c.sstride = sw < 3 ? 12 : 4;
+    c.se = sw < 3 ? a.w.p1 + eblk * 12 + 4 * sw : a.w.p2 + eblk * 4;
+    c.ring = smem + wave * MQ_S * MQ_STAGE;
+    c.ring_lds = (uint32_t)(uintptr_t)(mq_lds *)c.ring;
+    c.a_lds = (uint32_t)(uintptr_t)(mq_lds *)(smem + MQ_RING);
+
+    // activation operands of the first segment (their loads go out ahead of the copies), then the ring's prologue
+    MqCursor k;
+    k.sb = 0;
+    mq_seek(c, k, 0);
+    {
+        const MqSeg seg0 = mq_seg_load(a, arow, 0, c.nsb);
+        mq_order();
+        mq_copy<0>(c, k, ncb);
+        mq_copy<1>(c, k, ncb);
+        mq_copy<2>(c, k, ncb);
+        mq_seg_store(seg0, smem, 0, c.nsb);  // its wait leaves the copies in flight
+    }
+    __syncthreads();
+
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    int sb = 0, cb = 0;
+    // after each step: a column block is finished when its last super-block is
+    auto finish = [&]() {
+        if (++sb < c.nsb) return;
+        const int col = c.col0 + MQ_COLS * cb;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = 4 * c.grp + i;
+            const unsigned pi = (unsigned)__shfl(pair, row, 64);  // lane `row` holds that row's pair
+            if (row < cnt && col <= c.nmax) {
+                const unsigned t = pi / n_ids, s = pi - t * n_ids;
+                float *y = (float *)((uint8_t *)a.dst + (int64_t)s * a.dst_nb1 + (int64_t)t * a.dst_nb2);
+                y[col] = acc[i];
+            }
+            acc[i] = 0.f;
+        }
+        sb = 0;
+        cb++;
+    };
+#pragma unroll 1
+    for (int it = 0; it < c.nsteps; it += MQ_S) {
+        mq_step<0>(c, k, ncb, sb, acc);
+        finish();
+        if (it + 1 < c.nsteps) {
+            mq_step<1>(c, k, ncb, sb, acc);
+            finish();
+        }
+        if (it + 2 < c.nsteps) {
+            mq_step<2>(c, k, ncb, sb, acc);
+            finish();
+        }
+        if (it + 3 < c.nsteps) {
+            mq_step<3>(c, k, ncb, sb, acc);
+            finish();
+        }
+    }
+    mq_wait_vm<0>();  // no copy may still be landing in LDS when the workgroup ends
+}
+
+// Column blocks per workgroup: enough workgroups for about two per CU over the chunks the grid allows for.
+static int mq_cpb(const MulMatIdArgs &a) {
+    const int64_t nblk = (a.N + MQ_COLS - 1) / MQ_COLS;
+    const int64_t cpb = a.max_tiles * nblk / 512;
+    return (int)(cpb < 1 ? 1 : (cpb > nblk ? nblk : cpb));
+}
+
+bool mmid_q4k_supported(const MulMatIdArgs &a) {
+    return a.type == MX_TYPE_Q4_K && a.K % 256 == 0 && a.K / 256 <= MQ_KSEG &&
+           a.T * a.b_ne1 * a.K < ((int64_t)1 << 31) && a.N < ((int64_t)1 << 31) - MQ_COLS;
+}
+
+hipError_t launch_mmid_q4k(const MulMatIdArgs &a, hipStream_t s) {
+    if (!mmid_q4k_supported(a)) return hipErrorInvalidValue;
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t err = hipFuncSetAttribute((const void *)k_mmid_q4k,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, MQ_LDS);
+        if (err != hipSuccess) return err;
+        attr = true;
+    }
+    const int64_t nblk = (a.N + MQ_COLS - 1) / MQ_COLS;
+    const int cpb = mq_cpb(a);
+    const dim3 grid((unsigned)((nblk + cpb - 1) / cpb), (unsigned)a.max_tiles);
+    hipLaunchKernelGGL(k_mmid_q4k, grid, dim3(256), MQ_LDS, s, a, cpb);
+    return hipGetLastError();
+}
+
+}  // namespace mx

@@ -1,15 +1,18 @@
 // MUL_MAT_ID for routed experts: dst[:, s, t] = as[ids[s, t]] . quant(b[:, s % b_ne1, t]).
 //
-// Three launches, no host round trip:
-//   1. bucket: one workgroup counts (token, slot) pairs per expert, builds the list of experts that have any, and
-//      groups the pairs by expert (the matrix_row_counts / matrix_rows of ggml-cpu.c ggml_compute_forward_mul_mat_id).
-//   2. quant: every activation row is quantized once (ggml-cpu quantizes src1 once, before the experts run).
-//   3. experts: grid.y walks the experts that were touched; each workgroup streams a tile of its expert's rows once
-//      and applies it to up to 8 of the expert's pairs per pass, so an expert's weights are read once per 8 pairs and
-//      untouched experts cost nothing.
+// A few (token, slot) pairs (a decode step) take one mat-vec launch: each pair streams its expert's rows with the
+// activation quantized in the prologue. More pairs take two launches, no host round trip:
+//   1. prep: workgroup 0 counts (token, slot) pairs per expert, lists the experts that have any, groups the pairs by
+//      expert (the matrix_row_counts / matrix_rows of ggml-cpu.c ggml_compute_forward_mul_mat_id) and cuts each
+//      expert's pairs into chunks; the other workgroups quantize every activation row once (ggml-cpu quantizes src1
+//      once, before the experts run).
+//   2. experts: Q4_K experts run as a grouped MFMA product over the chunks (mmid_q4k.hip); the other types stream
+//      each touched expert's weights once per 8 pairs on dot4 (k_mmid_experts below). Untouched experts cost nothing.
 #include "mx_common.h"
 #include "mx_device.h"
 #include "mx_dot.h"
+
+#include <cstdlib>
 
 namespace mx {
 
@@ -28,73 +31,148 @@ size_t mul_mat_id_scratch(MulMatIdArgs *a, void *base) {
     a->xq = (int8_t *)(b + off);       off += al256((size_t)nrows * (size_t)a->K);
     a->xd = (float *)(b + off);        off += al256((size_t)nrows * (size_t)nsc * 4);
     a->xbs = (int32_t *)(b + off);     off += al256(a->type == MX_TYPE_Q8_0 ? 0 : (size_t)nrows * (size_t)(a->K / 16) * 4);
+    a->x16 = (_Float16 *)(b + off);    off += al256(a->type == MX_TYPE_Q4_K ? (size_t)nrows * (size_t)(a->K / 256) * 32 : 0);
+    // chunks: sum over experts of ceil(count / MMID_CHUNK) <= npairs / MMID_CHUNK + (experts with pairs)
+    a->max_tiles = npairs / MMID_CHUNK + (npairs < a->E ? npairs : a->E) + 1;
+    a->tiles = (int32_t *)(b + off);   off += al256((size_t)a->max_tiles * 12);
+    a->ntiles = (int32_t *)(b + off);  off += 256;
     return off;
 }
 
-__global__ __launch_bounds__(1024) void k_mmid_bucket(MulMatIdArgs a) {
-    extern __shared__ int cnt[];  // [E]
-    const int64_t npairs = a.n_ids * a.T;
-    for (int64_t e = threadIdx.x; e < a.E; e += 1024) cnt[e] = 0;
+// Exclusive prefix sums of three counters over the 256 threads of a workgroup (tmp: 4 waves' totals in LDS).
+__device__ __forceinline__ int3 scan3_256(int3 v, int3 *tmp, int3 *total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int3 inc = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int x = __shfl_up(inc.x, off, 64), y = __shfl_up(inc.y, off, 64), z = __shfl_up(inc.z, off, 64);
+        if (lane >= off) inc = make_int3(inc.x + x, inc.y + y, inc.z + z);
+    }
+    if (lane == 63) tmp[wave] = inc;
     __syncthreads();
-    for (int64_t p = threadIdx.x; p < npairs; p += 1024) {
-        const int64_t t = p / a.n_ids, s = p % a.n_ids;
+    int3 base = make_int3(0, 0, 0), all = make_int3(0, 0, 0);
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const int3 t = tmp[w];
+        if (w < wave) base = make_int3(base.x + t.x, base.y + t.y, base.z + t.z);
+        all = make_int3(all.x + t.x, all.y + t.y, all.z + t.z);
+    }
+    *total = all;
+    return make_int3(base.x + inc.x - v.x, base.y + inc.y - v.y, base.z + inc.z - v.z);
+}
+
+// Workgroup 0 of the prep launch: counts (token, slot) pairs per expert, lists the experts that have any, groups the
+// pairs by expert (the matrix_row_counts / matrix_rows of ggml-cpu.c ggml_compute_forward_mul_mat_id) and cuts each
+// expert's pairs into chunks of up to MMID_CHUNK. The order of pairs within an expert does not matter: every pair's
+// output is computed on its own.
+__device__ void mmid_bucket(const MulMatIdArgs &a) {
+    extern __shared__ int cnt[];  // [E]
+    __shared__ int3 tmp[4];
+    const int tid = threadIdx.x;
+    const int E = (int)a.E;
+    const int npairs = (int)(a.n_ids * a.T);
+    for (int e = tid; e < E; e += 256) cnt[e] = 0;
+    __syncthreads();
+    for (int p = tid; p < npairs; p += 256) {
+        const int t = p / (int)a.n_ids, s = p - t * (int)a.n_ids;
         const int32_t e = *(const int32_t *)((const uint8_t *)a.ids + s * a.ids_nb0 + t * a.ids_nb1);
-        if (e < 0 || e >= a.E) atomicOr(a.err, 2);  // ggml-cpu asserts; this pair is dropped and reported
+        if (e < 0 || e >= E) atomicOr(a.err, 2);  // ggml-cpu asserts; this pair is dropped and reported
         else atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0, nact = 0;
-        for (int64_t e = 0; e < a.E; e++) {
-            const int c = cnt[e];
-            a.counts[e] = c;
-            a.offsets[e] = run;
-            if (c > 0) a.active[1 + nact++] = (int32_t)e;
-            cnt[e] = run;  // becomes the fill cursor
-            run += c;
+    // each thread owns a run of consecutive experts
+    const int ept = (E + 255) / 256, e0 = tid * ept, e1 = min(E, e0 + ept);
+    int3 mine = make_int3(0, 0, 0);  // pairs, chunks, experts with pairs
+    for (int e = e0; e < e1; e++) {
+        const int c = cnt[e];
+        mine = make_int3(mine.x + c, mine.y + (c + MMID_CHUNK - 1) / MMID_CHUNK, mine.z + (c > 0));
+    }
+    int3 total;
+    int3 at = scan3_256(mine, tmp, &total);
+    for (int e = e0; e < e1; e++) {
+        const int c = cnt[e];
+        a.counts[e] = c;
+        a.offsets[e] = at.x;
+        if (c > 0) a.active[1 + at.z++] = e;
+        for (int i = 0; i < c; i += MMID_CHUNK, at.y++) {
+            a.tiles[3 * at.y] = at.x + i;
+            a.tiles[3 * at.y + 1] = min(MMID_CHUNK, c - i);
+            a.tiles[3 * at.y + 2] = e;
         }
-        a.active[0] = nact;
+        cnt[e] = at.x;  // becomes the fill cursor
+        at.x += c;
+    }
+    if (tid == 0) {
+        a.active[0] = total.z;
+        a.ntiles[0] = total.y;
     }
     __syncthreads();
-    for (int64_t p = threadIdx.x; p < npairs; p += 1024) {
-        const int64_t t = p / a.n_ids, s = p % a.n_ids;
+    for (int p = tid; p < npairs; p += 256) {
+        const int t = p / (int)a.n_ids, s = p - t * (int)a.n_ids;
         const int32_t e = *(const int32_t *)((const uint8_t *)a.ids + s * a.ids_nb0 + t * a.ids_nb1);
-        if (e < 0 || e >= a.E) continue;
-        const int pos = atomicAdd(&cnt[e], 1);
-        a.pairs[pos] = (int32_t)p;
+        if (e < 0 || e >= E) continue;
+        a.pairs[atomicAdd(&cnt[e], 1)] = p;
     }
 }
 
-// Quantizes activation row r = t * b_ne1 + s' of b into the scratch rows (same arithmetic as the fused prologue).
+// Quantizes activation row r = t * b_ne1 + s' of b into the scratch rows, 1024 elements per pass (the arithmetic of
+// the mat-vec prologue). Q4_K also gets each super-block's sub-block sums split as [64 h_j | l_j] in fp16.
 template <int TYPE>
-__global__ __launch_bounds__(256) void k_mmid_quant(MulMatIdArgs a) {
-    const int64_t r = blockIdx.y;
+__device__ void mmid_quant_row(const MulMatIdArgs &a, int64_t r) {
     const int64_t t = r / a.b_ne1, s = r % a.b_ne1;
     const float *x = (const float *)((const uint8_t *)a.b + s * a.b_nb1 + t * a.b_nb2);
-    const int64_t K = a.K;
-    const int64_t e = (int64_t)blockIdx.x * 1024 + 4 * threadIdx.x;
+    const int K = (int)a.K;
     const int lane = threadIdx.x & 63;
-    if (TYPE == MX_TYPE_Q8_0) {
-        const bool valid = e < K;
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (valid) v = *(const float4 *)(x + e);
-        float d;
-        int sum;
-        const int q = quant32_lane(v, a.rounding, &d, &sum);
-        if (valid) {
-            *(int *)(a.xq + r * K + e) = q;
-            if ((threadIdx.x & 7) == 0) a.xd[r * (K / 32) + e / 32] = h2f(f2h(d));
-        }
-    } else {
-        if ((int64_t)blockIdx.x * 1024 + 256 * (threadIdx.x >> 6) >= K) return;  // whole wave
-        const float4 v = *(const float4 *)(x + e);
-        float d;
-        int bs;
-        const int q = quant256_wave(v, lane, &d, &bs);
-        *(int *)(a.xq + r * K + e) = q;
-        if (lane == 0) a.xd[r * (K / 256) + e / 256] = d;
-        if ((lane & 3) == 0) a.xbs[r * (K / 16) + e / 16] = bs;
+    constexpr int PRE = 4;
+    float4 v[PRE];
+#pragma unroll
+    for (int i = 0; i < PRE; i++) {
+        const int e = 1024 * i + 4 * threadIdx.x;
+        v[i] = e < K ? *(const float4 *)(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    for (int base = 0; base < K; base += 1024) {
+        const int i = base / 1024;
+        const int e = base + 4 * threadIdx.x;
+        float4 xv;
+        if (i < PRE) {
+            xv = i == 0 ? v[0] : (i == 1 ? v[1] : (i == 2 ? v[2] : v[3]));
+        } else {
+            xv = e < K ? *(const float4 *)(x + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (TYPE == MX_TYPE_Q8_0) {
+            float d;
+            int sum;
+            const int q = quant32_lane(xv, a.rounding, &d, &sum);
+            if (e < K) {  // K % 32 == 0: the eight lanes of a block agree
+                *(int *)(a.xq + r * K + e) = q;
+                if ((threadIdx.x & 7) == 0) a.xd[r * (K / 32) + e / 32] = h2f(f2h(d));
+            }
+        } else {
+            if (base + 256 * (threadIdx.x >> 6) >= K) continue;  // whole wave
+            float d;
+            int bs;
+            const int q = quant256_wave(xv, lane, &d, &bs);
+            *(int *)(a.xq + r * K + e) = q;
+            if (lane == 0) a.xd[r * (K / 256) + e / 256] = d;
+            if ((lane & 3) == 0) a.xbs[r * (K / 16) + e / 16] = bs;
+            if (TYPE == MX_TYPE_Q4_K) {
+                const int bs32 = bs + dpp_i<dpp::HALF_MIRROR>(0, bs);  // lanes 8j..8j+7: sub-block j's sum
+                if ((lane & 7) == 0) {
+                    const int j = lane >> 3, h = bs32 >> 6;  // floor(bs32 / 64)
+                    _Float16 *o = a.x16 + (r * (K / 256) + e / 256) * 16;
+                    o[j] = (_Float16)(64 * h);
+                    o[8 + j] = (_Float16)(bs32 - 64 * h);
+                }
+            }
+        }
+    }
+}
+
+// One launch for both: workgroup 0 buckets the pairs, workgroup 1 + r quantizes activation row r.
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_mmid_prep(MulMatIdArgs a) {
+    if (blockIdx.x == 0) mmid_bucket(a);
+    else mmid_quant_row<TYPE>(a, (int64_t)blockIdx.x - 1);
 }
 
 template <int TYPE, int LPR>
@@ -157,15 +235,22 @@ __global__ __launch_bounds__(256) void k_mmid_experts(MulMatIdArgs a) {
     }
 }
 
+// MX_MMID_Q4K=0 keeps Q4_K experts on the mat-vec style kernel (k_mmid_experts).
+static bool mmid_q4k_disabled() {
+    static const bool off = [] {
+        const char *e = getenv("MX_MMID_Q4K");
+        return e && e[0] == '0';
+    }();
+    return off;
+}
+
 template <int TYPE>
 static hipError_t launch_typed(const MulMatIdArgs &a, hipStream_t s) {
     const int64_t nrows = a.T * a.b_ne1;
-    hipLaunchKernelGGL(k_mmid_bucket, dim3(1), dim3(1024), (size_t)a.E * 4, s, a);
-    hipError_t err = hipGetLastError();
+    hipLaunchKernelGGL(k_mmid_prep<TYPE>, dim3((unsigned)(nrows + 1)), dim3(256), (size_t)a.E * 4, s, a);
+    const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_mmid_quant<TYPE>, dim3((unsigned)((a.K + 1023) / 1024), (unsigned)nrows), dim3(256), 0, s, a);
-    err = hipGetLastError();
-    if (err != hipSuccess) return err;
+    if (TYPE == MX_TYPE_Q4_K && !mmid_q4k_disabled() && mmid_q4k_supported(a)) return launch_mmid_q4k(a, s);
     const int64_t npairs = a.n_ids * a.T;
     const unsigned gy = (unsigned)(npairs < a.E ? npairs : a.E);
     const size_t lds = act_lds_bytes(TYPE, a.K, MAX_COLS);
@@ -180,8 +265,52 @@ static hipError_t launch_typed(const MulMatIdArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Up to this many (token, slot) pairs run as one mat-vec launch per pair (MX_MMID_MATVEC_PAIRS overrides): each pair
+// streams its expert's rows with the activation quantized in the prologue, so a decode step's MUL_MAT_ID is a single
+// launch. More pairs go through the bucket and share each expert's weights between them.
+static int64_t mmid_matvec_pairs() {
+    static const int64_t v = [] {
+        const char *e = getenv("MX_MMID_MATVEC_PAIRS");
+        return e ? (int64_t)atoll(e) : (int64_t)16;
+    }();
+    return v;
+}
+
+static hipError_t launch_matvec_ids(const MulMatIdArgs &a, hipStream_t s) {
+    MatvecArgs m{};
+    m.type = a.type;
+    m.ncols = 1;
+    m.rounding = a.rounding;
+    m.K = a.K;
+    m.x = a.b;
+    m.x_col_stride = 0;
+    m.nbatch = (int)(a.n_ids * a.T);
+    m.ne12 = (int)a.n_ids;
+    m.ne02 = 1;
+    m.r2 = 1;
+    m.r3 = 1;
+    m.x_b2 = a.b_nb1 / 4;
+    m.x_b3 = a.b_nb2 / 4;
+    m.y_b2 = a.dst_nb1 / 4;
+    m.y_b3 = a.dst_nb2 / 4;
+    m.nprob = 1;
+    m.prob[0].w = a.w;
+    m.prob[0].N = a.N;
+    m.prob[0].row0 = 0;
+    m.prob[0].y = a.dst;
+    m.prob[0].y_col_stride = 0;
+    m.ids = a.ids;
+    m.ids_nb0 = a.ids_nb0;
+    m.ids_nb1 = a.ids_nb1;
+    m.n_mats = (int)a.E;
+    m.x_ne12 = (int)a.b_ne1;
+    m.err = a.err;
+    return launch_matvec(m, s);
+}
+
 hipError_t launch_mul_mat_id(const MulMatIdArgs &a, hipStream_t s) {
     if (a.n_ids * a.T == 0 || a.N == 0) return hipSuccess;
+    if (a.n_ids * a.T <= mmid_matvec_pairs()) return launch_matvec_ids(a, s);
     switch (a.type) {
         case MX_TYPE_Q8_0: return launch_typed<MX_TYPE_Q8_0>(a, s);
         case MX_TYPE_Q4_K: return launch_typed<MX_TYPE_Q4_K>(a, s);

@@ -399,7 +399,8 @@ MX_API int mx_supports_op(int op, const mx_tensor *src0, const mx_tensor *src1, 
             const int64_t n_ids = ids->ne[0], T = ids->ne[1];
             if (b->ne[2] != T || (b->ne[1] != 1 && b->ne[1] != n_ids)) return 0;
             if (dst->ne[0] != src0->ne[1] || dst->ne[1] != n_ids || dst->ne[2] != T || dst->ne[3] != 1) return 0;
-            if (src0->ne[2] > 65536) return 0;
+            // experts' pair counters live in LDS (4 bytes each); pairs are indexed with 32 bits
+            if (src0->ne[2] > 8192 || n_ids * T >= ((int64_t)1 << 31)) return 0;
             return mx::act_lds_bytes(src0->type, K, mx::MAX_COLS) <= kMaxLds;
         }
         default: return 0;

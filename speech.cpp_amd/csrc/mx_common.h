@@ -158,6 +158,12 @@ struct MatvecArgs {
     // problems sharing x (grid.y picks the problem)
     int nprob;
     MatvecProblem prob[4];
+    // MUL_MAT_ID with few (token, slot) pairs: when ids is set, slice (i12, i13) is slot i12 of token i13, its matrix
+    // is ids[i12, i13] (of n_mats), and it reads src1 slice (i12 % x_ne12, i13). Out-of-range ids set bit 2 of *err.
+    const int32_t *ids;
+    int64_t ids_nb0, ids_nb1;  // bytes
+    int n_mats, x_ne12;
+    int *err;
 };
 hipError_t launch_matvec(const MatvecArgs &a, hipStream_t s);
 
@@ -210,10 +216,19 @@ struct MulMatIdArgs {
     int8_t *xq;            // [T * b_ne1][K] quantized activation rows
     float *xd;             // [T * b_ne1][K / blk] their scales
     int32_t *xbs;          // [T * b_ne1][K / 16] their 16-element sums (K-quants)
+    _Float16 *x16;         // [T * b_ne1][K / 256][16] Q4_K: per super-block [64 h_j | l_j], bsum32_j = 64 h_j + l_j
+    int32_t *tiles;        // [max_tiles][3]: chunks of an expert's pairs: first (index into `pairs`), count, expert
+    int32_t *ntiles;       // [1] tiles written by the bucket kernel
+    int64_t max_tiles;
     int *err;
 };
+// Pairs per chunk: 16-row MFMA groups that share each expanded weight fragment.
+constexpr int MMID_CHUNK = 16;
 // Scratch bytes MUL_MAT_ID needs and the carving of `base` into the fields above.
 size_t mul_mat_id_scratch(MulMatIdArgs *a, void *base);
 hipError_t launch_mul_mat_id(const MulMatIdArgs &a, hipStream_t s);
+// Q4_K experts as a grouped product over chunks of up to MMID_CHUNK of an expert's pairs (16 x 16 x 64 int8 MFMA).
+bool mmid_q4k_supported(const MulMatIdArgs &a);  // Q4_K, K <= 2048
+hipError_t launch_mmid_q4k(const MulMatIdArgs &a, hipStream_t s);
 
 }  // namespace mx

@@ -237,12 +237,13 @@ def test_supports_op(mx, be):
 
 
 # --------------------------------------------------------------------------------------------------- MUL_MAT_ID
-def mmid_case(mx, be, t, E, K, N, n_ids, T, bcast, seed):
+def mmid_case(mx, be, t, E, K, N, n_ids, T, bcast, seed, skew=0.0):
     w = weights(t, E * N, K, seed).reshape(E, N, -1)
     B = 1 if bcast else n_ids
     x = acts(seed + 1, T * B, K).reshape(T, B, K)
     rng = np.random.default_rng(seed)
     logits = rng.standard_normal((T, E))
+    logits[:, :n_ids] += skew  # a large skew sends most tokens to the same experts
     ids = np.argsort(-logits, axis=1)[:, :n_ids].astype(np.int32)
     Wt = be.tensor(t, (K, N, E), w.reshape(E * N, -1))
     Xt = be.tensor(mx.F32, (K, B, T), x)
@@ -259,6 +260,14 @@ def mmid_case(mx, be, t, E, K, N, n_ids, T, bcast, seed):
 @pytest.mark.parametrize("bcast", [True, False], ids=["b_bcast", "b_per_slot"])
 def test_mul_mat_id(mx, be, t, T, bcast):
     y, y_ref = mmid_case(mx, be, t, E=8, K=512, N=96, n_ids=2, T=T, bcast=bcast, seed=0x5EED0900 + T + t)
+    assert rel_err(y, y_ref) <= TIGHT
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("skew", [0.0, 3.0], ids=["spread", "skewed"])
+def test_mul_mat_id_many_pairs(mx, be, t, skew):
+    """Experts with more than 16 pairs (several tiles, a ragged last one) and N not a multiple of the column tile."""
+    y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=70, bcast=False, seed=0x5EED0A00 + t, skew=skew)
     assert rel_err(y, y_ref) <= TIGHT
 
 
