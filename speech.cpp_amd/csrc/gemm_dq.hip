@@ -1,0 +1,436 @@
+// Prefill products (M > 8) on the fp16 matrix cores over dequantized tiles: Y = deq(W) . deq(quant(X)).
+//
+// The activations are quantized exactly as ggml-cpu quantizes src1 for the weight's vec_dot (Q8_0 blocks with the
+// fp16-rounded d) and written back as fp16(d * q); the weight tiles are dequantized in LDS to fp16(d * q). Both
+// roundings are single roundings of an exact product (relative error <= 2^-11 each), and the products accumulate over
+// all of K in fp32 inside the MFMA, so there is no per-block epilogue: the VALU work is the weight conversion, once
+// per workgroup and element. Against ggml-cpu's per-block integer sums the row-relative error is a few 1e-4.
+//
+// Tiles: BM x BN per workgroup of WGM x WGN waves, each (BM / WGM) x (BN / WGN) as 32 x 32 v_mfma_f32_32x32x16_f16
+// tiles.
+// K advances in stages of 64. Every wave copies its share of each stage straight into LDS with global_load_lds
+// (activations: fp16 rows; weights: the raw code bytes and block scales) three stages ahead, through rings of four
+// stages; one stage ahead of the matrix cores the workgroup converts the stage's raw weights into an fp16 tile (double
+// buffered). One barrier per stage. LDS accesses in the loop are inline assembly with explicit waits: the compiler
+// cannot see which stage a copy went to, and would otherwise wait for every copy in flight.
+#include "mx_common.h"
+#include "mx_device.h"
+
+#include <cstdio>
+#include <cstdlib>
+
+namespace mx {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void dq_lds;
+
+constexpr int DQ_KS = 64;  // K per stage
+constexpr int DQ_NS = 4;   // ring stages (copies run DQ_NS - 1 stages ahead)
+
+// LDS map of a BM x BN workgroup of NW waves. Row-major fp16 tiles of 64 halves (128 bytes) per row; the 16-byte
+// chunk c of row r sits at chunk c ^ ((r >> 1) & 7), so the 16 rows one pass of an MFMA fragment read touches hit all
+// 64 banks once.
+template <int BM, int BN, int NW>
+struct DqLds {
+    static constexpr int A = 0;                            // [stage][BM][128 B] activations
+    static constexpr int BH = A + DQ_NS * BM * 128;        // [2][BN][128 B] dequantized weights
+    static constexpr int RAW = BH + 2 * BN * 128;          // [stage][BN][64 B] weight codes
+    static constexpr int SC = RAW + DQ_NS * BN * 64;       // [stage][BN][4 B] the two block scales of each row
+    static constexpr int JUNK = SC + DQ_NS * BN * 4;       // [wave][1 KB] where copies beyond a tile's need land
+    static constexpr int SIZE = JUNK + NW * 1024;
+    // copy instructions per stage (64 lanes each): activation rows (16 B), code rows (16 B), scales (4 B), and per wave
+    static constexpr int NA = BM / 8, NC = BN / 16, NS4 = BN / 64;
+    static constexpr int PA = (NA + NW - 1) / NW, PC = (NC + NW - 1) / NW, PS = (NS4 + NW - 1) / NW;
+    static constexpr int OPS = PA + PC + PS;  // vector memory ops per wave and stage
+};
+
+__device__ __forceinline__ int dq_swz(int row) { return (row >> 1) & 7; }
+
+struct DqProblem {
+    WPlanes w;
+    int N;
+    float *y;
+    int64_t ldy;  // floats between consecutive m rows of y
+};
+struct DqArgs {
+    DqProblem prob[4];
+    int M, K;
+    const _Float16 *xh;  // [M][K] fp16(d * q) of the quantized activations
+};
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(dq_lds *)p; }
+
+template <int n>
+__device__ __forceinline__ void dq_wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+}
+
+// Activation rows -> Q8_0 blocks (ggml's quantize_row_q8_0, d rounded to fp16 as the dot reads it) -> fp16(d * q).
+__global__ __launch_bounds__(256) void k_dq_act_q8_0(const float *x, int64_t x_stride, int K, int rounding,
+                                                     _Float16 *xh) {
+    const int64_t m = blockIdx.y;
+    const int e = blockIdx.x * 1024 + 4 * threadIdx.x;
+    const bool valid = e < K;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (valid) v = *(const float4 *)(x + m * x_stride + e);
+    float d;
+    int sum;
+    const int q = quant32_lane(v, rounding, &d, &sum);
+    if (valid) {
+        const float dh = h2f(f2h(d));
+        typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+        // d * q is exact in fp32 (11 + 7 bits): one rounding to fp16
+        const v4h h = {(_Float16)(dh * (float)(int8_t)(q & 0xFF)), (_Float16)(dh * (float)(int8_t)((q >> 8) & 0xFF)),
+                       (_Float16)(dh * (float)(int8_t)((q >> 16) & 0xFF)),
+                       (_Float16)(dh * (float)(int8_t)((q >> 24) & 0xFF))};
+        *(v4h *)(xh + m * K + e) = h;
+    }
+}
+
+// Four signed bytes -> four exact fp16 values: (0x64 << 8 | (b ^ 0x80)) is the fp16 of 1152 + b, and 1152 is
+// subtracted exactly.
+__device__ __forceinline__ void dq_i8x4(uint32_t w, v2h &lo, v2h &hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const v2h off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = __builtin_bit_cast(v2h, p0) - off;
+    hi = __builtin_bit_cast(v2h, p1) - off;
+}
+
+// 16 codes of one Q8_0 block times its fp16 d: two 16-byte chunks of fp16(d * q) (one rounding of an exact product).
+__device__ __forceinline__ void dq_q8_0_16(v4i c, uint16_t dbits, v4i &o0, v4i &o1) {
+    _Float16 d;
+    __builtin_memcpy(&d, &dbits, 2);
+    const v2h dd = {d, d};
+    v2h h[8];
+    dq_i8x4((uint32_t)c.x, h[0], h[1]);
+    dq_i8x4((uint32_t)c.y, h[2], h[3]);
+    dq_i8x4((uint32_t)c.z, h[4], h[5]);
+    dq_i8x4((uint32_t)c.w, h[6], h[7]);
+#pragma unroll
+    for (int i = 0; i < 8; i++) h[i] = h[i] * dd;
+    o0 = v4i{__builtin_bit_cast(int, h[0]), __builtin_bit_cast(int, h[1]), __builtin_bit_cast(int, h[2]),
+             __builtin_bit_cast(int, h[3])};
+    o1 = v4i{__builtin_bit_cast(int, h[4]), __builtin_bit_cast(int, h[5]), __builtin_bit_cast(int, h[6]),
+             __builtin_bit_cast(int, h[7])};
+}
+
+// NF fragment reads (4, 6, 8 or 12) and the wait for them.
+template <int NF>
+__device__ __forceinline__ void dq_read(v8h (&f)[12], const uint32_t (&a)[12]) {
+    if constexpr (NF == 8) {
+        asm volatile(
+            "ds_read_b128 %0, %8\n"
+            "ds_read_b128 %1, %9\n"
+            "ds_read_b128 %2, %10\n"
+            "ds_read_b128 %3, %11\n"
+            "ds_read_b128 %4, %12\n"
+            "ds_read_b128 %5, %13\n"
+            "ds_read_b128 %6, %14\n"
+            "ds_read_b128 %7, %15\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]), "=&v"(f[6]), "=&v"(f[7])
+            : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7])
+            : "memory");
+    } else if constexpr (NF == 12) {
+        asm volatile(
+            "ds_read_b128 %0, %12\n"
+            "ds_read_b128 %1, %13\n"
+            "ds_read_b128 %2, %14\n"
+            "ds_read_b128 %3, %15\n"
+            "ds_read_b128 %4, %16\n"
+            "ds_read_b128 %5, %17\n"
+            "ds_read_b128 %6, %18\n"
+            "ds_read_b128 %7, %19\n"
+            "ds_read_b128 %8, %20\n"
+            "ds_read_b128 %9, %21\n"
+            "ds_read_b128 %10, %22\n"
+            "ds_read_b128 %11, %23\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]), "=&v"(f[6]), "=&v"(f[7]),
+              "=&v"(f[8]), "=&v"(f[9]), "=&v"(f[10]), "=&v"(f[11])
+            : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]), "v"(a[8]),
+              "v"(a[9]), "v"(a[10]), "v"(a[11])
+            : "memory");
+    } else if constexpr (NF == 6) {
+        asm volatile(
+            "ds_read_b128 %0, %6\n"
+            "ds_read_b128 %1, %7\n"
+            "ds_read_b128 %2, %8\n"
+            "ds_read_b128 %3, %9\n"
+            "ds_read_b128 %4, %10\n"
+            "ds_read_b128 %5, %11\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5])
+            : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5])
+            : "memory");
+    } else {
+        static_assert(NF == 4, "4, 6, 8 or 12 fragments");
+        asm volatile(
+            "ds_read_b128 %0, %4\n"
+            "ds_read_b128 %1, %5\n"
+            "ds_read_b128 %2, %6\n"
+            "ds_read_b128 %3, %7\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3])
+            : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3])
+            : "memory");
+    }
+}
+
+template <int BM, int BN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
+    constexpr int NW = WGM * WGN, NT = 64 * NW;
+    using L = DqLds<BM, BN, NW>;
+    constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+    constexpr int NF = (TM + TN) * 4;  // fragments of the stage's four K steps, read together
+    static_assert(NF == 8 || NF == 12, "wave tiles of 32 x 32 or 64 x 32");
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int z = blockIdx.z;
+    const DqProblem p = z == 0 ? a.prob[0] : (z == 1 ? a.prob[1] : (z == 2 ? a.prob[2] : a.prob[3]));
+    const int n0 = blockIdx.x * BN;
+    if (n0 >= p.N) return;  // uniform: a problem narrower than the grid
+    const int m0 = blockIdx.y * BM;
+    const int M = a.M, N = p.N, K = a.K, nst = K / DQ_KS, nblk = K / 32;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t lds = lds_addr(smem);
+
+    // Copy sources of this lane (stage 0; a stage adds 64 elements) and LDS destinations (stage 0; a stage adds its
+    // slot). Instruction j of a kind is issued by wave j / P (its jj = j % P); instructions past the tile's need copy
+    // a valid row again into the wave's junk area.
+    //   activations: instruction j covers rows 8 j .. 8 j + 7; lane i brings logical chunk (i & 7) ^ swz(row)
+    //   codes: instruction j covers rows 16 j .. 16 j + 15; lane i brings bytes 16 (i & 3) .. of its row
+    //   scales: instruction j covers rows 64 j .. 64 j + 63; lane i brings the stage's two block scales of its row
+    const _Float16 *asrc[L::PA];
+    uint32_t adst[L::PA];
+#pragma unroll
+    for (int jj = 0; jj < L::PA; jj++) {
+        const int j = wave * L::PA + jj, row = 8 * min(j, L::NA - 1) + (lane >> 3);
+        asrc[jj] = a.xh + (int64_t)min(m0 + row, M - 1) * K + 8 * ((lane & 7) ^ dq_swz(row));
+        adst[jj] = j < L::NA ? L::A + j * 1024 : L::JUNK + wave * 1024;
+    }
+    const uint8_t *csrc[L::PC];
+    uint32_t cdst[L::PC];
+#pragma unroll
+    for (int jj = 0; jj < L::PC; jj++) {
+        const int j = wave * L::PC + jj, row = 16 * min(j, L::NC - 1) + (lane >> 2);
+        csrc[jj] = p.w.p0 + (int64_t)min(n0 + row, N - 1) * K + 16 * (lane & 3);
+        cdst[jj] = j < L::NC ? L::RAW + j * 1024 : L::JUNK + wave * 1024;
+    }
+    const uint8_t *ssrc[L::PS];
+    uint32_t sdst[L::PS];
+#pragma unroll
+    for (int jj = 0; jj < L::PS; jj++) {
+        const int j = wave * L::PS + jj, row = 64 * min(j, L::NS4 - 1) + lane;
+        ssrc[jj] = p.w.p1 + (int64_t)min(n0 + row, N - 1) * nblk * 2;
+        sdst[jj] = j < L::NS4 ? L::SC + j * 256 : L::JUNK + wave * 1024;
+    }
+
+    auto issue = [&](int s) {
+        s = min(s, nst - 1);  // past the end: copy the last stage again into its own slot (identical bytes)
+        const int slot = s % DQ_NS;
+#pragma unroll
+        for (int jj = 0; jj < L::PA; jj++) {
+            const uint32_t d = adst[jj] + (adst[jj] < (uint32_t)L::JUNK ? slot * BM * 128 : 0);
+            __builtin_amdgcn_global_load_lds((const void *)(asrc[jj] + s * DQ_KS), (dq_lds *)(smem + d), 16, 0, 0);
+        }
+#pragma unroll
+        for (int jj = 0; jj < L::PC; jj++) {
+            const uint32_t d = cdst[jj] + (cdst[jj] < (uint32_t)L::JUNK ? slot * BN * 64 : 0);
+            __builtin_amdgcn_global_load_lds((const void *)(csrc[jj] + s * DQ_KS), (dq_lds *)(smem + d), 16, 0, 0);
+        }
+#pragma unroll
+        for (int jj = 0; jj < L::PS; jj++) {
+            const uint32_t d = sdst[jj] + (sdst[jj] < (uint32_t)L::JUNK ? slot * BN * 4 : 0);
+            __builtin_amdgcn_global_load_lds((const void *)(ssrc[jj] + s * 4), (dq_lds *)(smem + d), 4, 0, 0);
+        }
+    };
+
+    // Conversion of stage s's raw weights into fp16 tile buffer s & 1, in units of 16 codes: unit u is quarter u & 3
+    // of row u >> 2 (block (u & 3) >> 1 of the stage's two).
+    auto convert = [&](int s) {
+        const int slot = s % DQ_NS;
+#pragma unroll
+        for (int u = tid; u < BN * 4; u += NT) {
+            const int row = u >> 2, q = u & 3;
+            const uint32_t raw = lds + L::RAW + slot * BN * 64 + row * 64 + 16 * q;
+            const uint32_t sc = lds + L::SC + slot * BN * 4 + row * 4;
+            v4i c0;
+            uint32_t sw;
+            asm volatile(
+                "ds_read_b128 %0, %2\n"
+                "ds_read_b32 %1, %3\n"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(c0), "=&v"(sw)
+                : "v"(raw), "v"(sc)
+                : "memory");
+            v4i o[2];
+            dq_q8_0_16(c0, (uint16_t)((q >> 1) ? sw >> 16 : sw & 0xFFFF), o[0], o[1]);
+            const uint32_t out = lds + L::BH + (s & 1) * BN * 128 + row * 128;
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                asm volatile("ds_write_b128 %0, %1" ::"v"(out + 16 * ((2 * q + i) ^ dq_swz(row))), "v"(o[i])
+                             : "memory");
+        }
+    };
+
+    const int wm = (wave / WGN) * WM, wn = (wave % WGN) * WN;
+    const int fr = lane & 31, fh = lane >> 5;
+    // fragment offsets within a tile: row base plus the swizzled chunk of K step kk (chunk 2 kk + fh)
+    uint32_t aoff[TM][4], boff[TN][4];
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int row = wm + 32 * i + fr;
+            aoff[i][kk] = row * 128 + 16 * ((2 * kk + fh) ^ dq_swz(row));
+        }
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int row = wn + 32 * j + fr;
+            boff[j][kk] = row * 128 + 16 * ((2 * kk + fh) ^ dq_swz(row));
+        }
+    }
+    v16f acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    issue(0);
+    issue(1);
+    issue(2);
+    dq_wait_vm<2 * L::OPS>();  // stage 0 landed (this wave's copies)
+    __syncthreads();
+    convert(0);
+
+#pragma unroll 1
+    for (int s = 0; s < nst; s++) {
+        // this wave's copies of A(s) and of the raw weights of stage s + 1 have landed, and its LDS writes are done
+        dq_wait_vm<L::OPS>();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+        // the stage's fragments, then its MFMAs; the copies three stages ahead and the conversion of the next stage's
+        // weights follow while the matrix cores work through them
+        const uint32_t at = lds + L::A + (s % DQ_NS) * BM * 128;
+        const uint32_t bt = lds + L::BH + (s & 1) * BN * 128;
+        uint32_t ad[12];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+#pragma unroll
+            for (int i = 0; i < TM; i++) ad[kk * (TM + TN) + i] = at + aoff[i][kk];
+#pragma unroll
+            for (int j = 0; j < TN; j++) ad[kk * (TM + TN) + TM + j] = bt + boff[j][kk];
+        }
+#pragma unroll
+        for (int x = NF; x < 12; x++) ad[x] = 0;
+        v8h f[12];
+        dq_read<NF>(f, ad);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[kk * (TM + TN) + i], f[kk * (TM + TN) + TM + j],
+                                                                        acc[i][j], 0, 0, 0);
+        issue(s + DQ_NS - 1);
+        if (s + 1 < nst) convert(s + 1);
+    }
+    dq_wait_vm<0>();  // the copies of the stages past the end
+
+    // 32 x 32 accumulator layout: lane l, register r holds (row 8 (r / 4) + 4 (l / 32) + r % 4, col l % 32)
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn + 32 * j + fr;
+            if (n >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);
+                if (m < M) p.y[(int64_t)m * p.ldy + n] = acc[i][j][r];
+            }
+        }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Host side.
+// ------------------------------------------------------------------------------------------------------------------
+bool gemm_dq_supported(int type, int64_t M, int64_t K) {
+    static const bool off = [] {
+        const char *e = getenv("MX_GEMM_DQ");
+        return e && e[0] == '0';
+    }();
+    return !off && type == MX_TYPE_Q8_0 && K % DQ_KS == 0 && M * K < ((int64_t)1 << 31) && K < (1 << 24);
+}
+
+size_t gemm_dq_act_bytes(int64_t M, int64_t K) { return (size_t)M * (size_t)K * 2; }
+
+hipError_t launch_gemm_dq_act(int type, int rounding, const float *x, int64_t x_stride, int64_t M, int64_t K,
+                              void *xh, hipStream_t s) {
+    if (type != MX_TYPE_Q8_0) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((K + 1023) / 1024), (unsigned)M);
+    hipLaunchKernelGGL(k_dq_act_q8_0, grid, dim3(256), 0, s, x, x_stride, (int)K, rounding, (_Float16 *)xh);
+    return hipGetLastError();
+}
+
+template <int BM, int BN, int WGM, int WGN>
+static hipError_t launch_dq(const DqArgs &a, int nprob, int maxN, hipStream_t s) {
+    using L = DqLds<BM, BN, WGM * WGN>;
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm_dq_q8_0<BM, BN, WGM, WGN>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, L::SIZE);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    const dim3 grid((unsigned)((maxN + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM), (unsigned)nprob);
+    hipLaunchKernelGGL((k_gemm_dq_q8_0<BM, BN, WGM, WGN>), grid, dim3(64 * WGM * WGN), L::SIZE, s, a);
+    return hipGetLastError();
+}
+
+// Tile: the largest of 128 x 128, 128 x 64 and 64 x 64 that still gives a workgroup per CU. MX_GEMM_DQ_TILE=BMxBN
+// overrides.
+hipError_t launch_gemm_dq(int type, int nprob, const WPlanes *w, const int64_t *N, float *const *y,
+                          const int64_t *ldy, int64_t M, int64_t K, const void *xh, hipStream_t s) {
+    if (nprob < 1 || nprob > 4 || !gemm_dq_supported(type, M, K)) return hipErrorInvalidValue;
+    DqArgs a{};
+    int64_t maxN = 0, wg128 = 0;
+    for (int i = 0; i < nprob; i++) {
+        if (N[i] * K >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+        a.prob[i] = DqProblem{w[i], (int)N[i], y[i], ldy[i]};
+        maxN = N[i] > maxN ? N[i] : maxN;
+        wg128 += (N[i] + 127) / 128;
+    }
+    a.M = (int)M;
+    a.K = (int)K;
+    a.xh = (const _Float16 *)xh;
+    wg128 *= (M + 127) / 128;
+    int64_t wg64 = 0;
+    for (int i = 0; i < nprob; i++) wg64 += (N[i] + 63) / 64;
+    int bm = 64, bn = 64;
+    if (wg128 >= 256) bm = bn = 128;
+    else if (wg64 * ((M + 127) / 128) >= 256) bm = 128;
+    static const char *tile = getenv("MX_GEMM_DQ_TILE");
+    if (tile) {
+        int tm = 0, tn = 0;
+        if (sscanf(tile, "%dx%d", &tm, &tn) == 2 && (tm == 64 || tm == 128) && (tn == 64 || tn == 128) &&
+            !(tm == 64 && tn == 128)) {
+            bm = tm;
+            bn = tn;
+        }
+    }
+    if (bm == 128 && bn == 128) return launch_dq<128, 128, 2, 4>(a, nprob, (int)maxN, s);
+    if (bm == 128) return launch_dq<128, 64, 4, 2>(a, nprob, (int)maxN, s);
+    return launch_dq<64, 64, 2, 2>(a, nprob, (int)maxN, s);
+}
+
+}  // namespace mx

@@ -544,6 +544,35 @@ static int gemm_q4k_group(mx_backend *be, int n, const mx_tensor *const *src0, c
     return MX_SUCCESS;
 }
 
+// M > 8 on Q8_0 weights through the dequantizing fp16 GEMM: per batch slice, activations quantized once (as fp16 of
+// their Q8_0 values), then one launch for the whole group.
+static int gemm_dq_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
+                         const mx_tensor *const *dst) {
+    const mx_tensor *w0 = src0[0];
+    const int64_t K = w0->ne[0], M = src1->ne[1];
+    int rc = ensure_scratch(be, mx::gemm_dq_act_bytes(M, K));
+    if (rc) return rc;
+    const int64_t r2 = src1->ne[2] / w0->ne[2], r3 = src1->ne[3] / w0->ne[3];
+    for (int64_t i13 = 0; i13 < src1->ne[3]; i13++)
+        for (int64_t i12 = 0; i12 < src1->ne[2]; i12++) {
+            const float *x = (const float *)((const uint8_t *)src1->data + i12 * src1->nb[2] + i13 * src1->nb[3]);
+            HIP_OK(mx::launch_gemm_dq_act(w0->type, be->rounding, x, (int64_t)(src1->nb[1] / 4), M, K, be->scratch,
+                                          be->stream),
+                   "GEMM activation quantization");
+            mx::WPlanes w[4];
+            int64_t N[4], ldy[4];
+            float *y[4];
+            for (int i = 0; i < n; i++) {
+                w[i] = matrix_planes(src0[i], i12 / r2 + (i13 / r3) * src0[i]->ne[2]);
+                N[i] = src0[i]->ne[1];
+                y[i] = (float *)((uint8_t *)dst[i]->data + i12 * dst[i]->nb[2] + i13 * dst[i]->nb[3]);
+                ldy[i] = (int64_t)(dst[i]->nb[1] / 4);
+            }
+            HIP_OK(mx::launch_gemm_dq(w0->type, n, w, N, y, ldy, M, K, be->scratch, be->stream), "GEMM launch");
+        }
+    return MX_SUCCESS;
+}
+
 // Products sharing src1: n problems (n <= 4) of the same type and K, each with its own rows and dst.
 static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
                         const mx_tensor *const *dst) {
@@ -564,6 +593,11 @@ static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, con
     a.y_b3 = (int64_t)(dst[0]->nb[3] / 4);
     a.nprob = n;
     const int64_t M = src1->ne[1];
+    if (M > mx::MAX_COLS && mx::gemm_dq_supported(a.type, M, a.K)) {
+        bool fits = true;  // every weight's rows within 32-bit element offsets
+        for (int i = 0; i < n; i++) fits = fits && src0[i]->ne[1] * a.K < ((int64_t)1 << 31);
+        if (fits) return gemm_dq_group(be, n, src0, src1, dst);
+    }
     if (M > mx::MAX_COLS && mx::gemm_supported(a.type, a.K)) return gemm_group(be, n, src0, src1, dst);
     if (M > mx::MAX_COLS && a.type == MX_TYPE_Q4_K && a.K % 256 == 0 && !gemm_q4k_disabled())
         return gemm_q4k_group(be, n, src0, src1, dst);

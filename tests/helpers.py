@@ -22,3 +22,14 @@ def l2_rel(y: np.ndarray, y_ref: np.ndarray) -> float:
 def bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
     return a.shape == b.shape and np.array_equal(np.ascontiguousarray(a).view(np.uint8),
                                                  np.ascontiguousarray(b).view(np.uint8))
+
+
+def dq_model(oracle, wtype: int, w: np.ndarray, x: np.ndarray, K: int, rounding: int = 0) -> np.ndarray:
+    """What the dequantizing fp16 GEMM computes, exactly up to its fp32 summation order: every weight and every
+    quantized activation (the oracle's own quantization of x for the weight's dot) rounded once to fp16, products
+    summed in float64. Kernel against this model: ~1e-6; this model against the oracle: a few 1e-4."""
+    act_type = oracle.TYPE_Q8_0 if wtype == oracle.TYPE_Q8_0 else oracle.TYPE_Q8_K
+    wd = oracle.dequantize_rows(wtype, w, K).astype(np.float16).astype(np.float64)
+    xq = oracle.quantize_rows(act_type, np.ascontiguousarray(x, dtype=np.float32), rounding)
+    xd = oracle.dequantize_rows(act_type, xq, K).astype(np.float16).astype(np.float64)
+    return xd @ wd.T
