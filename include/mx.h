@@ -51,11 +51,13 @@ enum {
     MX_TYPE_I32 = 26,
 };
 
-/* The ops this device computes (the ggml adapter maps GGML_OP_GET_ROWS / GGML_OP_MUL_MAT / GGML_OP_MUL_MAT_ID). */
+/* The ops this device computes (the ggml adapter maps GGML_OP_GET_ROWS / GGML_OP_MUL_MAT / GGML_OP_MUL_MAT_ID /
+ * GGML_OP_ARGMAX). */
 enum {
     MX_OP_GET_ROWS = 1,
     MX_OP_MUL_MAT = 2,
     MX_OP_MUL_MAT_ID = 3,
+    MX_OP_ARGMAX = 4,
 };
 
 /* Rounding of the activation quantizers.
@@ -142,6 +144,12 @@ MX_API int mx_get_rows(mx_backend *be, const mx_tensor *src0, const mx_tensor *i
 MX_API int mx_mul_mat(mx_backend *be, const mx_tensor *src0, const mx_tensor *src1, const mx_tensor *dst);
 MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids,
                          const mx_tensor *dst);
+/* ARGMAX: dst[r] = the index of the largest value of row r of src, the first of equal ones, as speech.cpp's ggml
+ * fork computes GGML_OP_ARGMAX (src/families/fastconformer/decoder.cpp:56-62 first_argmax states the rule; the
+ * decoder's greedy pick, src/common/qwen3-decoder.cpp:426-429,501, reads back these four bytes per row instead of the
+ * logits). A NaN never compares greater: at index 0 it keeps index 0, elsewhere it is passed over.
+ *   mx_argmax(src [n, R] F32, rows 16-byte aligned) -> dst [R] I32 */
+MX_API int mx_argmax(mx_backend *be, const mx_tensor *src, const mx_tensor *dst);
 /* Several MUL_MAT nodes that read the same src1 (q/k/v, or gate/up) in one launch, as a backend's graph_compute
  * may fuse them. Each dst[i] = src0[i] x src1, exactly as n separate mx_mul_mat calls compute it. */
 MX_API int mx_mul_mat_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,

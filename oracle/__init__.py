@@ -66,6 +66,7 @@ def lib():
         L.orc_mul_mat.argtypes, L.orc_mul_mat.restype = [P, P, P, i32, i32], i32
         L.orc_mul_mat_id.argtypes, L.orc_mul_mat_id.restype = [P, P, P, P, i32, i32], i32
         L.orc_get_rows.argtypes, L.orc_get_rows.restype = [P, P, P], i32
+        L.orc_argmax.argtypes, L.orc_argmax.restype = [P, P], i32
         L.orc_fill_normal_rows.argtypes = [u64, i64, i64, i64, f32, f32, vp]
         L.orc_fill_normal_rows.restype = None
         _lib = L
@@ -215,6 +216,17 @@ def get_rows(wtype: int, table: np.ndarray, K: int, ids: np.ndarray) -> np.ndarr
     rc = lib().orc_get_rows(ctypes.byref(s0), ctypes.byref(si), ctypes.byref(d))
     if rc != 0:
         raise ValueError(f"orc_get_rows rc={rc}")
+    return out
+
+
+def argmax(x: np.ndarray) -> np.ndarray:
+    """ggml_argmax with the first of equal values: x float32 [R, n] -> int32 [R]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(x.shape[0], dtype=np.int32)
+    s0, d = _tensor(TYPE_F32, x, (x.shape[1], x.shape[0])), _tensor(TYPE_I32, out, (x.shape[0],))
+    rc = lib().orc_argmax(ctypes.byref(s0), ctypes.byref(d))
+    if rc != 0:
+        raise ValueError(f"orc_argmax rc={rc}")
     return out
 
 

@@ -779,6 +779,19 @@ int orc_get_rows(const orc_tensor *src0, const orc_tensor *ids, orc_tensor *dst)
     return 0;
 }
 
+/* ggml_argmax with the first of equal values (speech.cpp fastconformer/decoder.cpp:56-62; the fork's argmax). */
+int orc_argmax(const orc_tensor *src0, orc_tensor *dst) {
+    if (src0->type != ORC_TYPE_F32 || dst->type != ORC_TYPE_I32 || dst->ne[0] != src0->ne[1]) return -1;
+    for (int64_t r = 0; r < src0->ne[1]; r++) {
+        const float *v = (const float *)((const char *)src0->data + r * src0->nb[1]);
+        int64_t best = 0;
+        for (int64_t i = 1; i < src0->ne[0]; i++)
+            if (v[i] > v[best]) best = i;
+        *(int32_t *)((char *)dst->data + r * dst->nb[0]) = (int32_t)best;
+    }
+    return 0;
+}
+
 /* ------------------------------------------------------------------------------------------------------------------
  * Seeded synthetic data.
  * ---------------------------------------------------------------------------------------------------------------- */

@@ -83,6 +83,12 @@ int orc_mul_mat_id(const orc_tensor *as, const orc_tensor *b, const orc_tensor *
 /* ggml_compute_forward_get_rows: dst[:, i10, i11, i12] = dequant(src0[:, ids[i10,i11,i12], i11, i12]). */
 int orc_get_rows(const orc_tensor *src0, const orc_tensor *ids, orc_tensor *dst);
 
+/* ggml_argmax as speech.cpp's ggml fork computes it: dst[i1] = the index of the largest of row i1's ne0 values, the
+ * first of equal ones (fastconformer/decoder.cpp:56-62 first_argmax, the rule of the fork's argmax). A NaN never
+ * compares greater, so a NaN at index 0 keeps index 0 and NaNs elsewhere are passed over. src0 F32 [ne0, ne1],
+ * dst I32 [ne1]. */
+int orc_argmax(const orc_tensor *src0, orc_tensor *dst);
+
 /* Seeded synthetic data: splitmix64 -> xoshiro256** -> Box-Muller in double -> float. Row r of a tensor draws from
  * its own stream seeded by (seed, r), so rows can be generated in any order or in parallel. */
 void orc_fill_normal_rows(uint64_t seed, int64_t row0, int64_t nrows, int64_t n_per_row, float mean, float stddev,

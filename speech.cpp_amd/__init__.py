@@ -22,7 +22,7 @@ LIB_PATH = HERE / "libmx.so"
 F32, F16, Q8_0, Q8_1, Q4_K, Q6_K, Q8_K, I32 = 0, 1, 8, 9, 12, 14, 15, 26
 BLCK = {F32: 1, F16: 1, I32: 1, Q8_0: 32, Q8_1: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
 TSIZE = {F32: 4, F16: 2, I32: 4, Q8_0: 34, Q8_1: 36, Q4_K: 144, Q6_K: 210, Q8_K: 292}
-OP_GET_ROWS, OP_MUL_MAT, OP_MUL_MAT_ID = 1, 2, 3
+OP_GET_ROWS, OP_MUL_MAT, OP_MUL_MAT_ID, OP_ARGMAX = 1, 2, 3, 4
 ROUND_REF, ROUND_X86 = 0, 1
 SUCCESS, FAILED, ALLOC_FAILED, INVALID, UNSUPPORTED = 0, -1, -2, -3, -4
 
@@ -31,7 +31,7 @@ EXPORTS = [
     "mx_backend_stream", "mx_backend_synchronize", "mx_backend_set_rounding", "mx_last_error", "mx_buft_alignment",
     "mx_buft_max_size", "mx_tensor_alloc_size", "mx_buffer_alloc", "mx_buffer_free", "mx_buffer_clear",
     "mx_tensor_set", "mx_tensor_get", "mx_tensor_memset", "mx_tensor_copy", "mx_supports_op", "mx_get_rows",
-    "mx_mul_mat", "mx_mul_mat_id", "mx_mul_mat_group", "mx_quantize_act", "mx_graph_begin", "mx_graph_end",
+    "mx_mul_mat", "mx_mul_mat_id", "mx_mul_mat_group", "mx_argmax", "mx_quantize_act", "mx_graph_begin", "mx_graph_end",
     "mx_graph_launch", "mx_graph_free", "mx_event_new", "mx_event_record", "mx_event_synchronize",
     "mx_event_elapsed_ms", "mx_event_free", "mx_quantize_chunk", "mx_fill_normal_rows", "mx_quantize_normal_rows",
 ]
@@ -96,6 +96,7 @@ def lib():
         "mx_tensor_copy": ([vp, P, P], i32),
         "mx_supports_op": ([i32, P, P, P, P], i32),
         "mx_get_rows": ([vp, P, P, P], i32),
+        "mx_argmax": ([vp, P, P], i32),
         "mx_mul_mat": ([vp, P, P, P], i32),
         "mx_mul_mat_id": ([vp, P, P, P, P], i32),
         "mx_mul_mat_group": ([vp, i32, ctypes.POINTER(P), P, ctypes.POINTER(P)], i32),
@@ -267,6 +268,9 @@ class Backend:
 
     def mul_mat_id(self, as_: Tensor, b: Tensor, ids: Tensor, dst: Tensor) -> None:
         check(lib().mx_mul_mat_id(self.h, as_.ref(), b.ref(), ids.ref(), dst.ref()))
+
+    def argmax(self, src: Tensor, dst: Tensor) -> None:
+        check(lib().mx_argmax(self.h, src.ref(), dst.ref()))
 
     def quantize_act(self, t: int, rounding: int, x: Tensor, k: int, nrows: int) -> Tensor:
         out = Tensor(self, F32, (row_size(t, k) * nrows // 4 + 1,))

@@ -372,6 +372,14 @@ MX_API int mx_tensor_copy(mx_backend *be, const mx_tensor *src, const mx_tensor 
 // ---------------------------------------------------------------------------------------------------------- ops
 MX_API int mx_supports_op(int op, const mx_tensor *src0, const mx_tensor *src1, const mx_tensor *src2,
                           const mx_tensor *dst) {
+    if (op == MX_OP_ARGMAX) {  // f32 rows in, one I32 per row out
+        if (!src0 || src0->type != MX_TYPE_F32 || !shape_ok(src0) || src0->nb[0] != 4 || src0->nb[1] % 16 != 0 ||
+            !src0->data || !aligned16(src0->data) || src0->ne[2] != 1 || src0->ne[3] != 1)
+            return 0;
+        if (src0->ne[0] < 1 || src0->ne[0] >= ((int64_t)1 << 31) || src0->ne[1] > 0x7FFFFFFF) return 0;
+        return dst && dst->type == MX_TYPE_I32 && shape_ok(dst) && dst->nb[0] == 4 && dst->ne[0] == src0->ne[1] &&
+               dst->ne[1] == 1 && dst->ne[2] == 1 && dst->ne[3] == 1 && dst->data && ((uintptr_t)dst->data & 3) == 0;
+    }
     if (!weight_ok(src0) || !dst || dst->type != MX_TYPE_F32 || !shape_ok(dst) || dst->nb[0] != 4) return 0;
     const int64_t K = src0->ne[0];
     switch (op) {
@@ -679,6 +687,17 @@ MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b
     mx::mul_mat_id_scratch(&a, be->scratch);
     a.err = be->err;
     HIP_OK(mx::launch_mul_mat_id(a, be->stream), "MUL_MAT_ID launch");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_argmax(mx_backend *be, const mx_tensor *src, const mx_tensor *dst) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!mx_supports_op(MX_OP_ARGMAX, src, nullptr, nullptr, dst))
+        return fail(MX_UNSUPPORTED, "ARGMAX: unsupported types, shapes or strides");
+    HIP_OK(mx::launch_argmax((const float *)src->data, src->ne[0], src->ne[1], (int64_t)src->nb[1],
+                             (int32_t *)dst->data, (int64_t)dst->nb[0], be->stream),
+           "ARGMAX launch");
     return MX_SUCCESS;
 }
 

@@ -232,6 +232,10 @@ struct MulMatIdArgs {
     int64_t max_tiles;
     int *err;
 };
+// ARGMAX (first of equal values) over nrows rows of ne0 floats (row stride nb1 bytes) into dst (stride dst_nb0 bytes).
+hipError_t launch_argmax(const float *src, int64_t ne0, int64_t nrows, int64_t nb1, int32_t *dst, int64_t dst_nb0,
+                         hipStream_t s);
+
 // Pairs per chunk: 16-row MFMA groups that share each expanded weight fragment.
 constexpr int MMID_CHUNK = 16;
 // Scratch bytes MUL_MAT_ID needs and the carving of `base` into the fields above.

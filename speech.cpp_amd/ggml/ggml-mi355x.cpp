@@ -244,6 +244,11 @@ int run_nodes(BackendCtx *ctx, ggml_cgraph *cgraph) {
                 rc = mx_get_rows(ctx->be, &s0, &ids, &d);
                 break;
             }
+            case GGML_OP_ARGMAX: {
+                const mx_tensor s0 = desc(node->src[0]), d = desc(node);
+                rc = mx_argmax(ctx->be, &s0, &d);
+                break;
+            }
             default:
                 GGML_LOG_ERROR("%s: op %s is not computed by the MI355X backend\n", __func__, ggml_op_desc(node));
                 return MX_UNSUPPORTED;
@@ -370,8 +375,18 @@ bool in_our_buffer(const ggml_tensor *t, ggml_backend_dev_t dev) {
 }
 
 // True exactly for MUL_MAT / MUL_MAT_ID / GET_ROWS whose quantized weight (Q8_0, Q4_K, Q6_K) lives in this device's
-// buffer type, with the shapes and strides libmx computes; everything else stays on the CPU backend.
+// buffer type, and for ARGMAX over f32 logits in it (the greedy pick after the head, qwen3-decoder.cpp:428,501), with
+// the shapes and strides libmx computes; everything else stays on the CPU backend.
 bool dev_supports_op(ggml_backend_dev_t dev, const ggml_tensor *op) {
+    if (op->op == GGML_OP_ARGMAX) {
+        const ggml_tensor *x = op->src[0];
+        if (!in_our_buffer(x, dev)) return false;
+        mx_tensor s0 = desc(x), d = desc(op);
+        alignas(256) static const char placeholder[256] = {};
+        if (!s0.data) s0.data = (void *)placeholder;
+        if (!d.data) d.data = (void *)placeholder;
+        return mx_supports_op(MX_OP_ARGMAX, &s0, nullptr, nullptr, &d) != 0;
+    }
     if (op->op != GGML_OP_MUL_MAT && op->op != GGML_OP_MUL_MAT_ID && op->op != GGML_OP_GET_ROWS) return false;
     const ggml_tensor *w = op->src[0];
     if (!in_our_buffer(w, dev) || (w->view_src && w->view_offs != 0)) return false;

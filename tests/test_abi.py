@@ -89,3 +89,29 @@ def test_host_q8_0_exact_blocks(mx):
     import json
     for c in json.loads((ROOT / "tests" / "golden" / "q8_0_exact.json").read_text()):
         assert mx.quantize_chunk(mx.Q8_0, np.array(c["x"], np.float32)[None])[0].tobytes().hex() == c["block"]
+
+
+def test_supports_op_argmax(mx):
+    """ARGMAX: F32 rows (16-byte aligned starts) in, one I32 per row out; anything else is declined (host logic)."""
+    def desc(t, ne, nb, data=0x10000):
+        d = mx.MxTensor()
+        d.type = t
+        for i in range(4):
+            d.ne[i], d.nb[i] = ne[i], nb[i]
+        d.data = data
+        return d
+
+    L = mx.lib()
+    src = desc(mx.F32, (151936, 2, 1, 1), (4, 4 * 151936, 8 * 151936, 8 * 151936))
+    dst = desc(mx.I32, (2, 1, 1, 1), (4, 8, 8, 8))
+    assert L.mx_supports_op(mx.OP_ARGMAX, src, None, None, dst) == 1
+    odd = desc(mx.F32, (1001, 2, 1, 1), (4, 4004, 8008, 8008))            # rows not 16-byte aligned
+    assert L.mx_supports_op(mx.OP_ARGMAX, odd, None, None, dst) == 0
+    padded = desc(mx.F32, (1001, 2, 1, 1), (4, 4032, 8064, 8064))
+    assert L.mx_supports_op(mx.OP_ARGMAX, padded, None, None, dst) == 1
+    wrong_dst = desc(mx.F32, (2, 1, 1, 1), (4, 8, 8, 8))
+    assert L.mx_supports_op(mx.OP_ARGMAX, src, None, None, wrong_dst) == 0
+    short_dst = desc(mx.I32, (1, 1, 1, 1), (4, 4, 4, 4))
+    assert L.mx_supports_op(mx.OP_ARGMAX, src, None, None, short_dst) == 0
+    q = desc(mx.Q8_0, (1024, 2, 1, 1), (34, 1088, 2176, 2176))
+    assert L.mx_supports_op(mx.OP_ARGMAX, q, None, None, dst) == 0

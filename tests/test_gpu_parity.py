@@ -410,3 +410,52 @@ def test_mul_mat_gemm_kquant_group(mx, be, t):
     be.sync()
     for n, wi, Yi in zip(Ns, w, Y):
         assert rel_err(Yi.numpy().reshape(M, n), O.mul_mat(t, wi, x)) <= TIGHT
+
+
+# ------------------------------------------------------------------------------------------------------------ ARGMAX
+def argmax_rows(n, R, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((R, n)).astype(np.float32)
+    if R > 1:
+        x[1, [5, n // 3, n - 1]] = 50.0                  # ties spread over threads and waves: the first
+    if R > 2:
+        x[2, :] = 0.25                                   # all equal
+    if R > 3:
+        x[3, 0] = np.nan                                 # NaN at index 0 wins by default
+        x[3, 7] = 99.0
+    if R > 4:
+        x[4, [1, 100, n - 2]] = np.nan                   # NaNs elsewhere are passed over
+        x[4, n // 2] = 77.0
+    if R > 5:
+        x[5, :] = -np.inf
+    if R > 6:
+        x[6, n - 1] = np.inf
+    if R > 7:
+        x[7, 4 * 37 + 2] = 30.0                          # one max inside a 16-byte group, and its tie in the next
+        x[7, 4 * 38 + 1] = 30.0
+    return x
+
+
+@pytest.mark.parametrize("n,R", [(151936, 8), (3072, 11), (64, 3), (4, 1), (1000, 9)])
+def test_argmax_matches_oracle(mx, be, n, R):
+    x = argmax_rows(n, R, 0xA46 + n + R)
+    X = be.tensor(mx.F32, (n, R), x)
+    Y = be.tensor(mx.I32, (R,))
+    be.argmax(X, Y)
+    be.sync()
+    assert np.array_equal(Y.numpy().reshape(R), O.argmax(x))
+
+
+def test_argmax_padded_rows(mx, be):
+    """Rows whose length is not a multiple of four (the kernel's tail) inside 16-byte-aligned padded rows."""
+    n, R, pitch = 1001, 6, 1008
+    x = argmax_rows(n, R, 0xA47)
+    xp = np.zeros((R, pitch), np.float32)
+    xp[:, :n] = x
+    xp[:, n:] = 1e30                                     # padding must never be read as a value
+    X = mx.Tensor(be, mx.F32, (n, R), nb=(4, 4 * pitch, 4 * pitch * R, 4 * pitch * R))
+    X.set(xp.reshape(-1)[: (R - 1) * pitch + n])
+    Y = be.tensor(mx.I32, (R,))
+    be.argmax(X, Y)
+    be.sync()
+    assert np.array_equal(Y.numpy().reshape(R), O.argmax(x))

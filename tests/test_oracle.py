@@ -317,3 +317,32 @@ def test_cpu_fast_port_agrees_with_oracle():
         y = O.cpu_fast_mul_mat(t, w, x, 4)
         ref = O.mul_mat(t, w, x, rounding=O.ROUND_X86)
         assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+# ------------------------------------------------------------------------------------------------------------ argmax
+def test_argmax_first_of_ties_against_numpy():
+    """numpy's argmax also returns the first of equal maxima: on NaN-free rows the two must agree everywhere."""
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((64, 1003)).astype(np.float32)
+    x[1:8, [3, 500, 1002]] = 9.0             # the max three times: the first wins
+    x[8, :] = 1.5                            # all equal: index 0
+    x[9, :] = -np.inf                        # all -inf: index 0
+    x[10, 1002] = np.inf
+    x[11, [0, 1]] = [0.0, 7.0]
+    x[11, 2] = 7.0
+    x[12] = np.round(x[12])                  # many ties among small integers
+    assert np.array_equal(O.argmax(x), np.argmax(x, axis=1).astype(np.int32))
+
+
+def test_argmax_known_answers():
+    """NaN never compares greater (first_argmax's `v[i] > v[best]`): the cases numpy would answer differently."""
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    rows = [([nan, 1.0, 2.0, 3.0], 0),       # NaN at index 0: nothing is greater than it
+            ([1.0, nan, 3.0, 3.0], 2),       # NaN elsewhere is passed over; the first of the two 3s
+            ([nan, nan, nan, nan], 0),
+            ([-inf, -inf, -inf, nan], 0),
+            ([0.0, -0.0, 0.0, -1.0], 0),     # 0 and -0 are equal: the first
+            ([-0.0, 0.0, 5.0, inf], 3),
+            ([2.0, 1.0, nan, 2.0], 0)]
+    x = np.array([r for r, _ in rows], np.float32)
+    assert O.argmax(x).tolist() == [a for _, a in rows]
