@@ -35,6 +35,7 @@ ROOT = pathlib.Path(__file__).resolve().parent
 METRIC = "quant mat-vec weight GB/s (% HBM peak); decode tok/s at Qwen3-0.6B shape"
 HBM_PEAK_GBPS = 8000.0
 INT8_PEAK_TOPS = 5000.0   # dense int8 MFMA, MI355X
+FP16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, MI355X
 
 Q8_0, Q4_K, Q6_K = 8, 12, 14
 BLCK = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
@@ -198,13 +199,15 @@ def step_hbm_roofline(kernel, launches, ms_step, ms_other=0.0):
             "us_per_launch": round(ms * 1e3, 3)}
 
 
-def mfma_roofline(kernel, table, labels):
+def mfma_roofline(kernel, table, labels, peak=INT8_PEAK_TOPS, unit="TOP/s"):
+    """Algorithmic multiply-adds x 2 per launch over the labels' mean launch time, against the dense MFMA peak of the
+    arithmetic the kernel issues (int8 for the Q8_K/Q8_1 GEMMs, fp16 for the dequantizing Q8_0 GEMM)."""
     n = sum(table[l][0] for l in labels)
     ops = sum(table[l][2] for l in labels)
     ms = sum(table[l][3] * table[l][0] for l in labels)
     achieved = ops / (ms * 1e-3) / 1e12
-    return {"bound": "mfma", "kernel": kernel, "achieved": round(achieved, 1), "peak": INT8_PEAK_TOPS,
-            "unit": "TOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4), "launches_per_step": n,
+    return {"bound": "mfma", "kernel": kernel, "achieved": round(achieved, 1), "peak": peak,
+            "unit": unit, "frac": round(achieved / peak, 4), "launches_per_step": n,
             "ops_per_launch": int(ops / n), "us_per_launch": round(ms / n * 1e3, 3)}
 
 
@@ -326,7 +329,22 @@ def layer_launches(be, dec, acts, l, x_in, label_of):
 # ---------------------------------------------------------------------------------------------- decode (default)
 QWEN3_06B = dict(layers=28, hidden=1024, ffn=3072, nq=16, nkv=8, head_dim=128, vocab=151936)
 COPY_BYTES = 256 << 20  # the plain copy the counters are calibrated on
-TRAFFIC_FILE = ROOT / "profiles" / "k_matvec_q8_0_qwen3-0.6b_decode.traffic.txt"
+# HBM traffic per launch of each workload's dominant kernel, from two rocprofv3 --pmc passes over the workload
+# (FETCH_SIZE, then WRITE_SIZE), summarized by --summarize-pmc: workload -> (summary file, kernel name substring)
+TRAFFIC = {"decode": ("k_matvec_q8_0_qwen3-0.6b_decode.traffic.txt", "k_matvec"),
+           "matvec": ("k_matvec_q8_0_3072x1024_rotated.traffic.txt", "k_matvec"),
+           "prefill-q4k": ("k_gemm_q4k_qwen3-1.7b_prefill.traffic.txt", "k_gemm_q4k<"),
+           "asr-1.7b": ("k_gemm_dq_q8_0_qwen3-asr-1.7b_prefill.traffic.txt", "k_gemm_dq_q8_0"),
+           "moe": ("k_mmid_q4k_drama3_moe.traffic.txt", "k_mmid_q4k")}
+
+
+def calibration_copy(mx, be):
+    """A plain device copy of known size: the reference the HBM traffic counters are calibrated on."""
+    cp_src, cp_dst = be.tensor(mx.F32, (COPY_BYTES // 4,)), be.tensor(mx.F32, (COPY_BYTES // 4,))
+    mx.check(mx.lib().mx_tensor_copy(be.h, cp_src.ref(), cp_dst.ref()))
+    be.sync()
+    cp_src.free()
+    cp_dst.free()
 
 
 def decode_token_launches(be, mx, dec, acts, ids, x0, logits):
@@ -352,20 +370,13 @@ def run_decode(args, mx, be, threads):
     launches = decode_token_launches(be, mx, dec, acts, ids, x0, logits)
     weight_bytes = sum(L.weight_bytes for L in launches)
 
-    # A plain device copy of known size: the reference the HBM traffic counters are calibrated on.
-    cp_src, cp_dst = be.tensor(mx.F32, (COPY_BYTES // 4,)), be.tensor(mx.F32, (COPY_BYTES // 4,))
-    mx.check(mx.lib().mx_tensor_copy(be.h, cp_src.ref(), cp_dst.ref()))
-    be.sync()
-    cp_src.free()
-    cp_dst.free()
-
     ms_per_step = time_graph(be, launches, args.steps, args.warmup, not args.no_graph)
     # Roofline of the dominant kernel: k_matvec over Q8_0 at batch 1 (every launch of the step but the one GET_ROWS;
     # the template is instantiated per lanes-per-row, all the same code), timed inside the step.
     table = label_table(launches, per_label_pass(be, launches, reps=20))
     roof = step_hbm_roofline("k_matvec<Q8_0, NC=1>", [L for L in launches if L.label != "get_rows"], ms_per_step,
                              ms_other=table["get_rows"][3])
-    roof["traffic"] = read_traffic()
+    roof["traffic"] = read_traffic("decode")
     tok_s = 1e3 / ms_per_step
     step_gbps = weight_bytes / (ms_per_step * 1e-3) / 1e9
     result = base_result(args, round(tok_s, 2), "tok/s", ms_per_step, "int8", {
@@ -398,9 +409,10 @@ def cpu_decode(dec, seconds):
                       f"across {threads} threads"}
 
 
-def summarize_pmc(fetch_csv: str, write_csv: str) -> str:
-    """Per-dispatch HBM traffic of the step's mat-vecs from two rocprofv3 --pmc runs (FETCH_SIZE, then WRITE_SIZE,
-    KiB per dispatch), each scaled by what the counter reads for the run's plain 256 MiB device copy."""
+def summarize_pmc(fetch_csv: str, write_csv: str, kernel: str) -> str:
+    """Per-dispatch HBM traffic of the kernels whose name holds `kernel`, from two rocprofv3 --pmc runs (FETCH_SIZE,
+    then WRITE_SIZE, KiB per dispatch), each scaled by what the counter reads for the run's plain 256 MiB device
+    copy."""
     import csv
     import statistics
 
@@ -417,12 +429,12 @@ def summarize_pmc(fetch_csv: str, write_csv: str) -> str:
     copy = [k for k in f if "copyBuffer" in k]
     f_cal = max(max(f[k]) for k in copy) * 1024 / COPY_BYTES   # counter bytes per byte actually read
     w_cal = max(max(w[k]) for k in copy if k in w) * 1024 / COPY_BYTES
-    mv = [k for k in f if "k_matvec" in k]
+    mv = [k for k in f if kernel in k]
     fetch = [v for k in mv for v in f[k]]
     write = [v for k in mv for v in w.get(k, [])]
     fb = statistics.mean(fetch) * 1024 / f_cal
     wb = statistics.mean(write) * 1024 / w_cal if write else 0.0
-    lines = [f"kernel family: k_matvec<Q8_0,1,*> ({len(fetch)} dispatches)",
+    lines = [f"kernels matching '{kernel}': {len(fetch)} dispatches",
              f"copy calibration: FETCH_SIZE reads {f_cal:.4f} x and WRITE_SIZE {w_cal:.4f} x the bytes of a "
              f"{COPY_BYTES >> 20} MiB device copy",
              f"fetch_bytes_per_launch: {fb:.0f}", f"write_bytes_per_launch: {wb:.0f}",
@@ -430,10 +442,11 @@ def summarize_pmc(fetch_csv: str, write_csv: str) -> str:
     return "\n".join(lines)
 
 
-def read_traffic():
-    if not TRAFFIC_FILE.exists():
+def read_traffic(workload):
+    path = ROOT / "profiles" / TRAFFIC[workload][0]
+    if not path.exists():
         return None
-    for line in TRAFFIC_FILE.read_text().splitlines():
+    for line in path.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
             return int(float(line.split(":")[1]))
     return None
@@ -454,7 +467,7 @@ def run_matvec(args, mx, be, threads):
     launches = [Launch("matvec", nbytes, 0, lambda Wi=Wi: be.mul_mat(Wi, X, Y)) for Wi in W]
     ms_per_step = time_graph(be, launches, args.steps, args.warmup, not args.no_graph)
     roof = step_hbm_roofline("k_matvec<Q8_0, NC=1>", launches, ms_per_step)
-    roof["traffic"] = None
+    roof["traffic"] = read_traffic("matvec")
     gbps = nbytes * MATVEC_COPIES / (ms_per_step * 1e-3) / 1e9
     result = base_result(args, round(gbps, 1), "GB/s", ms_per_step, "int8", {
         "workload": "single Q8_0 MUL_MAT 3072x1024 at batch 1, rotated over 160 weight copies",
@@ -529,9 +542,9 @@ def run_prefill_q4k(args, mx, be, threads):
     ops = sum(L.ops for L in launches)
     ms_per_step = time_graph(be, launches, args.steps, args.warmup, not args.no_graph)
     table = label_table(launches, per_label_pass(be, launches, reps=5))
-    roof = mfma_roofline("k_gemm_kq<Q4_K> (with its Q8_K activation pass)", table,
+    roof = mfma_roofline("k_gemm_q4k (with its Q8_K activation pass)", table,
                          [l for l in table if l.endswith(":Q4_K")])
-    roof["traffic"] = None
+    roof["traffic"] = read_traffic("prefill-q4k")
     tops = ops / (ms_per_step * 1e-3) / 1e12
     result = base_result(args, round(tops, 2), "TOP/s", ms_per_step, "int8", {
         "workload": "qwen3-1.7b-shape talker prefill, M = 512", **S, "M": M, "weights": "Q4_K, Q6_K down",
@@ -554,16 +567,17 @@ def run_asr(args, mx, be, threads):
     types = {n: Q8_0 for n, _, _ in decoder_shapes(S["hidden"], S["ffn"], S["nq"], S["nkv"], S["head_dim"])}
     dec = Decoder(mx, be, 4, S["layers"], S["hidden"], S["ffn"], S["nq"], S["nkv"], S["head_dim"], S["vocab"], types,
                   threads, keep_host=args.cpu_seconds > 0)
-    acts = {M: DecodeActs(mx, be, dec, M, 0xAC700004 + M * 256, per_layer=False) for M in sorted(set(ASR_BLOCKS))}
+    blocks = tuple(args.blocks or ASR_BLOCKS)
+    acts = {M: DecodeActs(mx, be, dec, M, 0xAC700004 + M * 256, per_layer=False) for M in sorted(set(blocks))}
     dacts = DecodeActs(mx, be, dec, 1, 0xAC700004, per_layer=True)
     logits = be.tensor(mx.F32, (S["vocab"], 1))
     ids = be.tensor(mx.I32, (1,), np.array([4242], np.int32))
     x0 = be.tensor(mx.F32, (S["hidden"], 1))
     pre = []
-    for M in ASR_BLOCKS:
+    for M in blocks:
         pre += prefill_launches(be, dec, acts[M], lambda lab, t, M=M: f"prefill_M{M}")
-    last = acts[ASR_BLOCKS[-1]].acts[0]["final"]
-    head_x = be.tensor(mx.F32, (S["hidden"], 1), last.numpy().reshape(ASR_BLOCKS[-1], S["hidden"])[-1:])
+    last = acts[blocks[-1]].acts[0]["final"]
+    head_x = be.tensor(mx.F32, (S["hidden"], 1), last.numpy().reshape(blocks[-1], S["hidden"])[-1:])
     pre.append(Launch("head_last_row", dec.head_bytes(), 0, lambda: be.mul_mat(dec.embd, head_x, logits)))
     tok = decode_token_launches(be, mx, dec, dacts, ids, x0, logits)
     pre_ops = sum(L.ops for L in pre)
@@ -571,15 +585,21 @@ def run_asr(args, mx, be, threads):
     ms_tok = time_graph(be, tok, max(1, args.steps) * ASR_DECODE_TOKENS, args.warmup, not args.no_graph)
     ms_step = ms_pre + ASR_DECODE_TOKENS * ms_tok
     table = label_table(pre + tok, per_label_pass(be, pre + tok, reps=3))
-    roof = mfma_roofline("k_gemm_q8_0_i8 (with its activation pass)", table,
-                         [l for l in table if l.startswith("prefill_M512")])
-    roof["traffic"] = None
+    # the prefill GEMM dequantizes Q8_0 weights and Q8_0-quantized activations to fp16 and accumulates in fp32 on
+    # fp16 MFMA (MX_GEMM_DQ=0 selects the int8 MFMA GEMM); the decode mat-vecs use int8 dot products
+    dq = os.environ.get("MX_GEMM_DQ", "1") != "0"
+    roof = (mfma_roofline("k_gemm_dq_q8_0 (with its activation pass)", table,
+                          [l for l in table if l.startswith("prefill_M512")], FP16_PEAK_TFLOPS, "TFLOP/s") if dq else
+            mfma_roofline("k_gemm_q8_0_i8 (with its activation pass)", table,
+                          [l for l in table if l.startswith("prefill_M512")]))
+    roof["traffic"] = read_traffic("asr-1.7b") if dq else None
     tops = pre_ops / (ms_pre * 1e-3) / 1e12
     tok_w = sum(L.weight_bytes for L in tok)
-    result = base_result(args, round(tops, 2), "TOP/s", ms_step, "int8", {
+    result = base_result(args, round(tops, 2), "TOP/s", ms_step, "fp16" if dq else "int8", {
         "workload": "qwen3-asr-1.7b-shape Q8_0 prefill of 1564 rows + 32 decode tokens", **S,
-        "blocks": list(ASR_BLOCKS), "decode_tokens": ASR_DECODE_TOKENS, "weights": "Q8_0", "graph": not args.no_graph})
-    result.update({"int8_frac": round(tops / INT8_PEAK_TOPS, 4), "prefill_ms": round(ms_pre, 4),
+        "blocks": list(blocks), "decode_tokens": ASR_DECODE_TOKENS, "weights": "Q8_0", "graph": not args.no_graph})
+    result.update({"mfma_frac": round(tops / (FP16_PEAK_TFLOPS if dq else INT8_PEAK_TOPS), 4),
+                   "decode_dtype": "int8", "prefill_ms": round(ms_pre, 4),
                    "prefill_ops": pre_ops, "decode_ms_per_token": round(ms_tok, 5),
                    "decode_tok_s": round(1e3 / ms_tok, 2), "decode_weight_bytes_per_token": tok_w,
                    "decode_hbm_frac": round(tok_w / (ms_tok * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "roofline": roof,
@@ -616,7 +636,7 @@ def run_moe(args, mx, be, threads):
     log(f"expert weights generated and uploaded ({MOE_LAYERS} layer copies) in {time.time() - t0:.1f} s")
     per_expert = sum(row_bytes(Q4_K, K) * N for _, K, N in specs)
     per_batch, all_launches, ms_total = [], [], 0.0
-    for T in MOE_BATCHES:
+    for T in args.batches or MOE_BATCHES:
         launches, wbytes, distinct = [], 0, []
         xb = be.tensor(mx.F32, (MOE_H, 1, T), mx.fill_normal(0xAC700005 + T, T, MOE_H))
         xa = be.tensor(mx.F32, (MOE_F, MOE_K, T), mx.fill_normal(0xAC700105 + T, T * MOE_K, MOE_F))
@@ -652,8 +672,8 @@ def run_moe(args, mx, be, threads):
     total_b = sum(L.nbytes for _, ls, _ in all_launches for L in ls)
     gbps = total_b / (ms_total * 1e-3) / 1e9
     T_dom, l_dom, ms_dom = all_launches[-1]
-    roof = step_hbm_roofline(f"k_mmid_experts<Q4_K> at T = {T_dom} (with its bucket and Q8_K passes)", l_dom, ms_dom)
-    roof["traffic"] = None
+    roof = step_hbm_roofline(f"k_mmid_q4k at T = {T_dom} (with its bucket and Q8_K pass)", l_dom, ms_dom)
+    roof["traffic"] = read_traffic("moe")
     result = base_result(args, round(gbps, 1), "GB/s", ms_total, "int8", {
         "workload": "drama3-like MoE FFN layer via MUL_MAT_ID, token batches 1, 16, 256", "experts": MOE_E,
         "top_k": MOE_K, "hidden": MOE_H, "expert_ffn": MOE_F, "weights": "Q4_K", "layer_copies": MOE_LAYERS,
@@ -700,14 +720,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 skips it)")
     ap.add_argument("--no-graph", action="store_true", help="replay the step eagerly instead of as a graph")
+    ints = lambda v: [int(t) for t in v.split(",")]
+    ap.add_argument("--blocks", type=ints, default=None,
+                    help="asr-1.7b: prefill block rows (default 512,512,512,28; counter passes use 512,512,512)")
+    ap.add_argument("--batches", type=ints, default=None,
+                    help="moe: token batches (default 1,16,256; counter passes use 256)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help="print the traffic summary of two rocprofv3 --pmc runs of the decode benchmark and exit")
+                    help="print the traffic summary of two rocprofv3 --pmc runs of --workload's benchmark and exit")
     args = ap.parse_args()
     if args.summarize_pmc:
-        print(summarize_pmc(*args.summarize_pmc))
+        print(summarize_pmc(*args.summarize_pmc, TRAFFIC[args.workload][1]))
         return
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported by this build", file=sys.stderr)
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported", file=sys.stderr)
         sys.exit(2)
     steps, warmup = DEFAULT_STEPS[args.workload]
     args.steps = steps if args.steps is None else args.steps
@@ -721,6 +746,7 @@ def main():
         print("no GPU visible to libmx", file=sys.stderr)
         sys.exit(1)
     be = mx.Backend(0)
+    calibration_copy(mx, be)
     threads = max(1, len(os.sched_getaffinity(0)))
     result = WORKLOADS[args.workload](args, mx, be, threads)
     be.close()
