@@ -1,12 +1,14 @@
 // MUL_MAT_ID on Q4_K experts as a grouped product: dst[:, s, t] = as[ids[s, t]] . quant(b[:, s % b_ne1, t]).
 //
-// The prep launch cuts each expert's (token, slot) pairs into chunks of up to 16, the rows of one 16x16 MFMA tile. A
-// workgroup takes one chunk and a few blocks of 64 of the expert's weight rows (dst columns); wave w owns columns
-// 16 w .. 16 w + 15 of each block and streams their super-blocks block after block.
+// The prep launch cuts each expert's (token, slot) pairs into chunks of up to 32, the rows of two 16-row MFMA tiles.
+// A workgroup takes one chunk and a few blocks of 128 of the expert's weight rows (dst columns); wave w owns columns
+// 16 w .. 16 w + 15 of each block and streams their super-blocks block after block, so each weight byte leaves HBM
+// once per 32 pairs of its expert, and each decoded weight fragment feeds both 16-row tiles (a chunk of at most 16
+// pairs runs the one-tile form).
 //
 // The weights stream through a ring of four stages per wave in LDS, filled by global_load_lds copies issued three
 // steps ahead (no registers held for them). The chunk's activation operands (K <= 2048) are loaded into LDS once per
-// workgroup and shared by its four waves and all its column blocks.
+// workgroup and shared by its eight waves and all its column blocks.
 //
 // Arithmetic per 256-element super-block, as ggml-cpu's vec_dot_q4_K_q8_K (and the Q4_K prefill GEMM):
 //   y += dx * (d * sum_j sc_j * S_j  -  dmin * sum_j mn_j * bsum_j)
@@ -47,8 +49,10 @@ __device__ __forceinline__ uint32_t mq_min(uint32_t s1, uint32_t s2, int j) {
     return j < 4 ? lo : up;
 }
 
-constexpr int MQ_COLS = 64;  // dst columns per column block: 16 per wave
-static_assert(MMID_CHUNK == 16, "a chunk is one 16-row MFMA tile");
+constexpr int MQ_W = 8;              // waves per workgroup
+constexpr int MQ_COLS = 16 * MQ_W;   // dst columns per column block: 16 per wave
+constexpr int MQ_ROWS = 32;          // rows (pairs) of a chunk: two 16-row MFMA tiles
+static_assert(MMID_CHUNK == MQ_ROWS, "a chunk is two 16-row MFMA tiles");
 
 constexpr int MQ_S = 4;         // ring stages per wave
 constexpr int MQ_STAGE = 2304;  // one stage: 16 columns x (128 code bytes + 12 scale bytes + d | dmin)
@@ -65,14 +69,15 @@ __device__ __forceinline__ void mq_wait_vm() {
 __device__ __forceinline__ void mq_order() { asm volatile("" ::: "memory"); }
 
 // LDS of a workgroup: per wave a ring of MQ_S weight stages, then the chunk's activation operands for up to
-// MQ_KSEG super-blocks (one segment of K), laid out as the lanes read them:
-//   codes   [sb][q][grp][fr] x 16 bytes: row fr, elements 256 sb + 64 q + 16 grp .. + 15
-//   sums    [sb][fr] x 32 bytes: row fr's split sub-block sums [64 h_j | l_j] (fp16)
-//   scales  [sb][fr] floats: row fr's Q8_K scale
+// MQ_KSEG super-blocks (one segment of K), laid out as the lanes read them (tile g = rows 16 g .. 16 g + 15):
+//   codes   [sb][g][q][grp][fr] x 16 bytes: row 16 g + fr, elements 256 sb + 64 q + 16 grp .. + 15
+//   sums    [sb][g][fr] x 32 bytes: that row's split sub-block sums [64 h_j | l_j] (fp16)
+//   scales  [sb][g][fr] floats: that row's Q8_K scale
 constexpr int MQ_KSEG = 8;
-constexpr int MQ_RING = 4 * MQ_S * MQ_STAGE;
-constexpr int MQ_AQ = MQ_RING, MQ_A16 = MQ_AQ + MQ_KSEG * 4096, MQ_ADX = MQ_A16 + MQ_KSEG * 512;
-constexpr int MQ_LDS = MQ_ADX + MQ_KSEG * 64;
+constexpr int MQ_RING = MQ_W * MQ_S * MQ_STAGE;
+constexpr int MQ_AQ = MQ_RING, MQ_A16 = MQ_AQ + MQ_KSEG * 8192, MQ_ADX = MQ_A16 + MQ_KSEG * 1024;
+constexpr int MQ_LDS = MQ_ADX + MQ_KSEG * 128;
+static_assert(MQ_LDS <= 160 * 1024, "one workgroup per CU");
 
 // One wave's view of its work: the weight stream (ncb column blocks x nsb super-blocks).
 struct MqLane {
@@ -85,38 +90,43 @@ struct MqLane {
     uint32_t ring_lds, a_lds;  // LDS byte addresses of the ring and of the activation operands
 };
 
-// Segment `seg` of the chunk's activation operands, as this thread brings it to LDS: pieces of row t & 15 (arow: its
-// activation row). Loads past the segment repeat its last super-block; only the stores are conditional.
+// Segment `seg` of the chunk's activation operands, as thread t = 256 g + u brings it to LDS: pieces of row
+// 16 g + (t & 15) (arow: its activation row). Loads past the segment repeat its last super-block; only the stores
+// are conditional.
 struct MqSeg {
-    v4i codes[MQ_KSEG];  // thread t = (q, grp, fr): elements 64 q + 16 grp .. + 15 of each super-block
-    v4i sums;            // thread t = (sb, half, fr): 8 of the 16 split sums of super-block sb
-    float scale;         // thread t = (sb, fr): the Q8_K scale of super-block sb
+    v4i codes[MQ_KSEG];  // u = (q, grp, fr): elements 64 q + 16 grp .. + 15 of each super-block
+    v4i sums;            // u = (sb, half, fr): 8 of the 16 split sums of super-block sb
+    float scale;         // u = (sb, fr): the Q8_K scale of super-block sb
 };
 __device__ __forceinline__ MqSeg mq_seg_load(const MulMatIdArgs &a, int arow, int seg, int nsb) {
-    const int t = threadIdx.x;
+    const int u = threadIdx.x & 255;
     const int sb0 = MQ_KSEG * seg, last = min(MQ_KSEG, nsb - sb0) - 1;
     MqSeg r;
-    const int8_t *xs = a.xq + arow * (int)a.K + sb0 * 256 + 64 * (t >> 6) + 16 * ((t >> 4) & 3);
+    const int8_t *xs = a.xq + arow * (int)a.K + sb0 * 256 + 64 * (u >> 6) + 16 * ((u >> 4) & 3);
 #pragma unroll
     for (int i = 0; i < MQ_KSEG; i++) r.codes[i] = *(const v4i *)(xs + min(i, last) * 256);
-    r.sums = *(const v4i *)(a.x16 + (arow * nsb + sb0 + min(t >> 5, last)) * 16 + 8 * ((t >> 4) & 1));
-    r.scale = a.xd[arow * nsb + sb0 + min(t >> 4, last)];
+    r.sums = *(const v4i *)(a.x16 + (arow * nsb + sb0 + min(u >> 5, last)) * 16 + 8 * ((u >> 4) & 1));
+    r.scale = a.xd[arow * nsb + sb0 + min((u >> 4) & 7, last)];
     return r;
 }
 // The stores go through inline assembly: the compiler would otherwise order them after every copy in flight into
 // the (disjoint) ring, since it cannot tell the two LDS regions apart.
 __device__ __forceinline__ void mq_seg_store(const MqSeg &r, uint8_t *smem, int seg, int nsb) {
-    const int t = threadIdx.x, fr = t & 15;
+    const int g = threadIdx.x >> 8, u = threadIdx.x & 255, fr = u & 15;
     const int n = min(MQ_KSEG, nsb - MQ_KSEG * seg);
     const uint32_t base = (uint32_t)(uintptr_t)(mq_lds *)smem;
 #pragma unroll
     for (int i = 0; i < MQ_KSEG; i++)
-        if (i < n) asm volatile("ds_write_b128 %0, %1" ::"v"(base + MQ_AQ + i * 4096 + 16 * t), "v"(r.codes[i]) : "memory");
-    if ((t >> 5) < n)
-        asm volatile("ds_write_b128 %0, %1" ::"v"(base + MQ_A16 + (t >> 5) * 512 + fr * 32 + ((t >> 4) & 1) * 16),
+        if (i < n)
+            asm volatile("ds_write_b128 %0, %1" ::"v"(base + MQ_AQ + i * 8192 + g * 4096 + 16 * u), "v"(r.codes[i])
+                         : "memory");
+    if ((u >> 5) < n)
+        asm volatile("ds_write_b128 %0, %1" ::"v"(base + MQ_A16 + (u >> 5) * 1024 + g * 512 + fr * 32 +
+                                                  ((u >> 4) & 1) * 16),
                      "v"(r.sums) : "memory");
-    if ((t >> 4) < n)
-        asm volatile("ds_write_b32 %0, %1" ::"v"(base + MQ_ADX + (t >> 4) * 64 + fr * 4), "v"(r.scale) : "memory");
+    if ((u >> 4) < n)
+        asm volatile("ds_write_b32 %0, %1" ::"v"(base + MQ_ADX + (u >> 4) * 128 + g * 64 + fr * 4), "v"(r.scale)
+                     : "memory");
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
 
@@ -149,40 +159,67 @@ __device__ __forceinline__ void mq_copy(const MqLane &c, MqCursor &k, int ncb) {
 }
 
 // Step of the wave's stream: super-block sb (sbl within the loaded segment) of its column block, weights in ring
-// stage SLOT. Each step issues the copies MQ_S - 1 steps ahead (3 ops) and then waits for its own, which were issued
-// MQ_S - 1 copies (9 ops) earlier. Operands are read from LDS in one block with the compiler kept out of it: it cannot
-// see that the copies waited for wrote there.
-template <int SLOT>
-__device__ __forceinline__ void mq_step(const MqLane &c, MqCursor &k, int ncb, int sbl, float (&acc)[4]) {
+// stage SLOT, for NG 16-row tiles of the chunk. Each step issues the copies MQ_S - 1 steps ahead (3 ops) and then
+// waits for its own, which were issued MQ_S - 1 copies (9 ops) earlier. Operands are read from LDS in one block with
+// the compiler kept out of it: it cannot see that the copies waited for wrote there.
+template <int SLOT, int NG>
+__device__ __forceinline__ void mq_step(const MqLane &c, MqCursor &k, int ncb, int sbl, float (&acc)[NG][4]) {
     static_assert(MQ_S == 4, "the wait count assumes four stages");
     mq_copy<(SLOT + MQ_S - 1) % MQ_S>(c, k, ncb);
     mq_wait_vm<9>();
     const uint32_t st = c.ring_lds + SLOT * MQ_STAGE;
-    const uint32_t aq = c.a_lds + MQ_AQ - MQ_RING + sbl * 4096 + 16 * c.lane;
-    const uint32_t a16 = c.a_lds + MQ_A16 - MQ_RING + sbl * 512 + 32 * c.fr + 8 * c.grp;
-    const uint32_t adx = c.a_lds + MQ_ADX - MQ_RING + sbl * 64 + 16 * c.grp;
-    v4i w[4];   // code bytes 32 q + 16 (grp & 1) .. + 15 of column fr
-    uint4 sv;   // its scale words 0..2, d | dmin
-    v4i xa[4];  // activation bytes 64 q + 16 grp .. + 15 of row fr
-    v4h s16;    // row fr's split sums 4 grp .. 4 grp + 3
-    v4f dxv;    // Q8_K scales of rows 4 grp .. 4 grp + 3
-    asm volatile(
-        "ds_read_b128 %0, %11\n"
-        "ds_read_b128 %1, %11 offset:256\n"
-        "ds_read_b128 %2, %11 offset:512\n"
-        "ds_read_b128 %3, %11 offset:768\n"
-        "ds_read_b128 %4, %12 offset:2048\n"
-        "ds_read_b128 %5, %13\n"
-        "ds_read_b128 %6, %13 offset:1024\n"
-        "ds_read_b128 %7, %13 offset:2048\n"
-        "ds_read_b128 %8, %13 offset:3072\n"
-        "ds_read_b64 %9, %14\n"
-        "ds_read_b128 %10, %15\n"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(sv), "=&v"(xa[0]), "=&v"(xa[1]), "=&v"(xa[2]),
-          "=&v"(xa[3]), "=&v"(s16), "=&v"(dxv)  // early clobber: no output may share a register with an address
-        : "v"(st + 1024 * (c.grp & 1) + 16 * c.fr), "v"(st + 16 * c.fr), "v"(aq), "v"(a16), "v"(adx)
-        : "memory");
+    const uint32_t aq = c.a_lds + MQ_AQ - MQ_RING + sbl * 8192 + 16 * c.lane;
+    const uint32_t a16 = c.a_lds + MQ_A16 - MQ_RING + sbl * 1024 + 32 * c.fr + 8 * c.grp;
+    const uint32_t adx = c.a_lds + MQ_ADX - MQ_RING + sbl * 128 + 16 * c.grp;
+    v4i w[4];       // code bytes 32 q + 16 (grp & 1) .. + 15 of column fr
+    uint4 sv;       // its scale words 0..2, d | dmin
+    v4i xa[NG][4];  // activation bytes 64 q + 16 grp .. + 15 of row 16 g + fr
+    v4h s16[NG];    // that row's split sums 4 grp .. 4 grp + 3
+    v4f dxv[NG];    // Q8_K scales of rows 16 g + 4 grp .. + 3
+    if constexpr (NG == 1) {
+        asm volatile(
+            "ds_read_b128 %0, %11\n"
+            "ds_read_b128 %1, %11 offset:256\n"
+            "ds_read_b128 %2, %11 offset:512\n"
+            "ds_read_b128 %3, %11 offset:768\n"
+            "ds_read_b128 %4, %12 offset:2048\n"
+            "ds_read_b128 %5, %13\n"
+            "ds_read_b128 %6, %13 offset:1024\n"
+            "ds_read_b128 %7, %13 offset:2048\n"
+            "ds_read_b128 %8, %13 offset:3072\n"
+            "ds_read_b64 %9, %14\n"
+            "ds_read_b128 %10, %15\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(sv), "=&v"(xa[0][0]), "=&v"(xa[0][1]),
+              "=&v"(xa[0][2]), "=&v"(xa[0][3]), "=&v"(s16[0]), "=&v"(dxv[0])  // early clobber: no output may share
+            : "v"(st + 1024 * (c.grp & 1) + 16 * c.fr), "v"(st + 16 * c.fr), "v"(aq), "v"(a16), "v"(adx)  // an address
+            : "memory");
+    } else {
+        asm volatile(
+            "ds_read_b128 %0, %17\n"
+            "ds_read_b128 %1, %17 offset:256\n"
+            "ds_read_b128 %2, %17 offset:512\n"
+            "ds_read_b128 %3, %17 offset:768\n"
+            "ds_read_b128 %4, %18 offset:2048\n"
+            "ds_read_b128 %5, %19\n"
+            "ds_read_b128 %6, %19 offset:1024\n"
+            "ds_read_b128 %7, %19 offset:2048\n"
+            "ds_read_b128 %8, %19 offset:3072\n"
+            "ds_read_b128 %9, %19 offset:4096\n"
+            "ds_read_b128 %10, %19 offset:5120\n"
+            "ds_read_b128 %11, %19 offset:6144\n"
+            "ds_read_b128 %12, %19 offset:7168\n"
+            "ds_read_b64 %13, %20\n"
+            "ds_read_b64 %14, %20 offset:512\n"
+            "ds_read_b128 %15, %21\n"
+            "ds_read_b128 %16, %21 offset:64\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(sv), "=&v"(xa[0][0]), "=&v"(xa[0][1]),
+              "=&v"(xa[0][2]), "=&v"(xa[0][3]), "=&v"(xa[NG - 1][0]), "=&v"(xa[NG - 1][1]), "=&v"(xa[NG - 1][2]),
+              "=&v"(xa[NG - 1][3]), "=&v"(s16[0]), "=&v"(s16[NG - 1]), "=&v"(dxv[0]), "=&v"(dxv[NG - 1])
+            : "v"(st + 1024 * (c.grp & 1) + 16 * c.fr), "v"(st + 16 * c.fr), "v"(aq), "v"(a16), "v"(adx)
+            : "memory");
+    }
 
     const int grp = c.grp, hi = grp >> 1;
     const v4i mask = {0x0F0F0F0F, 0x0F0F0F0F, 0x0F0F0F0F, 0x0F0F0F0F};
@@ -191,7 +228,9 @@ __device__ __forceinline__ void mq_step(const MqLane &c, MqCursor &k, int ncb, i
 #pragma unroll
     for (int i = 0; i < 4; i++) b16[i] = (_Float16)(float)mq_min(sv.y, sv.z, 4 * (grp & 1) + i);
     const float d = h2f((uint16_t)(sv.w & 0xFFFF)), dmin = h2f((uint16_t)(sv.w >> 16));
-    v4i ih = {0, 0, 0, 0}, il = {0, 0, 0, 0};
+    v4i ih[NG], il[NG];
+#pragma unroll
+    for (int g = 0; g < NG; g++) ih[g] = il[g] = (v4i){0, 0, 0, 0};
 #pragma unroll
     for (int q = 0; q < 4; q++) {  // codes scaled by the hi / lo halves of their sub-block's scale
         const uint32_t sc = mq_scale(sv.x, sv.z, 2 * q + hi);
@@ -199,56 +238,39 @@ __device__ __forceinline__ void mq_step(const MqLane &c, MqCursor &k, int ncb, i
         const v4i cq = (w[q] >> (4 * hi)) & mask;
         const v4i bh = {mq_pk_mul(cq.x, h), mq_pk_mul(cq.y, h), mq_pk_mul(cq.z, h), mq_pk_mul(cq.w, h)};
         const v4i bl = {mq_pk_mul(cq.x, l), mq_pk_mul(cq.y, l), mq_pk_mul(cq.z, l), mq_pk_mul(cq.w, l)};
-        ih = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[q], bh, ih, 0, 0, 0);
-        il = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[q], bl, il, 0, 0, 0);
-    }
-    const v4f mt = __builtin_amdgcn_mfma_f32_16x16x16f16(s16, b16, (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {  // output row 4 grp + i
-        const int v = (ih[i] << 3) + il[i];
-        acc[i] = fmaf(dxv[i], fmaf(-dmin, mt[i], d * (float)v), acc[i]);
+        for (int g = 0; g < NG; g++) {
+            ih[g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[g][q], bh, ih[g], 0, 0, 0);
+            il[g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[g][q], bl, il[g], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+        const v4f mt = __builtin_amdgcn_mfma_f32_16x16x16f16(s16[g], b16, (v4f){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {  // output row 16 g + 4 grp + i
+            const int v = (ih[g][i] << 3) + il[g][i];
+            acc[g][i] = fmaf(dxv[g][i], fmaf(-dmin, mt[i], d * (float)v), acc[g][i]);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);  // steps do not interleave: one step's operands live at a time
 }
 
-// Grid: x = groups of `cpb` column blocks of MQ_COLS, y = chunks (workgroups past the last chunk leave at once).
-// Wave w owns columns 16 w .. 16 w + 15 of each block and streams super-blocks 0 .. nsb - 1 (nsb <= MQ_KSEG) of
-// every block; a block's sums are written when its last super-block is done.
-__global__ __launch_bounds__(256) void k_mmid_q4k(MulMatIdArgs a, int cpb) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const int chunk = blockIdx.y;
-    if (chunk >= a.ntiles[0]) return;  // uniform: fewer chunks than the grid allows
-    const int p0 = a.tiles[3 * chunk], cnt = a.tiles[3 * chunk + 1], e = a.tiles[3 * chunk + 2];
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int N = (int)a.N;
+// One workgroup's share with NG 16-row tiles (NG = 1 when the chunk has at most 16 pairs).
+template <int NG>
+__device__ __forceinline__ void mq_run(const MulMatIdArgs &a, MqLane &c, uint8_t *smem, int p0, int cnt, int ncb) {
     const unsigned n_ids = (unsigned)a.n_ids;
-    const int nblk = (N + MQ_COLS - 1) / MQ_COLS;
-    const int cb0 = blockIdx.x * cpb, ncb = min(cpb, nblk - cb0);
-
-    MqLane c;
-    c.lane = threadIdx.x & 63;
-    c.fr = c.lane & 15;
-    c.grp = c.lane >> 4;
-    c.nsb = (int)(a.K / 256);
-    c.nsteps = ncb * c.nsb;
-    // row fr of the chunk is pair p0 + fr (rows past the chunk repeat its last pair; their sums are dropped)
-    const int pair = a.pairs[p0 + min(c.fr, cnt - 1)];
-    const unsigned pt = (unsigned)pair / n_ids, ps = (unsigned)pair - pt * n_ids;
-    const int arow = (int)(pt * (unsigned)a.b_ne1 + (a.b_ne1 == 1 ? 0u : ps));
-    // Copy sources: lane l brings code bytes 32 grp + 16 h (h = 0, 1) of column fr, and scale word l & 3 of column
-    // l >> 2 (words 0..2: the 12 scale bytes, word 3: d | dmin). They land at stage + 1024 h + 16 l and stage + 2048 +
-    // 4 l: bytes 32 q + 16 h of column fr sit at stage + 1024 h + 256 q + 16 fr, its scale words at stage + 2048 + 16 fr.
-    const int64_t eblk = (int64_t)e * N * c.nsb;
-    c.nmax = N - 1;
-    c.col0 = cb0 * MQ_COLS + wave * 16 + c.fr;
-    c.scol0 = cb0 * MQ_COLS + wave * 16 + (c.lane >> 2);
-    c.qe = a.w.p0 + eblk * 128 + 32 * c.grp;
-    const int sw = c.lane & 3;
-    c.sstride = sw < 3 ? 12 : 4;
-    c.se = sw < 3 ? a.w.p1 + eblk * 12 + 4 * sw : a.w.p2 + eblk * 4;
-    c.ring = smem + wave * MQ_S * MQ_STAGE;
-    c.ring_lds = (uint32_t)(uintptr_t)(mq_lds *)c.ring;
-    c.a_lds = (uint32_t)(uintptr_t)(mq_lds *)(smem + MQ_RING);
+    // lane fr carries row 16 g + fr of tile g (rows past the chunk repeat its last pair; their sums are dropped)
+    int pair[NG];
+#pragma unroll
+    for (int g = 0; g < NG; g++) pair[g] = a.pairs[p0 + min(16 * g + c.fr, cnt - 1)];
+    // the activation row thread t brings to LDS: row 16 (t >> 8) + (t & 15) of the chunk
+    int arow;
+    {
+        const int pr = a.pairs[p0 + min(16 * (int)(threadIdx.x >> 8) + c.fr, cnt - 1)];
+        const unsigned pt = (unsigned)pr / n_ids, ps = (unsigned)pr - pt * n_ids;
+        arow = (int)(pt * (unsigned)a.b_ne1 + (a.b_ne1 == 1 ? 0u : ps));
+    }
 
     // activation operands of the first segment (their loads go out ahead of the copies), then the ring's prologue
     MqCursor k;
@@ -264,51 +286,104 @@ __global__ __launch_bounds__(256) void k_mmid_q4k(MulMatIdArgs a, int cpb) {
     }
     __syncthreads();
 
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float acc[NG][4];
+#pragma unroll
+    for (int g = 0; g < NG; g++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[g][i] = 0.f;
     int sb = 0, cb = 0;
     // after each step: a column block is finished when its last super-block is
     auto finish = [&]() {
         if (++sb < c.nsb) return;
         const int col = c.col0 + MQ_COLS * cb;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int row = 4 * c.grp + i;
-            const unsigned pi = (unsigned)__shfl(pair, row, 64);  // lane `row` holds that row's pair
-            if (row < cnt && col <= c.nmax) {
-                const unsigned t = pi / n_ids, s = pi - t * n_ids;
-                float *y = (float *)((uint8_t *)a.dst + (int64_t)s * a.dst_nb1 + (int64_t)t * a.dst_nb2);
-                y[col] = acc[i];
+        for (int g = 0; g < NG; g++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = 4 * c.grp + i;
+                const unsigned pi = (unsigned)__shfl(pair[g], row, 64);  // lane `row` holds that row's pair
+                if (16 * g + row < cnt && col <= c.nmax) {
+                    const unsigned t = pi / n_ids, s = pi - t * n_ids;
+                    float *y = (float *)((uint8_t *)a.dst + (int64_t)s * a.dst_nb1 + (int64_t)t * a.dst_nb2);
+                    y[col] = acc[g][i];
+                }
+                acc[g][i] = 0.f;
             }
-            acc[i] = 0.f;
-        }
         sb = 0;
         cb++;
     };
 #pragma unroll 1
     for (int it = 0; it < c.nsteps; it += MQ_S) {
-        mq_step<0>(c, k, ncb, sb, acc);
+        mq_step<0, NG>(c, k, ncb, sb, acc);
         finish();
         if (it + 1 < c.nsteps) {
-            mq_step<1>(c, k, ncb, sb, acc);
+            mq_step<1, NG>(c, k, ncb, sb, acc);
             finish();
         }
         if (it + 2 < c.nsteps) {
-            mq_step<2>(c, k, ncb, sb, acc);
+            mq_step<2, NG>(c, k, ncb, sb, acc);
             finish();
         }
         if (it + 3 < c.nsteps) {
-            mq_step<3>(c, k, ncb, sb, acc);
+            mq_step<3, NG>(c, k, ncb, sb, acc);
             finish();
         }
     }
     mq_wait_vm<0>();  // no copy may still be landing in LDS when the workgroup ends
 }
 
-// Column blocks per workgroup: enough workgroups for about two per CU over the chunks the grid allows for.
-static int mq_cpb(const MulMatIdArgs &a) {
-    const int64_t nblk = (a.N + MQ_COLS - 1) / MQ_COLS;
-    const int64_t cpb = a.max_tiles * nblk / 512;
-    return (int)(cpb < 1 ? 1 : (cpb > nblk ? nblk : cpb));
+// Grid: one workgroup per CU. The work is ntiles x nblk units (a chunk and one block of MQ_COLS columns); workgroup b
+// takes the contiguous units [b U / G, (b + 1) U / G), chunk by chunk, so every CU gets the same number of column
+// blocks to within one. Within a unit wave w owns columns 16 w .. 16 w + 15 of the block and streams super-blocks
+// 0 .. nsb - 1 (nsb <= MQ_KSEG); a block's sums are written when its last super-block is done.
+__global__ __launch_bounds__(64 * MQ_W) void k_mmid_q4k(MulMatIdArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int N = (int)a.N;
+    const int nblk = (N + MQ_COLS - 1) / MQ_COLS;
+    const int64_t units = (int64_t)a.ntiles[0] * nblk;
+    const int u1 = (int)((blockIdx.x + 1) * units / gridDim.x);
+    for (int u = (int)(blockIdx.x * units / gridDim.x); u < u1;) {
+        const int chunk = u / nblk, cb0 = u - chunk * nblk, ncb = min(nblk - cb0, u1 - u);
+        const int p0 = a.tiles[3 * chunk], cnt = a.tiles[3 * chunk + 1], e = a.tiles[3 * chunk + 2];
+        MqLane c;
+        c.lane = threadIdx.x & 63;
+        c.fr = c.lane & 15;
+        c.grp = c.lane >> 4;
+        c.nsb = (int)(a.K / 256);
+        c.nsteps = ncb * c.nsb;
+        // Copy sources: lane l brings code bytes 32 grp + 16 h (h = 0, 1) of column fr, and scale word l & 3 of
+        // column l >> 2 (words 0..2: the 12 scale bytes, word 3: d | dmin). They land at stage + 1024 h + 16 l and
+        // stage + 2048 + 4 l: bytes 32 q + 16 h of column fr sit at stage + 1024 h + 256 q + 16 fr, its scale words at
+        // stage + 2048 + 16 fr.
+        const int64_t eblk = (int64_t)e * N * c.nsb;
+        c.nmax = N - 1;
+        c.col0 = cb0 * MQ_COLS + wave * 16 + c.fr;
+        c.scol0 = cb0 * MQ_COLS + wave * 16 + (c.lane >> 2);
+        c.qe = a.w.p0 + eblk * 128 + 32 * c.grp;
+        const int sw = c.lane & 3;
+        c.sstride = sw < 3 ? 12 : 4;
+        c.se = sw < 3 ? a.w.p1 + eblk * 12 + 4 * sw : a.w.p2 + eblk * 4;
+        c.ring = smem + wave * MQ_S * MQ_STAGE;
+        c.ring_lds = (uint32_t)(uintptr_t)(mq_lds *)c.ring;
+        c.a_lds = (uint32_t)(uintptr_t)(mq_lds *)(smem + MQ_RING);
+        if (cnt > 16) mq_run<2>(a, c, smem, p0, cnt, ncb);
+        else mq_run<1>(a, c, smem, p0, cnt, ncb);
+        u += ncb;
+        __syncthreads();  // every wave is done with this chunk's activation operands before the next one's land
+    }
+}
+
+// Workgroups: one per CU of the current device.
+static int mq_grid() {
+    static const int n = [] {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            return 256;
+        return cus;
+    }();
+    return n;
 }
 
 bool mmid_q4k_supported(const MulMatIdArgs &a) {
@@ -325,10 +400,7 @@ hipError_t launch_mmid_q4k(const MulMatIdArgs &a, hipStream_t s) {
         if (err != hipSuccess) return err;
         attr = true;
     }
-    const int64_t nblk = (a.N + MQ_COLS - 1) / MQ_COLS;
-    const int cpb = mq_cpb(a);
-    const dim3 grid((unsigned)((nblk + cpb - 1) / cpb), (unsigned)a.max_tiles);
-    hipLaunchKernelGGL(k_mmid_q4k, grid, dim3(256), MQ_LDS, s, a, cpb);
+    hipLaunchKernelGGL(k_mmid_q4k, dim3((unsigned)mq_grid()), dim3(64 * MQ_W), MQ_LDS, s, a);
     return hipGetLastError();
 }
 

@@ -236,8 +236,8 @@ struct MulMatIdArgs {
 hipError_t launch_argmax(const float *src, int64_t ne0, int64_t nrows, int64_t nb1, int32_t *dst, int64_t dst_nb0,
                          hipStream_t s);
 
-// Pairs per chunk: 16-row MFMA groups that share each expanded weight fragment.
-constexpr int MMID_CHUNK = 16;
+// Pairs per chunk of one expert's (token, slot) pairs: two 16-row MFMA tiles that share each expanded weight fragment.
+constexpr int MMID_CHUNK = 32;
 // Scratch bytes MUL_MAT_ID needs and the carving of `base` into the fields above.
 size_t mul_mat_id_scratch(MulMatIdArgs *a, void *base);
 hipError_t launch_mul_mat_id(const MulMatIdArgs &a, hipStream_t s);

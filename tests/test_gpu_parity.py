@@ -257,14 +257,15 @@ def test_supports_op(mx, be):
 
 
 # --------------------------------------------------------------------------------------------------- MUL_MAT_ID
-def mmid_case(mx, be, t, E, K, N, n_ids, T, bcast, seed, skew=0.0):
+def mmid_case(mx, be, t, E, K, N, n_ids, T, bcast, seed, skew=0.0, ids=None):
     w = weights(t, E * N, K, seed).reshape(E, N, -1)
     B = 1 if bcast else n_ids
     x = acts(seed + 1, T * B, K).reshape(T, B, K)
-    rng = np.random.default_rng(seed)
-    logits = rng.standard_normal((T, E))
-    logits[:, :n_ids] += skew  # a large skew sends most tokens to the same experts
-    ids = np.argsort(-logits, axis=1)[:, :n_ids].astype(np.int32)
+    if ids is None:
+        rng = np.random.default_rng(seed)
+        logits = rng.standard_normal((T, E))
+        logits[:, :n_ids] += skew  # a large skew sends most tokens to the same experts
+        ids = np.argsort(-logits, axis=1)[:, :n_ids].astype(np.int32)
     Wt = be.tensor(t, (K, N, E), w.reshape(E * N, -1))
     Xt = be.tensor(mx.F32, (K, B, T), x)
     It = be.tensor(mx.I32, (n_ids, T), ids)
@@ -288,6 +289,26 @@ def test_mul_mat_id(mx, be, t, T, bcast):
 def test_mul_mat_id_many_pairs(mx, be, t, skew):
     """Experts with more than 16 pairs (several tiles, a ragged last one) and N not a multiple of the column tile."""
     y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=70, bcast=False, seed=0x5EED0A00 + t, skew=skew)
+    assert rel_err(y, y_ref) <= TIGHT
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+def test_mul_mat_id_chunk_edges(mx, be, t):
+    """Experts with exactly 16, 17, 32, 33 and 70 pairs (one or two 16-row tiles per chunk, a chunk of one pair)
+    and none, at K = 2048 (the longest K the Q4_K expert kernel keeps in LDS) with b broadcast over the slots."""
+    counts = [16, 17, 0, 32, 33, 70]
+    ids = np.concatenate([np.full(c, e, np.int32) for e, c in enumerate(counts)])
+    np.random.default_rng(7).shuffle(ids)
+    y, y_ref = mmid_case(mx, be, t, E=len(counts), K=2048, N=136, n_ids=1, T=len(ids), bcast=True,
+                         seed=0x5EED0B00 + t, ids=ids.reshape(-1, 1))
+    assert rel_err(y, y_ref) <= TIGHT
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+def test_mul_mat_id_moe_layer_shape(mx, be, t):
+    """The drama3-like layer's down product (64 experts, top-4 of 64 tokens, K = 1536, b per slot) on 520 of its
+    2048 output rows."""
+    y, y_ref = mmid_case(mx, be, t, E=64, K=1536, N=520, n_ids=4, T=64, bcast=False, seed=0x5EED0C00 + t)
     assert rel_err(y, y_ref) <= TIGHT
 
 
