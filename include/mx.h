@@ -46,6 +46,7 @@ enum {
     MX_TYPE_Q8_0 = 8,
     MX_TYPE_Q8_1 = 9,
     MX_TYPE_Q4_K = 12,
+    MX_TYPE_Q5_K = 13,
     MX_TYPE_Q6_K = 14,
     MX_TYPE_Q8_K = 15,
     MX_TYPE_I32 = 26,

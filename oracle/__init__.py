@@ -17,14 +17,16 @@ import numpy as np
 HERE = pathlib.Path(__file__).resolve().parent
 BUILD = HERE / "_build"
 
-TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q8_1, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K, TYPE_I32 = 0, 1, 8, 9, 12, 14, 15, 26
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q8_1, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_K, TYPE_I32 = \
+    0, 1, 8, 9, 12, 13, 14, 15, 26
 ROUND_REF, ROUND_X86 = 0, 1
 
-BLCK = {TYPE_F32: 1, TYPE_F16: 1, TYPE_I32: 1, TYPE_Q8_0: 32, TYPE_Q8_1: 32, TYPE_Q4_K: 256, TYPE_Q6_K: 256,
-        TYPE_Q8_K: 256}
-TSIZE = {TYPE_F32: 4, TYPE_F16: 2, TYPE_I32: 4, TYPE_Q8_0: 34, TYPE_Q8_1: 36, TYPE_Q4_K: 144, TYPE_Q6_K: 210,
-         TYPE_Q8_K: 292}
-VEC_DOT_TYPE = {TYPE_Q8_0: TYPE_Q8_0, TYPE_Q4_K: TYPE_Q8_K, TYPE_Q6_K: TYPE_Q8_K}
+BLCK = {TYPE_F32: 1, TYPE_F16: 1, TYPE_I32: 1, TYPE_Q8_0: 32, TYPE_Q8_1: 32, TYPE_Q4_K: 256, TYPE_Q5_K: 256,
+        TYPE_Q6_K: 256, TYPE_Q8_K: 256}
+TSIZE = {TYPE_F32: 4, TYPE_F16: 2, TYPE_I32: 4, TYPE_Q8_0: 34, TYPE_Q8_1: 36, TYPE_Q4_K: 144, TYPE_Q5_K: 176,
+         TYPE_Q6_K: 210, TYPE_Q8_K: 292}
+VEC_DOT_TYPE = {TYPE_Q8_0: TYPE_Q8_0, TYPE_Q4_K: TYPE_Q8_K, TYPE_Q5_K: TYPE_Q8_K, TYPE_Q6_K: TYPE_Q8_K,
+                TYPE_F16: TYPE_F16, TYPE_F32: TYPE_F32}
 
 
 def row_size(t: int, ne0: int) -> int:
@@ -56,7 +58,7 @@ def lib():
         L.orc_fp16_to_fp32.argtypes, L.orc_fp16_to_fp32.restype = [ctypes.c_uint16], f32
         for n in ("orc_quantize_row_q8_0", "orc_quantize_row_q8_1"):
             getattr(L, n).argtypes, getattr(L, n).restype = [vp, vp, i64, i32], None
-        for n in ("orc_quantize_row_q8_K", "orc_quantize_row_q4_K", "orc_quantize_row_q6_K"):
+        for n in ("orc_quantize_row_q8_K", "orc_quantize_row_q4_K", "orc_quantize_row_q5_K", "orc_quantize_row_q6_K"):
             getattr(L, n).argtypes, getattr(L, n).restype = [vp, vp, i64], None
         L.orc_quantize_chunk.argtypes, L.orc_quantize_chunk.restype = [i32, vp, vp, i64, i64, i64], ctypes.c_size_t
         L.orc_dequantize_row.argtypes, L.orc_dequantize_row.restype = [i32, vp, vp, i64], i32
@@ -120,6 +122,10 @@ def quantize_rows(t: int, x: np.ndarray, rounding: int = ROUND_REF) -> np.ndarra
             L.orc_quantize_row_q8_K(_p(src), _p(dst), K)
         elif t == TYPE_Q4_K:
             L.orc_quantize_row_q4_K(_p(src), _p(dst), K)
+        elif t == TYPE_Q5_K:
+            L.orc_quantize_row_q5_K(_p(src), _p(dst), K)
+        elif t in (TYPE_F16, TYPE_F32):
+            L.orc_quantize_chunk(t, _p(src), _p(dst), 0, 1, K)
         elif t == TYPE_Q6_K:
             L.orc_quantize_row_q6_K(_p(src), _p(dst), K)
         else:

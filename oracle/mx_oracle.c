@@ -1,5 +1,6 @@
 /*
- * CPU oracle: a plain-C restatement of ggml's CPU arithmetic for Q8_0 / Q4_K / Q6_K MUL_MAT, MUL_MAT_ID and GET_ROWS.
+ * CPU oracle: a plain-C restatement of ggml's CPU arithmetic for Q8_0 / Q4_K / Q5_K / Q6_K / F16 / F32 MUL_MAT,
+ * MUL_MAT_ID and GET_ROWS.
  *
  * TEST INFRASTRUCTURE ONLY -- the checker, never the thing measured or shipped.
  *
@@ -25,18 +26,26 @@
 #define K_SCALE_SIZE 12
 #define GROUP_MAX_EPS 1e-15f
 
-/* ggml-common.h block structs (sizes 34, 36, 292, 144, 210 bytes; the reference confirms 34/144/210 in
+/* ggml-common.h block structs (sizes 34, 36, 292, 144, 176, 210 bytes; the reference confirms 34/144/210 in
  * checks/compare/quantize_compare.py:27). */
 typedef struct { uint16_t d; int8_t qs[QK8_0]; } blk_q8_0;
 typedef struct { uint16_t d; uint16_t s; int8_t qs[QK8_1]; } blk_q8_1;
 typedef struct { float d; int8_t qs[QK_K]; int16_t bsums[QK_K / 16]; } blk_q8_K;
 typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[K_SCALE_SIZE]; uint8_t qs[QK_K / 2]; } blk_q4_K;
+typedef struct {
+    uint16_t d;
+    uint16_t dmin;
+    uint8_t scales[K_SCALE_SIZE];
+    uint8_t qh[QK_K / 8];
+    uint8_t qs[QK_K / 2];
+} blk_q5_K;
 typedef struct { uint8_t ql[QK_K / 2]; uint8_t qh[QK_K / 4]; int8_t scales[QK_K / 16]; uint16_t d; } blk_q6_K;
 
 _Static_assert(sizeof(blk_q8_0) == 34, "q8_0 block");
 _Static_assert(sizeof(blk_q8_1) == 36, "q8_1 block");
 _Static_assert(sizeof(blk_q8_K) == 292, "q8_K block");
 _Static_assert(sizeof(blk_q4_K) == 144, "q4_K block");
+_Static_assert(sizeof(blk_q5_K) == 176, "q5_K block");
 _Static_assert(sizeof(blk_q6_K) == 210, "q6_K block");
 
 /* ------------------------------------------------------------------------------------------------------------------
@@ -97,7 +106,7 @@ int64_t orc_blck_size(int type) {
         case ORC_TYPE_F32: case ORC_TYPE_F16: case ORC_TYPE_I32: return 1;
         case ORC_TYPE_Q8_0: return QK8_0;
         case ORC_TYPE_Q8_1: return QK8_1;
-        case ORC_TYPE_Q4_K: case ORC_TYPE_Q6_K: case ORC_TYPE_Q8_K: return QK_K;
+        case ORC_TYPE_Q4_K: case ORC_TYPE_Q5_K: case ORC_TYPE_Q6_K: case ORC_TYPE_Q8_K: return QK_K;
         default: return 0;
     }
 }
@@ -109,6 +118,7 @@ size_t orc_type_size(int type) {
         case ORC_TYPE_Q8_0: return sizeof(blk_q8_0);
         case ORC_TYPE_Q8_1: return sizeof(blk_q8_1);
         case ORC_TYPE_Q4_K: return sizeof(blk_q4_K);
+        case ORC_TYPE_Q5_K: return sizeof(blk_q5_K);
         case ORC_TYPE_Q6_K: return sizeof(blk_q6_K);
         case ORC_TYPE_Q8_K: return sizeof(blk_q8_K);
         default: return 0;
@@ -124,7 +134,9 @@ size_t orc_row_size(int type, int64_t ne) {
 int orc_vec_dot_type(int type) {
     switch (type) {
         case ORC_TYPE_Q8_0: return ORC_TYPE_Q8_0;
-        case ORC_TYPE_Q4_K: case ORC_TYPE_Q6_K: return ORC_TYPE_Q8_K;
+        case ORC_TYPE_Q4_K: case ORC_TYPE_Q5_K: case ORC_TYPE_Q6_K: return ORC_TYPE_Q8_K;
+        case ORC_TYPE_F16: return ORC_TYPE_F16;
+        case ORC_TYPE_F32: return ORC_TYPE_F32;
         default: return -1;
     }
 }
@@ -349,6 +361,79 @@ void orc_quantize_row_q4_K(const float *x, void *vy, int64_t k) {
     }
 }
 
+/* ggml-quants.c quantize_row_q5_K_ref: the Q4_K search with 5-bit codes (nmax 31, rmin -0.5, 15 steps); code bit 4
+ * of element l of sub-block j goes to bit j of qh[l]. */
+void orc_quantize_row_q5_K(const float *x, void *vy, int64_t k) {
+    blk_q5_K *y = (blk_q5_K *)vy;
+    uint8_t L[QK_K], Laux[32];
+    float weights[32], mins[QK_K / 32], scales[QK_K / 32];
+    for (int64_t i = 0; i < k / QK_K; i++) {
+        float max_scale = 0, max_min = 0;
+        for (int j = 0; j < QK_K / 32; ++j) {
+            float sum_x2 = 0;
+            for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
+            const float av_x = sqrtf(sum_x2 / 32);
+            for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
+            scales[j] = make_qkx2_quants(32, 31, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, -0.5f, 0.1f, 15, 0);
+            if (scales[j] > max_scale) max_scale = scales[j];
+            if (mins[j] > max_min) max_min = mins[j];
+        }
+        const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+        const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+        for (int j = 0; j < QK_K / 32; ++j) {
+            uint8_t ls = (uint8_t)nearest_int(inv_scale * scales[j]);
+            uint8_t lm = (uint8_t)nearest_int(inv_min * mins[j]);
+            ls = ls < 63 ? ls : 63;
+            lm = lm < 63 ? lm : 63;
+            if (j < 4) {
+                y[i].scales[j] = ls;
+                y[i].scales[j + 4] = lm;
+            } else {
+                y[i].scales[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+                y[i].scales[j - 4] |= (uint8_t)((ls >> 4) << 6);
+                y[i].scales[j - 0] |= (uint8_t)((lm >> 4) << 6);
+            }
+        }
+        y[i].d = FP32_TO_FP16(max_scale / 63.f);
+        y[i].dmin = FP32_TO_FP16(max_min / 63.f);
+        uint8_t sc, m;
+        for (int j = 0; j < QK_K / 32; ++j) {
+            get_scale_min_k4(j, y[i].scales, &sc, &m);
+            const float d = FP16_TO_FP32(y[i].d) * sc;
+            if (!d) continue;
+            const float dm = FP16_TO_FP32(y[i].dmin) * m;
+            for (int ii = 0; ii < 32; ++ii) {
+                int l = nearest_int((x[32 * j + ii] + dm) / d);
+                l = l < 0 ? 0 : (l > 31 ? 31 : l);
+                L[32 * j + ii] = (uint8_t)l;
+            }
+        }
+        uint8_t *qh = y[i].qh;
+        uint8_t *ql = y[i].qs;
+        memset(qh, 0, QK_K / 8);
+        uint8_t m1 = 1, m2 = 2;
+        for (int n = 0; n < QK_K; n += 64) {
+            for (int j = 0; j < 32; ++j) {
+                int l1 = L[n + j];
+                if (l1 > 15) {
+                    l1 -= 16;
+                    qh[j] |= m1;
+                }
+                int l2 = L[n + j + 32];
+                if (l2 > 15) {
+                    l2 -= 16;
+                    qh[j] |= m2;
+                }
+                ql[j] = (uint8_t)(l1 | (l2 << 4));
+            }
+            m1 <<= 2;
+            m2 <<= 2;
+            ql += 32;
+        }
+        x += QK_K;
+    }
+}
+
 /* ggml-quants.c make_qx_quants with rmse_type = 1 and no importance weights (the only form quantize_row_q6_K_ref uses). */
 static float make_qx_quants_rmse1(int n, int nmax, const float *x, int8_t *L) {
     float max = 0, amax = 0;
@@ -452,8 +537,9 @@ void orc_quantize_row_q6_K(const float *x, void *vy, int64_t k) {
     }
 }
 
-/* ggml-quants.c ggml_quantize_chunk with imatrix = NULL: quantize_q8_0 / quantize_q4_K / quantize_q6_K, each of which
- * quantizes the rows with the _ref quantizer. */
+/* ggml-quants.c ggml_quantize_chunk with imatrix = NULL: quantize_q8_0 / quantize_q4_K / quantize_q5_K /
+ * quantize_q6_K, each of which quantizes the rows with the _ref quantizer; F16 rows are converted with
+ * ggml_fp32_to_fp16_row and F32 rows copied. */
 size_t orc_quantize_chunk(int type, const float *src, void *dst, int64_t start, int64_t nrows, int64_t n_per_row) {
     const int64_t b = orc_blck_size(type);
     if (b == 0 || n_per_row % b != 0 || start % n_per_row != 0) return 0;
@@ -464,14 +550,20 @@ size_t orc_quantize_chunk(int type, const float *src, void *dst, int64_t start, 
     switch (type) {
         case ORC_TYPE_Q8_0: orc_quantize_row_q8_0(in, out, n, ORC_ROUND_REF); break;
         case ORC_TYPE_Q4_K: orc_quantize_row_q4_K(in, out, n); break;
+        case ORC_TYPE_Q5_K: orc_quantize_row_q5_K(in, out, n); break;
         case ORC_TYPE_Q6_K: orc_quantize_row_q6_K(in, out, n); break;
+        case ORC_TYPE_F16:
+            for (int64_t j = 0; j < n; j++) ((uint16_t *)out)[j] = FP32_TO_FP16(in[j]);
+            break;
+        case ORC_TYPE_F32: memcpy(out, in, (size_t)n * 4); break;
         default: return 0;
     }
     return (size_t)nrows * row_size;
 }
 
 /* ------------------------------------------------------------------------------------------------------------------
- * Dequantizers: ggml-quants.c dequantize_row_q8_0 / dequantize_row_q4_K / dequantize_row_q6_K.
+ * Dequantizers: ggml-quants.c dequantize_row_q8_0 / dequantize_row_q4_K / dequantize_row_q5_K /
+ * dequantize_row_q6_K; ggml_fp16_to_fp32_row for F16.
  * ---------------------------------------------------------------------------------------------------------------- */
 int orc_dequantize_row(int type, const void *vx, float *y, int64_t k) {
     switch (type) {
@@ -504,6 +596,31 @@ int orc_dequantize_row(int type, const void *vx, float *y, int64_t k) {
             }
             return 0;
         }
+        case ORC_TYPE_Q5_K: {
+            const blk_q5_K *x = (const blk_q5_K *)vx;
+            for (int64_t i = 0; i < k / QK_K; i++) {
+                const uint8_t *ql = x[i].qs;
+                const uint8_t *qh = x[i].qh;
+                const float d = FP16_TO_FP32(x[i].d);
+                const float min = FP16_TO_FP32(x[i].dmin);
+                int is = 0;
+                uint8_t sc, m;
+                uint8_t u1 = 1, u2 = 2;
+                for (int j = 0; j < QK_K; j += 64) {
+                    get_scale_min_k4(is + 0, x[i].scales, &sc, &m);
+                    const float d1 = d * sc, m1 = min * m;
+                    get_scale_min_k4(is + 1, x[i].scales, &sc, &m);
+                    const float d2 = d * sc, m2 = min * m;
+                    for (int l = 0; l < 32; ++l) *y++ = d1 * ((ql[l] & 0xF) + (qh[l] & u1 ? 16 : 0)) - m1;
+                    for (int l = 0; l < 32; ++l) *y++ = d2 * ((ql[l] >> 4) + (qh[l] & u2 ? 16 : 0)) - m2;
+                    ql += 32;
+                    is += 2;
+                    u1 <<= 2;
+                    u2 <<= 2;
+                }
+            }
+            return 0;
+        }
         case ORC_TYPE_Q6_K: {
             const blk_q6_K *x = (const blk_q6_K *)vx;
             for (int64_t i = 0; i < k / QK_K; i++) {
@@ -531,6 +648,9 @@ int orc_dequantize_row(int type, const void *vx, float *y, int64_t k) {
             }
             return 0;
         }
+        case ORC_TYPE_F16:
+            for (int64_t i = 0; i < k; i++) y[i] = FP16_TO_FP32(((const uint16_t *)vx)[i]);
+            return 0;
         case ORC_TYPE_F32:
             memcpy(y, vx, (size_t)k * 4);
             return 0;
@@ -540,7 +660,9 @@ int orc_dequantize_row(int type, const void *vx, float *y, int64_t k) {
 
 /* ------------------------------------------------------------------------------------------------------------------
  * Dot products (ggml-cpu/quants.c generic C: ggml_vec_dot_q8_0_q8_0_generic, ggml_vec_dot_q4_K_q8_K_generic,
- * ggml_vec_dot_q6_K_q8_K_generic). The x86 SIMD variants sum the same exact per-block integers in another fp32 order.
+ * ggml_vec_dot_q5_K_q8_K_generic, ggml_vec_dot_q6_K_q8_K_generic; ggml-cpu/vec.c ggml_vec_dot_f16 / ggml_vec_dot_f32
+ * without SIMD: fp32 products summed in double). The x86 SIMD variants sum the same exact per-block integers (or the
+ * same fp32 products) in another order.
  * ---------------------------------------------------------------------------------------------------------------- */
 
 /* Q4_K: the 8 six-bit scales and mins of a super-block, unpacked (the utmp / kmask shuffle of the generic dot). */
@@ -603,6 +725,65 @@ float orc_vec_dot(int type, int64_t n, const void *vx, const void *vy) {
         for (int l = 0; l < 8; ++l) sumf += sums[l];
         return sumf;
     }
+    if (type == ORC_TYPE_Q5_K) {
+        const blk_q5_K *x = (const blk_q5_K *)vx;
+        const blk_q8_K *y = (const blk_q8_K *)vy;
+        int8_t aux8[QK_K];
+        int16_t aux16[8];
+        float sums[8];
+        int32_t aux32[8];
+        memset(sums, 0, sizeof(sums));
+        float sumf = 0;
+        for (int64_t i = 0; i < n / QK_K; ++i) {
+            const uint8_t *q4 = x[i].qs;
+            const uint8_t *hm = x[i].qh;
+            const int8_t *q8 = y[i].qs;
+            memset(aux32, 0, sizeof(aux32));
+            int8_t *a = aux8;
+            uint8_t m = 1;
+            for (int j = 0; j < QK_K / 64; ++j) {
+                for (int l = 0; l < 32; ++l) a[l] = (int8_t)((q4[l] & 0xF) + (hm[l] & m ? 16 : 0));
+                a += 32;
+                m <<= 1;
+                for (int l = 0; l < 32; ++l) a[l] = (int8_t)((q4[l] >> 4) + (hm[l] & m ? 16 : 0));
+                a += 32;
+                m <<= 1;
+                q4 += 32;
+            }
+            uint8_t scales[8], mins[8];
+            q4k_scales_mins(x[i].scales, scales, mins);
+            int sumi = 0;
+            for (int j = 0; j < QK_K / 16; ++j) sumi += y[i].bsums[j] * mins[j / 2];
+            a = aux8;
+            for (int j = 0; j < QK_K / 32; ++j) {
+                const int32_t scale = scales[j];
+                for (int r = 0; r < 4; r++) {
+                    for (int l = 0; l < 8; ++l) aux16[l] = (int16_t)(q8[l] * a[l]);
+                    for (int l = 0; l < 8; ++l) aux32[l] += scale * aux16[l];
+                    q8 += 8;
+                    a += 8;
+                }
+            }
+            const float d = FP16_TO_FP32(x[i].d) * y[i].d;
+            for (int l = 0; l < 8; ++l) sums[l] += d * aux32[l];
+            const float dmin = FP16_TO_FP32(x[i].dmin) * y[i].d;
+            sumf -= dmin * sumi;
+        }
+        for (int l = 0; l < 8; ++l) sumf += sums[l];
+        return sumf;
+    }
+    if (type == ORC_TYPE_F16) {
+        const uint16_t *x = (const uint16_t *)vx, *y = (const uint16_t *)vy;
+        double sumf = 0.0;
+        for (int64_t i = 0; i < n; ++i) sumf += (double)(FP16_TO_FP32(x[i]) * FP16_TO_FP32(y[i]));
+        return (float)sumf;
+    }
+    if (type == ORC_TYPE_F32) {
+        const float *x = (const float *)vx, *y = (const float *)vy;
+        double sumf = 0.0;
+        for (int64_t i = 0; i < n; ++i) sumf += (double)(x[i] * y[i]);
+        return (float)sumf;
+    }
     if (type == ORC_TYPE_Q6_K) {
         const blk_q6_K *x = (const blk_q6_K *)vx;
         const blk_q8_K *y = (const blk_q8_K *)vy;
@@ -662,23 +843,38 @@ double orc_vec_dot_exact(int type, int64_t n, const void *vx, const void *vy) {
         }
         return acc;
     }
-    if (type == ORC_TYPE_Q4_K || type == ORC_TYPE_Q6_K) {
+    if (type == ORC_TYPE_F16 || type == ORC_TYPE_F32) {
+        for (int64_t i = 0; i < n; ++i)
+            acc += type == ORC_TYPE_F16
+                       ? (double)FP16_TO_FP32(((const uint16_t *)vx)[i]) * (double)FP16_TO_FP32(((const uint16_t *)vy)[i])
+                       : (double)((const float *)vx)[i] * (double)((const float *)vy)[i];
+        return acc;
+    }
+    if (type == ORC_TYPE_Q4_K || type == ORC_TYPE_Q5_K || type == ORC_TYPE_Q6_K) {
         const blk_q8_K *y = (const blk_q8_K *)vy;
         for (int64_t i = 0; i < n / QK_K; ++i) {
             int64_t isum = 0, msum = 0;
-            if (type == ORC_TYPE_Q4_K) {
-                const blk_q4_K *x = (const blk_q4_K *)vx + i;
+            if (type == ORC_TYPE_Q4_K || type == ORC_TYPE_Q5_K) {
+                /* the two types share d, dmin and the packed scales at the start of the block; Q5_K adds bit 4 of
+                 * element l of sub-block j as bit j of qh[l] */
+                const blk_q4_K *x4 = (const blk_q4_K *)vx + i;
+                const blk_q5_K *x5 = (const blk_q5_K *)vx + i;
+                const uint8_t *sc_bytes = type == ORC_TYPE_Q4_K ? x4->scales : x5->scales;
+                const uint8_t *qs = type == ORC_TYPE_Q4_K ? x4->qs : x5->qs;
+                const uint16_t d16 = type == ORC_TYPE_Q4_K ? x4->d : x5->d;
+                const uint16_t dmin16 = type == ORC_TYPE_Q4_K ? x4->dmin : x5->dmin;
                 uint8_t scales[8], mins[8];
-                q4k_scales_mins(x->scales, scales, mins);
+                q4k_scales_mins(sc_bytes, scales, mins);
                 for (int j = 0; j < QK_K; j++) {
                     const int sub = j / 32, chunk = j / 64, pos = j % 32, hi = (j / 32) & 1;
-                    const uint8_t byte = x->qs[chunk * 32 + pos];
-                    const int q = hi ? (byte >> 4) : (byte & 0xF);
+                    const uint8_t byte = qs[chunk * 32 + pos];
+                    int q = hi ? (byte >> 4) : (byte & 0xF);
+                    if (type == ORC_TYPE_Q5_K) q += ((x5->qh[pos] >> sub) & 1) << 4;
                     isum += (int64_t)scales[sub] * q * y[i].qs[j];
                     msum += (int64_t)mins[sub] * y[i].qs[j];
                 }
-                acc += (double)(FP16_TO_FP32(x->d) * y[i].d) * (double)isum -
-                       (double)(FP16_TO_FP32(x->dmin) * y[i].d) * (double)msum;
+                acc += (double)(FP16_TO_FP32(d16) * y[i].d) * (double)isum -
+                       (double)(FP16_TO_FP32(dmin16) * y[i].d) * (double)msum;
             } else {
                 const blk_q6_K *x = (const blk_q6_K *)vx + i;
                 for (int j = 0; j < QK_K; j++) {
@@ -700,9 +896,12 @@ double orc_vec_dot_exact(int type, int64_t n, const void *vx, const void *vy) {
 /* ------------------------------------------------------------------------------------------------------------------
  * Ops. ggml-cpu/ggml-cpu.c ggml_compute_forward_mul_mat / _mul_mat_id / _get_rows, single-threaded.
  * ---------------------------------------------------------------------------------------------------------------- */
+/* src1 rows converted to the weight's vec_dot_type (ggml-cpu.c: type_traits_cpu[vec_dot_type].from_float). */
 static void quantize_act_row(int vdt, const float *x, void *y, int64_t k, int rounding) {
     if (vdt == ORC_TYPE_Q8_0) orc_quantize_row_q8_0(x, y, k, rounding);
-    else orc_quantize_row_q8_K(x, y, k);
+    else if (vdt == ORC_TYPE_Q8_K) orc_quantize_row_q8_K(x, y, k);
+    else if (vdt == ORC_TYPE_F16) for (int64_t i = 0; i < k; i++) ((uint16_t *)y)[i] = FP32_TO_FP16(x[i]);
+    else memcpy(y, x, (size_t)k * 4);
 }
 
 int orc_mul_mat(const orc_tensor *src0, const orc_tensor *src1, orc_tensor *dst, int rounding, int exact) {

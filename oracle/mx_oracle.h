@@ -1,5 +1,5 @@
 /*
- * CPU oracle for the quantized MUL_MAT / MUL_MAT_ID / GET_ROWS path.
+ * CPU oracle for the MUL_MAT / MUL_MAT_ID / GET_ROWS path (Q8_0, Q4_K, Q5_K, Q6_K, F16, F32 weights).
  *
  * TEST INFRASTRUCTURE ONLY. This library is the checker: tests, the smoke check and the CPU-baseline leg of the
  * benchmark may call it; the product (libmx) never links or calls it.
@@ -29,6 +29,7 @@ enum {
     ORC_TYPE_Q8_0 = 8,
     ORC_TYPE_Q8_1 = 9,
     ORC_TYPE_Q4_K = 12,
+    ORC_TYPE_Q5_K = 13,
     ORC_TYPE_Q6_K = 14,
     ORC_TYPE_Q8_K = 15,
     ORC_TYPE_I32 = 26,
@@ -55,6 +56,7 @@ void orc_quantize_row_q8_0(const float *x, void *y, int64_t k, int rounding);
 void orc_quantize_row_q8_1(const float *x, void *y, int64_t k, int rounding);
 void orc_quantize_row_q8_K(const float *x, void *y, int64_t k);
 void orc_quantize_row_q4_K(const float *x, void *y, int64_t k);
+void orc_quantize_row_q5_K(const float *x, void *y, int64_t k);
 void orc_quantize_row_q6_K(const float *x, void *y, int64_t k);
 /* ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row, imatrix = NULL); returns bytes written. */
 size_t orc_quantize_chunk(int type, const float *src, void *dst, int64_t start, int64_t nrows, int64_t n_per_row);

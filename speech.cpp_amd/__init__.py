@@ -19,9 +19,9 @@ HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = HERE / "libmx.so"
 
 # ggml_type values
-F32, F16, Q8_0, Q8_1, Q4_K, Q6_K, Q8_K, I32 = 0, 1, 8, 9, 12, 14, 15, 26
-BLCK = {F32: 1, F16: 1, I32: 1, Q8_0: 32, Q8_1: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
-TSIZE = {F32: 4, F16: 2, I32: 4, Q8_0: 34, Q8_1: 36, Q4_K: 144, Q6_K: 210, Q8_K: 292}
+F32, F16, Q8_0, Q8_1, Q4_K, Q5_K, Q6_K, Q8_K, I32 = 0, 1, 8, 9, 12, 13, 14, 15, 26
+BLCK = {F32: 1, F16: 1, I32: 1, Q8_0: 32, Q8_1: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256}
+TSIZE = {F32: 4, F16: 2, I32: 4, Q8_0: 34, Q8_1: 36, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
 OP_GET_ROWS, OP_MUL_MAT, OP_MUL_MAT_ID, OP_ARGMAX = 1, 2, 3, 4
 ROUND_REF, ROUND_X86 = 0, 1
 SUCCESS, FAILED, ALLOC_FAILED, INVALID, UNSUPPORTED = 0, -1, -2, -3, -4

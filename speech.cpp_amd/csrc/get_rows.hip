@@ -1,6 +1,6 @@
 // GET_ROWS: dst[:, i10, i11, i12] = dequantize(src0[:, ids[i10, i11, i12], i11, i12]) from the planar layout, the
-// arithmetic of ggml-quants.c dequantize_row_{q8_0,q4_K,q6_K} (bit-exact: the same fp32 products in the same order,
-// with no product fused into a subtraction).
+// arithmetic of ggml-quants.c dequantize_row_{q8_0,q4_K,q5_K,q6_K} (bit-exact: the same fp32 products in the same
+// order, with no product fused into a subtraction); F16 rows are widened (ggml_fp16_to_fp32_row), F32 rows copied.
 #include "mx_common.h"
 #include "mx_device.h"
 
@@ -25,18 +25,27 @@ __global__ __launch_bounds__(256) void k_get_rows(GetRowsArgs a) {
     const int64_t K = a.K;
     for (int64_t e = 4 * threadIdx.x; e < K; e += 1024) {
         float o[4];
-        if (TYPE == MX_TYPE_Q8_0) {
+        if (TYPE == MX_TYPE_F32) {
+            const float4 v = *(const float4 *)((const float *)a.w.p0 + row * K + e);
+            o[0] = v.x, o[1] = v.y, o[2] = v.z, o[3] = v.w;
+        } else if (TYPE == MX_TYPE_F16) {
+            const uint2 h = *(const uint2 *)((const uint16_t *)a.w.p0 + row * K + e);
+            o[0] = h2f((uint16_t)(h.x & 0xFFFF)), o[1] = h2f((uint16_t)(h.x >> 16));
+            o[2] = h2f((uint16_t)(h.y & 0xFFFF)), o[3] = h2f((uint16_t)(h.y >> 16));
+        } else if (TYPE == MX_TYPE_Q8_0) {
             const int q4 = *(const int *)(a.w.p0 + row * K + e);
             const float d = h2f(*(const uint16_t *)(a.w.p1 + (row * (K / 32) + e / 32) * 2));
 #pragma unroll
             for (int j = 0; j < 4; j++) o[j] = (float)(int8_t)(q4 >> (8 * j)) * d;
-        } else if (TYPE == MX_TYPE_Q4_K) {
+        } else if (TYPE == MX_TYPE_Q4_K || TYPE == MX_TYPE_Q5_K) {
             const int64_t sb = row * (K / 256) + e / 256;
             const int ie = (int)(e % 256);          // element within the super-block
             const int sub = ie / 32;                // sub-block 0..7
             const int byte = (ie / 64) * 32 + ie % 32;
             const uint32_t q4 = *(const uint32_t *)(a.w.p0 + sb * 128 + byte);
-            const uint8_t *s = a.w.p1 + sb * 12;
+            // Q5_K: bit 4 of element l of sub-block j is bit j of qh[l]; its scales and d|dmin sit one plane later
+            const uint32_t qh = TYPE == MX_TYPE_Q5_K ? *(const uint32_t *)(a.w.p1 + sb * 32 + ie % 32) : 0u;
+            const uint8_t *s = (TYPE == MX_TYPE_Q5_K ? a.w.p2 : a.w.p1) + sb * 12;
             uint8_t sc, m;
             if (sub < 4) {
                 sc = s[sub] & 63;
@@ -45,14 +54,17 @@ __global__ __launch_bounds__(256) void k_get_rows(GetRowsArgs a) {
                 sc = (uint8_t)((s[sub + 4] & 0xF) | ((s[sub - 4] >> 6) << 4));
                 m = (uint8_t)((s[sub + 4] >> 4) | ((s[sub] >> 6) << 4));
             }
-            const uint32_t dm = *(const uint32_t *)(a.w.p2 + sb * 4);
+            const uint32_t dm = *(const uint32_t *)((TYPE == MX_TYPE_Q5_K ? a.w.p3 : a.w.p2) + sb * 4);
             const float d1 = h2f((uint16_t)(dm & 0xFFFF)) * sc;
             const float m1 = h2f((uint16_t)(dm >> 16)) * m;
             const int shift = (ie % 64) < 32 ? 0 : 4;
             {
 #pragma clang fp contract(off)
 #pragma unroll
-                for (int j = 0; j < 4; j++) o[j] = d1 * (float)((q4 >> (8 * j + shift)) & 0xF) - m1;
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t q = ((q4 >> (8 * j + shift)) & 0xF) + (((qh >> (8 * j + sub)) & 1) << 4);
+                    o[j] = d1 * (float)q - m1;
+                }
             }
         } else {
             const int64_t sb = row * (K / 256) + e / 256;
@@ -81,6 +93,9 @@ hipError_t launch_get_rows(const GetRowsArgs &a, hipStream_t s) {
     switch (a.type) {
         case MX_TYPE_Q8_0: hipLaunchKernelGGL(k_get_rows<MX_TYPE_Q8_0>, grid, dim3(256), 0, s, a); break;
         case MX_TYPE_Q4_K: hipLaunchKernelGGL(k_get_rows<MX_TYPE_Q4_K>, grid, dim3(256), 0, s, a); break;
+        case MX_TYPE_Q5_K: hipLaunchKernelGGL(k_get_rows<MX_TYPE_Q5_K>, grid, dim3(256), 0, s, a); break;
+        case MX_TYPE_F16: hipLaunchKernelGGL(k_get_rows<MX_TYPE_F16>, grid, dim3(256), 0, s, a); break;
+        case MX_TYPE_F32: hipLaunchKernelGGL(k_get_rows<MX_TYPE_F32>, grid, dim3(256), 0, s, a); break;
         case MX_TYPE_Q6_K: hipLaunchKernelGGL(k_get_rows<MX_TYPE_Q6_K>, grid, dim3(256), 0, s, a); break;
         default: return hipErrorInvalidValue;
     }

@@ -197,10 +197,12 @@ hipError_t launch_matvec(const MatvecArgs &a, hipStream_t s) {
     int64_t maxN = 0;
     for (int i = 0; i < a.nprob; i++) maxN = a.prob[i].N > maxN ? a.prob[i].N : maxN;
     if (maxN == 0) return hipSuccess;
+    if (a.type == MX_TYPE_F16 || a.type == MX_TYPE_F32) return launch_matvec_f(a, s);
     const size_t lds = act_lds_bytes(a.type, a.K, a.ncols);
     switch (a.type) {
         case MX_TYPE_Q8_0: return launch_type<MX_TYPE_Q8_0>(a, maxN, lds, s);
         case MX_TYPE_Q4_K: return launch_type<MX_TYPE_Q4_K>(a, maxN, lds, s);
+        case MX_TYPE_Q5_K: return launch_type<MX_TYPE_Q5_K>(a, maxN, lds, s);
         case MX_TYPE_Q6_K: return launch_type<MX_TYPE_Q6_K>(a, maxN, lds, s);
         default: return hipErrorInvalidValue;
     }

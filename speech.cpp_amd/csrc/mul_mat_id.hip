@@ -314,6 +314,7 @@ hipError_t launch_mul_mat_id(const MulMatIdArgs &a, hipStream_t s) {
     switch (a.type) {
         case MX_TYPE_Q8_0: return launch_typed<MX_TYPE_Q8_0>(a, s);
         case MX_TYPE_Q4_K: return launch_typed<MX_TYPE_Q4_K>(a, s);
+        case MX_TYPE_Q5_K: return launch_typed<MX_TYPE_Q5_K>(a, s);
         case MX_TYPE_Q6_K: return launch_typed<MX_TYPE_Q6_K>(a, s);
         default: return hipErrorInvalidValue;
     }

@@ -62,7 +62,7 @@ constexpr size_t kMaxLds = 64 * 1024;         // LDS a product kernel may ask fo
 int64_t blck(int type) {
     switch (type) {
         case MX_TYPE_Q8_0: case MX_TYPE_Q8_1: return 32;
-        case MX_TYPE_Q4_K: case MX_TYPE_Q6_K: case MX_TYPE_Q8_K: return 256;
+        case MX_TYPE_Q4_K: case MX_TYPE_Q5_K: case MX_TYPE_Q6_K: case MX_TYPE_Q8_K: return 256;
         case MX_TYPE_F32: case MX_TYPE_F16: case MX_TYPE_I32: return 1;
         default: return 0;
     }
@@ -74,6 +74,7 @@ size_t tsize(int type) {
         case MX_TYPE_Q8_0: return 34;
         case MX_TYPE_Q8_1: return 36;
         case MX_TYPE_Q4_K: return 144;
+        case MX_TYPE_Q5_K: return 176;
         case MX_TYPE_Q6_K: return 210;
         case MX_TYPE_Q8_K: return 292;
         default: return 0;
@@ -111,10 +112,19 @@ bool shape_ok(const mx_tensor *t) {
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
-// A quantized weight this device computes from: Q8_0 / Q4_K / Q6_K, whole blocks, contiguous (the planar layout is a
-// function of type and shape only).
+// A quantized weight this device computes from: Q8_0 / Q4_K / Q5_K / Q6_K, whole blocks, contiguous (the planar
+// layout is a function of type and shape only).
 bool weight_ok(const mx_tensor *w) {
     return w && mx::is_quantized(w->type) && shape_ok(w) && contiguous(w) && w->data && nelements(w) > 0;
+}
+
+// An F16 / F32 weight for MUL_MAT and GET_ROWS: contiguous ggml rows read with 16-byte loads (rows of a multiple of
+// 8 halves or 4 floats, 16-byte aligned data).
+bool float_weight_ok(const mx_tensor *w) {
+    if (!w || (w->type != MX_TYPE_F16 && w->type != MX_TYPE_F32) || !shape_ok(w) || !contiguous(w) || !w->data ||
+        nelements(w) == 0 || !aligned16(w->data))
+        return false;
+    return w->ne[0] % (w->type == MX_TYPE_F16 ? 8 : 4) == 0;
 }
 
 // F32 activations read with 16-byte loads: contiguous rows, 16-byte aligned rows and slices.
@@ -380,7 +390,8 @@ MX_API int mx_supports_op(int op, const mx_tensor *src0, const mx_tensor *src1, 
         return dst && dst->type == MX_TYPE_I32 && shape_ok(dst) && dst->nb[0] == 4 && dst->ne[0] == src0->ne[1] &&
                dst->ne[1] == 1 && dst->ne[2] == 1 && dst->ne[3] == 1 && dst->data && ((uintptr_t)dst->data & 3) == 0;
     }
-    if (!weight_ok(src0) || !dst || dst->type != MX_TYPE_F32 || !shape_ok(dst) || dst->nb[0] != 4) return 0;
+    const bool fw = op != MX_OP_MUL_MAT_ID && float_weight_ok(src0);  // routed experts are quantized
+    if (!(weight_ok(src0) || fw) || !dst || dst->type != MX_TYPE_F32 || !shape_ok(dst) || dst->nb[0] != 4) return 0;
     const int64_t K = src0->ne[0];
     switch (op) {
         case MX_OP_GET_ROWS: {

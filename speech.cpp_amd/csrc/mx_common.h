@@ -17,13 +17,15 @@ constexpr size_t PLANE_ALIGN = 256;
 // Device layout of a quantized tensor.
 //
 // ggml stores a tensor as an array of blocks (ggml-common.h): block_q8_0 {d, qs[32]} (34 B), block_q4_K {d, dmin,
-// scales[12], qs[128]} (144 B), block_q6_K {ql[128], qh[64], scales[16], d} (210 B). On this device each field becomes a
+// scales[12], qs[128]} (144 B), block_q5_K {d, dmin, scales[12], qh[32], qs[128]} (176 B), block_q6_K {ql[128],
+// qh[64], scales[16], d} (210 B). On this device each field becomes a
 // plane of its own: plane p holds that field of block 0, block 1, ... back to back, and each plane starts on a
 // 256-byte boundary. Blocks are numbered in ggml order (row-major over all rows of all matrices), so a row's quants
 // are contiguous and 16-byte aligned, which is what wide coalesced loads and MFMA tiles want.
 //
 //   Q8_0: plane 0 qs (32 B/block), plane 1 d (2 B/block)
 //   Q4_K: plane 0 qs (128 B/block), plane 1 scales (12 B/block), plane 2 d,dmin (4 B/block)
+//   Q5_K: plane 0 qs (128 B/block), plane 1 qh (32 B/block), plane 2 scales (12 B/block), plane 3 d,dmin (4 B/block)
 //   Q6_K: plane 0 ql (128 B/block), plane 1 qh (64 B/block), plane 2 scales (16 B/block), plane 3 d (2 B/block)
 //
 // The map from a byte of ggml's block to (plane, byte in plane) is a permutation, so a partial upload of ggml bytes at
@@ -44,20 +46,24 @@ struct TypeInfo {
 };
 
 inline const TypeInfo *type_info(int type) {
-    // Field order within ggml's structs: block_q8_0 {d, qs}; block_q4_K {d, dmin, scales, qs}; block_q6_K {ql, qh,
-    // scales, d}.
+    // Field order within ggml's structs: block_q8_0 {d, qs}; block_q4_K {d, dmin, scales, qs}; block_q5_K {d, dmin,
+    // scales, qh, qs}; block_q6_K {ql, qh, scales, d}.
     static const TypeInfo q8_0 = {MX_TYPE_Q8_0, 32, 34, 2, {{0, 2, 1}, {2, 32, 0}, {0, 0, 0}, {0, 0, 0}}};
     static const TypeInfo q4_k = {MX_TYPE_Q4_K, 256, 144, 3, {{0, 4, 2}, {4, 12, 1}, {16, 128, 0}, {0, 0, 0}}};
+    static const TypeInfo q5_k = {MX_TYPE_Q5_K, 256, 176, 4, {{0, 4, 3}, {4, 12, 2}, {16, 32, 1}, {48, 128, 0}}};
     static const TypeInfo q6_k = {MX_TYPE_Q6_K, 256, 210, 4, {{0, 128, 0}, {128, 64, 1}, {192, 16, 2}, {208, 2, 3}}};
     switch (type) {
         case MX_TYPE_Q8_0: return &q8_0;
         case MX_TYPE_Q4_K: return &q4_k;
+        case MX_TYPE_Q5_K: return &q5_k;
         case MX_TYPE_Q6_K: return &q6_k;
         default: return nullptr;
     }
 }
 
-inline bool is_quantized(int type) { return type == MX_TYPE_Q8_0 || type == MX_TYPE_Q4_K || type == MX_TYPE_Q6_K; }
+inline bool is_quantized(int type) {
+    return type == MX_TYPE_Q8_0 || type == MX_TYPE_Q4_K || type == MX_TYPE_Q5_K || type == MX_TYPE_Q6_K;
+}
 
 struct Planes {
     int n = 0;
@@ -166,6 +172,9 @@ struct MatvecArgs {
     int *err;
 };
 hipError_t launch_matvec(const MatvecArgs &a, hipStream_t s);
+// The same products on F16 / F32 weights in ggml's row-major layout (prob[i].w.p0 = the weight's data; K % 8 == 0 for
+// F16, K % 4 == 0 for F32; no ids mode).
+hipError_t launch_matvec_f(const MatvecArgs &a, hipStream_t s);
 
 // Prefill GEMM (M > 8): activations quantized once into scratch (gemm_act_bytes of quants, int8 or fp16 values by
 // gemm_mode(), plus M * K/32 fp32 block scales), then MFMA tiles.

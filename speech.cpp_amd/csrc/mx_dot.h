@@ -1,7 +1,7 @@
 // Per-chunk dot products of one weight row (planar layout) with up to NC quantized activation columns held in LDS.
 //
 // The integer part of every product is exact (v_dot4 over int8, int32 sums); scales are applied in fp32 as ggml's
-// CPU dots apply them (ggml-cpu/quants.c ggml_vec_dot_q8_0_q8_0 / _q4_K_q8_K / _q6_K_q8_K): d_w * d_x formed in fp32,
+// CPU dots apply them (ggml-cpu/quants.c ggml_vec_dot_q8_0_q8_0 / _q4_K_q8_K / _q5_K_q8_K / _q6_K_q8_K): d_w * d_x formed in fp32,
 // then times the exact integer sum. Only the order of the fp32 cross-block sum differs from the CPU.
 //
 // Activations in LDS, column c:
@@ -59,6 +59,13 @@ struct WChunk<MX_TYPE_Q4_K> {
     uint32_t dm;   // fp16 d | fp16 dmin << 16
 };
 template <>
+struct WChunk<MX_TYPE_Q5_K> {
+    int4 q;        // low 4 bits of 32 codes: 16 of sub-block j, 16 of sub-block j + 1
+    int4 qh;       // the 16 qh bytes of the same positions (bit j: bit 4 of sub-block j's code)
+    uint32_t s0, s1, s2;  // the 12 packed scale / min bytes
+    uint32_t dm;   // fp16 d | fp16 dmin << 16
+};
+template <>
 struct WChunk<MX_TYPE_Q6_K> {
     int4 ql, qh;
     uint32_t sc;   // the two int8 sub-block scales in bytes 0 and 1
@@ -79,6 +86,15 @@ __device__ __forceinline__ WChunk<TYPE> load_chunk(const WPlanes &w, int64_t gro
         r.s1 = sp[1];
         r.s2 = sp[2];
         r.dm = *(const uint32_t *)(w.p2 + blk * 4);
+    } else if constexpr (TYPE == MX_TYPE_Q5_K) {
+        const int64_t blk = grow * (K / 256) + (c >> 3);
+        r.q = *(const int4 *)(w.p0 + blk * 128 + 16 * (c & 7));
+        r.qh = *(const int4 *)(w.p1 + blk * 32 + 16 * (c & 1));
+        const uint32_t *sp = (const uint32_t *)(w.p2 + blk * 12);
+        r.s0 = sp[0];
+        r.s1 = sp[1];
+        r.s2 = sp[2];
+        r.dm = *(const uint32_t *)(w.p3 + blk * 4);
     } else {
         const int64_t blk = grow * (K / 256) + (c >> 3);
         const int t = c & 7, h = t >> 2, u = t & 3;
@@ -106,7 +122,7 @@ __device__ __forceinline__ void dot_chunk(const WChunk<TYPE> &wc, int64_t K, int
             const int s = dot16(wc.q, xv, 0);
             acc[col] += (float)s * (dw * xd[col * nblk + (c >> 1)]);
         }
-    } else if constexpr (TYPE == MX_TYPE_Q4_K) {
+    } else if constexpr (TYPE == MX_TYPE_Q4_K || TYPE == MX_TYPE_Q5_K) {
         const int64_t nsb = K / 256;
         const int sb = c >> 3, t = c & 7;
         const float d = h2f((uint16_t)(wc.dm & 0xFFFF)), dmin = h2f((uint16_t)(wc.dm >> 16));
@@ -115,9 +131,20 @@ __device__ __forceinline__ void dot_chunk(const WChunk<TYPE> &wc, int64_t K, int
         q4k_scale_min(wc.s0, wc.s1, wc.s2, jlo, sc_lo, m_lo);
         q4k_scale_min(wc.s0, wc.s1, wc.s2, jlo + 1, sc_hi, m_hi);
         const int4 q = wc.q;
-        const int4 qlo = make_int4(q.x & 0x0F0F0F0F, q.y & 0x0F0F0F0F, q.z & 0x0F0F0F0F, q.w & 0x0F0F0F0F);
-        const int4 qhi = make_int4((q.x >> 4) & 0x0F0F0F0F, (q.y >> 4) & 0x0F0F0F0F, (q.z >> 4) & 0x0F0F0F0F,
-                                   (q.w >> 4) & 0x0F0F0F0F);
+        int4 qlo = make_int4(q.x & 0x0F0F0F0F, q.y & 0x0F0F0F0F, q.z & 0x0F0F0F0F, q.w & 0x0F0F0F0F);
+        int4 qhi = make_int4((q.x >> 4) & 0x0F0F0F0F, (q.y >> 4) & 0x0F0F0F0F, (q.z >> 4) & 0x0F0F0F0F,
+                             (q.w >> 4) & 0x0F0F0F0F);
+        if constexpr (TYPE == MX_TYPE_Q5_K) {  // codes 0..31: bit 4 of sub-block j sits in bit j of each qh byte
+            const int4 h = wc.qh;
+            qlo.x |= ((h.x >> jlo) & 0x01010101) << 4;
+            qlo.y |= ((h.y >> jlo) & 0x01010101) << 4;
+            qlo.z |= ((h.z >> jlo) & 0x01010101) << 4;
+            qlo.w |= ((h.w >> jlo) & 0x01010101) << 4;
+            qhi.x |= ((h.x >> (jlo + 1)) & 0x01010101) << 4;
+            qhi.y |= ((h.y >> (jlo + 1)) & 0x01010101) << 4;
+            qhi.z |= ((h.z >> (jlo + 1)) & 0x01010101) << 4;
+            qhi.w |= ((h.w >> (jlo + 1)) & 0x01010101) << 4;
+        }
         const int lo_off = sb * 256 + 64 * (t >> 1) + 16 * (t & 1);
 #pragma unroll
         for (int col = 0; col < NC; col++) {
@@ -172,6 +199,7 @@ __device__ __forceinline__ void chunk_dot(const WPlanes &w, int64_t grow, int64_
 
 // LDS bytes the activations of `ncols` columns take.
 __host__ __device__ inline size_t act_lds_bytes(int type, int64_t K, int ncols) {
+    if (type == MX_TYPE_F16 || type == MX_TYPE_F32) return (size_t)ncols * (size_t)K * 4;  // fp32 (or fp16-rounded)
     if (type == MX_TYPE_Q8_0) return (size_t)ncols * (size_t)K + (size_t)ncols * (size_t)(K / 32) * 4;
     return (size_t)ncols * (size_t)K + (size_t)ncols * (size_t)(K / 256) * 4 + (size_t)ncols * (size_t)(K / 16) * 4;
 }

@@ -1,7 +1,7 @@
 // Host-side weight quantization: ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row, imatrix = NULL), the
 // path `speech quantize` takes (src/common/quantize.cpp:164-182), which with no importance matrix runs ggml-quants.c's
-// reference quantizers quantize_row_q8_0_ref / quantize_row_q4_K_ref / quantize_row_q6_K_ref. Also the seeded
-// synthetic generator used for weights and activations.
+// reference quantizers quantize_row_q8_0_ref / quantize_row_q4_K_ref / quantize_row_q5_K_ref / quantize_row_q6_K_ref
+// (F16 rows are converted, F32 rows copied). Also the seeded synthetic generator used for weights and activations.
 //
 // Compiled without FMA contraction (see the Makefile) so every product is rounded before it is summed, as in ggml-base,
 // which is built for the x86-64 baseline ISA.
@@ -68,11 +68,13 @@ void q8_0_block(const float *x, uint8_t *out) {
     for (int j = 0; j < 32; j++) out[2 + j] = (uint8_t)(int8_t)std::round(x[j] * id);
 }
 
-// make_qkx2_quants(n = 32, nmax = 15, rmin = -1, rdelta = 0.1, nstep = 20, use_mad = false): codes L[] and the
-// (scale, -min) pair of the asymmetric 4-bit fit with the least weighted squared error over 21 candidate scales.
-float fit_asym15(const float *x, const float *w, uint8_t *L, float *neg_min) {
-    constexpr int n = 32, nmax = 15, nstep = 20;
-    constexpr float rmin = -1.0f, rdelta = 0.1f;
+// make_qkx2_quants(n = 32, nmax, rmin, rdelta = 0.1, nstep, use_mad = false): codes L[] and the (scale, -min) pair of
+// the asymmetric fit with the least weighted squared error over nstep + 1 candidate scales. Q4_K fits with nmax = 15,
+// rmin = -1, nstep = 20; Q5_K with nmax = 31, rmin = -0.5, nstep = 15.
+template <int nmax, int nstep>
+float fit_asym(const float *x, const float *w, uint8_t *L, float *neg_min, float rmin) {
+    constexpr int n = 32;
+    constexpr float rdelta = 0.1f;
     float lo = x[0], hi = x[0], sw = w[0], sx = w[0] * x[0];
     for (int i = 1; i < n; i++) {
         if (x[i] < lo) lo = x[i];
@@ -141,9 +143,11 @@ void q4k_unpack(const uint8_t *s, int j, int &sc, int &m) {
     }
 }
 
-// quantize_row_q4_K_ref over one super-block: block_q4_K {fp16 d, dmin; uint8 scales[12]; uint8 qs[128]}.
-void q4_K_block(const float *x, uint8_t *out) {
-    std::array<uint8_t, 256> L{};
+// The shared first half of quantize_row_q4_K_ref / _q5_K_ref on one super-block: per 32-element sub-block an
+// asymmetric fit with NMAX + 1 levels, then the eight (scale, min) pairs as 6-bit integers against fp16 d and dmin,
+// written to out[0..15] (d, dmin, packed scales); returns the codes of the final rounding in L.
+template <int NMAX, int NSTEP>
+void k_scales_and_codes(const float *x, uint8_t *out, float rmin, std::array<uint8_t, 256> &L) {
     std::array<float, 8> scales{}, mins{};
     float wts[32];
     float max_scale = 0, max_min = 0;
@@ -153,7 +157,7 @@ void q4_K_block(const float *x, uint8_t *out) {
         for (int l = 0; l < 32; l++) s2 += xs[l] * xs[l];
         const float av = std::sqrt(s2 / 32);
         for (int l = 0; l < 32; l++) wts[l] = av + std::fabs(xs[l]);
-        scales[j] = fit_asym15(xs, wts, L.data() + 32 * j, &mins[j]);
+        scales[j] = fit_asym<NMAX, NSTEP>(xs, wts, L.data() + 32 * j, &mins[j], rmin);
         if (scales[j] > max_scale) max_scale = scales[j];
         if (mins[j] > max_min) max_min = mins[j];
     }
@@ -181,12 +185,36 @@ void q4_K_block(const float *x, uint8_t *out) {
         const float d = from_half(hd) * sc;
         if (d == 0.0f) continue;
         const float dm = from_half(hm) * m;
-        for (int i = 0; i < 32; i++) L[32 * j + i] = (uint8_t)std::clamp(rne((x[32 * j + i] + dm) / d), 0, 15);
+        for (int i = 0; i < 32; i++) L[32 * j + i] = (uint8_t)std::clamp(rne((x[32 * j + i] + dm) / d), 0, NMAX);
     }
+}
+
+// quantize_row_q4_K_ref over one super-block: block_q4_K {fp16 d, dmin; uint8 scales[12]; uint8 qs[128]}.
+void q4_K_block(const float *x, uint8_t *out) {
+    std::array<uint8_t, 256> L{};
+    k_scales_and_codes<15, 20>(x, out, -1.0f, L);
     uint8_t *qs = out + 16;
     for (int c = 0; c < 4; c++)
         for (int l = 0; l < 32; l++) qs[32 * c + l] = (uint8_t)(L[64 * c + l] | (L[64 * c + 32 + l] << 4));
 }
+
+// quantize_row_q5_K_ref over one super-block: block_q5_K {fp16 d, dmin; uint8 scales[12]; uint8 qh[32]; qs[128]}.
+// The low 4 bits of each code go to qs as in Q4_K; bit 4 of element l of sub-block j goes to bit j of qh[l].
+void q5_K_block(const float *x, uint8_t *out) {
+    std::array<uint8_t, 256> L{};
+    k_scales_and_codes<31, 15>(x, out, -0.5f, L);
+    uint8_t *qh = out + 16, *qs = out + 48;
+    std::memset(qh, 0, 32);
+    for (int c = 0; c < 4; c++)
+        for (int l = 0; l < 32; l++) {
+            const int lo = L[64 * c + l], hi = L[64 * c + 32 + l];
+            qs[32 * c + l] = (uint8_t)((lo & 0xF) | ((hi & 0xF) << 4));
+            qh[l] |= (uint8_t)(((lo >> 4) << (2 * c)) | ((hi >> 4) << (2 * c + 1)));
+        }
+}
+
+void f16_block(const float *x, uint8_t *out) { put16(out, to_half(*x)); }
+void f32_block(const float *x, uint8_t *out) { std::memcpy(out, x, 4); }
 
 // make_qx_quants(n = 16, nmax = 32, rmse_type = 1, no weights): symmetric 6-bit fit weighted by x^2, searched over
 // 19 scales; writes codes l + 32 to L and returns the scale.
@@ -279,7 +307,10 @@ bool geometry(int type, Geometry &g) {
     switch (type) {
         case MX_TYPE_Q8_0: g = {32, 34, q8_0_block}; return true;
         case MX_TYPE_Q4_K: g = {256, 144, q4_K_block}; return true;
+        case MX_TYPE_Q5_K: g = {256, 176, q5_K_block}; return true;
         case MX_TYPE_Q6_K: g = {256, 210, q6_K_block}; return true;
+        case MX_TYPE_F16: g = {1, 2, f16_block}; return true;
+        case MX_TYPE_F32: g = {1, 4, f32_block}; return true;
         default: return false;
     }
 }

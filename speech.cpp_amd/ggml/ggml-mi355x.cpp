@@ -374,8 +374,9 @@ bool in_our_buffer(const ggml_tensor *t, ggml_backend_dev_t dev) {
     return t && t->buffer && t->buffer->buft == dev_get_buffer_type(dev);
 }
 
-// True exactly for MUL_MAT / MUL_MAT_ID / GET_ROWS whose quantized weight (Q8_0, Q4_K, Q6_K) lives in this device's
-// buffer type, and for ARGMAX over f32 logits in it (the greedy pick after the head, qwen3-decoder.cpp:428,501), with
+// True exactly for MUL_MAT / MUL_MAT_ID / GET_ROWS whose weight lives in this device's buffer type -- Q8_0, Q4_K,
+// Q5_K, Q6_K for all three; F16 / F32 (the storages of storage.cpp:52-89 besides the K-quants) for MUL_MAT and
+// GET_ROWS -- and for ARGMAX over f32 logits in it (the greedy pick after the head, qwen3-decoder.cpp:428,501), with
 // the shapes and strides libmx computes; everything else stays on the CPU backend.
 bool dev_supports_op(ggml_backend_dev_t dev, const ggml_tensor *op) {
     if (op->op == GGML_OP_ARGMAX) {

@@ -11,6 +11,8 @@ layouts of ggml-common.h and from inputs for which every quantizer's result is f
   q4_K_grid.json    a super-block whose every 32-value sub-block lies on an exact grid d*sc_j*l - dmin*m_j with
                     l in 0..15 all present and max sc = max m = 63: any least-squares fit lands on the grid, so the
                     block is d = 2^-10, dmin = 2^-11, the given 6-bit scales/mins and codes l.
+  q5_K_grid.json    the Q4_K construction with 5-bit codes: every 32-value sub-block holds each l in 0..31 once, on
+                    d*sc_j*l - dmin*m_j; codes split into nibbles (qs) and bit 4 (bit j of qh[l]).
   q6_K_grid.json    a super-block whose 16-value sub-blocks lie on D*k_j*q with q in -32..31, q = -32 present and
                     max k = 128: the block is d = -D, scales = -k_j, codes q + 32.
 
@@ -102,6 +104,34 @@ def q4_K_grid():
     return {"x": x32.tolist(), "block": hexs(blk), "dequant": x32.tolist(), "sc": sc, "m": m}
 
 
+def q5_K_grid():
+    d, dmin = 2.0 ** -10, 2.0 ** -11
+    sc = [17, 63, 40, 2, 33, 63, 9, 58]
+    m = [63, 0, 12, 45, 63, 3, 28, 51]
+    rng = np.random.default_rng(5005)
+    L = np.zeros(256, np.int64)
+    x = np.zeros(256, np.float64)
+    for j in range(8):
+        l = rng.permutation(32)   # every level once: the fit has no freedom left
+        L[32 * j:32 * j + 32] = l
+        x[32 * j:32 * j + 32] = d * sc[j] * l - dmin * m[j]
+    x32 = x.astype(np.float32)
+    assert np.array_equal(x32.astype(np.float64), x)
+    # qs: byte 32c + i holds the low 4 bits of elements 64c + i (low nibble) and 64c + 32 + i (high nibble);
+    # qh[i] bit j holds bit 4 of element 32j + i
+    qs = bytearray(128)
+    qh = bytearray(32)
+    for c in range(4):
+        for i in range(32):
+            qs[32 * c + i] = (int(L[64 * c + i]) & 0xF) | ((int(L[64 * c + 32 + i]) & 0xF) << 4)
+    for j in range(8):
+        for i in range(32):
+            qh[i] |= ((int(L[32 * j + i]) >> 4) & 1) << j
+    blk = (f16_bits(d).to_bytes(2, "little") + f16_bits(dmin).to_bytes(2, "little") + pack_q4_K_scales(sc, m) +
+           bytes(qh) + bytes(qs))
+    return {"x": x32.tolist(), "block": hexs(blk), "dequant": x32.tolist(), "sc": sc, "m": m}
+
+
 def q6_K_grid():
     D = 2.0 ** -12
     k = [128, 100, 64, 37, 1, 90, 128, 12, 77, 50, 3, 127, 64, 99, 20, 45]
@@ -136,6 +166,7 @@ def main():
         "q8_ties.json": q8_ties(),
         "q8_K_ties.json": q8_K_ties(),
         "q4_K_grid.json": q4_K_grid(),
+        "q5_K_grid.json": q5_K_grid(),
         "q6_K_grid.json": q6_K_grid(),
     }
     for name, data in fixtures.items():

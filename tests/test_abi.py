@@ -44,7 +44,7 @@ def test_no_device_is_reported_cleanly_without_gpu(mx):
 
 
 def test_alloc_size_covers_every_plane(mx):
-    for t, K, N in [(mx.Q8_0, 1024, 3), (mx.Q4_K, 2048, 5), (mx.Q6_K, 6144, 7), (mx.Q6_K, 256, 1)]:
+    for t, K, N in [(mx.Q8_0, 1024, 3), (mx.Q4_K, 2048, 5), (mx.Q5_K, 1536, 3), (mx.Q6_K, 6144, 7), (mx.Q6_K, 256, 1)]:
         d = mx.MxTensor()
         d.type = t
         for i, v in enumerate((K, N, 1, 1)):
@@ -58,7 +58,7 @@ def test_alloc_size_covers_every_plane(mx):
         assert size % 256 == 0
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K])
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_F16, O.TYPE_F32])
 def test_host_quantizer_matches_oracle(mx, t):
     rng = np.random.default_rng(7 + t)
     for std in (0.02, 1.0, 3e-5):
@@ -77,7 +77,8 @@ def test_generator_matches_oracle(mx):
     assert np.array_equal(q, O.quantize_chunk(O.TYPE_Q6_K, O.fill_normal(99, 16, 512, 0.0, 0.02)))
 
 
-@pytest.mark.parametrize("name,t", [("q4_K_grid.json", O.TYPE_Q4_K), ("q6_K_grid.json", O.TYPE_Q6_K)])
+@pytest.mark.parametrize("name,t", [("q4_K_grid.json", O.TYPE_Q4_K), ("q5_K_grid.json", O.TYPE_Q5_K),
+                                    ("q6_K_grid.json", O.TYPE_Q6_K)])
 def test_host_quantizer_known_answer_blocks(mx, name, t):
     import json
     f = json.loads((ROOT / "tests" / "golden" / name).read_text())
@@ -115,3 +116,41 @@ def test_supports_op_argmax(mx):
     assert L.mx_supports_op(mx.OP_ARGMAX, src, None, None, short_dst) == 0
     q = desc(mx.Q8_0, (1024, 2, 1, 1), (34, 1088, 2176, 2176))
     assert L.mx_supports_op(mx.OP_ARGMAX, q, None, None, dst) == 0
+
+
+def desc_contig(mx, t, ne, data=0x10000):
+    d = mx.MxTensor()
+    d.type = t
+    nb = mx.contiguous_nb(t, ne)
+    for i in range(4):
+        d.ne[i] = ne[i]
+        d.nb[i] = nb[i]
+    d.data = data
+    return d
+
+
+def test_supports_op_weight_types(mx):
+    """Q5_K joins the quantized weights on every op; F16 / F32 weights take MUL_MAT and GET_ROWS (rows of whole
+    16-byte loads) but not MUL_MAT_ID, whose experts are quantized (host logic only)."""
+    L = mx.lib()
+    ok = lambda op, a, b, c, d: L.mx_supports_op(op, a, b, c, d) != 0
+    for t, K in [(mx.Q5_K, 512), (mx.F16, 1000), (mx.F32, 1004)]:
+        W = desc_contig(mx, t, (K, 48, 1, 1))
+        X = desc_contig(mx, mx.F32, (K, 3, 1, 1))
+        Y = desc_contig(mx, mx.F32, (48, 3, 1, 1))
+        assert ok(mx.OP_MUL_MAT, W, X, None, Y)
+        I = desc_contig(mx, mx.I32, (5, 1, 1, 1))
+        G = desc_contig(mx, mx.F32, (K, 5, 1, 1))
+        assert ok(mx.OP_GET_ROWS, W, I, None, G)
+        E = desc_contig(mx, t, (K, 48, 4, 1))
+        B = desc_contig(mx, mx.F32, (K, 1, 6, 1))
+        ids = desc_contig(mx, mx.I32, (2, 6, 1, 1))
+        D = desc_contig(mx, mx.F32, (48, 2, 6, 1))
+        assert ok(mx.OP_MUL_MAT_ID, E, B, ids, D) == (t == mx.Q5_K)
+    # F16 rows must hold whole 8-element loads, F32 rows whole 4-element ones
+    W = desc_contig(mx, mx.F16, (1004, 8, 1, 1))
+    X = desc_contig(mx, mx.F32, (1004, 1, 1, 1))
+    Y = desc_contig(mx, mx.F32, (8, 1, 1, 1))
+    assert not ok(mx.OP_MUL_MAT, W, X, None, Y)
+    W = desc_contig(mx, mx.F32, (1004, 8, 1, 1), data=0x10008)   # data not 16-byte aligned
+    assert not ok(mx.OP_MUL_MAT, W, X, None, Y)

@@ -35,8 +35,10 @@ def check_product(t, w, x, y, K, rounding=O.ROUND_REF):
         assert rel_err(y, dq_model(O, t, w, x, K, rounding)) <= TIGHT
     else:
         assert rel_err(y, y_ref) <= TIGHT
-QTYPES = [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K]
-NAMES = {O.TYPE_Q8_0: "q8_0", O.TYPE_Q4_K: "q4_K", O.TYPE_Q6_K: "q6_K"}
+QTYPES = [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K]
+FTYPES = [O.TYPE_F16, O.TYPE_F32]
+NAMES = {O.TYPE_Q8_0: "q8_0", O.TYPE_Q4_K: "q4_K", O.TYPE_Q5_K: "q5_K", O.TYPE_Q6_K: "q6_K", O.TYPE_F16: "f16",
+         O.TYPE_F32: "f32"}
 
 
 def weights(t, N, K, seed, std=0.02):
@@ -253,7 +255,10 @@ def test_supports_op(mx, be):
     Xbad = be.tensor(mx.F32, (W.ne[0] - 256, 1))
     assert not be.supports(mx.OP_MUL_MAT, W, Xbad, None, Y)
     F = be.tensor(mx.F32, (W.ne[0], 4))
-    assert not be.supports(mx.OP_MUL_MAT, F, X, None, Y)   # F32 weights stay on the CPU backend
+    assert be.supports(mx.OP_MUL_MAT, F, X, None, Y)       # F32 weights: the float mat-vec
+    H = be.tensor(mx.F16, (W.ne[0] - 4, 4))
+    Xh = be.tensor(mx.F32, (W.ne[0] - 4, 1))
+    assert not be.supports(mx.OP_MUL_MAT, H, Xh, None, Y)  # F16 rows of whole 8-element loads only
 
 
 # --------------------------------------------------------------------------------------------------- MUL_MAT_ID
@@ -380,7 +385,7 @@ def test_mul_mat_gemm_batched(mx, be):
         check_product(t, wm, x[0, i2], y[0, i2], K)
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
 @pytest.mark.parametrize("M,N,K", [(9, 100, 1024), (64, 256, 2048), (130, 333, 1536), (512, 1024, 3072),
                                    (100, 64, 6144)])
 def test_mul_mat_gemm_kquant(mx, be, t, M, N, K):
@@ -431,6 +436,58 @@ def test_mul_mat_gemm_kquant_group(mx, be, t):
     be.sync()
     for n, wi, Yi in zip(Ns, w, Y):
         assert rel_err(Yi.numpy().reshape(M, n), O.mul_mat(t, wi, x)) <= TIGHT
+
+
+# ------------------------------------------------------------------------------------------- F16 / F32 weights
+@pytest.mark.parametrize("t", FTYPES, ids=lambda t: NAMES[t])
+def test_float_get_rows_bit_exact(mx, be, t):
+    K, R = 1000, 40
+    table = weights(t, R, K, 0x5EED1000 + t, std=1.0)
+    ids = np.array([39, 0, 7, 7, 12], np.int32)
+    T = be.tensor(t, (K, R), table)
+    I = be.tensor(mx.I32, (len(ids),), ids)
+    D = be.tensor(mx.F32, (K, len(ids)))
+    be.get_rows(T, I, D)
+    be.sync()
+    assert bits_equal(D.numpy().reshape(len(ids), K), O.get_rows(t, table, K, ids))
+
+
+@pytest.mark.parametrize("t", FTYPES, ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("M,K", [(1, 64), (1, 4096), (3, 1000), (8, 2048), (20, 1024)])
+def test_float_mul_mat(mx, be, t, M, K):
+    """ggml-cpu's F16 product rounds src1 to fp16 first; F32 takes it as it is. Missing that rounding would show as
+    ~2e-4 of the row's largest output, ten times the bar held here."""
+    N = 203
+    w = weights(t, N, K, 0x5EED1100 + K + t)
+    x = acts(0xAC701100 + M, M, K)
+    y = run_mul_mat(mx, be, t, w, x, K, N)
+    assert rel_err(y, O.mul_mat(t, w, x)) <= TIGHT
+    assert rel_err(y, O.mul_mat(t, w, x, exact=True)) <= TIGHT
+
+
+@pytest.mark.parametrize("t", FTYPES, ids=lambda t: NAMES[t])
+def test_float_mul_mat_batched_group(mx, be, t):
+    """Broadcast batches (ne12 = 2 ne02) and a two-weight group sharing src1."""
+    K, N, M = 512, 72, 2
+    w = weights(t, N * 2, K, 0x5EED1200 + t)
+    x = acts(0xAC701200, M * 4, K).reshape(1, 4, M, K)
+    W = be.tensor(t, (K, N, 2, 1), w)
+    X = be.tensor(mx.F32, (K, M, 4, 1), x)
+    Y = be.tensor(mx.F32, (N, M, 4, 1))
+    be.mul_mat(W, X, Y)
+    be.sync()
+    y = Y.numpy()
+    for i2 in range(4):
+        wm = w[(i2 // 2) * N:(i2 // 2 + 1) * N]
+        assert rel_err(y[0, i2], O.mul_mat(t, wm, x[0, i2])) <= TIGHT
+    ws = [weights(t, n, K, 0x5EED1300 + n + t) for n in (96, 40)]
+    Wg = [be.tensor(t, (K, n), wi) for n, wi in zip((96, 40), ws)]
+    Xg = be.tensor(mx.F32, (K, 3), x.reshape(-1, K)[:3])
+    Yg = [be.tensor(mx.F32, (n, 3)) for n in (96, 40)]
+    be.mul_mat_group(Wg, Xg, Yg)
+    be.sync()
+    for n, wi, Yi in zip((96, 40), ws, Yg):
+        assert rel_err(Yi.numpy().reshape(3, n), O.mul_mat(t, wi, x.reshape(-1, K)[:3])) <= TIGHT
 
 
 # ------------------------------------------------------------------------------------------------------------ ARGMAX

@@ -57,6 +57,29 @@ def decode(t, blocks: np.ndarray) -> np.ndarray:
             q = (byte >> 4) if (e // 32) % 2 else (byte & 0xF)
             out[:, e] = d * sc[:, e // 32] * q - dmin * mn[:, e // 32]
         return out.reshape(-1)
+    if t == O.TYPE_Q5_K:
+        d = h2f(b[:, 0:2].copy().view(np.uint16)[:, 0]).astype(np.float64)
+        dmin = h2f(b[:, 2:4].copy().view(np.uint16)[:, 0]).astype(np.float64)
+        s = b[:, 4:16].astype(np.int64)
+        sc = np.zeros((len(b), 8), np.int64)
+        mn = np.zeros((len(b), 8), np.int64)
+        sc[:, :4] = s[:, 0:4] & 63
+        mn[:, :4] = s[:, 4:8] & 63
+        sc[:, 4:] = (s[:, 8:12] & 0xF) | ((s[:, 0:4] >> 6) << 4)
+        mn[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+        qh = b[:, 16:48].astype(np.int64)
+        qs = b[:, 48:176].astype(np.int64)
+        out = np.zeros((len(b), 256))
+        for e in range(256):
+            sub, pos = divmod(e, 32)
+            byte = qs[:, (e // 64) * 32 + pos]
+            q = ((byte >> 4) if sub % 2 else (byte & 0xF)) + 16 * ((qh[:, pos] >> sub) & 1)
+            out[:, e] = d * sc[:, sub] * q - dmin * mn[:, sub]
+        return out.reshape(-1)
+    if t == O.TYPE_F16:
+        return h2f(b.copy().view(np.uint16).reshape(-1)).astype(np.float64)
+    if t == O.TYPE_F32:
+        return b.copy().view(np.float32).reshape(-1).astype(np.float64)
     if t == O.TYPE_Q6_K:
         ql = b[:, 0:128].astype(np.int64)
         qh = b[:, 128:192].astype(np.int64)
@@ -139,7 +162,8 @@ def test_q8_K_first_of_tied_maxima():
     assert flipped != f["block"]
 
 
-@pytest.mark.parametrize("name,t", [("q4_K_grid.json", O.TYPE_Q4_K), ("q6_K_grid.json", O.TYPE_Q6_K)])
+@pytest.mark.parametrize("name,t", [("q4_K_grid.json", O.TYPE_Q4_K), ("q5_K_grid.json", O.TYPE_Q5_K),
+                                    ("q6_K_grid.json", O.TYPE_Q6_K)])
 def test_k_quant_grid_blocks(name, t):
     f = gold(name)
     x = np.array(f["x"], np.float32)[None]
@@ -149,6 +173,35 @@ def test_k_quant_grid_blocks(name, t):
     deq = O.dequantize_rows(t, blk[None], 256)[0]
     assert np.array_equal(deq, np.array(f["dequant"], np.float32))
     assert np.array_equal(decode(t, blk), np.array(f["dequant"], np.float64))
+
+
+def test_q5_K_grid_fixture_rejects_a_dropped_high_bit():
+    """Mutation check: the Q5_K grid block without its qh plane (bit 4 of every code) no longer decodes to the grid,
+    nor does one whose qh bits are read from the wrong sub-block."""
+    f = gold("q5_K_grid.json")
+    blk = bytearray.fromhex(f["block"])
+    want = np.array(f["dequant"])
+    dropped = bytearray(blk)
+    dropped[16:48] = bytes(32)
+    assert not np.array_equal(decode(O.TYPE_Q5_K, np.frombuffer(bytes(dropped), np.uint8)), want)
+    rotated = bytearray(blk)
+    rotated[16:48] = bytes(((v << 1) | (v >> 7)) & 0xFF for v in blk[16:48])
+    assert not np.array_equal(decode(O.TYPE_Q5_K, np.frombuffer(bytes(rotated), np.uint8)), want)
+    assert not np.array_equal(O.dequantize_rows(O.TYPE_Q5_K, np.frombuffer(bytes(dropped), np.uint8)[None], 256)[0],
+                              want.astype(np.float32))
+
+
+def test_f16_conversion_is_ieee_rounding():
+    """F16 weights and the F16 activations ggml pairs with them: numpy's IEEE float32 -> float16 rounding."""
+    x = np.concatenate([O.fill_normal(33, 4, 512), O.fill_normal(34, 1, 512) * np.float32(1e-6),
+                        O.fill_normal(35, 1, 512) * np.float32(3e4)])
+    q = O.quantize_rows(O.TYPE_F16, x)
+    with np.errstate(over="ignore"):   # the last row runs past 65504 into inf on purpose
+        h = x.astype(np.float16)
+    assert np.isinf(h).any()
+    assert np.array_equal(q.reshape(-1).view(np.uint16), h.view(np.uint16).reshape(-1))
+    assert np.array_equal(O.dequantize_rows(O.TYPE_F16, q, 512), h.astype(np.float32))
+    assert np.array_equal(O.quantize_rows(O.TYPE_F32, x).reshape(-1).view(np.float32), x.reshape(-1))
 
 
 def test_grid_fixture_rejects_swapped_nibbles():
@@ -204,9 +257,9 @@ def test_q8_matches_numpy_restatement():
         assert np.array_equal(O.quantize_rows(O.TYPE_Q8_1, x, r).reshape(-1), want1)
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K])
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K])
 def test_k_quant_weights_reconstruct(t):
-    """Validity of the weight quantizers on generic data: field ranges and a reconstruction error of a 4/6-bit fit."""
+    """Validity of the weight quantizers on generic data: field ranges and a reconstruction error of a 4/5/6-bit fit."""
     for std in (0.02, 1.0):
         w = O.fill_normal(50 + t, 32, 1024, 0.0, std)
         w[0] = 0.0
@@ -214,11 +267,11 @@ def test_k_quant_weights_reconstruct(t):
         deq = decode(t, q.reshape(-1))
         assert np.all(deq[:1024] == 0)
         err = np.sqrt(np.mean((deq - w.reshape(-1).astype(np.float64)) ** 2)) / std
-        assert err < (0.12 if t == O.TYPE_Q4_K else 0.03)
+        assert err < {O.TYPE_Q4_K: 0.12, O.TYPE_Q5_K: 0.06, O.TYPE_Q6_K: 0.03}[t]
         assert np.array_equal(O.dequantize_rows(t, q, 1024).reshape(-1), deq.astype(np.float32))
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K])
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_F16, O.TYPE_F32])
 def test_dequantizers_match_independent_decoder(t):
     w = O.fill_normal(60 + t, 16, 512, 0.0, 0.02)
     q = O.quantize_chunk(t, w)
@@ -227,7 +280,7 @@ def test_dequantizers_match_independent_decoder(t):
 
 def test_quantize_chunk_row_offsets():
     w = O.fill_normal(70, 6, 512, 0.0, 0.02)
-    for t in (O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K):
+    for t in (O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_F16, O.TYPE_F32):
         full = O.quantize_chunk(t, w)
         out = np.zeros_like(full)
         L = O.lib()
@@ -242,7 +295,7 @@ def brute_dot(t, wq, aq):
     return float(np.dot(decode(t, wq), decode(O.VEC_DOT_TYPE[t], aq)))
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K])
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_F16, O.TYPE_F32])
 def test_vec_dot_against_float64_brute_force(t):
     K = 2048
     w = O.quantize_chunk(t, O.fill_normal(80 + t, 8, K, 0.0, 0.02))
@@ -268,7 +321,7 @@ def test_brute_force_catches_a_dropped_min_term():
     assert abs(O.vec_dot(O.TYPE_Q4_K, K, np.frombuffer(bytes(wb), np.uint8), a) - brute_dot(O.TYPE_Q4_K, w, a)) > 1e-4 * scale
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K])
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_F16, O.TYPE_F32])
 def test_mul_mat_is_the_product_of_decoded_operands(t):
     K, N, M = 512, 24, 5
     w = O.quantize_chunk(t, O.fill_normal(100 + t, N, K, 0.0, 0.02))
@@ -296,7 +349,7 @@ def test_mul_mat_id_routes_each_pair(bcast):
             assert np.abs(y[ti, s] - ref).max() <= 1e-5 * np.abs(ref).max()
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K])
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_F16, O.TYPE_F32])
 def test_get_rows_is_the_decoded_row(t):
     K, R = 512, 9
     table = O.quantize_chunk(t, O.fill_normal(120 + t, R, K, 0.0, 0.02))
