@@ -196,6 +196,44 @@ MX_API void mx_fill_normal_rows(uint64_t seed, int64_t row0, int64_t nrows, int6
 MX_API size_t mx_quantize_normal_rows(int type, uint64_t seed, int64_t row0, int64_t nrows, int64_t n_per_row,
                                       float mean, float stddev, void *dst, int nthreads);
 
+/* ---------------------------------------------------------------------------------------------------------------
+ * GGUF model files straight into the buffer type, for a caller without a ggml context: the parse ggml's
+ * gguf_init_from_file(no_alloc = true) gives speech.cpp's ModelFile::open (src/common/model-file.cpp:35-47,136-160),
+ * and ModelFile::load (src/common/model-file.cpp:251-268), which reads each tensor from the file in 16 MB pieces and
+ * sets each piece on the device at its offset (ggml_backend_tensor_set; here mx_tensor_set). GGUF versions 2 and 3.
+ * Every ggml type a speech.cpp file stores (src/common/storage.cpp:30-89: F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, including
+ * the Q8_0 / F16 fallbacks inside K-quant files) is read; other known ggml types are held as plain bytes.
+ * mx_gguf_open returns NULL on a file it cannot open or parse (mx_last_error says which); strings returned point into
+ * the mx_gguf and live until mx_gguf_close. Value types are GGUF's: 0 u8 .. 12 f64, 8 string, 9 array.
+ * ------------------------------------------------------------------------------------------------------------- */
+typedef struct mx_gguf mx_gguf;
+typedef struct mx_gguf_tensor_info {
+    const char *name;
+    int32_t type;      /* ggml_type */
+    int32_t n_dims;
+    int64_t ne[4];     /* ggml order; axes past n_dims are 1 */
+    uint64_t offset;   /* from the start of the data section (gguf_get_tensor_offset) */
+    uint64_t nbytes;   /* ggml_nbytes of the contiguous tensor */
+} mx_gguf_tensor_info;
+
+MX_API mx_gguf *mx_gguf_open(const char *path);
+MX_API void mx_gguf_close(mx_gguf *f);
+MX_API uint64_t mx_gguf_data_offset(const mx_gguf *f);            /* gguf_get_data_offset */
+MX_API int64_t mx_gguf_n_tensors(const mx_gguf *f);               /* gguf_get_n_tensors */
+MX_API int mx_gguf_get_tensor(const mx_gguf *f, int64_t i, mx_gguf_tensor_info *out);
+MX_API int64_t mx_gguf_find_tensor(const mx_gguf *f, const char *name);  /* gguf_find_tensor; -1 if absent */
+MX_API int64_t mx_gguf_n_keys(const mx_gguf *f);                  /* gguf_get_n_kv */
+MX_API const char *mx_gguf_key(const mx_gguf *f, int64_t id);     /* gguf_get_key */
+MX_API int64_t mx_gguf_find_key(const mx_gguf *f, const char *key);      /* gguf_find_key; -1 if absent */
+MX_API int mx_gguf_key_type(const mx_gguf *f, int64_t id);        /* gguf_get_kv_type; -1 if no such key */
+MX_API int mx_gguf_get_str(const mx_gguf *f, int64_t id, const char **out, size_t *len);
+MX_API int mx_gguf_get_int(const mx_gguf *f, int64_t id, int64_t *out);   /* any integer or bool value */
+MX_API int mx_gguf_get_float(const mx_gguf *f, int64_t id, double *out);  /* f32 or f64 */
+MX_API int mx_gguf_get_arr(const mx_gguf *f, int64_t id, int *elem_type, uint64_t *n, const void **data);
+MX_API int mx_gguf_get_arr_str(const mx_gguf *f, int64_t id, uint64_t i, const char **out, size_t *len);
+/* Reads tensor i into dst (same type and ne; allocated with mx_tensor_alloc_size) in 16 MB pieces. */
+MX_API int mx_gguf_load_tensor(mx_backend *be, const mx_gguf *f, int64_t i, const mx_tensor *dst);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,10 @@ LIB_PATH = HERE / "libmx.so"
 F32, F16, Q8_0, Q8_1, Q4_K, Q5_K, Q6_K, Q8_K, I32 = 0, 1, 8, 9, 12, 13, 14, 15, 26
 BLCK = {F32: 1, F16: 1, I32: 1, Q8_0: 32, Q8_1: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256}
 TSIZE = {F32: 4, F16: 2, I32: 4, Q8_0: 34, Q8_1: 36, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
+# ggml types a model file may hold that the device keeps as plain bytes (Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, I8, I16,
+# I64, F64, BF16)
+BLCK.update({2: 32, 3: 32, 6: 32, 7: 32, 10: 256, 11: 256, 24: 1, 25: 1, 27: 1, 28: 1, 30: 1})
+TSIZE.update({2: 18, 3: 20, 6: 22, 7: 24, 10: 84, 11: 110, 24: 1, 25: 2, 27: 8, 28: 8, 30: 2})
 OP_GET_ROWS, OP_MUL_MAT, OP_MUL_MAT_ID, OP_ARGMAX = 1, 2, 3, 4
 ROUND_REF, ROUND_X86 = 0, 1
 SUCCESS, FAILED, ALLOC_FAILED, INVALID, UNSUPPORTED = 0, -1, -2, -3, -4
@@ -34,6 +38,9 @@ EXPORTS = [
     "mx_mul_mat", "mx_mul_mat_id", "mx_mul_mat_group", "mx_argmax", "mx_quantize_act", "mx_graph_begin", "mx_graph_end",
     "mx_graph_launch", "mx_graph_free", "mx_event_new", "mx_event_record", "mx_event_synchronize",
     "mx_event_elapsed_ms", "mx_event_free", "mx_quantize_chunk", "mx_fill_normal_rows", "mx_quantize_normal_rows",
+    "mx_gguf_open", "mx_gguf_close", "mx_gguf_data_offset", "mx_gguf_n_tensors", "mx_gguf_get_tensor",
+    "mx_gguf_find_tensor", "mx_gguf_n_keys", "mx_gguf_key", "mx_gguf_find_key", "mx_gguf_key_type", "mx_gguf_get_str",
+    "mx_gguf_get_int", "mx_gguf_get_float", "mx_gguf_get_arr", "mx_gguf_get_arr_str", "mx_gguf_load_tensor",
 ]
 
 
@@ -44,6 +51,11 @@ def row_size(t: int, ne0: int) -> int:
 class MxTensor(ctypes.Structure):
     _fields_ = [("type", ctypes.c_int32), ("pad_", ctypes.c_int32), ("ne", ctypes.c_int64 * 4),
                 ("nb", ctypes.c_uint64 * 4), ("data", ctypes.c_void_p)]
+
+
+class GgufTensorInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_int32), ("n_dims", ctypes.c_int32),
+                ("ne", ctypes.c_int64 * 4), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
 
 
 class MxError(RuntimeError):
@@ -113,6 +125,22 @@ def lib():
         "mx_quantize_chunk": ([i32, vp, vp, i64, i64, i64], sz),
         "mx_fill_normal_rows": ([u64, i64, i64, i64, f32, f32, vp], None),
         "mx_quantize_normal_rows": ([i32, u64, i64, i64, i64, f32, f32, vp, i32], sz),
+        "mx_gguf_open": ([ctypes.c_char_p], vp),
+        "mx_gguf_close": ([vp], None),
+        "mx_gguf_data_offset": ([vp], u64),
+        "mx_gguf_n_tensors": ([vp], i64),
+        "mx_gguf_get_tensor": ([vp, i64, ctypes.POINTER(GgufTensorInfo)], i32),
+        "mx_gguf_find_tensor": ([vp, ctypes.c_char_p], i64),
+        "mx_gguf_n_keys": ([vp], i64),
+        "mx_gguf_key": ([vp, i64], ctypes.c_char_p),
+        "mx_gguf_find_key": ([vp, ctypes.c_char_p], i64),
+        "mx_gguf_key_type": ([vp, i64], i32),
+        "mx_gguf_get_str": ([vp, i64, ctypes.POINTER(vp), ctypes.POINTER(sz)], i32),
+        "mx_gguf_get_int": ([vp, i64, ctypes.POINTER(i64)], i32),
+        "mx_gguf_get_float": ([vp, i64, ctypes.POINTER(ctypes.c_double)], i32),
+        "mx_gguf_get_arr": ([vp, i64, ctypes.POINTER(i32), ctypes.POINTER(u64), ctypes.POINTER(vp)], i32),
+        "mx_gguf_get_arr_str": ([vp, i64, u64, ctypes.POINTER(vp), ctypes.POINTER(sz)], i32),
+        "mx_gguf_load_tensor": ([vp, vp, i64, P], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -326,3 +354,91 @@ def device_description(device: int = 0) -> str:
     buf = ctypes.create_string_buffer(256)
     check(lib().mx_device_description(device, buf, 256))
     return buf.value.decode()
+
+
+# ------------------------------------------------------------------------------------------------------------ GGUF
+GGUF_ARRAY_DTYPES = {0: np.uint8, 1: np.int8, 2: np.uint16, 3: np.int16, 4: np.uint32, 5: np.int32, 6: np.float32,
+                     7: np.bool_, 10: np.uint64, 11: np.int64, 12: np.float64}
+
+
+class Gguf:
+    """A GGUF file parsed by libmx (mx_gguf_open): metadata, tensor infos, and tensors read into a backend's buffer
+    type in 16 MB pieces (mx_gguf_load_tensor) -- what speech.cpp's ModelFile::open / load do through ggml."""
+
+    def __init__(self, path):
+        self.h = lib().mx_gguf_open(str(path).encode())
+        if not self.h:
+            raise MxError(FAILED, lib().mx_last_error().decode(errors="replace"))
+
+    def close(self) -> None:
+        if self.h:
+            lib().mx_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def data_offset(self) -> int:
+        return int(lib().mx_gguf_data_offset(self.h))
+
+    def tensors(self) -> list:
+        out = []
+        for i in range(lib().mx_gguf_n_tensors(self.h)):
+            info = GgufTensorInfo()
+            check(lib().mx_gguf_get_tensor(self.h, i, ctypes.byref(info)))
+            out.append({"name": info.name.decode(), "type": info.type, "n_dims": info.n_dims, "ne": tuple(info.ne),
+                        "offset": int(info.offset), "nbytes": int(info.nbytes)})
+        return out
+
+    def find_tensor(self, name: str) -> int:
+        return int(lib().mx_gguf_find_tensor(self.h, name.encode()))
+
+    def keys(self) -> list:
+        return [lib().mx_gguf_key(self.h, i).decode() for i in range(lib().mx_gguf_n_keys(self.h))]
+
+    def get(self, key: str):
+        """The value of a key (None if absent): int, float, str, or a list / numpy array for arrays."""
+        L = lib()
+        i = L.mx_gguf_find_key(self.h, key.encode())
+        if i < 0:
+            return None
+        vt = L.mx_gguf_key_type(self.h, i)
+        if vt == 8:
+            p, n = ctypes.c_void_p(), ctypes.c_size_t()
+            check(L.mx_gguf_get_str(self.h, i, ctypes.byref(p), ctypes.byref(n)))
+            return ctypes.string_at(p.value, n.value).decode() if n.value else ""
+        if vt in (6, 12):
+            v = ctypes.c_double()
+            check(L.mx_gguf_get_float(self.h, i, ctypes.byref(v)))
+            return v.value
+        if vt == 9:
+            et, n, data = ctypes.c_int(), ctypes.c_uint64(), ctypes.c_void_p()
+            check(L.mx_gguf_get_arr(self.h, i, ctypes.byref(et), ctypes.byref(n), ctypes.byref(data)))
+            if et.value == 8:
+                out = []
+                for j in range(n.value):
+                    p, m = ctypes.c_void_p(), ctypes.c_size_t()
+                    check(L.mx_gguf_get_arr_str(self.h, i, j, ctypes.byref(p), ctypes.byref(m)))
+                    out.append(ctypes.string_at(p.value, m.value).decode() if m.value else "")
+                return out
+            dt = np.dtype(GGUF_ARRAY_DTYPES[et.value])
+            if n.value == 0:
+                return np.zeros(0, dt)
+            return np.frombuffer(ctypes.string_at(data.value, n.value * dt.itemsize), dt).copy()
+        v = ctypes.c_int64()
+        check(L.mx_gguf_get_int(self.h, i, ctypes.byref(v)))
+        return bool(v.value) if vt == 7 else v.value
+
+    def load(self, be: "Backend", name: str) -> "Tensor":
+        """Allocates the named tensor in the backend's buffer type and reads it from the file."""
+        i = self.find_tensor(name)
+        if i < 0:
+            raise KeyError(name)
+        info = self.tensors()[i]
+        T = be.tensor(info["type"], info["ne"])
+        check(lib().mx_gguf_load_tensor(be.h, self.h, i, T.ref()))
+        return T

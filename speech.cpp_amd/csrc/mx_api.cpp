@@ -9,6 +9,7 @@
 
 #include "mx_common.h"
 #include "mx_dot.h"
+#include "mx_error.h"
 
 struct mx_backend {
     int device = 0;
@@ -46,6 +47,15 @@ int fail(int code, const char *fmt, ...) {
     return code;
 }
 
+}  // namespace
+
+int mx::set_error(int code, const char *msg) {
+    g_error = msg ? msg : "";
+    return code;
+}
+
+namespace {
+
 int hip_fail(hipError_t e, const char *what) {
     return fail(e == hipErrorOutOfMemory ? MX_ALLOC_FAILED : MX_FAILED, "%s: %s", what, hipGetErrorString(e));
 }
@@ -59,20 +69,33 @@ int hip_fail(hipError_t e, const char *what) {
 constexpr size_t kStagingPiece = 64ull << 20;  // bytes per upload / download piece
 constexpr size_t kMaxLds = 64 * 1024;         // LDS a product kernel may ask for
 
+// ggml's block geometry (ggml-common.h). Types this device does not compute (Q4_0 ... Q3_K, integers, F64, BF16) are
+// held as plain bytes, so a model file's every tensor can live in the buffer type.
 int64_t blck(int type) {
     switch (type) {
+        case 2: case 3: case 6: case 7:                               // Q4_0, Q4_1, Q5_0, Q5_1
         case MX_TYPE_Q8_0: case MX_TYPE_Q8_1: return 32;
+        case 10: case 11:                                             // Q2_K, Q3_K
         case MX_TYPE_Q4_K: case MX_TYPE_Q5_K: case MX_TYPE_Q6_K: case MX_TYPE_Q8_K: return 256;
-        case MX_TYPE_F32: case MX_TYPE_F16: case MX_TYPE_I32: return 1;
+        case MX_TYPE_F32: case MX_TYPE_F16: case MX_TYPE_I32:
+        case 24: case 25: case 27: case 28: case 30: return 1;       // I8, I16, I64, F64, BF16
         default: return 0;
     }
 }
 size_t tsize(int type) {
     switch (type) {
+        case 24: return 1;
+        case MX_TYPE_F16: case 25: case 30: return 2;
         case MX_TYPE_F32: case MX_TYPE_I32: return 4;
-        case MX_TYPE_F16: return 2;
+        case 27: case 28: return 8;
+        case 2: return 18;
+        case 3: return 20;
+        case 6: return 22;
+        case 7: return 24;
         case MX_TYPE_Q8_0: return 34;
         case MX_TYPE_Q8_1: return 36;
+        case 10: return 84;
+        case 11: return 110;
         case MX_TYPE_Q4_K: return 144;
         case MX_TYPE_Q5_K: return 176;
         case MX_TYPE_Q6_K: return 210;
@@ -85,8 +108,8 @@ int64_t nelements(const mx_tensor *t) { return t->ne[0] * t->ne[1] * t->ne[2] * 
 
 // ggml_nbytes
 size_t nbytes(const mx_tensor *t) {
-    if (nelements(t) == 0) return 0;
     const int64_t b = blck(t->type);
+    if (nelements(t) == 0 || b == 0) return 0;
     size_t n = b == 1 ? tsize(t->type) : (size_t)(t->ne[0] / b) * t->nb[0];
     if (b == 1) {
         for (int i = 0; i < 4; i++) n += (size_t)(t->ne[i] - 1) * t->nb[i];
@@ -290,6 +313,7 @@ MX_API int mx_buffer_clear(mx_backend *be, void *base, size_t size, uint8_t valu
 
 static int tensor_range_ok(const mx_tensor *t, size_t offset, size_t size) {
     if (!t || !t->data || !shape_ok(t)) return fail(MX_INVALID, "invalid tensor");
+    if (blck(t->type) == 0) return fail(MX_UNSUPPORTED, "unknown tensor type %d", t->type);
     if (mx::is_quantized(t->type) && !contiguous(t)) return fail(MX_UNSUPPORTED, "quantized tensors must be contiguous");
     const size_t n = nbytes(t);
     if (offset > n || size > n - offset) return fail(MX_INVALID, "bytes [%zu, %zu) lie outside the tensor's %zu", offset,
