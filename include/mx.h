@@ -53,12 +53,18 @@ enum {
 };
 
 /* The ops this device computes (the ggml adapter maps GGML_OP_GET_ROWS / GGML_OP_MUL_MAT / GGML_OP_MUL_MAT_ID /
- * GGML_OP_ARGMAX). */
+ * GGML_OP_ARGMAX, and the decoder layer's GGML_OP_RMS_NORM / GGML_OP_ADD / GGML_OP_MUL / GGML_OP_GLU (swiglu) /
+ * GGML_OP_SET_ROWS; ROPE and FLASH_ATTN_EXT carry parameters and have supports functions of their own). */
 enum {
     MX_OP_GET_ROWS = 1,
     MX_OP_MUL_MAT = 2,
     MX_OP_MUL_MAT_ID = 3,
     MX_OP_ARGMAX = 4,
+    MX_OP_RMS_NORM = 5,
+    MX_OP_ADD = 6,
+    MX_OP_MUL = 7,
+    MX_OP_SWIGLU = 8,
+    MX_OP_SET_ROWS = 9,
 };
 
 /* Rounding of the activation quantizers.
@@ -151,6 +157,36 @@ MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b
  * logits). A NaN never compares greater: at index 0 it keeps index 0, elsewhere it is passed over.
  *   mx_argmax(src [n, R] F32, rows 16-byte aligned) -> dst [R] I32 */
 MX_API int mx_argmax(mx_backend *be, const mx_tensor *src, const mx_tensor *dst);
+/* ---------------------------------------------------------------------------------------------------------------
+ * The decoder layer's other ops, so a layer runs on the device without CPU round trips (src/common/qwen3-decoder.cpp
+ * Qwen3Decoder::layers :350-410, outputs :422-438): f32 rows with ne0 contiguous, any row strides.
+ *   mx_rms_norm(src [n, ...]) -> dst: ggml_rms_norm (:361,368-369,409,424); w [n] F32 or NULL multiplies the result
+ *     as the ggml_mul by the norm weight that follows it does (fused, same roundings).
+ *   mx_binary(MX_OP_ADD | MX_OP_MUL, a, b) -> dst: ggml_add (:405,411) / ggml_mul, b repeated over a's shape.
+ *   mx_swiglu(a, b) -> dst: ggml_swiglu_split (:411), silu(a) * b.
+ *   mx_rope(src [n, heads, rows], pos [rows] I32) -> dst: ggml_rope_ext (:375-376) in GGML_ROPE_TYPE_NEOX with
+ *     freq_factors NULL, ext_factor 0, attn_factor 1 (the decoder's arguments); other modes are unsupported.
+ *   mx_set_rows(src [n, rows] F32, idx [rows] I32 or I64) -> dst F16 rows: ggml_set_rows (:373,378) writing the new
+ *     keys and values into the f16 KV cache at their positions; an index out of range is reported by
+ *     mx_backend_synchronize as MX_INVALID and leaves the cache as it was.
+ *   mx_flash_attn_ext(q [D, n_q, n_head] F32, k, v [D, n_kv, n_kv_head] F16, mask [n_kv, >= n_q] F16 or NULL)
+ *     -> dst [D, n_head, n_q] F32: ggml_flash_attn_ext (:394-397) with max_bias 0 and no softcap; D 64 or 128;
+ *     q rounded to fp16 as ggml does, scores and the V sum in fp32 (the GGML_PREC_F32 the decoder sets).
+ * ------------------------------------------------------------------------------------------------------------- */
+MX_API int mx_rms_norm(mx_backend *be, const mx_tensor *src, const mx_tensor *dst, float eps, const mx_tensor *w);
+MX_API int mx_binary(mx_backend *be, int op, const mx_tensor *a, const mx_tensor *b, const mx_tensor *dst);
+MX_API int mx_swiglu(mx_backend *be, const mx_tensor *a, const mx_tensor *b, const mx_tensor *dst);
+MX_API int mx_supports_rope(const mx_tensor *src, const mx_tensor *pos, const mx_tensor *dst, int n_dims, int mode,
+                            float ext_factor, float attn_factor);
+MX_API int mx_rope(mx_backend *be, const mx_tensor *src, const mx_tensor *pos, const mx_tensor *dst, int n_dims,
+                   int mode, float freq_base, float freq_scale, float ext_factor, float attn_factor);
+MX_API int mx_set_rows(mx_backend *be, const mx_tensor *src, const mx_tensor *idx, const mx_tensor *dst);
+MX_API int mx_supports_flash_attn_ext(const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
+                                      const mx_tensor *mask, const mx_tensor *dst, float max_bias,
+                                      float logit_softcap);
+MX_API int mx_flash_attn_ext(mx_backend *be, const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
+                             const mx_tensor *mask, const mx_tensor *dst, float scale);
+
 /* Several MUL_MAT nodes that read the same src1 (q/k/v, or gate/up) in one launch, as a backend's graph_compute
  * may fuse them. Each dst[i] = src0[i] x src1, exactly as n separate mx_mul_mat calls compute it. */
 MX_API int mx_mul_mat_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,

@@ -69,6 +69,13 @@ def lib():
         L.orc_mul_mat_id.argtypes, L.orc_mul_mat_id.restype = [P, P, P, P, i32, i32], i32
         L.orc_get_rows.argtypes, L.orc_get_rows.restype = [P, P, P], i32
         L.orc_argmax.argtypes, L.orc_argmax.restype = [P, P], i32
+        L.orc_rms_norm.argtypes, L.orc_rms_norm.restype = [vp, vp, i64, i64, f32], None
+        L.orc_binary.argtypes, L.orc_binary.restype = [i32, vp, vp, vp, i64, i64, i64], None
+        L.orc_swiglu.argtypes, L.orc_swiglu.restype = [vp, vp, vp, i64], None
+        L.orc_rope_neox.argtypes, L.orc_rope_neox.restype = [vp, vp, vp, i64, i64, i64, i32, f32, f32], None
+        L.orc_set_rows_f16.argtypes, L.orc_set_rows_f16.restype = [vp, vp, vp, i64, i64, i64], i32
+        L.orc_flash_attn_ext.argtypes = [vp, vp, vp, vp, vp, i32, i64, i64, i64, i64, f32, i32]
+        L.orc_flash_attn_ext.restype = i32
         L.orc_fill_normal_rows.argtypes = [u64, i64, i64, i64, f32, f32, vp]
         L.orc_fill_normal_rows.restype = None
         _lib = L
@@ -233,6 +240,73 @@ def argmax(x: np.ndarray) -> np.ndarray:
     rc = lib().orc_argmax(ctypes.byref(s0), ctypes.byref(d))
     if rc != 0:
         raise ValueError(f"orc_argmax rc={rc}")
+    return out
+
+
+# ------------------------------------------------------------------------------------ the decoder layer's other ops
+def rms_norm(x: np.ndarray, eps: float) -> np.ndarray:
+    """ggml_rms_norm over the last axis of x (float32)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().orc_rms_norm(_p(x), _p(y), x.shape[-1], x.size // x.shape[-1], eps)
+    return y
+
+
+def binary(op: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """ggml_add / ggml_mul (op "add" / "mul") with b's rows repeated over a's rows (last axis = ne0)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    ne0 = a.shape[-1]
+    y = np.empty_like(a)
+    lib().orc_binary(0 if op == "add" else 1, _p(a), _p(b), _p(y), ne0, a.size // ne0, b.size // ne0)
+    return y
+
+
+def swiglu(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    y = np.empty_like(a)
+    lib().orc_swiglu(_p(a), _p(b), _p(y), a.size)
+    return y
+
+
+def rope_neox(x: np.ndarray, pos: np.ndarray, n_dims: int, freq_base: float, freq_scale: float = 1.0) -> np.ndarray:
+    """ggml_rope_ext(NEOX) on x float32 [rows, n_head, ne0] with pos int32 [rows]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    rows, n_head, ne0 = x.shape
+    y = np.empty_like(x)
+    lib().orc_rope_neox(_p(x), _p(pos), _p(y), ne0, n_head, rows, n_dims, freq_base, freq_scale)
+    return y
+
+
+def set_rows_f16(cache: np.ndarray, src: np.ndarray, idx: np.ndarray) -> np.ndarray:
+    """ggml_set_rows into an f16 cache: cache uint16 [R, ne0] (copied), src float32 [n, ne0], idx int32 [n]."""
+    out = np.ascontiguousarray(cache, dtype=np.uint16).copy()
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    if lib().orc_set_rows_f16(_p(src), _p(idx), _p(out), src.shape[1], src.shape[0], out.shape[0]) != 0:
+        raise ValueError("set_rows index out of range")
+    return out
+
+
+def flash_attn_ext(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask, scale: float, exact: bool = False):
+    """ggml_flash_attn_ext: q float32 [n_head, n_q, D]; k, v uint16 (fp16 bits) [n_kv_head, n_kv, D]; mask uint16
+    [n_q, n_kv] or None -> float32 [n_q, n_head, D] (the permuted output the decoder reshapes)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    n_head, n_q, D = q.shape
+    n_kv_head, n_kv, _ = k.shape
+    out = np.zeros((n_q, n_head, D), np.float32)
+    mp = 0
+    if mask is not None:
+        mask = np.ascontiguousarray(mask, dtype=np.uint16)
+        mp = _p(mask)
+    rc = lib().orc_flash_attn_ext(_p(q), _p(k), _p(v), mp or None, _p(out), D, n_q, n_head, n_kv, n_kv_head, scale,
+                                  int(exact))
+    if rc != 0:
+        raise ValueError(f"orc_flash_attn_ext rc={rc}")
     return out
 
 

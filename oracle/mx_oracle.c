@@ -992,6 +992,161 @@ int orc_argmax(const orc_tensor *src0, orc_tensor *dst) {
 }
 
 /* ------------------------------------------------------------------------------------------------------------------
+ * The decoder layer's other ops (qwen3-decoder.cpp:350-410), as ggml-cpu computes them on f32 rows.
+ * ---------------------------------------------------------------------------------------------------------------- */
+/* ggml-cpu ops.cpp ggml_compute_forward_rms_norm_f32: the sum of squares (each square rounded to float) in double,
+ * mean = sum / ne0 rounded to float, y = x * (1 / sqrtf(mean + eps)). */
+void orc_rms_norm(const float *x, float *y, int64_t ne0, int64_t nrows, float eps) {
+    for (int64_t r = 0; r < nrows; r++) {
+        const float *xr = x + r * ne0;
+        double sum = 0.0;
+        for (int64_t i = 0; i < ne0; i++) sum += (double)(xr[i] * xr[i]);
+        const float mean = (float)(sum / (double)ne0);
+        const float scale = 1.0f / sqrtf(mean + eps);
+        for (int64_t i = 0; i < ne0; i++) y[r * ne0 + i] = xr[i] * scale;
+    }
+}
+
+/* ggml-cpu binary ops (ggml_compute_forward_add / _mul on f32): dst = a op b with b's rows repeated over a's
+ * (b has ne0 elements per row and nb_rows rows; a's row r meets b's row r % nb_rows). op 0 add, 1 mul. */
+void orc_binary(int op, const float *a, const float *b, float *y, int64_t ne0, int64_t nrows, int64_t nb_rows) {
+    for (int64_t r = 0; r < nrows; r++)
+        for (int64_t i = 0; i < ne0; i++) {
+            const float u = a[r * ne0 + i], v = b[(r % nb_rows) * ne0 + i];
+            y[r * ne0 + i] = op == 0 ? u + v : u * v;
+        }
+}
+
+/* ggml-cpu ggml_vec_swiglu_f32 in its scalar form: y = silu(a) * b, silu(x) = x / (1 + expf(-x)). */
+void orc_swiglu(const float *a, const float *b, float *y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = a[i] / (1.0f + expf(-a[i])) * b[i];
+}
+
+/* ggml-cpu ggml_compute_forward_rope_f32, GGML_ROPE_TYPE_NEOX, no frequency factors, ext_factor 0, attn_factor 1:
+ * for position p the angles are theta_k = p * theta_scale^k (k = 0 .. n_dims/2 - 1), formed as ggml_rope_cache_init
+ * forms them (theta = p; theta *= theta_scale after each pair, theta_scale = powf(freq_base, -2 / n_dims), all
+ * float), and the pair (x[k], x[k + n_dims/2]) turns by theta_k. Channels past n_dims are copied. x: [ne0, n_head,
+ * nrows] with one position per row (pos[r]). */
+void orc_rope_neox(const float *x, const int32_t *pos, float *y, int64_t ne0, int64_t n_head, int64_t nrows,
+                   int n_dims, float freq_base, float freq_scale) {
+    const float theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    float *cache = (float *)malloc(sizeof(float) * (size_t)n_dims);
+    for (int64_t r = 0; r < nrows; r++) {
+        float theta = (float)pos[r];
+        for (int i0 = 0; i0 < n_dims; i0 += 2) {
+            const float t = freq_scale * theta;
+            cache[i0] = cosf(t);
+            cache[i0 + 1] = sinf(t);
+            theta *= theta_scale;
+        }
+        for (int64_t h = 0; h < n_head; h++) {
+            const float *xr = x + (r * n_head + h) * ne0;
+            float *yr = y + (r * n_head + h) * ne0;
+            for (int i0 = 0; i0 < n_dims; i0 += 2) {
+                const int ic = i0 / 2;
+                const float c = cache[i0], sn = cache[i0 + 1];
+                const float x0 = xr[ic], x1 = xr[ic + n_dims / 2];
+                yr[ic] = x0 * c - x1 * sn;
+                yr[ic + n_dims / 2] = x0 * sn + x1 * c;
+            }
+            for (int64_t i = n_dims; i < ne0; i++) yr[i] = xr[i];
+        }
+    }
+    free(cache);
+}
+
+/* ggml-cpu ggml_compute_forward_set_rows with an f16 destination: dst row idx[i] = fp16(src row i) (from_float,
+ * round to nearest even). dst holds dst_rows rows of ne0 halves; returns -2 for an index out of range. */
+int orc_set_rows_f16(const float *src, const int32_t *idx, uint16_t *dst, int64_t ne0, int64_t nrows,
+                     int64_t dst_rows) {
+    for (int64_t i = 0; i < nrows; i++) {
+        if (idx[i] < 0 || idx[i] >= dst_rows) return -2;
+        for (int64_t j = 0; j < ne0; j++) dst[idx[i] * ne0 + j] = FP32_TO_FP16(src[i * ne0 + j]);
+    }
+    return 0;
+}
+
+/* ggml-cpu ggml_compute_forward_flash_attn_ext_f16 (one chunk, F16 K and V, an f16 mask, no ALiBi, no softcap).
+ * Shapes as the decoder builds them: q [D, n_q, n_head] f32 (rows of one head contiguous: q[(h * n_q + i) * D]),
+ * K, V [D, n_kv, n_kv_head] f16 (k[(hk * n_kv + j) * D]), mask [n_kv, n_q] f16, dst [D, n_head, n_q] f32
+ * (dst[(i * n_head + h) * D], the permuted output). Head h reads K/V head h / (n_head / n_kv_head).
+ * exact = 0: the CPU's arithmetic -- q rounded to fp16, each k.q an fp32 sum of exact products, online softmax with
+ *            the V accumulator held in fp16 (ggml_vec_scale_f16 / ggml_vec_mad_f16 round after every step);
+ * exact = 1: the same attention with q rounded to fp16, every score and the softmax in double. */
+int orc_flash_attn_ext(const float *q, const uint16_t *k, const uint16_t *v, const uint16_t *mask, float *dst, int D,
+                       int64_t n_q, int64_t n_head, int64_t n_kv, int64_t n_kv_head, float scale, int exact) {
+    if (n_head % n_kv_head != 0) return -1;
+    const int64_t g = n_head / n_kv_head;
+    uint16_t *qh = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)D);
+    uint16_t *acc16 = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)D);
+    double *accd = (double *)malloc(sizeof(double) * (size_t)D);
+    double *sc = (double *)malloc(sizeof(double) * (size_t)(n_kv > 0 ? n_kv : 1));
+    for (int64_t h = 0; h < n_head; h++) {
+        const int64_t hk = h / g;
+        for (int64_t i = 0; i < n_q; i++) {
+            const float *qr = q + (h * n_q + i) * D;
+            for (int d = 0; d < D; d++) qh[d] = FP32_TO_FP16(qr[d]);
+            float *out = dst + (i * n_head + h) * D;
+            const uint16_t *mr = mask ? mask + i * n_kv : NULL;
+            if (!exact) {
+                float S = 0.0f, M = -INFINITY;
+                for (int d = 0; d < D; d++) acc16[d] = 0;
+                for (int64_t j = 0; j < n_kv; j++) {
+                    const float mv = mr ? FP16_TO_FP32(mr[j]) : 0.0f;
+                    if (mv == -INFINITY) continue;
+                    const uint16_t *kr = k + (hk * n_kv + j) * D;
+                    float s = 0.0f;
+                    for (int d = 0; d < D; d++) s += FP16_TO_FP32(kr[d]) * FP16_TO_FP32(qh[d]);
+                    s = s * scale;
+                    s += mv;
+                    const float Mold = M;
+                    float ms = 1.0f, vs = 1.0f;
+                    const uint16_t *vr = v + (hk * n_kv + j) * D;
+                    if (s > M) {
+                        M = s;
+                        ms = expf(Mold - M);
+                        for (int d = 0; d < D; d++) acc16[d] = FP32_TO_FP16(FP16_TO_FP32(acc16[d]) * ms);
+                    } else {
+                        vs = expf(s - M);
+                    }
+                    for (int d = 0; d < D; d++)
+                        acc16[d] = FP32_TO_FP16(FP16_TO_FP32(acc16[d]) + FP16_TO_FP32(vr[d]) * vs);
+                    S = S * ms + vs;
+                }
+                const float S_inv = S == 0.0f ? 0.0f : 1.0f / S;
+                for (int d = 0; d < D; d++) out[d] = FP16_TO_FP32(acc16[d]) * S_inv;
+            } else {
+                double M = -INFINITY;
+                for (int64_t j = 0; j < n_kv; j++) {
+                    const double mv = mr ? (double)FP16_TO_FP32(mr[j]) : 0.0;
+                    if (mv == -INFINITY) { sc[j] = -INFINITY; continue; }
+                    const uint16_t *kr = k + (hk * n_kv + j) * D;
+                    double s = 0.0;
+                    for (int d = 0; d < D; d++) s += (double)FP16_TO_FP32(kr[d]) * (double)FP16_TO_FP32(qh[d]);
+                    sc[j] = s * (double)scale + mv;
+                    if (sc[j] > M) M = sc[j];
+                }
+                double S = 0.0;
+                for (int d = 0; d < D; d++) accd[d] = 0.0;
+                for (int64_t j = 0; j < n_kv; j++) {
+                    if (sc[j] == -INFINITY) continue;
+                    const double p = exp(sc[j] - M);
+                    S += p;
+                    const uint16_t *vr = v + (hk * n_kv + j) * D;
+                    for (int d = 0; d < D; d++) accd[d] += p * (double)FP16_TO_FP32(vr[d]);
+                }
+                for (int d = 0; d < D; d++) out[d] = S == 0.0 ? 0.0f : (float)(accd[d] / S);
+            }
+        }
+    }
+    free(qh);
+    free(acc16);
+    free(accd);
+    free(sc);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------------------------------------------------
  * Seeded synthetic data.
  * ---------------------------------------------------------------------------------------------------------------- */
 static uint64_t splitmix64(uint64_t *s) {

@@ -91,6 +91,20 @@ int orc_get_rows(const orc_tensor *src0, const orc_tensor *ids, orc_tensor *dst)
  * dst I32 [ne1]. */
 int orc_argmax(const orc_tensor *src0, orc_tensor *dst);
 
+/* The decoder layer's other ops (src/common/qwen3-decoder.cpp:350-410) on contiguous f32 rows, as ggml-cpu computes
+ * them: RMS_NORM, ADD / MUL with src1 rows repeated (op 0 add, 1 mul), GLU SWIGLU (split form), ROPE in NEOX mode,
+ * SET_ROWS into an f16 cache, FLASH_ATTN_EXT over f16 K / V with an f16 mask (exact = 0: ggml-cpu's arithmetic with
+ * its fp16 V accumulator; exact = 1: the same attention in double). Shapes are given with each function. */
+void orc_rms_norm(const float *x, float *y, int64_t ne0, int64_t nrows, float eps);
+void orc_binary(int op, const float *a, const float *b, float *y, int64_t ne0, int64_t nrows, int64_t nb_rows);
+void orc_swiglu(const float *a, const float *b, float *y, int64_t n);
+void orc_rope_neox(const float *x, const int32_t *pos, float *y, int64_t ne0, int64_t n_head, int64_t nrows,
+                   int n_dims, float freq_base, float freq_scale);
+int orc_set_rows_f16(const float *src, const int32_t *idx, uint16_t *dst, int64_t ne0, int64_t nrows,
+                     int64_t dst_rows);
+int orc_flash_attn_ext(const float *q, const uint16_t *k, const uint16_t *v, const uint16_t *mask, float *dst, int D,
+                       int64_t n_q, int64_t n_head, int64_t n_kv, int64_t n_kv_head, float scale, int exact);
+
 /* Seeded synthetic data: splitmix64 -> xoshiro256** -> Box-Muller in double -> float. Row r of a tensor draws from
  * its own stream seeded by (seed, r), so rows can be generated in any order or in parallel. */
 void orc_fill_normal_rows(uint64_t seed, int64_t row0, int64_t nrows, int64_t n_per_row, float mean, float stddev,

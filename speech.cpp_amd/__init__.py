@@ -27,6 +27,8 @@ TSIZE = {F32: 4, F16: 2, I32: 4, Q8_0: 34, Q8_1: 36, Q4_K: 144, Q5_K: 176, Q6_K:
 BLCK.update({2: 32, 3: 32, 6: 32, 7: 32, 10: 256, 11: 256, 24: 1, 25: 1, 27: 1, 28: 1, 30: 1})
 TSIZE.update({2: 18, 3: 20, 6: 22, 7: 24, 10: 84, 11: 110, 24: 1, 25: 2, 27: 8, 28: 8, 30: 2})
 OP_GET_ROWS, OP_MUL_MAT, OP_MUL_MAT_ID, OP_ARGMAX = 1, 2, 3, 4
+OP_RMS_NORM, OP_ADD, OP_MUL, OP_SWIGLU, OP_SET_ROWS = 5, 6, 7, 8, 9
+ROPE_NEOX = 2
 ROUND_REF, ROUND_X86 = 0, 1
 SUCCESS, FAILED, ALLOC_FAILED, INVALID, UNSUPPORTED = 0, -1, -2, -3, -4
 
@@ -41,6 +43,8 @@ EXPORTS = [
     "mx_gguf_open", "mx_gguf_close", "mx_gguf_data_offset", "mx_gguf_n_tensors", "mx_gguf_get_tensor",
     "mx_gguf_find_tensor", "mx_gguf_n_keys", "mx_gguf_key", "mx_gguf_find_key", "mx_gguf_key_type", "mx_gguf_get_str",
     "mx_gguf_get_int", "mx_gguf_get_float", "mx_gguf_get_arr", "mx_gguf_get_arr_str", "mx_gguf_load_tensor",
+    "mx_rms_norm", "mx_binary", "mx_swiglu", "mx_supports_rope", "mx_rope", "mx_set_rows", "mx_supports_flash_attn_ext",
+    "mx_flash_attn_ext",
 ]
 
 
@@ -141,6 +145,14 @@ def lib():
         "mx_gguf_get_arr": ([vp, i64, ctypes.POINTER(i32), ctypes.POINTER(u64), ctypes.POINTER(vp)], i32),
         "mx_gguf_get_arr_str": ([vp, i64, u64, ctypes.POINTER(vp), ctypes.POINTER(sz)], i32),
         "mx_gguf_load_tensor": ([vp, vp, i64, P], i32),
+        "mx_rms_norm": ([vp, P, P, f32, P], i32),
+        "mx_binary": ([vp, i32, P, P, P], i32),
+        "mx_swiglu": ([vp, P, P, P], i32),
+        "mx_supports_rope": ([P, P, P, i32, i32, f32, f32], i32),
+        "mx_rope": ([vp, P, P, P, i32, i32, f32, f32, f32, f32], i32),
+        "mx_set_rows": ([vp, P, P, P], i32),
+        "mx_supports_flash_attn_ext": ([P, P, P, P, P, f32, f32], i32),
+        "mx_flash_attn_ext": ([vp, P, P, P, P, P, f32], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -221,6 +233,10 @@ class Tensor:
     def ref(self):
         return ctypes.byref(self.desc)
 
+    def view(self, ne, nb, offset: int = 0) -> "View":
+        """A ggml view of this tensor's memory (ggml_view_* / ggml_permute): other ne / nb, same bytes."""
+        return View(self, ne, nb, offset)
+
     def set(self, data: np.ndarray, offset: int = 0) -> "Tensor":
         data = np.ascontiguousarray(data)
         check(lib().mx_tensor_set(self.be.h, self.ref(), _p(data), offset, data.nbytes))
@@ -253,6 +269,26 @@ class Tensor:
                 lib().mx_buffer_free(self.be.h, self.base)
         except Exception:
             pass
+
+
+class View:
+    """A tensor descriptor over another tensor's memory (owns nothing)."""
+
+    def __init__(self, base: Tensor, ne, nb, offset: int = 0):
+        ne = tuple(int(v) for v in ne) + (1,) * (4 - len(ne))
+        nb = tuple(int(v) for v in nb) + (nb[-1] * ne[len(nb) - 1],) * (4 - len(nb))
+        self.base_tensor = base
+        self.type = base.type
+        self.ne = ne
+        self.desc = MxTensor()
+        self.desc.type = base.type
+        for i in range(4):
+            self.desc.ne[i] = ne[i]
+            self.desc.nb[i] = nb[i]
+        self.desc.data = base.base + offset
+
+    def ref(self):
+        return ctypes.byref(self.desc)
 
 
 class Backend:
@@ -299,6 +335,29 @@ class Backend:
 
     def argmax(self, src: Tensor, dst: Tensor) -> None:
         check(lib().mx_argmax(self.h, src.ref(), dst.ref()))
+
+    def rms_norm(self, src: Tensor, dst: Tensor, eps: float, w: Tensor | None = None) -> None:
+        check(lib().mx_rms_norm(self.h, src.ref(), dst.ref(), eps, w.ref() if w is not None else None))
+
+    def add(self, a: Tensor, b: Tensor, dst: Tensor) -> None:
+        check(lib().mx_binary(self.h, OP_ADD, a.ref(), b.ref(), dst.ref()))
+
+    def mul(self, a: Tensor, b: Tensor, dst: Tensor) -> None:
+        check(lib().mx_binary(self.h, OP_MUL, a.ref(), b.ref(), dst.ref()))
+
+    def swiglu(self, a: Tensor, b: Tensor, dst: Tensor) -> None:
+        check(lib().mx_swiglu(self.h, a.ref(), b.ref(), dst.ref()))
+
+    def rope(self, src: Tensor, pos: Tensor, dst: Tensor, n_dims: int, freq_base: float, freq_scale: float = 1.0,
+             mode: int = ROPE_NEOX) -> None:
+        check(lib().mx_rope(self.h, src.ref(), pos.ref(), dst.ref(), n_dims, mode, freq_base, freq_scale, 0.0, 1.0))
+
+    def set_rows(self, src: Tensor, idx: Tensor, dst: Tensor) -> None:
+        check(lib().mx_set_rows(self.h, src.ref(), idx.ref(), dst.ref()))
+
+    def flash_attn_ext(self, q: Tensor, k: Tensor, v: Tensor, mask: Tensor | None, dst: Tensor, scale: float) -> None:
+        check(lib().mx_flash_attn_ext(self.h, q.ref(), k.ref(), v.ref(), mask.ref() if mask is not None else None,
+                                      dst.ref(), scale))
 
     def quantize_act(self, t: int, rounding: int, x: Tensor, k: int, nrows: int) -> Tensor:
         out = Tensor(self, F32, (row_size(t, k) * nrows // 4 + 1,))

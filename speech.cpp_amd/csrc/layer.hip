@@ -1,0 +1,306 @@
+// The decoder layer's other ops on the device (src/common/qwen3-decoder.cpp:350-410): RMS_NORM (with the norm weight's
+// MUL fused when the graph has it next), ADD / MUL with broadcast, GLU SWIGLU, ROPE in NEOX mode, SET_ROWS into the
+// f16 KV cache, and FLASH_ATTN_EXT over that cache. Each restates ggml-cpu's arithmetic for f32 rows:
+//   RMS_NORM: squares rounded to float, summed in double, mean rounded to float, y = x * (1 / sqrtf(mean + eps));
+//   ROPE NEOX: angles p * theta_scale^k formed by the same chain of float products as ggml_rope_cache_init;
+//   SET_ROWS: fp16 of each value, round to nearest even (bit-exact);
+//   FLASH_ATTN_EXT: q rounded to fp16, k.q as an fp32 sum of exact products, online softmax; the V accumulator is
+//                   fp32, as the graph requests with ggml_prec_set_acc(GGML_PREC_F32) (ggml-cpu's own loop keeps it
+//                   in fp16).
+#include "mx_common.h"
+#include "mx_device.h"
+
+namespace mx {
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// ---------------------------------------------------------------------------------------------------------- RMS_NORM
+// One wave per row; rows (i1, i2, i3) of src and dst at their byte strides; w (ne0 floats) multiplies the normalized
+// row when given (the MUL by the norm weight that follows ggml_rms_norm in the graph, with its own rounding).
+__global__ __launch_bounds__(256) void k_rms_norm(RowsArgs a, float eps, const float *w) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= a.nrows) return;  // whole wave
+    const int lane = threadIdx.x & 63;
+    const int64_t i1 = row % a.ne1, i2 = (row / a.ne1) % a.ne2, i3 = row / (a.ne1 * a.ne2);
+    const float *x = (const float *)((const uint8_t *)a.src + i1 * a.s_nb1 + i2 * a.s_nb2 + i3 * a.s_nb3);
+    float *y = (float *)((uint8_t *)a.dst + i1 * a.d_nb1 + i2 * a.d_nb2 + i3 * a.d_nb3);
+    double sum = 0.0;
+    for (int64_t i = lane; i < a.ne0; i += 64) {
+        const float v = x[i];
+        sum += (double)(v * v);
+    }
+    sum = wave_sum_d(sum);
+    const float mean = (float)(sum / (double)a.ne0);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int64_t i = lane; i < a.ne0; i += 64) {
+        const float t = x[i] * scale;
+        y[i] = w ? t * w[i] : t;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------ ADD / MUL
+// dst[i] = a[i] op b[i mod b's shape] (ggml's repeat broadcast), dst contiguous in a's shape.
+__global__ __launch_bounds__(256) void k_binary(BinaryArgs a) {
+    const int64_t n = a.ne[0] * a.ne[1] * a.ne[2] * a.ne[3];
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+        const int64_t i0 = e % a.ne[0], i1 = (e / a.ne[0]) % a.ne[1], i2 = (e / (a.ne[0] * a.ne[1])) % a.ne[2];
+        const int64_t i3 = e / (a.ne[0] * a.ne[1] * a.ne[2]);
+        const float u = *(const float *)((const uint8_t *)a.a + i0 * 4 + i1 * a.a_nb[1] + i2 * a.a_nb[2] +
+                                         i3 * a.a_nb[3]);
+        const float v = *(const float *)((const uint8_t *)a.b + (i0 % a.b_ne[0]) * 4 + (i1 % a.b_ne[1]) * a.b_nb[1] +
+                                         (i2 % a.b_ne[2]) * a.b_nb[2] + (i3 % a.b_ne[3]) * a.b_nb[3]);
+        float *y = (float *)((uint8_t *)a.dst + i0 * 4 + i1 * a.d_nb[1] + i2 * a.d_nb[2] + i3 * a.d_nb[3]);
+        *y = a.op == 0 ? u + v : u * v;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------------------- SWIGLU
+// dst = silu(a) * b, silu(x) = x / (1 + expf(-x)) (ggml_vec_swiglu_f32's scalar form); rows at byte strides.
+__global__ __launch_bounds__(256) void k_swiglu(RowsArgs a, const float *b, int64_t b_nb1) {
+    const int64_t n = a.ne0 * a.nrows;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+        const int64_t i0 = e % a.ne0, r = e / a.ne0;
+        const float u = ((const float *)((const uint8_t *)a.src + r * a.s_nb1))[i0];
+        const float v = ((const float *)((const uint8_t *)b + r * b_nb1))[i0];
+        ((float *)((uint8_t *)a.dst + r * a.d_nb1))[i0] = u / (1.0f + expf(-u)) * v;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------ ROPE NEOX
+// x [ne0, ne1 = heads, ne2 = rows] at byte strides, one position per row. Thread per (pair k, head, row): the angle is
+// p * theta_scale^k by the float chain theta = p; theta *= theta_scale (k times), then times freq_scale.
+__global__ __launch_bounds__(256) void k_rope_neox(RowsArgs a, const int32_t *pos, int n_dims, float theta_scale,
+                                                   float freq_scale) {
+    const int64_t half = n_dims / 2;
+    const int64_t n = half * a.ne1 * a.ne2;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+        const int64_t k = e % half, h = (e / half) % a.ne1, r = e / (half * a.ne1);
+        const float *x = (const float *)((const uint8_t *)a.src + h * a.s_nb1 + r * a.s_nb2);
+        float *y = (float *)((uint8_t *)a.dst + h * a.d_nb1 + r * a.d_nb2);
+        float theta = (float)pos[r];
+        for (int64_t j = 0; j < k; j++) theta *= theta_scale;
+        const float t = freq_scale * theta;
+        const float c = cosf(t), s = sinf(t);
+        const float x0 = x[k], x1 = x[k + half];
+        y[k] = x0 * c - x1 * s;
+        y[k + half] = x0 * s + x1 * c;
+    }
+    // channels past n_dims are copied
+    const int64_t rest = a.ne0 - n_dims;
+    if (rest > 0) {
+        const int64_t m = rest * a.ne1 * a.ne2;
+        for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < m; e += (int64_t)gridDim.x * 256) {
+            const int64_t i = n_dims + e % rest, h = (e / rest) % a.ne1, r = e / (rest * a.ne1);
+            ((float *)((uint8_t *)a.dst + h * a.d_nb1 + r * a.d_nb2))[i] =
+                ((const float *)((const uint8_t *)a.src + h * a.s_nb1 + r * a.s_nb2))[i];
+        }
+    }
+}
+
+// -------------------------------------------------------------------------------------------------------- SET_ROWS
+// dst row idx[i] (f16, byte stride d_nb1) = fp16(src row i); an index outside [0, dst_rows) sets error bit 2 and
+// leaves the cache as it was.
+__global__ __launch_bounds__(256) void k_set_rows_f16(RowsArgs a, const void *idx, int idx_i64, int64_t dst_rows,
+                                                      int *err) {
+    const int64_t n = a.ne0 * a.nrows;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
+        const int64_t i0 = e % a.ne0, r = e / a.ne0;
+        const int64_t d = idx_i64 ? ((const int64_t *)idx)[r] : (int64_t)((const int32_t *)idx)[r];
+        if (d < 0 || d >= dst_rows) {
+            if (i0 == 0) atomicOr(err, 4);
+            continue;
+        }
+        const float v = ((const float *)((const uint8_t *)a.src + r * a.s_nb1))[i0];
+        ((uint16_t *)((uint8_t *)a.dst + d * a.d_nb1))[i0] = f2h(v);
+    }
+}
+
+// -------------------------------------------------------------------------------------------------- FLASH_ATTN_EXT
+// Pass 1: one wave per (kv split, head, query row) runs the online softmax over its split of the positions, 64 at a
+// time (lane j scores position j of the chunk; then each lane accumulates D/64 channels of V over the chunk), and
+// writes (max, sum, D accumulated channels) to the partials -- or, when there is one split, the normalized row to dst.
+// Pass 2 merges the splits of each (head, row).
+template <int D>
+__global__ __launch_bounds__(64) void k_fa_split(FaArgs a) {
+    static_assert(D == 64 || D == 128, "head size 64 or 128");
+    constexpr int DL = D / 64;  // channels per lane
+    __shared__ float qs[D];
+    __shared__ float ps[64];
+    const int lane = threadIdx.x;
+    const int64_t split = blockIdx.x, h = blockIdx.y, i = blockIdx.z;
+    const int64_t hk = h / a.gqa;
+    const float *q = (const float *)((const uint8_t *)a.q + i * a.q_nb1 + h * a.q_nb2);
+    for (int d = lane; d < D; d += 64) qs[d] = h2f(f2h(q[d]));  // ggml converts q to K's f16 first
+    __syncthreads();
+    const uint8_t *kb = (const uint8_t *)a.k + hk * a.k_nb2;
+    const uint8_t *vb = (const uint8_t *)a.v + hk * a.v_nb2;
+    const uint16_t *mrow = a.mask ? (const uint16_t *)((const uint8_t *)a.mask + i * a.m_nb1) : nullptr;
+    const int64_t j0 = split * a.split_len, j1 = min(a.n_kv, j0 + a.split_len);
+
+    float M = -INFINITY, S = 0.0f;
+    float acc[DL];
+#pragma unroll
+    for (int c = 0; c < DL; c++) acc[c] = 0.0f;
+    for (int64_t base = j0; base < j1; base += 64) {
+        const int64_t j = base + lane;
+        float s = -INFINITY;
+        if (j < j1) {
+            const float mv = mrow ? h2f(mrow[j]) : 0.0f;
+            if (mv != -INFINITY) {
+                const uint4 *kr = (const uint4 *)(kb + j * a.k_nb1);
+                float dot = 0.0f;
+#pragma unroll
+                for (int c = 0; c < D / 8; c++) {
+                    const uint4 w = kr[c];
+                    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        dot = fmaf(h2f((uint16_t)(wv[t] & 0xFFFF)), qs[8 * c + 2 * t], dot);
+                        dot = fmaf(h2f((uint16_t)(wv[t] >> 16)), qs[8 * c + 2 * t + 1], dot);
+                    }
+                }
+                s = dot * a.scale + mv;
+            }
+        }
+        const float mc = wave_max_f(s);
+        if (mc == -INFINITY) continue;  // every position of the chunk masked (uniform)
+        const float Mn = fmaxf(M, mc);
+        const float r = expf(M - Mn);   // 0 while M is -inf
+        const float p = s == -INFINITY ? 0.0f : expf(s - Mn);
+        S = S * r + wave_sum_f(p);
+#pragma unroll
+        for (int c = 0; c < DL; c++) acc[c] *= r;
+        M = Mn;
+        ps[lane] = p;
+        __syncthreads();
+        const int64_t nj = min((int64_t)64, j1 - base);
+        for (int64_t t = 0; t < nj; t++) {
+            const float pt = ps[t];
+            if (pt == 0.0f) continue;  // uniform
+            const uint16_t *vr = (const uint16_t *)(vb + (base + t) * a.v_nb1);
+#pragma unroll
+            for (int c = 0; c < DL; c++) acc[c] = fmaf(pt, h2f(vr[lane + 64 * c]), acc[c]);
+        }
+        __syncthreads();
+    }
+    if (a.nsplit == 1) {
+        float *o = a.dst + (i * a.n_head + h) * D;
+        const float inv = S == 0.0f ? 0.0f : 1.0f / S;
+#pragma unroll
+        for (int c = 0; c < DL; c++) o[lane + 64 * c] = acc[c] * inv;
+        return;
+    }
+    float *part = a.part + ((i * a.n_head + h) * a.nsplit + split) * (D + 2);
+#pragma unroll
+    for (int c = 0; c < DL; c++) part[2 + lane + 64 * c] = acc[c];
+    if (lane == 0) {
+        part[0] = M;
+        part[1] = S;
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void k_fa_merge(FaArgs a) {
+    constexpr int DL = D / 64;
+    const int lane = threadIdx.x;
+    const int64_t h = blockIdx.x, i = blockIdx.y;
+    const float *part = a.part + (i * a.n_head + h) * a.nsplit * (D + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < a.nsplit; s++) M = fmaxf(M, part[s * (D + 2)]);
+    float S = 0.0f, acc[DL];
+#pragma unroll
+    for (int c = 0; c < DL; c++) acc[c] = 0.0f;
+    if (M != -INFINITY) {
+        for (int s = 0; s < a.nsplit; s++) {
+            const float *ps = part + s * (D + 2);
+            if (ps[0] == -INFINITY) continue;
+            const float r = expf(ps[0] - M);
+            S = fmaf(ps[1], r, S);
+#pragma unroll
+            for (int c = 0; c < DL; c++) acc[c] = fmaf(ps[2 + lane + 64 * c], r, acc[c]);
+        }
+    }
+    float *o = a.dst + (i * a.n_head + h) * D;
+    const float inv = S == 0.0f ? 0.0f : 1.0f / S;
+#pragma unroll
+    for (int c = 0; c < DL; c++) o[lane + 64 * c] = acc[c] * inv;
+}
+
+// ---------------------------------------------------------------------------------------------------------- launches
+static unsigned grid_for(int64_t n) {
+    const int64_t g = (n + 255) / 256;
+    return (unsigned)(g < 1 ? 1 : (g > 65535 ? 65535 : g));
+}
+
+hipError_t launch_rms_norm(const RowsArgs &a, float eps, const float *w, hipStream_t s) {
+    if (a.nrows == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)((a.nrows + 3) / 4)), dim3(256), 0, s, a, eps, w);
+    return hipGetLastError();
+}
+
+hipError_t launch_binary(const BinaryArgs &a, hipStream_t s) {
+    const int64_t n = a.ne[0] * a.ne[1] * a.ne[2] * a.ne[3];
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_binary, dim3(grid_for(n)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const RowsArgs &a, const float *b, int64_t b_nb1, hipStream_t s) {
+    const int64_t n = a.ne0 * a.nrows;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_swiglu, dim3(grid_for(n)), dim3(256), 0, s, a, b, b_nb1);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_neox(const RowsArgs &a, const int32_t *pos, int n_dims, float theta_scale, float freq_scale,
+                            hipStream_t s) {
+    const int64_t n = (int64_t)(n_dims / 2) * a.ne1 * a.ne2;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rope_neox, dim3(grid_for(n)), dim3(256), 0, s, a, pos, n_dims, theta_scale, freq_scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_set_rows_f16(const RowsArgs &a, const void *idx, bool idx_i64, int64_t dst_rows, int *err,
+                               hipStream_t s) {
+    const int64_t n = a.ne0 * a.nrows;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_set_rows_f16, dim3(grid_for(n)), dim3(256), 0, s, a, idx, (int)idx_i64, dst_rows, err);
+    return hipGetLastError();
+}
+
+int fa_splits(int64_t n_q, int64_t n_head, int64_t n_kv) {
+    // enough waves for the chip: about 512 (split, head, row) waves, splits of at least 64 positions
+    int64_t nsplit = 1;
+    while (nsplit < 64 && n_q * n_head * nsplit < 512 && (n_kv + 2 * nsplit - 1) / (2 * nsplit) >= 64) nsplit *= 2;
+    return (int)nsplit;
+}
+
+hipError_t launch_flash_attn(const FaArgs &a, hipStream_t s) {
+    if (a.n_q == 0 || a.n_head == 0) return hipSuccess;
+    const dim3 g1((unsigned)a.nsplit, (unsigned)a.n_head, (unsigned)a.n_q);
+    if (a.D == 128) hipLaunchKernelGGL(k_fa_split<128>, g1, dim3(64), 0, s, a);
+    else if (a.D == 64) hipLaunchKernelGGL(k_fa_split<64>, g1, dim3(64), 0, s, a);
+    else return hipErrorInvalidValue;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.nsplit == 1) return e;
+    const dim3 g2((unsigned)a.n_head, (unsigned)a.n_q);
+    if (a.D == 128) hipLaunchKernelGGL(k_fa_merge<128>, g2, dim3(64), 0, s, a);
+    else hipLaunchKernelGGL(k_fa_merge<64>, g2, dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace mx

@@ -2,6 +2,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -15,7 +16,8 @@ struct mx_backend {
     int device = 0;
     hipStream_t stream = nullptr;
     int rounding = MX_ROUND_REF;
-    int *err = nullptr;              // device word: bit 0 GET_ROWS index out of range, bit 1 MUL_MAT_ID expert out of range
+    int *err = nullptr;              // device word: bit 0 GET_ROWS index, bit 1 MUL_MAT_ID expert, bit 2 SET_ROWS index
+                                     // out of range
     void *scratch = nullptr;         // grows on demand outside graph capture
     size_t scratch_size = 0;
     uint8_t *staging = nullptr;      // device staging for ggml-layout uploads and downloads
@@ -268,8 +270,9 @@ MX_API int mx_backend_synchronize(mx_backend *be) {
     if (flag) {
         const int zero = 0;
         HIP_OK(hipMemcpy(be->err, &zero, sizeof zero, hipMemcpyHostToDevice), "clear error word");
-        return fail(MX_INVALID, "%s%s", (flag & 1) ? "GET_ROWS met a row index out of range; its rows are zero. " : "",
-                    (flag & 2) ? "MUL_MAT_ID met an expert index out of range; its pairs were skipped." : "");
+        return fail(MX_INVALID, "%s%s%s", (flag & 1) ? "GET_ROWS met a row index out of range; its rows are zero. " : "",
+                    (flag & 2) ? "MUL_MAT_ID met an expert index out of range; its pairs were skipped. " : "",
+                    (flag & 4) ? "SET_ROWS met a row index out of range; those rows were not written." : "");
     }
     return MX_SUCCESS;
 }
@@ -403,9 +406,64 @@ MX_API int mx_tensor_copy(mx_backend *be, const mx_tensor *src, const mx_tensor 
     return MX_SUCCESS;
 }
 
+// f32 rows: ne0 contiguous floats, rows anywhere (the layer ops index rows at byte strides).
+static bool f32_any(const mx_tensor *t) {
+    return t && t->type == MX_TYPE_F32 && shape_ok(t) && t->nb[0] == 4 && t->data && ((uintptr_t)t->data & 3) == 0 &&
+           t->nb[1] % 4 == 0 && t->nb[2] % 4 == 0 && t->nb[3] % 4 == 0;
+}
+static bool same_shape(const mx_tensor *a, const mx_tensor *b) {
+    return a->ne[0] == b->ne[0] && a->ne[1] == b->ne[1] && a->ne[2] == b->ne[2] && a->ne[3] == b->ne[3];
+}
+static mx::RowsArgs rows_of(const mx_tensor *src, const mx_tensor *dst) {
+    mx::RowsArgs r{};
+    r.src = src->data;
+    r.dst = dst->data;
+    r.ne0 = src->ne[0];
+    r.ne1 = src->ne[1];
+    r.ne2 = src->ne[2];
+    r.nrows = src->ne[1] * src->ne[2] * src->ne[3];
+    r.s_nb1 = (int64_t)src->nb[1];
+    r.s_nb2 = (int64_t)src->nb[2];
+    r.s_nb3 = (int64_t)src->nb[3];
+    r.d_nb1 = (int64_t)dst->nb[1];
+    r.d_nb2 = (int64_t)dst->nb[2];
+    r.d_nb3 = (int64_t)dst->nb[3];
+    return r;
+}
+
+// The row-wise layer ops: RMS_NORM (src0, optional weight src1), ADD / MUL (a = src0, b = src1), SWIGLU (a, b),
+// SET_ROWS (src0 rows, src1 indices, dst f16 rows).
+static int supports_layer_op(int op, const mx_tensor *src0, const mx_tensor *src1, const mx_tensor *dst) {
+    switch (op) {
+        case MX_OP_RMS_NORM:
+            if (!f32_any(src0) || !f32_any(dst) || !same_shape(src0, dst) || src0->ne[0] < 1) return 0;
+            return !src1 || (f32_any(src1) && src1->ne[0] == src0->ne[0] && nelements(src1) == src1->ne[0]);
+        case MX_OP_ADD:
+        case MX_OP_MUL:
+            if (!f32_any(src0) || !f32_any(src1) || !f32_any(dst) || !same_shape(src0, dst)) return 0;
+            for (int i = 0; i < 4; i++)
+                if (src1->ne[i] < 1 || src0->ne[i] % src1->ne[i] != 0) return 0;
+            return 1;
+        case MX_OP_SWIGLU:
+            return f32_any(src0) && f32_any(src1) && f32_any(dst) && same_shape(src0, src1) && same_shape(src0, dst) &&
+                   src0->ne[2] == 1 && src0->ne[3] == 1;
+        case MX_OP_SET_ROWS: {
+            if (!f32_any(src0) || src0->ne[2] != 1 || src0->ne[3] != 1) return 0;
+            if (!src1 || (src1->type != MX_TYPE_I32 && src1->type != 27) || !src1->data || !shape_ok(src1) ||
+                src1->ne[0] != src0->ne[1] || nelements(src1) != src1->ne[0] || src1->nb[0] != (src1->type == 27 ? 8u : 4u))
+                return 0;
+            return dst && dst->type == MX_TYPE_F16 && shape_ok(dst) && dst->nb[0] == 2 && dst->data &&
+                   ((uintptr_t)dst->data & 1) == 0 && dst->ne[0] == src0->ne[0] && dst->ne[2] == 1 && dst->ne[3] == 1 &&
+                   dst->nb[1] % 2 == 0;
+        }
+        default: return 0;
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------- ops
 MX_API int mx_supports_op(int op, const mx_tensor *src0, const mx_tensor *src1, const mx_tensor *src2,
                           const mx_tensor *dst) {
+    if (op >= MX_OP_RMS_NORM && op <= MX_OP_SET_ROWS) return supports_layer_op(op, src0, src1, dst);
     if (op == MX_OP_ARGMAX) {  // f32 rows in, one I32 per row out
         if (!src0 || src0->type != MX_TYPE_F32 || !shape_ok(src0) || src0->nb[0] != 4 || src0->nb[1] % 16 != 0 ||
             !src0->data || !aligned16(src0->data) || src0->ne[2] != 1 || src0->ne[3] != 1)
@@ -733,6 +791,137 @@ MX_API int mx_argmax(mx_backend *be, const mx_tensor *src, const mx_tensor *dst)
     HIP_OK(mx::launch_argmax((const float *)src->data, src->ne[0], src->ne[1], (int64_t)src->nb[1],
                              (int32_t *)dst->data, (int64_t)dst->nb[0], be->stream),
            "ARGMAX launch");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_rms_norm(mx_backend *be, const mx_tensor *src, const mx_tensor *dst, float eps, const mx_tensor *w) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!supports_layer_op(MX_OP_RMS_NORM, src, w, dst)) return fail(MX_UNSUPPORTED, "RMS_NORM: unsupported tensors");
+    HIP_OK(mx::launch_rms_norm(rows_of(src, dst), eps, w ? (const float *)w->data : nullptr, be->stream),
+           "RMS_NORM launch");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_binary(mx_backend *be, int op, const mx_tensor *a, const mx_tensor *b, const mx_tensor *dst) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if ((op != MX_OP_ADD && op != MX_OP_MUL) || !supports_layer_op(op, a, b, dst))
+        return fail(MX_UNSUPPORTED, "ADD / MUL: unsupported op or tensors");
+    mx::BinaryArgs x{};
+    x.op = op == MX_OP_ADD ? 0 : 1;
+    x.a = (const float *)a->data;
+    x.b = (const float *)b->data;
+    x.dst = (float *)dst->data;
+    for (int i = 0; i < 4; i++) {
+        x.ne[i] = a->ne[i];
+        x.a_nb[i] = (int64_t)a->nb[i];
+        x.b_ne[i] = b->ne[i];
+        x.b_nb[i] = (int64_t)b->nb[i];
+        x.d_nb[i] = (int64_t)dst->nb[i];
+    }
+    HIP_OK(mx::launch_binary(x, be->stream), "ADD / MUL launch");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_swiglu(mx_backend *be, const mx_tensor *a, const mx_tensor *b, const mx_tensor *dst) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!supports_layer_op(MX_OP_SWIGLU, a, b, dst)) return fail(MX_UNSUPPORTED, "SWIGLU: unsupported tensors");
+    HIP_OK(mx::launch_swiglu(rows_of(a, dst), (const float *)b->data, (int64_t)b->nb[1], be->stream), "SWIGLU launch");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_supports_rope(const mx_tensor *src, const mx_tensor *pos, const mx_tensor *dst, int n_dims, int mode,
+                            float ext_factor, float attn_factor) {
+    if (!f32_any(src) || !f32_any(dst) || !same_shape(src, dst) || src->ne[3] != 1) return 0;
+    if (!pos || pos->type != MX_TYPE_I32 || !pos->data || pos->nb[0] != 4 || pos->ne[0] != src->ne[2] ||
+        nelements(pos) != pos->ne[0])
+        return 0;
+    // GGML_ROPE_TYPE_NEOX (2) with the decoder's plain arguments
+    return mode == 2 && n_dims > 0 && n_dims % 2 == 0 && n_dims <= src->ne[0] && ext_factor == 0.0f &&
+           attn_factor == 1.0f;
+}
+
+MX_API int mx_rope(mx_backend *be, const mx_tensor *src, const mx_tensor *pos, const mx_tensor *dst, int n_dims,
+                   int mode, float freq_base, float freq_scale, float ext_factor, float attn_factor) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!mx_supports_rope(src, pos, dst, n_dims, mode, ext_factor, attn_factor))
+        return fail(MX_UNSUPPORTED, "ROPE: unsupported mode, parameters or tensors");
+    // ggml_compute_forward_rope: theta_scale = powf(freq_base, -2.0f/n_dims), on the host as ggml-cpu forms it
+    const float theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    HIP_OK(mx::launch_rope_neox(rows_of(src, dst), (const int32_t *)pos->data, n_dims, theta_scale, freq_scale,
+                                be->stream),
+           "ROPE launch");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_set_rows(mx_backend *be, const mx_tensor *src, const mx_tensor *idx, const mx_tensor *dst) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!supports_layer_op(MX_OP_SET_ROWS, src, idx, dst)) return fail(MX_UNSUPPORTED, "SET_ROWS: unsupported tensors");
+    mx::RowsArgs r = rows_of(src, dst);
+    HIP_OK(mx::launch_set_rows_f16(r, idx->data, idx->type == 27, dst->ne[1], be->err, be->stream), "SET_ROWS launch");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_supports_flash_attn_ext(const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
+                                      const mx_tensor *mask, const mx_tensor *dst, float max_bias,
+                                      float logit_softcap) {
+    if (max_bias != 0.0f || logit_softcap != 0.0f) return 0;
+    if (!f32_any(q) || q->ne[3] != 1) return 0;
+    const int64_t D = q->ne[0];
+    if (D != 64 && D != 128) return 0;
+    for (const mx_tensor *t : {k, v}) {
+        if (!t || t->type != MX_TYPE_F16 || !shape_ok(t) || t->nb[0] != 2 || !t->data || t->ne[0] != D ||
+            t->ne[3] != 1 || !aligned16(t->data) || t->nb[1] % 16 != 0 || t->nb[2] % 16 != 0)
+            return 0;
+    }
+    if (k->ne[1] != v->ne[1] || k->ne[2] != v->ne[2] || k->ne[2] < 1 || q->ne[2] % k->ne[2] != 0) return 0;
+    if (mask && (mask->type != MX_TYPE_F16 || !shape_ok(mask) || mask->nb[0] != 2 || !mask->data ||
+                 mask->ne[0] < k->ne[1] || mask->ne[1] < q->ne[1] || mask->ne[2] != 1 || mask->ne[3] != 1 ||
+                 ((uintptr_t)mask->data & 1)))
+        return 0;
+    // the permuted output: dst [D, n_head, n_q] contiguous
+    return dst && dst->type == MX_TYPE_F32 && dst->ne[0] == D && dst->ne[1] == q->ne[2] && dst->ne[2] == q->ne[1] &&
+           dst->ne[3] == 1 && contiguous(dst) && dst->data && q->ne[1] <= 65535 && q->ne[2] <= 65535;
+}
+
+MX_API int mx_flash_attn_ext(mx_backend *be, const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
+                             const mx_tensor *mask, const mx_tensor *dst, float scale) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!mx_supports_flash_attn_ext(q, k, v, mask, dst, 0.0f, 0.0f))
+        return fail(MX_UNSUPPORTED, "FLASH_ATTN_EXT: unsupported tensors");
+    mx::FaArgs a{};
+    a.q = (const float *)q->data;
+    a.k = k->data;
+    a.v = v->data;
+    a.mask = mask ? mask->data : nullptr;
+    a.dst = (float *)dst->data;
+    a.D = (int)q->ne[0];
+    a.n_q = q->ne[1];
+    a.n_head = q->ne[2];
+    a.n_kv = k->ne[1];
+    a.gqa = q->ne[2] / k->ne[2];
+    a.q_nb1 = (int64_t)q->nb[1];
+    a.q_nb2 = (int64_t)q->nb[2];
+    a.k_nb1 = (int64_t)k->nb[1];
+    a.k_nb2 = (int64_t)k->nb[2];
+    a.v_nb1 = (int64_t)v->nb[1];
+    a.v_nb2 = (int64_t)v->nb[2];
+    a.m_nb1 = mask ? (int64_t)mask->nb[1] : 0;
+    a.scale = scale;
+    a.nsplit = mx::fa_splits(a.n_q, a.n_head, a.n_kv);
+    a.split_len = (a.n_kv + a.nsplit - 1) / a.nsplit;
+    a.split_len = (a.split_len + 63) / 64 * 64;
+    if (a.nsplit > 1) {
+        const size_t need = (size_t)a.n_q * (size_t)a.n_head * (size_t)a.nsplit * (size_t)(a.D + 2) * 4;
+        if ((rc = ensure_scratch(be, need))) return rc;
+        a.part = (float *)be->scratch;
+    }
+    HIP_OK(mx::launch_flash_attn(a, be->stream), "FLASH_ATTN_EXT launch");
     return MX_SUCCESS;
 }
 

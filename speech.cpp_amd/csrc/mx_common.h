@@ -241,6 +241,44 @@ struct MulMatIdArgs {
     int64_t max_tiles;
     int *err;
 };
+// Row-wise ops on f32 rows (layer.hip): src / dst rows (i1, i2, i3) at byte strides, ne0 contiguous floats.
+struct RowsArgs {
+    const void *src;
+    void *dst;
+    int64_t ne0, ne1, ne2, nrows;         // nrows = ne1 * ne2 * ne3
+    int64_t s_nb1, s_nb2, s_nb3, d_nb1, d_nb2, d_nb3;
+};
+hipError_t launch_rms_norm(const RowsArgs &a, float eps, const float *w, hipStream_t s);
+hipError_t launch_swiglu(const RowsArgs &a, const float *b, int64_t b_nb1, hipStream_t s);
+// x [ne0, ne1 heads, ne2 rows] (s_nb1: head stride, s_nb2: row stride) rotated pairwise, NEOX layout.
+hipError_t launch_rope_neox(const RowsArgs &a, const int32_t *pos, int n_dims, float theta_scale, float freq_scale,
+                            hipStream_t s);
+// f32 rows into f16 rows idx[r] of dst (d_nb1 bytes apart, dst_rows rows); a bad index sets *err |= 4.
+hipError_t launch_set_rows_f16(const RowsArgs &a, const void *idx, bool idx_i64, int64_t dst_rows, int *err,
+                               hipStream_t s);
+// dst = a op b (op 0 add, 1 mul), b repeated over a's shape; byte strides, ne0 contiguous.
+struct BinaryArgs {
+    int op;
+    const float *a, *b;
+    float *dst;
+    int64_t ne[4], a_nb[4], b_ne[4], b_nb[4], d_nb[4];
+};
+hipError_t launch_binary(const BinaryArgs &a, hipStream_t s);
+// Flash attention over f16 K / V: q rows (i, h) at q + i q_nb1 + h q_nb2 (f32), K / V position j of kv head hk at
+// k + j k_nb1 + hk k_nb2 (f16), mask row i at mask + i m_nb1 (f16, may be null); dst [D, n_head, n_q] contiguous.
+// nsplit > 1 needs part: n_q * n_head * nsplit * (D + 2) floats.
+struct FaArgs {
+    const float *q;
+    const void *k, *v, *mask;
+    float *dst, *part;
+    int D, nsplit;
+    int64_t n_q, n_head, n_kv, gqa, split_len;
+    int64_t q_nb1, q_nb2, k_nb1, k_nb2, v_nb1, v_nb2, m_nb1;
+    float scale;
+};
+int fa_splits(int64_t n_q, int64_t n_head, int64_t n_kv);
+hipError_t launch_flash_attn(const FaArgs &a, hipStream_t s);
+
 // ARGMAX (first of equal values) over nrows rows of ne0 floats (row stride nb1 bytes) into dst (stride dst_nb0 bytes).
 hipError_t launch_argmax(const float *src, int64_t ne0, int64_t nrows, int64_t nb1, int32_t *dst, int64_t dst_nb0,
                          hipStream_t s);

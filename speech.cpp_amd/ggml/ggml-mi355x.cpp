@@ -67,6 +67,24 @@ mx_tensor desc(const ggml_tensor *t) {
     return d;
 }
 
+// Operation parameters as ggml stores them in op_params (ggml.c: ggml_rms_norm_impl eps at 0; ggml_rope_impl n_dims
+// at 1, mode at 2, freq_base .. attn_factor at 5..8; ggml_flash_attn_ext scale, max_bias, logit_softcap at 0..2;
+// ggml_glu_impl the GLU op at 0 and `swapped` at 1).
+float op_f32(const ggml_tensor *t, int i) {
+    float v;
+    std::memcpy(&v, &t->op_params[i], sizeof v);
+    return v;
+}
+
+// The descriptor of a tensor the scheduler is still planning (no memory yet): an aligned placeholder address, so that
+// libmx checks shapes, strides and alignment as it will find them (this buffer type's allocations are 256-aligned).
+mx_tensor planned(const ggml_tensor *t) {
+    alignas(256) static const char placeholder[256] = {};
+    mx_tensor d = desc(t);
+    if (!d.data) d.data = (void *)placeholder;
+    return d;
+}
+
 enum ggml_status to_status(int rc) {
     if (rc == MX_SUCCESS) return GGML_STATUS_SUCCESS;
     if (rc == MX_ALLOC_FAILED) return GGML_STATUS_ALLOC_FAILED;
@@ -249,6 +267,39 @@ int run_nodes(BackendCtx *ctx, ggml_cgraph *cgraph) {
                 rc = mx_argmax(ctx->be, &s0, &d);
                 break;
             }
+            case GGML_OP_RMS_NORM: {
+                const mx_tensor s0 = desc(node->src[0]), d = desc(node);
+                rc = mx_rms_norm(ctx->be, &s0, &d, op_f32(node, 0), nullptr);
+                break;
+            }
+            case GGML_OP_ADD:
+            case GGML_OP_MUL: {
+                const mx_tensor a = desc(node->src[0]), b = desc(node->src[1]), d = desc(node);
+                rc = mx_binary(ctx->be, node->op == GGML_OP_ADD ? MX_OP_ADD : MX_OP_MUL, &a, &b, &d);
+                break;
+            }
+            case GGML_OP_GLU: {
+                const mx_tensor a = desc(node->src[0]), b = desc(node->src[1]), d = desc(node);
+                rc = mx_swiglu(ctx->be, &a, &b, &d);
+                break;
+            }
+            case GGML_OP_ROPE: {
+                const mx_tensor x = desc(node->src[0]), pos = desc(node->src[1]), d = desc(node);
+                rc = mx_rope(ctx->be, &x, &pos, &d, node->op_params[1], node->op_params[2], op_f32(node, 5),
+                             op_f32(node, 6), op_f32(node, 7), op_f32(node, 8));
+                break;
+            }
+            case GGML_OP_SET_ROWS: {
+                const mx_tensor src = desc(node->src[0]), idx = desc(node->src[1]), d = desc(node);
+                rc = mx_set_rows(ctx->be, &src, &idx, &d);
+                break;
+            }
+            case GGML_OP_FLASH_ATTN_EXT: {
+                const mx_tensor q = desc(node->src[0]), k = desc(node->src[1]), v = desc(node->src[2]), d = desc(node);
+                const mx_tensor m = node->src[3] ? desc(node->src[3]) : mx_tensor{};
+                rc = mx_flash_attn_ext(ctx->be, &q, &k, &v, node->src[3] ? &m : nullptr, &d, op_f32(node, 0));
+                break;
+            }
             default:
                 GGML_LOG_ERROR("%s: op %s is not computed by the MI355X backend\n", __func__, ggml_op_desc(node));
                 return MX_UNSUPPORTED;
@@ -376,9 +427,47 @@ bool in_our_buffer(const ggml_tensor *t, ggml_backend_dev_t dev) {
 
 // True exactly for MUL_MAT / MUL_MAT_ID / GET_ROWS whose weight lives in this device's buffer type -- Q8_0, Q4_K,
 // Q5_K, Q6_K for all three; F16 / F32 (the storages of storage.cpp:52-89 besides the K-quants) for MUL_MAT and
-// GET_ROWS -- and for ARGMAX over f32 logits in it (the greedy pick after the head, qwen3-decoder.cpp:428,501), with
-// the shapes and strides libmx computes; everything else stays on the CPU backend.
+// GET_ROWS --, for ARGMAX over f32 logits in it (the greedy pick after the head, qwen3-decoder.cpp:428,501), and for
+// the decoder layer's RMS_NORM, ADD, MUL, GLU (swiglu), ROPE (NEOX), SET_ROWS and FLASH_ATTN_EXT over a KV cache in
+// it, with the shapes, strides and parameters libmx computes; everything else stays on the CPU backend.
 bool dev_supports_op(ggml_backend_dev_t dev, const ggml_tensor *op) {
+    // the decoder layer's other ops (qwen3-decoder.cpp:350-410): f32 rows wherever they live (the scheduler copies
+    // inputs), except the KV cache, which SET_ROWS writes and FLASH_ATTN_EXT reads in place and must be this device's
+    switch (op->op) {
+        case GGML_OP_RMS_NORM: {
+            const mx_tensor s0 = planned(op->src[0]), d = planned(op);
+            return mx_supports_op(MX_OP_RMS_NORM, &s0, nullptr, nullptr, &d) != 0;
+        }
+        case GGML_OP_ADD:
+        case GGML_OP_MUL: {
+            const mx_tensor a = planned(op->src[0]), b = planned(op->src[1]), d = planned(op);
+            return mx_supports_op(op->op == GGML_OP_ADD ? MX_OP_ADD : MX_OP_MUL, &a, &b, nullptr, &d) != 0;
+        }
+        case GGML_OP_GLU: {
+            // the split form ggml_swiglu_split(a, b), not swapped
+            if (ggml_get_glu_op(op) != GGML_GLU_OP_SWIGLU || !op->src[1] || op->op_params[1] != 0) return false;
+            const mx_tensor a = planned(op->src[0]), b = planned(op->src[1]), d = planned(op);
+            return mx_supports_op(MX_OP_SWIGLU, &a, &b, nullptr, &d) != 0;
+        }
+        case GGML_OP_ROPE: {
+            if (op->src[2]) return false;  // frequency factors
+            const mx_tensor x = planned(op->src[0]), pos = planned(op->src[1]), d = planned(op);
+            return mx_supports_rope(&x, &pos, &d, op->op_params[1], op->op_params[2], op_f32(op, 7), op_f32(op, 8)) != 0;
+        }
+        case GGML_OP_SET_ROWS: {
+            if (!in_our_buffer(op->view_src ? op->view_src : op, dev)) return false;
+            const mx_tensor src = planned(op->src[0]), idx = planned(op->src[1]), d = planned(op);
+            return mx_supports_op(MX_OP_SET_ROWS, &src, &idx, nullptr, &d) != 0;
+        }
+        case GGML_OP_FLASH_ATTN_EXT: {
+            if (op->src[4] || !in_our_buffer(op->src[1], dev) || !in_our_buffer(op->src[2], dev)) return false;  // sinks
+            const mx_tensor q = planned(op->src[0]), k = planned(op->src[1]), v = planned(op->src[2]), d = planned(op);
+            const mx_tensor m = op->src[3] ? planned(op->src[3]) : mx_tensor{};
+            return mx_supports_flash_attn_ext(&q, &k, &v, op->src[3] ? &m : nullptr, &d, op_f32(op, 1),
+                                              op_f32(op, 2)) != 0;
+        }
+        default: break;
+    }
     if (op->op == GGML_OP_ARGMAX) {
         const ggml_tensor *x = op->src[0];
         if (!in_our_buffer(x, dev)) return false;

@@ -1,0 +1,157 @@
+"""The decoder layer's other ops on MI355X against the oracle: RMS_NORM (alone and with the norm weight fused),
+ADD / MUL, SWIGLU, ROPE NEOX, SET_ROWS into the f16 cache, and FLASH_ATTN_EXT over cache views as the decoder builds
+them (qwen3-decoder.cpp:350-410).
+
+Bars: SET_ROWS, ADD and MUL bit-exact; RMS_NORM within one float ulp (the CPU sums in double; so does the kernel, in
+another order); SWIGLU and ROPE within 2e-6 (expf / sinf / cosf of the device's math library); FLASH_ATTN_EXT within
+1e-5 of the row's largest output against the exact attention (fp32 V sum, as the graph's GGML_PREC_F32 asks), and
+no further from ggml-cpu's own loop, whose V accumulator is fp16, than that loop is from the exact attention."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(mx, be, x, t=None):
+    x = np.ascontiguousarray(x)
+    t = t if t is not None else mx.F32
+    return be.tensor(t, tuple(reversed(x.shape)), x)
+
+
+def out(mx, be, shape):
+    return be.tensor(mx.F32, tuple(reversed(shape)))
+
+
+def ulps(a, b):
+    ai = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+    bi = np.ascontiguousarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(ai - bi).max()
+
+
+@pytest.mark.parametrize("shape", [(7, 1024), (3, 16, 128), (2, 2048)])
+def test_rms_norm(mx, be, shape):
+    x = O.fill_normal(0x1A00 + shape[-1], int(np.prod(shape[:-1])), shape[-1]).reshape(shape)
+    X, Y = dev(mx, be, x), out(mx, be, shape)
+    be.rms_norm(X, Y, 1e-6)
+    be.sync()
+    ref = O.rms_norm(x, 1e-6)
+    got = Y.numpy().reshape(shape)
+    assert ulps(got, ref) <= 1
+    w = O.fill_normal(0x1B00, 1, shape[-1])[0]
+    W, Z = dev(mx, be, w), out(mx, be, shape)
+    be.rms_norm(X, Z, 1e-6, W)
+    be.sync()
+    assert ulps(Z.numpy().reshape(shape), O.binary("mul", ref, w)) <= 2
+
+
+def test_add_mul_broadcast(mx, be):
+    a = O.fill_normal(0x1C00, 6, 1024)
+    for b in (O.fill_normal(0x1C01, 1, 1024), O.fill_normal(0x1C02, 3, 1024), O.fill_normal(0x1C03, 6, 1024)):
+        A, B = dev(mx, be, a), dev(mx, be, b)
+        for op, fn in (("add", be.add), ("mul", be.mul)):
+            Y = out(mx, be, a.shape)
+            fn(A, B, Y)
+            be.sync()
+            assert np.array_equal(Y.numpy().reshape(a.shape), O.binary(op, a, b))
+
+
+def test_swiglu(mx, be):
+    a = O.fill_normal(0x1D00, 5, 3072) * np.float32(4)
+    b = O.fill_normal(0x1D01, 5, 3072)
+    A, B, Y = dev(mx, be, a), dev(mx, be, b), out(mx, be, a.shape)
+    be.swiglu(A, B, Y)
+    be.sync()
+    ref = O.swiglu(a, b)
+    assert np.abs(Y.numpy().reshape(a.shape) - ref).max() <= 2e-6 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("n_dims", [128, 64])
+def test_rope_neox(mx, be, n_dims):
+    rows, heads, D = 6, 16, 128
+    x = O.fill_normal(0x1E00, rows * heads, D).reshape(rows, heads, D)
+    pos = np.array([0, 1, 37, 1000, 4095, 70000], np.int32)
+    X, P, Y = dev(mx, be, x), dev(mx, be, pos, mx.I32), out(mx, be, x.shape)
+    be.rope(X, P, Y, n_dims, 1e6)
+    be.sync()
+    ref = O.rope_neox(x, pos, n_dims, 1e6)
+    assert np.abs(Y.numpy().reshape(x.shape) - ref).max() <= 2e-6
+
+
+def test_set_rows_into_f16_cache(mx, be):
+    kv_dim, cap = 1024, 64
+    cache = (O.fill_normal(0x1F00, cap, kv_dim)).astype(np.float16).view(np.uint16)
+    src = O.fill_normal(0x1F01, 3, kv_dim) * np.float32(50)
+    idx = np.array([63, 0, 17], np.int32)
+    C = dev(mx, be, cache, mx.F16)
+    S, I = dev(mx, be, src), dev(mx, be, idx, mx.I32)
+    be.set_rows(S, I, C)
+    be.sync()
+    got = np.frombuffer(C.get_bytes().tobytes(), np.uint16).reshape(cap, kv_dim)
+    assert np.array_equal(got, O.set_rows_f16(cache, src, idx))
+    bad = dev(mx, be, np.array([5, cap, 1], np.int32), mx.I32)
+    be.set_rows(S, bad, C)
+    with pytest.raises(mx.MxError) as e:
+        be.sync()
+    assert e.value.code == mx.INVALID
+    got2 = np.frombuffer(C.get_bytes().tobytes(), np.uint16).reshape(cap, kv_dim)
+    want = O.set_rows_f16(O.set_rows_f16(cache, src, idx), src[[0, 2]], np.array([5, 1], np.int32))
+    assert np.array_equal(got2, want)
+
+
+def fa_device(mx, be, n_head, n_kv_head, n_q, n_kv, cap, D, past, seed):
+    """q, K / V and mask laid out as Qwen3Decoder::layers builds them: q [D, n_head, n_q] read through
+    permute(0, 2, 1, 3); the f16 caches [n_kv_head * D, cap] read through view_3d + permute; the mask [n_kv, n_q]."""
+    q = O.fill_normal(seed, n_q * n_head, D).reshape(n_q, n_head, D)
+    kc = O.fill_normal(seed + 1, cap, n_kv_head * D).astype(np.float16).view(np.uint16).reshape(cap, n_kv_head, D)
+    vc = O.fill_normal(seed + 2, cap, n_kv_head * D).astype(np.float16).view(np.uint16).reshape(cap, n_kv_head, D)
+    m = np.zeros((n_q, n_kv), np.float32)
+    for i in range(n_q):
+        m[i, past + i + 1:] = -np.inf
+    mask = m.astype(np.float16).view(np.uint16)
+    Q = dev(mx, be, q)
+    K = dev(mx, be, kc, mx.F16)
+    V = dev(mx, be, vc, mx.F16)
+    M = dev(mx, be, mask, mx.F16)
+    kv_dim = n_kv_head * D
+    qh = Q.view((D, n_q, n_head), (4, n_head * D * 4, D * 4))
+    kh = K.view((D, n_kv, n_kv_head), (2, kv_dim * 2, D * 2))
+    vh = V.view((D, n_kv, n_kv_head), (2, kv_dim * 2, D * 2))
+    O_ = be.tensor(mx.F32, (D, n_head, n_q))
+    args = (q.transpose(1, 0, 2), kc[:n_kv].transpose(1, 0, 2), vc[:n_kv].transpose(1, 0, 2), mask)
+    return (qh, kh, vh, M, O_), args
+
+
+@pytest.mark.parametrize("n_head,n_kv_head,n_q,n_kv,cap,D,past", [
+    (16, 8, 1, 1024, 1280, 128, 1000),    # a 0.6B decode step: 1001 positions, read as 16 blocks of 64
+    (16, 8, 1, 64, 256, 128, 0),          # the first token
+    (16, 8, 40, 576, 640, 128, 530),      # a prefill block after earlier blocks
+    (8, 2, 5, 192, 192, 64, 150),         # head size 64, four heads per kv head
+])
+def test_flash_attn_ext(mx, be, n_head, n_kv_head, n_q, n_kv, cap, D, past):
+    (qh, kh, vh, M, Y), (q, k, v, mask) = fa_device(mx, be, n_head, n_kv_head, n_q, n_kv, cap, D, past,
+                                                    0x2A00 + n_q + D)
+    scale = 1.0 / np.sqrt(D)
+    assert mx.lib().mx_supports_flash_attn_ext(qh.ref(), kh.ref(), vh.ref(), M.ref(), Y.ref(), 0.0, 0.0)
+    be.flash_attn_ext(qh, kh, vh, M, Y, scale)
+    be.sync()
+    got = Y.numpy().reshape(n_q, n_head, D)
+    exact = O.flash_attn_ext(q, k, v, mask, scale, exact=True)
+    cpu = O.flash_attn_ext(q, k, v, mask, scale)
+    big = np.abs(exact).max(axis=2, keepdims=True)
+    assert (np.abs(got - exact) / big).max() <= 1e-5
+    # ggml-cpu's loop rounds its V accumulator to fp16 at every position (1.4 % of the row's largest output after
+    # 1000 positions): the device is never further from it than it is from the exact attention
+    cpu_dev = (np.abs(cpu - exact) / big).max()
+    assert (np.abs(got - cpu) / big).max() <= cpu_dev + 1e-5
+
+
+def test_flash_attn_unsupported_forms(mx, be):
+    (qh, kh, vh, M, Y), _ = fa_device(mx, be, 4, 2, 1, 64, 64, 128, 10, 0x2B00)
+    L = mx.lib()
+    assert not L.mx_supports_flash_attn_ext(qh.ref(), kh.ref(), vh.ref(), M.ref(), Y.ref(), 8.0, 0.0)   # ALiBi
+    assert not L.mx_supports_flash_attn_ext(qh.ref(), kh.ref(), vh.ref(), M.ref(), Y.ref(), 0.0, 30.0)  # softcap
+    with pytest.raises(mx.MxError) as e:
+        mx.check(L.mx_flash_attn_ext(be.h, qh.ref(), kh.ref(), kh.ref(), M.ref(), qh.ref(), 0.1))
+    assert e.value.code == mx.UNSUPPORTED
