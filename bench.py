@@ -6,10 +6,14 @@ Default workload (`--workload decode`): the decode step at the Qwen3-0.6B shape 
 q/k/v, attn_o, gate/up and down Q8_0 mat-vecs, then the 151936-row Q8_0 lm_head mat-vec -- 197 mat-vecs reading
 633,233,408 bytes of weights per token. Every weight tensor is distinct and lives in HBM; q/k/v and gate/up each run
 as one launch (they share their input). The ops between them (RMSNorm, RoPE, attention over the f16 KV cache, SwiGLU,
-argmax) stay on ggml's CPU backend in this design, so each mat-vec reads a synthetic N(0,1) activation vector resident
-in HBM. The step is recorded once as a graph and replayed.
+argmax) are not part of this workload, so each mat-vec reads a synthetic N(0,1) activation vector resident in HBM.
+The step is recorded once as a graph and replayed.
 
 Other workloads (one JSON line each, same keys):
+  decode-full  the same decode step with every op on the device, as Qwen3Decoder::layers builds it: RMSNorm (norm
+               weight fused), q/k/v, per-head q/k RMSNorm, NEOX RoPE, SET_ROWS into the f16 KV cache, flash attention
+               over the cache prefilled with N(0,1) to 1024 positions (1088 read as 17 blocks of 64, the new token at
+               1024), attn_o, residual add, RMSNorm, gate/up, SwiGLU, down, add; final RMSNorm, lm_head, ARGMAX
   matvec       one Q8_0 MUL_MAT 3072 x 1024 at batch 1, rotated over 160 distinct copies of the weight (535 MB)
   prefill-q4k  Qwen3-1.7B-shape talker prefill: 28 layers of Q4_K linears (Q6_K down), M = 512 rows
   asr-1.7b     Qwen3-ASR-1.7B-shape Q8_0 prefill of 1564 rows in blocks {512, 512, 512, 28}, the head on the last
@@ -17,7 +21,7 @@ Other workloads (one JSON line each, same keys):
   moe          one Drama3-like MoE FFN layer (gate, up, down MUL_MAT_ID; 64 Q4_K experts, top-4 of a softmax router)
                at token batches of 1, 16 and 256
 
-Prints one JSON line. --gpus N > 1 exits: this build runs on one GPU.
+Prints one JSON line. --gpus N > 1 exits: one GPU is measured.
 """
 from __future__ import annotations
 
@@ -452,6 +456,162 @@ def read_traffic(workload):
     return None
 
 
+# ---------------------------------------------------------------------------------------------- decode-full
+KV_PAST = 1024       # the f16 KV cache is prefilled with N(0,1) values to 1024 positions; the new token is the 1025th
+ATT_BLOCK = 64       # flash attention reads whole blocks of 64 positions (qwen3-decoder.cpp kAttentionBlock)
+RMS_EPS, ROPE_THETA = 1e-6, 1e6
+
+
+def full_step_launches(be, mx, dec, st, ids, nq, nkv, hd):
+    """The decode step's launches, in Qwen3Decoder::layers order (qwen3-decoder.cpp:350-412, outputs :422-438)."""
+    H, kv_dim, n_kv = dec.hidden, nkv * hd, st["n_kv"]
+    L = []
+    x, h, pos, mask = st["x"], st["h"], st["pos"], st["mask"]
+    L.append(Launch("get_rows", row_bytes(Q8_0, H) + 4 + 4 * H, 0, lambda: be.get_rows(dec.embd, ids, x)))
+    for l in range(dec.layers_n):
+        w, nw, c = dec.layers[l], st["norms"][l], st["cache"][l]
+        o = st["outs"]
+        qv = o["q"].view((hd, nq, 1), (4, hd * 4, nq * hd * 4))
+        kv = o["k"].view((hd, nkv, 1), (4, hd * 4, nkv * hd * 4))
+        qh = st["qr"].view((hd, 1, nq), (4, nq * hd * 4, hd * 4))
+        kh = c["k"].view((hd, n_kv, nkv), (2, kv_dim * 2, hd * 2))
+        vh = c["v"].view((hd, n_kv, nkv), (2, kv_dim * 2, hd * 2))
+        kr_rows = st["kr"].view((kv_dim, 1), (4, kv_dim * 4))
+        L += [Launch("norm", 8 * H, 0, lambda nw=nw: be.rms_norm(x, h, RMS_EPS, nw["attn"])),
+              Launch("qkv", dec.wbytes(l, ["q", "k", "v"]) + 4 * (H + (nq + 2 * nkv) * hd), 0,
+                     lambda w=w: be.mul_mat_group([w["q"], w["k"], w["v"]], h, [o["q"], o["k"], o["v"]]),
+                     weight_bytes=dec.wbytes(l, ["q", "k", "v"])),
+              Launch("qk_norm", 8 * nq * hd, 0, lambda qv=qv, nw=nw: be.rms_norm(qv, st["qn"], RMS_EPS, nw["q"])),
+              Launch("qk_norm", 8 * nkv * hd, 0, lambda kv=kv, nw=nw: be.rms_norm(kv, st["kn"], RMS_EPS, nw["k"])),
+              Launch("set_rows", 6 * kv_dim, 0, lambda c=c: be.set_rows(o["v"], pos, c["v"])),
+              Launch("rope", 8 * nq * hd, 0, lambda: be.rope(st["qn"], pos, st["qr"], hd, ROPE_THETA)),
+              Launch("rope", 8 * nkv * hd, 0, lambda: be.rope(st["kn"], pos, st["kr"], hd, ROPE_THETA)),
+              Launch("set_rows", 6 * kv_dim, 0, lambda c=c, kr_rows=kr_rows: be.set_rows(kr_rows, pos, c["k"])),
+              Launch("attention", 2 * 2 * (KV_PAST + 1) * kv_dim + 8 * nq * hd, 0,
+                     lambda qh=qh, kh=kh, vh=vh: be.flash_attn_ext(qh, kh, vh, mask, st["att"], 1.0 / np.sqrt(hd))),
+              Launch("attn_o", dec.wbytes(l, ["o"]) + 4 * (nq * hd + H), 0,
+                     lambda w=w: be.mul_mat(w["o"], st["att_rows"], o["o"]), weight_bytes=dec.wbytes(l, ["o"])),
+              Launch("add", 12 * H, 0, lambda: be.add(x, o["o"], x)),
+              Launch("norm", 8 * H, 0, lambda nw=nw: be.rms_norm(x, h, RMS_EPS, nw["ffn"])),
+              Launch("gate_up", dec.wbytes(l, ["gate", "up"]) + 4 * (H + 2 * dec.ffn), 0,
+                     lambda w=w: be.mul_mat_group([w["gate"], w["up"]], h, [o["gate"], o["up"]]),
+                     weight_bytes=dec.wbytes(l, ["gate", "up"])),
+              Launch("swiglu", 12 * dec.ffn, 0, lambda: be.swiglu(o["gate"], o["up"], st["act"])),
+              Launch("down", dec.wbytes(l, ["down"]) + 4 * (dec.ffn + H), 0,
+                     lambda w=w: be.mul_mat(w["down"], st["act"], o["down"]), weight_bytes=dec.wbytes(l, ["down"])),
+              Launch("add", 12 * H, 0, lambda: be.add(x, o["down"], x))]
+    L += [Launch("norm", 8 * H, 0, lambda: be.rms_norm(x, h, RMS_EPS, st["final_norm"])),
+          Launch("lm_head", dec.head_bytes() + 4 * (H + dec.vocab), 0, lambda: be.mul_mat(dec.embd, h, st["logits"]),
+                 weight_bytes=dec.head_bytes()),
+          Launch("argmax", 4 * dec.vocab + 4, 0, lambda: be.argmax(st["logits"], st["pick"]))]
+    return L
+
+
+def full_step_state(mx, be, dec, nq, nkv, hd, threads):
+    """Norm weights N(1, 0.1), the f16 KV caches (N(0,1) to KV_PAST positions), position and mask inputs, buffers."""
+    H, kv_dim = dec.hidden, nkv * hd
+    n_kv = (KV_PAST + 1 + ATT_BLOCK - 1) // ATT_BLOCK * ATT_BLOCK
+    st = {"n_kv": n_kv, "norms": [], "cache": []}
+    for l in range(dec.layers_n):
+        st["norms"].append({n: be.tensor(mx.F32, (k,), mx.fill_normal(0x7077 + 16 * l + i, 1, k, 1.0, 0.1))
+                            for i, (n, k) in enumerate([("attn", H), ("ffn", H), ("q", hd), ("k", hd)])})
+        c = {}
+        for j, n in enumerate(("k", "v")):
+            vals = np.zeros((n_kv, kv_dim), np.float16)
+            vals[:KV_PAST] = mx.fill_normal(0xCAC4E000 + 2 * l + j, KV_PAST, kv_dim).astype(np.float16)
+            c[n] = be.tensor(mx.F16, (kv_dim, n_kv), vals.view(np.uint16))
+        st["cache"].append(c)
+    st["final_norm"] = be.tensor(mx.F32, (H,), mx.fill_normal(0x7077F, 1, H, 1.0, 0.1))
+    st["x"], st["h"] = be.tensor(mx.F32, (H, 1)), be.tensor(mx.F32, (H, 1))
+    st["outs"] = {n: be.tensor(mx.F32, (N, 1)) for n, _, N in dec.shapes}
+    st["qn"], st["qr"] = be.tensor(mx.F32, (hd, nq, 1)), be.tensor(mx.F32, (hd, nq, 1))
+    st["kn"], st["kr"] = be.tensor(mx.F32, (hd, nkv, 1)), be.tensor(mx.F32, (hd, nkv, 1))
+    st["att"] = be.tensor(mx.F32, (hd, nq, 1))
+    st["att_rows"] = st["att"].view((nq * hd, 1), (4, nq * hd * 4))
+    st["act"] = be.tensor(mx.F32, (dec.ffn, 1))
+    st["logits"], st["pick"] = be.tensor(mx.F32, (dec.vocab, 1)), be.tensor(mx.I32, (1,))
+    st["pos"] = be.tensor(mx.I32, (1,), np.array([KV_PAST], np.int32))
+    m = np.zeros(n_kv, np.float32)
+    m[KV_PAST + 1:] = -np.inf
+    st["mask"] = be.tensor(mx.F16, (n_kv, 1), m.astype(np.float16).view(np.uint16))
+    return st
+
+
+def run_decode_full(args, mx, be, threads):
+    S = QWEN3_06B
+    nq, nkv, hd = S["nq"], S["nkv"], S["head_dim"]
+    dec = Decoder(mx, be, 2, S["layers"], S["hidden"], S["ffn"], nq, nkv, hd, S["vocab"],
+                  {n: Q8_0 for n, _, _ in decoder_shapes(S["hidden"], S["ffn"], nq, nkv, hd)}, threads,
+                  keep_host=args.cpu_seconds > 0)
+    st = full_step_state(mx, be, dec, nq, nkv, hd, threads)
+    ids = be.tensor(mx.I32, (1,), np.array([4242], np.int32))
+    launches = full_step_launches(be, mx, dec, st, ids, nq, nkv, hd)
+    weight_bytes = sum(L.weight_bytes for L in launches if L.label in ("qkv", "attn_o", "gate_up", "down", "lm_head"))
+    kv_bytes = dec.layers_n * 2 * 2 * (KV_PAST + 1) * nkv * hd
+    ms_per_step = time_graph(be, launches, args.steps, args.warmup, not args.no_graph)
+    table = label_table(launches, per_label_pass(be, launches, reps=10))
+    tok_s = 1e3 / ms_per_step
+    mv = [L for L in launches if L.label in ("qkv", "attn_o", "gate_up", "down", "lm_head")]
+    ms_mv = sum(table[lab][3] * table[lab][0] for lab in ("qkv", "attn_o", "gate_up", "down", "lm_head"))
+    roof = hbm_roofline("k_matvec<Q8_0, NC=1>", table, ["qkv", "attn_o", "gate_up", "down", "lm_head"])
+    roof["traffic"] = read_traffic("decode")
+    att = hbm_roofline("k_fa_split<128> + k_fa_merge", table, ["attention"])
+    result = base_result(args, round(tok_s, 2), "tok/s", ms_per_step, "int8", {
+        "workload": "qwen3-0.6b-shape decode step, batch 1, every op on the device, KV cache at 1024 positions",
+        **S, "weights": "Q8_0", "kv_cache": "f16", "kv_past": KV_PAST, "kv_read": st["n_kv"],
+        "launches_per_step": len(launches), "graph": not args.no_graph})
+    result.update({"weight_bytes_per_step": weight_bytes, "kv_bytes_per_step": kv_bytes,
+                   "GBps_step": round((weight_bytes + kv_bytes) / (ms_per_step * 1e-3) / 1e9, 1),
+                   "hbm_frac_step": round((weight_bytes + kv_bytes) / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                   "matvec_ms_per_step": round(ms_mv, 4), "roofline": roof, "attention_roofline": att})
+    if args.cpu_seconds > 0:
+        result["cpu_baseline"] = cpu_decode_full(dec, st, args.cpu_seconds, nq, nkv, hd)
+    return result
+
+
+def cpu_decode_full(dec, st, seconds, nq, nkv, hd):
+    """The full step on the host: the AVX2 port's mat-vecs on the physical cores, the scalar oracle's norms, RoPE and
+    flash attention (ggml-cpu's loop) on one thread, over host copies of the same weights and caches."""
+    O = load_oracle()
+    threads = O.physical_cores()
+    H, n_kv, kv_dim = dec.hidden, st["n_kv"], nkv * hd
+    # host caches as the oracle's attention reads them: [kv head, position, channel]
+    caches = [{n: np.ascontiguousarray(np.frombuffer(c[n].get_bytes().tobytes(), np.uint16)
+                                       .reshape(n_kv, nkv, hd).transpose(1, 0, 2)) for n in ("k", "v")}
+              for c in st["cache"]]
+    norms = [{n: t.numpy().reshape(-1) for n, t in nw.items()} for nw in st["norms"]]
+    fin = st["final_norm"].numpy().reshape(-1)
+    mask = np.zeros((1, n_kv), np.float32)
+    mask[0, KV_PAST + 1:] = -np.inf
+    mask = mask.astype(np.float16).view(np.uint16)
+    pos = np.array([KV_PAST], np.int32)
+
+    def token():
+        x = O.get_rows(O.TYPE_Q8_0, dec.host["embd"][4242:4243], H, np.array([0], np.int32))
+        for l in range(dec.layers_n):
+            hv = O.binary("mul", O.rms_norm(x, RMS_EPS), norms[l]["attn"])
+            q, k, v = (O.cpu_fast_mul_mat(O.TYPE_Q8_0, dec.host[(l, n)], hv, threads) for n in ("q", "k", "v"))
+            q = O.binary("mul", O.rms_norm(q.reshape(1, nq, hd), RMS_EPS), norms[l]["q"])
+            k = O.binary("mul", O.rms_norm(k.reshape(1, nkv, hd), RMS_EPS), norms[l]["k"])
+            q, k = O.rope_neox(q, pos, hd, ROPE_THETA), O.rope_neox(k, pos, hd, ROPE_THETA)
+            # SET_ROWS: the new position's keys and values into the f16 caches
+            caches[l]["k"][:, KV_PAST] = k.reshape(nkv, hd).astype(np.float16).view(np.uint16)
+            caches[l]["v"][:, KV_PAST] = v.reshape(nkv, hd).astype(np.float16).view(np.uint16)
+            att = O.flash_attn_ext(q.transpose(1, 0, 2), caches[l]["k"], caches[l]["v"], mask, 1.0 / np.sqrt(hd))
+            x = O.binary("add", x, O.cpu_fast_mul_mat(O.TYPE_Q8_0, dec.host[(l, "o")], att.reshape(1, -1), threads))
+            hv = O.binary("mul", O.rms_norm(x, RMS_EPS), norms[l]["ffn"])
+            g, u = (O.cpu_fast_mul_mat(O.TYPE_Q8_0, dec.host[(l, n)], hv, threads) for n in ("gate", "up"))
+            x = O.binary("add", x, O.cpu_fast_mul_mat(O.TYPE_Q8_0, dec.host[(l, "down")], O.swiglu(g, u), threads))
+        hv = O.binary("mul", O.rms_norm(x, RMS_EPS), fin)
+        return O.argmax(O.cpu_fast_mul_mat(O.TYPE_Q8_0, dec.host["embd"], hv, threads))
+
+    n, el = timed_sample(token, seconds)
+    return {"value": round(n / el, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} full decode tokens after one untimed token, {el:.1f} s: mat-vecs in the AVX2 port on "
+                      f"{threads} threads, norms / RoPE / SET_ROWS / flash attention (ggml-cpu's loop over 1025 "
+                      f"positions) / SwiGLU in the scalar oracle on one thread"}
+
+
 # ---------------------------------------------------------------------------------------------- matvec
 MATVEC_COPIES = 160  # 160 x 3,342,336 B = 535 MB of distinct weight copies, larger than the 256 MB last-level cache
 
@@ -707,9 +867,9 @@ def run_moe(args, mx, be, threads):
     return result
 
 
-WORKLOADS = {"decode": run_decode, "matvec": run_matvec, "prefill-q4k": run_prefill_q4k, "asr-1.7b": run_asr,
+WORKLOADS = {"decode": run_decode, "decode-full": run_decode_full, "matvec": run_matvec, "prefill-q4k": run_prefill_q4k, "asr-1.7b": run_asr,
              "moe": run_moe}
-DEFAULT_STEPS = {"decode": (300, 20), "matvec": (50, 5), "prefill-q4k": (20, 3), "asr-1.7b": (3, 1), "moe": (20, 3)}
+DEFAULT_STEPS = {"decode": (300, 20), "decode-full": (100, 10), "matvec": (50, 5), "prefill-q4k": (20, 3), "asr-1.7b": (3, 1), "moe": (20, 3)}
 
 
 def main():

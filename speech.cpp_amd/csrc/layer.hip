@@ -131,7 +131,8 @@ __global__ __launch_bounds__(256) void k_set_rows_f16(RowsArgs a, const void *id
 
 // -------------------------------------------------------------------------------------------------- FLASH_ATTN_EXT
 // Pass 1: one wave per (kv split, head, query row) runs the online softmax over its split of the positions, 64 at a
-// time (lane j scores position j of the chunk; then each lane accumulates D/64 channels of V over the chunk), and
+// time (lane j scores position j of the chunk; then each lane accumulates D/64 adjacent channels of V over the chunk,
+// all of the chunk's V loads in flight before the first product), and
 // writes (max, sum, D accumulated channels) to the partials -- or, when there is one split, the normalized row to dst.
 // Pass 2 merges the splits of each (head, row).
 template <int D>
@@ -187,26 +188,41 @@ __global__ __launch_bounds__(64) void k_fa_split(FaArgs a) {
         M = Mn;
         ps[lane] = p;
         __syncthreads();
-        const int64_t nj = min((int64_t)64, j1 - base);
-        for (int64_t t = 0; t < nj; t++) {
-            const float pt = ps[t];
-            if (pt == 0.0f) continue;  // uniform
-            const uint16_t *vr = (const uint16_t *)(vb + (base + t) * a.v_nb1);
+        // V rows of the chunk: lane l holds channels l, l + 64 (D = 128: packed in one 32-bit load of channels 2l,
+        // 2l + 1 -- the channel order of acc does not matter until the store, which follows it); every row's load is
+        // issued before the first product, rows past the split repeat its last row (their weight is 0)
+        const int64_t last = j1 - 1;
+        if constexpr (D == 128) {
+            uint32_t vv[64];
 #pragma unroll
-            for (int c = 0; c < DL; c++) acc[c] = fmaf(pt, h2f(vr[lane + 64 * c]), acc[c]);
+            for (int t = 0; t < 64; t++)
+                vv[t] = *(const uint32_t *)(vb + min(base + t, last) * a.v_nb1 + 4 * lane);
+#pragma unroll
+            for (int t = 0; t < 64; t++) {
+                const float pt = ps[t];
+                acc[0] = fmaf(pt, h2f((uint16_t)(vv[t] & 0xFFFF)), acc[0]);
+                acc[1] = fmaf(pt, h2f((uint16_t)(vv[t] >> 16)), acc[1]);
+            }
+        } else {
+            uint16_t vv[64];
+#pragma unroll
+            for (int t = 0; t < 64; t++) vv[t] = *(const uint16_t *)(vb + min(base + t, last) * a.v_nb1 + 2 * lane);
+#pragma unroll
+            for (int t = 0; t < 64; t++) acc[0] = fmaf(ps[t], h2f(vv[t]), acc[0]);
         }
         __syncthreads();
     }
+    // lane l holds channels DL l .. DL l + DL - 1
     if (a.nsplit == 1) {
         float *o = a.dst + (i * a.n_head + h) * D;
         const float inv = S == 0.0f ? 0.0f : 1.0f / S;
 #pragma unroll
-        for (int c = 0; c < DL; c++) o[lane + 64 * c] = acc[c] * inv;
+        for (int c = 0; c < DL; c++) o[DL * lane + c] = acc[c] * inv;
         return;
     }
     float *part = a.part + ((i * a.n_head + h) * a.nsplit + split) * (D + 2);
 #pragma unroll
-    for (int c = 0; c < DL; c++) part[2 + lane + 64 * c] = acc[c];
+    for (int c = 0; c < DL; c++) part[2 + DL * lane + c] = acc[c];
     if (lane == 0) {
         part[0] = M;
         part[1] = S;
@@ -231,13 +247,13 @@ __global__ __launch_bounds__(64) void k_fa_merge(FaArgs a) {
             const float r = expf(ps[0] - M);
             S = fmaf(ps[1], r, S);
 #pragma unroll
-            for (int c = 0; c < DL; c++) acc[c] = fmaf(ps[2 + lane + 64 * c], r, acc[c]);
+            for (int c = 0; c < DL; c++) acc[c] = fmaf(ps[2 + DL * lane + c], r, acc[c]);
         }
     }
     float *o = a.dst + (i * a.n_head + h) * D;
     const float inv = S == 0.0f ? 0.0f : 1.0f / S;
 #pragma unroll
-    for (int c = 0; c < DL; c++) o[lane + 64 * c] = acc[c] * inv;
+    for (int c = 0; c < DL; c++) o[DL * lane + c] = acc[c] * inv;
 }
 
 // ---------------------------------------------------------------------------------------------------------- launches
@@ -283,10 +299,12 @@ hipError_t launch_set_rows_f16(const RowsArgs &a, const void *idx, bool idx_i64,
 }
 
 int fa_splits(int64_t n_q, int64_t n_head, int64_t n_kv) {
-    // enough waves for the chip: about 512 (split, head, row) waves, splits of at least 64 positions
-    int64_t nsplit = 1;
-    while (nsplit < 64 && n_q * n_head * nsplit < 512 && (n_kv + 2 * nsplit - 1) / (2 * nsplit) >= 64) nsplit *= 2;
-    return (int)nsplit;
+    // about 512 (split, head, row) waves for the chip, each split a whole number of 64-position blocks
+    const int64_t blocks = (n_kv + 63) / 64;
+    int64_t want = (512 + n_q * n_head - 1) / (n_q * n_head);
+    want = want < 1 ? 1 : (want > blocks ? blocks : want);
+    const int64_t per = (blocks + want - 1) / want;  // blocks per split
+    return (int)((blocks + per - 1) / per);
 }
 
 hipError_t launch_flash_attn(const FaArgs &a, hipStream_t s) {

@@ -914,8 +914,7 @@ MX_API int mx_flash_attn_ext(mx_backend *be, const mx_tensor *q, const mx_tensor
     a.m_nb1 = mask ? (int64_t)mask->nb[1] : 0;
     a.scale = scale;
     a.nsplit = mx::fa_splits(a.n_q, a.n_head, a.n_kv);
-    a.split_len = (a.n_kv + a.nsplit - 1) / a.nsplit;
-    a.split_len = (a.split_len + 63) / 64 * 64;
+    a.split_len = ((a.n_kv + 63) / 64 + a.nsplit - 1) / a.nsplit * 64;  // whole 64-position blocks per split
     if (a.nsplit > 1) {
         const size_t need = (size_t)a.n_q * (size_t)a.n_head * (size_t)a.nsplit * (size_t)(a.D + 2) * 4;
         if ((rc = ensure_scratch(be, need))) return rc;

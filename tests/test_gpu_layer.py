@@ -155,3 +155,79 @@ def test_flash_attn_unsupported_forms(mx, be):
     with pytest.raises(mx.MxError) as e:
         mx.check(L.mx_flash_attn_ext(be.h, qh.ref(), kh.ref(), kh.ref(), M.ref(), qh.ref(), 0.1))
     assert e.value.code == mx.UNSUPPORTED
+
+
+def test_decoder_layers_chain(mx, be):
+    """Two Qwen3-style layers (hidden 256, 4 q / 2 kv heads of 64, FFN 512, Q8_0 linears, an f16 cache holding 70
+    positions) run op by op on the device as Qwen3Decoder::layers orders them, against the same chain in the oracle
+    (attention in its exact form): the residual stream after both layers within 1e-4 of its largest value."""
+    H, F, nq, nkv, hd, past, cap, eps, theta = 256, 512, 4, 2, 64, 70, 128, 1e-6, 1e6
+    kv_dim, n_kv = nkv * hd, 128
+    t = O.TYPE_Q8_0
+    shapes = [("q", H, nq * hd), ("k", H, kv_dim), ("v", H, kv_dim), ("o", nq * hd, H), ("gate", H, F), ("up", H, F),
+              ("down", F, H)]
+    layers = []
+    for l in range(2):
+        ws = {n: O.quantize_chunk(t, O.fill_normal(0x3A00 + 16 * l + i, N, K, 0.0, 0.05))
+              for i, (n, K, N) in enumerate(shapes)}
+        nw = {n: O.fill_normal(0x3B00 + 16 * l + i, 1, k, 1.0, 0.1)[0]
+              for i, (n, k) in enumerate([("attn", H), ("ffn", H), ("q", hd), ("k", hd)])}
+        cache = {n: np.zeros((cap, kv_dim), np.uint16) for n in ("k", "v")}
+        for j, n in enumerate(("k", "v")):
+            cache[n][:past] = O.fill_normal(0x3C00 + 2 * l + j, past, kv_dim).astype(np.float16).view(np.uint16)
+        layers.append((ws, nw, cache))
+    x0 = O.fill_normal(0x3D00, 1, H)
+    pos = np.array([past], np.int32)
+    m = np.zeros((1, n_kv), np.float32)
+    m[0, past + 1:] = -np.inf
+    mask = m.astype(np.float16).view(np.uint16)
+
+    # oracle chain
+    x = x0.copy()
+    for ws, nw, cache in layers:
+        h = O.binary("mul", O.rms_norm(x, eps), nw["attn"])
+        q, k, v = (O.mul_mat(t, ws[n], h) for n in ("q", "k", "v"))
+        q = O.rope_neox(O.binary("mul", O.rms_norm(q.reshape(1, nq, hd), eps), nw["q"]), pos, hd, theta)
+        k = O.rope_neox(O.binary("mul", O.rms_norm(k.reshape(1, nkv, hd), eps), nw["k"]), pos, hd, theta)
+        kc = O.set_rows_f16(cache["k"], k.reshape(1, kv_dim), pos)[:n_kv].reshape(n_kv, nkv, hd).transpose(1, 0, 2)
+        vc = O.set_rows_f16(cache["v"], v.reshape(1, kv_dim), pos)[:n_kv].reshape(n_kv, nkv, hd).transpose(1, 0, 2)
+        att = O.flash_attn_ext(q.transpose(1, 0, 2), kc, vc, mask, 1.0 / np.sqrt(hd), exact=True)
+        x = O.binary("add", x, O.mul_mat(t, ws["o"], att.reshape(1, -1)))
+        h = O.binary("mul", O.rms_norm(x, eps), nw["ffn"])
+        x = O.binary("add", x, O.mul_mat(t, ws["down"], O.swiglu(O.mul_mat(t, ws["gate"], h),
+                                                                O.mul_mat(t, ws["up"], h))))
+    # device chain
+    X = dev(mx, be, x0)
+    Hd = out(mx, be, (1, H))
+    P = dev(mx, be, pos, mx.I32)
+    M = dev(mx, be, mask, mx.F16)
+    for ws, nw, cache in layers:
+        W = {n: be.tensor(t, (K, N), ws[n]) for n, K, N in shapes}
+        NW = {n: dev(mx, be, v) for n, v in nw.items()}
+        C = {n: dev(mx, be, cache[n], mx.F16) for n in ("k", "v")}
+        Y = {n: be.tensor(mx.F32, (N, 1)) for n, _, N in shapes}
+        qn, qr = be.tensor(mx.F32, (hd, nq, 1)), be.tensor(mx.F32, (hd, nq, 1))
+        kn, kr = be.tensor(mx.F32, (hd, nkv, 1)), be.tensor(mx.F32, (hd, nkv, 1))
+        att = be.tensor(mx.F32, (hd, nq, 1))
+        act = be.tensor(mx.F32, (F, 1))
+        be.rms_norm(X, Hd, eps, NW["attn"])
+        be.mul_mat_group([W["q"], W["k"], W["v"]], Hd, [Y["q"], Y["k"], Y["v"]])
+        be.rms_norm(Y["q"].view((hd, nq, 1), (4, hd * 4, nq * hd * 4)), qn, eps, NW["q"])
+        be.rms_norm(Y["k"].view((hd, nkv, 1), (4, hd * 4, kv_dim * 4)), kn, eps, NW["k"])
+        be.set_rows(Y["v"], P, C["v"])
+        be.rope(qn, P, qr, hd, theta)
+        be.rope(kn, P, kr, hd, theta)
+        be.set_rows(kr.view((kv_dim, 1), (4, kv_dim * 4)), P, C["k"])
+        be.flash_attn_ext(qr.view((hd, 1, nq), (4, nq * hd * 4, hd * 4)),
+                          C["k"].view((hd, n_kv, nkv), (2, kv_dim * 2, hd * 2)),
+                          C["v"].view((hd, n_kv, nkv), (2, kv_dim * 2, hd * 2)), M, att, 1.0 / np.sqrt(hd))
+        be.mul_mat(W["o"], att.view((nq * hd, 1), (4, nq * hd * 4)), Y["o"])
+        be.add(X, Y["o"], X)
+        be.rms_norm(X, Hd, eps, NW["ffn"])
+        be.mul_mat_group([W["gate"], W["up"]], Hd, [Y["gate"], Y["up"]])
+        be.swiglu(Y["gate"], Y["up"], act)
+        be.mul_mat(W["down"], act, Y["down"])
+        be.add(X, Y["down"], X)
+        be.sync()
+    got = X.numpy().reshape(1, H)
+    assert np.abs(got - x).max() <= 1e-4 * np.abs(x).max()
