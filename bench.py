@@ -462,8 +462,10 @@ ATT_BLOCK = 64       # flash attention reads whole blocks of 64 positions (qwen3
 RMS_EPS, ROPE_THETA = 1e-6, 1e6
 
 
-def full_step_launches(be, mx, dec, st, ids, nq, nkv, hd):
-    """The decode step's launches, in Qwen3Decoder::layers order (qwen3-decoder.cpp:350-412, outputs :422-438)."""
+def full_step_launches(be, mx, dec, st, ids, nq, nkv, hd, fused=True):
+    """The decode step's launches, in Qwen3Decoder::layers order (qwen3-decoder.cpp:350-412, outputs :422-438). Fused:
+    norm + q/k/v, q/k norm + RoPE + KV stores, attention, attn_o + residual, norm + gate/up, SwiGLU + down + residual
+    (each fusion computes what the separate ops compute); unfused: one launch per ggml node."""
     H, kv_dim, n_kv = dec.hidden, nkv * hd, st["n_kv"]
     L = []
     x, h, pos, mask = st["x"], st["h"], st["pos"], st["mask"]
@@ -473,37 +475,61 @@ def full_step_launches(be, mx, dec, st, ids, nq, nkv, hd):
         o = st["outs"]
         qv = o["q"].view((hd, nq, 1), (4, hd * 4, nq * hd * 4))
         kv = o["k"].view((hd, nkv, 1), (4, hd * 4, nkv * hd * 4))
+        vv = o["v"].view((hd, nkv, 1), (4, hd * 4, nkv * hd * 4))
         qh = st["qr"].view((hd, 1, nq), (4, nq * hd * 4, hd * 4))
         kh = c["k"].view((hd, n_kv, nkv), (2, kv_dim * 2, hd * 2))
         vh = c["v"].view((hd, n_kv, nkv), (2, kv_dim * 2, hd * 2))
         kr_rows = st["kr"].view((kv_dim, 1), (4, kv_dim * 4))
+        wq, wo, wg, wd = (dec.wbytes(l, n) for n in (["q", "k", "v"], ["o"], ["gate", "up"], ["down"]))
+        attention = Launch("attention", 2 * 2 * (KV_PAST + 1) * kv_dim + 8 * nq * hd, 0,
+                           lambda qh=qh, kh=kh, vh=vh: be.flash_attn_ext(qh, kh, vh, mask, st["att"], 1.0 / np.sqrt(hd)))
+        if fused:
+            L += [Launch("qkv", wq + 4 * (H + (nq + 2 * nkv) * hd), 0,
+                         lambda w=w, nw=nw: be.mul_mat_fused([w["q"], w["k"], w["v"]], x, [o["q"], o["k"], o["v"]],
+                                                             norm_w=nw["attn"], eps=RMS_EPS), weight_bytes=wq),
+                  Launch("qkv_post", 4 * (2 * nq * hd + 2 * kv_dim) + 2 * 2 * kv_dim, 0,
+                         lambda qv=qv, kv=kv, vv=vv, nw=nw, c=c: be.qk_norm_rope_kv(
+                             qv, kv, vv, nw["q"], nw["k"], pos, st["qr"], c["k"], c["v"], RMS_EPS, ROPE_THETA)),
+                  attention,
+                  Launch("attn_o", wo + 4 * (nq * hd + 2 * H), 0,
+                         lambda w=w: be.mul_mat_fused([w["o"]], st["att_rows"], [x], residual=[x]), weight_bytes=wo),
+                  Launch("gate_up", wg + 4 * (H + 2 * dec.ffn), 0,
+                         lambda w=w, nw=nw: be.mul_mat_fused([w["gate"], w["up"]], x, [o["gate"], o["up"]],
+                                                             norm_w=nw["ffn"], eps=RMS_EPS), weight_bytes=wg),
+                  Launch("down", wd + 4 * (2 * dec.ffn + 2 * H), 0,
+                         lambda w=w: be.mul_mat_fused([w["down"]], o["gate"], [x], glu_b=o["up"], residual=[x]),
+                         weight_bytes=wd)]
+            continue
         L += [Launch("norm", 8 * H, 0, lambda nw=nw: be.rms_norm(x, h, RMS_EPS, nw["attn"])),
-              Launch("qkv", dec.wbytes(l, ["q", "k", "v"]) + 4 * (H + (nq + 2 * nkv) * hd), 0,
+              Launch("qkv", wq + 4 * (H + (nq + 2 * nkv) * hd), 0,
                      lambda w=w: be.mul_mat_group([w["q"], w["k"], w["v"]], h, [o["q"], o["k"], o["v"]]),
-                     weight_bytes=dec.wbytes(l, ["q", "k", "v"])),
+                     weight_bytes=wq),
               Launch("qk_norm", 8 * nq * hd, 0, lambda qv=qv, nw=nw: be.rms_norm(qv, st["qn"], RMS_EPS, nw["q"])),
               Launch("qk_norm", 8 * nkv * hd, 0, lambda kv=kv, nw=nw: be.rms_norm(kv, st["kn"], RMS_EPS, nw["k"])),
               Launch("set_rows", 6 * kv_dim, 0, lambda c=c: be.set_rows(o["v"], pos, c["v"])),
               Launch("rope", 8 * nq * hd, 0, lambda: be.rope(st["qn"], pos, st["qr"], hd, ROPE_THETA)),
               Launch("rope", 8 * nkv * hd, 0, lambda: be.rope(st["kn"], pos, st["kr"], hd, ROPE_THETA)),
               Launch("set_rows", 6 * kv_dim, 0, lambda c=c, kr_rows=kr_rows: be.set_rows(kr_rows, pos, c["k"])),
-              Launch("attention", 2 * 2 * (KV_PAST + 1) * kv_dim + 8 * nq * hd, 0,
-                     lambda qh=qh, kh=kh, vh=vh: be.flash_attn_ext(qh, kh, vh, mask, st["att"], 1.0 / np.sqrt(hd))),
-              Launch("attn_o", dec.wbytes(l, ["o"]) + 4 * (nq * hd + H), 0,
-                     lambda w=w: be.mul_mat(w["o"], st["att_rows"], o["o"]), weight_bytes=dec.wbytes(l, ["o"])),
+              attention,
+              Launch("attn_o", wo + 4 * (nq * hd + H), 0,
+                     lambda w=w: be.mul_mat(w["o"], st["att_rows"], o["o"]), weight_bytes=wo),
               Launch("add", 12 * H, 0, lambda: be.add(x, o["o"], x)),
               Launch("norm", 8 * H, 0, lambda nw=nw: be.rms_norm(x, h, RMS_EPS, nw["ffn"])),
-              Launch("gate_up", dec.wbytes(l, ["gate", "up"]) + 4 * (H + 2 * dec.ffn), 0,
-                     lambda w=w: be.mul_mat_group([w["gate"], w["up"]], h, [o["gate"], o["up"]]),
-                     weight_bytes=dec.wbytes(l, ["gate", "up"])),
+              Launch("gate_up", wg + 4 * (H + 2 * dec.ffn), 0,
+                     lambda w=w: be.mul_mat_group([w["gate"], w["up"]], h, [o["gate"], o["up"]]), weight_bytes=wg),
               Launch("swiglu", 12 * dec.ffn, 0, lambda: be.swiglu(o["gate"], o["up"], st["act"])),
-              Launch("down", dec.wbytes(l, ["down"]) + 4 * (dec.ffn + H), 0,
-                     lambda w=w: be.mul_mat(w["down"], st["act"], o["down"]), weight_bytes=dec.wbytes(l, ["down"])),
+              Launch("down", wd + 4 * (dec.ffn + H), 0,
+                     lambda w=w: be.mul_mat(w["down"], st["act"], o["down"]), weight_bytes=wd),
               Launch("add", 12 * H, 0, lambda: be.add(x, o["down"], x))]
-    L += [Launch("norm", 8 * H, 0, lambda: be.rms_norm(x, h, RMS_EPS, st["final_norm"])),
-          Launch("lm_head", dec.head_bytes() + 4 * (H + dec.vocab), 0, lambda: be.mul_mat(dec.embd, h, st["logits"]),
-                 weight_bytes=dec.head_bytes()),
-          Launch("argmax", 4 * dec.vocab + 4, 0, lambda: be.argmax(st["logits"], st["pick"]))]
+    if fused:
+        L.append(Launch("lm_head", dec.head_bytes() + 4 * (H + dec.vocab), 0,
+                        lambda: be.mul_mat_fused([dec.embd], x, [st["logits"]], norm_w=st["final_norm"], eps=RMS_EPS),
+                        weight_bytes=dec.head_bytes()))
+    else:
+        L += [Launch("norm", 8 * H, 0, lambda: be.rms_norm(x, h, RMS_EPS, st["final_norm"])),
+              Launch("lm_head", dec.head_bytes() + 4 * (H + dec.vocab), 0,
+                     lambda: be.mul_mat(dec.embd, h, st["logits"]), weight_bytes=dec.head_bytes())]
+    L.append(Launch("argmax", 4 * dec.vocab + 4, 0, lambda: be.argmax(st["logits"], st["pick"])))
     return L
 
 
@@ -545,7 +571,7 @@ def run_decode_full(args, mx, be, threads):
                   keep_host=args.cpu_seconds > 0)
     st = full_step_state(mx, be, dec, nq, nkv, hd, threads)
     ids = be.tensor(mx.I32, (1,), np.array([4242], np.int32))
-    launches = full_step_launches(be, mx, dec, st, ids, nq, nkv, hd)
+    launches = full_step_launches(be, mx, dec, st, ids, nq, nkv, hd, fused=not args.unfused)
     weight_bytes = sum(L.weight_bytes for L in launches if L.label in ("qkv", "attn_o", "gate_up", "down", "lm_head"))
     kv_bytes = dec.layers_n * 2 * 2 * (KV_PAST + 1) * nkv * hd
     ms_per_step = time_graph(be, launches, args.steps, args.warmup, not args.no_graph)
@@ -559,7 +585,7 @@ def run_decode_full(args, mx, be, threads):
     result = base_result(args, round(tok_s, 2), "tok/s", ms_per_step, "int8", {
         "workload": "qwen3-0.6b-shape decode step, batch 1, every op on the device, KV cache at 1024 positions",
         **S, "weights": "Q8_0", "kv_cache": "f16", "kv_past": KV_PAST, "kv_read": st["n_kv"],
-        "launches_per_step": len(launches), "graph": not args.no_graph})
+        "launches_per_step": len(launches), "fused": not args.unfused, "graph": not args.no_graph})
     result.update({"weight_bytes_per_step": weight_bytes, "kv_bytes_per_step": kv_bytes,
                    "GBps_step": round((weight_bytes + kv_bytes) / (ms_per_step * 1e-3) / 1e9, 1),
                    "hbm_frac_step": round((weight_bytes + kv_bytes) / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
@@ -880,6 +906,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 skips it)")
     ap.add_argument("--no-graph", action="store_true", help="replay the step eagerly instead of as a graph")
+    ap.add_argument("--unfused", action="store_true", help="decode-full: one launch per ggml node, no fusions")
     ints = lambda v: [int(t) for t in v.split(",")]
     ap.add_argument("--blocks", type=ints, default=None,
                     help="asr-1.7b: prefill block rows (default 512,512,512,28; counter passes use 512,512,512)")

@@ -181,11 +181,39 @@ MX_API int mx_supports_rope(const mx_tensor *src, const mx_tensor *pos, const mx
 MX_API int mx_rope(mx_backend *be, const mx_tensor *src, const mx_tensor *pos, const mx_tensor *dst, int n_dims,
                    int mode, float freq_base, float freq_scale, float ext_factor, float attn_factor);
 MX_API int mx_set_rows(mx_backend *be, const mx_tensor *src, const mx_tensor *idx, const mx_tensor *dst);
+/* The attention block's per-head work between the q/k/v products and attention (qwen3-decoder.cpp:366-378) in one
+ * launch, each value as the separate ops compute it: q_out = rope(mul(rms_norm(q), q_norm)); the keys
+ * rope(mul(rms_norm(k), k_norm)) and the values v written into the f16 caches at row pos[r] (set_rows). q, k, v:
+ * [128, heads, rows] F32 (views of the products' outputs), q_norm / k_norm [128], pos [rows] I32, caches
+ * [heads_kv * 128, capacity] F16. Head size 128, NEOX over all of it, ext_factor 0, attn_factor 1; else
+ * MX_UNSUPPORTED and the ops run separately. A position outside the caches is reported by mx_backend_synchronize. */
+MX_API int mx_qk_norm_rope_kv(mx_backend *be, const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
+                              const mx_tensor *q_norm, const mx_tensor *k_norm, const mx_tensor *pos,
+                              const mx_tensor *q_out, const mx_tensor *k_cache, const mx_tensor *v_cache, float eps,
+                              int n_dims, int mode, float freq_base, float freq_scale, float ext_factor,
+                              float attn_factor);
 MX_API int mx_supports_flash_attn_ext(const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
                                       const mx_tensor *mask, const mx_tensor *dst, float max_bias,
                                       float logit_softcap);
 MX_API int mx_flash_attn_ext(mx_backend *be, const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
                              const mx_tensor *mask, const mx_tensor *dst, float scale);
+
+/* A product fused with the ops the decoder puts around it, each computed exactly as the separate op computes it (the
+ * same roundings), for a graph_compute that recognises the sequence:
+ *   norm_w:   src1 columns become mul(rms_norm(src1, norm_eps), norm_w) first (qwen3-decoder.cpp:361-363 before
+ *             q/k/v, :409-411 before gate/up);
+ *   glu_b:    src1 columns become swiglu(src1, glu_b) first (ggml_swiglu_split(gate, up) before down, :411);
+ *   residual: dst[i] = add(residual[i], product) (:405,411 the residual stream; residual[i] may be dst[i]).
+ * n products (1..4) share src1 as in mx_mul_mat_group; quantized weights, at most 8 columns (the mat-vec path);
+ * anything else returns MX_UNSUPPORTED and the ops run separately. glu_b has src1's layout, residual[i] dst[i]'s. */
+typedef struct mx_fusion {
+    const mx_tensor *norm_w;            /* F32 [K] or NULL */
+    float norm_eps;
+    const mx_tensor *glu_b;             /* F32 like src1, or NULL */
+    const mx_tensor *const *residual;   /* n entries (each may be NULL), or NULL */
+} mx_fusion;
+MX_API int mx_mul_mat_fused(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
+                            const mx_tensor *const *dst, const mx_fusion *f);
 
 /* Several MUL_MAT nodes that read the same src1 (q/k/v, or gate/up) in one launch, as a backend's graph_compute
  * may fuse them. Each dst[i] = src0[i] x src1, exactly as n separate mx_mul_mat calls compute it. */

@@ -44,7 +44,7 @@ EXPORTS = [
     "mx_gguf_find_tensor", "mx_gguf_n_keys", "mx_gguf_key", "mx_gguf_find_key", "mx_gguf_key_type", "mx_gguf_get_str",
     "mx_gguf_get_int", "mx_gguf_get_float", "mx_gguf_get_arr", "mx_gguf_get_arr_str", "mx_gguf_load_tensor",
     "mx_rms_norm", "mx_binary", "mx_swiglu", "mx_supports_rope", "mx_rope", "mx_set_rows", "mx_supports_flash_attn_ext",
-    "mx_flash_attn_ext",
+    "mx_flash_attn_ext", "mx_mul_mat_fused", "mx_qk_norm_rope_kv",
 ]
 
 
@@ -55,6 +55,11 @@ def row_size(t: int, ne0: int) -> int:
 class MxTensor(ctypes.Structure):
     _fields_ = [("type", ctypes.c_int32), ("pad_", ctypes.c_int32), ("ne", ctypes.c_int64 * 4),
                 ("nb", ctypes.c_uint64 * 4), ("data", ctypes.c_void_p)]
+
+
+class MxFusion(ctypes.Structure):
+    _fields_ = [("norm_w", ctypes.POINTER(MxTensor)), ("norm_eps", ctypes.c_float),
+                ("glu_b", ctypes.POINTER(MxTensor)), ("residual", ctypes.POINTER(ctypes.POINTER(MxTensor)))]
 
 
 class GgufTensorInfo(ctypes.Structure):
@@ -153,6 +158,8 @@ def lib():
         "mx_set_rows": ([vp, P, P, P], i32),
         "mx_supports_flash_attn_ext": ([P, P, P, P, P, f32, f32], i32),
         "mx_flash_attn_ext": ([vp, P, P, P, P, P, f32], i32),
+        "mx_mul_mat_fused": ([vp, i32, ctypes.POINTER(P), P, ctypes.POINTER(P), ctypes.POINTER(MxFusion)], i32),
+        "mx_qk_norm_rope_kv": ([vp, P, P, P, P, P, P, P, P, P, f32, i32, i32, f32, f32, f32, f32], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -335,6 +342,27 @@ class Backend:
 
     def argmax(self, src: Tensor, dst: Tensor) -> None:
         check(lib().mx_argmax(self.h, src.ref(), dst.ref()))
+
+    def mul_mat_fused(self, src0s, src1, dsts, norm_w=None, eps: float = 0.0, glu_b=None, residual=None) -> None:
+        """dst[i] = residual[i] + src0[i] x f(src1), f = mul(rms_norm(., eps), norm_w) and / or swiglu(., glu_b)."""
+        P = ctypes.POINTER(MxTensor)
+        w = (P * len(src0s))(*[ctypes.pointer(s.desc) for s in src0s])
+        y = (P * len(dsts))(*[ctypes.pointer(d.desc) for d in dsts])
+        f = MxFusion()
+        f.norm_w = ctypes.pointer(norm_w.desc) if norm_w is not None else None
+        f.norm_eps = eps
+        f.glu_b = ctypes.pointer(glu_b.desc) if glu_b is not None else None
+        res = None
+        if residual is not None:
+            res = (P * len(residual))(*[ctypes.pointer(r.desc) if r is not None else None for r in residual])
+            f.residual = ctypes.cast(res, ctypes.POINTER(P))
+        check(lib().mx_mul_mat_fused(self.h, len(src0s), w, src1.ref(), y, ctypes.byref(f)))
+
+    def qk_norm_rope_kv(self, q, k, v, q_norm, k_norm, pos, q_out, k_cache, v_cache, eps: float, freq_base: float,
+                        n_dims: int = 128, freq_scale: float = 1.0) -> None:
+        check(lib().mx_qk_norm_rope_kv(self.h, q.ref(), k.ref(), v.ref(), q_norm.ref(), k_norm.ref(), pos.ref(),
+                                       q_out.ref(), k_cache.ref(), v_cache.ref(), eps, n_dims, ROPE_NEOX, freq_base,
+                                       freq_scale, 0.0, 1.0))
 
     def rms_norm(self, src: Tensor, dst: Tensor, eps: float, w: Tensor | None = None) -> None:
         check(lib().mx_rms_norm(self.h, src.ref(), dst.ref(), eps, w.ref() if w is not None else None))

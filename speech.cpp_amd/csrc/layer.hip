@@ -129,12 +129,100 @@ __global__ __launch_bounds__(256) void k_set_rows_f16(RowsArgs a, const void *id
     }
 }
 
+// ------------------------------------------------------------------------------------- q / k norm, RoPE, KV stores
+// The attention block's per-head work between the q/k/v products and attention (qwen3-decoder.cpp:366-378) in one
+// launch, head size 128 with RoPE over all of it: one wave per (head item, row); lane l holds channels l and l + 64,
+// which are the NEOX pair l. Items 0 .. nq-1: q heads, normed (rms_norm then mul by q_norm), turned, written to
+// q_out; nq .. nq+nkv-1: k heads, normed with k_norm, turned, written to the f16 K cache at row pos; then the v heads
+// written to the V cache at row pos. Arithmetic as k_rms_norm, k_rope_neox and k_set_rows_f16 perform it.
+__global__ __launch_bounds__(256) void k_qkv_post(QkvPostArgs a) {
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6), r = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    if (item >= a.nq + 2 * a.nkv) return;  // whole wave
+    const int64_t p = a.pos[r];
+    if (p < 0 || p >= a.cache_rows) {
+        if (lane == 0 && item == 0) atomicOr(a.err, 4);
+        if (item >= a.nq) return;  // nothing is stored at a bad row; q is still written
+    }
+    if (item >= a.nq + a.nkv) {  // v head
+        const int64_t h = item - a.nq - a.nkv;
+        const float *v = (const float *)((const uint8_t *)a.v + h * a.v_nb1 + r * a.v_nb2);
+        uint16_t *dst = (uint16_t *)((uint8_t *)a.vc + p * a.vc_nb1) + h * 128;
+        dst[lane] = f2h(v[lane]);
+        dst[lane + 64] = f2h(v[lane + 64]);
+        return;
+    }
+    const bool isq = item < a.nq;
+    const int64_t h = isq ? item : item - a.nq;
+    const float *x = isq ? (const float *)((const uint8_t *)a.q + h * a.q_nb1 + r * a.q_nb2)
+                         : (const float *)((const uint8_t *)a.k + h * a.k_nb1 + r * a.k_nb2);
+    const float *w = isq ? a.qw : a.kw;
+    const float x0 = x[lane], x1 = x[lane + 64];
+    double ss = (double)(x0 * x0) + (double)(x1 * x1);
+    ss = wave_sum_d(ss);
+    const float mean = (float)(ss / 128.0);
+    const float scale = 1.0f / sqrtf(mean + a.eps);
+    const float y0 = (x0 * scale) * w[lane], y1 = (x1 * scale) * w[lane + 64];
+    float theta = (float)p;
+    for (int j = 0; j < lane; j++) theta *= a.theta_scale;
+    const float t = a.freq_scale * theta;
+    const float c = cosf(t), s = sinf(t);
+    const float o0 = y0 * c - y1 * s, o1 = y0 * s + y1 * c;
+    if (isq) {
+        float *o = (float *)((uint8_t *)a.q_out + h * a.qo_nb1 + r * a.qo_nb2);
+        o[lane] = o0;
+        o[lane + 64] = o1;
+    } else {
+        uint16_t *dst = (uint16_t *)((uint8_t *)a.kc + p * a.kc_nb1) + h * 128;
+        dst[lane] = f2h(o0);
+        dst[lane + 64] = f2h(o1);
+    }
+}
+
+hipError_t launch_qkv_post(const QkvPostArgs &a, int64_t rows, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    const dim3 grid((unsigned)((a.nq + 2 * a.nkv + 3) / 4), (unsigned)rows);
+    hipLaunchKernelGGL(k_qkv_post, grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
 // -------------------------------------------------------------------------------------------------- FLASH_ATTN_EXT
 // Pass 1: one wave per (kv split, head, query row) runs the online softmax over its split of the positions, 64 at a
 // time (lane j scores position j of the chunk; then each lane accumulates D/64 adjacent channels of V over the chunk,
 // all of the chunk's V loads in flight before the first product), and
 // writes (max, sum, D accumulated channels) to the partials -- or, when there is one split, the normalized row to dst.
 // Pass 2 merges the splits of each (head, row).
+// The loads of one 64-position chunk, issued together ahead of their use: lane j's key row (position base + j),
+// every lane's DL channels of the 64 value rows, and lane j's mask value. Positions past the split repeat its last
+// one; their score is -inf, so neither their key nor their value counts.
+template <int D>
+struct FaChunk {
+    uint4 k[D / 8];
+    uint32_t v[64];  // D = 128: channels 2l, 2l + 1 of row t; D = 64: channel l (low half)
+    float mv;
+};
+
+template <int D>
+__device__ __forceinline__ void fa_load_k(FaChunk<D> &c, const FaArgs &a, const uint8_t *kb, const uint16_t *mrow,
+                                          int64_t base, int64_t j1) {
+    const int lane = threadIdx.x;
+    const int64_t j = base + lane, jj = min(j, j1 - 1);
+    const uint4 *kr = (const uint4 *)(kb + jj * a.k_nb1);
+#pragma unroll
+    for (int t = 0; t < D / 8; t++) c.k[t] = kr[t];
+    c.mv = j < j1 ? (mrow ? h2f(mrow[j]) : 0.0f) : -INFINITY;
+}
+template <int D>
+__device__ __forceinline__ void fa_load_v(FaChunk<D> &c, const FaArgs &a, const uint8_t *vb, int64_t base,
+                                          int64_t j1) {
+    const int lane = threadIdx.x;
+#pragma unroll
+    for (int t = 0; t < 64; t++) {
+        const uint8_t *row = vb + min(base + t, j1 - 1) * a.v_nb1;
+        c.v[t] = D == 128 ? *(const uint32_t *)(row + 4 * lane) : (uint32_t)*(const uint16_t *)(row + 2 * lane);
+    }
+}
+
 template <int D>
 __global__ __launch_bounds__(64) void k_fa_split(FaArgs a) {
     static_assert(D == 64 || D == 128, "head size 64 or 128");
@@ -144,73 +232,64 @@ __global__ __launch_bounds__(64) void k_fa_split(FaArgs a) {
     const int lane = threadIdx.x;
     const int64_t split = blockIdx.x, h = blockIdx.y, i = blockIdx.z;
     const int64_t hk = h / a.gqa;
-    const float *q = (const float *)((const uint8_t *)a.q + i * a.q_nb1 + h * a.q_nb2);
-    for (int d = lane; d < D; d += 64) qs[d] = h2f(f2h(q[d]));  // ggml converts q to K's f16 first
-    __syncthreads();
     const uint8_t *kb = (const uint8_t *)a.k + hk * a.k_nb2;
     const uint8_t *vb = (const uint8_t *)a.v + hk * a.v_nb2;
     const uint16_t *mrow = a.mask ? (const uint16_t *)((const uint8_t *)a.mask + i * a.m_nb1) : nullptr;
     const int64_t j0 = split * a.split_len, j1 = min(a.n_kv, j0 + a.split_len);
+    FaChunk<D> ch;
+    if (j0 < j1) {  // the first chunk's loads go out before q's
+        fa_load_k<D>(ch, a, kb, mrow, j0, j1);
+        fa_load_v<D>(ch, a, vb, j0, j1);
+    }
+    const float *q = (const float *)((const uint8_t *)a.q + i * a.q_nb1 + h * a.q_nb2);
+    for (int d = lane; d < D; d += 64) qs[d] = h2f(f2h(q[d]));  // ggml converts q to K's f16 first
+    __syncthreads();
 
     float M = -INFINITY, S = 0.0f;
     float acc[DL];
 #pragma unroll
     for (int c = 0; c < DL; c++) acc[c] = 0.0f;
     for (int64_t base = j0; base < j1; base += 64) {
-        const int64_t j = base + lane;
+        const bool more = base + 64 < j1;  // uniform
         float s = -INFINITY;
-        if (j < j1) {
-            const float mv = mrow ? h2f(mrow[j]) : 0.0f;
-            if (mv != -INFINITY) {
-                const uint4 *kr = (const uint4 *)(kb + j * a.k_nb1);
-                float dot = 0.0f;
+        if (ch.mv != -INFINITY) {
+            float dot = 0.0f;
 #pragma unroll
-                for (int c = 0; c < D / 8; c++) {
-                    const uint4 w = kr[c];
-                    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+            for (int c = 0; c < D / 8; c++) {
+                const uint32_t wv[4] = {ch.k[c].x, ch.k[c].y, ch.k[c].z, ch.k[c].w};
 #pragma unroll
-                    for (int t = 0; t < 4; t++) {
-                        dot = fmaf(h2f((uint16_t)(wv[t] & 0xFFFF)), qs[8 * c + 2 * t], dot);
-                        dot = fmaf(h2f((uint16_t)(wv[t] >> 16)), qs[8 * c + 2 * t + 1], dot);
-                    }
+                for (int t = 0; t < 4; t++) {
+                    dot = fmaf(h2f((uint16_t)(wv[t] & 0xFFFF)), qs[8 * c + 2 * t], dot);
+                    dot = fmaf(h2f((uint16_t)(wv[t] >> 16)), qs[8 * c + 2 * t + 1], dot);
                 }
-                s = dot * a.scale + mv;
             }
+            s = dot * a.scale + ch.mv;
         }
+        if (more) fa_load_k<D>(ch, a, kb, mrow, base + 64, j1);  // the key registers are free again
         const float mc = wave_max_f(s);
-        if (mc == -INFINITY) continue;  // every position of the chunk masked (uniform)
-        const float Mn = fmaxf(M, mc);
-        const float r = expf(M - Mn);   // 0 while M is -inf
-        const float p = s == -INFINITY ? 0.0f : expf(s - Mn);
-        S = S * r + wave_sum_f(p);
+        if (mc != -INFINITY) {  // uniform: a chunk with every position masked adds nothing
+            const float Mn = fmaxf(M, mc);
+            const float r = expf(M - Mn);  // 0 while M is -inf
+            const float p = s == -INFINITY ? 0.0f : expf(s - Mn);
+            S = S * r + wave_sum_f(p);
 #pragma unroll
-        for (int c = 0; c < DL; c++) acc[c] *= r;
-        M = Mn;
-        ps[lane] = p;
-        __syncthreads();
-        // V rows of the chunk: lane l holds channels l, l + 64 (D = 128: packed in one 32-bit load of channels 2l,
-        // 2l + 1 -- the channel order of acc does not matter until the store, which follows it); every row's load is
-        // issued before the first product, rows past the split repeat its last row (their weight is 0)
-        const int64_t last = j1 - 1;
-        if constexpr (D == 128) {
-            uint32_t vv[64];
-#pragma unroll
-            for (int t = 0; t < 64; t++)
-                vv[t] = *(const uint32_t *)(vb + min(base + t, last) * a.v_nb1 + 4 * lane);
+            for (int c = 0; c < DL; c++) acc[c] *= r;
+            M = Mn;
+            ps[lane] = p;
+            __syncthreads();
 #pragma unroll
             for (int t = 0; t < 64; t++) {
                 const float pt = ps[t];
-                acc[0] = fmaf(pt, h2f((uint16_t)(vv[t] & 0xFFFF)), acc[0]);
-                acc[1] = fmaf(pt, h2f((uint16_t)(vv[t] >> 16)), acc[1]);
+                if constexpr (D == 128) {
+                    acc[0] = fmaf(pt, h2f((uint16_t)(ch.v[t] & 0xFFFF)), acc[0]);
+                    acc[1] = fmaf(pt, h2f((uint16_t)(ch.v[t] >> 16)), acc[1]);
+                } else {
+                    acc[0] = fmaf(pt, h2f((uint16_t)ch.v[t]), acc[0]);
+                }
             }
-        } else {
-            uint16_t vv[64];
-#pragma unroll
-            for (int t = 0; t < 64; t++) vv[t] = *(const uint16_t *)(vb + min(base + t, last) * a.v_nb1 + 2 * lane);
-#pragma unroll
-            for (int t = 0; t < 64; t++) acc[0] = fmaf(ps[t], h2f(vv[t]), acc[0]);
+            __syncthreads();
         }
-        __syncthreads();
+        if (more) fa_load_v<D>(ch, a, vb, base + 64, j1);
     }
     // lane l holds channels DL l .. DL l + DL - 1
     if (a.nsplit == 1) {
@@ -229,26 +308,40 @@ __global__ __launch_bounds__(64) void k_fa_split(FaArgs a) {
     }
 }
 
+// Pass 2: one wave per (head, row). Lane s holds split s's max and sum (nsplit <= 64), so the splits' weights
+// exp(m_s - M) and the total come from one round of loads and two wave reductions; the channels are gathered eight
+// splits at a time, their loads in flight together.
 template <int D>
 __global__ __launch_bounds__(64) void k_fa_merge(FaArgs a) {
     constexpr int DL = D / 64;
     const int lane = threadIdx.x;
     const int64_t h = blockIdx.x, i = blockIdx.y;
-    const float *part = a.part + (i * a.n_head + h) * a.nsplit * (D + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < a.nsplit; s++) M = fmaxf(M, part[s * (D + 2)]);
-    float S = 0.0f, acc[DL];
+    const int ns = a.nsplit;
+    const float *part = a.part + (i * a.n_head + h) * ns * (D + 2);
+    float ms = -INFINITY, ss = 0.0f;
+    if (lane < ns) {
+        ms = part[lane * (D + 2)];
+        ss = part[lane * (D + 2) + 1];
+    }
+    const float M = wave_max_f(ms);
+    const float w = (ms == -INFINITY) ? 0.0f : expf(ms - M);  // a split with nothing visible weighs 0
+    const float S = wave_sum_f(ss * w);
+    float acc[DL];
 #pragma unroll
     for (int c = 0; c < DL; c++) acc[c] = 0.0f;
-    if (M != -INFINITY) {
-        for (int s = 0; s < a.nsplit; s++) {
-            const float *ps = part + s * (D + 2);
-            if (ps[0] == -INFINITY) continue;
-            const float r = expf(ps[0] - M);
-            S = fmaf(ps[1], r, S);
+    for (int s0 = 0; s0 < ns; s0 += 8) {
+        float v[8][DL], ws[8];
 #pragma unroll
-            for (int c = 0; c < DL; c++) acc[c] = fmaf(ps[2 + DL * lane + c], r, acc[c]);
+        for (int u = 0; u < 8; u++) {
+            const int sp = min(s0 + u, ns - 1);
+            ws[u] = s0 + u < ns ? __shfl(w, sp, 64) : 0.0f;
+#pragma unroll
+            for (int c = 0; c < DL; c++) v[u][c] = part[sp * (D + 2) + 2 + DL * lane + c];
         }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+#pragma unroll
+            for (int c = 0; c < DL; c++) acc[c] = fmaf(v[u][c], ws[u], acc[c]);
     }
     float *o = a.dst + (i * a.n_head + h) * D;
     const float inv = S == 0.0f ? 0.0f : 1.0f / S;
@@ -303,6 +396,7 @@ int fa_splits(int64_t n_q, int64_t n_head, int64_t n_kv) {
     const int64_t blocks = (n_kv + 63) / 64;
     int64_t want = (512 + n_q * n_head - 1) / (n_q * n_head);
     want = want < 1 ? 1 : (want > blocks ? blocks : want);
+    want = want > 64 ? 64 : want;  // the merge holds one split per lane
     const int64_t per = (blocks + want - 1) / want;  // blocks per split
     return (int)((blocks + per - 1) / per);
 }

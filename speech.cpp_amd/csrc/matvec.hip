@@ -57,6 +57,83 @@ __device__ __forceinline__ float4 load_x4(const float *xc, int e, int K) {
     return e < K ? v : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
+// The fused prologue: each column x becomes silu(x) * glu_b (ggml_vec_swiglu_f32's scalar form) when glu_b is set,
+// then mul(rms_norm(x, eps), norm_w) when norm_w is set -- the squares (rounded to float) summed in double over the
+// workgroup, the mean rounded to float, x * (1 / sqrtf(mean + eps)) then times the weight, as the separate ops round
+// -- and is quantized. Pieces of 1024 elements past the preloaded ones are read again after the sum.
+template <int TYPE, int NC>
+__device__ __forceinline__ void fused_prologue(const MatvecArgs &a, const float *x, int xi12, int i13,
+                                               float4 (&xr)[NC][xpre<NC>()], int8_t *xq, float *xd, int *xbs) {
+    constexpr int XP = xpre<NC>();
+    constexpr int XDB = TYPE == MX_TYPE_Q8_0 ? 32 : 256;
+    const int K = (int)a.K;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ double red[NC][4];
+    const float *gb = a.glu_b ? a.glu_b + xi12 * a.x_b2 + i13 * a.x_b3 : nullptr;
+    auto piece = [&](int c, int base, float4 v) -> float4 {  // glu of one loaded piece
+        if (gb) {
+            const float4 b = load_x4(gb + c * a.x_col_stride, base + 4 * tid, K);
+            v.x = v.x / (1.0f + expf(-v.x)) * b.x;
+            v.y = v.y / (1.0f + expf(-v.y)) * b.y;
+            v.z = v.z / (1.0f + expf(-v.z)) * b.z;
+            v.w = v.w / (1.0f + expf(-v.w)) * b.w;
+        }
+        return v;
+    };
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+#pragma unroll
+        for (int i = 0; i < XP; i++) xr[c][i] = piece(c, 1024 * i, xr[c][i]);
+    float scale[NC];
+    if (a.norm_w) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            double ss = 0.0;
+#pragma unroll
+            for (int i = 0; i < XP; i++) {
+                const float4 v = xr[c][i];  // zero past K
+                ss += (double)(v.x * v.x) + (double)(v.y * v.y) + (double)(v.z * v.z) + (double)(v.w * v.w);
+            }
+            for (int base = 1024 * XP; base < K; base += 1024) {
+                const float4 v = piece(c, base, load_x4(x + c * a.x_col_stride, base + 4 * tid, K));
+                ss += (double)(v.x * v.x) + (double)(v.y * v.y) + (double)(v.z * v.z) + (double)(v.w * v.w);
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+            if (lane == 0) red[c][wave] = ss;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const double tot = red[c][0] + red[c][1] + red[c][2] + red[c][3];
+            const float mean = (float)(tot / (double)K);
+            scale[c] = 1.0f / sqrtf(mean + a.norm_eps);
+        }
+    }
+    auto normed = [&](int c, int base, float4 v) -> float4 {
+        if (a.norm_w) {
+            const float4 w = load_x4(a.norm_w, base + 4 * tid, K);
+            v.x = (v.x * scale[c]) * w.x;
+            v.y = (v.y * scale[c]) * w.y;
+            v.z = (v.z * scale[c]) * w.z;
+            v.w = (v.w * scale[c]) * w.w;
+        }
+        return v;
+    };
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+        const float *xc = x + c * a.x_col_stride;
+#pragma unroll
+        for (int i = 0; i < XP; i++)
+            if (1024 * i < K)
+                quantize_piece<TYPE>(normed(c, 1024 * i, xr[c][i]), 1024 * i, K, a.rounding, xq + c * K,
+                                     xd + c * (K / XDB), xbs + c * (K / 16));
+        for (int base = 1024 * XP; base < K; base += 1024)
+            quantize_piece<TYPE>(normed(c, base, piece(c, base, load_x4(xc, base + 4 * tid, K))), base, K, a.rounding,
+                                 xq + c * K, xd + c * (K / XDB), xbs + c * (K / 16));
+    }
+}
+
 template <int TYPE, int NC, int LPR>
 __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -112,16 +189,20 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     float *xd = (float *)(smem + (size_t)NC * K);
     constexpr int XDB = TYPE == MX_TYPE_Q8_0 ? 32 : 256;
     int *xbs = (int *)(xd + NC * (K / XDB));
+    if (a.glu_b || a.norm_w) {  // uniform: the fused prologue
+        fused_prologue<TYPE, NC>(a, x, xi12, i13, xr, xq, xd, xbs);
+    } else {
 #pragma unroll
-    for (int c = 0; c < NC; c++) {
-        const float *xc = x + c * a.x_col_stride;
+        for (int c = 0; c < NC; c++) {
+            const float *xc = x + c * a.x_col_stride;
 #pragma unroll
-        for (int i = 0; i < XP; i++)
-            if (1024 * i < K) quantize_piece<TYPE>(xr[c][i], 1024 * i, K, a.rounding, xq + c * K, xd + c * (K / XDB),
-                                                   xbs + c * (K / 16));
-        for (int base = 1024 * XP; base < K; base += 1024)
-            quantize_piece<TYPE>(load_x4(xc, base + 4 * tid, K), base, K, a.rounding, xq + c * K, xd + c * (K / XDB),
-                                 xbs + c * (K / 16));
+            for (int i = 0; i < XP; i++)
+                if (1024 * i < K) quantize_piece<TYPE>(xr[c][i], 1024 * i, K, a.rounding, xq + c * K, xd + c * (K / XDB),
+                                                       xbs + c * (K / 16));
+            for (int base = 1024 * XP; base < K; base += 1024)
+                quantize_piece<TYPE>(load_x4(xc, base + 4 * tid, K), base, K, a.rounding, xq + c * K,
+                                     xd + c * (K / XDB), xbs + c * (K / 16));
+        }
     }
     __syncthreads();
     if (!has_row) return;  // whole LPR-lane groups leave together; no barrier follows
@@ -140,9 +221,15 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
 #pragma unroll
     for (int c = 0; c < NC; c++) acc[c] = sum_lanes<LPR>(acc[c]);
     if (sub == LPR - 1) {  // the lane holding the group's sum
-        float *y = p.y + i12 * a.y_b2 + i13 * a.y_b3 + row;
+        const int64_t off = i12 * a.y_b2 + i13 * a.y_b3 + row;
+        float *y = p.y + off;
+        if (p.res) {  // the residual ADD that follows the product, fused
 #pragma unroll
-        for (int c = 0; c < NC; c++) y[c * p.y_col_stride] = acc[c];
+            for (int c = 0; c < NC; c++) y[c * p.y_col_stride] = p.res[off + c * p.y_col_stride] + acc[c];
+        } else {
+#pragma unroll
+            for (int c = 0; c < NC; c++) y[c * p.y_col_stride] = acc[c];
+        }
     }
 }
 

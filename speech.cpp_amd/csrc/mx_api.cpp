@@ -674,9 +674,10 @@ static int gemm_dq_group(mx_backend *be, int n, const mx_tensor *const *src0, co
     return MX_SUCCESS;
 }
 
-// Products sharing src1: n problems (n <= 4) of the same type and K, each with its own rows and dst.
+// Products sharing src1: n problems (n <= 4) of the same type and K, each with its own rows and dst; `f` (validated
+// by mx_mul_mat_fused, mat-vec path only) fuses the neighbouring norm / SwiGLU / residual ADD.
 static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
-                        const mx_tensor *const *dst) {
+                        const mx_tensor *const *dst, const mx_fusion *f = nullptr) {
     const mx_tensor *w0 = src0[0];
     mx::MatvecArgs a{};
     a.type = w0->type;
@@ -694,6 +695,11 @@ static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, con
     a.y_b3 = (int64_t)(dst[0]->nb[3] / 4);
     a.nprob = n;
     const int64_t M = src1->ne[1];
+    if (f) {
+        a.glu_b = f->glu_b ? (const float *)f->glu_b->data : nullptr;
+        a.norm_w = f->norm_w ? (const float *)f->norm_w->data : nullptr;
+        a.norm_eps = f->norm_eps;
+    }
     if (M > mx::MAX_COLS && mx::gemm_dq_supported(a.type, M, a.K)) {
         bool fits = true;  // every weight's rows within 32-bit element offsets
         for (int i = 0; i < n; i++) fits = fits && src0[i]->ne[1] * a.K < ((int64_t)1 << 31);
@@ -714,6 +720,9 @@ static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, con
             a.prob[i].row0 = 0;
             a.prob[i].y_col_stride = (int64_t)(dst[i]->nb[1] / 4);
             a.prob[i].y = (float *)dst[i]->data + m0 * a.prob[i].y_col_stride;
+            a.prob[i].res = f && f->residual && f->residual[i]
+                                ? (const float *)f->residual[i]->data + m0 * a.prob[i].y_col_stride
+                                : nullptr;
         }
         HIP_OK(mx::launch_matvec(a, be->stream), "MUL_MAT launch");
     }
@@ -746,6 +755,34 @@ MX_API int mx_mul_mat_group(mx_backend *be, int n, const mx_tensor *const *src0,
         if ((rc = matvec_group(be, k, src0 + i0, src1, dst + i0))) return rc;
     }
     return MX_SUCCESS;
+}
+
+static bool same_layout(const mx_tensor *a, const mx_tensor *b) {
+    return a && b && a->type == b->type && same_shape(a, b) && a->nb[0] == b->nb[0] && a->nb[1] == b->nb[1] &&
+           a->nb[2] == b->nb[2] && a->nb[3] == b->nb[3];
+}
+
+MX_API int mx_mul_mat_fused(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
+                            const mx_tensor *const *dst, const mx_fusion *f) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (n <= 0 || n > 4 || !src0 || !dst || !f) return fail(MX_INVALID, "fused product: 1 to 4 products and a fusion");
+    for (int i = 0; i < n; i++) {
+        if (!weight_ok(src0[i]) || !mx_supports_op(MX_OP_MUL_MAT, src0[i], src1, nullptr, dst[i]))
+            return fail(MX_UNSUPPORTED, "fused product %d: unsupported types, shapes or strides", i);
+        if (src0[i]->type != src0[0]->type || src0[i]->ne[0] != src0[0]->ne[0])
+            return fail(MX_UNSUPPORTED, "fused products must share the weight type and K");
+        if (f->residual && f->residual[i] && !same_layout(f->residual[i], dst[i]))
+            return fail(MX_UNSUPPORTED, "fused residual %d must have dst's shape and strides", i);
+    }
+    const int64_t K = src0[0]->ne[0];
+    if (src1->ne[1] > mx::MAX_COLS || src1->ne[2] * src1->ne[3] > mx::MAX_BATCH)
+        return fail(MX_UNSUPPORTED, "fusions run on the mat-vec path: at most %d columns", mx::MAX_COLS);
+    if (f->norm_w && (!f32_any(f->norm_w) || nelements(f->norm_w) != K || !aligned16(f->norm_w->data)))
+        return fail(MX_UNSUPPORTED, "the norm weight must be K contiguous floats, 16-byte aligned");
+    if (f->glu_b && !same_layout(f->glu_b, src1)) return fail(MX_UNSUPPORTED, "glu_b must have src1's layout");
+    if (nelements(src1) == 0) return MX_SUCCESS;
+    return matvec_group(be, n, src0, src1, dst, f);
 }
 
 MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids,
@@ -863,6 +900,57 @@ MX_API int mx_set_rows(mx_backend *be, const mx_tensor *src, const mx_tensor *id
     if (!supports_layer_op(MX_OP_SET_ROWS, src, idx, dst)) return fail(MX_UNSUPPORTED, "SET_ROWS: unsupported tensors");
     mx::RowsArgs r = rows_of(src, dst);
     HIP_OK(mx::launch_set_rows_f16(r, idx->data, idx->type == 27, dst->ne[1], be->err, be->stream), "SET_ROWS launch");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_qk_norm_rope_kv(mx_backend *be, const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
+                              const mx_tensor *q_norm, const mx_tensor *k_norm, const mx_tensor *pos,
+                              const mx_tensor *q_out, const mx_tensor *k_cache, const mx_tensor *v_cache, float eps,
+                              int n_dims, int mode, float freq_base, float freq_scale, float ext_factor,
+                              float attn_factor) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    auto heads = [](const mx_tensor *t) { return f32_any(t) && t->ne[0] == 128 && t->ne[3] == 1; };
+    auto cache = [](const mx_tensor *c, int64_t nkv) {
+        return c && c->type == MX_TYPE_F16 && shape_ok(c) && c->nb[0] == 2 && c->data && ((uintptr_t)c->data & 1) == 0 &&
+               c->ne[0] == nkv * 128 && c->ne[2] == 1 && c->ne[3] == 1 && c->nb[1] % 2 == 0;
+    };
+    auto norm = [](const mx_tensor *w) { return f32_any(w) && w->ne[0] == 128 && nelements(w) == 128; };
+    if (!heads(q) || !heads(k) || !heads(v) || !heads(q_out) || !same_shape(q, q_out) || !same_shape(k, v) ||
+        k->ne[2] != q->ne[2] || !norm(q_norm) || !norm(k_norm) || !cache(k_cache, k->ne[1]) ||
+        !cache(v_cache, k->ne[1]) || n_dims != 128 || mode != 2 || ext_factor != 0.0f || attn_factor != 1.0f)
+        return fail(MX_UNSUPPORTED, "q/k norm + RoPE + KV store: head size 128, NEOX over all of it, f16 caches");
+    if (!pos || pos->type != MX_TYPE_I32 || !pos->data || pos->nb[0] != 4 || pos->ne[0] != q->ne[2] ||
+        nelements(pos) != pos->ne[0])
+        return fail(MX_UNSUPPORTED, "q/k norm + RoPE + KV store: one I32 position per row");
+    mx::QkvPostArgs a{};
+    a.q = (const float *)q->data;
+    a.k = (const float *)k->data;
+    a.v = (const float *)v->data;
+    a.qw = (const float *)q_norm->data;
+    a.kw = (const float *)k_norm->data;
+    a.pos = (const int32_t *)pos->data;
+    a.q_out = (float *)q_out->data;
+    a.kc = k_cache->data;
+    a.vc = v_cache->data;
+    a.nq = q->ne[1];
+    a.nkv = k->ne[1];
+    a.cache_rows = std::min(k_cache->ne[1], v_cache->ne[1]);
+    a.q_nb1 = (int64_t)q->nb[1];
+    a.q_nb2 = (int64_t)q->nb[2];
+    a.k_nb1 = (int64_t)k->nb[1];
+    a.k_nb2 = (int64_t)k->nb[2];
+    a.v_nb1 = (int64_t)v->nb[1];
+    a.v_nb2 = (int64_t)v->nb[2];
+    a.qo_nb1 = (int64_t)q_out->nb[1];
+    a.qo_nb2 = (int64_t)q_out->nb[2];
+    a.kc_nb1 = (int64_t)k_cache->nb[1];
+    a.vc_nb1 = (int64_t)v_cache->nb[1];
+    a.eps = eps;
+    a.theta_scale = powf(freq_base, -2.0f / (float)n_dims);  // as ggml-cpu forms it
+    a.freq_scale = freq_scale;
+    a.err = be->err;
+    HIP_OK(mx::launch_qkv_post(a, q->ne[2], be->stream), "q/k norm + RoPE + KV store launch");
     return MX_SUCCESS;
 }
 

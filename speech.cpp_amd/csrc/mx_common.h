@@ -149,6 +149,7 @@ struct MatvecProblem {
     int64_t row0;          // first row of the matrix within the tensor's planes
     float *y;              // dst column 0 of this problem
     int64_t y_col_stride;  // floats between its dst columns
+    const float *res;      // residual added to the product (same layout as y; may be y), or null
 };
 struct MatvecArgs {
     int type;
@@ -170,6 +171,11 @@ struct MatvecArgs {
     int64_t ids_nb0, ids_nb1;  // bytes
     int n_mats, x_ne12;
     int *err;
+    // Fusions of the neighbouring decoder ops into the prologue (no ids mode): each src1 column becomes
+    // silu(x) * glu_b (glu_b: same layout as x) and then mul(rms_norm(., norm_eps), norm_w) before it is quantized.
+    const float *glu_b;
+    const float *norm_w;
+    float norm_eps;
 };
 hipError_t launch_matvec(const MatvecArgs &a, hipStream_t s);
 // The same products on F16 / F32 weights in ggml's row-major layout (prob[i].w.p0 = the weight's data; K % 8 == 0 for
@@ -277,6 +283,20 @@ struct FaArgs {
     float scale;
 };
 int fa_splits(int64_t n_q, int64_t n_head, int64_t n_kv);
+// q / k norm + NEOX RoPE + KV-cache stores for head size 128 (k_qkv_post): q, k, v heads h of row r at
+// base + h nb1 + r nb2 (F32); q_out likewise; the caches' row p at kc / vc + p kc_nb1 / vc_nb1 (F16, head h at
+// channel 128 h); pos[r] outside [0, cache_rows) sets *err |= 4 and stores nothing for that row.
+struct QkvPostArgs {
+    const float *q, *k, *v, *qw, *kw;
+    const int32_t *pos;
+    float *q_out;
+    void *kc, *vc;
+    int64_t nq, nkv, cache_rows;
+    int64_t q_nb1, q_nb2, k_nb1, k_nb2, v_nb1, v_nb2, qo_nb1, qo_nb2, kc_nb1, vc_nb1;
+    float eps, theta_scale, freq_scale;
+    int *err;
+};
+hipError_t launch_qkv_post(const QkvPostArgs &a, int64_t rows, hipStream_t s);
 hipError_t launch_flash_attn(const FaArgs &a, hipStream_t s);
 
 // ARGMAX (first of equal values) over nrows rows of ne0 floats (row stride nb1 bytes) into dst (stride dst_nb0 bytes).

@@ -231,3 +231,82 @@ def test_decoder_layers_chain(mx, be):
         be.sync()
     got = X.numpy().reshape(1, H)
     assert np.abs(got - x).max() <= 1e-4 * np.abs(x).max()
+
+
+def test_fused_products_equal_the_separate_ops(mx, be):
+    """mul(rms_norm) before q/k/v, swiglu before down and the residual add after it, fused into the mat-vec: the
+    same bits as the separate ops, and within the products' bar of the oracle."""
+    H, F, t, eps = 1024, 3072, O.TYPE_Q8_0, 1e-6
+    wq = [O.quantize_chunk(t, O.fill_normal(0x4A00 + i, n, H, 0.0, 0.02)) for i, n in enumerate((2048, 1024, 1024))]
+    wd = O.quantize_chunk(t, O.fill_normal(0x4A10, H, F, 0.0, 0.02))
+    x = O.fill_normal(0x4A20, 1, H) * np.float32(3)
+    nw = O.fill_normal(0x4A21, 1, H, 1.0, 0.1)[0]
+    g, u = O.fill_normal(0x4A22, 1, F), O.fill_normal(0x4A23, 1, F)
+    X, NW, G, U = dev(mx, be, x), dev(mx, be, nw), dev(mx, be, g), dev(mx, be, u)
+    WQ = [be.tensor(t, (H, w.shape[0]), w) for w in wq]
+    WD = be.tensor(t, (F, H), wd)
+    # separate ops
+    Hn = out(mx, be, (1, H))
+    be.rms_norm(X, Hn, eps, NW)
+    Ys = [out(mx, be, (1, w.shape[0])) for w in wq]
+    be.mul_mat_group(WQ, Hn, Ys)
+    A = out(mx, be, (1, F))
+    be.swiglu(G, U, A)
+    D = out(mx, be, (1, H))
+    be.mul_mat(WD, A, D)
+    R = dev(mx, be, x)
+    be.add(R, D, R)
+    # fused
+    Yf = [out(mx, be, (1, w.shape[0])) for w in wq]
+    be.mul_mat_fused(WQ, X, Yf, norm_w=NW, eps=eps)
+    Rf = dev(mx, be, x)
+    be.mul_mat_fused([WD], G, [Rf], glu_b=U, residual=[Rf])
+    be.sync()
+    for ys, yf in zip(Ys, Yf):
+        assert np.array_equal(ys.numpy(), yf.numpy())
+    assert np.array_equal(R.numpy(), Rf.numpy())
+    h = O.binary("mul", O.rms_norm(x, eps), nw)
+    for w, yf in zip(wq, Yf):
+        assert rel_err_rows(yf.numpy().reshape(1, -1), O.mul_mat(t, w, h)) <= 2e-5
+    ref = O.binary("add", x, O.mul_mat(t, wd, O.swiglu(g, u)))
+    assert np.abs(Rf.numpy().reshape(1, H) - ref).max() <= 2e-5 * np.abs(ref).max()
+
+
+def rel_err_rows(y, ref):
+    return float((np.abs(y - ref).max(axis=1) / np.abs(ref).max(axis=1)).max())
+
+
+def test_fused_qk_norm_rope_kv_equals_the_separate_ops(mx, be):
+    nq, nkv, hd, cap, eps, theta = 16, 8, 128, 96, 1e-6, 1e6
+    kv_dim = nkv * hd
+    q = O.fill_normal(0x4B00, 1, nq * hd) * np.float32(2)
+    k = O.fill_normal(0x4B01, 1, kv_dim)
+    v = O.fill_normal(0x4B02, 1, kv_dim)
+    qw, kw = O.fill_normal(0x4B03, 1, hd, 1.0, 0.1)[0], O.fill_normal(0x4B04, 1, hd, 1.0, 0.1)[0]
+    pos = np.array([77], np.int32)
+    cache0 = O.fill_normal(0x4B05, cap, kv_dim).astype(np.float16).view(np.uint16)
+    Q, K, V, QW, KW, P = dev(mx, be, q), dev(mx, be, k), dev(mx, be, v), dev(mx, be, qw), dev(mx, be, kw), \
+        dev(mx, be, pos, mx.I32)
+    qv = Q.view((hd, nq, 1), (4, hd * 4, nq * hd * 4))
+    kv = K.view((hd, nkv, 1), (4, hd * 4, kv_dim * 4))
+    vv = V.view((hd, nkv, 1), (4, hd * 4, kv_dim * 4))
+    # separate ops
+    KC, VC = dev(mx, be, cache0, mx.F16), dev(mx, be, cache0, mx.F16)
+    qn, kn = be.tensor(mx.F32, (hd, nq, 1)), be.tensor(mx.F32, (hd, nkv, 1))
+    qr, kr = be.tensor(mx.F32, (hd, nq, 1)), be.tensor(mx.F32, (hd, nkv, 1))
+    be.rms_norm(qv, qn, eps, QW)
+    be.rms_norm(kv, kn, eps, KW)
+    be.set_rows(V, P, VC)
+    be.rope(qn, P, qr, hd, theta)
+    be.rope(kn, P, kr, hd, theta)
+    be.set_rows(kr.view((kv_dim, 1), (4, kv_dim * 4)), P, KC)
+    # fused
+    KC2, VC2 = dev(mx, be, cache0, mx.F16), dev(mx, be, cache0, mx.F16)
+    qo = be.tensor(mx.F32, (hd, nq, 1))
+    be.qk_norm_rope_kv(qv, kv, vv, QW, KW, P, qo, KC2, VC2, eps, theta)
+    be.sync()
+    assert np.array_equal(qo.numpy(), qr.numpy())
+    assert np.array_equal(KC2.get_bytes(), KC.get_bytes())
+    assert np.array_equal(VC2.get_bytes(), VC.get_bytes())
+    ref_q = O.rope_neox(O.binary("mul", O.rms_norm(q.reshape(1, nq, hd), eps), qw), pos, hd, theta)
+    assert np.abs(qo.numpy().reshape(1, nq, hd) - ref_q).max() <= 2e-6
