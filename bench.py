@@ -521,14 +521,10 @@ def full_step_launches(be, mx, dec, st, ids, nq, nkv, hd, fused=True):
               Launch("down", wd + 4 * (dec.ffn + H), 0,
                      lambda w=w: be.mul_mat(w["down"], st["act"], o["down"]), weight_bytes=wd),
               Launch("add", 12 * H, 0, lambda: be.add(x, o["down"], x))]
-    if fused:
-        L.append(Launch("lm_head", dec.head_bytes() + 4 * (H + dec.vocab), 0,
-                        lambda: be.mul_mat_fused([dec.embd], x, [st["logits"]], norm_w=st["final_norm"], eps=RMS_EPS),
-                        weight_bytes=dec.head_bytes()))
-    else:
-        L += [Launch("norm", 8 * H, 0, lambda: be.rms_norm(x, h, RMS_EPS, st["final_norm"])),
-              Launch("lm_head", dec.head_bytes() + 4 * (H + dec.vocab), 0,
-                     lambda: be.mul_mat(dec.embd, h, st["logits"]), weight_bytes=dec.head_bytes())]
+    # the head keeps its norm apart: fused, each of its 9,496 workgroups would redo the norm's reduction
+    L += [Launch("norm", 8 * H, 0, lambda: be.rms_norm(x, h, RMS_EPS, st["final_norm"])),
+          Launch("lm_head", dec.head_bytes() + 4 * (H + dec.vocab), 0,
+                 lambda: be.mul_mat(dec.embd, h, st["logits"]), weight_bytes=dec.head_bytes())]
     L.append(Launch("argmax", 4 * dec.vocab + 4, 0, lambda: be.argmax(st["logits"], st["pick"])))
     return L
 

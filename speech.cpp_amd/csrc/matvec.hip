@@ -63,14 +63,23 @@ __device__ __forceinline__ float4 load_x4(const float *xc, int e, int K) {
 // -- and is quantized. Pieces of 1024 elements past the preloaded ones are read again after the sum.
 template <int TYPE, int NC>
 __device__ __forceinline__ void fused_prologue(const MatvecArgs &a, const float *x, int xi12, int i13,
-                                               float4 (&xr)[NC][xpre<NC>()], int8_t *xq, float *xd, int *xbs) {
+                                               float4 (&xr)[NC][xpre<NC>()], const float4 (&br)[NC][xpre<NC>()],
+                                               const float4 (&wr)[xpre<NC>()], int8_t *xq, float *xd, int *xbs) {
     constexpr int XP = xpre<NC>();
     constexpr int XDB = TYPE == MX_TYPE_Q8_0 ? 32 : 256;
     const int K = (int)a.K;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     __shared__ double red[NC][4];
     const float *gb = a.glu_b ? a.glu_b + xi12 * a.x_b2 + i13 * a.x_b3 : nullptr;
-    auto piece = [&](int c, int base, float4 v) -> float4 {  // glu of one loaded piece
+    // glu of one loaded piece; the preloaded pieces' second operands came in with x (br)
+    auto piece_b = [&](float4 v, float4 b) -> float4 {
+        v.x = v.x / (1.0f + expf(-v.x)) * b.x;
+        v.y = v.y / (1.0f + expf(-v.y)) * b.y;
+        v.z = v.z / (1.0f + expf(-v.z)) * b.z;
+        v.w = v.w / (1.0f + expf(-v.w)) * b.w;
+        return v;
+    };
+    auto piece = [&](int c, int base, float4 v) -> float4 {
         if (gb) {
             const float4 b = load_x4(gb + c * a.x_col_stride, base + 4 * tid, K);
             v.x = v.x / (1.0f + expf(-v.x)) * b.x;
@@ -80,10 +89,12 @@ __device__ __forceinline__ void fused_prologue(const MatvecArgs &a, const float 
         }
         return v;
     };
+    if (gb) {
 #pragma unroll
-    for (int c = 0; c < NC; c++)
+        for (int c = 0; c < NC; c++)
 #pragma unroll
-        for (int i = 0; i < XP; i++) xr[c][i] = piece(c, 1024 * i, xr[c][i]);
+            for (int i = 0; i < XP; i++) xr[c][i] = piece_b(xr[c][i], br[c][i]);
+    }
     float scale[NC];
     if (a.norm_w) {
 #pragma unroll
@@ -112,7 +123,7 @@ __device__ __forceinline__ void fused_prologue(const MatvecArgs &a, const float 
     }
     auto normed = [&](int c, int base, float4 v) -> float4 {
         if (a.norm_w) {
-            const float4 w = load_x4(a.norm_w, base + 4 * tid, K);
+            const float4 w = base < 1024 * XP ? wr[base / 1024] : load_x4(a.norm_w, base + 4 * tid, K);
             v.x = (v.x * scale[c]) * w.x;
             v.y = (v.y * scale[c]) * w.y;
             v.z = (v.z * scale[c]) * w.z;
@@ -166,6 +177,19 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     for (int c = 0; c < NC; c++)
 #pragma unroll
         for (int i = 0; i < XP; i++) xr[c][i] = load_x4(x + c * a.x_col_stride, 1024 * i + 4 * tid, K);
+    // the fused prologue's other operands come in with x: SwiGLU's second input and the norm weight
+    float4 br[NC][XP], wr[XP];
+    if (a.glu_b) {
+        const float *gb = a.glu_b + xi12 * a.x_b2 + i13 * a.x_b3;
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int i = 0; i < XP; i++) br[c][i] = load_x4(gb + c * a.x_col_stride, 1024 * i + 4 * tid, K);
+    }
+    if (a.norm_w) {
+#pragma unroll
+        for (int i = 0; i < XP; i++) wr[i] = load_x4(a.norm_w, 1024 * i + 4 * tid, K);
+    }
 
     const MatvecProblem p = pick_problem(a, (int)blockIdx.y);
     constexpr int G = 64 / LPR;  // rows in flight per wave
@@ -177,6 +201,14 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     // lane-dependent branch, so they issue back to back.
     const int64_t grow = p.row0 + (int64_t)mat * p.N + (has_row ? row : p.N - 1);
     const int nchunks = K / chunk_elems<TYPE>();
+
+    // the residual the epilogue adds, requested now rather than after the reduction
+    const int64_t yoff = i12 * a.y_b2 + i13 * a.y_b3 + row;
+    float rr[NC];
+    if (p.res && has_row && sub == LPR - 1) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) rr[c] = p.res[yoff + c * p.y_col_stride];
+    }
 
     WChunk<TYPE> pre[PRELOAD];
 #pragma unroll
@@ -190,7 +222,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     constexpr int XDB = TYPE == MX_TYPE_Q8_0 ? 32 : 256;
     int *xbs = (int *)(xd + NC * (K / XDB));
     if (a.glu_b || a.norm_w) {  // uniform: the fused prologue
-        fused_prologue<TYPE, NC>(a, x, xi12, i13, xr, xq, xd, xbs);
+        fused_prologue<TYPE, NC>(a, x, xi12, i13, xr, br, wr, xq, xd, xbs);
     } else {
 #pragma unroll
         for (int c = 0; c < NC; c++) {
@@ -221,11 +253,10 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
 #pragma unroll
     for (int c = 0; c < NC; c++) acc[c] = sum_lanes<LPR>(acc[c]);
     if (sub == LPR - 1) {  // the lane holding the group's sum
-        const int64_t off = i12 * a.y_b2 + i13 * a.y_b3 + row;
-        float *y = p.y + off;
+        float *y = p.y + yoff;
         if (p.res) {  // the residual ADD that follows the product, fused
 #pragma unroll
-            for (int c = 0; c < NC; c++) y[c * p.y_col_stride] = p.res[off + c * p.y_col_stride] + acc[c];
+            for (int c = 0; c < NC; c++) y[c * p.y_col_stride] = rr[c] + acc[c];
         } else {
 #pragma unroll
             for (int c = 0; c < NC; c++) y[c * p.y_col_stride] = acc[c];

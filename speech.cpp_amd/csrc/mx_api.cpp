@@ -825,8 +825,10 @@ MX_API int mx_argmax(mx_backend *be, const mx_tensor *src, const mx_tensor *dst)
     if (rc) return rc;
     if (!mx_supports_op(MX_OP_ARGMAX, src, nullptr, nullptr, dst))
         return fail(MX_UNSUPPORTED, "ARGMAX: unsupported types, shapes or strides");
+    const int parts = mx::argmax_parts(src->ne[0], src->ne[1]);
+    if (parts > 1 && (rc = ensure_scratch(be, (size_t)src->ne[1] * (size_t)parts * 8))) return rc;
     HIP_OK(mx::launch_argmax((const float *)src->data, src->ne[0], src->ne[1], (int64_t)src->nb[1],
-                             (int32_t *)dst->data, (int64_t)dst->nb[0], be->stream),
+                             (int32_t *)dst->data, (int64_t)dst->nb[0], be->scratch, be->stream),
            "ARGMAX launch");
     return MX_SUCCESS;
 }

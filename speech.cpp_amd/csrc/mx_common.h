@@ -300,8 +300,11 @@ hipError_t launch_qkv_post(const QkvPostArgs &a, int64_t rows, hipStream_t s);
 hipError_t launch_flash_attn(const FaArgs &a, hipStream_t s);
 
 // ARGMAX (first of equal values) over nrows rows of ne0 floats (row stride nb1 bytes) into dst (stride dst_nb0 bytes).
+// Rows of more than 8192 floats split into argmax_parts(ne0, nrows) parts, whose (value, index) pairs go to scratch
+// (nrows * parts float2).
+int argmax_parts(int64_t ne0, int64_t nrows);
 hipError_t launch_argmax(const float *src, int64_t ne0, int64_t nrows, int64_t nb1, int32_t *dst, int64_t dst_nb0,
-                         hipStream_t s);
+                         void *scratch, hipStream_t s);
 
 // Pairs per chunk of one expert's (token, slot) pairs: two 16-row MFMA tiles that share each expanded weight fragment.
 constexpr int MMID_CHUNK = 32;

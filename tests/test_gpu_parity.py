@@ -524,6 +524,25 @@ def test_argmax_matches_oracle(mx, be, n, R):
     assert np.array_equal(Y.numpy().reshape(R), O.argmax(x))
 
 
+def test_argmax_rows_split_over_workgroups(mx, be):
+    """A vocabulary-sized row is split over many workgroups: ties across the parts, a part that holds only NaNs and
+    a NaN at index 0 still follow the first-of-equal rule."""
+    n = 151936
+    x = np.random.default_rng(0xA48).standard_normal((3, n)).astype(np.float32)
+    x[0, [70001, 100, 151935]] = 50.0           # the first of three, in three parts
+    x[1, 4096 * 5:4096 * 9] = np.nan           # whole parts of NaN
+    x[1, [4096 * 9, 4096 * 30 + 3]] = 9.0      # tie in two parts
+    x[2, 0] = np.nan                            # index 0 wins
+    x[2, 77] = 1e30
+    for R in (1, 3):
+        X = be.tensor(mx.F32, (n, R), x[:R])
+        Y = be.tensor(mx.I32, (R,))
+        be.argmax(X, Y)
+        be.sync()
+        assert np.array_equal(Y.numpy().reshape(R), O.argmax(x[:R]))
+    assert list(O.argmax(x)) == [100, 4096 * 9, 0]
+
+
 def test_argmax_padded_rows(mx, be):
     """Rows whose length is not a multiple of four (the kernel's tail) inside 16-byte-aligned padded rows."""
     n, R, pitch = 1001, 6, 1008
