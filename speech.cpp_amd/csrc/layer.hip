@@ -8,6 +8,10 @@
 //                   fp32, as the graph requests with ggml_prec_set_acc(GGML_PREC_F32) (ggml-cpu's own loop keeps it
 //                   in fp16).
 #include "mx_common.h"
+
+#ifndef MX_FA_GROUP_WGS
+#define MX_FA_GROUP_WGS 256  // k_fa_gqa workgroups a launch aims for (at most one 64-position chunk each, if so many)
+#endif
 #include "mx_device.h"
 
 namespace mx {
@@ -312,10 +316,8 @@ __global__ __launch_bounds__(64) void k_fa_split(FaArgs a) {
 // exp(m_s - M) and the total come from one round of loads and two wave reductions; the channels are gathered eight
 // splits at a time, their loads in flight together.
 template <int D>
-__global__ __launch_bounds__(64) void k_fa_merge(FaArgs a) {
-    constexpr int DL = D / 64;
-    const int lane = threadIdx.x;
-    const int64_t h = blockIdx.x, i = blockIdx.y;
+__device__ __forceinline__ void fa_merge_head(const FaArgs &a, int64_t h, int64_t i, int lane) {
+    constexpr int DL = D / 64, NB = 64 / DL;  // NB splits' channels per round of loads (64 registers)
     const int ns = a.nsplit;
     const float *part = a.part + (i * a.n_head + h) * ns * (D + 2);
     float ms = -INFINITY, ss = 0.0f;
@@ -323,30 +325,190 @@ __global__ __launch_bounds__(64) void k_fa_merge(FaArgs a) {
         ms = part[lane * (D + 2)];
         ss = part[lane * (D + 2) + 1];
     }
+    float v[NB][DL];
+    auto gather = [&](int s0) {
+#pragma unroll
+        for (int u = 0; u < NB; u++) {
+            const int sp = min(s0 + u, ns - 1);
+#pragma unroll
+            for (int c = 0; c < DL; c++) v[u][c] = part[sp * (D + 2) + 2 + DL * lane + c];
+        }
+    };
+    gather(0);  // the first round's loads travel with the maxima's
     const float M = wave_max_f(ms);
     const float w = (ms == -INFINITY) ? 0.0f : expf(ms - M);  // a split with nothing visible weighs 0
     const float S = wave_sum_f(ss * w);
     float acc[DL];
 #pragma unroll
     for (int c = 0; c < DL; c++) acc[c] = 0.0f;
-    for (int s0 = 0; s0 < ns; s0 += 8) {
-        float v[8][DL], ws[8];
+    for (int s0 = 0; s0 < ns; s0 += NB) {
+        if (s0 > 0) gather(s0);
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int sp = min(s0 + u, ns - 1);
-            ws[u] = s0 + u < ns ? __shfl(w, sp, 64) : 0.0f;
+        for (int u = 0; u < NB; u++) {
+            const float wu = s0 + u < ns ? __shfl(w, min(s0 + u, ns - 1), 64) : 0.0f;
 #pragma unroll
-            for (int c = 0; c < DL; c++) v[u][c] = part[sp * (D + 2) + 2 + DL * lane + c];
+            for (int c = 0; c < DL; c++) acc[c] = fmaf(v[u][c], wu, acc[c]);
         }
-#pragma unroll
-        for (int u = 0; u < 8; u++)
-#pragma unroll
-            for (int c = 0; c < DL; c++) acc[c] = fmaf(v[u][c], ws[u], acc[c]);
     }
     float *o = a.dst + (i * a.n_head + h) * D;
     const float inv = S == 0.0f ? 0.0f : 1.0f / S;
 #pragma unroll
     for (int c = 0; c < DL; c++) o[DL * lane + c] = acc[c] * inv;
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void k_fa_merge(FaArgs a) {
+    fa_merge_head<D>(a, blockIdx.x, blockIdx.y, threadIdx.x);
+}
+
+// One 64-position chunk of 256-byte K and V rows for 256 threads: thread t copies 16 bytes of rows t / 16 + 16 u,
+// threads 0..63 the mask of position t. Rows past j1 repeat row j1 - 1 and are masked.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 class here is kept in scratch)
+struct FaStage {
+    u32x4 k[4], v[4];
+    float mv;
+};
+
+__device__ __forceinline__ void fa_stage_load(FaStage &st, const FaArgs &a, const uint8_t *kb, const uint8_t *vb,
+                                              const uint16_t *mrow, int64_t base, int64_t j1, int tid) {
+    const int lr = tid >> 4, seg = tid & 15;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int64_t jr = min(base + lr + 16 * u, j1 - 1);
+        st.k[u] = *(const u32x4 *)(kb + jr * a.k_nb1 + 16 * seg);
+        st.v[u] = *(const u32x4 *)(vb + jr * a.v_nb1 + 16 * seg);
+    }
+    st.mv = -INFINITY;
+    if (tid < 64 && base + tid < j1) st.mv = mrow ? h2f(mrow[base + tid]) : 0.0f;
+}
+
+// Pass 1 for head size 128 and GQA groups of G = 1, 2 or 4 q heads per kv head: one 256-thread workgroup per (split,
+// kv head, query row) serves the group's G heads, so a group reads K and V once. Per 64-position chunk the keys and
+// values are copied to LDS with coalesced 16-byte loads (sixteen threads per 256-byte row); T = 256 / (64 G) threads share each
+// score (CPT channels each, then a shuffle sum); one wave per head runs the online softmax over the chunk; and for
+// P.V each thread owns a channel pair of one head over PLEN positions, the position parts added at the end.
+template <int G>
+__global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a) {
+    constexpr int D = 128, T = 256 / (G * 64), CPT = D / T, PP = 256 / G / 64, PLEN = 64 / PP;
+    constexpr int KS = D * 2 + 16;  // bytes per K row in LDS: padded so 16 rows read at one offset miss each other
+    __shared__ __align__(16) uint8_t Ks[64 * KS];
+    __shared__ __align__(16) uint32_t Vs[64 * 64];  // [position][channel pair]
+    __shared__ __align__(16) float qs[G][D];
+    __shared__ float ps[G][64], mvs[64], hm[G], hs[G], hr[G];
+    __shared__ __align__(16) float accs[PP * G * D];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t split = blockIdx.x, hk = blockIdx.y, i = blockIdx.z;
+    const uint8_t *kb = (const uint8_t *)a.k + hk * a.k_nb2;
+    const uint8_t *vb = (const uint8_t *)a.v + hk * a.v_nb2;
+    const uint16_t *mrow = a.mask ? (const uint16_t *)((const uint8_t *)a.mask + i * a.m_nb1) : nullptr;
+    const int64_t j0 = split * a.split_len, j1 = min(a.n_kv, j0 + a.split_len);
+    const int lr = tid >> 4, seg = tid & 15;  // copy role: 16 threads per row, rows lr + 16 t, 16 bytes each
+    FaStage st;
+    if (j0 < j1) fa_stage_load(st, a, kb, vb, mrow, j0, j1, tid);  // the first chunk's loads go out before q's
+    for (int e = tid; e < G * D; e += 256) {
+        const int g = e / D, d = e % D;
+        const float *q = (const float *)((const uint8_t *)a.q + i * a.q_nb1 + (hk * G + g) * a.q_nb2);
+        qs[g][d] = h2f(f2h(q[d]));  // ggml converts q to K's f16 first
+    }
+    if (tid < G) {
+        hm[tid] = -INFINITY;
+        hs[tid] = 0.0f;
+    }
+    // roles: score (g_s, pos_s, part_s); P.V (g_v, channel pair cp, positions part_v)
+    const int dot = tid / T, g_s = dot / 64, pos_s = dot % 64, part_s = tid % T;
+    const int wv = tid % (256 / G), g_v = tid / (256 / G), cp = wv % 64, part_v = wv / 64;
+    float acc0 = 0.0f, acc1 = 0.0f;
+    for (int64_t base = j0; base < j1; base += 64) {
+        __syncthreads();  // the previous chunk is done with Ks, Vs, ps
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            *(u32x4 *)(Ks + (lr + 16 * t) * KS + 16 * seg) = st.k[t];
+            *(u32x4 *)(Vs + (lr + 16 * t) * 64 + 4 * seg) = st.v[t];
+        }
+        if (tid < 64) mvs[tid] = st.mv;
+        __syncthreads();
+        if (base + 64 < j1) fa_stage_load(st, a, kb, vb, mrow, base + 64, j1, tid);  // overlaps this chunk's work
+        // scores
+        {
+            const uint8_t *kr = Ks + pos_s * KS + part_s * CPT * 2;
+            const float *qv = qs[g_s] + part_s * CPT;
+            float d0 = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CPT / 8; c++) {
+                const uint4 w = *(const uint4 *)(kr + 16 * c);
+                const float4 qa = *(const float4 *)(qv + 8 * c), qb = *(const float4 *)(qv + 8 * c + 4);
+                d0 = fmaf(h2f((uint16_t)(w.x & 0xFFFF)), qa.x, d0);
+                d0 = fmaf(h2f((uint16_t)(w.x >> 16)), qa.y, d0);
+                d0 = fmaf(h2f((uint16_t)(w.y & 0xFFFF)), qa.z, d0);
+                d0 = fmaf(h2f((uint16_t)(w.y >> 16)), qa.w, d0);
+                d0 = fmaf(h2f((uint16_t)(w.z & 0xFFFF)), qb.x, d0);
+                d0 = fmaf(h2f((uint16_t)(w.z >> 16)), qb.y, d0);
+                d0 = fmaf(h2f((uint16_t)(w.w & 0xFFFF)), qb.z, d0);
+                d0 = fmaf(h2f((uint16_t)(w.w >> 16)), qb.w, d0);
+            }
+            if constexpr (T >= 2) d0 += __shfl_xor(d0, 1, 64);
+            if constexpr (T >= 4) d0 += __shfl_xor(d0, 2, 64);
+            const float m = mvs[pos_s];
+            if (part_s == 0) ps[g_s][pos_s] = m == -INFINITY ? -INFINITY : d0 * a.scale + m;
+        }
+        __syncthreads();
+        // online softmax, one wave per head
+        if (wave < G) {
+            const float sv = ps[wave][lane];
+            const float mc = wave_max_f(sv);
+            const float Mold = hm[wave];
+            float r = 1.0f, p = 0.0f, Mn = Mold;
+            if (mc != -INFINITY) {
+                Mn = fmaxf(Mold, mc);
+                r = expf(Mold - Mn);
+                p = sv == -INFINITY ? 0.0f : expf(sv - Mn);
+            }
+            const float sum = wave_sum_f(p);
+            ps[wave][lane] = p;
+            if (lane == 0) {
+                hr[wave] = r;
+                hm[wave] = Mn;
+                hs[wave] = hs[wave] * r + sum;
+            }
+        }
+        __syncthreads();
+        // P.V
+        {
+            const float r = hr[g_v];
+            acc0 *= r;
+            acc1 *= r;
+#pragma unroll
+            for (int t = 0; t < PLEN; t++) {
+                const int j = part_v * PLEN + t;
+                const float pj = ps[g_v][j];
+                const uint32_t v2 = Vs[j * 64 + cp];
+                acc0 = fmaf(pj, h2f((uint16_t)(v2 & 0xFFFF)), acc0);
+                acc1 = fmaf(pj, h2f((uint16_t)(v2 >> 16)), acc1);
+            }
+        }
+    }
+    __syncthreads();
+    accs[(part_v * G + g_v) * D + 2 * cp] = acc0;
+    accs[(part_v * G + g_v) * D + 2 * cp + 1] = acc1;
+    __syncthreads();
+    for (int e = tid; e < G * D; e += 256) {
+        const int g = e / D, c = e % D;
+        float tot = 0.0f;
+#pragma unroll
+        for (int pp = 0; pp < PP; pp++) tot += accs[(pp * G + g) * D + c];
+        const int64_t h = hk * G + g;
+        if (a.nsplit == 1) {
+            const float S = hs[g];
+            a.dst[(i * a.n_head + h) * D + c] = tot * (S == 0.0f ? 0.0f : 1.0f / S);
+        } else {
+            float *part = a.part + ((i * a.n_head + h) * a.nsplit + split) * (D + 2);
+            part[2 + c] = tot;
+            if (c == 0) {
+                part[0] = hm[g];
+                part[1] = hs[g];
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------- launches
@@ -391,10 +553,16 @@ hipError_t launch_set_rows_f16(const RowsArgs &a, const void *idx, bool idx_i64,
     return hipGetLastError();
 }
 
-int fa_splits(int64_t n_q, int64_t n_head, int64_t n_kv) {
-    // about 512 (split, head, row) waves for the chip, each split a whole number of 64-position blocks
+static bool fa_grouped(int D, int64_t gqa) { return D == 128 && (gqa == 1 || gqa == 2 || gqa == 4); }
+
+int fa_splits(int64_t n_q, int64_t n_head, int64_t n_kv, int64_t gqa, int D) {
+    // each split a whole number of 64-position blocks: about MX_FA_GROUP_WGS (split, kv head, row) workgroups for
+    // k_fa_gqa, about 512 (split, head, row) waves for k_fa_split
     const int64_t blocks = (n_kv + 63) / 64;
-    int64_t want = (512 + n_q * n_head - 1) / (n_q * n_head);
+    const bool grouped = fa_grouped(D, gqa);
+    const int64_t units = grouped ? n_q * (n_head / gqa) : n_q * n_head;
+    const int64_t target = grouped ? MX_FA_GROUP_WGS : 512;
+    int64_t want = (target + units - 1) / units;
     want = want < 1 ? 1 : (want > blocks ? blocks : want);
     want = want > 64 ? 64 : want;  // the merge holds one split per lane
     const int64_t per = (blocks + want - 1) / want;  // blocks per split
@@ -404,7 +572,11 @@ int fa_splits(int64_t n_q, int64_t n_head, int64_t n_kv) {
 hipError_t launch_flash_attn(const FaArgs &a, hipStream_t s) {
     if (a.n_q == 0 || a.n_head == 0) return hipSuccess;
     const dim3 g1((unsigned)a.nsplit, (unsigned)a.n_head, (unsigned)a.n_q);
-    if (a.D == 128) hipLaunchKernelGGL(k_fa_split<128>, g1, dim3(64), 0, s, a);
+    const dim3 gk((unsigned)a.nsplit, (unsigned)(a.n_head / a.gqa), (unsigned)a.n_q);
+    if (fa_grouped(a.D, a.gqa) && a.gqa == 2) hipLaunchKernelGGL(k_fa_gqa<2>, gk, dim3(256), 0, s, a);
+    else if (fa_grouped(a.D, a.gqa) && a.gqa == 1) hipLaunchKernelGGL(k_fa_gqa<1>, gk, dim3(256), 0, s, a);
+    else if (fa_grouped(a.D, a.gqa)) hipLaunchKernelGGL(k_fa_gqa<4>, gk, dim3(256), 0, s, a);
+    else if (a.D == 128) hipLaunchKernelGGL(k_fa_split<128>, g1, dim3(64), 0, s, a);
     else if (a.D == 64) hipLaunchKernelGGL(k_fa_split<64>, g1, dim3(64), 0, s, a);
     else return hipErrorInvalidValue;
     hipError_t e = hipGetLastError();

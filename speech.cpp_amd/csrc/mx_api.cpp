@@ -1003,7 +1003,7 @@ MX_API int mx_flash_attn_ext(mx_backend *be, const mx_tensor *q, const mx_tensor
     a.v_nb2 = (int64_t)v->nb[2];
     a.m_nb1 = mask ? (int64_t)mask->nb[1] : 0;
     a.scale = scale;
-    a.nsplit = mx::fa_splits(a.n_q, a.n_head, a.n_kv);
+    a.nsplit = mx::fa_splits(a.n_q, a.n_head, a.n_kv, a.gqa, a.D);
     a.split_len = ((a.n_kv + 63) / 64 + a.nsplit - 1) / a.nsplit * 64;  // whole 64-position blocks per split
     if (a.nsplit > 1) {
         const size_t need = (size_t)a.n_q * (size_t)a.n_head * (size_t)a.nsplit * (size_t)(a.D + 2) * 4;

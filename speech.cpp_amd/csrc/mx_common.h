@@ -282,7 +282,7 @@ struct FaArgs {
     int64_t q_nb1, q_nb2, k_nb1, k_nb2, v_nb1, v_nb2, m_nb1;
     float scale;
 };
-int fa_splits(int64_t n_q, int64_t n_head, int64_t n_kv);
+int fa_splits(int64_t n_q, int64_t n_head, int64_t n_kv, int64_t gqa, int D);
 // q / k norm + NEOX RoPE + KV-cache stores for head size 128 (k_qkv_post): q, k, v heads h of row r at
 // base + h nb1 + r nb2 (F32); q_out likewise; the caches' row p at kc / vc + p kc_nb1 / vc_nb1 (F16, head h at
 // channel 128 h); pos[r] outside [0, cache_rows) sets *err |= 4 and stores nothing for that row.
