@@ -86,35 +86,43 @@ class Launch:
         self.weight_bytes = nbytes if weight_bytes is None else weight_bytes
 
 
-def per_label_pass(be, launches, reps: int):
+def per_label_pass(be, launches, reps: int, use_graph: bool = True):
     """Mean time (ms) per launch of each label: each label's launches are recorded as a graph of their own and
     replayed, so no event sits between two kernels. A label of few small launches repeats them inside its graph (up to
     32 launches), so the graph's own launch cost does not swamp them; launches of 16 MB and more are recorded once, as
-    a repeat would find them in the 256 MB last-level cache. All graphs are recorded first and freed last."""
+    a repeat would find them in the 256 MB last-level cache. All graphs are recorded first and freed last. Without
+    graphs the same launches are issued eagerly between the events."""
     labels = []
     for L in launches:
         if L.label not in labels:
             labels.append(L.label)
-    graphs, counts = {}, {}
+    graphs, counts, runs = {}, {}, {}
     for lab in labels:
         mine = [L for L in launches if L.label == lab]
         rep = 1 if max(L.nbytes for L in mine) >= (16 << 20) else max(1, 32 // len(mine))
-        be.graph_begin()
-        for _ in range(rep):
-            for L in mine:
-                L.fn()
-        graphs[lab] = be.graph_end()
+
+        def run(mine=mine, rep=rep):
+            for _ in range(rep):
+                for L in mine:
+                    L.fn()
+        if use_graph:
+            be.graph_begin()
+            run()
+            graphs[lab] = be.graph_end()
+            runs[lab] = (lambda g=graphs[lab]: be.graph_launch(g))
+        else:
+            runs[lab] = run
         counts[lab] = rep * len(mine)
     out = {}
     e0, e1 = be.event(), be.event()
     for lab in labels:
         count = counts[lab]
         for _ in range(3):
-            be.graph_launch(graphs[lab])
+            runs[lab]()
         be.sync()
         be.record(e0)
         for _ in range(reps):
-            be.graph_launch(graphs[lab])
+            runs[lab]()
         be.record(e1)
         be.sync()
         out[lab] = be.elapsed_ms(e0, e1) / (reps * count)
@@ -377,7 +385,7 @@ def run_decode(args, mx, be, threads):
     ms_per_step = time_graph(be, launches, args.steps, args.warmup, not args.no_graph)
     # Roofline of the dominant kernel: k_matvec over Q8_0 at batch 1 (every launch of the step but the one GET_ROWS;
     # the template is instantiated per lanes-per-row, all the same code), timed inside the step.
-    table = label_table(launches, per_label_pass(be, launches, reps=20))
+    table = label_table(launches, per_label_pass(be, launches, reps=20, use_graph=not args.no_graph))
     roof = step_hbm_roofline("k_matvec<Q8_0, NC=1>", [L for L in launches if L.label != "get_rows"], ms_per_step,
                              ms_other=table["get_rows"][3])
     roof["traffic"] = read_traffic("decode")
@@ -571,13 +579,13 @@ def run_decode_full(args, mx, be, threads):
     weight_bytes = sum(L.weight_bytes for L in launches if L.label in ("qkv", "attn_o", "gate_up", "down", "lm_head"))
     kv_bytes = dec.layers_n * 2 * 2 * (KV_PAST + 1) * nkv * hd
     ms_per_step = time_graph(be, launches, args.steps, args.warmup, not args.no_graph)
-    table = label_table(launches, per_label_pass(be, launches, reps=10))
+    table = label_table(launches, per_label_pass(be, launches, reps=10, use_graph=not args.no_graph))
     tok_s = 1e3 / ms_per_step
     mv = [L for L in launches if L.label in ("qkv", "attn_o", "gate_up", "down", "lm_head")]
     ms_mv = sum(table[lab][3] * table[lab][0] for lab in ("qkv", "attn_o", "gate_up", "down", "lm_head"))
     roof = hbm_roofline("k_matvec<Q8_0, NC=1>", table, ["qkv", "attn_o", "gate_up", "down", "lm_head"])
     roof["traffic"] = read_traffic("decode")
-    att = hbm_roofline("k_fa_split<128> + k_fa_merge", table, ["attention"])
+    att = hbm_roofline("k_fa_gqa<2> + k_fa_merge<128>", table, ["attention"])
     result = base_result(args, round(tok_s, 2), "tok/s", ms_per_step, "int8", {
         "workload": "qwen3-0.6b-shape decode step, batch 1, every op on the device, KV cache at 1024 positions",
         **S, "weights": "Q8_0", "kv_cache": "f16", "kv_past": KV_PAST, "kv_read": st["n_kv"],
@@ -723,7 +731,7 @@ def run_prefill_q4k(args, mx, be, threads):
     launches = prefill_launches(be, dec, acts, lambda lab, t: f"{lab}:{NAME[t]}")
     ops = sum(L.ops for L in launches)
     ms_per_step = time_graph(be, launches, args.steps, args.warmup, not args.no_graph)
-    table = label_table(launches, per_label_pass(be, launches, reps=5))
+    table = label_table(launches, per_label_pass(be, launches, reps=5, use_graph=not args.no_graph))
     roof = mfma_roofline("k_gemm_q4k (with its Q8_K activation pass)", table,
                          [l for l in table if l.endswith(":Q4_K")])
     roof["traffic"] = read_traffic("prefill-q4k")
@@ -766,7 +774,7 @@ def run_asr(args, mx, be, threads):
     ms_pre = time_graph(be, pre, max(1, args.steps), args.warmup, not args.no_graph)
     ms_tok = time_graph(be, tok, max(1, args.steps) * ASR_DECODE_TOKENS, args.warmup, not args.no_graph)
     ms_step = ms_pre + ASR_DECODE_TOKENS * ms_tok
-    table = label_table(pre + tok, per_label_pass(be, pre + tok, reps=3))
+    table = label_table(pre + tok, per_label_pass(be, pre + tok, reps=3, use_graph=not args.no_graph))
     # the prefill GEMM dequantizes Q8_0 weights and Q8_0-quantized activations to fp16 and accumulates in fp32 on
     # fp16 MFMA (MX_GEMM_DQ=0 selects the int8 MFMA GEMM); the decode mat-vecs use int8 dot products
     dq = os.environ.get("MX_GEMM_DQ", "1") != "0"
@@ -901,7 +909,8 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample (0 skips it)")
-    ap.add_argument("--no-graph", action="store_true", help="replay the step eagerly instead of as a graph")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="replay the step (and each label's launches) eagerly instead of as graphs")
     ap.add_argument("--unfused", action="store_true", help="decode-full: one launch per ggml node, no fusions")
     ints = lambda v: [int(t) for t in v.split(",")]
     ap.add_argument("--blocks", type=ints, default=None,

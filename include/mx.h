@@ -1,5 +1,6 @@
 /*
- * libmx -- an MI355X (gfx950) device for ggml's quantized MUL_MAT, MUL_MAT_ID and GET_ROWS.
+ * libmx -- an MI355X (gfx950) device for ggml's quantized MUL_MAT, MUL_MAT_ID and GET_ROWS, with the ops either side
+ * of them in a decoder step (ARGMAX, RMS_NORM, ADD, MUL, SwiGLU, RoPE, SET_ROWS, FLASH_ATTN_EXT) and a GGUF loader.
  *
  * The C ABI below is the drop-in boundary. speech.cpp reaches these ops through ggml's backend plugin interface
  * (ggml-backend-impl.h: ggml_backend_reg_i / ggml_backend_device_i / ggml_backend_i / ggml_backend_buffer_type_i /
@@ -11,7 +12,7 @@
  *    arguments, which a ggml adapter reports as GGML_STATUS_FAILED (src/common/graph.cpp:13-31 maps them to the
  *    Device and OutOfMemory faults). No entry point aborts on bad input; the message is in mx_last_error().
  *  - Tensors follow ggml order: ne[0] is the fastest axis, nb[] are byte strides.
- *  - Quantized tensors (Q8_0, Q4_K, Q6_K) held by this library are stored in its own device layout: each tensor's
+ *  - Quantized tensors (Q8_0, Q4_K, Q5_K, Q6_K) held by this library are stored in its own device layout: each tensor's
  *    allocation is split into planes (quants, scales, super-block scales) so every plane is 256-byte aligned and every
  *    row of quants is contiguous. mx_tensor_set / mx_tensor_get take and return ggml's own block bytes (GGUF layout),
  *    at any byte offset and size, so ggml and GGUF never see the device layout. Float and integer tensors are plain.

@@ -42,15 +42,37 @@ __global__ __launch_bounds__(256) void k_rms_norm(RowsArgs a, float eps, const f
     const int64_t i1 = row % a.ne1, i2 = (row / a.ne1) % a.ne2, i3 = row / (a.ne1 * a.ne2);
     const float *x = (const float *)((const uint8_t *)a.src + i1 * a.s_nb1 + i2 * a.s_nb2 + i3 * a.s_nb3);
     float *y = (float *)((uint8_t *)a.dst + i1 * a.d_nb1 + i2 * a.d_nb2 + i3 * a.d_nb3);
+    // eight loads per lane in flight at a time; each lane still adds its elements in index order
+    const int64_t n = a.ne0, full = n - n % 512;
     double sum = 0.0;
-    for (int64_t i = lane; i < a.ne0; i += 64) {
+    for (int64_t i0 = 0; i0 < full; i0 += 512) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = x[i0 + 64 * u + lane];
+#pragma unroll
+        for (int u = 0; u < 8; u++) sum += (double)(v[u] * v[u]);
+    }
+    for (int64_t i = full + lane; i < n; i += 64) {
         const float v = x[i];
         sum += (double)(v * v);
     }
     sum = wave_sum_d(sum);
-    const float mean = (float)(sum / (double)a.ne0);
+    const float mean = (float)(sum / (double)n);
     const float scale = 1.0f / sqrtf(mean + eps);
-    for (int64_t i = lane; i < a.ne0; i += 64) {
+    for (int64_t i0 = 0; i0 < full; i0 += 512) {
+        float v[8], g[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            v[u] = x[i0 + 64 * u + lane];
+            g[u] = w ? w[i0 + 64 * u + lane] : 1.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float t = v[u] * scale;
+            y[i0 + 64 * u + lane] = w ? t * g[u] : t;
+        }
+    }
+    for (int64_t i = full + lane; i < n; i += 64) {
         const float t = x[i] * scale;
         y[i] = w ? t * w[i] : t;
     }
@@ -143,30 +165,33 @@ __global__ __launch_bounds__(256) void k_qkv_post(QkvPostArgs a) {
     const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6), r = blockIdx.y;
     const int lane = threadIdx.x & 63;
     if (item >= a.nq + 2 * a.nkv) return;  // whole wave
-    const int64_t p = a.pos[r];
-    if (p < 0 || p >= a.cache_rows) {
-        if (lane == 0 && item == 0) atomicOr(a.err, 4);
-        if (item >= a.nq) return;  // nothing is stored at a bad row; q is still written
+    const bool isq = item < a.nq, isv = item >= a.nq + a.nkv;
+    const int64_t h = isq ? item : (isv ? item - a.nq - a.nkv : item - a.nq);
+    const float *x = isq ? (const float *)((const uint8_t *)a.q + h * a.q_nb1 + r * a.q_nb2)
+                         : isv ? (const float *)((const uint8_t *)a.v + h * a.v_nb1 + r * a.v_nb2)
+                               : (const float *)((const uint8_t *)a.k + h * a.k_nb1 + r * a.k_nb2);
+    const float x0 = x[lane], x1 = x[lane + 64];  // the head's loads go out with the position's
+    float w0 = 0.0f, w1 = 0.0f;
+    if (!isv) {
+        const float *w = isq ? a.qw : a.kw;
+        w0 = w[lane];
+        w1 = w[lane + 64];
     }
-    if (item >= a.nq + a.nkv) {  // v head
-        const int64_t h = item - a.nq - a.nkv;
-        const float *v = (const float *)((const uint8_t *)a.v + h * a.v_nb1 + r * a.v_nb2);
+    const int64_t p = a.pos[r];
+    const bool bad = p < 0 || p >= a.cache_rows;  // nothing is stored at a bad row; q is still written
+    if (bad && lane == 0 && item == 0) atomicOr(a.err, 4);
+    if (isv) {
+        if (bad) return;
         uint16_t *dst = (uint16_t *)((uint8_t *)a.vc + p * a.vc_nb1) + h * 128;
-        dst[lane] = f2h(v[lane]);
-        dst[lane + 64] = f2h(v[lane + 64]);
+        dst[lane] = f2h(x0);
+        dst[lane + 64] = f2h(x1);
         return;
     }
-    const bool isq = item < a.nq;
-    const int64_t h = isq ? item : item - a.nq;
-    const float *x = isq ? (const float *)((const uint8_t *)a.q + h * a.q_nb1 + r * a.q_nb2)
-                         : (const float *)((const uint8_t *)a.k + h * a.k_nb1 + r * a.k_nb2);
-    const float *w = isq ? a.qw : a.kw;
-    const float x0 = x[lane], x1 = x[lane + 64];
     double ss = (double)(x0 * x0) + (double)(x1 * x1);
     ss = wave_sum_d(ss);
     const float mean = (float)(ss / 128.0);
     const float scale = 1.0f / sqrtf(mean + a.eps);
-    const float y0 = (x0 * scale) * w[lane], y1 = (x1 * scale) * w[lane + 64];
+    const float y0 = (x0 * scale) * w0, y1 = (x1 * scale) * w1;
     float theta = (float)p;
     for (int j = 0; j < lane; j++) theta *= a.theta_scale;
     const float t = a.freq_scale * theta;
@@ -176,7 +201,7 @@ __global__ __launch_bounds__(256) void k_qkv_post(QkvPostArgs a) {
         float *o = (float *)((uint8_t *)a.q_out + h * a.qo_nb1 + r * a.qo_nb2);
         o[lane] = o0;
         o[lane + 64] = o1;
-    } else {
+    } else if (!bad) {
         uint16_t *dst = (uint16_t *)((uint8_t *)a.kc + p * a.kc_nb1) + h * 128;
         dst[lane] = f2h(o0);
         dst[lane + 64] = f2h(o1);
@@ -191,11 +216,12 @@ hipError_t launch_qkv_post(const QkvPostArgs &a, int64_t rows, hipStream_t s) {
 }
 
 // -------------------------------------------------------------------------------------------------- FLASH_ATTN_EXT
-// Pass 1: one wave per (kv split, head, query row) runs the online softmax over its split of the positions, 64 at a
-// time (lane j scores position j of the chunk; then each lane accumulates D/64 adjacent channels of V over the chunk,
-// all of the chunk's V loads in flight before the first product), and
-// writes (max, sum, D accumulated channels) to the partials -- or, when there is one split, the normalized row to dst.
-// Pass 2 merges the splits of each (head, row).
+// Pass 1 splits the positions into whole 64-position blocks and writes (max, sum, D accumulated channels) per (split,
+// head, row) to the partials -- or, when there is one split, the normalized row to dst. Head size 128 with 1, 2 or 4
+// q heads per kv head takes k_fa_gqa (one workgroup per kv head's group); other shapes take k_fa_split, one wave per
+// (kv split, head, query row): lane j scores position j of each 64-position chunk, then each lane accumulates D/64
+// adjacent channels of V over the chunk, all of the chunk's V loads in flight before the first product.
+// Pass 2 (k_fa_merge) merges the splits of each (head, row).
 // The loads of one 64-position chunk, issued together ahead of their use: lane j's key row (position base + j),
 // every lane's DL channels of the 64 value rows, and lane j's mask value. Positions past the split repeat its last
 // one; their score is -inf, so neither their key nor their value counts.
@@ -313,8 +339,8 @@ __global__ __launch_bounds__(64) void k_fa_split(FaArgs a) {
 }
 
 // Pass 2: one wave per (head, row). Lane s holds split s's max and sum (nsplit <= 64), so the splits' weights
-// exp(m_s - M) and the total come from one round of loads and two wave reductions; the channels are gathered eight
-// splits at a time, their loads in flight together.
+// exp(m_s - M) and the total come from one round of loads and two wave reductions; the channels are gathered 64 / DL
+// splits at a time, their loads in flight together (the first round's with the maxima's).
 template <int D>
 __device__ __forceinline__ void fa_merge_head(const FaArgs &a, int64_t h, int64_t i, int lane) {
     constexpr int DL = D / 64, NB = 64 / DL;  // NB splits' channels per round of loads (64 registers)
@@ -384,9 +410,11 @@ __device__ __forceinline__ void fa_stage_load(FaStage &st, const FaArgs &a, cons
 
 // Pass 1 for head size 128 and GQA groups of G = 1, 2 or 4 q heads per kv head: one 256-thread workgroup per (split,
 // kv head, query row) serves the group's G heads, so a group reads K and V once. Per 64-position chunk the keys and
-// values are copied to LDS with coalesced 16-byte loads (sixteen threads per 256-byte row); T = 256 / (64 G) threads share each
-// score (CPT channels each, then a shuffle sum); one wave per head runs the online softmax over the chunk; and for
-// P.V each thread owns a channel pair of one head over PLEN positions, the position parts added at the end.
+// values are copied to LDS with coalesced 16-byte loads (sixteen threads per 256-byte row), the next chunk's loads
+// issued before this chunk's arithmetic; T = 256 / (64 G) threads share each score (CPT channels each, then a shuffle
+// sum); one wave per head runs the online softmax over the chunk; and for P.V each thread owns a channel pair of one
+// head over PLEN positions, the position parts added at the end. The split count aims at MX_FA_GROUP_WGS workgroups:
+// at decode that is one chunk per workgroup, the fastest form measured (fewer, longer splits serialize their chunks).
 template <int G>
 __global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a) {
     constexpr int D = 128, T = 256 / (G * 64), CPT = D / T, PP = 256 / G / 64, PLEN = 64 / PP;
