@@ -16,6 +16,7 @@
 #include "mx_common.h"
 #include "mx_device.h"
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 
@@ -26,6 +27,10 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void dq_lds;
+
+#ifndef MX_DQ_WGN128
+#define MX_DQ_WGN128 4  // waves across N in a 128 x 128 tile (4: 64 x 32 per wave; 2: 64 x 64)
+#endif
 
 constexpr int DQ_KS = 64;  // K per stage
 constexpr int DQ_NS = 4;   // ring stages (copies run DQ_NS - 1 stages ahead)
@@ -59,6 +64,10 @@ struct DqArgs {
     DqProblem prob[4];
     int M, K;
     const _Float16 *xh;  // [M][K] fp16(d * q) of the quantized activations
+    int nprob, nsplit;   // grid.z = nprob * nsplit: problem z % nprob, K split z / nprob
+    int ntot;            // sum of the problems' N: columns of the split partials
+    int col0[4];         // first partial column of each problem
+    float *ws;           // nsplit > 1: [nsplit][M][ntot] partial sums, added in split order by k_dq_reduce
 };
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(dq_lds *)p; }
@@ -119,10 +128,35 @@ __device__ __forceinline__ void dq_q8_0_16(v4i c, uint16_t dbits, v4i &o0, v4i &
              __builtin_bit_cast(int, h[7])};
 }
 
-// NF fragment reads (4, 6, 8 or 12) and the wait for them.
+// NF fragment reads (4, 6, 8, 12 or 16) and the wait for them.
 template <int NF>
-__device__ __forceinline__ void dq_read(v8h (&f)[12], const uint32_t (&a)[12]) {
-    if constexpr (NF == 8) {
+__device__ __forceinline__ void dq_read(v8h (&f)[16], const uint32_t (&a)[16]) {
+    if constexpr (NF == 16) {
+        asm volatile(
+            "ds_read_b128 %0, %16\n"
+            "ds_read_b128 %1, %17\n"
+            "ds_read_b128 %2, %18\n"
+            "ds_read_b128 %3, %19\n"
+            "ds_read_b128 %4, %20\n"
+            "ds_read_b128 %5, %21\n"
+            "ds_read_b128 %6, %22\n"
+            "ds_read_b128 %7, %23\n"
+            "ds_read_b128 %8, %24\n"
+            "ds_read_b128 %9, %25\n"
+            "ds_read_b128 %10, %26\n"
+            "ds_read_b128 %11, %27\n"
+            "ds_read_b128 %12, %28\n"
+            "ds_read_b128 %13, %29\n"
+            "ds_read_b128 %14, %30\n"
+            "ds_read_b128 %15, %31\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]), "=&v"(f[6]), "=&v"(f[7]),
+              "=&v"(f[8]), "=&v"(f[9]), "=&v"(f[10]), "=&v"(f[11]), "=&v"(f[12]), "=&v"(f[13]), "=&v"(f[14]),
+              "=&v"(f[15])
+            : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]), "v"(a[8]),
+              "v"(a[9]), "v"(a[10]), "v"(a[11]), "v"(a[12]), "v"(a[13]), "v"(a[14]), "v"(a[15])
+            : "memory");
+    } else if constexpr (NF == 8) {
         asm volatile(
             "ds_read_b128 %0, %8\n"
             "ds_read_b128 %1, %9\n"
@@ -188,14 +222,17 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
     using L = DqLds<BM, BN, NW>;
     constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
     constexpr int NF = (TM + TN) * 4;  // fragments of the stage's four K steps, read together
-    static_assert(NF == 8 || NF == 12, "wave tiles of 32 x 32 or 64 x 32");
+    static_assert(NF == 8 || NF == 12 || NF == 16, "wave tiles of 32 x 32, 64 x 32 or 64 x 64");
     extern __shared__ __align__(16) uint8_t smem[];
-    const int z = blockIdx.z;
-    const DqProblem p = z == 0 ? a.prob[0] : (z == 1 ? a.prob[1] : (z == 2 ? a.prob[2] : a.prob[3]));
+    const int z = blockIdx.z, pi = z % a.nprob, split = z / a.nprob;
+    const DqProblem p = pi == 0 ? a.prob[0] : (pi == 1 ? a.prob[1] : (pi == 2 ? a.prob[2] : a.prob[3]));
     const int n0 = blockIdx.x * BN;
     if (n0 >= p.N) return;  // uniform: a problem narrower than the grid
     const int m0 = blockIdx.y * BM;
-    const int M = a.M, N = p.N, K = a.K, nst = K / DQ_KS, nblk = K / 32;
+    const int M = a.M, N = p.N, K = a.K, nblk = K / 32;
+    // this workgroup's stages: [sb, sb + nst) of K / 64 (the host makes every split non-empty)
+    const int per = (K / DQ_KS + a.nsplit - 1) / a.nsplit, sb = split * per;
+    const int nst = min(K / DQ_KS - sb, per);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t lds = lds_addr(smem);
@@ -211,7 +248,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
 #pragma unroll
     for (int jj = 0; jj < L::PA; jj++) {
         const int j = wave * L::PA + jj, row = 8 * min(j, L::NA - 1) + (lane >> 3);
-        asrc[jj] = a.xh + (int64_t)min(m0 + row, M - 1) * K + 8 * ((lane & 7) ^ dq_swz(row));
+        asrc[jj] = a.xh + (int64_t)min(m0 + row, M - 1) * K + sb * DQ_KS + 8 * ((lane & 7) ^ dq_swz(row));
         adst[jj] = j < L::NA ? L::A + j * 1024 : L::JUNK + wave * 1024;
     }
     const uint8_t *csrc[L::PC];
@@ -219,7 +256,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
 #pragma unroll
     for (int jj = 0; jj < L::PC; jj++) {
         const int j = wave * L::PC + jj, row = 16 * min(j, L::NC - 1) + (lane >> 2);
-        csrc[jj] = p.w.p0 + (int64_t)min(n0 + row, N - 1) * K + 16 * (lane & 3);
+        csrc[jj] = p.w.p0 + (int64_t)min(n0 + row, N - 1) * K + sb * DQ_KS + 16 * (lane & 3);
         cdst[jj] = j < L::NC ? L::RAW + j * 1024 : L::JUNK + wave * 1024;
     }
     const uint8_t *ssrc[L::PS];
@@ -227,7 +264,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
 #pragma unroll
     for (int jj = 0; jj < L::PS; jj++) {
         const int j = wave * L::PS + jj, row = 64 * min(j, L::NS4 - 1) + lane;
-        ssrc[jj] = p.w.p1 + (int64_t)min(n0 + row, N - 1) * nblk * 2;
+        ssrc[jj] = p.w.p1 + (int64_t)min(n0 + row, N - 1) * nblk * 2 + sb * 4;
         sdst[jj] = j < L::NS4 ? L::SC + j * 256 : L::JUNK + wave * 1024;
     }
 
@@ -321,7 +358,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
         // weights follow while the matrix cores work through them
         const uint32_t at = lds + L::A + (s % DQ_NS) * BM * 128;
         const uint32_t bt = lds + L::BH + (s & 1) * BN * 128;
-        uint32_t ad[12];
+        uint32_t ad[16];
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
 #pragma unroll
@@ -330,8 +367,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
             for (int j = 0; j < TN; j++) ad[kk * (TM + TN) + TM + j] = bt + boff[j][kk];
         }
 #pragma unroll
-        for (int x = NF; x < 12; x++) ad[x] = 0;
-        v8h f[12];
+        for (int x = NF; x < 16; x++) ad[x] = 0;
+        v8h f[16];
         dq_read<NF>(f, ad);
 #pragma unroll
         for (int kk = 0; kk < 4; kk++)
@@ -347,6 +384,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
     dq_wait_vm<0>();  // the copies of the stages past the end
 
     // 32 x 32 accumulator layout: lane l, register r holds (row 8 (r / 4) + 4 (l / 32) + r % 4, col l % 32)
+    float *y = p.y;
+    int64_t ldy = p.ldy;
+    if (a.nsplit > 1) {  // this split's partial sums
+        y = a.ws + (int64_t)split * M * a.ntot + a.col0[pi];
+        ldy = a.ntot;
+    }
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -356,9 +399,30 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);
-                if (m < M) p.y[(int64_t)m * p.ldy + n] = acc[i][j][r];
+                if (m < M) y[(int64_t)m * ldy + n] = acc[i][j][r];
             }
         }
+}
+
+// y[m][col] = sum of the nsplit partials of (m, col), split 0 first; one thread per (column, row).
+__global__ __launch_bounds__(256) void k_dq_reduce(DqArgs a) {
+    const int c = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+    if (c >= a.ntot) return;
+    const int64_t plane = (int64_t)a.M * a.ntot;
+    const float *ws = a.ws + (int64_t)m * a.ntot + c;
+    float v[8];
+    float sum = 0.0f;
+    for (int s0 = 0; s0 < a.nsplit; s0 += 8) {  // eight partials' loads in flight at a time
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = s0 + u < a.nsplit ? ws[(s0 + u) * plane] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (s0 + u < a.nsplit) sum += v[u];
+    }
+    int pi = 0;
+    while (pi + 1 < a.nprob && c >= a.col0[pi + 1]) pi++;
+    const DqProblem &p = pi == 0 ? a.prob[0] : (pi == 1 ? a.prob[1] : (pi == 2 ? a.prob[2] : a.prob[3]));
+    p.y[(int64_t)m * p.ldy + (c - a.col0[pi])] = sum;
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -374,6 +438,61 @@ bool gemm_dq_supported(int type, int64_t M, int64_t K) {
 
 size_t gemm_dq_act_bytes(int64_t M, int64_t K) { return (size_t)M * (size_t)K * 2; }
 
+namespace {
+
+struct DqPlan {
+    int bm, bn, nsplit;
+    int64_t ntot;
+};
+
+// Tile: 128 x 128 when that gives at least 128 workgroups (half the CUs: measured at M = 512, a 128-workgroup grid of
+// 128 x 128 tiles beats a 256-workgroup grid of 128 x 64 ones by 1.3x), else 64 x 64 (MX_GEMM_DQ_TILE=BMxBN
+// overrides). When 64 x 64 tiles still leave CUs idle (few rows: a short prefill block), K is split so that about 512
+// workgroups stream the weights, each over at least four stages (MX_GEMM_DQ_SPLIT=n overrides); the split's reduce
+// pass costs more than it saves on the large tiles.
+DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K) {
+    DqPlan pl{64, 64, 1, 0};
+    int64_t wg128 = 0;
+    for (int i = 0; i < nprob; i++) {
+        wg128 += (N[i] + 127) / 128;
+        pl.ntot += N[i];
+    }
+    wg128 *= (M + 127) / 128;
+    if (wg128 >= 128) pl.bm = pl.bn = 128;
+    static const char *tile = getenv("MX_GEMM_DQ_TILE");
+    if (tile) {
+        int tm = 0, tn = 0;
+        if (sscanf(tile, "%dx%d", &tm, &tn) == 2 && (tm == 64 || tm == 128) && (tn == 64 || tn == 128) &&
+            !(tm == 64 && tn == 128)) {
+            pl.bm = tm;
+            pl.bn = tn;
+        }
+    }
+    int64_t tiles = 0;
+    for (int i = 0; i < nprob; i++) tiles += (N[i] + pl.bn - 1) / pl.bn;
+    tiles *= (M + pl.bm - 1) / pl.bm;
+    const int64_t nst = K / DQ_KS;
+    int64_t want = tiles < 256 && pl.bn == 64 ? (512 + tiles - 1) / tiles : 1;
+    static const int forced = [] {
+        const char *e = getenv("MX_GEMM_DQ_SPLIT");
+        return e ? atoi(e) : 0;
+    }();
+    if (forced > 0) want = forced;
+    want = std::min<int64_t>(want, std::max<int64_t>(1, forced > 0 ? nst : nst / 4));
+    const int64_t per = (nst + want - 1) / want;  // stages per split; no split is left empty
+    pl.nsplit = (int)((nst + per - 1) / per);
+    return pl;
+}
+
+}  // namespace
+
+size_t gemm_dq_scratch_bytes(int nprob, const int64_t *N, int64_t M, int64_t K) {
+    const DqPlan pl = dq_plan(nprob, N, M, K);
+    size_t b = (gemm_dq_act_bytes(M, K) + 255) / 256 * 256;
+    if (pl.nsplit > 1) b += (size_t)pl.nsplit * (size_t)M * (size_t)pl.ntot * 4;
+    return b;
+}
+
 hipError_t launch_gemm_dq_act(int type, int rounding, const float *x, int64_t x_stride, int64_t M, int64_t K,
                               void *xh, hipStream_t s) {
     if (type != MX_TYPE_Q8_0) return hipErrorInvalidValue;
@@ -383,7 +502,7 @@ hipError_t launch_gemm_dq_act(int type, int rounding, const float *x, int64_t x_
 }
 
 template <int BM, int BN, int WGM, int WGN>
-static hipError_t launch_dq(const DqArgs &a, int nprob, int maxN, hipStream_t s) {
+static hipError_t launch_dq(const DqArgs &a, int maxN, hipStream_t s) {
     using L = DqLds<BM, BN, WGM * WGN>;
     static bool attr = false;
     if (!attr) {
@@ -392,45 +511,39 @@ static hipError_t launch_dq(const DqArgs &a, int nprob, int maxN, hipStream_t s)
         if (e != hipSuccess) return e;
         attr = true;
     }
-    const dim3 grid((unsigned)((maxN + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM), (unsigned)nprob);
+    const dim3 grid((unsigned)((maxN + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM), (unsigned)(a.nprob * a.nsplit));
     hipLaunchKernelGGL((k_gemm_dq_q8_0<BM, BN, WGM, WGN>), grid, dim3(64 * WGM * WGN), L::SIZE, s, a);
     return hipGetLastError();
 }
 
-// Tile: the largest of 128 x 128, 128 x 64 and 64 x 64 that still gives a workgroup per CU. MX_GEMM_DQ_TILE=BMxBN
-// overrides.
 hipError_t launch_gemm_dq(int type, int nprob, const WPlanes *w, const int64_t *N, float *const *y,
-                          const int64_t *ldy, int64_t M, int64_t K, const void *xh, hipStream_t s) {
+                          const int64_t *ldy, int64_t M, int64_t K, void *scratch, hipStream_t s) {
     if (nprob < 1 || nprob > 4 || !gemm_dq_supported(type, M, K)) return hipErrorInvalidValue;
+    const DqPlan pl = dq_plan(nprob, N, M, K);
     DqArgs a{};
-    int64_t maxN = 0, wg128 = 0;
+    int64_t maxN = 0;
     for (int i = 0; i < nprob; i++) {
         if (N[i] * K >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
         a.prob[i] = DqProblem{w[i], (int)N[i], y[i], ldy[i]};
+        a.col0[i] = i == 0 ? 0 : a.col0[i - 1] + (int)N[i - 1];
         maxN = N[i] > maxN ? N[i] : maxN;
-        wg128 += (N[i] + 127) / 128;
     }
+    if (maxN == 0 || M == 0) return hipSuccess;
+    if (pl.nsplit > 1 && M * pl.ntot * pl.nsplit >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
     a.M = (int)M;
     a.K = (int)K;
-    a.xh = (const _Float16 *)xh;
-    wg128 *= (M + 127) / 128;
-    int64_t wg64 = 0;
-    for (int i = 0; i < nprob; i++) wg64 += (N[i] + 63) / 64;
-    int bm = 64, bn = 64;
-    if (wg128 >= 256) bm = bn = 128;
-    else if (wg64 * ((M + 127) / 128) >= 256) bm = 128;
-    static const char *tile = getenv("MX_GEMM_DQ_TILE");
-    if (tile) {
-        int tm = 0, tn = 0;
-        if (sscanf(tile, "%dx%d", &tm, &tn) == 2 && (tm == 64 || tm == 128) && (tn == 64 || tn == 128) &&
-            !(tm == 64 && tn == 128)) {
-            bm = tm;
-            bn = tn;
-        }
-    }
-    if (bm == 128 && bn == 128) return launch_dq<128, 128, 2, 4>(a, nprob, (int)maxN, s);
-    if (bm == 128) return launch_dq<128, 64, 4, 2>(a, nprob, (int)maxN, s);
-    return launch_dq<64, 64, 2, 2>(a, nprob, (int)maxN, s);
+    a.xh = (const _Float16 *)scratch;
+    a.nprob = nprob;
+    a.nsplit = pl.nsplit;
+    a.ntot = (int)pl.ntot;
+    a.ws = (float *)((uint8_t *)scratch + (gemm_dq_act_bytes(M, K) + 255) / 256 * 256);
+    hipError_t e;
+    if (pl.bm == 128 && pl.bn == 128) e = launch_dq<128, 128, 2, MX_DQ_WGN128>(a, (int)maxN, s);
+    else if (pl.bm == 128) e = launch_dq<128, 64, 4, 2>(a, (int)maxN, s);
+    else e = launch_dq<64, 64, 2, 2>(a, (int)maxN, s);
+    if (e != hipSuccess || pl.nsplit == 1) return e;
+    hipLaunchKernelGGL(k_dq_reduce, dim3((unsigned)((pl.ntot + 255) / 256), (unsigned)M), dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 }  // namespace mx

@@ -651,7 +651,9 @@ static int gemm_dq_group(mx_backend *be, int n, const mx_tensor *const *src0, co
                          const mx_tensor *const *dst) {
     const mx_tensor *w0 = src0[0];
     const int64_t K = w0->ne[0], M = src1->ne[1];
-    int rc = ensure_scratch(be, mx::gemm_dq_act_bytes(M, K));
+    int64_t Ns[4];
+    for (int i = 0; i < n; i++) Ns[i] = src0[i]->ne[1];
+    int rc = ensure_scratch(be, mx::gemm_dq_scratch_bytes(n, Ns, M, K));
     if (rc) return rc;
     const int64_t r2 = src1->ne[2] / w0->ne[2], r3 = src1->ne[3] / w0->ne[3];
     for (int64_t i13 = 0; i13 < src1->ne[3]; i13++)

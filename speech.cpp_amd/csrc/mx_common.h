@@ -193,14 +193,16 @@ hipError_t launch_gemm(int type, const WPlanes &w, int64_t M, int64_t N, int64_t
 inline bool gemm_supported(int type, int64_t K) { return type == MX_TYPE_Q8_0 && K % 128 == 0; }
 
 // Prefill GEMM on the fp16 matrix cores over dequantized tiles (Q8_0 weights): launch_gemm_dq_act writes the
-// activations' quantized values as fp16 into `xh` (gemm_dq_act_bytes), launch_gemm_dq runs up to four weights sharing
-// them in one launch. MX_GEMM_DQ=0 turns it off (the int8 kernel then runs).
+// activations' quantized values as fp16 at the start of `scratch`, launch_gemm_dq runs up to four weights sharing
+// them in one launch (plus a reduce launch when K is split; the partial sums follow the activations in scratch).
+// gemm_dq_scratch_bytes is the scratch both need. MX_GEMM_DQ=0 turns it off (the int8 kernel then runs).
 bool gemm_dq_supported(int type, int64_t M, int64_t K);
 size_t gemm_dq_act_bytes(int64_t M, int64_t K);
+size_t gemm_dq_scratch_bytes(int nprob, const int64_t *N, int64_t M, int64_t K);
 hipError_t launch_gemm_dq_act(int type, int rounding, const float *x, int64_t x_stride, int64_t M, int64_t K,
-                              void *xh, hipStream_t s);
+                              void *scratch, hipStream_t s);
 hipError_t launch_gemm_dq(int type, int nprob, const WPlanes *w, const int64_t *N, float *const *y,
-                          const int64_t *ldy, int64_t M, int64_t K, const void *xh, hipStream_t s);
+                          const int64_t *ldy, int64_t M, int64_t K, void *scratch, hipStream_t s);
 
 // Prefill GEMM on Q4_K / Q6_K weights: launch_gemm_kq_quant writes x (M rows of K floats, row stride x_stride) as
 // Q8_K into `scratch` (gemm_kq_act_bytes), launch_gemm_kq multiplies it into y (row stride ldy).

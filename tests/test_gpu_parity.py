@@ -370,6 +370,27 @@ def test_mul_mat_gemm_q8_0(mx, be, M, N, K):
     check_product(t, w, x, y, K)
 
 
+def test_mul_mat_gemm_group_q8_0_split(mx, be):
+    """A short block (28 rows) through the grouped fp16 GEMM: K is split over several workgroups per tile and the
+    partial sums of the three products are added by one reduce pass; a second run gives the same bits."""
+    t, K, M = O.TYPE_Q8_0, 2048, 28
+    Ns = [200, 64, 72]
+    ws = [weights(t, n, K, 0x5EED0E00 + i) for i, n in enumerate(Ns)]
+    x = acts(0xAC700E00, M, K)
+    W = [be.tensor(t, (K, n), w) for n, w in zip(Ns, ws)]
+    X = be.tensor(mx.F32, (K, M), x)
+    Y = [be.tensor(mx.F32, (n, M)) for n in Ns]
+    be.mul_mat_group(W, X, Y)
+    be.sync()
+    first = [yt.numpy().reshape(M, n).copy() for n, yt in zip(Ns, Y)]
+    for n, w, y in zip(Ns, ws, first):
+        check_product(t, w, x, y, K)
+    be.mul_mat_group(W, X, Y)
+    be.sync()
+    for n, yt, y in zip(Ns, Y, first):
+        assert bits_equal(yt.numpy().reshape(M, n), y)
+
+
 def test_mul_mat_gemm_batched(mx, be):
     t, K, N, M = O.TYPE_Q8_0, 1024, 96, 40
     w = weights(t, N * 2, K, 0x5EED0B00)
