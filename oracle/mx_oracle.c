@@ -563,7 +563,7 @@ size_t orc_quantize_chunk(int type, const float *src, void *dst, int64_t start, 
 
 /* ------------------------------------------------------------------------------------------------------------------
  * Dequantizers: ggml-quants.c dequantize_row_q8_0 / dequantize_row_q4_K / dequantize_row_q5_K /
- * dequantize_row_q6_K; ggml_fp16_to_fp32_row for F16.
+ * dequantize_row_q6_K / dequantize_row_q8_K (fp32 d times each quant); ggml_fp16_to_fp32_row for F16.
  * ---------------------------------------------------------------------------------------------------------------- */
 int orc_dequantize_row(int type, const void *vx, float *y, int64_t k) {
     switch (type) {
@@ -646,6 +646,12 @@ int orc_dequantize_row(int type, const void *vx, float *y, int64_t k) {
                     sc += 8;
                 }
             }
+            return 0;
+        }
+        case ORC_TYPE_Q8_K: {
+            const blk_q8_K *x = (const blk_q8_K *)vx;
+            for (int64_t i = 0; i < k / QK_K; i++)
+                for (int j = 0; j < QK_K; ++j) y[i * QK_K + j] = x[i].d * x[i].qs[j];
             return 0;
         }
         case ORC_TYPE_F16:

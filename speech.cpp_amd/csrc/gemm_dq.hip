@@ -1,22 +1,28 @@
-// Prefill products (M > 8) on the fp16 matrix cores over dequantized tiles: Y = deq(W) . deq(quant(X)).
+// Prefill products (M > 8) on the fp16 matrix cores over dequantized tiles: Y = deq(W) . deq(quant(X)), for Q8_0 and
+// Q6_K weights.
 //
 // The activations are quantized exactly as ggml-cpu quantizes src1 for the weight's vec_dot (Q8_0 blocks with the
-// fp16-rounded d) and written back as fp16(d * q); the weight tiles are dequantized in LDS to fp16(d * q). Both
-// roundings are single roundings of an exact product (relative error <= 2^-11 each), and the products accumulate over
-// all of K in fp32 inside the MFMA, so there is no per-block epilogue: the VALU work is the weight conversion, once
-// per workgroup and element. Against ggml-cpu's per-block integer sums the row-relative error is a few 1e-4.
+// fp16-rounded d for Q8_0 weights; Q8_K blocks with their fp32 d for Q6_K) and written back as fp16(d * q); the weight
+// tiles are dequantized in LDS to fp16(d * q) (Q6_K: fp16(d * sc * q), the exact fp32 product of ggml's
+// dequantize_row_q6_K rounded once). The weight rounding is a single rounding of an exact product, the activation one
+// too for Q8_0 (Q8_K's fp32 d * q is rounded to fp32 first, as ggml forms it); relative error <= 2^-11 each. The
+// products accumulate over all of K in fp32 inside the MFMA, so there is no per-block epilogue: the VALU work is the
+// weight conversion, once per workgroup and element. Against ggml-cpu's per-block integer sums the row-relative error
+// is a few 1e-4.
 //
 // Tiles: BM x BN per workgroup of WGM x WGN waves, each (BM / WGM) x (BN / WGN) as 32 x 32 v_mfma_f32_32x32x16_f16
 // tiles.
 // K advances in stages of 64. Every wave copies its share of each stage straight into LDS with global_load_lds
-// (activations: fp16 rows; weights: the raw code bytes and block scales) three stages ahead, through rings of four
-// stages; one stage ahead of the matrix cores the workgroup converts the stage's raw weights into an fp16 tile (double
-// buffered). One barrier per stage. LDS accesses in the loop are inline assembly with explicit waits: the compiler
+// (activations: fp16 rows; weights: the raw code bytes and scales -- Q8_0: 64 codes and two block scales per row;
+// Q6_K: the 64 ql and 32 qh bytes of the stage's half super-block, its four sub-block scales and d) three stages
+// ahead, through rings of four stages; one stage ahead of the matrix cores the workgroup converts the stage's raw
+// weights into an fp16 tile (double buffered). One barrier per stage. LDS accesses in the loop are inline assembly with explicit waits: the compiler
 // cannot see which stage a copy went to, and would otherwise wait for every copy in flight.
 #include "mx_common.h"
 #include "mx_device.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdio>
 #include <cstdlib>
 
@@ -38,18 +44,25 @@ constexpr int DQ_NS = 4;   // ring stages (copies run DQ_NS - 1 stages ahead)
 // LDS map of a BM x BN workgroup of NW waves. Row-major fp16 tiles of 64 halves (128 bytes) per row; the 16-byte
 // chunk c of row r sits at chunk c ^ ((r >> 1) & 7), so the 16 rows one pass of an MFMA fragment read touches hit all
 // 64 banks once.
-template <int BM, int BN, int NW>
+template <int WT, int BM, int BN, int NW>
 struct DqLds {
+    static constexpr bool K6 = WT == MX_TYPE_Q6_K;
     static constexpr int A = 0;                            // [stage][BM][128 B] activations
     static constexpr int BH = A + DQ_NS * BM * 128;        // [2][BN][128 B] dequantized weights
-    static constexpr int RAW = BH + 2 * BN * 128;          // [stage][BN][64 B] weight codes
-    static constexpr int SC = RAW + DQ_NS * BN * 64;       // [stage][BN][4 B] the two block scales of each row
-    static constexpr int JUNK = SC + DQ_NS * BN * 4;       // [wave][1 KB] where copies beyond a tile's need land
-    static constexpr int SIZE = JUNK + NW * 1024;
-    // copy instructions per stage (64 lanes each): activation rows (16 B), code rows (16 B), scales (4 B), and per wave
-    static constexpr int NA = BM / 8, NC = BN / 16, NS4 = BN / 64;
-    static constexpr int PA = (NA + NW - 1) / NW, PC = (NC + NW - 1) / NW, PS = (NS4 + NW - 1) / NW;
-    static constexpr int OPS = PA + PC + PS;  // vector memory ops per wave and stage
+    static constexpr int RAW = BH + 2 * BN * 128;          // [stage][BN][64 B] codes (Q8_0) / ql bytes (Q6_K)
+    static constexpr int QH = RAW + DQ_NS * BN * 64;       // [stage][BN][32 B] qh bytes (Q6_K)
+    static constexpr int SC = QH + (K6 ? DQ_NS * BN * 32 : 0);  // [stage][BN][4 B] two fp16 scales / four int8 scales
+    static constexpr int DD = SC + DQ_NS * BN * 4;         // [stage][BN][4 B] the fp16 d pair holding the row's (Q6_K)
+    static constexpr int JUNK = DD + (K6 ? DQ_NS * BN * 4 : 0);  // [wave][1 KB] where copies beyond a tile's need land
+    static constexpr int RS = JUNK + NW * 1024;            // [BM] the tile rows' 2^-e
+    static constexpr int SIZE = RS + BM * 4;
+    // copy instructions per stage (64 lanes each): activation rows (16 B), code rows (16 B), qh rows (16 B), scales
+    // (4 B), d (4 B), and per wave
+    static constexpr int NA = BM / 8, NC = BN / 16, NH = K6 ? BN / 32 : 0, NS4 = BN / 64, ND = K6 ? BN / 64 : 0;
+    static constexpr int PA = (NA + NW - 1) / NW, PC = (NC + NW - 1) / NW, PH = (NH + NW - 1) / NW;
+    static constexpr int PS = (NS4 + NW - 1) / NW, PD = (ND + NW - 1) / NW;
+    static constexpr int OPS = PA + PC + PH + PS + PD;  // vector memory ops per wave and stage
+    static_assert(SIZE <= 160 * 1024, "LDS");
 };
 
 __device__ __forceinline__ int dq_swz(int row) { return (row >> 1) & 7; }
@@ -63,7 +76,8 @@ struct DqProblem {
 struct DqArgs {
     DqProblem prob[4];
     int M, K;
-    const _Float16 *xh;  // [M][K] fp16(d * q) of the quantized activations
+    const _Float16 *xh;  // [M][K] fp16(2^e_m d q) of the quantized activations
+    const float *rs;     // [M] 2^-e_m, applied to each row's sums
     int nprob, nsplit;   // grid.z = nprob * nsplit: problem z % nprob, K split z / nprob
     int ntot;            // sum of the problems' N: columns of the split partials
     int col0[4];         // first partial column of each problem
@@ -77,25 +91,153 @@ __device__ __forceinline__ void dq_wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
 }
 
-// Activation rows -> Q8_0 blocks (ggml's quantize_row_q8_0, d rounded to fp16 as the dot reads it) -> fp16(d * q).
-__global__ __launch_bounds__(256) void k_dq_act_q8_0(const float *x, int64_t x_stride, int K, int rounding,
-                                                     _Float16 *xh) {
-    const int64_t m = blockIdx.y;
-    const int e = blockIdx.x * 1024 + 4 * threadIdx.x;
-    const bool valid = e < K;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (valid) v = *(const float4 *)(x + m * x_stride + e);
-    float d;
-    int sum;
-    const int q = quant32_lane(v, rounding, &d, &sum);
-    if (valid) {
-        const float dh = h2f(f2h(d));
-        typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-        // d * q is exact in fp32 (11 + 7 bits): one rounding to fp16
-        const v4h h = {(_Float16)(dh * (float)(int8_t)(q & 0xFF)), (_Float16)(dh * (float)(int8_t)((q >> 8) & 0xFF)),
-                       (_Float16)(dh * (float)(int8_t)((q >> 16) & 0xFF)),
-                       (_Float16)(dh * (float)(int8_t)((q >> 24) & 0xFF))};
-        *(v4h *)(xh + m * K + e) = h;
+// The fp16 activation values of a row carry a power-of-two scale 2^e, e chosen so that the row's largest |d q| lands
+// in [2^14, 2^15): clear of fp16's overflow (65504) and of its subnormals, where ggml's fp32 sums lose nothing. The
+// GEMM multiplies its sums by rs[m] = 2^-e. Both scalings are exact, so a row that fp16 already holds in its normal
+// range gives the same bits as unscaled values would.
+__device__ __forceinline__ int dq_row_exp(float amax) {
+    if (amax == 0.0f) return 0;
+    int E = (int)((__float_as_uint(amax) >> 23) & 0xFF);  // amax in [2^(E-127), 2^(E-126))
+    if (E == 0) E = 1;
+    const int e = 141 - E;
+    return e < -126 ? -126 : (e > 127 ? 127 : e);
+}
+__device__ __forceinline__ float dq_pow2(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
+
+constexpr int DQ_ACT_NT = 1024;  // threads of an activation-pass workgroup (one row)
+
+__device__ __forceinline__ float dq_block_max(float v, float *red) {  // over a DQ_ACT_NT-thread workgroup
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < DQ_ACT_NT / 64; w++) r = fmaxf(r, red[w]);
+    return r;
+}
+
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+constexpr int DQ_ACT_REG = 4;  // 4-element pieces per thread an activation row keeps in registers (K <= 16384)
+constexpr int DQ_ACT_CH = 4 * DQ_ACT_NT;  // elements per pass of the workgroup
+
+__device__ __forceinline__ float4 dq_ld4(const float *xr, int e, int K) {
+    return e < K ? *(const float4 *)(xr + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+// d q of four packed codes, each exact in fp32 for Q8_0's fp16 d (11 + 7 bits); for Q8_K's fp32 d the product ggml's
+// dequantize_row_q8_K forms
+__device__ __forceinline__ float4 dq_vals(int q, float d) {
+    return make_float4(d * (float)(int8_t)(q & 0xFF), d * (float)(int8_t)((q >> 8) & 0xFF),
+                       d * (float)(int8_t)((q >> 16) & 0xFF), d * (float)(int8_t)((q >> 24) & 0xFF));
+}
+__device__ __forceinline__ float dq_amax4(float4 p) { return fmaxf(fmaxf(fabsf(p.x), fabsf(p.y)), fmaxf(fabsf(p.z), fabsf(p.w))); }
+__device__ __forceinline__ v4h dq_h4(float4 p, float sc) {
+    return v4h{(_Float16)(p.x * sc), (_Float16)(p.y * sc), (_Float16)(p.z * sc), (_Float16)(p.w * sc)};
+}
+
+// Activation row m (one workgroup) -> Q8_0 blocks (ggml's quantize_row_q8_0, d rounded to fp16 as the dot reads it)
+// -> fp16(2^e d q): d q is exact in fp32 and so is its scaling; one rounding to fp16. The row is quantized once, its
+// codes kept in registers while the workgroup finds the row's largest |d q| (rows longer than DQ_ACT_REG * DQ_ACT_CH
+// are quantized twice).
+__global__ __launch_bounds__(DQ_ACT_NT) void k_dq_act_q8_0(const float *x, int64_t x_stride, int K, int rounding,
+                                                            _Float16 *xh, float *rs) {
+    __shared__ float red[DQ_ACT_NT / 64];
+    const int64_t m = blockIdx.x;
+    const int t4 = 4 * threadIdx.x;
+    const float *xr = x + m * x_stride;
+    _Float16 *out = xh + m * K;
+    float amax = 0.0f;
+    if (K <= DQ_ACT_REG * DQ_ACT_CH) {
+        float4 v[DQ_ACT_REG];
+        int q[DQ_ACT_REG];
+        float dh[DQ_ACT_REG];
+#pragma unroll
+        for (int c = 0; c < DQ_ACT_REG; c++) v[c] = dq_ld4(xr, DQ_ACT_CH * c + t4, K);
+#pragma unroll
+        for (int c = 0; c < DQ_ACT_REG; c++)
+            if (DQ_ACT_CH * c < K) {  // uniform: every lane joins the 8-lane block reductions
+                float d;
+                int sum;
+                q[c] = quant32_lane(v[c], rounding, &d, &sum);
+                dh[c] = h2f(f2h(d));
+                amax = fmaxf(amax, dq_amax4(dq_vals(q[c], dh[c])));
+            }
+        const int ex = dq_row_exp(dq_block_max(amax, red));
+        if (threadIdx.x == 0) rs[m] = dq_pow2(-ex);
+        const float sc = dq_pow2(ex);
+#pragma unroll
+        for (int c = 0; c < DQ_ACT_REG; c++)
+            if (DQ_ACT_CH * c + t4 < K) *(v4h *)(out + DQ_ACT_CH * c + t4) = dq_h4(dq_vals(q[c], dh[c]), sc);
+        return;
+    }
+    for (int c = 0; c < K; c += DQ_ACT_CH) {
+        float d;
+        int sum;
+        const int q = quant32_lane(dq_ld4(xr, c + t4, K), rounding, &d, &sum);
+        amax = fmaxf(amax, dq_amax4(dq_vals(q, h2f(f2h(d)))));
+    }
+    const int ex = dq_row_exp(dq_block_max(amax, red));
+    if (threadIdx.x == 0) rs[m] = dq_pow2(-ex);
+    for (int c = 0; c < K; c += DQ_ACT_CH) {
+        float d;
+        int sum;
+        const int q = quant32_lane(dq_ld4(xr, c + t4, K), rounding, &d, &sum);
+        if (c + t4 < K) *(v4h *)(out + c + t4) = dq_h4(dq_vals(q, h2f(f2h(d))), dq_pow2(ex));
+    }
+}
+
+// Activation row m -> Q8_K blocks (ggml's quantize_row_q8_K_ref, the pairing of Q6_K weights) -> fp16(2^e fp32(d q)),
+// the product ggml's dequantize_row_q8_K forms, scaled and rounded once more. Wave w takes blocks w, w + 16, ...
+__global__ __launch_bounds__(DQ_ACT_NT) void k_dq_act_q8k(const float *x, int64_t x_stride, int K, _Float16 *xh,
+                                                           float *rs) {
+    constexpr int NWV = DQ_ACT_NT / 64;
+    __shared__ float red[NWV];
+    const int64_t m = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nsb = K / 256;
+    const float *xr = x + m * x_stride;
+    _Float16 *out = xh + m * K;
+    float amax = 0.0f;
+    if (nsb <= NWV * DQ_ACT_REG) {
+        float4 v[DQ_ACT_REG];
+        int q[DQ_ACT_REG];
+        float dq[DQ_ACT_REG];
+#pragma unroll
+        for (int i = 0; i < DQ_ACT_REG; i++) {
+            const int sb = wave + NWV * i;
+            v[i] = sb < nsb ? *(const float4 *)(xr + sb * 256 + 4 * lane) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < DQ_ACT_REG; i++)
+            if (wave + NWV * i < nsb) {  // wave-uniform
+                int bs16;
+                q[i] = quant256_wave(v[i], lane, &dq[i], &bs16);
+                amax = fmaxf(amax, dq_amax4(dq_vals(q[i], dq[i])));
+            }
+        const int ex = dq_row_exp(dq_block_max(amax, red));
+        if (threadIdx.x == 0) rs[m] = dq_pow2(-ex);
+        const float sc = dq_pow2(ex);
+#pragma unroll
+        for (int i = 0; i < DQ_ACT_REG; i++) {
+            const int sb = wave + NWV * i;
+            if (sb < nsb) *(v4h *)(out + sb * 256 + 4 * lane) = dq_h4(dq_vals(q[i], dq[i]), sc);
+        }
+        return;
+    }
+    for (int sb = wave; sb < nsb; sb += NWV) {
+        float d;
+        int bs16;
+        const int q = quant256_wave(*(const float4 *)(xr + sb * 256 + 4 * lane), lane, &d, &bs16);
+        amax = fmaxf(amax, dq_amax4(dq_vals(q, d)));
+    }
+    const int ex = dq_row_exp(dq_block_max(amax, red));
+    if (threadIdx.x == 0) rs[m] = dq_pow2(-ex);
+    for (int sb = wave; sb < nsb; sb += NWV) {
+        float d;
+        int bs16;
+        const int q = quant256_wave(*(const float4 *)(xr + sb * 256 + 4 * lane), lane, &d, &bs16);
+        *(v4h *)(out + sb * 256 + 4 * lane) = dq_h4(dq_vals(q, d), dq_pow2(ex));
     }
 }
 
@@ -126,6 +268,31 @@ __device__ __forceinline__ void dq_q8_0_16(v4i c, uint16_t dbits, v4i &o0, v4i &
              __builtin_bit_cast(int, h[3])};
     o1 = v4i{__builtin_bit_cast(int, h[4]), __builtin_bit_cast(int, h[5]), __builtin_bit_cast(int, h[6]),
              __builtin_bit_cast(int, h[7])};
+}
+
+// 16 Q6_K codes of one sub-block: code t = ((ql_t >> ls) & 15) | (((qh_t >> hs) & 3) << 4), value code - 32, times
+// d * sc (exact in fp32: 11 + 8 bits) -- (code - 32) * d * sc is exact in fp32 too (<= 24 bits), formed by one fma, and
+// rounded once to fp16.
+__device__ __forceinline__ void dq_q6_k_16(v4i ql, v4i qh, int hs, int ls, int sc, uint16_t dbits, v4i &o0, v4i &o1) {
+    _Float16 dh;
+    __builtin_memcpy(&dh, &dbits, 2);
+    const float ds = (float)dh * (float)sc, off = -32.0f * ds;
+    const uint32_t lw[4] = {(uint32_t)ql.x, (uint32_t)ql.y, (uint32_t)ql.z, (uint32_t)ql.w};
+    const uint32_t hw[4] = {(uint32_t)qh.x, (uint32_t)qh.y, (uint32_t)qh.z, (uint32_t)qh.w};
+    int r[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t c = ((lw[k] >> ls) & 0x0F0F0F0Fu) | (((hw[k] >> hs) & 0x03030303u) << 4);
+        v2h lo, hi;
+        lo.x = (_Float16)fmaf((float)(c & 0xFF), ds, off);
+        lo.y = (_Float16)fmaf((float)((c >> 8) & 0xFF), ds, off);
+        hi.x = (_Float16)fmaf((float)((c >> 16) & 0xFF), ds, off);
+        hi.y = (_Float16)fmaf((float)(c >> 24), ds, off);
+        r[2 * k] = __builtin_bit_cast(int, lo);
+        r[2 * k + 1] = __builtin_bit_cast(int, hi);
+    }
+    o0 = v4i{r[0], r[1], r[2], r[3]};
+    o1 = v4i{r[4], r[5], r[6], r[7]};
 }
 
 // NF fragment reads (4, 6, 8, 12 or 16) and the wait for them.
@@ -216,10 +383,10 @@ __device__ __forceinline__ void dq_read(v8h (&f)[16], const uint32_t (&a)[16]) {
     }
 }
 
-template <int BM, int BN, int WGM, int WGN>
-__global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
+template <int WT, int BM, int BN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     constexpr int NW = WGM * WGN, NT = 64 * NW;
-    using L = DqLds<BM, BN, NW>;
+    using L = DqLds<WT, BM, BN, NW>;
     constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
     constexpr int NF = (TM + TN) * 4;  // fragments of the stage's four K steps, read together
     static_assert(NF == 8 || NF == 12 || NF == 16, "wave tiles of 32 x 32, 64 x 32 or 64 x 64");
@@ -237,12 +404,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t lds = lds_addr(smem);
 
-    // Copy sources of this lane (stage 0; a stage adds 64 elements) and LDS destinations (stage 0; a stage adds its
-    // slot). Instruction j of a kind is issued by wave j / P (its jj = j % P); instructions past the tile's need copy
-    // a valid row again into the wave's junk area.
+    // Copy sources of this lane (row bases; issue adds the stage's offset) and LDS destinations (stage 0; a stage adds
+    // its slot). Instruction j of a kind is issued by wave j / P (its jj = j % P); instructions past the tile's need
+    // copy a valid row again into the wave's junk area.
     //   activations: instruction j covers rows 8 j .. 8 j + 7; lane i brings logical chunk (i & 7) ^ swz(row)
-    //   codes: instruction j covers rows 16 j .. 16 j + 15; lane i brings bytes 16 (i & 3) .. of its row
-    //   scales: instruction j covers rows 64 j .. 64 j + 63; lane i brings the stage's two block scales of its row
+    //   codes / ql: instruction j covers rows 16 j .. 16 j + 15; lane i brings bytes 16 (i & 3) .. of its row
+    //   qh: instruction j covers rows 32 j .. 32 j + 31; lane i brings bytes 16 (i & 1) .. of its row
+    //   scales, d: instruction j covers rows 64 j .. 64 j + 63; lane i brings its row's four bytes
+    const int nsb = K / 256;  // Q6_K super-blocks per row
     const _Float16 *asrc[L::PA];
     uint32_t adst[L::PA];
 #pragma unroll
@@ -256,59 +425,111 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
 #pragma unroll
     for (int jj = 0; jj < L::PC; jj++) {
         const int j = wave * L::PC + jj, row = 16 * min(j, L::NC - 1) + (lane >> 2);
-        csrc[jj] = p.w.p0 + (int64_t)min(n0 + row, N - 1) * K + sb * DQ_KS + 16 * (lane & 3);
+        const int64_t grow = min(n0 + row, N - 1);
+        csrc[jj] = (L::K6 ? p.w.p0 + grow * nsb * 128 : p.w.p0 + grow * K + sb * DQ_KS) + 16 * (lane & 3);
         cdst[jj] = j < L::NC ? L::RAW + j * 1024 : L::JUNK + wave * 1024;
+    }
+    const uint8_t *hsrc[L::PH > 0 ? L::PH : 1];
+    uint32_t hdst[L::PH > 0 ? L::PH : 1];
+#pragma unroll
+    for (int jj = 0; jj < L::PH; jj++) {
+        const int j = wave * L::PH + jj, row = 32 * min(j, L::NH - 1) + (lane >> 1);
+        hsrc[jj] = p.w.p1 + (int64_t)min(n0 + row, N - 1) * nsb * 64 + 16 * (lane & 1);
+        hdst[jj] = j < L::NH ? L::QH + j * 1024 : L::JUNK + wave * 1024;
     }
     const uint8_t *ssrc[L::PS];
     uint32_t sdst[L::PS];
 #pragma unroll
     for (int jj = 0; jj < L::PS; jj++) {
         const int j = wave * L::PS + jj, row = 64 * min(j, L::NS4 - 1) + lane;
-        ssrc[jj] = p.w.p1 + (int64_t)min(n0 + row, N - 1) * nblk * 2 + sb * 4;
+        const int64_t grow = min(n0 + row, N - 1);
+        ssrc[jj] = L::K6 ? p.w.p2 + grow * nsb * 16 : p.w.p1 + grow * nblk * 2 + sb * 4;
         sdst[jj] = j < L::NS4 ? L::SC + j * 256 : L::JUNK + wave * 1024;
     }
+    int64_t dsb[L::PD > 0 ? L::PD : 1];  // the row's first super-block index in the d plane
+    uint32_t ddst[L::PD > 0 ? L::PD : 1];
+#pragma unroll
+    for (int jj = 0; jj < L::PD; jj++) {
+        const int j = wave * L::PD + jj, row = 64 * min(j, L::ND - 1) + lane;
+        dsb[jj] = (int64_t)min(n0 + row, N - 1) * nsb;
+        ddst[jj] = j < L::ND ? L::DD + j * 256 : L::JUNK + wave * 1024;
+    }
 
-    auto issue = [&](int s) {
-        s = min(s, nst - 1);  // past the end: copy the last stage again into its own slot (identical bytes)
-        const int slot = s % DQ_NS;
+    auto issue = [&](int t) {
+        t = min(t, nst - 1);  // past the end: copy the last stage again into its own slot (identical bytes)
+        const int slot = t % DQ_NS, g = sb + t;  // g: the stage's index along the whole of K
 #pragma unroll
         for (int jj = 0; jj < L::PA; jj++) {
             const uint32_t d = adst[jj] + (adst[jj] < (uint32_t)L::JUNK ? slot * BM * 128 : 0);
-            __builtin_amdgcn_global_load_lds((const void *)(asrc[jj] + s * DQ_KS), (dq_lds *)(smem + d), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(asrc[jj] + t * DQ_KS), (dq_lds *)(smem + d), 16, 0, 0);
         }
+        // Q6_K: stage g is quarter g & 3 of super-block g >> 2; both quarters of a half read the half's ql and qh
+        const int coff = L::K6 ? (g >> 2) * 128 + ((g >> 1) & 1) * 64 : t * DQ_KS;
 #pragma unroll
         for (int jj = 0; jj < L::PC; jj++) {
             const uint32_t d = cdst[jj] + (cdst[jj] < (uint32_t)L::JUNK ? slot * BN * 64 : 0);
-            __builtin_amdgcn_global_load_lds((const void *)(csrc[jj] + s * DQ_KS), (dq_lds *)(smem + d), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(csrc[jj] + coff), (dq_lds *)(smem + d), 16, 0, 0);
         }
+#pragma unroll
+        for (int jj = 0; jj < L::PH; jj++) {
+            const uint32_t d = hdst[jj] + (hdst[jj] < (uint32_t)L::JUNK ? slot * BN * 32 : 0);
+            __builtin_amdgcn_global_load_lds((const void *)(hsrc[jj] + (g >> 2) * 64 + ((g >> 1) & 1) * 32),
+                                             (dq_lds *)(smem + d), 16, 0, 0);
+        }
+        const int soff = L::K6 ? (g >> 2) * 16 + (g & 3) * 4 : t * 4;
 #pragma unroll
         for (int jj = 0; jj < L::PS; jj++) {
             const uint32_t d = sdst[jj] + (sdst[jj] < (uint32_t)L::JUNK ? slot * BN * 4 : 0);
-            __builtin_amdgcn_global_load_lds((const void *)(ssrc[jj] + s * 4), (dq_lds *)(smem + d), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(ssrc[jj] + soff), (dq_lds *)(smem + d), 4, 0, 0);
+        }
+#pragma unroll
+        for (int jj = 0; jj < L::PD; jj++) {  // the aligned pair of fp16 d holding this row's (which half: convert)
+            const uint32_t d = ddst[jj] + (ddst[jj] < (uint32_t)L::JUNK ? slot * BN * 4 : 0);
+            const int64_t e = dsb[jj] + (g >> 2);
+            __builtin_amdgcn_global_load_lds((const void *)(p.w.p3 + (e >> 1) * 4), (dq_lds *)(smem + d), 4, 0, 0);
         }
     };
 
-    // Conversion of stage s's raw weights into fp16 tile buffer s & 1, in units of 16 codes: unit u is quarter u & 3
-    // of row u >> 2 (block (u & 3) >> 1 of the stage's two).
-    auto convert = [&](int s) {
-        const int slot = s % DQ_NS;
+    // Conversion of stage t's raw weights into fp16 tile buffer t & 1, in units of 16 codes: unit u is quarter u & 3
+    // of row u >> 2.
+    auto convert = [&](int t) {
+        const int slot = t % DQ_NS, g = sb + t;
 #pragma unroll
         for (int u = tid; u < BN * 4; u += NT) {
             const int row = u >> 2, q = u & 3;
             const uint32_t raw = lds + L::RAW + slot * BN * 64 + row * 64 + 16 * q;
             const uint32_t sc = lds + L::SC + slot * BN * 4 + row * 4;
-            v4i c0;
-            uint32_t sw;
-            asm volatile(
-                "ds_read_b128 %0, %2\n"
-                "ds_read_b32 %1, %3\n"
-                "s_waitcnt lgkmcnt(0)"
-                : "=&v"(c0), "=&v"(sw)
-                : "v"(raw), "v"(sc)
-                : "memory");
             v4i o[2];
-            dq_q8_0_16(c0, (uint16_t)((q >> 1) ? sw >> 16 : sw & 0xFFFF), o[0], o[1]);
-            const uint32_t out = lds + L::BH + (s & 1) * BN * 128 + row * 128;
+            if constexpr (!L::K6) {  // Q8_0: quarter q is half of block q >> 1
+                v4i c0;
+                uint32_t sw;
+                asm volatile(
+                    "ds_read_b128 %0, %2\n"
+                    "ds_read_b32 %1, %3\n"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(c0), "=&v"(sw)
+                    : "v"(raw), "v"(sc)
+                    : "memory");
+                dq_q8_0_16(c0, (uint16_t)((q >> 1) ? sw >> 16 : sw & 0xFFFF), o[0], o[1]);
+            } else {  // Q6_K: sub-block 4 (g & 3) + q of the super-block
+                const uint32_t qh = lds + L::QH + slot * BN * 32 + row * 32 + 16 * (q & 1);
+                const uint32_t dd = lds + L::DD + slot * BN * 4 + row * 4;
+                v4i l0, h0;
+                uint32_t sw, dw;
+                asm volatile(
+                    "ds_read_b128 %0, %4\n"
+                    "ds_read_b128 %1, %5\n"
+                    "ds_read_b32 %2, %6\n"
+                    "ds_read_b32 %3, %7\n"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(l0), "=&v"(h0), "=&v"(sw), "=&v"(dw)
+                    : "v"(raw), "v"(qh), "v"(sc), "v"(dd)
+                    : "memory");
+                const int64_t e = (int64_t)min(n0 + row, N - 1) * nsb + (g >> 2);
+                dq_q6_k_16(l0, h0, (g & 1) * 4 + (q >> 1) * 2, (g & 1) * 4, (int8_t)(sw >> (8 * q)),
+                           (uint16_t)((e & 1) ? dw >> 16 : dw & 0xFFFF), o[0], o[1]);
+            }
+            const uint32_t out = lds + L::BH + (t & 1) * BN * 128 + row * 128;
 #pragma unroll
             for (int i = 0; i < 2; i++)
                 asm volatile("ds_write_b128 %0, %1" ::"v"(out + 16 * ((2 * q + i) ^ dq_swz(row))), "v"(o[i])
@@ -341,10 +562,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
+    const float rs_row = a.rs[min(m0 + (tid < BM ? tid : 0), M - 1)];  // requested ahead of the copies
     issue(0);
     issue(1);
     issue(2);
     dq_wait_vm<2 * L::OPS>();  // stage 0 landed (this wave's copies)
+    if (tid < BM) *(float *)(smem + L::RS + 4 * tid) = rs_row;  // the tile rows' 2^-e, read by the epilogue
     __syncthreads();
     convert(0);
 
@@ -390,6 +613,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
         y = a.ws + (int64_t)split * M * a.ntot + a.col0[pi];
         ldy = a.ntot;
     }
+    const float *rsl = (const float *)(smem + L::RS);  // the rows' 2^-e
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -399,30 +623,43 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq_q8_0(DqArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);
-                if (m < M) y[(int64_t)m * ldy + n] = acc[i][j][r];
+                if (m < M) y[(int64_t)m * ldy + n] = acc[i][j][r] * rsl[m - m0];
             }
         }
 }
 
-// y[m][col] = sum of the nsplit partials of (m, col), split 0 first; one thread per (column, row).
+// y[m][col] = sum of the nsplit partials of (m, col), split 0 first; one thread per VW columns of a row (VW = 4 when
+// every problem's width, row stride and base allow 16-byte accesses).
+template <int VW>
 __global__ __launch_bounds__(256) void k_dq_reduce(DqArgs a) {
-    const int c = blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+    using V = typename std::conditional<VW == 4, float4, float>::type;
+    const int c = (blockIdx.x * 256 + threadIdx.x) * VW, m = blockIdx.y;
     if (c >= a.ntot) return;
     const int64_t plane = (int64_t)a.M * a.ntot;
     const float *ws = a.ws + (int64_t)m * a.ntot + c;
-    float v[8];
-    float sum = 0.0f;
+    auto add = [](V &s, V v) {
+        if constexpr (VW == 4) {
+            s.x += v.x;
+            s.y += v.y;
+            s.z += v.z;
+            s.w += v.w;
+        } else {
+            s += v;
+        }
+    };
+    V v[8], sum{};
     for (int s0 = 0; s0 < a.nsplit; s0 += 8) {  // eight partials' loads in flight at a time
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = s0 + u < a.nsplit ? ws[(s0 + u) * plane] : 0.0f;
+        for (int u = 0; u < 8; u++)
+            if (s0 + u < a.nsplit) v[u] = *(const V *)(ws + (s0 + u) * plane);
 #pragma unroll
         for (int u = 0; u < 8; u++)
-            if (s0 + u < a.nsplit) sum += v[u];
+            if (s0 + u < a.nsplit) add(sum, v[u]);
     }
     int pi = 0;
     while (pi + 1 < a.nprob && c >= a.col0[pi + 1]) pi++;
     const DqProblem &p = pi == 0 ? a.prob[0] : (pi == 1 ? a.prob[1] : (pi == 2 ? a.prob[2] : a.prob[3]));
-    p.y[(int64_t)m * p.ldy + (c - a.col0[pi])] = sum;
+    *(V *)(p.y + (int64_t)m * p.ldy + (c - a.col0[pi])) = sum;
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -433,7 +670,8 @@ bool gemm_dq_supported(int type, int64_t M, int64_t K) {
         const char *e = getenv("MX_GEMM_DQ");
         return e && e[0] == '0';
     }();
-    return !off && type == MX_TYPE_Q8_0 && K % DQ_KS == 0 && M * K < ((int64_t)1 << 31) && K < (1 << 24);
+    return !off && ((type == MX_TYPE_Q8_0 && K % DQ_KS == 0) || (type == MX_TYPE_Q6_K && K % 256 == 0)) &&
+           M * K < ((int64_t)1 << 31) && K < (1 << 24);
 }
 
 size_t gemm_dq_act_bytes(int64_t M, int64_t K) { return (size_t)M * (size_t)K * 2; }
@@ -458,7 +696,11 @@ DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K) {
         pl.ntot += N[i];
     }
     wg128 *= (M + 127) / 128;
-    if (wg128 >= 128) pl.bm = pl.bn = 128;
+    const int64_t nst = K / DQ_KS;
+    // long products (K >= 4096) whose 128 x 128 grid is smaller still keep the large tile and split K instead (at
+    // M = 512, N = 2048, K = 6144: four splits of 24 stages and the reduce beat 256 tiles of 64 x 64)
+    const bool split128 = wg128 >= 32 && wg128 < 128 && nst >= 64;
+    if (wg128 >= 128 || split128) pl.bm = pl.bn = 128;
     static const char *tile = getenv("MX_GEMM_DQ_TILE");
     if (tile) {
         int tm = 0, tn = 0;
@@ -471,8 +713,8 @@ DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K) {
     int64_t tiles = 0;
     for (int i = 0; i < nprob; i++) tiles += (N[i] + pl.bn - 1) / pl.bn;
     tiles *= (M + pl.bm - 1) / pl.bm;
-    const int64_t nst = K / DQ_KS;
     int64_t want = tiles < 256 && pl.bn == 64 ? (512 + tiles - 1) / tiles : 1;
+    if (split128 && pl.bm == 128 && pl.bn == 128) want = (256 + tiles - 1) / tiles;
     static const int forced = [] {
         const char *e = getenv("MX_GEMM_DQ_SPLIT");
         return e ? atoi(e) : 0;
@@ -486,34 +728,53 @@ DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K) {
 
 }  // namespace
 
+// scratch: [xh: M K fp16][rs: M floats][partials: nsplit M ntot floats], each part 256-byte aligned
+static size_t dq_rs_offset(int64_t M, int64_t K) { return (gemm_dq_act_bytes(M, K) + 255) / 256 * 256; }
+static size_t dq_ws_offset(int64_t M, int64_t K) { return dq_rs_offset(M, K) + ((size_t)M * 4 + 255) / 256 * 256; }
+
 size_t gemm_dq_scratch_bytes(int nprob, const int64_t *N, int64_t M, int64_t K) {
     const DqPlan pl = dq_plan(nprob, N, M, K);
-    size_t b = (gemm_dq_act_bytes(M, K) + 255) / 256 * 256;
+    size_t b = dq_ws_offset(M, K);
     if (pl.nsplit > 1) b += (size_t)pl.nsplit * (size_t)M * (size_t)pl.ntot * 4;
     return b;
 }
 
 hipError_t launch_gemm_dq_act(int type, int rounding, const float *x, int64_t x_stride, int64_t M, int64_t K,
                               void *xh, hipStream_t s) {
-    if (type != MX_TYPE_Q8_0) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((K + 1023) / 1024), (unsigned)M);
-    hipLaunchKernelGGL(k_dq_act_q8_0, grid, dim3(256), 0, s, x, x_stride, (int)K, rounding, (_Float16 *)xh);
+    float *rs = (float *)((uint8_t *)xh + dq_rs_offset(M, K));
+    if (M == 0) return hipSuccess;
+    if (type == MX_TYPE_Q8_0) {
+        hipLaunchKernelGGL(k_dq_act_q8_0, dim3((unsigned)M), dim3(DQ_ACT_NT), 0, s, x, x_stride, (int)K, rounding,
+                           (_Float16 *)xh, rs);
+    } else if (type == MX_TYPE_Q6_K && K % 256 == 0) {  // Q8_K has one rounding form
+        hipLaunchKernelGGL(k_dq_act_q8k, dim3((unsigned)M), dim3(DQ_ACT_NT), 0, s, x, x_stride, (int)K, (_Float16 *)xh,
+                           rs);
+    } else {
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
-template <int BM, int BN, int WGM, int WGN>
+template <int WT, int BM, int BN, int WGM, int WGN>
 static hipError_t launch_dq(const DqArgs &a, int maxN, hipStream_t s) {
-    using L = DqLds<BM, BN, WGM * WGN>;
+    using L = DqLds<WT, BM, BN, WGM * WGN>;
     static bool attr = false;
     if (!attr) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm_dq_q8_0<BM, BN, WGM, WGN>,
+        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm_dq<WT, BM, BN, WGM, WGN>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, L::SIZE);
         if (e != hipSuccess) return e;
         attr = true;
     }
     const dim3 grid((unsigned)((maxN + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM), (unsigned)(a.nprob * a.nsplit));
-    hipLaunchKernelGGL((k_gemm_dq_q8_0<BM, BN, WGM, WGN>), grid, dim3(64 * WGM * WGN), L::SIZE, s, a);
+    hipLaunchKernelGGL((k_gemm_dq<WT, BM, BN, WGM, WGN>), grid, dim3(64 * WGM * WGN), L::SIZE, s, a);
     return hipGetLastError();
+}
+
+template <int WT>
+static hipError_t launch_dq_type(const DqArgs &a, const DqPlan &pl, int maxN, hipStream_t s) {
+    if (pl.bm == 128 && pl.bn == 128) return launch_dq<WT, 128, 128, 2, MX_DQ_WGN128>(a, maxN, s);
+    if (pl.bm == 128) return launch_dq<WT, 128, 64, 4, 2>(a, maxN, s);
+    return launch_dq<WT, 64, 64, 2, 2>(a, maxN, s);
 }
 
 hipError_t launch_gemm_dq(int type, int nprob, const WPlanes *w, const int64_t *N, float *const *y,
@@ -533,16 +794,18 @@ hipError_t launch_gemm_dq(int type, int nprob, const WPlanes *w, const int64_t *
     a.M = (int)M;
     a.K = (int)K;
     a.xh = (const _Float16 *)scratch;
+    a.rs = (const float *)((const uint8_t *)scratch + dq_rs_offset(M, K));
     a.nprob = nprob;
     a.nsplit = pl.nsplit;
     a.ntot = (int)pl.ntot;
-    a.ws = (float *)((uint8_t *)scratch + (gemm_dq_act_bytes(M, K) + 255) / 256 * 256);
-    hipError_t e;
-    if (pl.bm == 128 && pl.bn == 128) e = launch_dq<128, 128, 2, MX_DQ_WGN128>(a, (int)maxN, s);
-    else if (pl.bm == 128) e = launch_dq<128, 64, 4, 2>(a, (int)maxN, s);
-    else e = launch_dq<64, 64, 2, 2>(a, (int)maxN, s);
+    a.ws = (float *)((uint8_t *)scratch + dq_ws_offset(M, K));
+    const hipError_t e = type == MX_TYPE_Q8_0 ? launch_dq_type<MX_TYPE_Q8_0>(a, pl, (int)maxN, s)
+                                              : launch_dq_type<MX_TYPE_Q6_K>(a, pl, (int)maxN, s);
     if (e != hipSuccess || pl.nsplit == 1) return e;
-    hipLaunchKernelGGL(k_dq_reduce, dim3((unsigned)((pl.ntot + 255) / 256), (unsigned)M), dim3(256), 0, s, a);
+    bool v4 = true;
+    for (int i = 0; i < nprob; i++) v4 = v4 && N[i] % 4 == 0 && ldy[i] % 4 == 0 && (uintptr_t)y[i] % 16 == 0;
+    if (v4) hipLaunchKernelGGL(k_dq_reduce<4>, dim3((unsigned)((pl.ntot / 4 + 255) / 256), (unsigned)M), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(k_dq_reduce<1>, dim3((unsigned)((pl.ntot + 255) / 256), (unsigned)M), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

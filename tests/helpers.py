@@ -24,12 +24,23 @@ def bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
                                                  np.ascontiguousarray(b).view(np.uint8))
 
 
+def dq_row_exp(amax: np.ndarray) -> np.ndarray:
+    """The power of two the fp16 GEMM scales an activation row by: 2^e puts the row's largest |value| in
+    [2^14, 2^15) (e = 0 for an all-zero row; e within [-126, 127])."""
+    _, ex = np.frexp(amax.astype(np.float64))  # amax = f 2^ex, f in [0.5, 1)
+    e = np.where(amax > 0, 15 - ex, 0)
+    return np.clip(e, -126, 127)
+
+
 def dq_model(oracle, wtype: int, w: np.ndarray, x: np.ndarray, K: int, rounding: int = 0) -> np.ndarray:
     """What the dequantizing fp16 GEMM computes, exactly up to its fp32 summation order: every weight and every
-    quantized activation (the oracle's own quantization of x for the weight's dot) rounded once to fp16, products
-    summed in float64. Kernel against this model: ~1e-6; this model against the oracle: a few 1e-4."""
+    quantized activation (the oracle's own quantization of x for the weight's dot, its fp32 values times the row's
+    power-of-two scale) rounded once to fp16, products summed in float64 and the scale taken off. Kernel against this
+    model: ~1e-6; this model against the oracle: a few 1e-4."""
     act_type = oracle.TYPE_Q8_0 if wtype == oracle.TYPE_Q8_0 else oracle.TYPE_Q8_K
     wd = oracle.dequantize_rows(wtype, w, K).astype(np.float16).astype(np.float64)
     xq = oracle.quantize_rows(act_type, np.ascontiguousarray(x, dtype=np.float32), rounding)
-    xd = oracle.dequantize_rows(act_type, xq, K).astype(np.float16).astype(np.float64)
+    xv = oracle.dequantize_rows(act_type, xq, K).astype(np.float64)
+    sc = np.ldexp(1.0, dq_row_exp(np.abs(xv).max(axis=1)))[:, None]
+    xd = (xv * sc).astype(np.float16).astype(np.float64) / sc
     return xd @ wd.T

@@ -20,7 +20,7 @@ DQ = __import__("os").environ.get("MX_GEMM_DQ", "1") != "0"
 
 def uses_dq(t, M, K):
     """Whether MUL_MAT takes the dequantizing fp16 GEMM (its dispatch rule)."""
-    return DQ and t == O.TYPE_Q8_0 and M > 8 and K % 64 == 0
+    return DQ and M > 8 and ((t == O.TYPE_Q8_0 and K % 64 == 0) or (t == O.TYPE_Q6_K and K % 256 == 0))
 
 
 def check_product(t, w, x, y, K, rounding=O.ROUND_REF):
@@ -174,8 +174,10 @@ def test_mul_mat_small_m(mx, be, t, M):
     w = weights(t, N, K, 0x5EED0400 + t)
     x = acts(0xAC700400 + M, M, K)
     y = run_mul_mat(mx, be, t, w, x, K, N)
-    y_ref = O.mul_mat(t, w, x)
-    assert rel_err(y, y_ref) <= TIGHT
+    if uses_dq(t, M, K):  # past eight columns Q8_0 / Q6_K take the fp16 GEMM
+        check_product(t, w, x, y, K)
+        return
+    assert rel_err(y, O.mul_mat(t, w, x)) <= TIGHT
     assert rel_err(y, O.mul_mat(t, w, x, exact=True)) <= TIGHT
 
 
@@ -391,6 +393,22 @@ def test_mul_mat_gemm_group_q8_0_split(mx, be):
         assert bits_equal(yt.numpy().reshape(M, n), y)
 
 
+@pytest.mark.parametrize("t,M,Ns,K", [(O.TYPE_Q8_0, 160, [3000], 4096), (O.TYPE_Q6_K, 160, [3000], 4096),
+                                      (O.TYPE_Q8_0, 140, [1024, 1024], 4096)], ids=["q8_0", "q6_K", "q8_0_group"])
+def test_mul_mat_gemm_long_k(mx, be, t, M, Ns, K):
+    """Long products whose 128 x 128 grid is small keep the large tile and split K: ragged widths through the scalar
+    reduce, a two-weight group of widths divisible by four through the vector one."""
+    ws = [weights(t, n, K, 0x5EED1400 + n + t) for n in Ns]
+    x = acts(0xAC701400 + M, M, K)
+    W = [be.tensor(t, (K, n), w) for n, w in zip(Ns, ws)]
+    X = be.tensor(mx.F32, (K, M), x)
+    Y = [be.tensor(mx.F32, (n, M)) for n in Ns]
+    be.mul_mat_group(W, X, Y)
+    be.sync()
+    for n, w, yt in zip(Ns, ws, Y):
+        check_product(t, w, x, yt.numpy().reshape(M, n), K)
+
+
 def test_mul_mat_gemm_batched(mx, be):
     t, K, N, M = O.TYPE_Q8_0, 1024, 96, 40
     w = weights(t, N * 2, K, 0x5EED0B00)
@@ -413,7 +431,7 @@ def test_mul_mat_gemm_kquant(mx, be, t, M, N, K):
     w = weights(t, N, K, 0x5EED0C00 + M + N + t)
     x = acts(0xAC700C00 + M, M, K)
     y = run_mul_mat(mx, be, t, w, x, K, N)
-    assert rel_err(y, O.mul_mat(t, w, x)) <= TIGHT
+    check_product(t, w, x, y, K)
 
 
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
@@ -440,7 +458,7 @@ def test_mul_mat_gemm_kquant_batched(mx, be, t):
     y = Y.numpy()
     for i2 in range(4):
         wm = w[(i2 // 2) * N:(i2 // 2 + 1) * N]
-        assert rel_err(y[0, i2], O.mul_mat(t, wm, x[0, i2])) <= TIGHT
+        check_product(t, wm, x[0, i2], y[0, i2], K)
 
 
 @pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
@@ -456,7 +474,7 @@ def test_mul_mat_gemm_kquant_group(mx, be, t):
     be.mul_mat_group(W, X, Y)
     be.sync()
     for n, wi, Yi in zip(Ns, w, Y):
-        assert rel_err(Yi.numpy().reshape(M, n), O.mul_mat(t, wi, x)) <= TIGHT
+        check_product(t, wi, x, Yi.numpy().reshape(M, n), K)
 
 
 # ------------------------------------------------------------------------------------------- F16 / F32 weights

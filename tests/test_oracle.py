@@ -224,6 +224,22 @@ def test_q8_K_bsums_and_range():
     assert np.all(q[4:8, :4].view(np.float32) == 0)  # the zero row's four blocks have d = 0
 
 
+def test_q8_K_dequantize():
+    """ggml's dequantize_row_q8_K (d * q in fp32): a row of k / 128 whose first largest magnitude is -127 / 128
+    quantizes to d = 1 / 128, q = k and comes back exactly; random rows match the independent decoder rounded to
+    fp32."""
+    k = np.concatenate([np.arange(-127, 128), [127]]).astype(np.float32)
+    x = (k / 128.0).astype(np.float32)[None]
+    q = O.quantize_rows(O.TYPE_Q8_K, x)
+    assert q[0, :4].view(np.float32)[0] == np.float32(1.0 / 128)
+    assert np.array_equal(q[0, 4:260].view(np.int8), k.astype(np.int8))
+    assert np.array_equal(O.dequantize_rows(O.TYPE_Q8_K, q, 256), x)
+    y = O.fill_normal(33, 3, 512)
+    qy = O.quantize_rows(O.TYPE_Q8_K, y)
+    got = O.dequantize_rows(O.TYPE_Q8_K, qy, 512)
+    assert np.array_equal(got.reshape(-1).view(np.uint32), decode(O.TYPE_Q8_K, qy.reshape(-1)).astype(np.float32).view(np.uint32))
+
+
 def test_q8_0_roundtrip_full_range_blocks():
     rng = np.random.default_rng(8)
     q = rng.integers(-127, 128, size=(64, 32))
