@@ -346,7 +346,7 @@ COPY_BYTES = 256 << 20  # the plain copy the counters are calibrated on
 TRAFFIC = {"decode": ("k_matvec_q8_0_qwen3-0.6b_decode.traffic.txt", "k_matvec"),
            "matvec": ("k_matvec_q8_0_3072x1024_rotated.traffic.txt", "k_matvec"),
            "prefill-q4k": ("k_gemm_q4k_qwen3-1.7b_prefill.traffic.txt", "k_gemm_q4k<"),
-           "asr-1.7b": ("k_gemm_dq_q8_0_qwen3-asr-1.7b_prefill.traffic.txt", "k_gemm_dq_q8_0"),
+           "asr-1.7b": ("k_gemm_dq_q8_0_qwen3-asr-1.7b_prefill.traffic.txt", "k_gemm_dq<8,"),
            "moe": ("k_mmid_q4k_drama3_moe.traffic.txt", "k_mmid_q4k")}
 
 
@@ -742,7 +742,10 @@ def run_prefill_q4k(args, mx, be, threads):
     wb = dec.layer_bytes()
     result.update({"int8_frac": round(tops / INT8_PEAK_TOPS, 4), "ops_per_step": ops, "weight_bytes": wb,
                    "tok_s": round(M / (ms_per_step * 1e-3), 1), "roofline": roof,
-                   "q6_k_down": mfma_roofline("k_gemm_kq<Q6_K>", table, ["down:Q6_K"])})
+                   "q6_k_down": (mfma_roofline("k_gemm_dq<Q6_K> (with its Q8_K activation pass)", table, ["down:Q6_K"],
+                                               FP16_PEAK_TFLOPS, "TFLOP/s")
+                                 if os.environ.get("MX_GEMM_DQ", "1") != "0" else
+                                 mfma_roofline("k_gemm_kq<Q6_K>", table, ["down:Q6_K"]))})
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_prefill(dec, M, args.cpu_seconds, types)
     return result
@@ -778,7 +781,7 @@ def run_asr(args, mx, be, threads):
     # the prefill GEMM dequantizes Q8_0 weights and Q8_0-quantized activations to fp16 and accumulates in fp32 on
     # fp16 MFMA (MX_GEMM_DQ=0 selects the int8 MFMA GEMM); the decode mat-vecs use int8 dot products
     dq = os.environ.get("MX_GEMM_DQ", "1") != "0"
-    roof = (mfma_roofline("k_gemm_dq_q8_0 (with its activation pass)", table,
+    roof = (mfma_roofline("k_gemm_dq<Q8_0> (with its activation pass)", table,
                           [l for l in table if l.startswith("prefill_M512")], FP16_PEAK_TFLOPS, "TFLOP/s") if dq else
             mfma_roofline("k_gemm_q8_0_i8 (with its activation pass)", table,
                           [l for l in table if l.startswith("prefill_M512")]))

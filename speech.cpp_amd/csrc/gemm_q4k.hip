@@ -528,7 +528,9 @@ hipError_t launch_gemm_q4k(int nprob, const WPlanes *w, const int64_t *N, float 
     a.xq = sp.xq;
     a.xd = sp.xd;
     a.x16 = sp.x16;
-    // Tile: 128 x 128 (eight waves, two per SIMD) when that gives the chip enough workgroups, else 128 x 64 (four).
+    // Tile: 128 x 128 (eight waves, two per SIMD) when that gives at least 128 workgroups, else 128 x 64 (four).
+    // Measured at M = 512: q/k/v (N = 4096) on 128 workgroups of 128 x 128 takes 29.7 us against 43.3 us on 256 of
+    // 128 x 64; attn_o (N = 2048) on 64 of 128 x 128 takes 29.0 us against 24.8 us on 128 of 128 x 64.
     // MX_GEMM_Q4K_TILE=1 forces 128 x 128, =2 128 x 64.
     static const int tile = [] {
         const char *e = getenv("MX_GEMM_Q4K_TILE");
@@ -536,7 +538,7 @@ hipError_t launch_gemm_q4k(int nprob, const WPlanes *w, const int64_t *N, float 
     }();
     int64_t wg_big = 0;
     for (int i = 0; i < nprob; i++) wg_big += (N[i] + 127) / 128 * ((M + 127) / 128);
-    if (tile == 1 || (tile != 2 && wg_big >= 160)) return launch_q4g<Q4gT<2, 2, 4>>(a, nprob, (int)maxN, s);
+    if (tile == 1 || (tile != 2 && wg_big >= 128)) return launch_q4g<Q4gT<2, 2, 4>>(a, nprob, (int)maxN, s);
     return launch_q4g<Q4gT<2, 2, 2>>(a, nprob, (int)maxN, s);
 }
 

@@ -145,7 +145,9 @@ __device__ __forceinline__ void fused_prologue(const MatvecArgs &a, const float 
     }
 }
 
-template <int TYPE, int NC, int LPR>
+// FUSED: the instantiation that reads the fused operands (norm weight, SwiGLU input, residual); the plain one is
+// compiled without them, so products with no fusion keep their smaller register footprint.
+template <int TYPE, int NC, int LPR, bool FUSED>
 __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int K = (int)a.K;
@@ -179,14 +181,14 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
         for (int i = 0; i < XP; i++) xr[c][i] = load_x4(x + c * a.x_col_stride, 1024 * i + 4 * tid, K);
     // the fused prologue's other operands come in with x: SwiGLU's second input and the norm weight
     float4 br[NC][XP], wr[XP];
-    if (a.glu_b) {
+    if (FUSED && a.glu_b) {
         const float *gb = a.glu_b + xi12 * a.x_b2 + i13 * a.x_b3;
 #pragma unroll
         for (int c = 0; c < NC; c++)
 #pragma unroll
             for (int i = 0; i < XP; i++) br[c][i] = load_x4(gb + c * a.x_col_stride, 1024 * i + 4 * tid, K);
     }
-    if (a.norm_w) {
+    if (FUSED && a.norm_w) {
 #pragma unroll
         for (int i = 0; i < XP; i++) wr[i] = load_x4(a.norm_w, 1024 * i + 4 * tid, K);
     }
@@ -205,7 +207,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     // the residual the epilogue adds, requested now rather than after the reduction
     const int64_t yoff = i12 * a.y_b2 + i13 * a.y_b3 + row;
     float rr[NC];
-    if (p.res && has_row && sub == LPR - 1) {
+    if (FUSED && p.res && has_row && sub == LPR - 1) {
 #pragma unroll
         for (int c = 0; c < NC; c++) rr[c] = p.res[yoff + c * p.y_col_stride];
     }
@@ -221,8 +223,23 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     float *xd = (float *)(smem + (size_t)NC * K);
     constexpr int XDB = TYPE == MX_TYPE_Q8_0 ? 32 : 256;
     int *xbs = (int *)(xd + NC * (K / XDB));
-    if (a.glu_b || a.norm_w) {  // uniform: the fused prologue
-        fused_prologue<TYPE, NC>(a, x, xi12, i13, xr, br, wr, xq, xd, xbs);
+    if constexpr (FUSED) {
+        if (a.glu_b || a.norm_w) {  // uniform: the fused prologue
+            fused_prologue<TYPE, NC>(a, x, xi12, i13, xr, br, wr, xq, xd, xbs);
+        } else {
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const float *xc = x + c * a.x_col_stride;
+#pragma unroll
+                for (int i = 0; i < XP; i++)
+                    if (1024 * i < K)
+                        quantize_piece<TYPE>(xr[c][i], 1024 * i, K, a.rounding, xq + c * K, xd + c * (K / XDB),
+                                             xbs + c * (K / 16));
+                for (int base = 1024 * XP; base < K; base += 1024)
+                    quantize_piece<TYPE>(load_x4(xc, base + 4 * tid, K), base, K, a.rounding, xq + c * K,
+                                         xd + c * (K / XDB), xbs + c * (K / 16));
+            }
+        }
     } else {
 #pragma unroll
         for (int c = 0; c < NC; c++) {
@@ -254,7 +271,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     for (int c = 0; c < NC; c++) acc[c] = sum_lanes<LPR>(acc[c]);
     if (sub == LPR - 1) {  // the lane holding the group's sum
         float *y = p.y + yoff;
-        if (p.res) {  // the residual ADD that follows the product, fused
+        if (FUSED && p.res) {  // the residual ADD that follows the product, fused
 #pragma unroll
             for (int c = 0; c < NC; c++) y[c * p.y_col_stride] = rr[c] + acc[c];
         } else {
@@ -268,7 +285,10 @@ template <int TYPE, int NC, int LPR>
 static hipError_t launch_one(const MatvecArgs &a, int64_t maxN, size_t lds, hipStream_t s) {
     constexpr int G = 64 / LPR;
     dim3 grid((unsigned)((maxN + 4 * G - 1) / (4 * G)), (unsigned)a.nprob, (unsigned)a.nbatch);
-    hipLaunchKernelGGL((k_matvec<TYPE, NC, LPR>), grid, dim3(256), lds, s, a);
+    bool fused = a.glu_b || a.norm_w;
+    for (int i = 0; i < a.nprob; i++) fused = fused || a.prob[i].res;
+    if (fused) hipLaunchKernelGGL((k_matvec<TYPE, NC, LPR, true>), grid, dim3(256), lds, s, a);
+    else hipLaunchKernelGGL((k_matvec<TYPE, NC, LPR, false>), grid, dim3(256), lds, s, a);
     return hipGetLastError();
 }
 
