@@ -42,8 +42,8 @@ constexpr int DQ_KS = 64;  // K per stage
 constexpr int DQ_NS = 4;   // ring stages (copies run DQ_NS - 1 stages ahead)
 
 // LDS map of a BM x BN workgroup of NW waves. Row-major fp16 tiles of 64 halves (128 bytes) per row; the 16-byte
-// chunk c of row r sits at chunk c ^ ((r >> 1) & 7), so the 16 rows one pass of an MFMA fragment read touches hit all
-// 64 banks once.
+// chunk c of row r sits at chunk c ^ ((r ^ (r >> 3)) & 7): any 8 consecutive rows an MFMA fragment read touches use 8
+// different chunks (all 32 banks of a 128-byte cycle), and 16 consecutive rows cover all 64 banks of a 256-byte one.
 template <int WT, int BM, int BN, int NW>
 struct DqLds {
     static constexpr bool K6 = WT == MX_TYPE_Q6_K;
@@ -65,7 +65,7 @@ struct DqLds {
     static_assert(SIZE <= 160 * 1024, "LDS");
 };
 
-__device__ __forceinline__ int dq_swz(int row) { return (row >> 1) & 7; }
+__device__ __forceinline__ int dq_swz(int row) { return (row ^ (row >> 3)) & 7; }
 
 struct DqProblem {
     WPlanes w;
