@@ -472,7 +472,7 @@ RMS_EPS, ROPE_THETA = 1e-6, 1e6
 
 def full_step_launches(be, mx, dec, st, ids, nq, nkv, hd, fused=True):
     """The decode step's launches, in Qwen3Decoder::layers order (qwen3-decoder.cpp:350-412, outputs :422-438). Fused:
-    norm + q/k/v, q/k norm + RoPE + KV stores, attention, attn_o + residual, norm + gate/up, SwiGLU + down + residual
+    norm + q/k/v, q/k norm + RoPE + KV stores + attention, attn_o + residual, norm + gate/up, SwiGLU + down + residual
     (each fusion computes what the separate ops compute); unfused: one launch per ggml node."""
     H, kv_dim, n_kv = dec.hidden, nkv * hd, st["n_kv"]
     L = []
@@ -495,10 +495,11 @@ def full_step_launches(be, mx, dec, st, ids, nq, nkv, hd, fused=True):
             L += [Launch("qkv", wq + 4 * (H + (nq + 2 * nkv) * hd), 0,
                          lambda w=w, nw=nw: be.mul_mat_fused([w["q"], w["k"], w["v"]], x, [o["q"], o["k"], o["v"]],
                                                              norm_w=nw["attn"], eps=RMS_EPS), weight_bytes=wq),
-                  Launch("qkv_post", 4 * (2 * nq * hd + 2 * kv_dim) + 2 * 2 * kv_dim, 0,
-                         lambda qv=qv, kv=kv, vv=vv, nw=nw, c=c: be.qk_norm_rope_kv(
-                             qv, kv, vv, nw["q"], nw["k"], pos, st["qr"], c["k"], c["v"], RMS_EPS, ROPE_THETA)),
-                  attention,
+                  # q / k norms, RoPE and the KV stores ride in the attention launch (mx_attn_decode)
+                  Launch("attention", attention.nbytes + 4 * (nq * hd + 2 * kv_dim) + 2 * 2 * kv_dim, 0,
+                         lambda qv=qv, kv=kv, vv=vv, nw=nw, c=c, kh=kh, vh=vh: be.attn_decode(
+                             qv, kv, vv, nw["q"], nw["k"], pos, c["k"], c["v"], kh, vh, mask, st["att"], RMS_EPS,
+                             ROPE_THETA, 1.0 / np.sqrt(hd))),
                   Launch("attn_o", wo + 4 * (nq * hd + 2 * H), 0,
                          lambda w=w: be.mul_mat_fused([w["o"]], st["att_rows"], [x], residual=[x]), weight_bytes=wo),
                   Launch("gate_up", wg + 4 * (H + 2 * dec.ffn), 0,

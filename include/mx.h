@@ -193,6 +193,19 @@ MX_API int mx_qk_norm_rope_kv(mx_backend *be, const mx_tensor *q, const mx_tenso
                               const mx_tensor *q_out, const mx_tensor *k_cache, const mx_tensor *v_cache, float eps,
                               int n_dims, int mode, float freq_base, float freq_scale, float ext_factor,
                               float attn_factor);
+/* One decode row's attention with the q / k norms, RoPE and KV-cache stores before it, in one launch: no single ggml
+ * op -- mx_qk_norm_rope_kv(q, k, v, q_norm, k_norm, pos, q_out, k_cache, v_cache, ...) followed by
+ * mx_flash_attn_ext(q_out viewed [128, 1, heads], k_view, v_view, mask, dst, scale) (qwen3-decoder.cpp:366-397), for
+ * a caller or graph_compute that recognises the pair. Every value as those two compute it; the roped q is not written
+ * out. One row (pos holds one position), head size 128, 1, 2 or 4 q heads per kv head, k_view / v_view the caches
+ * read from row 0 ([128, n_kv, heads_kv], head stride 256 bytes); anything else returns MX_UNSUPPORTED and the two
+ * calls run separately. */
+MX_API int mx_attn_decode(mx_backend *be, const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
+                          const mx_tensor *q_norm, const mx_tensor *k_norm, const mx_tensor *pos,
+                          const mx_tensor *k_cache, const mx_tensor *v_cache, const mx_tensor *k_view,
+                          const mx_tensor *v_view, const mx_tensor *mask, const mx_tensor *dst, float eps, int n_dims,
+                          int mode, float freq_base, float freq_scale, float ext_factor, float attn_factor,
+                          float scale);
 MX_API int mx_supports_flash_attn_ext(const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
                                       const mx_tensor *mask, const mx_tensor *dst, float max_bias,
                                       float logit_softcap);

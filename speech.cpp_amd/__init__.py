@@ -44,7 +44,7 @@ EXPORTS = [
     "mx_gguf_find_tensor", "mx_gguf_n_keys", "mx_gguf_key", "mx_gguf_find_key", "mx_gguf_key_type", "mx_gguf_get_str",
     "mx_gguf_get_int", "mx_gguf_get_float", "mx_gguf_get_arr", "mx_gguf_get_arr_str", "mx_gguf_load_tensor",
     "mx_rms_norm", "mx_binary", "mx_swiglu", "mx_supports_rope", "mx_rope", "mx_set_rows", "mx_supports_flash_attn_ext",
-    "mx_flash_attn_ext", "mx_mul_mat_fused", "mx_qk_norm_rope_kv",
+    "mx_flash_attn_ext", "mx_mul_mat_fused", "mx_qk_norm_rope_kv", "mx_attn_decode",
 ]
 
 
@@ -160,6 +160,7 @@ def lib():
         "mx_flash_attn_ext": ([vp, P, P, P, P, P, f32], i32),
         "mx_mul_mat_fused": ([vp, i32, ctypes.POINTER(P), P, ctypes.POINTER(P), ctypes.POINTER(MxFusion)], i32),
         "mx_qk_norm_rope_kv": ([vp, P, P, P, P, P, P, P, P, P, f32, i32, i32, f32, f32, f32, f32], i32),
+        "mx_attn_decode": ([vp, P, P, P, P, P, P, P, P, P, P, P, P, f32, i32, i32, f32, f32, f32, f32, f32], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -363,6 +364,14 @@ class Backend:
         check(lib().mx_qk_norm_rope_kv(self.h, q.ref(), k.ref(), v.ref(), q_norm.ref(), k_norm.ref(), pos.ref(),
                                        q_out.ref(), k_cache.ref(), v_cache.ref(), eps, n_dims, ROPE_NEOX, freq_base,
                                        freq_scale, 0.0, 1.0))
+
+    def attn_decode(self, q, k, v, q_norm, k_norm, pos, k_cache, v_cache, k_view, v_view, mask, dst, eps: float,
+                    freq_base: float, scale: float, n_dims: int = 128, freq_scale: float = 1.0) -> None:
+        """qk_norm_rope_kv then flash_attn_ext over the caches, for one decode row, in one launch."""
+        check(lib().mx_attn_decode(self.h, q.ref(), k.ref(), v.ref(), q_norm.ref(), k_norm.ref(), pos.ref(),
+                                   k_cache.ref(), v_cache.ref(), k_view.ref(), v_view.ref(),
+                                   mask.ref() if mask is not None else None, dst.ref(), eps, n_dims, ROPE_NEOX,
+                                   freq_base, freq_scale, 0.0, 1.0, scale))
 
     def rms_norm(self, src: Tensor, dst: Tensor, eps: float, w: Tensor | None = None) -> None:
         check(lib().mx_rms_norm(self.h, src.ref(), dst.ref(), eps, w.ref() if w is not None else None))

@@ -14,6 +14,11 @@
 #endif
 #include "mx_device.h"
 
+// No contraction of a * b + c into an fma unless written as fmaf: ggml-cpu forms RoPE's x0 cos - x1 sin (and the other
+// expressions here) with separate roundings, and the same expression inlined into two kernels must round alike (the
+// fused q / k post and attention kernels give the bits of the separate ones).
+#pragma clang fp contract(off)
+
 namespace mx {
 
 __device__ __forceinline__ double wave_sum_d(double v) {
@@ -161,6 +166,23 @@ __global__ __launch_bounds__(256) void k_set_rows_f16(RowsArgs a, const void *id
 // which are the NEOX pair l. Items 0 .. nq-1: q heads, normed (rms_norm then mul by q_norm), turned, written to
 // q_out; nq .. nq+nkv-1: k heads, normed with k_norm, turned, written to the f16 K cache at row pos; then the v heads
 // written to the V cache at row pos. Arithmetic as k_rms_norm, k_rope_neox and k_set_rows_f16 perform it.
+// One head of 128 (lane l holds channels l and l + 64, the NEOX pair l): rms_norm then mul by w, then RoPE at position
+// p; the arithmetic of k_rms_norm and k_rope_neox.
+__device__ __forceinline__ void qk_norm_rope(float x0, float x1, float w0, float w1, int64_t p, float eps,
+                                             float theta_scale, float freq_scale, int lane, float &o0, float &o1) {
+    double ss = (double)(x0 * x0) + (double)(x1 * x1);
+    ss = wave_sum_d(ss);
+    const float mean = (float)(ss / 128.0);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    const float y0 = (x0 * scale) * w0, y1 = (x1 * scale) * w1;
+    float theta = (float)p;
+    for (int j = 0; j < lane; j++) theta *= theta_scale;
+    const float t = freq_scale * theta;
+    const float c = cosf(t), s = sinf(t);
+    o0 = y0 * c - y1 * s;
+    o1 = y0 * s + y1 * c;
+}
+
 __global__ __launch_bounds__(256) void k_qkv_post(QkvPostArgs a) {
     const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6), r = blockIdx.y;
     const int lane = threadIdx.x & 63;
@@ -187,16 +209,8 @@ __global__ __launch_bounds__(256) void k_qkv_post(QkvPostArgs a) {
         dst[lane + 64] = f2h(x1);
         return;
     }
-    double ss = (double)(x0 * x0) + (double)(x1 * x1);
-    ss = wave_sum_d(ss);
-    const float mean = (float)(ss / 128.0);
-    const float scale = 1.0f / sqrtf(mean + a.eps);
-    const float y0 = (x0 * scale) * w0, y1 = (x1 * scale) * w1;
-    float theta = (float)p;
-    for (int j = 0; j < lane; j++) theta *= a.theta_scale;
-    const float t = a.freq_scale * theta;
-    const float c = cosf(t), s = sinf(t);
-    const float o0 = y0 * c - y1 * s, o1 = y0 * s + y1 * c;
+    float o0, o1;
+    qk_norm_rope(x0, x1, w0, w1, p, a.eps, a.theta_scale, a.freq_scale, lane, o0, o1);
     if (isq) {
         float *o = (float *)((uint8_t *)a.q_out + h * a.qo_nb1 + r * a.qo_nb2);
         o[lane] = o0;
@@ -415,8 +429,14 @@ __device__ __forceinline__ void fa_stage_load(FaStage &st, const FaArgs &a, cons
 // sum); one wave per head runs the online softmax over the chunk; and for P.V each thread owns a channel pair of one
 // head over PLEN positions, the position parts added at the end. The split count aims at MX_FA_GROUP_WGS workgroups:
 // at decode that is one chunk per workgroup, the fastest form measured (fewer, longer splits serialize their chunks).
-template <int G>
-__global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a) {
+//
+// POST (one query row): the q / k norms, RoPE and KV-cache stores of k_qkv_post run in the prologue, from the raw
+// q / k / v of pa (heads at pa.*_nb1): wave g turns q head hk G + g into qs; the workgroup whose split holds the new
+// position p (the last split when p lies past the positions read) turns kv head hk's key, stores key and value into
+// the caches at row p and stages them from LDS in place of that row's (not yet written) cache bytes. No other
+// workgroup reads row p, so the stores race with nothing.
+template <int G, bool POST>
+__global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a, QkvPostArgs pa) {
     constexpr int D = 128, T = 256 / (G * 64), CPT = D / T, PP = 256 / G / 64, PLEN = 64 / PP;
     constexpr int KS = D * 2 + 16;  // bytes per K row in LDS: padded so 16 rows read at one offset miss each other
     __shared__ __align__(16) uint8_t Ks[64 * KS];
@@ -433,10 +453,46 @@ __global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a) {
     const int lr = tid >> 4, seg = tid & 15;  // copy role: 16 threads per row, rows lr + 16 t, 16 bytes each
     FaStage st;
     if (j0 < j1) fa_stage_load(st, a, kb, vb, mrow, j0, j1, tid);  // the first chunk's loads go out before q's
-    for (int e = tid; e < G * D; e += 256) {
-        const int g = e / D, d = e % D;
-        const float *q = (const float *)((const uint8_t *)a.q + i * a.q_nb1 + (hk * G + g) * a.q_nb2);
-        qs[g][d] = h2f(f2h(q[d]));  // ggml converts q to K's f16 first
+    __shared__ __align__(16) uint16_t knew[POST ? D : 1], vnew[POST ? D : 1];
+    bool mine = false;  // POST: this workgroup stores (and reads from LDS) the new row p
+    int64_t p = -1;
+    if constexpr (!POST) {
+        for (int e = tid; e < G * D; e += 256) {
+            const int g = e / D, d = e % D;
+            const float *q = (const float *)((const uint8_t *)a.q + i * a.q_nb1 + (hk * G + g) * a.q_nb2);
+            qs[g][d] = h2f(f2h(q[d]));  // ggml converts q to K's f16 first
+        }
+    } else {
+        p = pa.pos[0];
+        const bool bad = p < 0 || p >= pa.cache_rows;  // nothing is stored at a bad row; q is still turned
+        mine = !bad && ((p >= j0 && p < j1) || (split == a.nsplit - 1 && p >= j1));
+        if (bad && split == 0 && hk == 0 && tid == 0) atomicOr(pa.err, 4);
+        if (wave < G) {
+            const float *x = (const float *)((const uint8_t *)pa.q + (hk * G + wave) * pa.q_nb1);
+            float o0, o1;
+            qk_norm_rope(x[lane], x[lane + 64], pa.qw[lane], pa.qw[lane + 64], p, pa.eps, pa.theta_scale,
+                         pa.freq_scale, lane, o0, o1);
+            qs[wave][lane] = h2f(f2h(o0));  // ggml converts q to K's f16 first
+            qs[wave][lane + 64] = h2f(f2h(o1));
+        }
+        if (mine && wave == (G & 3)) {  // a wave with no q head (wave 0 after its head when G = 4)
+            const float *x = (const float *)((const uint8_t *)pa.k + hk * pa.k_nb1);
+            const float *v = (const float *)((const uint8_t *)pa.v + hk * pa.v_nb1);
+            float o0, o1;
+            qk_norm_rope(x[lane], x[lane + 64], pa.kw[lane], pa.kw[lane + 64], p, pa.eps, pa.theta_scale,
+                         pa.freq_scale, lane, o0, o1);
+            const uint16_t k0 = f2h(o0), k1 = f2h(o1), v0 = f2h(v[lane]), v1 = f2h(v[lane + 64]);
+            uint16_t *kc = (uint16_t *)((uint8_t *)pa.kc + p * pa.kc_nb1) + hk * D;
+            uint16_t *vc = (uint16_t *)((uint8_t *)pa.vc + p * pa.vc_nb1) + hk * D;
+            kc[lane] = k0;
+            kc[lane + 64] = k1;
+            vc[lane] = v0;
+            vc[lane + 64] = v1;
+            knew[lane] = k0;
+            knew[lane + 64] = k1;
+            vnew[lane] = v0;
+            vnew[lane + 64] = v1;
+        }
     }
     if (tid < G) {
         hm[tid] = -INFINITY;
@@ -450,8 +506,13 @@ __global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a) {
         __syncthreads();  // the previous chunk is done with Ks, Vs, ps
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            *(u32x4 *)(Ks + (lr + 16 * t) * KS + 16 * seg) = st.k[t];
-            *(u32x4 *)(Vs + (lr + 16 * t) * 64 + 4 * seg) = st.v[t];
+            u32x4 kk = st.k[t], vv = st.v[t];
+            if (POST && mine && base + lr + 16 * t == p) {  // the new row, from the prologue
+                kk = *(const u32x4 *)(knew + 8 * seg);
+                vv = *(const u32x4 *)(vnew + 8 * seg);
+            }
+            *(u32x4 *)(Ks + (lr + 16 * t) * KS + 16 * seg) = kk;
+            *(u32x4 *)(Vs + (lr + 16 * t) * 64 + 4 * seg) = vv;
         }
         if (tid < 64) mvs[tid] = st.mv;
         __syncthreads();
@@ -601,9 +662,10 @@ hipError_t launch_flash_attn(const FaArgs &a, hipStream_t s) {
     if (a.n_q == 0 || a.n_head == 0) return hipSuccess;
     const dim3 g1((unsigned)a.nsplit, (unsigned)a.n_head, (unsigned)a.n_q);
     const dim3 gk((unsigned)a.nsplit, (unsigned)(a.n_head / a.gqa), (unsigned)a.n_q);
-    if (fa_grouped(a.D, a.gqa) && a.gqa == 2) hipLaunchKernelGGL(k_fa_gqa<2>, gk, dim3(256), 0, s, a);
-    else if (fa_grouped(a.D, a.gqa) && a.gqa == 1) hipLaunchKernelGGL(k_fa_gqa<1>, gk, dim3(256), 0, s, a);
-    else if (fa_grouped(a.D, a.gqa)) hipLaunchKernelGGL(k_fa_gqa<4>, gk, dim3(256), 0, s, a);
+    const QkvPostArgs none{};
+    if (fa_grouped(a.D, a.gqa) && a.gqa == 2) hipLaunchKernelGGL((k_fa_gqa<2, false>), gk, dim3(256), 0, s, a, none);
+    else if (fa_grouped(a.D, a.gqa) && a.gqa == 1) hipLaunchKernelGGL((k_fa_gqa<1, false>), gk, dim3(256), 0, s, a, none);
+    else if (fa_grouped(a.D, a.gqa)) hipLaunchKernelGGL((k_fa_gqa<4, false>), gk, dim3(256), 0, s, a, none);
     else if (a.D == 128) hipLaunchKernelGGL(k_fa_split<128>, g1, dim3(64), 0, s, a);
     else if (a.D == 64) hipLaunchKernelGGL(k_fa_split<64>, g1, dim3(64), 0, s, a);
     else return hipErrorInvalidValue;
@@ -612,6 +674,18 @@ hipError_t launch_flash_attn(const FaArgs &a, hipStream_t s) {
     const dim3 g2((unsigned)a.n_head, (unsigned)a.n_q);
     if (a.D == 128) hipLaunchKernelGGL(k_fa_merge<128>, g2, dim3(64), 0, s, a);
     else hipLaunchKernelGGL(k_fa_merge<64>, g2, dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_decode(const FaArgs &a, const QkvPostArgs &pa, hipStream_t s) {
+    if (a.n_q != 1 || !fa_grouped(a.D, a.gqa)) return hipErrorInvalidValue;
+    const dim3 gk((unsigned)a.nsplit, (unsigned)(a.n_head / a.gqa), 1);
+    if (a.gqa == 2) hipLaunchKernelGGL((k_fa_gqa<2, true>), gk, dim3(256), 0, s, a, pa);
+    else if (a.gqa == 1) hipLaunchKernelGGL((k_fa_gqa<1, true>), gk, dim3(256), 0, s, a, pa);
+    else hipLaunchKernelGGL((k_fa_gqa<4, true>), gk, dim3(256), 0, s, a, pa);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.nsplit == 1) return e;
+    hipLaunchKernelGGL(k_fa_merge<128>, dim3((unsigned)a.n_head, 1), dim3(64), 0, s, a);
     return hipGetLastError();
 }
 

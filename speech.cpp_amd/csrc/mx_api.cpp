@@ -907,13 +907,11 @@ MX_API int mx_set_rows(mx_backend *be, const mx_tensor *src, const mx_tensor *id
     return MX_SUCCESS;
 }
 
-MX_API int mx_qk_norm_rope_kv(mx_backend *be, const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
-                              const mx_tensor *q_norm, const mx_tensor *k_norm, const mx_tensor *pos,
-                              const mx_tensor *q_out, const mx_tensor *k_cache, const mx_tensor *v_cache, float eps,
-                              int n_dims, int mode, float freq_base, float freq_scale, float ext_factor,
-                              float attn_factor) {
-    int rc = check_be(be);
-    if (rc) return rc;
+// Validation and arguments of the q / k norm + RoPE + KV store step (mx_qk_norm_rope_kv; mx_attn_decode).
+static int qkv_post_args(mx_backend *be, const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
+                         const mx_tensor *q_norm, const mx_tensor *k_norm, const mx_tensor *pos, const mx_tensor *q_out,
+                         const mx_tensor *k_cache, const mx_tensor *v_cache, float eps, int n_dims, int mode,
+                         float freq_base, float freq_scale, float ext_factor, float attn_factor, mx::QkvPostArgs *a) {
     auto heads = [](const mx_tensor *t) { return f32_any(t) && t->ne[0] == 128 && t->ne[3] == 1; };
     auto cache = [](const mx_tensor *c, int64_t nkv) {
         return c && c->type == MX_TYPE_F16 && shape_ok(c) && c->nb[0] == 2 && c->data && ((uintptr_t)c->data & 1) == 0 &&
@@ -927,33 +925,46 @@ MX_API int mx_qk_norm_rope_kv(mx_backend *be, const mx_tensor *q, const mx_tenso
     if (!pos || pos->type != MX_TYPE_I32 || !pos->data || pos->nb[0] != 4 || pos->ne[0] != q->ne[2] ||
         nelements(pos) != pos->ne[0])
         return fail(MX_UNSUPPORTED, "q/k norm + RoPE + KV store: one I32 position per row");
+    a->q = (const float *)q->data;
+    a->k = (const float *)k->data;
+    a->v = (const float *)v->data;
+    a->qw = (const float *)q_norm->data;
+    a->kw = (const float *)k_norm->data;
+    a->pos = (const int32_t *)pos->data;
+    a->q_out = (float *)q_out->data;
+    a->kc = k_cache->data;
+    a->vc = v_cache->data;
+    a->nq = q->ne[1];
+    a->nkv = k->ne[1];
+    a->cache_rows = std::min(k_cache->ne[1], v_cache->ne[1]);
+    a->q_nb1 = (int64_t)q->nb[1];
+    a->q_nb2 = (int64_t)q->nb[2];
+    a->k_nb1 = (int64_t)k->nb[1];
+    a->k_nb2 = (int64_t)k->nb[2];
+    a->v_nb1 = (int64_t)v->nb[1];
+    a->v_nb2 = (int64_t)v->nb[2];
+    a->qo_nb1 = (int64_t)q_out->nb[1];
+    a->qo_nb2 = (int64_t)q_out->nb[2];
+    a->kc_nb1 = (int64_t)k_cache->nb[1];
+    a->vc_nb1 = (int64_t)v_cache->nb[1];
+    a->eps = eps;
+    a->theta_scale = powf(freq_base, -2.0f / (float)n_dims);  // as ggml-cpu forms it
+    a->freq_scale = freq_scale;
+    a->err = be->err;
+    return MX_SUCCESS;
+}
+
+MX_API int mx_qk_norm_rope_kv(mx_backend *be, const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
+                              const mx_tensor *q_norm, const mx_tensor *k_norm, const mx_tensor *pos,
+                              const mx_tensor *q_out, const mx_tensor *k_cache, const mx_tensor *v_cache, float eps,
+                              int n_dims, int mode, float freq_base, float freq_scale, float ext_factor,
+                              float attn_factor) {
+    int rc = check_be(be);
+    if (rc) return rc;
     mx::QkvPostArgs a{};
-    a.q = (const float *)q->data;
-    a.k = (const float *)k->data;
-    a.v = (const float *)v->data;
-    a.qw = (const float *)q_norm->data;
-    a.kw = (const float *)k_norm->data;
-    a.pos = (const int32_t *)pos->data;
-    a.q_out = (float *)q_out->data;
-    a.kc = k_cache->data;
-    a.vc = v_cache->data;
-    a.nq = q->ne[1];
-    a.nkv = k->ne[1];
-    a.cache_rows = std::min(k_cache->ne[1], v_cache->ne[1]);
-    a.q_nb1 = (int64_t)q->nb[1];
-    a.q_nb2 = (int64_t)q->nb[2];
-    a.k_nb1 = (int64_t)k->nb[1];
-    a.k_nb2 = (int64_t)k->nb[2];
-    a.v_nb1 = (int64_t)v->nb[1];
-    a.v_nb2 = (int64_t)v->nb[2];
-    a.qo_nb1 = (int64_t)q_out->nb[1];
-    a.qo_nb2 = (int64_t)q_out->nb[2];
-    a.kc_nb1 = (int64_t)k_cache->nb[1];
-    a.vc_nb1 = (int64_t)v_cache->nb[1];
-    a.eps = eps;
-    a.theta_scale = powf(freq_base, -2.0f / (float)n_dims);  // as ggml-cpu forms it
-    a.freq_scale = freq_scale;
-    a.err = be->err;
+    if ((rc = qkv_post_args(be, q, k, v, q_norm, k_norm, pos, q_out, k_cache, v_cache, eps, n_dims, mode, freq_base,
+                            freq_scale, ext_factor, attn_factor, &a)))
+        return rc;
     HIP_OK(mx::launch_qkv_post(a, q->ne[2], be->stream), "q/k norm + RoPE + KV store launch");
     return MX_SUCCESS;
 }
@@ -980,39 +991,78 @@ MX_API int mx_supports_flash_attn_ext(const mx_tensor *q, const mx_tensor *k, co
            dst->ne[3] == 1 && contiguous(dst) && dst->data && q->ne[1] <= 65535 && q->ne[2] <= 65535;
 }
 
+// Validation, arguments and scratch of an attention launch (mx_flash_attn_ext; mx_attn_decode).
+static int fa_args(mx_backend *be, const mx_tensor *q, const mx_tensor *k, const mx_tensor *v, const mx_tensor *mask,
+                   const mx_tensor *dst, float scale, mx::FaArgs *a) {
+    if (!mx_supports_flash_attn_ext(q, k, v, mask, dst, 0.0f, 0.0f))
+        return fail(MX_UNSUPPORTED, "FLASH_ATTN_EXT: unsupported tensors");
+    a->q = (const float *)q->data;
+    a->k = k->data;
+    a->v = v->data;
+    a->mask = mask ? mask->data : nullptr;
+    a->dst = (float *)dst->data;
+    a->D = (int)q->ne[0];
+    a->n_q = q->ne[1];
+    a->n_head = q->ne[2];
+    a->n_kv = k->ne[1];
+    a->gqa = q->ne[2] / k->ne[2];
+    a->q_nb1 = (int64_t)q->nb[1];
+    a->q_nb2 = (int64_t)q->nb[2];
+    a->k_nb1 = (int64_t)k->nb[1];
+    a->k_nb2 = (int64_t)k->nb[2];
+    a->v_nb1 = (int64_t)v->nb[1];
+    a->v_nb2 = (int64_t)v->nb[2];
+    a->m_nb1 = mask ? (int64_t)mask->nb[1] : 0;
+    a->scale = scale;
+    a->nsplit = mx::fa_splits(a->n_q, a->n_head, a->n_kv, a->gqa, a->D);
+    a->split_len = ((a->n_kv + 63) / 64 + a->nsplit - 1) / a->nsplit * 64;  // whole 64-position blocks per split
+    if (a->nsplit > 1) {
+        const size_t need = (size_t)a->n_q * (size_t)a->n_head * (size_t)a->nsplit * (size_t)(a->D + 2) * 4;
+        int rc = ensure_scratch(be, need);
+        if (rc) return rc;
+        a->part = (float *)be->scratch;
+    }
+    return MX_SUCCESS;
+}
+
 MX_API int mx_flash_attn_ext(mx_backend *be, const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
                              const mx_tensor *mask, const mx_tensor *dst, float scale) {
     int rc = check_be(be);
     if (rc) return rc;
-    if (!mx_supports_flash_attn_ext(q, k, v, mask, dst, 0.0f, 0.0f))
-        return fail(MX_UNSUPPORTED, "FLASH_ATTN_EXT: unsupported tensors");
     mx::FaArgs a{};
-    a.q = (const float *)q->data;
-    a.k = k->data;
-    a.v = v->data;
-    a.mask = mask ? mask->data : nullptr;
-    a.dst = (float *)dst->data;
-    a.D = (int)q->ne[0];
-    a.n_q = q->ne[1];
-    a.n_head = q->ne[2];
-    a.n_kv = k->ne[1];
-    a.gqa = q->ne[2] / k->ne[2];
-    a.q_nb1 = (int64_t)q->nb[1];
-    a.q_nb2 = (int64_t)q->nb[2];
-    a.k_nb1 = (int64_t)k->nb[1];
-    a.k_nb2 = (int64_t)k->nb[2];
-    a.v_nb1 = (int64_t)v->nb[1];
-    a.v_nb2 = (int64_t)v->nb[2];
-    a.m_nb1 = mask ? (int64_t)mask->nb[1] : 0;
-    a.scale = scale;
-    a.nsplit = mx::fa_splits(a.n_q, a.n_head, a.n_kv, a.gqa, a.D);
-    a.split_len = ((a.n_kv + 63) / 64 + a.nsplit - 1) / a.nsplit * 64;  // whole 64-position blocks per split
-    if (a.nsplit > 1) {
-        const size_t need = (size_t)a.n_q * (size_t)a.n_head * (size_t)a.nsplit * (size_t)(a.D + 2) * 4;
-        if ((rc = ensure_scratch(be, need))) return rc;
-        a.part = (float *)be->scratch;
-    }
+    if ((rc = fa_args(be, q, k, v, mask, dst, scale, &a))) return rc;
     HIP_OK(mx::launch_flash_attn(a, be->stream), "FLASH_ATTN_EXT launch");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_attn_decode(mx_backend *be, const mx_tensor *q, const mx_tensor *k, const mx_tensor *v,
+                          const mx_tensor *q_norm, const mx_tensor *k_norm, const mx_tensor *pos,
+                          const mx_tensor *k_cache, const mx_tensor *v_cache, const mx_tensor *k_view,
+                          const mx_tensor *v_view, const mx_tensor *mask, const mx_tensor *dst, float eps, int n_dims,
+                          int mode, float freq_base, float freq_scale, float ext_factor, float attn_factor,
+                          float scale) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    mx::QkvPostArgs pa{};
+    // the roped q is not written: q stands in for q_out in the checks
+    if ((rc = qkv_post_args(be, q, k, v, q_norm, k_norm, pos, q, k_cache, v_cache, eps, n_dims, mode, freq_base,
+                            freq_scale, ext_factor, attn_factor, &pa)))
+        return rc;
+    if (q->ne[2] != 1) return fail(MX_UNSUPPORTED, "fused attention: one decode row");
+    for (const mx_tensor *t : {k_view, v_view})
+        if (!t || t->ne[2] != k->ne[1] || t->nb[2] != 256) return fail(MX_UNSUPPORTED, "fused attention: cache views");
+    if (k_view->data != k_cache->data || v_view->data != v_cache->data || k_view->nb[1] != k_cache->nb[1] ||
+        v_view->nb[1] != v_cache->nb[1])
+        return fail(MX_UNSUPPORTED, "fused attention: the views must read the caches from row 0");
+    mx_tensor qa = *q;  // q as the attention reads it: [128, 1 row, heads]
+    qa.ne[1] = 1;
+    qa.ne[2] = q->ne[1];
+    qa.nb[1] = q->nb[2];
+    qa.nb[2] = q->nb[1];
+    mx::FaArgs a{};
+    if ((rc = fa_args(be, &qa, k_view, v_view, mask, dst, scale, &a))) return rc;
+    if (a.gqa != 1 && a.gqa != 2 && a.gqa != 4) return fail(MX_UNSUPPORTED, "fused attention: 1, 2 or 4 q heads per kv head");
+    HIP_OK(mx::launch_attn_decode(a, pa, be->stream), "fused attention launch");
     return MX_SUCCESS;
 }
 

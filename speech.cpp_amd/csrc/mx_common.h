@@ -300,6 +300,9 @@ struct QkvPostArgs {
 };
 hipError_t launch_qkv_post(const QkvPostArgs &a, int64_t rows, hipStream_t s);
 hipError_t launch_flash_attn(const FaArgs &a, hipStream_t s);
+// One decode row: launch_qkv_post and launch_flash_attn in one attention launch (head size 128, gqa 1, 2 or 4; the
+// attention reads the caches pa stores into).
+hipError_t launch_attn_decode(const FaArgs &a, const QkvPostArgs &pa, hipStream_t s);
 
 // ARGMAX (first of equal values) over nrows rows of ne0 floats (row stride nb1 bytes) into dst (stride dst_nb0 bytes).
 // Rows of more than 8192 floats split into argmax_parts(ne0, nrows) parts, whose (value, index) pairs go to scratch

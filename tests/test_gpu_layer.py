@@ -317,3 +317,53 @@ def test_fused_qk_norm_rope_kv_equals_the_separate_ops(mx, be):
     assert np.array_equal(VC2.get_bytes(), VC.get_bytes())
     ref_q = O.rope_neox(O.binary("mul", O.rms_norm(q.reshape(1, nq, hd), eps), qw), pos, hd, theta)
     assert np.abs(qo.numpy().reshape(1, nq, hd) - ref_q).max() <= 2e-6
+
+
+@pytest.mark.parametrize("nq,nkv,p,n_kv", [
+    (16, 8, 1000, 1088),   # a 0.6B decode step: the new row inside the last split
+    (8, 8, 63, 64),        # one q head per kv head, the new row last of a single chunk
+    (16, 4, 130, 256),     # four q heads per kv head, the new row first of the third chunk
+    (16, 8, 300, 256),     # the new row past the positions read: stored, not attended
+])
+def test_attn_decode_equals_the_separate_ops(mx, be, nq, nkv, p, n_kv):
+    """mx_attn_decode gives the bits of mx_qk_norm_rope_kv followed by mx_flash_attn_ext: the output and both
+    caches."""
+    hd, cap, eps, theta = 128, 320 if n_kv < 320 else 1280, 1e-6, 1e6
+    kv_dim = nkv * hd
+    seed = 0x4C00 + nq + nkv + p
+    q = O.fill_normal(seed, 1, nq * hd) * np.float32(2)
+    k = O.fill_normal(seed + 1, 1, kv_dim)
+    v = O.fill_normal(seed + 2, 1, kv_dim)
+    qw, kw = O.fill_normal(seed + 3, 1, hd, 1.0, 0.1)[0], O.fill_normal(seed + 4, 1, hd, 1.0, 0.1)[0]
+    pos = np.array([p], np.int32)
+    cache0 = O.fill_normal(seed + 5, cap, kv_dim).astype(np.float16).view(np.uint16)
+    m = np.zeros((1, n_kv), np.float32)
+    m[0, p + 1:] = -np.inf
+    mask = m.astype(np.float16).view(np.uint16)
+    Q, K, V, QW, KW, P = dev(mx, be, q), dev(mx, be, k), dev(mx, be, v), dev(mx, be, qw), dev(mx, be, kw), \
+        dev(mx, be, pos, mx.I32)
+    M = dev(mx, be, mask, mx.F16)
+    qv = Q.view((hd, nq, 1), (4, hd * 4, nq * hd * 4))
+    kv = K.view((hd, nkv, 1), (4, hd * 4, kv_dim * 4))
+    vv = V.view((hd, nkv, 1), (4, hd * 4, kv_dim * 4))
+    scale = 1.0 / np.sqrt(hd)
+
+    def views(KC, VC):
+        return (KC.view((hd, n_kv, nkv), (2, kv_dim * 2, hd * 2)), VC.view((hd, n_kv, nkv), (2, kv_dim * 2, hd * 2)))
+
+    KC, VC = dev(mx, be, cache0, mx.F16), dev(mx, be, cache0, mx.F16)
+    qo = be.tensor(mx.F32, (hd, nq, 1))
+    Y = be.tensor(mx.F32, (hd, nq, 1))
+    be.qk_norm_rope_kv(qv, kv, vv, QW, KW, P, qo, KC, VC, eps, theta)
+    kh, vh = views(KC, VC)
+    be.flash_attn_ext(qo.view((hd, 1, nq), (4, nq * hd * 4, hd * 4)), kh, vh, M, Y, scale)
+    KC2, VC2 = dev(mx, be, cache0, mx.F16), dev(mx, be, cache0, mx.F16)
+    Y2 = be.tensor(mx.F32, (hd, nq, 1))
+    kh2, vh2 = views(KC2, VC2)
+    be.attn_decode(qv, kv, vv, QW, KW, P, KC2, VC2, kh2, vh2, M, Y2, eps, theta, scale)
+    be.sync()
+    assert np.array_equal(KC2.get_bytes(), KC.get_bytes())
+    assert np.array_equal(VC2.get_bytes(), VC.get_bytes())
+    y, y2 = Y.numpy().reshape(nq, hd), Y2.numpy().reshape(nq, hd)
+    diff = np.argwhere(y.view(np.uint32) != y2.view(np.uint32))
+    assert len(diff) == 0, (len(diff), diff[:8].tolist(), float(np.abs(y - y2).max()))
