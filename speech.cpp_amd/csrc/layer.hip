@@ -175,8 +175,12 @@ __device__ __forceinline__ void qk_norm_rope(float x0, float x1, float w0, float
     const float mean = (float)(ss / 128.0);
     const float scale = 1.0f / sqrtf(mean + eps);
     const float y0 = (x0 * scale) * w0, y1 = (x1 * scale) * w1;
-    float theta = (float)p;
-    for (int j = 0; j < lane; j++) theta *= theta_scale;
+    float theta = (float)p;  // the chain p * theta_scale ... (lane factors), unrolled and branch-free
+#pragma unroll
+    for (int j = 0; j < 63; j++) {
+        const float next = theta * theta_scale;
+        theta = j < lane ? next : theta;
+    }
     const float t = freq_scale * theta;
     const float c = cosf(t), s = sinf(t);
     o0 = y0 * c - y1 * s;
@@ -451,37 +455,52 @@ __global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a, QkvPostArgs pa) {
     const uint16_t *mrow = a.mask ? (const uint16_t *)((const uint8_t *)a.mask + i * a.m_nb1) : nullptr;
     const int64_t j0 = split * a.split_len, j1 = min(a.n_kv, j0 + a.split_len);
     const int lr = tid >> 4, seg = tid & 15;  // copy role: 16 threads per row, rows lr + 16 t, 16 bytes each
-    FaStage st;
-    if (j0 < j1) fa_stage_load(st, a, kb, vb, mrow, j0, j1, tid);  // the first chunk's loads go out before q's
     __shared__ __align__(16) uint16_t knew[POST ? D : 1], vnew[POST ? D : 1];
     bool mine = false;  // POST: this workgroup stores (and reads from LDS) the new row p
     int64_t p = -1;
+    float hx0 = 0.f, hx1 = 0.f, hw0 = 0.f, hw1 = 0.f, kx0 = 0.f, kx1 = 0.f, kw0 = 0.f, kw1 = 0.f, v0f = 0.f, v1f = 0.f;
+    if constexpr (POST) {  // the raw heads' loads go out first: the prologue works on them while the chunk loads
+        p = pa.pos[0];
+        const bool bad = p < 0 || p >= pa.cache_rows;
+        mine = !bad && ((p >= j0 && p < j1) || (split == a.nsplit - 1 && p >= j1));
+        if (wave < G) {
+            const float *x = (const float *)((const uint8_t *)pa.q + (hk * G + wave) * pa.q_nb1);
+            hx0 = x[lane];
+            hx1 = x[lane + 64];
+            hw0 = pa.qw[lane];
+            hw1 = pa.qw[lane + 64];
+        }
+        if (mine && wave == (G & 3)) {
+            const float *x = (const float *)((const uint8_t *)pa.k + hk * pa.k_nb1);
+            const float *v = (const float *)((const uint8_t *)pa.v + hk * pa.v_nb1);
+            kx0 = x[lane];
+            kx1 = x[lane + 64];
+            kw0 = pa.kw[lane];
+            kw1 = pa.kw[lane + 64];
+            v0f = v[lane];
+            v1f = v[lane + 64];
+        }
+        if (bad && split == 0 && hk == 0 && tid == 0) atomicOr(pa.err, 4);
+    }
+    FaStage st;
+    if (j0 < j1) fa_stage_load(st, a, kb, vb, mrow, j0, j1, tid);  // the first chunk's loads go out before q's
     if constexpr (!POST) {
         for (int e = tid; e < G * D; e += 256) {
             const int g = e / D, d = e % D;
             const float *q = (const float *)((const uint8_t *)a.q + i * a.q_nb1 + (hk * G + g) * a.q_nb2);
             qs[g][d] = h2f(f2h(q[d]));  // ggml converts q to K's f16 first
         }
-    } else {
-        p = pa.pos[0];
-        const bool bad = p < 0 || p >= pa.cache_rows;  // nothing is stored at a bad row; q is still turned
-        mine = !bad && ((p >= j0 && p < j1) || (split == a.nsplit - 1 && p >= j1));
-        if (bad && split == 0 && hk == 0 && tid == 0) atomicOr(pa.err, 4);
+    } else {  // nothing is stored at a bad row; q is still turned
         if (wave < G) {
-            const float *x = (const float *)((const uint8_t *)pa.q + (hk * G + wave) * pa.q_nb1);
             float o0, o1;
-            qk_norm_rope(x[lane], x[lane + 64], pa.qw[lane], pa.qw[lane + 64], p, pa.eps, pa.theta_scale,
-                         pa.freq_scale, lane, o0, o1);
+            qk_norm_rope(hx0, hx1, hw0, hw1, p, pa.eps, pa.theta_scale, pa.freq_scale, lane, o0, o1);
             qs[wave][lane] = h2f(f2h(o0));  // ggml converts q to K's f16 first
             qs[wave][lane + 64] = h2f(f2h(o1));
         }
         if (mine && wave == (G & 3)) {  // a wave with no q head (wave 0 after its head when G = 4)
-            const float *x = (const float *)((const uint8_t *)pa.k + hk * pa.k_nb1);
-            const float *v = (const float *)((const uint8_t *)pa.v + hk * pa.v_nb1);
             float o0, o1;
-            qk_norm_rope(x[lane], x[lane + 64], pa.kw[lane], pa.kw[lane + 64], p, pa.eps, pa.theta_scale,
-                         pa.freq_scale, lane, o0, o1);
-            const uint16_t k0 = f2h(o0), k1 = f2h(o1), v0 = f2h(v[lane]), v1 = f2h(v[lane + 64]);
+            qk_norm_rope(kx0, kx1, kw0, kw1, p, pa.eps, pa.theta_scale, pa.freq_scale, lane, o0, o1);
+            const uint16_t k0 = f2h(o0), k1 = f2h(o1), v0 = f2h(v0f), v1 = f2h(v1f);
             uint16_t *kc = (uint16_t *)((uint8_t *)pa.kc + p * pa.kc_nb1) + hk * D;
             uint16_t *vc = (uint16_t *)((uint8_t *)pa.vc + p * pa.vc_nb1) + hk * D;
             kc[lane] = k0;
