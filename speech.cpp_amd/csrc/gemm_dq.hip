@@ -482,8 +482,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             const uint32_t d = sdst[jj] + (sdst[jj] < (uint32_t)L::JUNK ? slot * BN * 4 : 0);
             __builtin_amdgcn_global_load_lds((const void *)(ssrc[jj] + soff), (dq_lds *)(smem + d), 4, 0, 0);
         }
+        // d: the 4-byte-aligned pair of fp16 d holding this row's (which half: convert). When the plane holds an odd
+        // number of d, the last pair runs 2 bytes past them -- inside the plane's padding to 256 bytes, which an odd
+        // count of 2-byte values never fills exactly.
 #pragma unroll
-        for (int jj = 0; jj < L::PD; jj++) {  // the aligned pair of fp16 d holding this row's (which half: convert)
+        for (int jj = 0; jj < L::PD; jj++) {
             const uint32_t d = ddst[jj] + (ddst[jj] < (uint32_t)L::JUNK ? slot * BN * 4 : 0);
             const int64_t e = dsb[jj] + (g >> 2);
             __builtin_amdgcn_global_load_lds((const void *)(p.w.p3 + (e >> 1) * 4), (dq_lds *)(smem + d), 4, 0, 0);
