@@ -367,3 +367,31 @@ def test_attn_decode_equals_the_separate_ops(mx, be, nq, nkv, p, n_kv):
     y, y2 = Y.numpy().reshape(nq, hd), Y2.numpy().reshape(nq, hd)
     diff = np.argwhere(y.view(np.uint32) != y2.view(np.uint32))
     assert len(diff) == 0, (len(diff), diff[:8].tolist(), float(np.abs(y - y2).max()))
+
+
+def test_attn_decode_unsupported_forms(mx, be):
+    """Two rows, views that do not start at cache row 0, or a group of three q heads per kv head: MX_UNSUPPORTED
+    (the caller runs mx_qk_norm_rope_kv and mx_flash_attn_ext instead); nothing is launched."""
+    hd, nkv, cap, n_kv = 128, 2, 128, 64
+    kv_dim = nkv * hd
+    L = mx.lib()
+
+    def case(nq, rows, view_row0):
+        Q = be.tensor(mx.F32, (hd, nq, rows))
+        K = be.tensor(mx.F32, (hd, nkv, rows))
+        V = be.tensor(mx.F32, (hd, nkv, rows))
+        W = be.tensor(mx.F32, (hd,))
+        P = be.tensor(mx.I32, (rows,), np.arange(rows, dtype=np.int32))
+        KC, VC = be.tensor(mx.F16, (kv_dim, cap)), be.tensor(mx.F16, (kv_dim, cap))
+        off = view_row0 * kv_dim * 2
+        kh = KC.view((hd, n_kv, nkv), (2, kv_dim * 2, hd * 2), off)
+        vh = VC.view((hd, n_kv, nkv), (2, kv_dim * 2, hd * 2), off)
+        Y = be.tensor(mx.F32, (hd, nq, rows))
+        return L.mx_attn_decode(be.h, Q.ref(), K.ref(), V.ref(), W.ref(), W.ref(), P.ref(), KC.ref(), VC.ref(),
+                                kh.ref(), vh.ref(), None, Y.ref(), 1e-6, 128, mx.ROPE_NEOX, 1e6, 1.0, 0.0, 1.0, 0.1)
+
+    assert case(4, 1, 0) == 0            # the supported form, for contrast (no mask: every position visible)
+    assert case(4, 2, 0) == mx.UNSUPPORTED
+    assert case(4, 1, 8) == mx.UNSUPPORTED
+    assert case(6, 1, 0) == mx.UNSUPPORTED
+    be.sync()
