@@ -20,6 +20,7 @@
 // cannot see which stage a copy went to, and would otherwise wait for every copy in flight.
 #include "mx_common.h"
 #include "mx_device.h"
+#include "mx_dot.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -46,19 +47,24 @@ constexpr int DQ_NS = 4;   // ring stages (copies run DQ_NS - 1 stages ahead)
 // different chunks (all 32 banks of a 128-byte cycle), and 16 consecutive rows cover all 64 banks of a 256-byte one.
 template <int WT, int BM, int BN, int NW>
 struct DqLds {
-    static constexpr bool K6 = WT == MX_TYPE_Q6_K;
+    static constexpr bool K6 = WT == MX_TYPE_Q6_K, K5 = WT == MX_TYPE_Q5_K;
+    // raw bytes per weight row and stage: codes (Q8_0 codes, Q6_K ql, Q5_K qs), qh, scales, d
+    static constexpr int RB = K5 ? 32 : 64, HB = K6 || K5 ? 32 : 0, SB = K5 ? 12 : 4, DB = K6 || K5 ? 4 : 0;
     static constexpr int A = 0;                            // [stage][BM][128 B] activations
     static constexpr int BH = A + DQ_NS * BM * 128;        // [2][BN][128 B] dequantized weights
-    static constexpr int RAW = BH + 2 * BN * 128;          // [stage][BN][64 B] codes (Q8_0) / ql bytes (Q6_K)
-    static constexpr int QH = RAW + DQ_NS * BN * 64;       // [stage][BN][32 B] qh bytes (Q6_K)
-    static constexpr int SC = QH + (K6 ? DQ_NS * BN * 32 : 0);  // [stage][BN][4 B] two fp16 scales / four int8 scales
-    static constexpr int DD = SC + DQ_NS * BN * 4;         // [stage][BN][4 B] the fp16 d pair holding the row's (Q6_K)
-    static constexpr int JUNK = DD + (K6 ? DQ_NS * BN * 4 : 0);  // [wave][1 KB] where copies beyond a tile's need land
+    static constexpr int RAW = BH + 2 * BN * 128;          // [stage][BN][RB] codes
+    static constexpr int QH = RAW + DQ_NS * BN * RB;       // [stage][BN][HB] qh bytes
+    static constexpr int SC = QH + DQ_NS * BN * HB;        // [stage][BN][SB] scales (Q8_0 two fp16, Q6_K four int8,
+                                                           // Q5_K the 12 packed bytes)
+    static constexpr int DD = SC + DQ_NS * BN * SB;        // [stage][BN][DB] Q6_K: the fp16 d pair holding the row's;
+                                                           // Q5_K: d | dmin
+    static constexpr int JUNK = DD + DQ_NS * BN * DB;      // [wave][1 KB] where copies beyond a tile's need land
     static constexpr int RS = JUNK + NW * 1024;            // [BM] the tile rows' 2^-e
     static constexpr int SIZE = RS + BM * 4;
-    // copy instructions per stage (64 lanes each): activation rows (16 B), code rows (16 B), qh rows (16 B), scales
-    // (4 B), d (4 B), and per wave
-    static constexpr int NA = BM / 8, NC = BN / 16, NH = K6 ? BN / 32 : 0, NS4 = BN / 64, ND = K6 ? BN / 64 : 0;
+    // copy instructions per stage (64 lanes each): activation rows (16 B), code rows (16 B), qh rows (16 B), scale
+    // words (4 B), d words (4 B), and per wave
+    static constexpr int NA = BM / 8, NC = BN * RB / 1024, NH = BN * HB / 1024, NS4 = BN * SB / 256,
+                         ND = BN * DB / 256;
     static constexpr int PA = (NA + NW - 1) / NW, PC = (NC + NW - 1) / NW, PH = (NH + NW - 1) / NW;
     static constexpr int PS = (NS4 + NW - 1) / NW, PD = (ND + NW - 1) / NW;
     static constexpr int OPS = PA + PC + PH + PS + PD;  // vector memory ops per wave and stage
@@ -295,6 +301,30 @@ __device__ __forceinline__ void dq_q6_k_16(v4i ql, v4i qh, int hs, int ls, int s
     o1 = v4i{r[4], r[5], r[6], r[7]};
 }
 
+// 16 Q5_K codes of sub-block `sub`: code t = ((qs_t >> ls) & 15) | (((qh_t >> sub) & 1) << 4), value
+// d sc code - dmin m as ggml's dequantize_row_q5_K forms it in fp32 (d sc code and dmin m are exact products, one
+// rounding in the difference), then rounded once to fp16.
+__device__ __forceinline__ void dq_q5_k_16(v4i qs, v4i qh, int sub, int ls, int sc, int m, uint32_t dm, v4i &o0,
+                                           v4i &o1) {
+    const float d1 = h2f((uint16_t)(dm & 0xFFFF)) * (float)sc, m1 = h2f((uint16_t)(dm >> 16)) * (float)m;
+    const uint32_t lw[4] = {(uint32_t)qs.x, (uint32_t)qs.y, (uint32_t)qs.z, (uint32_t)qs.w};
+    const uint32_t hw[4] = {(uint32_t)qh.x, (uint32_t)qh.y, (uint32_t)qh.z, (uint32_t)qh.w};
+    int r[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t c = ((lw[k] >> ls) & 0x0F0F0F0Fu) | (((hw[k] >> sub) & 0x01010101u) << 4);
+        v2h lo, hi;
+        lo.x = (_Float16)(d1 * (float)(c & 0xFF) - m1);
+        lo.y = (_Float16)(d1 * (float)((c >> 8) & 0xFF) - m1);
+        hi.x = (_Float16)(d1 * (float)((c >> 16) & 0xFF) - m1);
+        hi.y = (_Float16)(d1 * (float)(c >> 24) - m1);
+        r[2 * k] = __builtin_bit_cast(int, lo);
+        r[2 * k + 1] = __builtin_bit_cast(int, hi);
+    }
+    o0 = v4i{r[0], r[1], r[2], r[3]};
+    o1 = v4i{r[4], r[5], r[6], r[7]};
+}
+
 // NF fragment reads (4, 6, 8, 12 or 16) and the wait for them.
 template <int NF>
 __device__ __forceinline__ void dq_read(v8h (&f)[16], const uint32_t (&a)[16]) {
@@ -424,9 +454,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     uint32_t cdst[L::PC];
 #pragma unroll
     for (int jj = 0; jj < L::PC; jj++) {
-        const int j = wave * L::PC + jj, row = 16 * min(j, L::NC - 1) + (lane >> 2);
+        constexpr int LR = L::RB / 16;  // lanes per code row
+        const int j = wave * L::PC + jj, row = (64 / LR) * min(j, L::NC - 1) + lane / LR;
         const int64_t grow = min(n0 + row, N - 1);
-        csrc[jj] = (L::K6 ? p.w.p0 + grow * nsb * 128 : p.w.p0 + grow * K + sb * DQ_KS) + 16 * (lane & 3);
+        csrc[jj] = (L::K6 || L::K5 ? p.w.p0 + grow * nsb * 128 : p.w.p0 + grow * K + sb * DQ_KS) + 16 * (lane % LR);
         cdst[jj] = j < L::NC ? L::RAW + j * 1024 : L::JUNK + wave * 1024;
     }
     const uint8_t *hsrc[L::PH > 0 ? L::PH : 1];
@@ -434,16 +465,21 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
 #pragma unroll
     for (int jj = 0; jj < L::PH; jj++) {
         const int j = wave * L::PH + jj, row = 32 * min(j, L::NH - 1) + (lane >> 1);
-        hsrc[jj] = p.w.p1 + (int64_t)min(n0 + row, N - 1) * nsb * 64 + 16 * (lane & 1);
+        hsrc[jj] = p.w.p1 + (int64_t)min(n0 + row, N - 1) * nsb * (L::K5 ? 32 : 64) + 16 * (lane & 1);
         hdst[jj] = j < L::NH ? L::QH + j * 1024 : L::JUNK + wave * 1024;
     }
     const uint8_t *ssrc[L::PS];
     uint32_t sdst[L::PS];
 #pragma unroll
     for (int jj = 0; jj < L::PS; jj++) {
-        const int j = wave * L::PS + jj, row = 64 * min(j, L::NS4 - 1) + lane;
-        const int64_t grow = min(n0 + row, N - 1);
-        ssrc[jj] = L::K6 ? p.w.p2 + grow * nsb * 16 : p.w.p1 + grow * nblk * 2 + sb * 4;
+        const int j = wave * L::PS + jj, wd = 64 * min(j, L::NS4 - 1) + lane;  // scale word wd of the stage
+        if constexpr (L::K5) {  // word c of row wd / 3's 12 bytes
+            const int64_t grow = min(n0 + wd / 3, N - 1);
+            ssrc[jj] = p.w.p2 + grow * nsb * 12 + 4 * (wd % 3);
+        } else {
+            const int64_t grow = min(n0 + wd, N - 1);
+            ssrc[jj] = L::K6 ? p.w.p2 + grow * nsb * 16 : p.w.p1 + grow * nblk * 2 + sb * 4;
+        }
         sdst[jj] = j < L::NS4 ? L::SC + j * 256 : L::JUNK + wave * 1024;
     }
     int64_t dsb[L::PD > 0 ? L::PD : 1];  // the row's first super-block index in the d plane
@@ -463,23 +499,26 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             const uint32_t d = adst[jj] + (adst[jj] < (uint32_t)L::JUNK ? slot * BM * 128 : 0);
             __builtin_amdgcn_global_load_lds((const void *)(asrc[jj] + t * DQ_KS), (dq_lds *)(smem + d), 16, 0, 0);
         }
-        // Q6_K: stage g is quarter g & 3 of super-block g >> 2; both quarters of a half read the half's ql and qh
-        const int coff = L::K6 ? (g >> 2) * 128 + ((g >> 1) & 1) * 64 : t * DQ_KS;
+        // K-quants: stage g is quarter g & 3 of super-block g >> 2. Q6_K: both quarters of a half read the half's ql
+        // and qh; Q5_K: the quarter's 32 qs bytes and the super-block's 32 qh bytes
+        const int coff = L::K6   ? (g >> 2) * 128 + ((g >> 1) & 1) * 64
+                         : L::K5 ? (g >> 2) * 128 + (g & 3) * 32
+                                 : t * DQ_KS;
 #pragma unroll
         for (int jj = 0; jj < L::PC; jj++) {
-            const uint32_t d = cdst[jj] + (cdst[jj] < (uint32_t)L::JUNK ? slot * BN * 64 : 0);
+            const uint32_t d = cdst[jj] + (cdst[jj] < (uint32_t)L::JUNK ? slot * BN * L::RB : 0);
             __builtin_amdgcn_global_load_lds((const void *)(csrc[jj] + coff), (dq_lds *)(smem + d), 16, 0, 0);
         }
 #pragma unroll
         for (int jj = 0; jj < L::PH; jj++) {
-            const uint32_t d = hdst[jj] + (hdst[jj] < (uint32_t)L::JUNK ? slot * BN * 32 : 0);
-            __builtin_amdgcn_global_load_lds((const void *)(hsrc[jj] + (g >> 2) * 64 + ((g >> 1) & 1) * 32),
-                                             (dq_lds *)(smem + d), 16, 0, 0);
+            const uint32_t d = hdst[jj] + (hdst[jj] < (uint32_t)L::JUNK ? slot * BN * L::HB : 0);
+            const int hoff = L::K5 ? (g >> 2) * 32 : (g >> 2) * 64 + ((g >> 1) & 1) * 32;
+            __builtin_amdgcn_global_load_lds((const void *)(hsrc[jj] + hoff), (dq_lds *)(smem + d), 16, 0, 0);
         }
-        const int soff = L::K6 ? (g >> 2) * 16 + (g & 3) * 4 : t * 4;
+        const int soff = L::K6 ? (g >> 2) * 16 + (g & 3) * 4 : L::K5 ? (g >> 2) * 12 : t * 4;
 #pragma unroll
         for (int jj = 0; jj < L::PS; jj++) {
-            const uint32_t d = sdst[jj] + (sdst[jj] < (uint32_t)L::JUNK ? slot * BN * 4 : 0);
+            const uint32_t d = sdst[jj] + (sdst[jj] < (uint32_t)L::JUNK ? slot * BN * L::SB : 0);
             __builtin_amdgcn_global_load_lds((const void *)(ssrc[jj] + soff), (dq_lds *)(smem + d), 4, 0, 0);
         }
         // d: the 4-byte-aligned pair of fp16 d holding this row's (which half: convert). When the plane holds an odd
@@ -489,7 +528,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
         for (int jj = 0; jj < L::PD; jj++) {
             const uint32_t d = ddst[jj] + (ddst[jj] < (uint32_t)L::JUNK ? slot * BN * 4 : 0);
             const int64_t e = dsb[jj] + (g >> 2);
-            __builtin_amdgcn_global_load_lds((const void *)(p.w.p3 + (e >> 1) * 4), (dq_lds *)(smem + d), 4, 0, 0);
+            const uint8_t *src = L::K5 ? p.w.p3 + e * 4 : p.w.p3 + (e >> 1) * 4;
+            __builtin_amdgcn_global_load_lds((const void *)src, (dq_lds *)(smem + d), 4, 0, 0);
         }
     };
 
@@ -500,10 +540,30 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
 #pragma unroll
         for (int u = tid; u < BN * 4; u += NT) {
             const int row = u >> 2, q = u & 3;
-            const uint32_t raw = lds + L::RAW + slot * BN * 64 + row * 64 + 16 * q;
-            const uint32_t sc = lds + L::SC + slot * BN * 4 + row * 4;
+            const uint32_t raw = lds + L::RAW + slot * BN * L::RB + row * L::RB + 16 * (L::K5 ? (q & 1) : q);
+            const uint32_t sc = lds + L::SC + slot * BN * L::SB + row * L::SB;
             v4i o[2];
-            if constexpr (!L::K6) {  // Q8_0: quarter q is half of block q >> 1
+            if constexpr (L::K5) {  // Q5_K: sub-block 2 (g & 3) + (q >> 1): codes 16 (q & 1) .. of its 32
+                const uint32_t qh = lds + L::QH + slot * BN * 32 + row * 32 + 16 * (q & 1);
+                const uint32_t dd = lds + L::DD + slot * BN * 4 + row * 4;
+                v4i l0, h0;
+                uint32_t s0, s1, s2, dw;
+                asm volatile(
+                    "ds_read_b128 %0, %6\n"
+                    "ds_read_b128 %1, %7\n"
+                    "ds_read_b32 %2, %8\n"
+                    "ds_read_b32 %3, %8 offset:4\n"
+                    "ds_read_b32 %4, %8 offset:8\n"
+                    "ds_read_b32 %5, %9\n"
+                    "s_waitcnt lgkmcnt(0)"
+                    : "=&v"(l0), "=&v"(h0), "=&v"(s0), "=&v"(s1), "=&v"(s2), "=&v"(dw)
+                    : "v"(raw), "v"(qh), "v"(sc), "v"(dd)
+                    : "memory");
+                const int sub = 2 * (g & 3) + (q >> 1);
+                int scv, mv;
+                q4k_scale_min(s0, s1, s2, sub, scv, mv);
+                dq_q5_k_16(l0, h0, sub, 4 * (q >> 1), scv, mv, dw, o[0], o[1]);
+            } else if constexpr (!L::K6) {  // Q8_0: quarter q is half of block q >> 1
                 v4i c0;
                 uint32_t sw;
                 asm volatile(
@@ -673,7 +733,8 @@ bool gemm_dq_supported(int type, int64_t M, int64_t K) {
         const char *e = getenv("MX_GEMM_DQ");
         return e && e[0] == '0';
     }();
-    return !off && ((type == MX_TYPE_Q8_0 && K % DQ_KS == 0) || (type == MX_TYPE_Q6_K && K % 256 == 0)) &&
+    return !off &&
+           ((type == MX_TYPE_Q8_0 && K % DQ_KS == 0) || ((type == MX_TYPE_Q6_K || type == MX_TYPE_Q5_K) && K % 256 == 0)) &&
            M * K < ((int64_t)1 << 31) && K < (1 << 24);
 }
 
@@ -749,7 +810,7 @@ hipError_t launch_gemm_dq_act(int type, int rounding, const float *x, int64_t x_
     if (type == MX_TYPE_Q8_0) {
         hipLaunchKernelGGL(k_dq_act_q8_0, dim3((unsigned)M), dim3(DQ_ACT_NT), 0, s, x, x_stride, (int)K, rounding,
                            (_Float16 *)xh, rs);
-    } else if (type == MX_TYPE_Q6_K && K % 256 == 0) {  // Q8_K has one rounding form
+    } else if ((type == MX_TYPE_Q6_K || type == MX_TYPE_Q5_K) && K % 256 == 0) {  // Q8_K has one rounding form
         hipLaunchKernelGGL(k_dq_act_q8k, dim3((unsigned)M), dim3(DQ_ACT_NT), 0, s, x, x_stride, (int)K, (_Float16 *)xh,
                            rs);
     } else {
@@ -802,8 +863,9 @@ hipError_t launch_gemm_dq(int type, int nprob, const WPlanes *w, const int64_t *
     a.nsplit = pl.nsplit;
     a.ntot = (int)pl.ntot;
     a.ws = (float *)((uint8_t *)scratch + dq_ws_offset(M, K));
-    const hipError_t e = type == MX_TYPE_Q8_0 ? launch_dq_type<MX_TYPE_Q8_0>(a, pl, (int)maxN, s)
-                                              : launch_dq_type<MX_TYPE_Q6_K>(a, pl, (int)maxN, s);
+    const hipError_t e = type == MX_TYPE_Q8_0   ? launch_dq_type<MX_TYPE_Q8_0>(a, pl, (int)maxN, s)
+                         : type == MX_TYPE_Q6_K ? launch_dq_type<MX_TYPE_Q6_K>(a, pl, (int)maxN, s)
+                                                : launch_dq_type<MX_TYPE_Q5_K>(a, pl, (int)maxN, s);
     if (e != hipSuccess || pl.nsplit == 1) return e;
     bool v4 = true;
     for (int i = 0; i < nprob; i++) v4 = v4 && N[i] % 4 == 0 && ldy[i] % 4 == 0 && (uintptr_t)y[i] % 16 == 0;

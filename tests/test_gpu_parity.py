@@ -20,7 +20,7 @@ DQ = __import__("os").environ.get("MX_GEMM_DQ", "1") != "0"
 
 def uses_dq(t, M, K):
     """Whether MUL_MAT takes the dequantizing fp16 GEMM (its dispatch rule)."""
-    return DQ and M > 8 and ((t == O.TYPE_Q8_0 and K % 64 == 0) or (t == O.TYPE_Q6_K and K % 256 == 0))
+    return DQ and M > 8 and ((t == O.TYPE_Q8_0 and K % 64 == 0) or (t in (O.TYPE_Q5_K, O.TYPE_Q6_K) and K % 256 == 0))
 
 
 def check_product(t, w, x, y, K, rounding=O.ROUND_REF):
@@ -394,7 +394,8 @@ def test_mul_mat_gemm_group_q8_0_split(mx, be):
 
 
 @pytest.mark.parametrize("t,M,Ns,K", [(O.TYPE_Q8_0, 160, [3000], 4096), (O.TYPE_Q6_K, 160, [3000], 4096),
-                                      (O.TYPE_Q8_0, 140, [1024, 1024], 4096)], ids=["q8_0", "q6_K", "q8_0_group"])
+                                      (O.TYPE_Q5_K, 160, [3000], 4096), (O.TYPE_Q8_0, 140, [1024, 1024], 4096)],
+                         ids=["q8_0", "q6_K", "q5_K", "q8_0_group"])
 def test_mul_mat_gemm_long_k(mx, be, t, M, Ns, K):
     """Long products whose 128 x 128 grid is small keep the large tile and split K: ragged widths through the scalar
     reduce, a two-weight group of widths divisible by four through the vector one."""
