@@ -1,23 +1,23 @@
-// Prefill products (M > 8) on the fp16 matrix cores over dequantized tiles: Y = deq(W) . deq(quant(X)), for Q8_0 and
-// Q6_K weights.
+// Prefill products (M > 8) on the fp16 matrix cores over dequantized tiles: Y = deq(W) . deq(quant(X)), for Q8_0, Q5_K
+// and Q6_K weights.
 //
 // The activations are quantized exactly as ggml-cpu quantizes src1 for the weight's vec_dot (Q8_0 blocks with the
-// fp16-rounded d for Q8_0 weights; Q8_K blocks with their fp32 d for Q6_K) and written back as fp16(d * q); the weight
-// tiles are dequantized in LDS to fp16(d * q) (Q6_K: fp16(d * sc * q), the exact fp32 product of ggml's
-// dequantize_row_q6_K rounded once). The weight rounding is a single rounding of an exact product, the activation one
-// too for Q8_0 (Q8_K's fp32 d * q is rounded to fp32 first, as ggml forms it); relative error <= 2^-11 each. The
-// products accumulate over all of K in fp32 inside the MFMA, so there is no per-block epilogue: the VALU work is the
-// weight conversion, once per workgroup and element. Against ggml-cpu's per-block integer sums the row-relative error
-// is a few 1e-4.
+// fp16-rounded d for Q8_0 weights; Q8_K blocks with their fp32 d for the K-quants) and written back as fp16(d * q);
+// the weight tiles are dequantized in LDS to fp16(d * q) (Q6_K: fp16(d * sc * q), the exact fp32 product of ggml's
+// dequantize_row_q6_K rounded once; Q5_K: fp16(d sc q - dmin m), dequantize_row_q5_K's fp32 value rounded once).
+// The weight rounding is a single rounding of ggml's fp32 value, the activation one too for Q8_0 (Q8_K's fp32 d * q
+// is rounded to fp32 first, as ggml forms it); relative error <= 2^-11 each. The products accumulate over all of K
+// in fp32 inside the MFMA, so there is no per-block epilogue: the VALU work is the weight conversion, once per
+// workgroup and element. Against ggml-cpu's per-block integer sums the row-relative error is a few 1e-4.
 //
 // Tiles: BM x BN per workgroup of WGM x WGN waves, each (BM / WGM) x (BN / WGN) as 32 x 32 v_mfma_f32_32x32x16_f16
-// tiles.
-// K advances in stages of 64. Every wave copies its share of each stage straight into LDS with global_load_lds
-// (activations: fp16 rows; weights: the raw code bytes and scales -- Q8_0: 64 codes and two block scales per row;
-// Q6_K: the 64 ql and 32 qh bytes of the stage's half super-block, its four sub-block scales and d) three stages
-// ahead, through rings of four stages; one stage ahead of the matrix cores the workgroup converts the stage's raw
-// weights into an fp16 tile (double buffered). One barrier per stage. LDS accesses in the loop are inline assembly with explicit waits: the compiler
-// cannot see which stage a copy went to, and would otherwise wait for every copy in flight.
+// tiles. K advances in stages of 64. Every wave copies its share of each stage straight into LDS with
+// global_load_lds three stages ahead, through rings of four stages: activations as fp16 rows; weights as raw bytes
+// (Q8_0: 64 codes and two block scales per row; Q6_K: the 64 ql and 32 qh bytes of the stage's half super-block, its
+// four sub-block scales and d; Q5_K: the quarter's 32 qs bytes, the super-block's 32 qh bytes, its 12 scale bytes and
+// d | dmin). One stage ahead of the matrix cores the workgroup converts the stage's raw weights into an fp16 tile
+// (double buffered). One barrier per stage. LDS accesses in the loop are inline assembly with explicit waits: the
+// compiler cannot see which stage a copy went to, and would otherwise wait for every copy in flight.
 #include "mx_common.h"
 #include "mx_device.h"
 #include "mx_dot.h"
