@@ -38,6 +38,9 @@ typedef __attribute__((address_space(3))) void dq_lds;
 #ifndef MX_DQ_WGN128
 #define MX_DQ_WGN128 4  // waves across N in a 128 x 128 tile (4: 64 x 32 per wave; 2: 64 x 64)
 #endif
+#ifndef MX_DQ_DIRECT_B
+#define MX_DQ_DIRECT_B 1  // Q8_0: B fragments converted in registers from the raw codes (0: through an fp16 LDS tile)
+#endif
 
 constexpr int DQ_KS = 64;  // K per stage
 constexpr int DQ_NS = 4;   // ring stages (copies run DQ_NS - 1 stages ahead)
@@ -48,11 +51,13 @@ constexpr int DQ_NS = 4;   // ring stages (copies run DQ_NS - 1 stages ahead)
 template <int WT, int BM, int BN, int NW>
 struct DqLds {
     static constexpr bool K6 = WT == MX_TYPE_Q6_K, K5 = WT == MX_TYPE_Q5_K;
+    // Q8_0 with direct B: each wave converts its B fragments from the raw codes, so there is no fp16 weight tile
+    static constexpr bool DIRB = MX_DQ_DIRECT_B && !K6 && !K5;
     // raw bytes per weight row and stage: codes (Q8_0 codes, Q6_K ql, Q5_K qs), qh, scales, d
     static constexpr int RB = K5 ? 32 : 64, HB = K6 || K5 ? 32 : 0, SB = K5 ? 12 : 4, DB = K6 || K5 ? 4 : 0;
     static constexpr int A = 0;                            // [stage][BM][128 B] activations
     static constexpr int BH = A + DQ_NS * BM * 128;        // [2][BN][128 B] dequantized weights
-    static constexpr int RAW = BH + 2 * BN * 128;          // [stage][BN][RB] codes
+    static constexpr int RAW = BH + (DIRB ? 0 : 2 * BN * 128);  // [stage][BN][RB] codes
     static constexpr int QH = RAW + DQ_NS * BN * RB;       // [stage][BN][HB] qh bytes
     static constexpr int SC = QH + DQ_NS * BN * HB;        // [stage][BN][SB] scales (Q8_0 two fp16, Q6_K four int8,
                                                            // Q5_K the 12 packed bytes)
@@ -413,6 +418,47 @@ __device__ __forceinline__ void dq_read(v8h (&f)[16], const uint32_t (&a)[16]) {
     }
 }
 
+// Direct B (Q8_0, one 32-column B tile per wave): the wave's 4 TM A fragments, its two 16-byte raw code chunks and
+// its row's scale word, and the wait for them.
+template <int TM>
+__device__ __forceinline__ void dq_read_ab(v8h (&f)[8], v4i (&b)[2], uint32_t &sw, const uint32_t (&a)[8],
+                                           uint32_t b0, uint32_t b1, uint32_t sc) {
+    if constexpr (TM == 2) {
+        asm volatile(
+            "ds_read_b128 %8, %11\n"
+            "ds_read_b128 %9, %12\n"
+            "ds_read_b32 %10, %13\n"
+            "ds_read_b128 %0, %14\n"
+            "ds_read_b128 %1, %15\n"
+            "ds_read_b128 %2, %16\n"
+            "ds_read_b128 %3, %17\n"
+            "ds_read_b128 %4, %18\n"
+            "ds_read_b128 %5, %19\n"
+            "ds_read_b128 %6, %20\n"
+            "ds_read_b128 %7, %21\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]), "=&v"(f[6]), "=&v"(f[7]),
+              "=&v"(b[0]), "=&v"(b[1]), "=&v"(sw)
+            : "v"(b0), "v"(b1), "v"(sc), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]),
+              "v"(a[7])
+            : "memory");
+    } else {
+        static_assert(TM == 1, "wave tiles of 32 or 64 rows");
+        asm volatile(
+            "ds_read_b128 %4, %7\n"
+            "ds_read_b128 %5, %8\n"
+            "ds_read_b32 %6, %9\n"
+            "ds_read_b128 %0, %10\n"
+            "ds_read_b128 %1, %11\n"
+            "ds_read_b128 %2, %12\n"
+            "ds_read_b128 %3, %13\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(b[0]), "=&v"(b[1]), "=&v"(sw)
+            : "v"(b0), "v"(b1), "v"(sc), "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3])
+            : "memory");
+    }
+}
+
 template <int WT, int BM, int BN, int WGM, int WGN>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     constexpr int NW = WGM * WGN, NT = 64 * NW;
@@ -457,7 +503,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
         constexpr int LR = L::RB / 16;  // lanes per code row
         const int j = wave * L::PC + jj, row = (64 / LR) * min(j, L::NC - 1) + lane / LR;
         const int64_t grow = min(n0 + row, N - 1);
-        csrc[jj] = (L::K6 || L::K5 ? p.w.p0 + grow * nsb * 128 : p.w.p0 + grow * K + sb * DQ_KS) + 16 * (lane % LR);
+        // direct B: row r's chunk c lands at chunk c ^ ((r >> 2) & 3), so the 16 rows a fragment read's lane group
+        // touches cover all 64 banks
+        const int cc = L::DIRB ? (lane % LR) ^ ((row >> 2) & 3) : lane % LR;
+        csrc[jj] = (L::K6 || L::K5 ? p.w.p0 + grow * nsb * 128 : p.w.p0 + grow * K + sb * DQ_KS) + 16 * cc;
         cdst[jj] = j < L::NC ? L::RAW + j * 1024 : L::JUNK + wave * 1024;
     }
     const uint8_t *hsrc[L::PH > 0 ? L::PH : 1];
@@ -602,14 +651,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
 
     const int wm = (wave / WGN) * WM, wn = (wave % WGN) * WN;
     const int fr = lane & 31, fh = lane >> 5;
-    // fragment offsets within a tile: row base plus the swizzled chunk of K step kk (chunk 2 kk + fh)
+    // fragment offsets within a tile: row base plus the swizzled chunk of K step kk: chunk 2 kk + fh; with direct B,
+    // chunk 4 (kk >> 1) + 2 fh + (kk & 1), the halves of the 16 codes 16 (2 (kk >> 1) + fh) .. a lane converts at once
+    // (any assignment of K to the MFMA's k slots serves, as long as A and B share it)
     uint32_t aoff[TM][4], boff[TN][4];
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) {
 #pragma unroll
         for (int i = 0; i < TM; i++) {
-            const int row = wm + 32 * i + fr;
-            aoff[i][kk] = row * 128 + 16 * ((2 * kk + fh) ^ dq_swz(row));
+            const int row = wm + 32 * i + fr, c = L::DIRB ? 4 * (kk >> 1) + 2 * fh + (kk & 1) : 2 * kk + fh;
+            aoff[i][kk] = row * 128 + 16 * (c ^ dq_swz(row));
         }
 #pragma unroll
         for (int j = 0; j < TN; j++) {
@@ -629,17 +680,55 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     issue(0);
     issue(1);
     issue(2);
-    dq_wait_vm<2 * L::OPS>();  // stage 0 landed (this wave's copies)
-    if (tid < BM) *(float *)(smem + L::RS + 4 * tid) = rs_row;  // the tile rows' 2^-e, read by the epilogue
-    __syncthreads();
-    convert(0);
+    if constexpr (!L::DIRB) {
+        dq_wait_vm<2 * L::OPS>();  // stage 0 landed (this wave's copies)
+        if (tid < BM) *(float *)(smem + L::RS + 4 * tid) = rs_row;  // the tile rows' 2^-e, read by the epilogue
+        __syncthreads();
+        convert(0);
+    } else {
+        if (tid < BM) *(float *)(smem + L::RS + 4 * tid) = rs_row;  // visible after the loop's first barrier
+    }
+    // direct B: this lane's raw chunk 2 kk2 + fh of row wn + fr, swizzled as the copies placed it, and its scale word
+    const int brow = wn + fr;
+    const uint32_t boffd0 = brow * L::RB + 16 * ((0 + fh) ^ ((brow >> 2) & 3));
+    const uint32_t boffd1 = brow * L::RB + 16 * ((2 + fh) ^ ((brow >> 2) & 3));
 
 #pragma unroll 1
     for (int s = 0; s < nst; s++) {
-        // this wave's copies of A(s) and of the raw weights of stage s + 1 have landed, and its LDS writes are done
-        dq_wait_vm<L::OPS>();
+        // this wave's copies of A(s) and of the raw weights of stage s + 1 (direct B: of stage s) have landed, and its
+        // LDS writes are done
+        if constexpr (L::DIRB) dq_wait_vm<2 * L::OPS>();
+        else dq_wait_vm<L::OPS>();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
+        if constexpr (L::DIRB) {
+            static_assert(TN == 1, "direct B: one 32-column B tile per wave");
+            const uint32_t at = lds + L::A + (s % DQ_NS) * BM * 128;
+            const uint32_t rt = lds + L::RAW + (s % DQ_NS) * BN * L::RB;
+            uint32_t ad[8];
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+                for (int i = 0; i < TM; i++) ad[kk * TM + i] = at + aoff[i][kk];
+#pragma unroll
+            for (int x = 4 * TM; x < 8; x++) ad[x] = 0;
+            v8h fa[8];
+            v4i braw[2];
+            uint32_t sw;
+            dq_read_ab<TM>(fa, braw, sw, ad, rt + boffd0, rt + boffd1,
+                           lds + L::SC + (s % DQ_NS) * BN * L::SB + brow * L::SB);
+            v4i bq[4];  // K steps 2 kk2 and 2 kk2 + 1 from chunk kk2 (block kk2 of the stage)
+            dq_q8_0_16(braw[0], (uint16_t)(sw & 0xFFFF), bq[0], bq[1]);
+            dq_q8_0_16(braw[1], (uint16_t)(sw >> 16), bq[2], bq[3]);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+                    acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk * TM + i], __builtin_bit_cast(v8h, bq[kk]),
+                                                                        acc[i][0], 0, 0, 0);
+            issue(s + DQ_NS - 1);
+            continue;
+        }
         // the stage's fragments, then its MFMAs; the copies three stages ahead and the conversion of the next stage's
         // weights follow while the matrix cores work through them
         const uint32_t at = lds + L::A + (s % DQ_NS) * BM * 128;
@@ -665,7 +754,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[kk * (TM + TN) + i], f[kk * (TM + TN) + TM + j],
                                                                         acc[i][j], 0, 0, 0);
         issue(s + DQ_NS - 1);
-        if (s + 1 < nst) convert(s + 1);
+        if constexpr (!L::DIRB)
+            if (s + 1 < nst) convert(s + 1);
     }
     dq_wait_vm<0>();  // the copies of the stages past the end
 
