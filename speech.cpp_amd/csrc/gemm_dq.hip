@@ -12,12 +12,15 @@
 //
 // Tiles: BM x BN per workgroup of WGM x WGN waves, each (BM / WGM) x (BN / WGN) as 32 x 32 v_mfma_f32_32x32x16_f16
 // tiles. K advances in stages of 64. Every wave copies its share of each stage straight into LDS with
-// global_load_lds three stages ahead, through rings of four stages: activations as fp16 rows; weights as raw bytes
-// (Q8_0: 64 codes and two block scales per row; Q6_K: the 64 ql and 32 qh bytes of the stage's half super-block, its
-// four sub-block scales and d; Q5_K: the quarter's 32 qs bytes, the super-block's 32 qh bytes, its 12 scale bytes and
-// d | dmin). One stage ahead of the matrix cores the workgroup converts the stage's raw weights into an fp16 tile
-// (double buffered). One barrier per stage. LDS accesses in the loop are inline assembly with explicit waits: the
-// compiler cannot see which stage a copy went to, and would otherwise wait for every copy in flight.
+// global_load_lds, through rings of four stages (three ahead; Q8_0: three stages, two ahead): activations as fp16
+// rows; weights as raw bytes (Q8_0: 64 codes and two block scales per row; Q6_K: the 64 ql and 32 qh bytes of the
+// stage's half super-block, its four sub-block scales and d; Q5_K: the quarter's 32 qs bytes, the super-block's 32 qh
+// bytes, its 12 scale bytes and d | dmin). K-quants: one stage ahead of the matrix cores the workgroup converts the
+// stage's raw weights into an fp16 tile (double buffered). Q8_0: each wave converts its own B fragments in registers
+// from the raw codes (16 codes per lane and chunk), so there is no fp16 weight tile and a 128 x 128 workgroup needs
+// 76 KB: two of them share a CU and cover each other's barrier waits. One barrier per stage. LDS accesses in the loop
+// are inline assembly with explicit waits: the compiler cannot see which stage a copy went to, and would otherwise
+// wait for every copy in flight.
 #include "mx_common.h"
 #include "mx_device.h"
 #include "mx_dot.h"
@@ -41,9 +44,10 @@ typedef __attribute__((address_space(3))) void dq_lds;
 #ifndef MX_DQ_DIRECT_B
 #define MX_DQ_DIRECT_B 1  // Q8_0: B fragments converted in registers from the raw codes (0: through an fp16 LDS tile)
 #endif
-
 constexpr int DQ_KS = 64;  // K per stage
-constexpr int DQ_NS = 4;   // ring stages (copies run DQ_NS - 1 stages ahead)
+#ifndef MX_DQ_NS_DIRB
+#define MX_DQ_NS_DIRB 3  // ring stages of the direct-B (Q8_0) tiles: 76 KB at 128 x 128, two workgroups per CU
+#endif
 
 // LDS map of a BM x BN workgroup of NW waves. Row-major fp16 tiles of 64 halves (128 bytes) per row; the 16-byte
 // chunk c of row r sits at chunk c ^ ((r ^ (r >> 3)) & 7): any 8 consecutive rows an MFMA fragment read touches use 8
@@ -53,19 +57,18 @@ struct DqLds {
     static constexpr bool K6 = WT == MX_TYPE_Q6_K, K5 = WT == MX_TYPE_Q5_K;
     // Q8_0 with direct B: each wave converts its B fragments from the raw codes, so there is no fp16 weight tile
     static constexpr bool DIRB = MX_DQ_DIRECT_B && !K6 && !K5;
+    // ring stages: the copies run NS - 1 stages ahead of the matrix cores
+    static constexpr int NS = DIRB ? MX_DQ_NS_DIRB : 4;
     // raw bytes per weight row and stage: codes (Q8_0 codes, Q6_K ql, Q5_K qs), qh, scales, d
     static constexpr int RB = K5 ? 32 : 64, HB = K6 || K5 ? 32 : 0, SB = K5 ? 12 : 4, DB = K6 || K5 ? 4 : 0;
     static constexpr int A = 0;                            // [stage][BM][128 B] activations
-    static constexpr int BH = A + DQ_NS * BM * 128;        // [2][BN][128 B] dequantized weights
+    static constexpr int BH = A + NS * BM * 128;        // [2][BN][128 B] dequantized weights
     static constexpr int RAW = BH + (DIRB ? 0 : 2 * BN * 128);  // [stage][BN][RB] codes
-    static constexpr int QH = RAW + DQ_NS * BN * RB;       // [stage][BN][HB] qh bytes
-    static constexpr int SC = QH + DQ_NS * BN * HB;        // [stage][BN][SB] scales (Q8_0 two fp16, Q6_K four int8,
+    static constexpr int QH = RAW + NS * BN * RB;       // [stage][BN][HB] qh bytes
+    static constexpr int SC = QH + NS * BN * HB;        // [stage][BN][SB] scales (Q8_0 two fp16, Q6_K four int8,
                                                            // Q5_K the 12 packed bytes)
-    static constexpr int DD = SC + DQ_NS * BN * SB;        // [stage][BN][DB] Q6_K: the fp16 d pair holding the row's;
+    static constexpr int DD = SC + NS * BN * SB;        // [stage][BN][DB] Q6_K: the fp16 d pair holding the row's;
                                                            // Q5_K: d | dmin
-    static constexpr int JUNK = DD + DQ_NS * BN * DB;      // [wave][1 KB] where copies beyond a tile's need land
-    static constexpr int RS = JUNK + NW * 1024;            // [BM] the tile rows' 2^-e
-    static constexpr int SIZE = RS + BM * 4;
     // copy instructions per stage (64 lanes each): activation rows (16 B), code rows (16 B), qh rows (16 B), scale
     // words (4 B), d words (4 B), and per wave
     static constexpr int NA = BM / 8, NC = BN * RB / 1024, NH = BN * HB / 1024, NS4 = BN * SB / 256,
@@ -73,6 +76,13 @@ struct DqLds {
     static constexpr int PA = (NA + NW - 1) / NW, PC = (NC + NW - 1) / NW, PH = (NH + NW - 1) / NW;
     static constexpr int PS = (NS4 + NW - 1) / NW, PD = (ND + NW - 1) / NW;
     static constexpr int OPS = PA + PC + PH + PS + PD;  // vector memory ops per wave and stage
+    // junk bytes per wave: the largest copy instruction some wave issues beyond the tile's need
+    static constexpr int JB = PA * NW > NA || PC * NW > NC || PH * NW > NH ? 1024
+                              : PS * NW > NS4 || PD * NW > ND            ? 256
+                                                                         : 0;
+    static constexpr int JUNK = DD + NS * BN * DB;      // [wave][JB] where copies beyond a tile's need land
+    static constexpr int RS = JUNK + NW * JB;           // [BM] the tile rows' 2^-e
+    static constexpr int SIZE = RS + BM * 4;
     static_assert(SIZE <= 160 * 1024, "LDS");
 };
 
@@ -494,7 +504,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     for (int jj = 0; jj < L::PA; jj++) {
         const int j = wave * L::PA + jj, row = 8 * min(j, L::NA - 1) + (lane >> 3);
         asrc[jj] = a.xh + (int64_t)min(m0 + row, M - 1) * K + sb * DQ_KS + 8 * ((lane & 7) ^ dq_swz(row));
-        adst[jj] = j < L::NA ? L::A + j * 1024 : L::JUNK + wave * 1024;
+        adst[jj] = j < L::NA ? L::A + j * 1024 : L::JUNK + wave * L::JB;
     }
     const uint8_t *csrc[L::PC];
     uint32_t cdst[L::PC];
@@ -507,7 +517,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
         // touches cover all 64 banks
         const int cc = L::DIRB ? (lane % LR) ^ ((row >> 2) & 3) : lane % LR;
         csrc[jj] = (L::K6 || L::K5 ? p.w.p0 + grow * nsb * 128 : p.w.p0 + grow * K + sb * DQ_KS) + 16 * cc;
-        cdst[jj] = j < L::NC ? L::RAW + j * 1024 : L::JUNK + wave * 1024;
+        cdst[jj] = j < L::NC ? L::RAW + j * 1024 : L::JUNK + wave * L::JB;
     }
     const uint8_t *hsrc[L::PH > 0 ? L::PH : 1];
     uint32_t hdst[L::PH > 0 ? L::PH : 1];
@@ -515,7 +525,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     for (int jj = 0; jj < L::PH; jj++) {
         const int j = wave * L::PH + jj, row = 32 * min(j, L::NH - 1) + (lane >> 1);
         hsrc[jj] = p.w.p1 + (int64_t)min(n0 + row, N - 1) * nsb * (L::K5 ? 32 : 64) + 16 * (lane & 1);
-        hdst[jj] = j < L::NH ? L::QH + j * 1024 : L::JUNK + wave * 1024;
+        hdst[jj] = j < L::NH ? L::QH + j * 1024 : L::JUNK + wave * L::JB;
     }
     const uint8_t *ssrc[L::PS];
     uint32_t sdst[L::PS];
@@ -529,7 +539,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             const int64_t grow = min(n0 + wd, N - 1);
             ssrc[jj] = L::K6 ? p.w.p2 + grow * nsb * 16 : p.w.p1 + grow * nblk * 2 + sb * 4;
         }
-        sdst[jj] = j < L::NS4 ? L::SC + j * 256 : L::JUNK + wave * 1024;
+        sdst[jj] = j < L::NS4 ? L::SC + j * 256 : L::JUNK + wave * L::JB;
     }
     int64_t dsb[L::PD > 0 ? L::PD : 1];  // the row's first super-block index in the d plane
     uint32_t ddst[L::PD > 0 ? L::PD : 1];
@@ -537,12 +547,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     for (int jj = 0; jj < L::PD; jj++) {
         const int j = wave * L::PD + jj, row = 64 * min(j, L::ND - 1) + lane;
         dsb[jj] = (int64_t)min(n0 + row, N - 1) * nsb;
-        ddst[jj] = j < L::ND ? L::DD + j * 256 : L::JUNK + wave * 1024;
+        ddst[jj] = j < L::ND ? L::DD + j * 256 : L::JUNK + wave * L::JB;
     }
 
     auto issue = [&](int t) {
         t = min(t, nst - 1);  // past the end: copy the last stage again into its own slot (identical bytes)
-        const int slot = t % DQ_NS, g = sb + t;  // g: the stage's index along the whole of K
+        const int slot = t % L::NS, g = sb + t;  // g: the stage's index along the whole of K
 #pragma unroll
         for (int jj = 0; jj < L::PA; jj++) {
             const uint32_t d = adst[jj] + (adst[jj] < (uint32_t)L::JUNK ? slot * BM * 128 : 0);
@@ -585,7 +595,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     // Conversion of stage t's raw weights into fp16 tile buffer t & 1, in units of 16 codes: unit u is quarter u & 3
     // of row u >> 2.
     auto convert = [&](int t) {
-        const int slot = t % DQ_NS, g = sb + t;
+        const int slot = t % L::NS, g = sb + t;
 #pragma unroll
         for (int u = tid; u < BN * 4; u += NT) {
             const int row = u >> 2, q = u & 3;
@@ -677,11 +687,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
     const float rs_row = a.rs[min(m0 + (tid < BM ? tid : 0), M - 1)];  // requested ahead of the copies
-    issue(0);
-    issue(1);
-    issue(2);
+#pragma unroll
+    for (int t = 0; t < L::NS - 1; t++) issue(t);
     if constexpr (!L::DIRB) {
-        dq_wait_vm<2 * L::OPS>();  // stage 0 landed (this wave's copies)
+        dq_wait_vm<(L::NS - 2) * L::OPS>();  // stage 0 landed (this wave's copies)
         if (tid < BM) *(float *)(smem + L::RS + 4 * tid) = rs_row;  // the tile rows' 2^-e, read by the epilogue
         __syncthreads();
         convert(0);
@@ -697,14 +706,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     for (int s = 0; s < nst; s++) {
         // this wave's copies of A(s) and of the raw weights of stage s + 1 (direct B: of stage s) have landed, and its
         // LDS writes are done
-        if constexpr (L::DIRB) dq_wait_vm<2 * L::OPS>();
-        else dq_wait_vm<L::OPS>();
+        if constexpr (L::DIRB) dq_wait_vm<(L::NS - 2) * L::OPS>();
+        else dq_wait_vm<(L::NS - 3) * L::OPS>();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
         if constexpr (L::DIRB) {
             static_assert(TN == 1, "direct B: one 32-column B tile per wave");
-            const uint32_t at = lds + L::A + (s % DQ_NS) * BM * 128;
-            const uint32_t rt = lds + L::RAW + (s % DQ_NS) * BN * L::RB;
+            const uint32_t at = lds + L::A + (s % L::NS) * BM * 128;
+            const uint32_t rt = lds + L::RAW + (s % L::NS) * BN * L::RB;
             uint32_t ad[8];
 #pragma unroll
             for (int kk = 0; kk < 4; kk++)
@@ -716,7 +725,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             v4i braw[2];
             uint32_t sw;
             dq_read_ab<TM>(fa, braw, sw, ad, rt + boffd0, rt + boffd1,
-                           lds + L::SC + (s % DQ_NS) * BN * L::SB + brow * L::SB);
+                           lds + L::SC + (s % L::NS) * BN * L::SB + brow * L::SB);
             v4i bq[4];  // K steps 2 kk2 and 2 kk2 + 1 from chunk kk2 (block kk2 of the stage)
             dq_q8_0_16(braw[0], (uint16_t)(sw & 0xFFFF), bq[0], bq[1]);
             dq_q8_0_16(braw[1], (uint16_t)(sw >> 16), bq[2], bq[3]);
@@ -726,12 +735,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
                 for (int i = 0; i < TM; i++)
                     acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk * TM + i], __builtin_bit_cast(v8h, bq[kk]),
                                                                         acc[i][0], 0, 0, 0);
-            issue(s + DQ_NS - 1);
+            issue(s + L::NS - 1);
             continue;
         }
         // the stage's fragments, then its MFMAs; the copies three stages ahead and the conversion of the next stage's
         // weights follow while the matrix cores work through them
-        const uint32_t at = lds + L::A + (s % DQ_NS) * BM * 128;
+        const uint32_t at = lds + L::A + (s % L::NS) * BM * 128;
         const uint32_t bt = lds + L::BH + (s & 1) * BN * 128;
         uint32_t ad[16];
 #pragma unroll
@@ -753,7 +762,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
                 for (int j = 0; j < TN; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[kk * (TM + TN) + i], f[kk * (TM + TN) + TM + j],
                                                                         acc[i][j], 0, 0, 0);
-        issue(s + DQ_NS - 1);
+        issue(s + L::NS - 1);
         if constexpr (!L::DIRB)
             if (s + 1 < nst) convert(s + 1);
     }
