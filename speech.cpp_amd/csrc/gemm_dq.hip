@@ -44,6 +44,9 @@ typedef __attribute__((address_space(3))) void dq_lds;
 #ifndef MX_DQ_DIRECT_B
 #define MX_DQ_DIRECT_B 1  // Q8_0: B fragments converted in registers from the raw codes (0: through an fp16 LDS tile)
 #endif
+#ifndef MX_DQ_Q8_WGM128
+#define MX_DQ_Q8_WGM128 1  // Q8_0 128 x 128 tiles: waves across M (1: four waves of 128 x 32; 2: eight of 64 x 32)
+#endif
 constexpr int DQ_KS = 64;  // K per stage
 #ifndef MX_DQ_NS_DIRB
 #define MX_DQ_NS_DIRB 3  // ring stages of the direct-B (Q8_0) tiles: 76 KB at 128 x 128, two workgroups per CU
@@ -475,7 +478,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     using L = DqLds<WT, BM, BN, NW>;
     constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
     constexpr int NF = (TM + TN) * 4;  // fragments of the stage's four K steps, read together
-    static_assert(NF == 8 || NF == 12 || NF == 16, "wave tiles of 32 x 32, 64 x 32 or 64 x 64");
+    static_assert(L::DIRB ? TN == 1 && (TM == 1 || TM == 2 || TM == 4) : NF == 8 || NF == 12 || NF == 16,
+                  "wave tiles of 32 x 32, 64 x 32 or 64 x 64; direct B: 32, 64 or 128 x 32");
     extern __shared__ __align__(16) uint8_t smem[];
     const int z = blockIdx.z, pi = z % a.nprob, split = z / a.nprob;
     const DqProblem p = pi == 0 ? a.prob[0] : (pi == 1 ? a.prob[1] : (pi == 2 ? a.prob[2] : a.prob[3]));
@@ -711,21 +715,28 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
         if constexpr (L::DIRB) {
-            static_assert(TN == 1, "direct B: one 32-column B tile per wave");
             const uint32_t at = lds + L::A + (s % L::NS) * BM * 128;
             const uint32_t rt = lds + L::RAW + (s % L::NS) * BN * L::RB;
-            uint32_t ad[8];
+            // A fragment x = kk TM + i: x < 8 in fa, the rest (TM = 4: K steps 2 and 3) in fb
+            uint32_t ad[8], ae[16];
 #pragma unroll
             for (int kk = 0; kk < 4; kk++)
 #pragma unroll
-                for (int i = 0; i < TM; i++) ad[kk * TM + i] = at + aoff[i][kk];
+                for (int i = 0; i < TM; i++) {
+                    const int x = kk * TM + i;
+                    if (x < 8) ad[x] = at + aoff[i][kk];
+                    else ae[x - 8] = at + aoff[i][kk];
+                }
 #pragma unroll
             for (int x = 4 * TM; x < 8; x++) ad[x] = 0;
-            v8h fa[8];
+#pragma unroll
+            for (int x = (TM == 4 ? 8 : 0); x < 16; x++) ae[x] = 0;
+            v8h fa[8], fb[16];
             v4i braw[2];
             uint32_t sw;
-            dq_read_ab<TM>(fa, braw, sw, ad, rt + boffd0, rt + boffd1,
-                           lds + L::SC + (s % L::NS) * BN * L::SB + brow * L::SB);
+            dq_read_ab<TM == 4 ? 2 : TM>(fa, braw, sw, ad, rt + boffd0, rt + boffd1,
+                                         lds + L::SC + (s % L::NS) * BN * L::SB + brow * L::SB);
+            if constexpr (TM == 4) dq_read<8>(fb, ae);
             v4i bq[4];  // K steps 2 kk2 and 2 kk2 + 1 from chunk kk2 (block kk2 of the stage)
             dq_q8_0_16(braw[0], (uint16_t)(sw & 0xFFFF), bq[0], bq[1]);
             dq_q8_0_16(braw[1], (uint16_t)(sw >> 16), bq[2], bq[3]);
@@ -733,11 +744,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             for (int kk = 0; kk < 4; kk++)
 #pragma unroll
                 for (int i = 0; i < TM; i++)
-                    acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk * TM + i], __builtin_bit_cast(v8h, bq[kk]),
-                                                                        acc[i][0], 0, 0, 0);
+                    acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        kk * TM + i < 8 ? fa[kk * TM + i] : fb[kk * TM + i - 8], __builtin_bit_cast(v8h, bq[kk]),
+                        acc[i][0], 0, 0, 0);
             issue(s + L::NS - 1);
-            continue;
-        }
+        } else {
         // the stage's fragments, then its MFMAs; the copies three stages ahead and the conversion of the next stage's
         // weights follow while the matrix cores work through them
         const uint32_t at = lds + L::A + (s % L::NS) * BM * 128;
@@ -763,8 +774,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[kk * (TM + TN) + i], f[kk * (TM + TN) + TM + j],
                                                                         acc[i][j], 0, 0, 0);
         issue(s + L::NS - 1);
-        if constexpr (!L::DIRB)
-            if (s + 1 < nst) convert(s + 1);
+        if (s + 1 < nst) convert(s + 1);
+        }
     }
     dq_wait_vm<0>();  // the copies of the stages past the end
 
@@ -935,6 +946,10 @@ static hipError_t launch_dq(const DqArgs &a, int maxN, hipStream_t s) {
 
 template <int WT>
 static hipError_t launch_dq_type(const DqArgs &a, const DqPlan &pl, int maxN, hipStream_t s) {
+    if constexpr (WT == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B && MX_DQ_Q8_WGM128 == 1) {
+        // direct B: four waves of 128 x 32, so every B fragment is converted by one wave only
+        if (pl.bm == 128 && pl.bn == 128) return launch_dq<WT, 128, 128, 1, 4>(a, maxN, s);
+    }
     if (pl.bm == 128 && pl.bn == 128) return launch_dq<WT, 128, 128, 2, MX_DQ_WGN128>(a, maxN, s);
     if (pl.bm == 128) return launch_dq<WT, 128, 64, 4, 2>(a, maxN, s);
     return launch_dq<WT, 64, 64, 2, 2>(a, maxN, s);
