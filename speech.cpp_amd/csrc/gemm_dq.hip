@@ -47,6 +47,9 @@ typedef __attribute__((address_space(3))) void dq_lds;
 #ifndef MX_DQ_Q8_WGM128
 #define MX_DQ_Q8_WGM128 1  // Q8_0 128 x 128 tiles: waves across M (1: four waves of 128 x 32; 2: eight of 64 x 32)
 #endif
+#ifndef MX_DQ_HALF
+#define MX_DQ_HALF 1  // Q8_0 128 x 32 waves: the second half of a stage's A reads overlaps the first half's MFMAs
+#endif
 constexpr int DQ_KS = 64;  // K per stage
 #ifndef MX_DQ_NS_DIRB
 #define MX_DQ_NS_DIRB 3  // ring stages of the direct-B (Q8_0) tiles: 76 KB at 128 x 128, two workgroups per CU
@@ -472,6 +475,29 @@ __device__ __forceinline__ void dq_read_ab(v8h (&f)[8], v4i (&b)[2], uint32_t &s
     }
 }
 
+// Eight fragment reads without their wait, and the wait: dq_wait8's operands tie the registers to it, so that nothing
+// reads them before the data has landed.
+__device__ __forceinline__ void dq_issue8(v8h (&f)[16], const uint32_t (&a)[16]) {
+    asm volatile(
+        "ds_read_b128 %0, %8\n"
+        "ds_read_b128 %1, %9\n"
+        "ds_read_b128 %2, %10\n"
+        "ds_read_b128 %3, %11\n"
+        "ds_read_b128 %4, %12\n"
+        "ds_read_b128 %5, %13\n"
+        "ds_read_b128 %6, %14\n"
+        "ds_read_b128 %7, %15"
+        : "=&v"(f[0]), "=&v"(f[1]), "=&v"(f[2]), "=&v"(f[3]), "=&v"(f[4]), "=&v"(f[5]), "=&v"(f[6]), "=&v"(f[7])
+        : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7])
+        : "memory");
+}
+__device__ __forceinline__ void dq_wait8(v8h (&f)[16]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7])
+                 :
+                 : "memory");
+}
+
 template <int WT, int BM, int BN, int WGM, int WGN>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     constexpr int NW = WGM * WGN, NT = 64 * NW;
@@ -736,17 +762,41 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             uint32_t sw;
             dq_read_ab<TM == 4 ? 2 : TM>(fa, braw, sw, ad, rt + boffd0, rt + boffd1,
                                          lds + L::SC + (s % L::NS) * BN * L::SB + brow * L::SB);
-            if constexpr (TM == 4) dq_read<8>(fb, ae);
             v4i bq[4];  // K steps 2 kk2 and 2 kk2 + 1 from chunk kk2 (block kk2 of the stage)
-            dq_q8_0_16(braw[0], (uint16_t)(sw & 0xFFFF), bq[0], bq[1]);
-            dq_q8_0_16(braw[1], (uint16_t)(sw >> 16), bq[2], bq[3]);
+            if constexpr (TM == 4 && MX_DQ_HALF) {
+                // K steps 2 and 3: their A fragments are read, and chunk 1 converted, while steps 0 and 1 run
+                dq_issue8(fb, ae);
 #pragma unroll
-            for (int kk = 0; kk < 4; kk++)
+                for (int x = 0; x < 8; x++) asm volatile("" : "+v"(fa[x]));  // steps 0 and 1 stay behind the reads
+                dq_q8_0_16(braw[0], (uint16_t)(sw & 0xFFFF), bq[0], bq[1]);
 #pragma unroll
-                for (int i = 0; i < TM; i++)
-                    acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                        kk * TM + i < 8 ? fa[kk * TM + i] : fb[kk * TM + i - 8], __builtin_bit_cast(v8h, bq[kk]),
-                        acc[i][0], 0, 0, 0);
+                for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+                        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk * TM + i],
+                                                                            __builtin_bit_cast(v8h, bq[kk]), acc[i][0],
+                                                                            0, 0, 0);
+                dq_q8_0_16(braw[1], (uint16_t)(sw >> 16), bq[2], bq[3]);
+                dq_wait8(fb);
+#pragma unroll
+                for (int kk = 2; kk < 4; kk++)
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+                        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[(kk - 2) * TM + i],
+                                                                            __builtin_bit_cast(v8h, bq[kk]), acc[i][0],
+                                                                            0, 0, 0);
+            } else {
+                if constexpr (TM == 4) dq_read<8>(fb, ae);
+                dq_q8_0_16(braw[0], (uint16_t)(sw & 0xFFFF), bq[0], bq[1]);
+                dq_q8_0_16(braw[1], (uint16_t)(sw >> 16), bq[2], bq[3]);
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++)
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+                        acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            kk * TM + i < 8 ? fa[kk * TM + i] : fb[kk * TM + i - 8], __builtin_bit_cast(v8h, bq[kk]),
+                            acc[i][0], 0, 0, 0);
+            }
             issue(s + L::NS - 1);
         } else {
         // the stage's fragments, then its MFMAs; the copies three stages ahead and the conversion of the next stage's
