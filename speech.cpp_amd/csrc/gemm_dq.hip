@@ -907,9 +907,9 @@ struct DqPlan {
     int64_t ntot;
 };
 
-// Tile: 128 x 128 when that gives at least 128 workgroups (half the CUs: measured at M = 512, a 128-workgroup grid of
-// 128 x 128 tiles beats a 256-workgroup grid of 128 x 64 ones by 1.3x), else 64 x 64 (MX_GEMM_DQ_TILE=BMxBN
-// overrides). When 64 x 64 tiles still leave CUs idle (few rows: a short prefill block), K is split so that about 512
+// Tile: 128 x 128 when that gives at least 128 workgroups for a group of products, 192 for a single one (measured at
+// M = 512, a 128-workgroup grid of 128 x 128 tiles beats a 256-workgroup grid of 128 x 64 ones by 1.3x), else 64 x 64
+// (MX_GEMM_DQ_TILE=BMxBN overrides). When 64 x 64 tiles still leave CUs idle (few rows: a short prefill block), K is split so that about 512
 // workgroups stream the weights, each over at least four stages (MX_GEMM_DQ_SPLIT=n overrides); the split's reduce
 // pass costs more than it saves on the large tiles.
 DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K) {
@@ -924,7 +924,10 @@ DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K) {
     // long products (K >= 4096) whose 128 x 128 grid is smaller still keep the large tile and split K instead (at
     // M = 512, N = 2048, K = 6144: four splits of 24 stages and the reduce beat 256 tiles of 64 x 64)
     const bool split128 = wg128 >= 32 && wg128 < 128 && nst >= 64;
-    if (wg128 >= 128 || split128) pl.bm = pl.bn = 128;
+    // a single product needs 192 workgroups of 128 x 128 (M = 512, N = 4096: 31.3 us on 64 x 64 tiles against 37.0; M =
+    // 1024, N = 2048: 35.0 against 40.0), a group of them 128 (the ASR q/k/v group of widths 2048 + 1024 + 1024 at
+    // M = 512 is faster on 128 x 128)
+    if (wg128 >= (nprob == 1 ? 192 : 128) || split128) pl.bm = pl.bn = 128;
     static const char *tile = getenv("MX_GEMM_DQ_TILE");
     if (tile) {
         int tm = 0, tn = 0;

@@ -363,7 +363,7 @@ def test_graph_replay_matches_eager(mx, be):
 
 # ----------------------------------------------------------------------------------------------- MUL_MAT, M > 8
 @pytest.mark.parametrize("M,N,K", [(9, 100, 1024), (64, 256, 2048), (130, 333, 1024), (512, 2048, 2048),
-                                   (100, 64, 6144), (650, 2900, 512), (300, 6000, 256)])
+                                   (100, 64, 6144), (650, 4500, 512), (300, 8100, 256)])
 def test_mul_mat_gemm_q8_0(mx, be, M, N, K):
     """The last two take 128 x 128 tiles unsplit with ragged rows and columns; the last has four stages of K, one more
     than the copy ring holds."""
