@@ -745,7 +745,7 @@ def run_prefill_q4k(args, mx, be, threads):
                    "tok_s": round(M / (ms_per_step * 1e-3), 1), "roofline": roof,
                    "q6_k_down": (mfma_roofline("k_gemm_dq<Q6_K> (with its Q8_K activation pass)", table, ["down:Q6_K"],
                                                FP16_PEAK_TFLOPS, "TFLOP/s")
-                                 if os.environ.get("MX_GEMM_DQ", "1") != "0" else
+                                 if be.get_option("gemm_kquant") == 0 else
                                  mfma_roofline("k_gemm_kq<Q6_K>", table, ["down:Q6_K"]))})
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = cpu_prefill(dec, M, args.cpu_seconds, types)
@@ -780,8 +780,8 @@ def run_asr(args, mx, be, threads):
     ms_step = ms_pre + ASR_DECODE_TOKENS * ms_tok
     table = label_table(pre + tok, per_label_pass(be, pre + tok, reps=3, use_graph=not args.no_graph))
     # the prefill GEMM dequantizes Q8_0 weights and Q8_0-quantized activations to fp16 and accumulates in fp32 on
-    # fp16 MFMA (MX_GEMM_DQ=0 selects the int8 MFMA GEMM); the decode mat-vecs use int8 dot products
-    dq = os.environ.get("MX_GEMM_DQ", "1") != "0"
+    # fp16 MFMA (--opt gemm_q8_0=1 selects the int8 MFMA GEMM); the decode mat-vecs use int8 dot products
+    dq = be.get_option("gemm_q8_0") == 0
     roof = (mfma_roofline("k_gemm_dq<Q8_0> (with its activation pass)", table,
                           [l for l in table if l.startswith("prefill_M512")], FP16_PEAK_TFLOPS, "TFLOP/s") if dq else
             mfma_roofline("k_gemm_q8_0_i8 (with its activation pass)", table,
@@ -921,6 +921,8 @@ def main():
                     help="asr-1.7b: prefill block rows (default 512,512,512,28; counter passes use 512,512,512)")
     ap.add_argument("--batches", type=ints, default=None,
                     help="moe: token batches (default 1,16,256; counter passes use 256)")
+    ap.add_argument("--opt", action="append", default=[], metavar="NAME=VALUE",
+                    help="a kernel choice of the backend (mx_backend_set_option), e.g. gemm_q8_0=1; repeatable")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the traffic summary of two rocprofv3 --pmc runs of --workload's benchmark and exit")
     args = ap.parse_args()
@@ -942,6 +944,9 @@ def main():
         print("no GPU visible to libmx", file=sys.stderr)
         sys.exit(1)
     be = mx.Backend(0)
+    for kv in args.opt:
+        name, value = kv.split("=", 1)
+        be.set_option(name, int(value))
     calibration_copy(mx, be)
     threads = max(1, len(os.sched_getaffinity(0)))
     result = WORKLOADS[args.workload](args, mx, be, threads)

@@ -108,6 +108,33 @@ MX_API void *mx_backend_stream(mx_backend *be);
 MX_API int mx_backend_synchronize(mx_backend *be);
 /* Activation rounding used by mx_mul_mat / mx_mul_mat_id from now on (MX_ROUND_REF by default). */
 MX_API int mx_backend_set_rounding(mx_backend *be, int rounding);
+
+/* Kernel choices of a backend's products. No counterpart in speech.cpp or ggml's backend interface: this is the
+ * device's own test and measurement control (ggml's GPU backends read process-wide environment switches for the same
+ * purpose). Every option is 0 by default, which lets the dispatcher pick per product; a forced choice sends every
+ * product it covers to one kernel, so a test can reach each kernel the dispatcher may pick, in one process. A product
+ * the forced kernel cannot compute fails with MX_UNSUPPORTED (or MX_FAILED for a tile the kernel lacks) instead of
+ * going elsewhere. Values outside those listed are refused with MX_INVALID.
+ *   MX_OPT_GEMM_Q8_0          Q8_0 at M > 8: 0 the fp16 dequantizing GEMM, 1 the int8 MFMA GEMM (K % 128 == 0)
+ *   MX_OPT_GEMM_KQUANT        Q4_K / Q6_K at M > 8: 0 as picked (scale-split int8 for Q4_K, fp16 dequantizing for
+ *                             Q6_K), 1 the VALU-scaled int8 GEMM
+ *   MX_OPT_GEMM_TILE_M / _N   the GEMM's tile, 0 / 64 / 128 each (0 0: picked per product)
+ *   MX_OPT_GEMM_SPLIT         K splits of the fp16 dequantizing GEMM, 0 (picked) .. 64
+ *   MX_OPT_MATVEC_LPR         lanes per weight row of the mat-vec: 0 (picked), 16, 32, 64
+ *   MX_OPT_MMID_KERNEL        MUL_MAT_ID with many pairs: 0 as picked, 1 the generic experts kernel
+ *   MX_OPT_MMID_MATVEC_PAIRS  MUL_MAT_ID runs as one mat-vec launch up to this many (token, slot) pairs (16; 0..4096) */
+enum {
+    MX_OPT_GEMM_Q8_0 = 1,
+    MX_OPT_GEMM_KQUANT = 2,
+    MX_OPT_GEMM_TILE_M = 3,
+    MX_OPT_GEMM_TILE_N = 4,
+    MX_OPT_GEMM_SPLIT = 5,
+    MX_OPT_MATVEC_LPR = 6,
+    MX_OPT_MMID_KERNEL = 7,
+    MX_OPT_MMID_MATVEC_PAIRS = 8,
+};
+MX_API int mx_backend_set_option(mx_backend *be, int option, int64_t value);
+MX_API int mx_backend_get_option(mx_backend *be, int option, int64_t *value);
 /* The last error message of the calling thread ("" if none). */
 MX_API const char *mx_last_error(void);
 
@@ -244,11 +271,15 @@ MX_API int mx_quantize_act(mx_backend *be, int type, int rounding, const float *
  * Replay of a fixed sequence of ops with one launch (the role CUDA graphs play inside ggml-cuda's graph_compute;
  * the kept decode-step graph of src/common/qwen3-decoder.cpp:187-208,462-490). Between mx_graph_begin and
  * mx_graph_end the ops are recorded, not run; mx_graph_launch replays them on the backend's stream. Record after one
- * eager run of the same ops so every scratch buffer has its final size.
+ * eager run of the same ops so every scratch buffer has its final size. A recorded graph holds the address of the
+ * backend's scratch: once a later op grows the scratch (and frees the old one), mx_graph_launch refuses every graph
+ * recorded before that with MX_FAILED, and the caller records it again. A graph launches only on the backend that
+ * recorded it (MX_INVALID otherwise).
  * ------------------------------------------------------------------------------------------------------------- */
 MX_API int mx_graph_begin(mx_backend *be);
 MX_API int mx_graph_end(mx_backend *be, mx_graph **graph);
 MX_API int mx_graph_launch(mx_backend *be, mx_graph *graph);
+/* Waits for the graph's replays on its backend's stream, then frees it; free graphs before their backend. */
 MX_API void mx_graph_free(mx_graph *graph);
 
 /* ---------------------------------------------------------------------------------------------------------------

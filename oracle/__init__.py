@@ -197,6 +197,22 @@ def mul_mat(wtype: int, w: np.ndarray, x: np.ndarray, rounding: int = ROUND_REF,
     return y
 
 
+def mul_mat_par(wtype: int, w: np.ndarray, x: np.ndarray, rounding: int = ROUND_REF, threads: int = 0) -> np.ndarray:
+    """mul_mat over row ranges of w on several host threads (ctypes releases the GIL during each call): the same
+    oracle, the same per-output arithmetic, for products too large for one thread in a test's time."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    threads = threads or physical_cores()
+    N = w.shape[0]
+    if threads <= 1 or N < 2 * threads:
+        return mul_mat(wtype, w, x, rounding)
+    step = (N + threads - 1) // threads
+    parts = [(a, min(N, a + step)) for a in range(0, N, step)]
+    with ThreadPoolExecutor(len(parts)) as ex:
+        outs = list(ex.map(lambda r: mul_mat(wtype, np.ascontiguousarray(w[r[0]:r[1]]), x, rounding), parts))
+    return np.concatenate(outs, axis=-1)
+
+
 def mul_mat_id(wtype: int, w: np.ndarray, x: np.ndarray, ids: np.ndarray, rounding: int = ROUND_REF,
                exact: bool = False) -> np.ndarray:
     """ggml_mul_mat_id: w uint8 [E, N, row_size]; x float32 [T, B, K] (B = 1 or n_ids); ids int32 [T, n_ids]

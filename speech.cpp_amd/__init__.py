@@ -30,11 +30,15 @@ OP_GET_ROWS, OP_MUL_MAT, OP_MUL_MAT_ID, OP_ARGMAX = 1, 2, 3, 4
 OP_RMS_NORM, OP_ADD, OP_MUL, OP_SWIGLU, OP_SET_ROWS = 5, 6, 7, 8, 9
 ROPE_NEOX = 2
 ROUND_REF, ROUND_X86 = 0, 1
+# mx_backend_set_option keys (include/mx.h MX_OPT_*)
+OPTIONS = {"gemm_q8_0": 1, "gemm_kquant": 2, "tile_m": 3, "tile_n": 4, "split": 5, "matvec_lpr": 6, "mmid_kernel": 7,
+           "mmid_matvec_pairs": 8}
 SUCCESS, FAILED, ALLOC_FAILED, INVALID, UNSUPPORTED = 0, -1, -2, -3, -4
 
 EXPORTS = [
     "mx_device_count", "mx_device_description", "mx_device_memory", "mx_backend_init", "mx_backend_free",
-    "mx_backend_stream", "mx_backend_synchronize", "mx_backend_set_rounding", "mx_last_error", "mx_buft_alignment",
+    "mx_backend_stream", "mx_backend_synchronize", "mx_backend_set_rounding", "mx_backend_set_option",
+    "mx_backend_get_option", "mx_last_error", "mx_buft_alignment",
     "mx_buft_max_size", "mx_tensor_alloc_size", "mx_buffer_alloc", "mx_buffer_free", "mx_buffer_clear",
     "mx_tensor_set", "mx_tensor_get", "mx_tensor_memset", "mx_tensor_copy", "mx_supports_op", "mx_get_rows",
     "mx_mul_mat", "mx_mul_mat_id", "mx_mul_mat_group", "mx_argmax", "mx_quantize_act", "mx_graph_begin", "mx_graph_end",
@@ -104,6 +108,8 @@ def lib():
         "mx_backend_stream": ([vp], vp),
         "mx_backend_synchronize": ([vp], i32),
         "mx_backend_set_rounding": ([vp, i32], i32),
+        "mx_backend_set_option": ([vp, i32, i64], i32),
+        "mx_backend_get_option": ([vp, i32, ctypes.POINTER(i64)], i32),
         "mx_last_error": ([], ctypes.c_char_p),
         "mx_buft_alignment": ([], sz),
         "mx_buft_max_size": ([], sz),
@@ -325,6 +331,31 @@ class Backend:
 
     def set_rounding(self, r: int) -> None:
         check(lib().mx_backend_set_rounding(self.h, r))
+
+    def set_option(self, name: str, value: int) -> None:
+        """A kernel choice of this backend (mx_backend_set_option; names are the keys of OPTIONS)."""
+        check(lib().mx_backend_set_option(self.h, OPTIONS[name], int(value)))
+
+    def get_option(self, name: str) -> int:
+        v = ctypes.c_int64()
+        check(lib().mx_backend_get_option(self.h, OPTIONS[name], ctypes.byref(v)))
+        return int(v.value)
+
+    def options(self, **kw):
+        """Context manager: the given options set for the block, the previous values restored after it."""
+        import contextlib
+
+        @contextlib.contextmanager
+        def cm():
+            old = {k: self.get_option(k) for k in kw}
+            try:
+                for k, v in kw.items():
+                    self.set_option(k, v)
+                yield self
+            finally:
+                for k, v in old.items():
+                    self.set_option(k, v)
+        return cm()
 
     def get_rows(self, src0: Tensor, ids: Tensor, dst: Tensor) -> None:
         check(lib().mx_get_rows(self.h, src0.ref(), ids.ref(), dst.ref()))

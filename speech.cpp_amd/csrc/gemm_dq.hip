@@ -121,13 +121,15 @@ __device__ __forceinline__ void dq_wait_vm() {
 // The fp16 activation values of a row carry a power-of-two scale 2^e, e chosen so that the row's largest |d q| lands
 // in [2^14, 2^15): clear of fp16's overflow (65504) and of its subnormals, where ggml's fp32 sums lose nothing. The
 // GEMM multiplies its sums by rs[m] = 2^-e. Both scalings are exact, so a row that fp16 already holds in its normal
-// range gives the same bits as unscaled values would.
+// range gives the same bits as unscaled values would. e is at most 126, so rs stays a normal float: a row whose
+// largest |d q| is below 2^-112 (possible with Q8_K's fp32 d) lands lower than 2^14 but still in fp16's normal range
+// down to 2^-140.
 __device__ __forceinline__ int dq_row_exp(float amax) {
     if (amax == 0.0f) return 0;
     int E = (int)((__float_as_uint(amax) >> 23) & 0xFF);  // amax in [2^(E-127), 2^(E-126))
     if (E == 0) E = 1;
     const int e = 141 - E;
-    return e < -126 ? -126 : (e > 127 ? 127 : e);
+    return e < -126 ? -126 : (e > 126 ? 126 : e);  // 2^-e stays a normal float (2^-127 would be subnormal)
 }
 __device__ __forceinline__ float dq_pow2(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
 
@@ -889,12 +891,7 @@ __global__ __launch_bounds__(256) void k_dq_reduce(DqArgs a) {
 // Host side.
 // ------------------------------------------------------------------------------------------------------------------
 bool gemm_dq_supported(int type, int64_t M, int64_t K) {
-    static const bool off = [] {
-        const char *e = getenv("MX_GEMM_DQ");
-        return e && e[0] == '0';
-    }();
-    return !off &&
-           ((type == MX_TYPE_Q8_0 && K % DQ_KS == 0) || ((type == MX_TYPE_Q6_K || type == MX_TYPE_Q5_K) && K % 256 == 0)) &&
+    return ((type == MX_TYPE_Q8_0 && K % DQ_KS == 0) || ((type == MX_TYPE_Q6_K || type == MX_TYPE_Q5_K) && K % 256 == 0)) &&
            M * K < ((int64_t)1 << 31) && K < (1 << 24);
 }
 
@@ -909,10 +906,11 @@ struct DqPlan {
 
 // Tile: 128 x 128 when that gives at least 128 workgroups for a group of products, 192 for a single one (measured at
 // M = 512, a 128-workgroup grid of 128 x 128 tiles beats a 256-workgroup grid of 128 x 64 ones by 1.3x), else 64 x 64
-// (MX_GEMM_DQ_TILE=BMxBN overrides). When 64 x 64 tiles still leave CUs idle (few rows: a short prefill block), K is split so that about 512
-// workgroups stream the weights, each over at least four stages (MX_GEMM_DQ_SPLIT=n overrides); the split's reduce
-// pass costs more than it saves on the large tiles.
-DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K) {
+// (a backend's tile option overrides it: 64 x 64, 128 x 64 or 128 x 128). When 64 x 64 tiles still leave CUs idle
+// (few rows: a short prefill block), K is split so that about 512 workgroups stream the weights, each over at least
+// four stages (a backend's split option overrides it); the split's reduce pass costs more than it saves on the large
+// tiles. A forced tile the kernel lacks gives bm = 0 (refused by the launch).
+DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o) {
     DqPlan pl{64, 64, 1, 0};
     int64_t wg128 = 0;
     for (int i = 0; i < nprob; i++) {
@@ -928,13 +926,14 @@ DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K) {
     // 1024, N = 2048: 35.0 against 40.0), a group of them 128 (the ASR q/k/v group of widths 2048 + 1024 + 1024 at
     // M = 512 is faster on 128 x 128)
     if (wg128 >= (nprob == 1 ? 192 : 128) || split128) pl.bm = pl.bn = 128;
-    static const char *tile = getenv("MX_GEMM_DQ_TILE");
-    if (tile) {
-        int tm = 0, tn = 0;
-        if (sscanf(tile, "%dx%d", &tm, &tn) == 2 && (tm == 64 || tm == 128) && (tn == 64 || tn == 128) &&
-            !(tm == 64 && tn == 128)) {
+    if (o.tile_m || o.tile_n) {
+        const int tm = o.tile_m, tn = o.tile_n;
+        if ((tm == 64 || tm == 128) && (tn == 64 || tn == 128) && !(tm == 64 && tn == 128)) {
             pl.bm = tm;
             pl.bn = tn;
+        } else {
+            pl.bm = pl.bn = 0;
+            return pl;
         }
     }
     int64_t tiles = 0;
@@ -942,10 +941,7 @@ DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K) {
     tiles *= (M + pl.bm - 1) / pl.bm;
     int64_t want = tiles < 256 && pl.bn == 64 ? (512 + tiles - 1) / tiles : 1;
     if (split128 && pl.bm == 128 && pl.bn == 128) want = (256 + tiles - 1) / tiles;
-    static const int forced = [] {
-        const char *e = getenv("MX_GEMM_DQ_SPLIT");
-        return e ? atoi(e) : 0;
-    }();
+    const int forced = o.split;
     if (forced > 0) want = forced;
     want = std::min<int64_t>(want, std::max<int64_t>(1, forced > 0 ? nst : nst / 4));
     const int64_t per = (nst + want - 1) / want;  // stages per split; no split is left empty
@@ -959,8 +955,8 @@ DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K) {
 static size_t dq_rs_offset(int64_t M, int64_t K) { return (gemm_dq_act_bytes(M, K) + 255) / 256 * 256; }
 static size_t dq_ws_offset(int64_t M, int64_t K) { return dq_rs_offset(M, K) + ((size_t)M * 4 + 255) / 256 * 256; }
 
-size_t gemm_dq_scratch_bytes(int nprob, const int64_t *N, int64_t M, int64_t K) {
-    const DqPlan pl = dq_plan(nprob, N, M, K);
+size_t gemm_dq_scratch_bytes(int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o) {
+    const DqPlan pl = dq_plan(nprob, N, M, K, o);
     size_t b = dq_ws_offset(M, K);
     if (pl.nsplit > 1) b += (size_t)pl.nsplit * (size_t)M * (size_t)pl.ntot * 4;
     return b;
@@ -1009,9 +1005,10 @@ static hipError_t launch_dq_type(const DqArgs &a, const DqPlan &pl, int maxN, hi
 }
 
 hipError_t launch_gemm_dq(int type, int nprob, const WPlanes *w, const int64_t *N, float *const *y,
-                          const int64_t *ldy, int64_t M, int64_t K, void *scratch, hipStream_t s) {
+                          const int64_t *ldy, int64_t M, int64_t K, void *scratch, const Options &o, hipStream_t s) {
     if (nprob < 1 || nprob > 4 || !gemm_dq_supported(type, M, K)) return hipErrorInvalidValue;
-    const DqPlan pl = dq_plan(nprob, N, M, K);
+    const DqPlan pl = dq_plan(nprob, N, M, K, o);
+    if (pl.bm == 0) return hipErrorInvalidValue;
     DqArgs a{};
     int64_t maxN = 0;
     for (int i = 0; i < nprob; i++) {

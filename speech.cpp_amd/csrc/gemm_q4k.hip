@@ -510,7 +510,7 @@ static hipError_t launch_q4g(const Q4gArgs &a, int nprob, int maxN, hipStream_t 
 }
 
 hipError_t launch_gemm_q4k(int nprob, const WPlanes *w, const int64_t *N, float *const *y, const int64_t *ldy,
-                           int64_t M, int64_t K, const void *scratch, hipStream_t s) {
+                           int64_t M, int64_t K, const void *scratch, const Options &o, hipStream_t s) {
     if (nprob < 1 || nprob > 4 || K % 256 != 0 || M <= 0) return hipErrorInvalidValue;
     // 32-bit buffer offsets: activations M * K bytes, weight codes N * K / 2 bytes
     if ((uint64_t)M * (uint64_t)K >= (1ull << 31)) return hipErrorInvalidValue;
@@ -531,14 +531,15 @@ hipError_t launch_gemm_q4k(int nprob, const WPlanes *w, const int64_t *N, float 
     // Tile: 128 x 128 (eight waves, two per SIMD) when that gives at least 128 workgroups, else 128 x 64 (four).
     // Measured at M = 512: q/k/v (N = 4096) on 128 workgroups of 128 x 128 takes 29.7 us against 43.3 us on 256 of
     // 128 x 64; attn_o (N = 2048) on 64 of 128 x 128 takes 29.0 us against 24.8 us on 128 of 128 x 64.
-    // MX_GEMM_Q4K_TILE=1 forces 128 x 128, =2 128 x 64.
-    static const int tile = [] {
-        const char *e = getenv("MX_GEMM_Q4K_TILE");
-        return e ? atoi(e) : 0;
-    }();
+    // A backend's tile option forces 128 x 128 or 128 x 64; any other forced pair is refused.
     int64_t wg_big = 0;
     for (int i = 0; i < nprob; i++) wg_big += (N[i] + 127) / 128 * ((M + 127) / 128);
-    if (tile == 1 || (tile != 2 && wg_big >= 128)) return launch_q4g<Q4gT<2, 2, 4>>(a, nprob, (int)maxN, s);
+    bool big = wg_big >= 128;
+    if (o.tile_m || o.tile_n) {
+        if (o.tile_m != 128 || (o.tile_n != 128 && o.tile_n != 64)) return hipErrorInvalidValue;
+        big = o.tile_n == 128;
+    }
+    if (big) return launch_q4g<Q4gT<2, 2, 4>>(a, nprob, (int)maxN, s);
     return launch_q4g<Q4gT<2, 2, 2>>(a, nprob, (int)maxN, s);
 }
 

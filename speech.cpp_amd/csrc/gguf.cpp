@@ -14,6 +14,7 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <new>
 #include <string>
 #include <vector>
 
@@ -134,7 +135,7 @@ bool read_value(Reader &r, mx_gguf::Kv &kv) {
         if (!r.num(et) || !r.num(kv.n)) return false;
         kv.elem_type = (int)et;
         if (et == 8) {
-            if (kv.n > r.size - r.pos) {  // every string takes at least its 8-byte length
+            if (kv.n > (r.size - r.pos) / 8) {  // every string takes at least its 8-byte length
                 r.why = "an array runs past the end of the file";
                 return false;
             }
@@ -244,14 +245,16 @@ bool parse(FILE *f, mx_gguf &g, std::string &why) {
             why = "the rows of " + t.name + " are not whole blocks of its type";
             return false;
         }
-        // ggml_nbytes of a contiguous tensor, with overflow checks
-        unsigned __int128 n = (unsigned __int128)(t.ne[0] / geo.blck) * geo.bytes;
-        for (int d = 1; d < 4; d++) n *= (uint64_t)t.ne[d];
-        if (n > (unsigned __int128)g.file_size) {
+        // ggml_nbytes of a contiguous tensor; every multiply is checked, so no shape can wrap past the size check
+        // (four axes of up to 2^40 would overflow even 128 bits)
+        uint64_t n = 0;
+        bool wrapped = __builtin_mul_overflow((uint64_t)(t.ne[0] / geo.blck), (uint64_t)geo.bytes, &n);
+        for (int d = 1; d < 4 && !wrapped; d++) wrapped = __builtin_mul_overflow(n, (uint64_t)t.ne[d], &n);
+        if (wrapped || n > g.file_size) {
             why = "the tensor " + t.name + " is larger than the file";
             return false;
         }
-        t.nbytes = (uint64_t)n;
+        t.nbytes = n;
         if (t.offset % g.alignment != 0) {
             why = "the tensor " + t.name + " is not aligned to general.alignment";
             return false;
@@ -293,7 +296,14 @@ MX_API mx_gguf *mx_gguf_open(const char *path) {
     g->file_size = (uint64_t)ftello(f.get());
     std::rewind(f.get());
     std::string why;
-    if (!parse(f.get(), *g, why)) {
+    bool ok = false;
+    try {
+        ok = parse(f.get(), *g, why);
+    } catch (const std::bad_alloc &) {  // the bounds keep every container within the file's size; this is the rest
+        mx::set_error(MX_ALLOC_FAILED, (std::string("out of host memory reading ") + path).c_str());
+        return nullptr;
+    }
+    if (!ok) {
         mx::set_error(MX_INVALID, (std::string("cannot read ") + path + " as a GGUF file: " + why).c_str());
         return nullptr;
     }

@@ -294,12 +294,8 @@ static hipError_t launch_one(const MatvecArgs &a, int64_t maxN, size_t lds, hipS
 
 // Lanes per row: the fewest (16, 32 or 64) whose chunks per lane all fit the preload, so every weight byte of a lane
 // is requested before the activation prologue; rows longer than that take 64 lanes. Measured on the decode shapes
-// (K 1024..3072): one full preload beats more workgroups with shorter streams. MX_MATVEC_LPR overrides it.
-static int pick_lpr(int64_t nchunks) {
-    static const int forced = [] {
-        const char *e = getenv("MX_MATVEC_LPR");
-        return e ? atoi(e) : 0;
-    }();
+// (K 1024..3072): one full preload beats more workgroups with shorter streams. A backend's option forces it.
+static int pick_lpr(int64_t nchunks, int forced) {
     if (forced == 16 || forced == 32 || forced == 64) return forced;
     int lpr = 16;
     while (lpr < 64 && nchunks > (int64_t)PRELOAD * lpr) lpr *= 2;
@@ -309,7 +305,7 @@ static int pick_lpr(int64_t nchunks) {
 template <int TYPE, int NC>
 static hipError_t launch_nc(const MatvecArgs &a, int64_t maxN, size_t lds, hipStream_t s) {
     const int64_t nchunks = a.K / chunk_elems<TYPE>();
-    switch (pick_lpr(nchunks)) {
+    switch (pick_lpr(nchunks, a.lpr)) {
         case 16: return launch_one<TYPE, NC, 16>(a, maxN, lds, s);
         case 32: return launch_one<TYPE, NC, 32>(a, maxN, lds, s);
         default: return launch_one<TYPE, NC, 64>(a, maxN, lds, s);

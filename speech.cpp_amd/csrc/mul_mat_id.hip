@@ -235,22 +235,13 @@ __global__ __launch_bounds__(256) void k_mmid_experts(MulMatIdArgs a) {
     }
 }
 
-// MX_MMID_Q4K=0 keeps Q4_K experts on the mat-vec style kernel (k_mmid_experts).
-static bool mmid_q4k_disabled() {
-    static const bool off = [] {
-        const char *e = getenv("MX_MMID_Q4K");
-        return e && e[0] == '0';
-    }();
-    return off;
-}
-
 template <int TYPE>
 static hipError_t launch_typed(const MulMatIdArgs &a, hipStream_t s) {
     const int64_t nrows = a.T * a.b_ne1;
     hipLaunchKernelGGL(k_mmid_prep<TYPE>, dim3((unsigned)(nrows + 1)), dim3(256), (size_t)a.E * 4, s, a);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    if (TYPE == MX_TYPE_Q4_K && !mmid_q4k_disabled() && mmid_q4k_supported(a)) return launch_mmid_q4k(a, s);
+    if (TYPE == MX_TYPE_Q4_K && !a.generic && mmid_q4k_supported(a)) return launch_mmid_q4k(a, s);
     const int64_t npairs = a.n_ids * a.T;
     const unsigned gy = (unsigned)(npairs < a.E ? npairs : a.E);
     const size_t lds = act_lds_bytes(TYPE, a.K, MAX_COLS);
@@ -265,17 +256,9 @@ static hipError_t launch_typed(const MulMatIdArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Up to this many (token, slot) pairs run as one mat-vec launch per pair (MX_MMID_MATVEC_PAIRS overrides): each pair
-// streams its expert's rows with the activation quantized in the prologue, so a decode step's MUL_MAT_ID is a single
-// launch. More pairs go through the bucket and share each expert's weights between them.
-static int64_t mmid_matvec_pairs() {
-    static const int64_t v = [] {
-        const char *e = getenv("MX_MMID_MATVEC_PAIRS");
-        return e ? (int64_t)atoll(e) : (int64_t)16;
-    }();
-    return v;
-}
-
+// Up to a.matvec_pairs (token, slot) pairs (16 unless a backend's option says otherwise) run as one mat-vec launch
+// per pair: each pair streams its expert's rows with the activation quantized in the prologue, so a decode step's
+// MUL_MAT_ID is a single launch. More pairs go through the bucket and share each expert's weights between them.
 static hipError_t launch_matvec_ids(const MulMatIdArgs &a, hipStream_t s) {
     MatvecArgs m{};
     m.type = a.type;
@@ -305,12 +288,13 @@ static hipError_t launch_matvec_ids(const MulMatIdArgs &a, hipStream_t s) {
     m.n_mats = (int)a.E;
     m.x_ne12 = (int)a.b_ne1;
     m.err = a.err;
+    m.lpr = a.lpr;
     return launch_matvec(m, s);
 }
 
 hipError_t launch_mul_mat_id(const MulMatIdArgs &a, hipStream_t s) {
     if (a.n_ids * a.T == 0 || a.N == 0) return hipSuccess;
-    if (a.n_ids * a.T <= mmid_matvec_pairs()) return launch_matvec_ids(a, s);
+    if (a.n_ids * a.T <= a.matvec_pairs) return launch_matvec_ids(a, s);
     switch (a.type) {
         case MX_TYPE_Q8_0: return launch_typed<MX_TYPE_Q8_0>(a, s);
         case MX_TYPE_Q4_K: return launch_typed<MX_TYPE_Q4_K>(a, s);

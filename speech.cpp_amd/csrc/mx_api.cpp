@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <string>
 
 #include "mx_common.h"
@@ -20,14 +21,18 @@ struct mx_backend {
                                      // out of range
     void *scratch = nullptr;         // grows on demand outside graph capture
     size_t scratch_size = 0;
+    uint64_t scratch_gen = 0;        // counts scratch reallocations: a graph recorded before one holds a freed address
     uint8_t *staging = nullptr;      // device staging for ggml-layout uploads and downloads
     size_t staging_size = 0;
     bool capturing = false;
+    mx::Options opt;                 // kernel choices (mx_backend_set_option)
 };
 
 struct mx_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    const mx_backend *be = nullptr;  // the backend whose stream and scratch the recorded kernels use
+    uint64_t scratch_gen = 0;        // be->scratch_gen when recorded
 };
 
 struct mx_event {
@@ -174,6 +179,7 @@ int ensure_scratch(mx_backend *be, size_t bytes) {
     be->scratch = nullptr;
     be->scratch_size = 0;
     const size_t size = std::max<size_t>(mx::align_up(bytes + bytes / 2, 1 << 20), 1 << 20);
+    be->scratch_gen++;  // graphs recorded before this point hold the freed address
     HIP_OK(hipMalloc(&be->scratch, size), "allocate scratch");
     be->scratch_size = size;
     return MX_SUCCESS;
@@ -252,6 +258,66 @@ MX_API void mx_backend_free(mx_backend *be) {
 }
 
 MX_API void *mx_backend_stream(mx_backend *be) { return be ? (void *)be->stream : nullptr; }
+
+MX_API int mx_backend_set_option(mx_backend *be, int option, int64_t value) {
+    if (!be) return fail(MX_INVALID, "null backend");
+    mx::Options &o = be->opt;
+    auto in = [&](std::initializer_list<int64_t> ok) {
+        for (int64_t v : ok)
+            if (v == value) return true;
+        return false;
+    };
+    switch (option) {
+        case MX_OPT_GEMM_Q8_0:
+            if (!in({0, 1})) break;
+            o.gemm_q8_0 = (int)value;
+            return MX_SUCCESS;
+        case MX_OPT_GEMM_KQUANT:
+            if (!in({0, 1})) break;
+            o.gemm_kquant = (int)value;
+            return MX_SUCCESS;
+        case MX_OPT_GEMM_TILE_M:
+        case MX_OPT_GEMM_TILE_N:
+            if (!in({0, 64, 128})) break;
+            (option == MX_OPT_GEMM_TILE_M ? o.tile_m : o.tile_n) = (int)value;
+            return MX_SUCCESS;
+        case MX_OPT_GEMM_SPLIT:
+            if (value < 0 || value > 64) break;
+            o.split = (int)value;
+            return MX_SUCCESS;
+        case MX_OPT_MATVEC_LPR:
+            if (!in({0, 16, 32, 64})) break;
+            o.matvec_lpr = (int)value;
+            return MX_SUCCESS;
+        case MX_OPT_MMID_KERNEL:
+            if (!in({0, 1})) break;
+            o.mmid_kernel = (int)value;
+            return MX_SUCCESS;
+        case MX_OPT_MMID_MATVEC_PAIRS:
+            if (value < 0 || value > 4096) break;
+            o.mmid_matvec_pairs = value;
+            return MX_SUCCESS;
+        default:
+            return fail(MX_INVALID, "unknown option %d", option);
+    }
+    return fail(MX_INVALID, "option %d cannot take the value %lld", option, (long long)value);
+}
+
+MX_API int mx_backend_get_option(mx_backend *be, int option, int64_t *value) {
+    if (!be || !value) return fail(MX_INVALID, "null argument");
+    const mx::Options &o = be->opt;
+    switch (option) {
+        case MX_OPT_GEMM_Q8_0: *value = o.gemm_q8_0; return MX_SUCCESS;
+        case MX_OPT_GEMM_KQUANT: *value = o.gemm_kquant; return MX_SUCCESS;
+        case MX_OPT_GEMM_TILE_M: *value = o.tile_m; return MX_SUCCESS;
+        case MX_OPT_GEMM_TILE_N: *value = o.tile_n; return MX_SUCCESS;
+        case MX_OPT_GEMM_SPLIT: *value = o.split; return MX_SUCCESS;
+        case MX_OPT_MATVEC_LPR: *value = o.matvec_lpr; return MX_SUCCESS;
+        case MX_OPT_MMID_KERNEL: *value = o.mmid_kernel; return MX_SUCCESS;
+        case MX_OPT_MMID_MATVEC_PAIRS: *value = o.mmid_matvec_pairs; return MX_SUCCESS;
+        default: return fail(MX_INVALID, "unknown option %d", option);
+    }
+}
 
 MX_API int mx_backend_set_rounding(mx_backend *be, int rounding) {
     if (!be) return fail(MX_INVALID, "null backend");
@@ -577,7 +643,8 @@ static int gemm_group(mx_backend *be, int n, const mx_tensor *const *src0, const
                 const int64_t N = src0[i]->ne[1];
                 const mx::WPlanes w = matrix_planes(src0[i], i12 / r2 + (i13 / r3) * src0[i]->ne[2]);
                 float *y = (float *)((uint8_t *)dst[i]->data + i12 * dst[i]->nb[2] + i13 * dst[i]->nb[3]);
-                HIP_OK(mx::launch_gemm(src0[i]->type, w, M, N, K, xq, xd, y, (int64_t)(dst[i]->nb[1] / 4), be->stream),
+                HIP_OK(mx::launch_gemm(src0[i]->type, w, M, N, K, xq, xd, y, (int64_t)(dst[i]->nb[1] / 4), be->opt,
+                                       be->stream),
                        "GEMM launch");
             }
         }
@@ -608,15 +675,6 @@ static int gemm_kq_group(mx_backend *be, int n, const mx_tensor *const *src0, co
     return MX_SUCCESS;
 }
 
-// MX_GEMM_Q4K=0 sends Q4_K prefill to the VALU-scaled kernel (k_gemm_kq) instead.
-static bool gemm_q4k_disabled() {
-    static const bool off = [] {
-        const char *e = getenv("MX_GEMM_Q4K");
-        return e && e[0] == '0';
-    }();
-    return off;
-}
-
 // M > 8 on Q4_K weights: per batch slice, activations quantized once, then one launch for the whole group.
 static int gemm_q4k_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
                           const mx_tensor *const *dst) {
@@ -639,7 +697,7 @@ static int gemm_q4k_group(mx_backend *be, int n, const mx_tensor *const *src0, c
                 y[i] = (float *)((uint8_t *)dst[i]->data + i12 * dst[i]->nb[2] + i13 * dst[i]->nb[3]);
                 ldy[i] = (int64_t)(dst[i]->nb[1] / 4);
             }
-            HIP_OK(mx::launch_gemm_q4k(n, w, N, y, ldy, M, K, be->scratch, be->stream),
+            HIP_OK(mx::launch_gemm_q4k(n, w, N, y, ldy, M, K, be->scratch, be->opt, be->stream),
                    "Q4_K GEMM launch");
         }
     return MX_SUCCESS;
@@ -653,7 +711,7 @@ static int gemm_dq_group(mx_backend *be, int n, const mx_tensor *const *src0, co
     const int64_t K = w0->ne[0], M = src1->ne[1];
     int64_t Ns[4];
     for (int i = 0; i < n; i++) Ns[i] = src0[i]->ne[1];
-    int rc = ensure_scratch(be, mx::gemm_dq_scratch_bytes(n, Ns, M, K));
+    int rc = ensure_scratch(be, mx::gemm_dq_scratch_bytes(n, Ns, M, K, be->opt));
     if (rc) return rc;
     const int64_t r2 = src1->ne[2] / w0->ne[2], r3 = src1->ne[3] / w0->ne[3];
     for (int64_t i13 = 0; i13 < src1->ne[3]; i13++)
@@ -671,7 +729,8 @@ static int gemm_dq_group(mx_backend *be, int n, const mx_tensor *const *src0, co
                 y[i] = (float *)((uint8_t *)dst[i]->data + i12 * dst[i]->nb[2] + i13 * dst[i]->nb[3]);
                 ldy[i] = (int64_t)(dst[i]->nb[1] / 4);
             }
-            HIP_OK(mx::launch_gemm_dq(w0->type, n, w, N, y, ldy, M, K, be->scratch, be->stream), "GEMM launch");
+            HIP_OK(mx::launch_gemm_dq(w0->type, n, w, N, y, ldy, M, K, be->scratch, be->opt, be->stream),
+                   "GEMM launch");
         }
     return MX_SUCCESS;
 }
@@ -697,20 +756,31 @@ static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, con
     a.y_b3 = (int64_t)(dst[0]->nb[3] / 4);
     a.nprob = n;
     const int64_t M = src1->ne[1];
+    a.lpr = be->opt.matvec_lpr;
     if (f) {
         a.glu_b = f->glu_b ? (const float *)f->glu_b->data : nullptr;
         a.norm_w = f->norm_w ? (const float *)f->norm_w->data : nullptr;
         a.norm_eps = f->norm_eps;
     }
-    if (M > mx::MAX_COLS && mx::gemm_dq_supported(a.type, M, a.K)) {
+    if (M > mx::MAX_COLS) {
+        // The GEMM each weight type takes at M > 8 (a backend's options may force another one; a product the forced
+        // kernel cannot compute is refused rather than sent elsewhere, so a test of a forced kernel tests it).
+        const mx::Options &o = be->opt;
         bool fits = true;  // every weight's rows within 32-bit element offsets
         for (int i = 0; i < n; i++) fits = fits && src0[i]->ne[1] * a.K < ((int64_t)1 << 31);
-        if (fits) return gemm_dq_group(be, n, src0, src1, dst);
+        if (a.type == MX_TYPE_Q8_0 && o.gemm_q8_0 == 1) {
+            if (!mx::gemm_supported(a.type, a.K)) return fail(MX_UNSUPPORTED, "int8 Q8_0 GEMM: K must be a multiple of 128");
+            return gemm_group(be, n, src0, src1, dst);
+        }
+        if ((a.type == MX_TYPE_Q4_K || a.type == MX_TYPE_Q6_K) && o.gemm_kquant == 1) {
+            if (!mx::gemm_kq_supported(a.type, a.K)) return fail(MX_UNSUPPORTED, "int8 K-quant GEMM: K % 256");
+            return gemm_kq_group(be, n, src0, src1, dst);
+        }
+        if (fits && mx::gemm_dq_supported(a.type, M, a.K)) return gemm_dq_group(be, n, src0, src1, dst);
+        if (mx::gemm_supported(a.type, a.K)) return gemm_group(be, n, src0, src1, dst);
+        if (a.type == MX_TYPE_Q4_K && a.K % 256 == 0) return gemm_q4k_group(be, n, src0, src1, dst);
+        if (mx::gemm_kq_supported(a.type, a.K)) return gemm_kq_group(be, n, src0, src1, dst);
     }
-    if (M > mx::MAX_COLS && mx::gemm_supported(a.type, a.K)) return gemm_group(be, n, src0, src1, dst);
-    if (M > mx::MAX_COLS && a.type == MX_TYPE_Q4_K && a.K % 256 == 0 && !gemm_q4k_disabled())
-        return gemm_q4k_group(be, n, src0, src1, dst);
-    if (M > mx::MAX_COLS && mx::gemm_kq_supported(a.type, a.K)) return gemm_kq_group(be, n, src0, src1, dst);
     const int ncmax = max_cols(a.type, a.K);
     for (int64_t m0 = 0; m0 < M; m0 += ncmax) {
         a.ncols = (int)std::min<int64_t>(ncmax, M - m0);
@@ -813,6 +883,9 @@ MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b
     a.dst = (float *)dst->data;
     a.dst_nb1 = (int64_t)dst->nb[1];
     a.dst_nb2 = (int64_t)dst->nb[2];
+    a.generic = be->opt.mmid_kernel;
+    a.matvec_pairs = be->opt.mmid_matvec_pairs;
+    a.lpr = be->opt.matvec_lpr;
     if (a.n_ids * a.T == 0) return MX_SUCCESS;
     const size_t need = mx::mul_mat_id_scratch(&a, nullptr);
     if ((rc = ensure_scratch(be, need))) return rc;
@@ -1100,6 +1173,8 @@ MX_API int mx_graph_end(mx_backend *be, mx_graph **graph) {
     HIP_OK(hipStreamEndCapture(be->stream, &g), "end capture");
     mx_graph *out = new mx_graph();
     out->graph = g;
+    out->be = be;
+    out->scratch_gen = be->scratch_gen;
     hipError_t e = hipGraphInstantiate(&out->exec, g, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         (void)hipGraphDestroy(g);
@@ -1114,12 +1189,21 @@ MX_API int mx_graph_launch(mx_backend *be, mx_graph *graph) {
     int rc = check_be(be);
     if (rc) return rc;
     if (!graph) return fail(MX_INVALID, "null graph");
+    if (graph->be != be) return fail(MX_INVALID, "the graph was recorded on another backend");
+    if (graph->scratch_gen != be->scratch_gen)
+        return fail(MX_FAILED, "the graph was recorded before an op grew the backend's scratch (its kernels hold the "
+                               "freed buffer); record it again");
     HIP_OK(hipGraphLaunch(graph->exec, be->stream), "launch graph");
     return MX_SUCCESS;
 }
 
 MX_API void mx_graph_free(mx_graph *graph) {
     if (!graph) return;
+    // a replay may still be running on the recording backend's stream: let it finish before its exec goes
+    if (graph->be && graph->be->stream) {
+        (void)hipSetDevice(graph->be->device);
+        (void)hipStreamSynchronize(graph->be->stream);
+    }
     if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
     if (graph->graph) (void)hipGraphDestroy(graph->graph);
     delete graph;

@@ -102,6 +102,20 @@ inline WPlanes wplanes(const void *base, const Planes &pl) {
 }
 
 // ------------------------------------------------------------------------------------------------------------------
+// Kernel choices of one backend (mx_backend_set_option). Zero everywhere is the dispatcher's own pick; a forced
+// choice reaches one kernel so that every kernel the dispatcher can pick is testable in one process.
+// ------------------------------------------------------------------------------------------------------------------
+struct Options {
+    int gemm_q8_0 = 0;              // Q8_0 at M > 8: 0 the fp16 dequantizing GEMM, 1 the int8 MFMA GEMM
+    int gemm_kquant = 0;            // Q4_K / Q6_K at M > 8: 0 as picked, 1 the VALU-scaled int8 GEMM (k_gemm_kq)
+    int tile_m = 0, tile_n = 0;     // GEMM tile (0: picked per product)
+    int split = 0;                  // K splits of the fp16 dequantizing GEMM (0: picked)
+    int matvec_lpr = 0;             // lanes per row of the mat-vec: 16, 32 or 64 (0: picked)
+    int mmid_kernel = 0;            // MUL_MAT_ID with many pairs: 0 as picked, 1 the generic experts kernel
+    int64_t mmid_matvec_pairs = 16; // MUL_MAT_ID runs as one mat-vec launch up to this many (token, slot) pairs
+};
+
+// ------------------------------------------------------------------------------------------------------------------
 // Kernel launchers (defined in the .hip files). All run on `s`. Return hipError_t of the launch.
 // ------------------------------------------------------------------------------------------------------------------
 // Scatter `n` ggml-layout bytes (from device staging `src`), which are bytes [offset, offset + n) of a tensor of
@@ -176,33 +190,33 @@ struct MatvecArgs {
     const float *glu_b;
     const float *norm_w;
     float norm_eps;
+    int lpr;               // lanes per row forced (16, 32, 64), or 0 to pick by K
 };
 hipError_t launch_matvec(const MatvecArgs &a, hipStream_t s);
 // The same products on F16 / F32 weights in ggml's row-major layout (prob[i].w.p0 = the weight's data; K % 8 == 0 for
 // F16, K % 4 == 0 for F32; no ids mode).
 hipError_t launch_matvec_f(const MatvecArgs &a, hipStream_t s);
 
-// Prefill GEMM (M > 8): activations quantized once into scratch (gemm_act_bytes of quants, int8 or fp16 values by
-// gemm_mode(), plus M * K/32 fp32 block scales), then MFMA tiles.
-int gemm_mode();
+// Prefill GEMM on int8 MFMA (Q8_0, M > 8): activations quantized once into scratch (gemm_act_bytes of int8 quants,
+// plus M * K/32 fp32 block scales), then MFMA tiles. A forced tile the kernel lacks is refused (hipErrorInvalidValue).
 size_t gemm_act_bytes(int64_t M, int64_t K);
 hipError_t launch_gemm_quant(int type, int rounding, const float *x, int64_t x_stride, int64_t M, int64_t K,
                              void *xq, float *xd, hipStream_t s);
 hipError_t launch_gemm(int type, const WPlanes &w, int64_t M, int64_t N, int64_t K, const void *xq, const float *xd,
-                       float *y, int64_t ldy, hipStream_t s);
+                       float *y, int64_t ldy, const Options &o, hipStream_t s);
 inline bool gemm_supported(int type, int64_t K) { return type == MX_TYPE_Q8_0 && K % 128 == 0; }
 
 // Prefill GEMM on the fp16 matrix cores over dequantized tiles (Q8_0 weights): launch_gemm_dq_act writes the
 // activations' quantized values as fp16 at the start of `scratch`, launch_gemm_dq runs up to four weights sharing
 // them in one launch (plus a reduce launch when K is split; the partial sums follow the activations in scratch).
-// gemm_dq_scratch_bytes is the scratch both need. MX_GEMM_DQ=0 turns it off (the int8 kernel then runs).
+// gemm_dq_scratch_bytes is the scratch both need (for the tile and split `o` forces, or those picked).
 bool gemm_dq_supported(int type, int64_t M, int64_t K);
 size_t gemm_dq_act_bytes(int64_t M, int64_t K);
-size_t gemm_dq_scratch_bytes(int nprob, const int64_t *N, int64_t M, int64_t K);
+size_t gemm_dq_scratch_bytes(int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o);
 hipError_t launch_gemm_dq_act(int type, int rounding, const float *x, int64_t x_stride, int64_t M, int64_t K,
                               void *scratch, hipStream_t s);
 hipError_t launch_gemm_dq(int type, int nprob, const WPlanes *w, const int64_t *N, float *const *y,
-                          const int64_t *ldy, int64_t M, int64_t K, void *scratch, hipStream_t s);
+                          const int64_t *ldy, int64_t M, int64_t K, void *scratch, const Options &o, hipStream_t s);
 
 // Prefill GEMM on Q4_K / Q6_K weights: launch_gemm_kq_quant writes x (M rows of K floats, row stride x_stride) as
 // Q8_K into `scratch` (gemm_kq_act_bytes), launch_gemm_kq multiplies it into y (row stride ldy).
@@ -216,7 +230,7 @@ hipError_t launch_gemm_kq(int type, const WPlanes &w, int64_t M, int64_t N, int6
 size_t gemm_q4k_act_bytes(int64_t M, int64_t K);
 hipError_t launch_gemm_q4k_quant(const float *x, int64_t x_stride, int64_t M, int64_t K, void *scratch, hipStream_t s);
 hipError_t launch_gemm_q4k(int nprob, const WPlanes *w, const int64_t *N, float *const *y, const int64_t *ldy,
-                           int64_t M, int64_t K, const void *scratch, hipStream_t s);
+                           int64_t M, int64_t K, const void *scratch, const Options &o, hipStream_t s);
 inline bool gemm_kq_supported(int type, int64_t K) {
     return (type == MX_TYPE_Q4_K || type == MX_TYPE_Q6_K) && K % 256 == 0;
 }
@@ -248,6 +262,9 @@ struct MulMatIdArgs {
     int32_t *ntiles;       // [1] tiles written by the bucket kernel
     int64_t max_tiles;
     int *err;
+    int generic;               // 1: the generic experts kernel even where a specialised one exists
+    int64_t matvec_pairs;      // up to this many pairs: one mat-vec launch, no bucketing
+    int lpr;                   // mat-vec lanes per row forced, or 0
 };
 // Row-wise ops on f32 rows (layer.hip): src / dst rows (i1, i2, i3) at byte strides, ne0 contiguous floats.
 struct RowsArgs {

@@ -39,11 +39,23 @@ struct BufferCtx {
     size_t size = 0;
 };
 
-// One step of the last graph computed, to recognise a graph computed again with the same tensors.
-struct NodeKey {
-    int op;
-    const void *data[4];
+// What one tensor of a node contributes to the key of a graph: every field a launch reads -- its type, shape, byte
+// strides, data address and view offset.
+struct TensorKey {
+    int32_t type;
+    int32_t pad_;
     int64_t ne[4];
+    uint64_t nb[4];
+    const void *data;
+    uint64_t view_offs;
+};
+
+// One step of the last graph computed, to recognise a graph computed again with the same tensors: the node (with its
+// operation parameters: eps, RoPE's dims / mode / bases, attention's scale) and its first five sources.
+struct NodeKey {
+    int32_t op;
+    int32_t op_params[GGML_MAX_OP_PARAMS / sizeof(int32_t)];
+    TensorKey t[6];
     bool operator==(const NodeKey &o) const { return std::memcmp(this, &o, sizeof(NodeKey)) == 0; }
 };
 
@@ -312,23 +324,37 @@ int run_nodes(BackendCtx *ctx, ggml_cgraph *cgraph) {
     return MX_SUCCESS;
 }
 
+void key_of(const ggml_tensor *t, TensorKey &k) {
+    if (!t) return;  // stays zero
+    k.type = (int32_t)t->type;
+    for (int d = 0; d < 4; d++) {
+        k.ne[d] = t->ne[d];
+        k.nb[d] = (uint64_t)t->nb[d];
+    }
+    k.data = t->data;
+    k.view_offs = (uint64_t)t->view_offs;
+}
+
 std::vector<NodeKey> keys_of(ggml_cgraph *cgraph) {
     std::vector<NodeKey> keys;
     for (int i = 0; i < ggml_graph_n_nodes(cgraph); i++) {
         const ggml_tensor *t = ggml_graph_node(cgraph, i);
         NodeKey k;
         std::memset(&k, 0, sizeof k);
-        k.op = (int)t->op;
-        k.data[0] = t->data;
-        for (int s = 0; s < 3; s++) k.data[s + 1] = t->src[s] ? t->src[s]->data : nullptr;
-        for (int d = 0; d < 4; d++) k.ne[d] = t->ne[d];
+        k.op = (int32_t)t->op;
+        std::memcpy(k.op_params, t->op_params, sizeof k.op_params);
+        key_of(t, k.t[0]);
+        for (int s = 0; s < 5; s++) key_of(t->src[s], k.t[s + 1]);
         keys.push_back(k);
     }
     return keys;
 }
 
 // The same graph over the same tensors computed again (the kept decode-step graph, src/common/qwen3-decoder.cpp:
-// 187-208) is recorded once its scratch has its final size and replayed with one launch from then on.
+// 187-208) is recorded once its scratch has its final size and replayed with one launch from then on. A graph that
+// differs in any node's op, parameters, or any tensor's type, shape, strides, address or view offset is computed
+// eagerly and the recording dropped (mx_graph_free waits for a replay still in flight). A recording libmx refuses
+// because the scratch grew since (MX_FAILED) is recorded again on the next identical graph.
 enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgraph) {
     auto *ctx = (BackendCtx *)backend->context;
     std::vector<NodeKey> keys = keys_of(cgraph);
@@ -340,7 +366,13 @@ enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgra
         mx_graph_free(ctx->replay);
         ctx->replay = nullptr;
     }
-    if (ctx->replay) return to_status(mx_graph_launch(ctx->be, ctx->replay));
+    if (ctx->replay) {
+        const int rc = mx_graph_launch(ctx->be, ctx->replay);
+        if (rc == MX_SUCCESS) return GGML_STATUS_SUCCESS;
+        mx_graph_free(ctx->replay);  // recorded before the scratch grew: compute eagerly, record again next time
+        ctx->replay = nullptr;
+        ctx->repeats = 1;
+    }
     if (ctx->repeats >= 2) {
         int rc = mx_graph_begin(ctx->be);
         if (rc == MX_SUCCESS) {

@@ -26,10 +26,10 @@ def bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
 
 def dq_row_exp(amax: np.ndarray) -> np.ndarray:
     """The power of two the fp16 GEMM scales an activation row by: 2^e puts the row's largest |value| in
-    [2^14, 2^15) (e = 0 for an all-zero row; e within [-126, 127])."""
+    [2^14, 2^15) (e = 0 for an all-zero row; e within [-126, 126], so 2^-e is a normal float)."""
     _, ex = np.frexp(amax.astype(np.float64))  # amax = f 2^ex, f in [0.5, 1)
     e = np.where(amax > 0, 15 - ex, 0)
-    return np.clip(e, -126, 127)
+    return np.clip(e, -126, 126)
 
 
 def dq_model(oracle, wtype: int, w: np.ndarray, x: np.ndarray, K: int, rounding: int = 0) -> np.ndarray:

@@ -81,7 +81,8 @@ def broken(tmp_path, name, blob):
 
 
 @pytest.mark.parametrize("case", ["magic", "version", "truncated_header", "data_past_end", "misaligned", "unknown_type",
-                                  "partial_block", "alignment", "counts", "string_length", "ndims"])
+                                  "partial_block", "alignment", "counts", "string_length", "ndims", "wrapped_shape",
+                                  "string_array"])
 def test_broken_files_are_refused(mx, tmp_path, case):
     tensors = tensor_set()[:3]
     blob, start = gguf_bytes(KVS[:3], tensors, alignment=64)
@@ -119,6 +120,19 @@ def test_broken_files_are_refused(mx, tmp_path, case):
     elif case == "ndims":
         blob, _ = gguf_bytes(KVS[:3], [("w", O.TYPE_F32, (4, 1, 1, 1, 1), bytes(16))], alignment=64)
         why = "dimensions"
+    elif case == "wrapped_shape":
+        # 4 * 2^32 * 2^32 * 2^32 * 2^30 bytes is 2^128: exactly 0 in 128-bit arithmetic, so only checked multiplies
+        # refuse it
+        blob, _ = gguf_bytes(KVS[:3], [("w", O.TYPE_F32, (1 << 32, 1 << 32, 1 << 32, 1 << 30), bytes(64))],
+                             alignment=64)
+        why = "larger than the file"
+    elif case == "string_array":
+        # an array of strings whose count fits the remaining bytes but not 8 bytes of length per string
+        kv = [("general.architecture", STRING, "x"), ("t.strs", ARRAY, (STRING, ["ab"] * 3))]
+        blob, _ = gguf_bytes(kv, tensors[:1], alignment=64)
+        at = blob.index(b"t.strs") + len(b"t.strs") + 4 + 4   # past the key, the value type and the element type
+        blob = blob[:at] + (len(blob) - at - 16).to_bytes(8, "little") + blob[at + 8:]
+        why = "an array runs past the end"
     with pytest.raises(mx.MxError) as e:
         mx.Gguf(broken(tmp_path, case + ".gguf", blob))
     assert why in str(e.value)

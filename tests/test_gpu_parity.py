@@ -15,21 +15,23 @@ pytestmark = pytest.mark.gpu
 
 TOL = 1e-3         # the parity bar
 TIGHT = 2e-5       # what exact integer sums with an fp32 cross-block sum give
-DQ = __import__("os").environ.get("MX_GEMM_DQ", "1") != "0"
 
 
-def uses_dq(t, M, K):
-    """Whether MUL_MAT takes the dequantizing fp16 GEMM (its dispatch rule)."""
-    return DQ and M > 8 and ((t == O.TYPE_Q8_0 and K % 64 == 0) or (t in (O.TYPE_Q5_K, O.TYPE_Q6_K) and K % 256 == 0))
+def uses_dq(t, M, K, int8=False):
+    """Whether MUL_MAT takes the dequantizing fp16 GEMM (its dispatch rule; int8: an int8 GEMM forced by the backend's
+    options)."""
+    return not int8 and M > 8 and ((t == O.TYPE_Q8_0 and K % 64 == 0) or
+                                   (t in (O.TYPE_Q5_K, O.TYPE_Q6_K) and K % 256 == 0))
 
 
-def check_product(t, w, x, y, K, rounding=O.ROUND_REF):
+def check_product(t, w, x, y, K, rounding=O.ROUND_REF, int8=False, y_ref=None):
     """Parity of one product. The integer paths sum the oracle's exact per-block integers: held to TIGHT. The
     dequantizing fp16 GEMM rounds each operand to fp16 once: held to TOL against the oracle and to TIGHT against a
     model of exactly that rounding, which a dropped or misplaced term would miss by far more."""
     M = x.shape[0]
-    y_ref = O.mul_mat(t, w, x, rounding=rounding)
-    if uses_dq(t, M, K):
+    if y_ref is None:
+        y_ref = O.mul_mat(t, w, x, rounding=rounding)
+    if uses_dq(t, M, K, int8):
         assert rel_err(y, y_ref) <= TOL
         assert l2_rel(y, y_ref) <= TOL
         assert rel_err(y, dq_model(O, t, w, x, K, rounding)) <= TIGHT
