@@ -179,6 +179,18 @@ MX_API int mx_get_rows(mx_backend *be, const mx_tensor *src0, const mx_tensor *i
 MX_API int mx_mul_mat(mx_backend *be, const mx_tensor *src0, const mx_tensor *src1, const mx_tensor *dst);
 MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids,
                          const mx_tensor *dst);
+/* MUL_MAT_ID that allocates nothing. No counterpart in speech.cpp or ggml's backend interface: for callers that
+ * cannot allocate device memory -- code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * The same products as mx_mul_mat_id, on the same kernels and with the same results, but its scratch (the bucketing
+ * tables, the quantized activation rows, the chunk list) lives in a static device array of MX_NOALLOC_SCRATCH_BYTES
+ * that each GPU holds from the first mx_backend_init on it until the process ends; the call itself calls no
+ * allocator. A call needing more scratch (mx_mul_mat_id_noalloc_bytes) fails with MX_UNSUPPORTED. Every call on one
+ * GPU shares that GPU's array, which keeps the last call's contents (each call writes everything it reads before
+ * reading it): calls that overlap on one GPU -- two streams, two backends -- race. */
+#define MX_NOALLOC_SCRATCH_BYTES (16u << 20)
+MX_API size_t mx_mul_mat_id_noalloc_bytes(const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids);
+MX_API int mx_mul_mat_id_noalloc(mx_backend *be, const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids,
+                                 const mx_tensor *dst);
 /* ARGMAX: dst[r] = the index of the largest value of row r of src, the first of equal ones, as speech.cpp's ggml
  * fork computes GGML_OP_ARGMAX (src/families/fastconformer/decoder.cpp:56-62 first_argmax states the rule; the
  * decoder's greedy pick, src/common/qwen3-decoder.cpp:426-429,501, reads back these four bytes per row instead of the

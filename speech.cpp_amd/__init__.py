@@ -49,8 +49,9 @@ EXPORTS = [
     "mx_gguf_get_int", "mx_gguf_get_float", "mx_gguf_get_arr", "mx_gguf_get_arr_str", "mx_gguf_load_tensor",
     "mx_rms_norm", "mx_binary", "mx_swiglu", "mx_supports_rope", "mx_rope", "mx_set_rows", "mx_supports_flash_attn_ext",
     "mx_flash_attn_ext", "mx_mul_mat_fused", "mx_qk_norm_rope_kv", "mx_attn_decode", "mx_decoder_new", "mx_decoder_free",
-    "mx_decoder_step",
+    "mx_decoder_step", "mx_mul_mat_id_noalloc", "mx_mul_mat_id_noalloc_bytes",
 ]
+NOALLOC_SCRATCH_BYTES = 16 << 20  # MX_NOALLOC_SCRATCH_BYTES
 
 
 def row_size(t: int, ne0: int) -> int:
@@ -185,6 +186,8 @@ def lib():
         "mx_decoder_new": ([vp, ctypes.POINTER(MxQwen3)], vp),
         "mx_decoder_free": ([vp], None),
         "mx_decoder_step": ([vp, P, P, P, P], i32),
+        "mx_mul_mat_id_noalloc": ([vp, P, P, P, P], i32),
+        "mx_mul_mat_id_noalloc_bytes": ([P, P, P], sz),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -389,6 +392,10 @@ class Backend:
 
     def mul_mat_id(self, as_: Tensor, b: Tensor, ids: Tensor, dst: Tensor) -> None:
         check(lib().mx_mul_mat_id(self.h, as_.ref(), b.ref(), ids.ref(), dst.ref()))
+
+    def mul_mat_id_noalloc(self, as_: Tensor, b: Tensor, ids: Tensor, dst: Tensor) -> None:
+        """MUL_MAT_ID on the GPU's static scratch: allocates nothing (mx_mul_mat_id_noalloc)."""
+        check(lib().mx_mul_mat_id_noalloc(self.h, as_.ref(), b.ref(), ids.ref(), dst.ref()))
 
     def argmax(self, src: Tensor, dst: Tensor) -> None:
         check(lib().mx_argmax(self.h, src.ref(), dst.ref()))

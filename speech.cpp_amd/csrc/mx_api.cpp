@@ -8,6 +8,7 @@
 #include <cstring>
 #include <initializer_list>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -174,6 +175,38 @@ bool f32_rows_ok(const mx_tensor *x) {
            x->nb[3] % 16 == 0 && aligned16(x->data) && x->ne[0] % 4 == 0;
 }
 
+// The scratch of the entry point that allocates nothing (mx_mul_mat_id_noalloc): a static device array, one copy per
+// GPU, held until the process ends. Host code never passes `scratch` itself to a kernel (in host code the name is a
+// stand-in, not a device address): mx_backend_init looks up each device's copy once, with that device current, and
+// the entry point uses that address.
+constexpr int kNoAllocDevices = 64;
+std::mutex g_noalloc_mu;
+bool g_noalloc_done[kNoAllocDevices] = {};
+void *g_noalloc_ptr[kNoAllocDevices] = {};
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[MX_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// With `device` current: its copy of `scratch`, looked up on the first call for the device.
+void noalloc_setup(int device) {
+    if (device < 0 || device >= kNoAllocDevices) return;
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (g_noalloc_done[device]) return;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_noalloc_ptr[device] = e == hipSuccess ? p : nullptr;
+    g_noalloc_done[device] = true;
+}
+
+void *noalloc_scratch(int device) {
+    if (device < 0 || device >= kNoAllocDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    return g_noalloc_ptr[device];
+}
+
 int check_be(mx_backend *be) {
     if (!be) return fail(MX_INVALID, "null backend");
     if (hipSetDevice(be->device) != hipSuccess) return fail(MX_FAILED, "cannot select device %d", be->device);
@@ -245,6 +278,7 @@ MX_API mx_backend *mx_backend_init(int device) {
         fail(MX_FAILED, "cannot select device %d", device);
         return nullptr;
     }
+    noalloc_setup(device);
     mx_backend *be = new mx_backend();
     be->device = device;
     if (hipStreamCreateWithFlags(&be->stream, hipStreamNonBlocking) != hipSuccess ||
@@ -871,14 +905,11 @@ MX_API int mx_mul_mat_fused(mx_backend *be, int n, const mx_tensor *const *src0,
     return matvec_group(be, n, src0, src1, dst, f);
 }
 
-MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids,
-                         const mx_tensor *dst) {
-    int rc = check_be(be);
-    if (rc) return rc;
-    if (!mx_supports_op(MX_OP_MUL_MAT_ID, as, b, ids, dst))
-        return fail(MX_UNSUPPORTED, "MUL_MAT_ID: unsupported types, shapes or strides");
+// The launch arguments of a MUL_MAT_ID (scratch not yet carved).
+static void mmid_args(mx_backend *be, const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids,
+                      const mx_tensor *dst, mx::MulMatIdArgs &a) {
     const mx::Planes pl = mx::planes_of(as->type, nelements(as));
-    mx::MulMatIdArgs a{};
+    a = mx::MulMatIdArgs{};
     a.type = as->type;
     a.rounding = be->rounding;
     a.w = mx::wplanes(as->data, pl);
@@ -900,11 +931,56 @@ MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b
     a.generic = be->opt.mmid_kernel;
     a.matvec_pairs = be->opt.mmid_matvec_pairs;
     a.lpr = be->opt.matvec_lpr;
+    a.err = be->err;
+}
+
+MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids,
+                         const mx_tensor *dst) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!mx_supports_op(MX_OP_MUL_MAT_ID, as, b, ids, dst))
+        return fail(MX_UNSUPPORTED, "MUL_MAT_ID: unsupported types, shapes or strides");
+    mx::MulMatIdArgs a;
+    mmid_args(be, as, b, ids, dst, a);
     if (a.n_ids * a.T == 0) return MX_SUCCESS;
     const size_t need = mx::mul_mat_id_scratch(&a, nullptr);
     if ((rc = ensure_scratch(be, need))) return rc;
     mx::mul_mat_id_scratch(&a, be->scratch);
-    a.err = be->err;
+    HIP_OK(mx::launch_mul_mat_id(a, be->stream), "MUL_MAT_ID launch");
+    return MX_SUCCESS;
+}
+
+MX_API size_t mx_mul_mat_id_noalloc_bytes(const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids) {
+    if (!as || !b || !ids || !mx::is_quantized(as->type) || !shape_ok(as) || !shape_ok(ids)) return 0;
+    mx::MulMatIdArgs a{};
+    a.type = as->type;
+    a.K = as->ne[0];
+    a.N = as->ne[1];
+    a.E = as->ne[2];
+    a.n_ids = ids->ne[0];
+    a.T = ids->ne[1];
+    a.b_ne1 = b->ne[1];
+    return mx::mul_mat_id_scratch(&a, nullptr);
+}
+
+MX_API int mx_mul_mat_id_noalloc(mx_backend *be, const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids,
+                                 const mx_tensor *dst) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!mx_supports_op(MX_OP_MUL_MAT_ID, as, b, ids, dst))
+        return fail(MX_UNSUPPORTED, "MUL_MAT_ID: unsupported types, shapes or strides");
+    mx::MulMatIdArgs a;
+    mmid_args(be, as, b, ids, dst, a);
+    if (a.n_ids * a.T == 0) return MX_SUCCESS;
+    void *ptr = noalloc_scratch(be->device);
+    if (!ptr) return fail(MX_FAILED, "MUL_MAT_ID without allocating: device %d has no address for its static scratch",
+                          be->device);
+    const size_t need = mx::mul_mat_id_scratch(&a, nullptr);
+    if (need > MX_NOALLOC_SCRATCH_BYTES)
+        return fail(MX_UNSUPPORTED, "MUL_MAT_ID without allocating needs %zu bytes of scratch, above its %u", need,
+                    (unsigned)MX_NOALLOC_SCRATCH_BYTES);
+    // every table and row the kernels read from the scratch is written by the prep launch first: nothing to clear
+    mx::mul_mat_id_scratch(&a, ptr);
     HIP_OK(mx::launch_mul_mat_id(a, be->stream), "MUL_MAT_ID launch");
     return MX_SUCCESS;
 }
