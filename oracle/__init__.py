@@ -61,6 +61,9 @@ def lib():
         for n in ("orc_quantize_row_q8_K", "orc_quantize_row_q4_K", "orc_quantize_row_q5_K", "orc_quantize_row_q6_K"):
             getattr(L, n).argtypes, getattr(L, n).restype = [vp, vp, i64], None
         L.orc_quantize_chunk.argtypes, L.orc_quantize_chunk.restype = [i32, vp, vp, i64, i64, i64], ctypes.c_size_t
+        L.orc_make_qkx2_quants.argtypes = [i32, i32, vp, vp, vp, vp, f32, f32, i32, i32]
+        L.orc_make_qkx2_quants.restype = f32
+        L.orc_make_qx_quants.argtypes, L.orc_make_qx_quants.restype = [i32, i32, vp, vp], f32
         L.orc_dequantize_row.argtypes, L.orc_dequantize_row.restype = [i32, vp, vp, i64], i32
         L.orc_vec_dot.argtypes, L.orc_vec_dot.restype = [i32, i64, vp, vp], f32
         L.orc_vec_dot_exact.argtypes, L.orc_vec_dot_exact.restype = [i32, i64, vp, vp], ctypes.c_double
@@ -149,6 +152,24 @@ def quantize_chunk(t: int, x: np.ndarray) -> np.ndarray:
     if n != out.size:
         raise ValueError("quantize_chunk failed")
     return out
+
+
+def make_qkx2_quants(x: np.ndarray, weights: np.ndarray, nmax: int, rmin: float, rdelta: float, nstep: int):
+    """ggml's make_qkx2_quants on one sub-block (use_mad = 0): (scale, min, codes) with x ~ scale * code + min."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(weights, dtype=np.float32)
+    L = np.zeros(x.size, np.uint8)
+    neg_min = np.zeros(1, np.float32)
+    scale = lib().orc_make_qkx2_quants(x.size, nmax, _p(x), _p(w), _p(L), _p(neg_min), rmin, rdelta, nstep, 0)
+    return np.float32(scale), -neg_min[0], L
+
+
+def make_qx_quants(x: np.ndarray, nmax: int):
+    """ggml's make_qx_quants (rmse_type 1, no importance weights) on one sub-block: (scale, codes - nmax)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    L = np.zeros(x.size, np.int8)
+    scale = lib().orc_make_qx_quants(x.size, nmax, _p(x), _p(L))
+    return np.float32(scale), L.astype(np.int64) - nmax
 
 
 def dequantize_rows(t: int, q: np.ndarray, K: int) -> np.ndarray:

@@ -480,6 +480,18 @@ static float make_qx_quants_rmse1(int n, int nmax, const float *x, int8_t *L) {
     return scale;
 }
 
+float orc_make_qkx2_quants(int n, int nmax, const float *x, const float *weights, uint8_t *L, float *neg_min,
+                           float rmin, float rdelta, int nstep, int use_mad) {
+    uint8_t Laux[256];
+    if (n < 1 || n > 256) return NAN;
+    return make_qkx2_quants(n, nmax, x, weights, L, neg_min, Laux, rmin, rdelta, nstep, use_mad);
+}
+
+float orc_make_qx_quants(int n, int nmax, const float *x, int8_t *L) {
+    if (n < 1 || n > 256) return NAN;
+    return make_qx_quants_rmse1(n, nmax, x, L);
+}
+
 /* ggml-quants.c quantize_row_q6_K_ref */
 void orc_quantize_row_q6_K(const float *x, void *vy, int64_t k) {
     blk_q6_K *y = (blk_q6_K *)vy;

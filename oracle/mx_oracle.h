@@ -58,6 +58,12 @@ void orc_quantize_row_q8_K(const float *x, void *y, int64_t k);
 void orc_quantize_row_q4_K(const float *x, void *y, int64_t k);
 void orc_quantize_row_q5_K(const float *x, void *y, int64_t k);
 void orc_quantize_row_q6_K(const float *x, void *y, int64_t k);
+/* The two candidate searches of the K-quant weight quantizers on one sub-block, exposed for the tests that pin them:
+ * make_qkx2_quants (Q4_K / Q5_K: returns the scale, *neg_min = -min) and make_qx_quants with rmse_type 1 (Q6_K:
+ * returns the scale; L holds code + nmax). n <= 256. */
+float orc_make_qkx2_quants(int n, int nmax, const float *x, const float *weights, uint8_t *L, float *neg_min,
+                           float rmin, float rdelta, int nstep, int use_mad);
+float orc_make_qx_quants(int n, int nmax, const float *x, int8_t *L);
 /* ggml_quantize_chunk(type, src, dst, start, nrows, n_per_row, imatrix = NULL); returns bytes written. */
 size_t orc_quantize_chunk(int type, const float *src, void *dst, int64_t start, int64_t nrows, int64_t n_per_row);
 

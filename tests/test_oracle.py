@@ -8,9 +8,14 @@ model files and dumps that are not in its tree, so the oracle is pinned by:
   * an independent numpy decoder of every block layout, compared bit for bit with the oracle's dequantizers;
   * exact float64 brute force over independently decoded values for every dot, MUL_MAT, MUL_MAT_ID and GET_ROWS;
   * invariants (bsums = sums of quants, quantize(dequantize(b)) == b for full-range Q8_0 blocks);
-  * mutation checks: a plausible mistake (swapped nibbles, a dropped min term, a wrong scale index) fails the checks.
-Parity unpinned: the candidate searches inside make_qkx2_quants / make_qx_quants on generic data (only an import of
-ggml could fix those bytes); the grid fixtures pin everything around them, and the kernels read whatever bytes the
+  * mutation checks: a plausible mistake (swapped nibbles, a dropped min term, a wrong scale index) fails the checks;
+  * for the K-quant weight quantizers on generic data: every code is the nearest point of its sub-block's grid given
+    the packed scales; the packed 6-bit (Q4_K / Q5_K) and int8 (Q6_K) scales and d / dmin are the roundings of the
+    sub-block fits; make_qx_quants's fit is the best of its candidate family (evaluated in float64); make_qkx2_quants
+    agrees bit for bit with an independent numpy statement and never loses to its min-max start -- each with a
+    mutation (another rmin, fewer steps, other weights, a narrower family) shown to fail.
+Parity unpinned: make_qkx2_quants's path-dependent search on generic data is fixed only by two restatements of ggml's
+published algorithm (oracle and numpy); a misreading shared by both would pass. The kernels read whatever bytes the
 quantizer wrote, so their parity does not depend on it.
 """
 import json
@@ -415,3 +420,233 @@ def test_argmax_known_answers():
             ([2.0, 1.0, nan, 2.0], 0)]
     x = np.array([r for r, _ in rows], np.float32)
     assert O.argmax(x).tolist() == [a for _, a in rows]
+
+
+# ------------------------------------------------------------------ the K-quant candidate searches on generic data
+# make_qkx2_quants (Q4_K: nmax 15, rmin -1, rdelta 0.1, 20 steps; Q5_K: nmax 31, rmin -0.5, 15 steps) and
+# make_qx_quants (Q6_K) each return the best of a fixed family of candidate fits. On generic data nothing but ggml
+# could give their bytes, so these checks pin the searches by optimality instead: the oracle's answer must be the
+# best member (within float32 noise) of the family as defined, evaluated independently in float64 numpy, and the
+# packed block must be the rounding of those fits. Mutation checks show that a search over a wrong family (another
+# rmin, fewer steps, other weights) fails the same check.
+QKX2 = {O.TYPE_Q4_K: (15, -1.0, 0.1, 20), O.TYPE_Q5_K: (31, -0.5, 0.1, 15)}
+
+
+def subblocks(n, size, seed):
+    """Sub-blocks of several shapes: normal, shifted so every value is positive or negative, heavy-tailed, small."""
+    base = O.fill_normal(seed, n, size, 0.0, 1.0).astype(np.float64)
+    out = []
+    for i, r in enumerate(base):
+        kind = i % 5
+        r = {0: r, 1: r + 2.5, 2: r - 2.5, 3: r ** 3, 4: r * 1e-3}[kind]
+        out.append(r.astype(np.float32))
+    return np.stack(out)
+
+
+def kquant_weights(x):
+    """quantize_row_q4_K_ref's weights of a 32-value sub-block: sqrt(mean of squares) + |x|, summed in order in float32."""
+    av = np.sqrt(np.cumsum(x * x, dtype=np.float32)[-1] / np.float32(32))
+    return (av + np.abs(x)).astype(np.float32)
+
+
+def qkx2_numpy(x, w, nmax, rmin, rdelta, nstep):
+    """make_qkx2_quants (use_mad = 0) restated in numpy from ggml's description, each candidate's codes vectorized and
+    its sums taken in order in float32 (np.cumsum), as the C loop takes them: start from the min-max fit (min clamped
+    to <= 0), then for is = 0..nstep round x - min with iscale = (nmax + rmin + rdelta is) / (max - min), fit the
+    weighted least-squares (scale, min) of those codes (min > 0: min = 0 and the scale alone), and keep the fit whose
+    weighted squared error is smaller -- min and the span max - min follow the fit kept. Returns (scale, min, codes)."""
+    f32 = np.float32
+    seq = lambda v: np.cumsum(v, dtype=f32)[-1]
+    lo, hi = min(f32(x.min()), f32(0)), f32(x.max())
+    sum_w, sum_x = seq(w), seq(w * x)
+    if hi == lo:
+        return f32(0), lo, np.zeros(x.size, np.uint8)
+    iscale = f32(nmax) / (hi - lo)
+    scale = f32(1) / iscale
+    L = np.clip(np.rint(iscale * (x - lo)), 0, nmax).astype(np.uint8)
+    best = seq(w * (scale * L.astype(f32) + lo - x) ** 2)
+    for i in range(nstep + 1):
+        isc = (f32(rmin) + f32(rdelta) * f32(i) + f32(nmax)) / (hi - lo)
+        l = np.clip(np.rint(isc * (x - lo)), 0, nmax).astype(f32)
+        sl, sl2, sxl = seq(w * l), seq(w * l * l), seq(w * l * x)
+        D = sum_w * sl2 - sl * sl
+        if D > 0:
+            sc, mn = (sum_w * sxl - sum_x * sl) / D, (sl2 * sum_x - sl * sxl) / D
+            if mn > 0:
+                mn, sc = f32(0), sxl / sl2
+            err = seq(w * (sc * l + mn - x) ** 2)
+            if err < best:
+                L, best, scale, lo = l.astype(np.uint8), err, sc, mn
+    return scale, lo, L
+
+
+def qkx2_differs(t, xs, search):
+    """Indices of the sub-blocks where search(x, w) -> (scale, min, codes) differs from the numpy restatement."""
+    nmax, rmin, rdelta, nstep = QKX2[t]
+    bad = []
+    for i, x in enumerate(xs):
+        w = kquant_weights(x)
+        s, m, L = search(x, w)
+        s2, m2, L2 = qkx2_numpy(x, w, nmax, rmin, rdelta, nstep)
+        if not (np.float32(s) == s2 and np.float32(m) == m2 and np.array_equal(L, L2)):
+            bad.append(i)
+    return bad
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K], ids=["q4_K", "q5_K"])
+def test_make_qkx2_quants_matches_a_numpy_restatement(t):
+    """The oracle's search and an independent numpy statement of it agree bit for bit on 600 sub-blocks of five
+    shapes, and its fit is never worse than the min-max fit it starts from; a search with another rmin, fewer steps
+    or uniform weights differs on many of them. (Both statements follow ggml's published algorithm; ggml's own C is
+    not here to run, so a misreading shared by both would pass: parity unpinned at that point.)"""
+    nmax, rmin, rdelta, nstep = QKX2[t]
+    xs = subblocks(600, 32, 0x0A11 + t)
+    ours = lambda x, w: O.make_qkx2_quants(x, w, nmax, rmin, rdelta, nstep)
+    assert qkx2_differs(t, xs, ours) == []
+    for x in xs:
+        w = kquant_weights(x)
+        s, m, L = ours(x, w)
+        lo, hi = min(float(x.min()), 0.0), float(x.max())
+        if hi == lo:
+            continue
+        wd, xd = w.astype(np.float64), x.astype(np.float64)
+        l0 = np.clip(np.rint(np.float32(nmax) / np.float32(hi - lo) * (x - np.float32(lo))), 0, nmax)
+        e0 = np.sum(wd * ((hi - lo) / nmax * l0 + lo - xd) ** 2)
+        assert np.sum(wd * (float(s) * L + float(m) - xd) ** 2) <= e0 * (1 + 1e-5) + 1e-30
+    for wrong in (lambda x, w: O.make_qkx2_quants(x, w, nmax, rmin + 0.5, rdelta, nstep),
+                  lambda x, w: O.make_qkx2_quants(x, w, nmax, rmin, rdelta, nstep - 5),
+                  lambda x, w: O.make_qkx2_quants(x, np.ones_like(w), nmax, rmin, rdelta, nstep)):
+        assert len(qkx2_differs(t, xs, wrong)) >= 30
+
+
+def qx_objective(x, l):
+    """make_qx_quants's figure of merit for codes l (x^2 weights): (sum w x l)^2 / sum w l^2, the weighted error it
+    saves with the least-squares scale."""
+    xd, ld = x.astype(np.float64), l.astype(np.float64)
+    w = xd * xd
+    s2 = float(np.sum(w * ld * ld))
+    return float(np.sum(w * xd * ld)) ** 2 / s2 if s2 > 0 else 0.0
+
+
+def qx_best(x, nmax, steps):
+    """The best figure of merit over make_qx_quants's candidates iscale = -(nmax + 0.1 is) / max, is in steps, where
+    max is the value of largest magnitude and codes are clamped to [-nmax, nmax - 1]."""
+    mx = x[np.argmax(np.abs(x))]
+    best = 0.0
+    for i in steps:
+        isc = -(np.float32(nmax) + np.float32(0.1) * np.float32(i)) / mx
+        l = np.clip(np.rint(np.float32(isc) * x), -nmax, nmax - 1)
+        best = max(best, qx_objective(x, l))
+    return best
+
+
+def test_make_qx_quants_is_the_best_of_its_candidates():
+    xs = subblocks(800, 16, 0x0B11)
+    steps = range(-9, 10)
+    for x in xs:
+        s, l = O.make_qx_quants(x, 32)
+        assert np.all((l >= -32) & (l <= 31))
+        obj = qx_objective(x, l)
+        assert obj >= qx_best(x, 32, steps) * (1 - 1e-5)
+        xd, ld = x.astype(np.float64), l.astype(np.float64)
+        assert abs(float(s) - np.sum(xd ** 3 * ld) / np.sum(xd * xd * ld * ld)) <= 1e-5 * abs(float(s))
+    # teeth: the best over a narrower family (is in -5..5) falls short of the full family's on some blocks, so an
+    # oracle searching that family would fail the check above
+    short = sum(qx_best(x, 32, range(-5, 6)) < qx_best(x, 32, steps) * (1 - 1e-5) for x in xs)
+    assert short >= 3
+
+
+def kquant_fields(t, blocks):
+    """Per block of Q4_K / Q5_K / Q6_K bytes: d, dmin (float32 of the fp16 fields), the sub-block scales and mins as
+    integers, and the 256 codes, decoded from ggml-common.h's layout."""
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1, O.TSIZE[t])
+    n = len(b)
+    q = np.zeros((n, 256), np.int64)
+    if t == O.TYPE_Q6_K:
+        ql, qh = b[:, 0:128].astype(np.int64), b[:, 128:192].astype(np.int64)
+        sc = b[:, 192:208].view(np.int8).astype(np.int64)
+        d = h2f(b[:, 208:210].copy().view(np.uint16)[:, 0])
+        for e in range(256):
+            h, r = divmod(e, 128)
+            quarter, l = divmod(r, 32)
+            lb = ql[:, 64 * h + l + 32 * (quarter & 1)]
+            q[:, e] = ((lb & 0xF) if quarter < 2 else (lb >> 4)) | (((qh[:, 32 * h + l] >> (2 * quarter)) & 3) << 4)
+        return dict(d=d, sc=sc, q=q)
+    d = h2f(b[:, 0:2].copy().view(np.uint16)[:, 0])
+    dmin = h2f(b[:, 2:4].copy().view(np.uint16)[:, 0])
+    s = b[:, 4:16].astype(np.int64)
+    sc = np.concatenate([s[:, 0:4] & 63, (s[:, 8:12] & 0xF) | ((s[:, 0:4] >> 6) << 4)], axis=1)
+    mn = np.concatenate([s[:, 4:8] & 63, (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)], axis=1)
+    qs = b[:, 16:144].astype(np.int64) if t == O.TYPE_Q4_K else b[:, 48:176].astype(np.int64)
+    for e in range(256):
+        sub, pos = divmod(e, 32)
+        byte = qs[:, (e // 64) * 32 + pos]
+        q[:, e] = (byte >> 4) if sub % 2 else (byte & 0xF)
+        if t == O.TYPE_Q5_K:
+            q[:, e] += 16 * ((b[:, 16 + pos].astype(np.int64) >> sub) & 1)
+    return dict(d=d, dmin=dmin, sc=sc, mn=mn, q=q)
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K], ids=["q4_K", "q5_K"])
+def test_k_quant_scales_are_the_rounded_subblock_fits(t):
+    """Each super-block's 6-bit scales and mins are nearest_int(63 s_j / max s) and nearest_int(63 m_j / max m),
+    capped at 63, and d / dmin are fp16(max / 63), where (s_j, -m_j) are make_qkx2_quants's fits of its eight
+    sub-blocks with the format's weights and search parameters."""
+    nmax, rmin, rdelta, nstep = QKX2[t]
+    x = subblocks(48, 256, 0x0C11 + t).reshape(-1)
+    f = kquant_fields(t, O.quantize_chunk(t, x.reshape(-1, 256)))
+    for i in range(len(f["d"])):
+        fits = [O.make_qkx2_quants(xs, kquant_weights(xs), nmax, rmin, rdelta, nstep)
+                for xs in x[256 * i:256 * (i + 1)].reshape(8, 32)]
+        s = np.array([fit[0] for fit in fits], np.float32)
+        m = np.array([-fit[1] for fit in fits], np.float32)
+        ms, mm = max(np.float32(0), s.max()), max(np.float32(0), m.max())
+        ls = np.minimum(63, np.rint((np.float32(63) / ms if ms > 0 else np.float32(0)) * s)).astype(np.int64)
+        lm = np.minimum(63, np.rint((np.float32(63) / mm if mm > 0 else np.float32(0)) * m)).astype(np.int64)
+        assert np.array_equal(f["sc"][i], ls) and np.array_equal(f["mn"][i], lm), i
+        assert f["d"][i] == np.float32(np.float16(ms / np.float32(63)))
+        assert f["dmin"][i] == np.float32(np.float16(mm / np.float32(63)))
+        if ms > 0:
+            assert ls.max() == 63
+
+
+def test_q6_K_scales_are_the_rounded_subblock_fits():
+    """Q6_K's int8 scales are min(127, nearest_int(-128 s_j / max_scale)) and d = fp16(-max_scale / 128), where s_j
+    are make_qx_quants's fits of the sixteen 16-value sub-blocks and max_scale the fit of largest magnitude; that
+    sub-block's scale is -128."""
+    x = subblocks(48, 256, 0x0D11).reshape(-1)
+    f = kquant_fields(O.TYPE_Q6_K, O.quantize_chunk(O.TYPE_Q6_K, x.reshape(-1, 256)))
+    for i in range(len(f["d"])):
+        s = np.array([O.make_qx_quants(xs, 32)[0] for xs in x[256 * i:256 * (i + 1)].reshape(16, 16)], np.float32)
+        ms = s[np.argmax(np.abs(s))]
+        isc = np.float32(-128) / ms
+        want = np.minimum(127, np.rint(isc * s)).astype(np.int64)
+        assert np.array_equal(f["sc"][i], want), i
+        assert f["d"][i] == np.float32(np.float16(np.float32(1) / isc))
+        assert f["sc"][i].min() == -128
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K], ids=["q4_K", "q5_K", "q6_K"])
+def test_k_quant_codes_are_nearest_grid_points(t):
+    """Given a block's packed scales, every code is the grid point nearest its value: for Q4_K / Q5_K the grid of
+    sub-block j is d sc_j l - dmin m_j (l = 0 .. 15 / 31), for Q6_K d sc_j (l - 32) (l = 0 .. 63). Sub-blocks whose
+    scale rounded to zero keep the search's codes and are skipped."""
+    x = subblocks(64, 256, 0x0E11 + t).reshape(-1)
+    f = kquant_fields(t, O.quantize_chunk(t, x.reshape(-1, 256)))
+    x = x.reshape(-1, 256).astype(np.float64)
+    sub = 16 if t == O.TYPE_Q6_K else 32
+    levels = {O.TYPE_Q4_K: 16, O.TYPE_Q5_K: 32, O.TYPE_Q6_K: 64}[t]
+    checked = 0
+    for i in range(len(x)):
+        for j in range(256 // sub):
+            step = float(f["d"][i]) * float(f["sc"][i][j])
+            if step == 0:
+                continue
+            l = np.arange(levels, dtype=np.float64)
+            grid = step * (l - 32) if t == O.TYPE_Q6_K else step * l - float(f["dmin"][i]) * float(f["mn"][i][j])
+            xs = x[i, sub * j:sub * (j + 1)]
+            dist = np.abs(xs[:, None] - grid[None, :])
+            got = dist[np.arange(sub), f["q"][i, sub * j:sub * (j + 1)]]
+            assert np.all(got <= dist.min(axis=1) + 1e-6 * abs(step)), (i, j)
+            checked += 1
+    assert checked > 0.9 * len(x) * (256 // sub)
