@@ -26,6 +26,7 @@ Prints one JSON line. --gpus N > 1 exits: one GPU is measured.
 from __future__ import annotations
 
 import argparse
+import subprocess
 import importlib.util
 import json
 import os
@@ -86,11 +87,27 @@ class Launch:
         self.weight_bytes = nbytes if weight_bytes is None else weight_bytes
 
 
+# A copy of EVICT_BYTES through the backend's stream pushes every earlier line out of the 256 MB last-level cache
+# (and the L2s); set up by main() once the backend exists.
+EVICT_BYTES = 256 << 20
+EVICT = None
+
+
+def make_evictor(mx, be):
+    src, dst = be.tensor(mx.F32, (EVICT_BYTES // 4,)), be.tensor(mx.F32, (EVICT_BYTES // 4,))
+
+    def evict():
+        mx.check(mx.lib().mx_tensor_copy(be.h, src.ref(), dst.ref()))
+    return evict
+
+
 def per_label_pass(be, launches, reps: int, use_graph: bool = True):
     """Mean time (ms) per launch of each label: each label's launches are recorded as a graph of their own and
     replayed, so no event sits between two kernels. A label of few small launches repeats them inside its graph (up to
     32 launches), so the graph's own launch cost does not swamp them; launches of 16 MB and more are recorded once, as
-    a repeat would find them in the 256 MB last-level cache. All graphs are recorded first and freed last. Without
+    a repeat would find them in the 256 MB last-level cache. A label whose distinct weights total less than twice that
+    cache is timed one replay at a time with the caches flushed before each (a 512 MB copy outside the events), so
+    its replays read their weights from HBM as the step does. All graphs are recorded first and freed last. Without
     graphs the same launches are issued eagerly between the events."""
     labels = []
     for L in launches:
@@ -120,6 +137,18 @@ def per_label_pass(be, launches, reps: int, use_graph: bool = True):
         for _ in range(3):
             runs[lab]()
         be.sync()
+        distinct = sum(L.weight_bytes for L in launches if L.label == lab)
+        if EVICT is not None and distinct < 2 * EVICT_BYTES:
+            total = 0.0
+            for _ in range(reps):
+                EVICT()
+                be.record(e0)
+                runs[lab]()
+                be.record(e1)
+                be.sync()
+                total += be.elapsed_ms(e0, e1)
+            out[lab] = total / (reps * count)
+            continue
         be.record(e0)
         for _ in range(reps):
             runs[lab]()
@@ -228,6 +257,34 @@ def base_result(args, value, unit, ms_per_step, dtype, config, higher=True):
             "ms_per_step": round(ms_per_step, 5), "higher_is_better": higher, "scaling": "weak", "vs_baseline": None,
             "dtype": dtype, "data": "synthetic (seeded N(0,0.02) weights quantized by ggml's reference quantizers; "
                                     "N(0,1) activations)", "config": config}
+
+
+def host_info():
+    """The host the CPU baseline ran on: what lscpu and nproc report, the cores the port used, and the instruction set
+    of its Q8_0 dot."""
+    info = {"nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0))}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        keep = ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core", "NUMA node(s)", "CPU max MHz",
+                "L3 cache")
+        info["lscpu"] = {k.strip(): v.strip() for k, v in (l.split(":", 1) for l in out.splitlines() if ":" in l)
+                         if k.strip() in keep}
+        flags = next((l.split(":", 1)[1].split() for l in out.splitlines() if l.startswith("Flags")), [])
+        info["avx2"], info["avx512_vnni"] = "avx2" in flags, "avx512_vnni" in flags
+    except (OSError, subprocess.SubprocessError, StopIteration):
+        info["lscpu"] = None
+    O = load_oracle()
+    info["physical_cores"] = O.physical_cores()
+    info["q8_0_dot"] = {2: "AVX512-VNNI vpdpbusd", 1: "AVX2 maddubs"}[O.fast().cpf_q8_0_isa()]
+    return info
+
+
+def cpu_result(many, one):
+    """A CPU baseline measured on the physical cores (`many`) with its one-thread twin (`one`) and the host."""
+    out = dict(many)
+    out["value_1thread"], out["sample_1thread"] = one["value"], one["sample"]
+    out["host"] = host_info()
+    return out
 
 
 def timed_sample(fn, seconds: float):
@@ -396,15 +453,31 @@ def run_decode(args, mx, be, threads):
         "ops_per_step": "1 GET_ROWS + 197 MUL_MAT in 114 launches", "graph": not args.no_graph})
     result.update({"weight_bytes_per_step": weight_bytes, "weight_GBps": round(step_gbps, 1),
                    "hbm_frac_step": round(step_gbps / HBM_PEAK_GBPS, 4), "roofline": roof})
+    if args.full_step:
+        result.update(decode_full_extra(args, mx, be, dec))
     if args.cpu_seconds > 0:
-        result["cpu_baseline"] = cpu_decode(dec, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_result(cpu_decode(dec, args.cpu_seconds),
+                                            cpu_decode(dec, args.cpu_seconds / 3, threads=1))
     return result
 
 
-def cpu_decode(dec, seconds):
-    """The oracle's AVX2 multi-threaded port of ggml's CPU mul_mat on the same weights, one token at a time."""
+def decode_full_extra(args, mx, be, dec):
+    """The whole decode step on the same weights (every op on the device, fused, KV cache at KV_PAST positions), timed
+    as the decode-full workload times it: its tokens per second beside the products-only step."""
+    S = QWEN3_06B
+    st = full_step_state(mx, be, dec, S["nq"], S["nkv"], S["head_dim"], 1)
+    ids = be.tensor(mx.I32, (1,), np.array([4242], np.int32))
+    launches = full_step_launches(be, mx, dec, st, ids, S["nq"], S["nkv"], S["head_dim"], fused=True)
+    steps, warmup = DEFAULT_STEPS["decode-full"]
+    ms = time_graph(be, launches, steps, warmup, not args.no_graph)
+    return {"decode_full_tok_s": round(1e3 / ms, 2), "decode_full_ms_per_token": round(ms, 5),
+            "decode_full_launches": len(launches)}
+
+
+def cpu_decode(dec, seconds, threads=None):
+    """The oracle's multi-threaded port of ggml's CPU mul_mat on the same weights, one token at a time."""
     O = load_oracle()
-    threads = O.physical_cores()
+    threads = threads or O.physical_cores()
     x = {K: O.fill_normal(0xAC700002 + K, 1, K) for K in {K for _, K, _ in dec.shapes}}
 
     def token():
@@ -417,7 +490,7 @@ def cpu_decode(dec, seconds):
     n, el = timed_sample(token, seconds)
     return {"value": round(n / el, 2), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{n} full decode tokens (1 GET_ROWS + 197 Q8_0 mat-vecs, 633 MB of weights each) after one "
-                      f"untimed token, {el:.1f} s, AVX2 int8 dots, src1 quantized once per product, rows split "
+                      f"untimed token, {el:.1f} s, int8 dots, src1 quantized once per product, rows split "
                       f"across {threads} threads"}
 
 
@@ -596,15 +669,16 @@ def run_decode_full(args, mx, be, threads):
                    "hbm_frac_step": round((weight_bytes + kv_bytes) / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                    "matvec_ms_per_step": round(ms_mv, 4), "roofline": roof, "attention_roofline": att})
     if args.cpu_seconds > 0:
-        result["cpu_baseline"] = cpu_decode_full(dec, st, args.cpu_seconds, nq, nkv, hd)
+        result["cpu_baseline"] = cpu_result(cpu_decode_full(dec, st, args.cpu_seconds, nq, nkv, hd),
+                                            cpu_decode_full(dec, st, args.cpu_seconds / 3, nq, nkv, hd, threads=1))
     return result
 
 
-def cpu_decode_full(dec, st, seconds, nq, nkv, hd):
-    """The full step on the host: the AVX2 port's mat-vecs on the physical cores, the scalar oracle's norms, RoPE and
+def cpu_decode_full(dec, st, seconds, nq, nkv, hd, threads=None):
+    """The full step on the host: the port's mat-vecs on the physical cores, the scalar oracle's norms, RoPE and
     flash attention (ggml-cpu's loop) on one thread, over host copies of the same weights and caches."""
     O = load_oracle()
-    threads = O.physical_cores()
+    threads = threads or O.physical_cores()
     H, n_kv, kv_dim = dec.hidden, st["n_kv"], nkv * hd
     # host caches as the oracle's attention reads them: [kv head, position, channel]
     caches = [{n: np.ascontiguousarray(np.frombuffer(c[n].get_bytes().tobytes(), np.uint16)
@@ -638,7 +712,7 @@ def cpu_decode_full(dec, st, seconds, nq, nkv, hd):
 
     n, el = timed_sample(token, seconds)
     return {"value": round(n / el, 2), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} full decode tokens after one untimed token, {el:.1f} s: mat-vecs in the AVX2 port on "
+            "sample": f"{n} full decode tokens after one untimed token, {el:.1f} s: mat-vecs in the port on "
                       f"{threads} threads, norms / RoPE / SET_ROWS / flash attention (ggml-cpu's loop over 1025 "
                       f"positions) / SwiGLU in the scalar oracle on one thread"}
 
@@ -671,14 +745,17 @@ def run_matvec(args, mx, be, threads):
         host = np.ascontiguousarray(np.broadcast_to(w, (MATVEC_COPIES,) + w.shape))
         i = [0]
 
-        def one():
-            O.cpu_fast_mul_mat(O.TYPE_Q8_0, host[i[0] % MATVEC_COPIES], x, cores)
-            i[0] += 1
+        runs = []
+        for c, sec in ((cores, args.cpu_seconds), (1, args.cpu_seconds / 3)):
+            cores_now = c
 
-        n, el = timed_sample(one, args.cpu_seconds)
-        result["cpu_baseline"] = {"value": round(n * nbytes / el / 1e9, 2), "unit": "GB/s", "cores": cores,
-                                  "kind": "port", "sample": f"{n} products over {MATVEC_COPIES} rotated host copies, "
-                                                            f"{el:.1f} s, AVX2, {cores} threads"}
+            def one_c(c=cores_now):
+                O.cpu_fast_mul_mat(O.TYPE_Q8_0, host[i[0] % MATVEC_COPIES], x, c)
+                i[0] += 1
+            n, el = timed_sample(one_c, sec)
+            runs.append({"value": round(n * nbytes / el / 1e9, 2), "unit": "GB/s", "cores": c, "kind": "port",
+                         "sample": f"{n} products over {MATVEC_COPIES} rotated host copies, {el:.1f} s, {c} threads"})
+        result["cpu_baseline"] = cpu_result(runs[0], runs[1])
     return result
 
 
@@ -693,10 +770,10 @@ def prefill_launches(be, dec, acts, label_of):
     return L
 
 
-def cpu_prefill(dec, M, seconds, types):
-    """The AVX2 port of ggml's CPU mul_mat on the same weights at M rows, layer by layer, bounded by `seconds`."""
+def cpu_prefill(dec, M, seconds, types, cores=None):
+    """The port of ggml's CPU mul_mat on the same weights at M rows, layer by layer, bounded by `seconds`."""
     O = load_oracle()
-    cores = O.physical_cores()
+    cores = cores or O.physical_cores()
     x = {K: O.fill_normal(0xAC700300 + K, M, K) for K in {K for _, K, _ in dec.shapes}}
     state = {"l": 0, "ops": 0}
 
@@ -717,7 +794,7 @@ def cpu_prefill(dec, M, seconds, types):
         if el >= seconds:
             break
     return {"value": round(state["ops"] / el / 1e12, 4), "unit": "TOP/s", "cores": cores, "kind": "port",
-            "sample": f"{n} layers' 7 products at M = {M} after one untimed layer, {el:.1f} s, AVX2 int8 dots, "
+            "sample": f"{n} layers' 7 products at M = {M} after one untimed layer, {el:.1f} s, int8 dots, "
                       f"{cores} threads"}
 
 
@@ -748,7 +825,8 @@ def run_prefill_q4k(args, mx, be, threads):
                                  if be.get_option("gemm_kquant") == 0 else
                                  mfma_roofline("k_gemm_kq<Q6_K>", table, ["down:Q6_K"]))})
     if args.cpu_seconds > 0:
-        result["cpu_baseline"] = cpu_prefill(dec, M, args.cpu_seconds, types)
+        result["cpu_baseline"] = cpu_result(cpu_prefill(dec, M, args.cpu_seconds, types),
+                                            cpu_prefill(dec, M, args.cpu_seconds / 3, types, cores=1))
     return result
 
 
@@ -801,7 +879,8 @@ def run_asr(args, mx, be, threads):
                                                         [L for L in tok if L.label != "get_rows"], ms_tok,
                                                         ms_other=table["get_rows"][3])})
     if args.cpu_seconds > 0:
-        result["cpu_baseline"] = cpu_prefill(dec, 512, args.cpu_seconds, types)
+        result["cpu_baseline"] = cpu_result(cpu_prefill(dec, 512, args.cpu_seconds, types),
+                                            cpu_prefill(dec, 512, args.cpu_seconds / 3, types, cores=1))
     return result
 
 
@@ -882,22 +961,23 @@ def run_moe(args, mx, be, threads):
         xa = O.fill_normal(0xAC700105 + T, T * MOE_K, MOE_F).reshape(T, MOE_K, MOE_F)
         hw = {name: host[name].reshape(MOE_E, N, -1) for name, _, N in specs}
 
-        def layer():
+        def layer(c):
             for name in ("gate", "up"):
                 for e in np.unique(ids):
                     rows = np.nonzero((ids == e).any(axis=1))[0]
-                    O.cpu_fast_mul_mat(O.TYPE_Q4_K, hw[name][e], xb[rows], cores)
+                    O.cpu_fast_mul_mat(O.TYPE_Q4_K, hw[name][e], xb[rows], c)
             for e in np.unique(ids):
                 t_idx, s_idx = np.nonzero(ids == e)
-                O.cpu_fast_mul_mat(O.TYPE_Q4_K, hw["down"][e], xa[t_idx, s_idx], cores)
+                O.cpu_fast_mul_mat(O.TYPE_Q4_K, hw["down"][e], xa[t_idx, s_idx], c)
 
-        n, el = timed_sample(layer, args.cpu_seconds)
         wb = len(np.unique(ids)) * per_expert
-        result["cpu_baseline"] = {"value": round(n * wb / el / 1e9, 2), "unit": "GB/s", "cores": cores,
-                                  "kind": "port",
-                                  "sample": f"{n} MoE layers at T = {T} ({len(np.unique(ids))} distinct experts), "
-                                            f"per-expert AVX2 products over the routed rows, {el:.1f} s, {cores} "
-                                            f"threads"}
+        runs = []
+        for c, sec in ((cores, args.cpu_seconds), (1, args.cpu_seconds / 3)):
+            n, el = timed_sample(lambda c=c: layer(c), sec)
+            runs.append({"value": round(n * wb / el / 1e9, 2), "unit": "GB/s", "cores": c, "kind": "port",
+                         "sample": f"{n} MoE layers at T = {T} ({len(np.unique(ids))} distinct experts), "
+                                   f"per-expert AVX2 products over the routed rows, {el:.1f} s, {c} threads"})
+        result["cpu_baseline"] = cpu_result(runs[0], runs[1])
     return result
 
 
@@ -916,6 +996,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="replay the step (and each label's launches) eagerly instead of as graphs")
     ap.add_argument("--unfused", action="store_true", help="decode-full: one launch per ggml node, no fusions")
+    ap.add_argument("--no-full-step", dest="full_step", action="store_false",
+                    help="decode: skip timing the whole step (decode_full_tok_s) beside the products")
     ints = lambda v: [int(t) for t in v.split(",")]
     ap.add_argument("--blocks", type=ints, default=None,
                     help="asr-1.7b: prefill block rows (default 512,512,512,28; counter passes use 512,512,512)")
@@ -948,6 +1030,8 @@ def main():
         name, value = kv.split("=", 1)
         be.set_option(name, int(value))
     calibration_copy(mx, be)
+    global EVICT
+    EVICT = make_evictor(mx, be)
     threads = max(1, len(os.sched_getaffinity(0)))
     result = WORKLOADS[args.workload](args, mx, be, threads)
     be.close()

@@ -95,6 +95,7 @@ def fast():
         P = ctypes.POINTER(OrcTensor)
         F.cpf_mul_mat.argtypes, F.cpf_mul_mat.restype = [P, P, P, ctypes.c_int], ctypes.c_int
         F.cpf_have_avx2.argtypes, F.cpf_have_avx2.restype = [], ctypes.c_int
+        F.cpf_q8_0_isa.argtypes, F.cpf_q8_0_isa.restype = [], ctypes.c_int
         _fast = F
     return _fast
 

@@ -1,5 +1,5 @@
 /*
- * Multi-threaded AVX2 restatement of ggml's CPU MUL_MAT for Q8_0 / Q4_K / Q6_K weights.
+ * Multi-threaded AVX2 / AVX-512-VNNI restatement of ggml's CPU MUL_MAT for Q8_0 / Q4_K / Q6_K weights.
  *
  * TEST INFRASTRUCTURE ONLY: the timed CPU baseline beside the GPU figures (kind "port": ggml itself is absent from the
  * reference tree, see `.gitmodules:1-4`). It follows ggml_compute_forward_mul_mat (ggml-cpu/ggml-cpu.c): src1 is
@@ -29,6 +29,24 @@ AVX2 static inline __m256i dot_i8_to_i32(__m256i x, __m256i y) {
     const __m256i sy = _mm256_sign_epi8(y, x);
     const __m256i p16 = _mm256_maddubs_epi16(ax, sy);
     return _mm256_madd_epi16(p16, _mm256_set1_epi16(1));
+}
+
+/* The same products through one vpdpbusd (ggml's mul_sum_i8_pairs_float where the host has AVX512-VNNI with
+ * AVX512VL): |x| as the unsigned operand, sign(y, x) as the signed one, summed in fours into int32 lanes. The int32
+ * lane sums equal the maddubs / madd pair's, so the output is bit-identical to the AVX2 path. */
+#define VNNI __attribute__((target("avx2,fma,f16c,avx512f,avx512vl,avx512vnni")))
+
+VNNI static float dot_q8_0_vnni(int64_t n, const blk_q8_0 *x, const blk_q8_0 *y) {
+    __m256 acc = _mm256_setzero_ps();
+    for (int64_t ib = 0; ib < n / 32; ++ib) {
+        const __m256 d = _mm256_set1_ps(_cvtsh_ss(x[ib].d) * _cvtsh_ss(y[ib].d));
+        const __m256i qx = _mm256_loadu_si256((const __m256i *)x[ib].qs);
+        const __m256i qy = _mm256_loadu_si256((const __m256i *)y[ib].qs);
+        const __m256i s = _mm256_dpbusd_epi32(_mm256_setzero_si256(), _mm256_sign_epi8(qx, qx),
+                                              _mm256_sign_epi8(qy, qx));
+        acc = _mm256_fmadd_ps(d, _mm256_cvtepi32_ps(s), acc);
+    }
+    return hsum8(acc);
 }
 
 AVX2 static float dot_q8_0(int64_t n, const blk_q8_0 *x, const blk_q8_0 *y) {
@@ -122,9 +140,22 @@ int cpf_have_avx2(void) {
     return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma") && __builtin_cpu_supports("f16c");
 }
 
+static int have_vnni(void) {
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx512vnni") && __builtin_cpu_supports("avx512vl");
+}
+
+/* The instruction set the Q8_0 dot runs on here: 2 = AVX512-VNNI (vpdpbusd), 1 = AVX2 (maddubs + madd). K-quant dots
+ * are AVX2 on every host, as in ggml's x86 quants.c. */
+int cpf_q8_0_isa(void) { return have_vnni() ? 2 : 1; }
+
 static float dot_any(int type, int64_t n, const void *x, const void *y) {
+    static int vnni = -1;
+    if (vnni < 0) vnni = have_vnni();
     switch (type) {
-        case ORC_TYPE_Q8_0: return dot_q8_0(n, (const blk_q8_0 *)x, (const blk_q8_0 *)y);
+        case ORC_TYPE_Q8_0:
+            return vnni ? dot_q8_0_vnni(n, (const blk_q8_0 *)x, (const blk_q8_0 *)y)
+                        : dot_q8_0(n, (const blk_q8_0 *)x, (const blk_q8_0 *)y);
         case ORC_TYPE_Q4_K: return dot_q4_K(n, (const blk_q4_K *)x, (const blk_q8_K *)y);
         case ORC_TYPE_Q6_K: return dot_q6_K(n, (const blk_q6_K *)x, (const blk_q8_K *)y);
         default: return NAN;
