@@ -981,9 +981,61 @@ def run_moe(args, mx, be, threads):
     return result
 
 
+def run_peaks(args, mx, be, threads):
+    """Practical ceilings of this device, measured with the products' own launch path: a streaming read of a 4 GiB
+    buffer (16 times the last-level cache) swept over loads in flight, plain / nontemporal loads and grid sizes; and
+    int8 / fp16 MFMA issue from register operands. The products' roofline fractions stay quoted against the published
+    peaks; these say how much of each peak a kernel can reach at all."""
+    nbytes = 4 << 30
+    buf = be.tensor(mx.F32, (nbytes // 4,))
+    mx.check(mx.lib().mx_tensor_memset(be.h, buf.ref(), 0, 0, nbytes))
+    e0, e1 = be.event(), be.event()
+
+    def timed(fn, reps):
+        fn()
+        be.sync()
+        be.record(e0)
+        for _ in range(reps):
+            fn()
+        be.record(e1)
+        be.sync()
+        return be.elapsed_ms(e0, e1) / reps
+
+    sweep = []
+    for loads in (4, 8, 16):
+        for nt in (False, True):
+            for wgs in (1024, 2048, 4096, 8192, 16384):
+                ms = timed(lambda: be.peak_read(buf, wgs, loads, nt), args.steps)
+                gbps = nbytes / (ms * 1e-3) / 1e9
+                sweep.append({"loads": loads, "nontemporal": nt, "workgroups": wgs, "us": round(ms * 1e3, 2),
+                              "GBps": round(gbps, 1)})
+                log(f"read loads={loads:2d} nt={int(nt)} wgs={wgs:5d}: {ms * 1e3:8.1f} us  {gbps:7.1f} GB/s")
+    best = max(sweep, key=lambda r: r["GBps"])
+    mfma = {}
+    for kind, name, per, peak in ((0, "int8", 65536, INT8_PEAK_TOPS), (1, "fp16", 32768, FP16_PEAK_TFLOPS)):
+        rows = []
+        for wgs in (256, 1024, 2048):
+            iters = 20000
+            ms = timed(lambda: be.peak_mfma(kind, wgs, iters), 3)
+            t = wgs * 4 * iters * 8 * per / (ms * 1e-3) / 1e12
+            rows.append({"workgroups": wgs, "iters": iters, "ms": round(ms, 3), "T_per_s": round(t, 1),
+                         "frac": round(t / peak, 4)})
+            log(f"mfma {name} wgs={wgs:5d}: {ms:8.3f} ms  {t:8.1f} T/s  ({t / peak:.3f} of {peak:.0f})")
+        mfma[name] = {"best": max(rows, key=lambda r: r["T_per_s"]), "sweep": rows, "peak": peak,
+                      "unit": "TOP/s" if kind == 0 else "TFLOP/s"}
+    be.event_free(e0)
+    be.event_free(e1)
+    buf.free()
+    result = base_result(args, best["GBps"], "GB/s", best["us"] * 1e-3, "u8", {
+        "workload": "peak micro-benchmarks: 4 GiB streaming read; int8 and fp16 MFMA issue", "read_bytes": nbytes})
+    result.update({"hbm_read_best": best, "hbm_read_frac_of_published": round(best["GBps"] / HBM_PEAK_GBPS, 4),
+                   "hbm_read_sweep": sweep, "mfma": mfma})
+    return result
+
+
 WORKLOADS = {"decode": run_decode, "decode-full": run_decode_full, "matvec": run_matvec, "prefill-q4k": run_prefill_q4k, "asr-1.7b": run_asr,
-             "moe": run_moe}
-DEFAULT_STEPS = {"decode": (300, 20), "decode-full": (100, 10), "matvec": (50, 5), "prefill-q4k": (20, 3), "asr-1.7b": (3, 1), "moe": (20, 3)}
+             "moe": run_moe, "peaks": run_peaks}
+DEFAULT_STEPS = {"decode": (300, 20), "decode-full": (100, 10), "matvec": (50, 5), "prefill-q4k": (20, 3), "asr-1.7b": (3, 1), "moe": (20, 3), "peaks": (5, 1)}
 
 
 def main():

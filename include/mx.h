@@ -322,6 +322,19 @@ MX_API int mx_quantize_act(mx_backend *be, int type, int rounding, const float *
                            size_t x_row_stride, void *out);
 
 /* ---------------------------------------------------------------------------------------------------------------
+ * Measurement: no counterpart in speech.cpp or ggml. Peak micro-benchmarks launched on the backend's stream, for the
+ * practical ceilings the products' roofline fractions are read beside (the caller times them with mx_event_*).
+ *   mx_peak_read: one streaming read of `bytes` at `src` (device memory, 16-byte aligned, a multiple of 16 bytes) by
+ *                 `workgroups` (1..65536) of 256 threads, `loads` (1, 2, 4, 8 or 16) 16-byte loads in flight per
+ *                 thread, nontemporal when `nontemporal` is set; nothing is written.
+ *   mx_peak_mfma: `workgroups` (1..65536) of four waves, each issuing `iters` (1..1e7) rounds of eight independent
+ *                 MFMAs on register operands: kind 0 v_mfma_i32_32x32x32_i8 (65,536 int8 ops each), kind 1
+ *                 v_mfma_f32_32x32x16_f16 (32,768 flops each).
+ * ------------------------------------------------------------------------------------------------------------- */
+MX_API int mx_peak_read(mx_backend *be, const void *src, size_t bytes, int workgroups, int loads, int nontemporal);
+MX_API int mx_peak_mfma(mx_backend *be, int kind, int workgroups, int iters);
+
+/* ---------------------------------------------------------------------------------------------------------------
  * Replay of a fixed sequence of ops with one launch (the role CUDA graphs play inside ggml-cuda's graph_compute;
  * the kept decode-step graph of src/common/qwen3-decoder.cpp:187-208,462-490). Between mx_graph_begin and
  * mx_graph_end the ops are recorded, not run; mx_graph_launch replays them on the backend's stream. Record after one

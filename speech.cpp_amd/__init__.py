@@ -49,7 +49,7 @@ EXPORTS = [
     "mx_gguf_get_int", "mx_gguf_get_float", "mx_gguf_get_arr", "mx_gguf_get_arr_str", "mx_gguf_load_tensor",
     "mx_rms_norm", "mx_binary", "mx_swiglu", "mx_supports_rope", "mx_rope", "mx_set_rows", "mx_supports_flash_attn_ext",
     "mx_flash_attn_ext", "mx_mul_mat_fused", "mx_qk_norm_rope_kv", "mx_attn_decode", "mx_decoder_new", "mx_decoder_free",
-    "mx_decoder_step", "mx_mul_mat_id_noalloc", "mx_mul_mat_id_noalloc_bytes",
+    "mx_decoder_step", "mx_mul_mat_id_noalloc", "mx_mul_mat_id_noalloc_bytes", "mx_peak_read", "mx_peak_mfma",
 ]
 NOALLOC_SCRATCH_BYTES = 16 << 20  # MX_NOALLOC_SCRATCH_BYTES
 
@@ -144,6 +144,8 @@ def lib():
         "mx_mul_mat_id": ([vp, P, P, P, P], i32),
         "mx_mul_mat_group": ([vp, i32, ctypes.POINTER(P), P, ctypes.POINTER(P)], i32),
         "mx_quantize_act": ([vp, i32, i32, vp, i64, i64, sz, vp], i32),
+        "mx_peak_read": ([vp, vp, sz, i32, i32, i32], i32),
+        "mx_peak_mfma": ([vp, i32, i32, i32], i32),
         "mx_graph_begin": ([vp], i32),
         "mx_graph_end": ([vp, ctypes.POINTER(vp)], i32),
         "mx_graph_launch": ([vp, vp], i32),
@@ -457,6 +459,14 @@ class Backend:
         check(lib().mx_quantize_act(self.h, t, rounding, ctypes.c_void_p(x.base), k, nrows, x.desc.nb[1],
                                     ctypes.c_void_p(out.base)))
         return out
+
+    def peak_read(self, src: Tensor, workgroups: int, loads: int, nontemporal: bool = False) -> None:
+        """One streaming read of all of src's bytes (mx_peak_read)."""
+        check(lib().mx_peak_read(self.h, ctypes.c_void_p(src.base), src.nbytes, workgroups, loads, int(nontemporal)))
+
+    def peak_mfma(self, kind: int, workgroups: int, iters: int) -> None:
+        """Rounds of independent MFMAs on register operands (mx_peak_mfma): kind 0 int8, 1 fp16."""
+        check(lib().mx_peak_mfma(self.h, kind, workgroups, iters))
 
     def supports(self, op: int, src0: Tensor, src1: Tensor | None, src2: Tensor | None, dst: Tensor) -> bool:
         r = lambda t: t.ref() if t is not None else None  # noqa: E731

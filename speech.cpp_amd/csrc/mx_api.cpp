@@ -1229,6 +1229,31 @@ MX_API int mx_attn_decode(mx_backend *be, const mx_tensor *q, const mx_tensor *k
     return MX_SUCCESS;
 }
 
+MX_API int mx_peak_read(mx_backend *be, const void *src, size_t bytes, int workgroups, int loads, int nontemporal) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (!src || !aligned16(src) || bytes % 16 != 0) return fail(MX_INVALID, "peak read: 16-byte aligned whole chunks");
+    if (workgroups < 1 || workgroups > 65536) return fail(MX_INVALID, "peak read: 1 to 65536 workgroups");
+    if (loads != 1 && loads != 2 && loads != 4 && loads != 8 && loads != 16)
+        return fail(MX_INVALID, "peak read: 1, 2, 4, 8 or 16 loads in flight");
+    if ((rc = ensure_scratch(be, (size_t)workgroups * 4))) return rc;
+    HIP_OK(mx::launch_peak_read(src, (int64_t)bytes, workgroups, loads, nontemporal != 0, (int *)be->scratch,
+                                be->stream),
+           "peak read launch");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_peak_mfma(mx_backend *be, int kind, int workgroups, int iters) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (kind != 0 && kind != 1) return fail(MX_INVALID, "peak mfma: kind 0 (int8) or 1 (fp16)");
+    if (workgroups < 1 || workgroups > 65536 || iters < 1 || iters > 10000000)
+        return fail(MX_INVALID, "peak mfma: 1 to 65536 workgroups, 1 to 1e7 rounds");
+    if ((rc = ensure_scratch(be, (size_t)workgroups * 4))) return rc;
+    HIP_OK(mx::launch_peak_mfma(kind, workgroups, iters, (int *)be->scratch, be->stream), "peak mfma launch");
+    return MX_SUCCESS;
+}
+
 MX_API int mx_quantize_act(mx_backend *be, int type, int rounding, const float *x, int64_t k, int64_t nrows,
                            size_t x_row_stride, void *out) {
     int rc = check_be(be);

@@ -325,6 +325,13 @@ hipError_t launch_attn_decode(const FaArgs &a, const QkvPostArgs &pa, hipStream_
 // Rows of more than 8192 floats split into argmax_parts(ne0, nrows) parts, whose (value, index) pairs go to scratch
 // (nrows * parts float2).
 int argmax_parts(int64_t ne0, int64_t nrows);
+// Peak micro-benchmarks (peak.hip): a streaming read of `bytes` (a multiple of 16, 16-byte aligned) by `workgroups`
+// of 256 threads with `loads` (1, 2, 4, 8, 16) 16-byte loads in flight per thread; `iters` rounds of eight independent
+// MFMAs per wave (kind 0: v_mfma_i32_32x32x32_i8, 1: v_mfma_f32_32x32x16_f16). sink: workgroups ints, never written
+// in practice.
+hipError_t launch_peak_read(const void *src, int64_t bytes, int workgroups, int loads, bool nontemporal, int *sink,
+                            hipStream_t s);
+hipError_t launch_peak_mfma(int kind, int workgroups, int iters, int *sink, hipStream_t s);
 hipError_t launch_argmax(const float *src, int64_t ne0, int64_t nrows, int64_t nb1, int32_t *dst, int64_t dst_nb0,
                          void *scratch, hipStream_t s);
 
