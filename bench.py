@@ -87,17 +87,21 @@ class Launch:
         self.weight_bytes = nbytes if weight_bytes is None else weight_bytes
 
 
-# A copy of EVICT_BYTES through the backend's stream pushes every earlier line out of the 256 MB last-level cache
-# (and the L2s); set up by main() once the backend exists.
+# A read of 2 x EVICT_BYTES through the backend's stream pushes every earlier line out of the 256 MB last-level cache
+# (and the L2s), leaving clean lines behind (a copy would leave dirty ones, whose write-back the next kernel would
+# pay for); set up by main() once the backend exists.
 EVICT_BYTES = 256 << 20
 EVICT = None
 
 
 def make_evictor(mx, be):
-    src, dst = be.tensor(mx.F32, (EVICT_BYTES // 4,)), be.tensor(mx.F32, (EVICT_BYTES // 4,))
+    buf = be.tensor(mx.F32, (2 * EVICT_BYTES // 4,))
+    mx.check(mx.lib().mx_tensor_memset(be.h, buf.ref(), 0, 0, 2 * EVICT_BYTES))
 
     def evict():
-        mx.check(mx.lib().mx_tensor_copy(be.h, src.ref(), dst.ref()))
+        be.peak_read(buf, 8192, 16)
+    evict()  # sizes the backend's scratch now, before any graph is recorded
+    be.sync()
     return evict
 
 
@@ -106,7 +110,7 @@ def per_label_pass(be, launches, reps: int, use_graph: bool = True):
     replayed, so no event sits between two kernels. A label of few small launches repeats them inside its graph (up to
     32 launches), so the graph's own launch cost does not swamp them; launches of 16 MB and more are recorded once, as
     a repeat would find them in the 256 MB last-level cache. A label whose distinct weights total less than twice that
-    cache is timed one replay at a time with the caches flushed before each (a 512 MB copy outside the events), so
+    cache is timed one replay at a time with the caches flushed before each (a 512 MB read outside the events), so
     its replays read their weights from HBM as the step does. All graphs are recorded first and freed last. Without
     graphs the same launches are issued eagerly between the events."""
     labels = []

@@ -143,7 +143,8 @@ __device__ __forceinline__ void mq_seek(const MqLane &c, MqCursor &k, int cb) {
 }
 
 // Copies the cursor's super-block of the wave's 16 columns into ring stage SLOT (3 vector memory ops) and advances
-// the cursor; past the last step it stays on the last one, so the copies after the end repeat it.
+// the cursor; past the last step it stays on the last one, so the copies after the end repeat it. (Nontemporal copies
+// measured 8-11 % slower here: T = 16 86 -> 96 us, T = 256 120 -> 128 us.)
 template <int SLOT>
 __device__ __forceinline__ void mq_copy(const MqLane &c, MqCursor &k, int ncb) {
     uint8_t *st = c.ring + SLOT * MQ_STAGE;

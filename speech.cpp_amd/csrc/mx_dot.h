@@ -72,38 +72,49 @@ struct WChunk<MX_TYPE_Q6_K> {
     uint32_t d;    // fp16 d (low half)
 };
 
+// Weight bytes are read once per launch: they are loaded nontemporal (the streaming hint), which measured 10-40 %
+// faster than plain loads for reads that miss the caches (the peak read micro-benchmark).
+typedef int wl_v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 ld_w16(const uint8_t *p) {
+    const wl_v4i v = __builtin_nontemporal_load((const wl_v4i *)p);
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t ld_w32(const uint8_t *p) { return __builtin_nontemporal_load((const uint32_t *)p); }
+__device__ __forceinline__ uint32_t ld_w16b(const uint8_t *p) { return __builtin_nontemporal_load((const uint16_t *)p); }
+__device__ __forceinline__ uint32_t ld_w8(const uint8_t *p) { return __builtin_nontemporal_load(p); }
+
 template <int TYPE>
 __device__ __forceinline__ WChunk<TYPE> load_chunk(const WPlanes &w, int64_t grow, int64_t K, int c) {
     WChunk<TYPE> r;
     if constexpr (TYPE == MX_TYPE_Q8_0) {
-        r.q = *(const int4 *)(w.p0 + grow * K + 16 * c);
-        r.d = *(const uint16_t *)(w.p1 + (grow * (K / 32) + (c >> 1)) * 2);
+        r.q = ld_w16(w.p0 + grow * K + 16 * c);
+        r.d = ld_w16b(w.p1 + (grow * (K / 32) + (c >> 1)) * 2);
     } else if constexpr (TYPE == MX_TYPE_Q4_K) {
         const int64_t blk = grow * (K / 256) + (c >> 3);
-        r.q = *(const int4 *)(w.p0 + blk * 128 + 16 * (c & 7));
-        const uint32_t *sp = (const uint32_t *)(w.p1 + blk * 12);
-        r.s0 = sp[0];
-        r.s1 = sp[1];
-        r.s2 = sp[2];
-        r.dm = *(const uint32_t *)(w.p2 + blk * 4);
+        r.q = ld_w16(w.p0 + blk * 128 + 16 * (c & 7));
+        const uint8_t *sp = w.p1 + blk * 12;
+        r.s0 = ld_w32(sp);
+        r.s1 = ld_w32(sp + 4);
+        r.s2 = ld_w32(sp + 8);
+        r.dm = ld_w32(w.p2 + blk * 4);
     } else if constexpr (TYPE == MX_TYPE_Q5_K) {
         const int64_t blk = grow * (K / 256) + (c >> 3);
-        r.q = *(const int4 *)(w.p0 + blk * 128 + 16 * (c & 7));
-        r.qh = *(const int4 *)(w.p1 + blk * 32 + 16 * (c & 1));
-        const uint32_t *sp = (const uint32_t *)(w.p2 + blk * 12);
-        r.s0 = sp[0];
-        r.s1 = sp[1];
-        r.s2 = sp[2];
-        r.dm = *(const uint32_t *)(w.p3 + blk * 4);
+        r.q = ld_w16(w.p0 + blk * 128 + 16 * (c & 7));
+        r.qh = ld_w16(w.p1 + blk * 32 + 16 * (c & 1));
+        const uint8_t *sp = w.p2 + blk * 12;
+        r.s0 = ld_w32(sp);
+        r.s1 = ld_w32(sp + 4);
+        r.s2 = ld_w32(sp + 8);
+        r.dm = ld_w32(w.p3 + blk * 4);
     } else {
         const int64_t blk = grow * (K / 256) + (c >> 3);
         const int t = c & 7, h = t >> 2, u = t & 3;
-        r.ql = *(const int4 *)(w.p0 + blk * 128 + 64 * h + 16 * u);
-        r.qh = *(const int4 *)(w.p1 + blk * 64 + 32 * h + 16 * (u & 1));
+        r.ql = ld_w16(w.p0 + blk * 128 + 64 * h + 16 * u);
+        r.qh = ld_w16(w.p1 + blk * 64 + 32 * h + 16 * (u & 1));
         const int lo_sc = 8 * h + 2 * (u >> 1) + (u & 1);  // (128h + 32(u>>1) + 16(u&1)) / 16
         const uint8_t *sp = w.p2 + blk * 16;
-        r.sc = (uint32_t)sp[lo_sc] | ((uint32_t)sp[lo_sc + 4] << 8);
-        r.d = *(const uint16_t *)(w.p3 + blk * 2);
+        r.sc = ld_w8(sp + lo_sc) | (ld_w8(sp + lo_sc + 4) << 8);
+        r.d = ld_w16b(w.p3 + blk * 2);
     }
     return r;
 }
