@@ -378,14 +378,19 @@ struct FaStage {
     float mv;
 };
 
+// NT: nontemporal loads, for a decode row, whose workgroups each read their cache chunk once (several query rows
+// read each chunk once per row, and keep the plain loads that leave it in the cache for the next).
+template <bool NT>
 __device__ __forceinline__ void fa_stage_load(FaStage &st, const FaArgs &a, const uint8_t *kb, const uint8_t *vb,
                                               const uint16_t *mrow, int64_t base, int64_t j1, int tid) {
     const int lr = tid >> 4, seg = tid & 15;
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int64_t jr = min(base + lr + 16 * u, j1 - 1);
-        st.k[u] = *(const u32x4 *)(kb + jr * a.k_nb1 + 16 * seg);
-        st.v[u] = *(const u32x4 *)(vb + jr * a.v_nb1 + 16 * seg);
+        const u32x4 *kp = (const u32x4 *)(kb + jr * a.k_nb1 + 16 * seg);
+        const u32x4 *vp = (const u32x4 *)(vb + jr * a.v_nb1 + 16 * seg);
+        st.k[u] = NT ? __builtin_nontemporal_load(kp) : *kp;
+        st.v[u] = NT ? __builtin_nontemporal_load(vp) : *vp;
     }
     st.mv = -INFINITY;
     if (tid < 64 && base + tid < j1) st.mv = mrow ? h2f(mrow[base + tid]) : 0.0f;
@@ -448,7 +453,7 @@ __global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a, QkvPostArgs pa) {
         if (bad && split == 0 && hk == 0 && tid == 0) atomicOr(pa.err, 4);
     }
     FaStage st;
-    if (j0 < j1) fa_stage_load(st, a, kb, vb, mrow, j0, j1, tid);  // the first chunk's loads go out before q's
+    if (j0 < j1) fa_stage_load<POST>(st, a, kb, vb, mrow, j0, j1, tid);  // the first chunk's loads go out before q's
     if constexpr (!POST) {
         for (int e = tid; e < G * D; e += 256) {
             const int g = e / D, d = e % D;
@@ -500,7 +505,7 @@ __global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a, QkvPostArgs pa) {
         }
         if (tid < 64) mvs[tid] = st.mv;
         __syncthreads();
-        if (base + 64 < j1) fa_stage_load(st, a, kb, vb, mrow, base + 64, j1, tid);  // overlaps this chunk's work
+        if (base + 64 < j1) fa_stage_load<POST>(st, a, kb, vb, mrow, base + 64, j1, tid);  // overlaps this chunk's work
         // scores
         {
             const uint8_t *kr = Ks + pos_s * KS + part_s * CPT * 2;
