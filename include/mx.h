@@ -121,7 +121,8 @@ MX_API int mx_backend_set_rounding(mx_backend *be, int rounding);
  *   MX_OPT_GEMM_TILE_M / _N   the GEMM's tile, 0 / 64 / 128 each (0 0: picked per product)
  *   MX_OPT_GEMM_SPLIT         K splits of the fp16 dequantizing GEMM, 0 (picked) .. 64
  *   MX_OPT_MATVEC_LPR         lanes per weight row of the mat-vec: 0 (picked), 16, 32, 64
- *   MX_OPT_MMID_KERNEL        MUL_MAT_ID with many pairs: 0 as picked, 1 the generic experts kernel
+ *   MX_OPT_MMID_KERNEL        MUL_MAT_ID with many pairs: 0 as picked (Q4_K: the grouped MFMA product), 1 the
+ *                             experts kernel, 2 the grouped MFMA product
  *   MX_OPT_MMID_MATVEC_PAIRS  MUL_MAT_ID runs as one mat-vec launch up to this many (token, slot) pairs (16; 0..4096) */
 enum {
     MX_OPT_GEMM_Q8_0 = 1,

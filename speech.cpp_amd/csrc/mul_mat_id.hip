@@ -175,6 +175,12 @@ __global__ __launch_bounds__(256) void k_mmid_prep(MulMatIdArgs a) {
     else mmid_quant_row<TYPE>(a, (int64_t)blockIdx.x - 1);
 }
 
+// Weight chunks each lane requests before an expert's activation rows are copied to LDS (one-pass experts).
+constexpr int MMID_PRELOAD = 4;
+
+// One workgroup per (block of 4 G weight rows, active expert): the expert's pairs in passes of up to NC columns, each
+// pass copying their quantized rows to LDS and streaming the rows' weights against them. An expert with at most NC
+// pairs (every one at small batches) runs in one pass whose weight loads go out first.
 template <int TYPE, int LPR>
 __global__ __launch_bounds__(256) void k_mmid_experts(MulMatIdArgs a) {
     constexpr int NC = MAX_COLS;
@@ -198,6 +204,52 @@ __global__ __launch_bounds__(256) void k_mmid_experts(MulMatIdArgs a) {
     const int64_t grow = (int64_t)e * a.N + row;
     const int nchunks = (int)(K / chunk_elems<TYPE>());
 
+    if (cnt <= NC) {  // uniform: one pass, whose weight chunks go out before the activation copies
+        constexpr int PRE = MMID_PRELOAD;
+        const int64_t prow = (int64_t)e * a.N + (has_row ? row : a.N - 1);  // rows past the end load the last row
+        WChunk<TYPE> pre[PRE];
+#pragma unroll
+        for (int i = 0; i < PRE; i++) {
+            const int c = sub + i * LPR;
+            pre[i] = load_chunk<TYPE>(a.w, prow, K, c < nchunks ? c : nchunks - 1);
+        }
+        for (int col = 0; col < cnt; col++) {
+            const int p = a.pairs[off + col];
+            const int64_t t = p / a.n_ids, s = p % a.n_ids;
+            const int64_t r = t * a.b_ne1 + (s % a.b_ne1);
+            for (int64_t k = 16 * threadIdx.x; k < K; k += 16 * 256)
+                *(int4 *)(xq + col * K + k) = *(const int4 *)(a.xq + r * K + k);
+            for (int64_t k = threadIdx.x; k < nsc; k += 256) xd[col * nsc + k] = a.xd[r * nsc + k];
+            if (TYPE != MX_TYPE_Q8_0)
+                for (int64_t k = threadIdx.x; k < K / 16; k += 256) xbs[col * (K / 16) + k] = a.xbs[r * (K / 16) + k];
+        }
+        __syncthreads();
+        if (!has_row) return;  // whole LPR-lane groups leave together; no barrier follows
+        float acc[NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++) acc[c] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PRE; i++) {
+            const int c = sub + i * LPR;
+            if (c < nchunks) dot_chunk<TYPE, NC, true>(pre[i], K, c, xq, xd, xbs, cnt, acc);
+        }
+#pragma unroll 2
+        for (int c = sub + PRE * LPR; c < nchunks; c += LPR) chunk_dot<TYPE, NC, true>(a.w, grow, K, c, xq, xd, xbs, cnt, acc);
+#pragma unroll
+        for (int c = 0; c < NC; c++) acc[c] = sum_lanes<LPR>(acc[c]);
+        if (sub == LPR - 1) {
+#pragma unroll
+            for (int col = 0; col < NC; col++) {
+                if (col < cnt) {
+                    const int p = a.pairs[off + col];
+                    const int64_t t = p / a.n_ids, s = p % a.n_ids;
+                    float *y = (float *)((uint8_t *)a.dst + s * a.dst_nb1 + t * a.dst_nb2);
+                    y[row] = acc[col];
+                }
+            }
+        }
+        return;
+    }
     for (int g0 = 0; g0 < cnt; g0 += NC) {
         const int ng = cnt - g0 < NC ? cnt - g0 : NC;
         __syncthreads();  // the previous pass is done with LDS
@@ -241,14 +293,18 @@ static hipError_t launch_typed(const MulMatIdArgs &a, hipStream_t s) {
     hipLaunchKernelGGL(k_mmid_prep<TYPE>, dim3((unsigned)(nrows + 1)), dim3(256), (size_t)a.E * 4, s, a);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
-    if (TYPE == MX_TYPE_Q4_K && !a.generic && mmid_q4k_supported(a)) return launch_mmid_q4k(a, s);
     const int64_t npairs = a.n_ids * a.T;
+    // Q4_K: the grouped MFMA product unless an option asks for the experts kernel (measured at 16 tokens x top-4 of
+    // 64 experts, 64 pairs: 86 us per layer grouped against 114 us on the one-pass experts kernel)
+    const bool grouped = a.generic != 1;
+    if (TYPE == MX_TYPE_Q4_K && grouped && mmid_q4k_supported(a)) return launch_mmid_q4k(a, s);
     const unsigned gy = (unsigned)(npairs < a.E ? npairs : a.E);
     const size_t lds = act_lds_bytes(TYPE, a.K, MAX_COLS);
+    // lanes per row: the fewest whose chunks per lane fit the preload (as the mat-vec picks them)
     const int64_t nchunks = a.K / chunk_elems<TYPE>();
-    if (nchunks <= 128) {
+    if (nchunks <= 16 * MMID_PRELOAD) {
         hipLaunchKernelGGL((k_mmid_experts<TYPE, 16>), dim3((unsigned)((a.N + 15) / 16), gy), dim3(256), lds, s, a);
-    } else if (nchunks <= 256) {
+    } else if (nchunks <= 32 * MMID_PRELOAD) {
         hipLaunchKernelGGL((k_mmid_experts<TYPE, 32>), dim3((unsigned)((a.N + 7) / 8), gy), dim3(256), lds, s, a);
     } else {
         hipLaunchKernelGGL((k_mmid_experts<TYPE, 64>), dim3((unsigned)((a.N + 3) / 4), gy), dim3(256), lds, s, a);

@@ -111,7 +111,8 @@ struct Options {
     int tile_m = 0, tile_n = 0;     // GEMM tile (0: picked per product)
     int split = 0;                  // K splits of the fp16 dequantizing GEMM (0: picked)
     int matvec_lpr = 0;             // lanes per row of the mat-vec: 16, 32 or 64 (0: picked)
-    int mmid_kernel = 0;            // MUL_MAT_ID with many pairs: 0 as picked, 1 the generic experts kernel
+    int mmid_kernel = 0;            // MUL_MAT_ID with many pairs: 0 as picked, 1 the experts kernel, 2 the grouped
+                                    // MFMA product (Q4_K)
     int64_t mmid_matvec_pairs = 16; // MUL_MAT_ID runs as one mat-vec launch up to this many (token, slot) pairs
 };
 
@@ -262,7 +263,7 @@ struct MulMatIdArgs {
     int32_t *ntiles;       // [1] tiles written by the bucket kernel
     int64_t max_tiles;
     int *err;
-    int generic;               // 1: the generic experts kernel even where a specialised one exists
+    int generic;               // 0 as picked, 1: the experts kernel, 2: the grouped MFMA product (Q4_K)
     int64_t matvec_pairs;      // up to this many pairs: one mat-vec launch, no bucketing
     int lpr;                   // mat-vec lanes per row forced, or 0
 };

@@ -1,9 +1,11 @@
 """Every kernel the products' dispatcher can pick, reached in one process: by the shapes that pick it by default
 (config 3's Q4_K prefill groups on the 128 x 128 eight-wave tile) and by a backend's options
 (mx_backend_set_option: the int8 Q8_0 GEMM, the VALU-scaled int8 K-quant GEMM, each GEMM tile, forced K splits, the
-mat-vec's lanes per row, the generic MUL_MAT_ID kernel and its mat-vec threshold), each held to the oracle at the
+mat-vec's lanes per row, the MUL_MAT_ID experts kernel or grouped product and its mat-vec threshold), each held to the oracle at the
 parity bars of test_gpu_parity.py. Also the graph rule that a graph recorded before the backend's scratch grew is
 refused."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -125,10 +127,17 @@ def test_matvec_every_lanes_per_row(mx, be, t, K):
 # --------------------------------------------------------------------------------------- MUL_MAT_ID paths
 @pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
 def test_mmid_every_path(mx, be, t):
-    """The generic experts kernel where the Q4_K one would run; the bucketed path for a single token (mat-vec
-    threshold 0); the mat-vec path for 64 pairs (threshold 64)."""
+    """The experts kernel where the grouped Q4_K product would run, in several passes per expert (40 tokens) and in
+    its one-pass form (16 tokens); the grouped product at a small batch (one-tile chunks); the bucketed path for a
+    single token (mat-vec threshold 0); the mat-vec path for 64 pairs (threshold 64)."""
     with be.options(mmid_kernel=1):
         y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=40, bcast=False, seed=0x5EED3600 + t)
+        assert rel_err(y, y_ref) <= TIGHT
+    with be.options(mmid_kernel=2):
+        y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=16, bcast=True, seed=0x5EED3630 + t)
+        assert rel_err(y, y_ref) <= TIGHT
+    with be.options(mmid_kernel=1):
+        y, y_ref = mmid_case(mx, be, t, E=64, K=2048, N=192, n_ids=4, T=16, bcast=True, seed=0x5EED3640 + t)
         assert rel_err(y, y_ref) <= TIGHT
     with be.options(mmid_matvec_pairs=0):
         y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=1, bcast=True, seed=0x5EED3610 + t)
@@ -140,7 +149,8 @@ def test_mmid_every_path(mx, be, t):
 
 # --------------------------------------------------------------------------------------- refusals
 def test_options_refused(mx, be):
-    for name, bad in [("gemm_q8_0", 2), ("tile_m", 96), ("matvec_lpr", 8), ("split", -1), ("mmid_matvec_pairs", -1)]:
+    for name, bad in [("gemm_q8_0", 2), ("tile_m", 96), ("matvec_lpr", 8), ("split", -1), ("mmid_matvec_pairs", -1),
+                      ("mmid_kernel", 3)]:
         with pytest.raises(mx.MxError) as e:
             be.set_option(name, bad)
         assert e.value.code == mx.INVALID
@@ -210,3 +220,22 @@ def test_graph_refused_after_scratch_grows(mx):
     finally:
         other.close()
         be.close()
+
+
+# --------------------------------------------------------------------------------------- peak micro-benchmarks
+def test_peak_entry_points(mx, be):
+    """mx_peak_read / mx_peak_mfma run (small sizes) and refuse what they cannot take."""
+    buf = be.tensor(mx.F32, (1 << 20,))
+    be.peak_read(buf, 64, 4)
+    be.peak_read(buf, 64, 16, nontemporal=True)
+    be.peak_mfma(0, 8, 10)
+    be.peak_mfma(1, 8, 10)
+    be.sync()
+    L = mx.lib()
+    for rc in (L.mx_peak_read(be.h, ctypes.c_void_p(buf.base), 100, 64, 4, 0),        # not whole 16-byte chunks
+               L.mx_peak_read(be.h, ctypes.c_void_p(buf.base + 4), 4096, 64, 4, 0),   # misaligned
+               L.mx_peak_read(be.h, ctypes.c_void_p(buf.base), 4096, 64, 3, 0),       # loads in flight
+               L.mx_peak_read(be.h, ctypes.c_void_p(buf.base), 4096, 0, 4, 0),        # no workgroups
+               L.mx_peak_mfma(be.h, 2, 8, 10), L.mx_peak_mfma(be.h, 0, 8, 0)):
+        assert rc == mx.INVALID
+    buf.free()
