@@ -123,7 +123,10 @@ MX_API int mx_backend_set_rounding(mx_backend *be, int rounding);
  *   MX_OPT_MATVEC_LPR         lanes per weight row of the mat-vec: 0 (picked), 16, 32, 64
  *   MX_OPT_MMID_KERNEL        MUL_MAT_ID with many pairs: 0 as picked (Q4_K: the grouped MFMA product), 1 the
  *                             experts kernel, 2 the grouped MFMA product
- *   MX_OPT_MMID_MATVEC_PAIRS  MUL_MAT_ID runs as one mat-vec launch up to this many (token, slot) pairs (16; 0..4096) */
+ *   MX_OPT_MMID_MATVEC_PAIRS  MUL_MAT_ID runs as one mat-vec launch up to this many (token, slot) pairs (16; 0..4096)
+ *   MX_OPT_MMID_CHUNK         pairs per chunk of an expert's pairs in the grouped Q4_K product: 0 as picked (16 when
+ *                             the pairs average at most four per expert, else 32), 16 (one 16-row tile per chunk),
+ *                             32 (two tiles sharing each decoded weight fragment) */
 enum {
     MX_OPT_GEMM_Q8_0 = 1,
     MX_OPT_GEMM_KQUANT = 2,
@@ -133,6 +136,7 @@ enum {
     MX_OPT_MATVEC_LPR = 6,
     MX_OPT_MMID_KERNEL = 7,
     MX_OPT_MMID_MATVEC_PAIRS = 8,
+    MX_OPT_MMID_CHUNK = 9,
 };
 MX_API int mx_backend_set_option(mx_backend *be, int option, int64_t value);
 MX_API int mx_backend_get_option(mx_backend *be, int option, int64_t *value);

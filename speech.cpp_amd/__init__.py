@@ -32,7 +32,7 @@ ROPE_NEOX = 2
 ROUND_REF, ROUND_X86 = 0, 1
 # mx_backend_set_option keys (include/mx.h MX_OPT_*)
 OPTIONS = {"gemm_q8_0": 1, "gemm_kquant": 2, "tile_m": 3, "tile_n": 4, "split": 5, "matvec_lpr": 6, "mmid_kernel": 7,
-           "mmid_matvec_pairs": 8}
+           "mmid_matvec_pairs": 8, "mmid_chunk": 9}
 SUCCESS, FAILED, ALLOC_FAILED, INVALID, UNSUPPORTED = 0, -1, -2, -3, -4
 
 EXPORTS = [

@@ -1,13 +1,17 @@
 // MUL_MAT_ID on Q4_K experts as a grouped product: dst[:, s, t] = as[ids[s, t]] . quant(b[:, s % b_ne1, t]).
 //
-// The prep launch cuts each expert's (token, slot) pairs into chunks of up to 32, the rows of two 16-row MFMA tiles.
+// The prep launch cuts each expert's (token, slot) pairs into chunks of up to 32, the rows of two 16-row MFMA tiles
+// (or, when the pairs average at most four per expert, of up to 16: one tile, in a kernel form without the second).
 // A workgroup takes one chunk and a few blocks of 128 of the expert's weight rows (dst columns); wave w owns columns
 // 16 w .. 16 w + 15 of each block and streams their super-blocks block after block, so each weight byte leaves HBM
 // once per 32 pairs of its expert, and each decoded weight fragment feeds both 16-row tiles (a chunk of at most 16
 // pairs runs the one-tile form).
 //
-// The weights stream through a ring of four stages per wave in LDS, filled by global_load_lds copies issued three
-// steps ahead (no registers held for them). The chunk's activation operands (K <= 2048) are loaded into LDS once per
+// The weights stream through a ring of two stages per wave in LDS, filled by global_load_lds copies issued one step
+// ahead (no registers held for them). Deeper rings were slower at every depth tried (us per 64-expert top-4 layer,
+// gate + up + down, at 16 / 256 tokens: two-tile chunks with 2 stages 81.6 / 118.9, 3 stages 82.5 / 119.0, 4 stages
+// 85.4 / 119.4; one-tile chunks at 16 tokens with 2 stages 78.9, 3 stages 80.3, 6 stages 89.3, and two workgroups
+// per CU 85.1): the weight stream does not wait on latency. The chunk's activation operands (K <= 2048) are loaded into LDS once per
 // workgroup and shared by its eight waves and all its column blocks.
 //
 // Arithmetic per 256-element super-block, as ggml-cpu's vec_dot_q4_K_q8_K (and the Q4_K prefill GEMM):
@@ -51,10 +55,8 @@ __device__ __forceinline__ uint32_t mq_min(uint32_t s1, uint32_t s2, int j) {
 
 constexpr int MQ_W = 8;              // waves per workgroup
 constexpr int MQ_COLS = 16 * MQ_W;   // dst columns per column block: 16 per wave
-constexpr int MQ_ROWS = 32;          // rows (pairs) of a chunk: two 16-row MFMA tiles
-static_assert(MMID_CHUNK == MQ_ROWS, "a chunk is two 16-row MFMA tiles");
+static_assert(MMID_CHUNK == 32 && MMID_CHUNK_SMALL == 16, "a chunk is one or two 16-row MFMA tiles");
 
-constexpr int MQ_S = 4;         // ring stages per wave
 constexpr int MQ_STAGE = 2304;  // one stage: 16 columns x (128 code bytes + 12 scale bytes + d | dmin)
 
 typedef __attribute__((address_space(3))) void mq_lds;
@@ -68,16 +70,21 @@ __device__ __forceinline__ void mq_wait_vm() {
 // Keeps the memory ops before it ahead of the ones after it (the wait counts depend on their issue order).
 __device__ __forceinline__ void mq_order() { asm volatile("" ::: "memory"); }
 
-// LDS of a workgroup: per wave a ring of MQ_S weight stages, then the chunk's activation operands for up to
-// MQ_KSEG super-blocks (one segment of K), laid out as the lanes read them (tile g = rows 16 g .. 16 g + 15):
+// LDS of a workgroup whose chunks have up to NGMAX 16-row tiles and whose waves stream through rings of S stages: per
+// wave a ring of S weight stages, then the chunk's activation operands for up to MQ_KSEG super-blocks (one segment
+// of K), laid out as the lanes read them (tile g = rows 16 g .. 16 g + 15):
 //   codes   [sb][g][q][grp][fr] x 16 bytes: row 16 g + fr, elements 256 sb + 64 q + 16 grp .. + 15
 //   sums    [sb][g][fr] x 32 bytes: that row's split sub-block sums [64 h_j | l_j] (fp16)
 //   scales  [sb][g][fr] floats: that row's Q8_K scale
 constexpr int MQ_KSEG = 8;
-constexpr int MQ_RING = MQ_W * MQ_S * MQ_STAGE;
-constexpr int MQ_AQ = MQ_RING, MQ_A16 = MQ_AQ + MQ_KSEG * 8192, MQ_ADX = MQ_A16 + MQ_KSEG * 1024;
-constexpr int MQ_LDS = MQ_ADX + MQ_KSEG * 128;
-static_assert(MQ_LDS <= 160 * 1024, "one workgroup per CU");
+template <int NGMAX, int S>
+struct MqMap {
+    static constexpr int RING = MQ_W * S * MQ_STAGE;
+    static constexpr int AQ_SB = 4096 * NGMAX, A16_SB = 512 * NGMAX, ADX_SB = 64 * NGMAX;  // per super-block
+    static constexpr int AQ = RING, A16 = AQ + MQ_KSEG * AQ_SB, ADX = A16 + MQ_KSEG * A16_SB;
+    static constexpr int SIZE = ADX + MQ_KSEG * ADX_SB;
+    static_assert(SIZE <= 160 * 1024, "one workgroup per CU");
+};
 
 // One wave's view of its work: the weight stream (ncb column blocks x nsb super-blocks).
 struct MqLane {
@@ -90,8 +97,8 @@ struct MqLane {
     uint32_t ring_lds, a_lds;  // LDS byte addresses of the ring and of the activation operands
 };
 
-// Segment `seg` of the chunk's activation operands, as thread t = 256 g + u brings it to LDS: pieces of row
-// 16 g + (t & 15) (arow: its activation row). Loads past the segment repeat its last super-block; only the stores
+// Segment `seg` of the chunk's activation operands, as thread t = 256 g + u (g < NGMAX) brings it to LDS: pieces of
+// row 16 g + (t & 15) (arow: its activation row). Loads past the segment repeat its last super-block; only the stores
 // are conditional.
 struct MqSeg {
     v4i codes[MQ_KSEG];  // u = (q, grp, fr): elements 64 q + 16 grp .. + 15 of each super-block
@@ -111,6 +118,7 @@ __device__ __forceinline__ MqSeg mq_seg_load(const MulMatIdArgs &a, int arow, in
 }
 // The stores go through inline assembly: the compiler would otherwise order them after every copy in flight into
 // the (disjoint) ring, since it cannot tell the two LDS regions apart.
+template <typename Map>
 __device__ __forceinline__ void mq_seg_store(const MqSeg &r, uint8_t *smem, int seg, int nsb) {
     const int g = threadIdx.x >> 8, u = threadIdx.x & 255, fr = u & 15;
     const int n = min(MQ_KSEG, nsb - MQ_KSEG * seg);
@@ -118,14 +126,16 @@ __device__ __forceinline__ void mq_seg_store(const MqSeg &r, uint8_t *smem, int 
 #pragma unroll
     for (int i = 0; i < MQ_KSEG; i++)
         if (i < n)
-            asm volatile("ds_write_b128 %0, %1" ::"v"(base + MQ_AQ + i * 8192 + g * 4096 + 16 * u), "v"(r.codes[i])
+            asm volatile("ds_write_b128 %0, %1" ::"v"(base + Map::AQ + i * Map::AQ_SB + g * 4096 + 16 * u),
+                         "v"(r.codes[i])
                          : "memory");
     if ((u >> 5) < n)
-        asm volatile("ds_write_b128 %0, %1" ::"v"(base + MQ_A16 + (u >> 5) * 1024 + g * 512 + fr * 32 +
+        asm volatile("ds_write_b128 %0, %1" ::"v"(base + Map::A16 + (u >> 5) * Map::A16_SB + g * 512 + fr * 32 +
                                                   ((u >> 4) & 1) * 16),
                      "v"(r.sums) : "memory");
     if ((u >> 4) < n)
-        asm volatile("ds_write_b32 %0, %1" ::"v"(base + MQ_ADX + (u >> 4) * 128 + g * 64 + fr * 4), "v"(r.scale)
+        asm volatile("ds_write_b32 %0, %1" ::"v"(base + Map::ADX + (u >> 4) * Map::ADX_SB + g * 64 + fr * 4),
+                     "v"(r.scale)
                      : "memory");
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 }
@@ -160,18 +170,17 @@ __device__ __forceinline__ void mq_copy(const MqLane &c, MqCursor &k, int ncb) {
 }
 
 // Step of the wave's stream: super-block sb (sbl within the loaded segment) of its column block, weights in ring
-// stage SLOT, for NG 16-row tiles of the chunk. Each step issues the copies MQ_S - 1 steps ahead (3 ops) and then
-// waits for its own, which were issued MQ_S - 1 copies (9 ops) earlier. Operands are read from LDS in one block with
-// the compiler kept out of it: it cannot see that the copies waited for wrote there.
-template <int SLOT, int NG>
+// stage SLOT of S, for NG 16-row tiles of the chunk. Each step issues the copies S - 1 steps ahead (3 ops) and then
+// waits for its own, which were issued S - 1 copies (3 (S - 1) ops) earlier. Operands are read from LDS in one block
+// with the compiler kept out of it: it cannot see that the copies waited for wrote there.
+template <typename Map, int S, int SLOT, int NG>
 __device__ __forceinline__ void mq_step(const MqLane &c, MqCursor &k, int ncb, int sbl, float (&acc)[NG][4]) {
-    static_assert(MQ_S == 4, "the wait count assumes four stages");
-    mq_copy<(SLOT + MQ_S - 1) % MQ_S>(c, k, ncb);
-    mq_wait_vm<9>();
+    mq_copy<(SLOT + S - 1) % S>(c, k, ncb);
+    mq_wait_vm<3 * (S - 1)>();
     const uint32_t st = c.ring_lds + SLOT * MQ_STAGE;
-    const uint32_t aq = c.a_lds + MQ_AQ - MQ_RING + sbl * 8192 + 16 * c.lane;
-    const uint32_t a16 = c.a_lds + MQ_A16 - MQ_RING + sbl * 1024 + 32 * c.fr + 8 * c.grp;
-    const uint32_t adx = c.a_lds + MQ_ADX - MQ_RING + sbl * 128 + 16 * c.grp;
+    const uint32_t aq = c.a_lds + Map::AQ - Map::RING + sbl * Map::AQ_SB + 16 * c.lane;
+    const uint32_t a16 = c.a_lds + Map::A16 - Map::RING + sbl * Map::A16_SB + 32 * c.fr + 8 * c.grp;
+    const uint32_t adx = c.a_lds + Map::ADX - Map::RING + sbl * Map::ADX_SB + 16 * c.grp;
     v4i w[4];       // code bytes 32 q + 16 (grp & 1) .. + 15 of column fr
     uint4 sv;       // its scale words 0..2, d | dmin
     v4i xa[NG][4];  // activation bytes 64 q + 16 grp .. + 15 of row 16 g + fr
@@ -257,15 +266,37 @@ __device__ __forceinline__ void mq_step(const MqLane &c, MqCursor &k, int ncb, i
     __builtin_amdgcn_sched_barrier(0);  // steps do not interleave: one step's operands live at a time
 }
 
+// Steps SLOT .. S - 1 of one turn of the ring (steps it + SLOT, ...), each while steps remain.
+template <typename Map, int S, int SLOT, int NG, typename F>
+__device__ __forceinline__ void mq_turn(const MqLane &c, MqCursor &k, int ncb, int it, int &sb, float (&acc)[NG][4],
+                                        F &finish) {
+    if constexpr (SLOT < S) {
+        if (SLOT > 0 && it + SLOT >= c.nsteps) return;
+        mq_step<Map, S, SLOT, NG>(c, k, ncb, sb, acc);
+        finish();
+        mq_turn<Map, S, SLOT + 1, NG>(c, k, ncb, it, sb, acc, finish);
+    }
+}
+// Copies SLOT .. S - 2 of the ring's prologue.
+template <int S, int SLOT>
+__device__ __forceinline__ void mq_prologue(const MqLane &c, MqCursor &k, int ncb) {
+    if constexpr (SLOT < S - 1) {
+        mq_copy<SLOT>(c, k, ncb);
+        mq_prologue<S, SLOT + 1>(c, k, ncb);
+    }
+}
+
 // One workgroup's share with NG 16-row tiles (NG = 1 when the chunk has at most 16 pairs).
-template <int NG>
+template <typename Map, int S, int NG>
 __device__ __forceinline__ void mq_run(const MulMatIdArgs &a, MqLane &c, uint8_t *smem, int p0, int cnt, int ncb) {
     const unsigned n_ids = (unsigned)a.n_ids;
     // lane fr carries row 16 g + fr of tile g (rows past the chunk repeat its last pair; their sums are dropped)
     int pair[NG];
 #pragma unroll
     for (int g = 0; g < NG; g++) pair[g] = a.pairs[p0 + min(16 * g + c.fr, cnt - 1)];
-    // the activation row thread t brings to LDS: row 16 (t >> 8) + (t & 15) of the chunk
+    // the activation row thread t brings to LDS: row 16 (t >> 8) + (t & 15) of the chunk (threads of a tile the
+    // kernel form lacks bring nothing)
+    const bool seg_thread = (int)(threadIdx.x >> 8) < Map::AQ_SB / 4096;
     int arow;
     {
         const int pr = a.pairs[p0 + min(16 * (int)(threadIdx.x >> 8) + c.fr, cnt - 1)];
@@ -278,12 +309,11 @@ __device__ __forceinline__ void mq_run(const MulMatIdArgs &a, MqLane &c, uint8_t
     k.sb = 0;
     mq_seek(c, k, 0);
     {
-        const MqSeg seg0 = mq_seg_load(a, arow, 0, c.nsb);
+        MqSeg seg0;
+        if (seg_thread) seg0 = mq_seg_load(a, arow, 0, c.nsb);
         mq_order();
-        mq_copy<0>(c, k, ncb);
-        mq_copy<1>(c, k, ncb);
-        mq_copy<2>(c, k, ncb);
-        mq_seg_store(seg0, smem, 0, c.nsb);  // its wait leaves the copies in flight
+        mq_prologue<S, 0>(c, k, ncb);
+        if (seg_thread) mq_seg_store<Map>(seg0, smem, 0, c.nsb);  // its wait leaves the copies in flight
     }
     __syncthreads();
 
@@ -314,30 +344,18 @@ __device__ __forceinline__ void mq_run(const MulMatIdArgs &a, MqLane &c, uint8_t
         cb++;
     };
 #pragma unroll 1
-    for (int it = 0; it < c.nsteps; it += MQ_S) {
-        mq_step<0, NG>(c, k, ncb, sb, acc);
-        finish();
-        if (it + 1 < c.nsteps) {
-            mq_step<1, NG>(c, k, ncb, sb, acc);
-            finish();
-        }
-        if (it + 2 < c.nsteps) {
-            mq_step<2, NG>(c, k, ncb, sb, acc);
-            finish();
-        }
-        if (it + 3 < c.nsteps) {
-            mq_step<3, NG>(c, k, ncb, sb, acc);
-            finish();
-        }
-    }
+    for (int it = 0; it < c.nsteps; it += S) mq_turn<Map, S, 0, NG>(c, k, ncb, it, sb, acc, finish);
     mq_wait_vm<0>();  // no copy may still be landing in LDS when the workgroup ends
 }
 
 // Grid: one workgroup per CU. The work is ntiles x nblk units (a chunk and one block of MQ_COLS columns); workgroup b
 // takes the contiguous units [b U / G, (b + 1) U / G), chunk by chunk, so every CU gets the same number of column
 // blocks to within one. Within a unit wave w owns columns 16 w .. 16 w + 15 of the block and streams super-blocks
-// 0 .. nsb - 1 (nsb <= MQ_KSEG); a block's sums are written when its last super-block is done.
+// 0 .. nsb - 1 (nsb <= MQ_KSEG); a block's sums are written when its last super-block is done. NGMAX = 1: the host
+// cut the pairs into chunks of at most 16.
+template <int NGMAX, int S>
 __global__ __launch_bounds__(64 * MQ_W) void k_mmid_q4k(MulMatIdArgs a) {
+    using Map = MqMap<NGMAX, S>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int N = (int)a.N;
@@ -365,11 +383,11 @@ __global__ __launch_bounds__(64 * MQ_W) void k_mmid_q4k(MulMatIdArgs a) {
         const int sw = c.lane & 3;
         c.sstride = sw < 3 ? 12 : 4;
         c.se = sw < 3 ? a.w.p1 + eblk * 12 + 4 * sw : a.w.p2 + eblk * 4;
-        c.ring = smem + wave * MQ_S * MQ_STAGE;
+        c.ring = smem + wave * S * MQ_STAGE;
         c.ring_lds = (uint32_t)(uintptr_t)(mq_lds *)c.ring;
-        c.a_lds = (uint32_t)(uintptr_t)(mq_lds *)(smem + MQ_RING);
-        if (cnt > 16) mq_run<2>(a, c, smem, p0, cnt, ncb);
-        else mq_run<1>(a, c, smem, p0, cnt, ncb);
+        c.a_lds = (uint32_t)(uintptr_t)(mq_lds *)(smem + Map::RING);
+        if (NGMAX > 1 && cnt > 16) mq_run<Map, S, NGMAX>(a, c, smem, p0, cnt, ncb);
+        else mq_run<Map, S, 1>(a, c, smem, p0, cnt, ncb);
         u += ncb;
         __syncthreads();  // every wave is done with this chunk's activation operands before the next one's land
     }
@@ -392,17 +410,25 @@ bool mmid_q4k_supported(const MulMatIdArgs &a) {
            a.T * a.b_ne1 * a.K < ((int64_t)1 << 31) && a.N < ((int64_t)1 << 31) - MQ_COLS;
 }
 
-hipError_t launch_mmid_q4k(const MulMatIdArgs &a, hipStream_t s) {
-    if (!mmid_q4k_supported(a)) return hipErrorInvalidValue;
+template <int NGMAX, int S>
+static hipError_t launch_form(const MulMatIdArgs &a, hipStream_t s) {
+    constexpr size_t lds = MqMap<NGMAX, S>::SIZE;
     static bool attr = false;
     if (!attr) {
-        const hipError_t err = hipFuncSetAttribute((const void *)k_mmid_q4k,
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, MQ_LDS);
+        const hipError_t err = hipFuncSetAttribute((const void *)k_mmid_q4k<NGMAX, S>,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (err != hipSuccess) return err;
         attr = true;
     }
-    hipLaunchKernelGGL(k_mmid_q4k, dim3((unsigned)mq_grid()), dim3(64 * MQ_W), MQ_LDS, s, a);
+    hipLaunchKernelGGL((k_mmid_q4k<NGMAX, S>), dim3((unsigned)mq_grid()), dim3(64 * MQ_W), lds, s, a);
     return hipGetLastError();
+}
+
+hipError_t launch_mmid_q4k(const MulMatIdArgs &a, hipStream_t s) {
+    if (!mmid_q4k_supported(a)) return hipErrorInvalidValue;
+    if (a.chunk == MMID_CHUNK_SMALL) return launch_form<1, 2>(a, s);
+    if (a.chunk == MMID_CHUNK) return launch_form<2, 2>(a, s);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace mx

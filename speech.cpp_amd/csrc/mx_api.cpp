@@ -342,6 +342,10 @@ MX_API int mx_backend_set_option(mx_backend *be, int option, int64_t value) {
             if (value < 0 || value > 4096) break;
             o.mmid_matvec_pairs = value;
             return MX_SUCCESS;
+        case MX_OPT_MMID_CHUNK:
+            if (!in({0, 16, 32})) break;
+            o.mmid_chunk = (int)value;
+            return MX_SUCCESS;
         default:
             return fail(MX_INVALID, "unknown option %d", option);
     }
@@ -360,6 +364,7 @@ MX_API int mx_backend_get_option(mx_backend *be, int option, int64_t *value) {
         case MX_OPT_MATVEC_LPR: *value = o.matvec_lpr; return MX_SUCCESS;
         case MX_OPT_MMID_KERNEL: *value = o.mmid_kernel; return MX_SUCCESS;
         case MX_OPT_MMID_MATVEC_PAIRS: *value = o.mmid_matvec_pairs; return MX_SUCCESS;
+        case MX_OPT_MMID_CHUNK: *value = o.mmid_chunk; return MX_SUCCESS;
         default: return fail(MX_INVALID, "unknown option %d", option);
     }
 }
@@ -929,6 +934,7 @@ static void mmid_args(mx_backend *be, const mx_tensor *as, const mx_tensor *b, c
     a.dst_nb1 = (int64_t)dst->nb[1];
     a.dst_nb2 = (int64_t)dst->nb[2];
     a.generic = be->opt.mmid_kernel;
+    a.chunk = mx::mmid_chunk_for(a.n_ids * a.T, a.E, be->opt.mmid_chunk);
     a.matvec_pairs = be->opt.mmid_matvec_pairs;
     a.lpr = be->opt.matvec_lpr;
     a.err = be->err;

@@ -114,6 +114,7 @@ struct Options {
     int mmid_kernel = 0;            // MUL_MAT_ID with many pairs: 0 as picked, 1 the experts kernel, 2 the grouped
                                     // MFMA product (Q4_K)
     int64_t mmid_matvec_pairs = 16; // MUL_MAT_ID runs as one mat-vec launch up to this many (token, slot) pairs
+    int mmid_chunk = 0;             // pairs per chunk of the grouped Q4_K product: 16 or 32 (0: picked)
 };
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -264,6 +265,7 @@ struct MulMatIdArgs {
     int64_t max_tiles;
     int *err;
     int generic;               // 0 as picked, 1: the experts kernel, 2: the grouped MFMA product (Q4_K)
+    int chunk;                 // pairs per chunk of an expert's pairs: MMID_CHUNK_SMALL or MMID_CHUNK
     int64_t matvec_pairs;      // up to this many pairs: one mat-vec launch, no bucketing
     int lpr;                   // mat-vec lanes per row forced, or 0
 };
@@ -375,12 +377,15 @@ size_t decode_lds_bytes();
 size_t decode_ll_words(const DecArgs &a, int grid);
 hipError_t launch_decode_step(const DecArgs &a, int grid, bool cooperative, hipStream_t s);
 
-// Pairs per chunk of one expert's (token, slot) pairs: two 16-row MFMA tiles that share each expanded weight fragment.
-constexpr int MMID_CHUNK = 32;
+// Pairs per chunk of one expert's (token, slot) pairs: two 16-row MFMA tiles that share each expanded weight fragment,
+// or one tile (few pairs per expert: no second tile's operands to stage, and a lighter kernel form).
+constexpr int MMID_CHUNK = 32, MMID_CHUNK_SMALL = 16;
+// The chunk size a MUL_MAT_ID of npairs pairs over E experts takes (forced: a backend's option, 16 or 32; else 0).
+int mmid_chunk_for(int64_t npairs, int64_t E, int forced);
 // Scratch bytes MUL_MAT_ID needs and the carving of `base` into the fields above.
 size_t mul_mat_id_scratch(MulMatIdArgs *a, void *base);
 hipError_t launch_mul_mat_id(const MulMatIdArgs &a, hipStream_t s);
-// Q4_K experts as a grouped product over chunks of up to MMID_CHUNK of an expert's pairs (16 x 16 x 64 int8 MFMA).
+// Q4_K experts as a grouped product over chunks of up to a.chunk of an expert's pairs (16 x 16 x 64 int8 MFMA).
 bool mmid_q4k_supported(const MulMatIdArgs &a);  // Q4_K, K <= 2048
 hipError_t launch_mmid_q4k(const MulMatIdArgs &a, hipStream_t s);
 

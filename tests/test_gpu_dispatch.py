@@ -129,7 +129,8 @@ def test_matvec_every_lanes_per_row(mx, be, t, K):
 def test_mmid_every_path(mx, be, t):
     """The experts kernel where the grouped Q4_K product would run, in several passes per expert (40 tokens) and in
     its one-pass form (16 tokens); the grouped product at a small batch (one-tile chunks); the bucketed path for a
-    single token (mat-vec threshold 0); the mat-vec path for 64 pairs (threshold 64)."""
+    single token (mat-vec threshold 0); the mat-vec path for 64 pairs (threshold 64); the grouped product's chunk
+    forms where the other one would be picked."""
     with be.options(mmid_kernel=1):
         y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=40, bcast=False, seed=0x5EED3600 + t)
         assert rel_err(y, y_ref) <= TIGHT
@@ -139,6 +140,11 @@ def test_mmid_every_path(mx, be, t):
     with be.options(mmid_kernel=1):
         y, y_ref = mmid_case(mx, be, t, E=64, K=2048, N=192, n_ids=4, T=16, bcast=True, seed=0x5EED3640 + t)
         assert rel_err(y, y_ref) <= TIGHT
+    for chunk in (16, 32):  # the grouped product's one-tile form at 40 tokens, its two-tile form at 16
+        with be.options(mmid_chunk=chunk):
+            y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=40 if chunk == 16 else 16, bcast=False,
+                                 seed=0x5EED3650 + t + chunk)
+            assert rel_err(y, y_ref) <= TIGHT, f"chunks of {chunk}"
     with be.options(mmid_matvec_pairs=0):
         y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=1, bcast=True, seed=0x5EED3610 + t)
         assert rel_err(y, y_ref) <= TIGHT
@@ -150,7 +156,7 @@ def test_mmid_every_path(mx, be, t):
 # --------------------------------------------------------------------------------------- refusals
 def test_options_refused(mx, be):
     for name, bad in [("gemm_q8_0", 2), ("tile_m", 96), ("matvec_lpr", 8), ("split", -1), ("mmid_matvec_pairs", -1),
-                      ("mmid_kernel", 3)]:
+                      ("mmid_kernel", 3), ("mmid_chunk", 8)]:
         with pytest.raises(mx.MxError) as e:
             be.set_option(name, bad)
         assert e.value.code == mx.INVALID

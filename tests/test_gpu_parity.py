@@ -302,14 +302,17 @@ def test_mul_mat_id_many_pairs(mx, be, t, skew):
 
 
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
-def test_mul_mat_id_chunk_edges(mx, be, t):
+@pytest.mark.parametrize("chunk", [0, 16], ids=["chunk_picked", "chunk16"])
+def test_mul_mat_id_chunk_edges(mx, be, t, chunk):
     """Experts with exactly 16, 17, 32, 33 and 70 pairs (one or two 16-row tiles per chunk, a chunk of one pair)
-    and none, at K = 2048 (the longest K the Q4_K expert kernel keeps in LDS) with b broadcast over the slots."""
+    and none, at K = 2048 (the longest K the Q4_K expert kernel keeps in LDS) with b broadcast over the slots; for
+    Q4_K in chunks of 32 (as picked here) and of 16 (the kernel form without a second tile)."""
     counts = [16, 17, 0, 32, 33, 70]
     ids = np.concatenate([np.full(c, e, np.int32) for e, c in enumerate(counts)])
     np.random.default_rng(7).shuffle(ids)
-    y, y_ref = mmid_case(mx, be, t, E=len(counts), K=2048, N=136, n_ids=1, T=len(ids), bcast=True,
-                         seed=0x5EED0B00 + t, ids=ids.reshape(-1, 1))
+    with be.options(mmid_chunk=chunk):
+        y, y_ref = mmid_case(mx, be, t, E=len(counts), K=2048, N=136, n_ids=1, T=len(ids), bcast=True,
+                             seed=0x5EED0B00 + t, ids=ids.reshape(-1, 1))
     assert rel_err(y, y_ref) <= TIGHT
 
 
