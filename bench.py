@@ -928,11 +928,11 @@ def run_moe(args, mx, be, threads):
             wgu = d * row_bytes(Q4_K, MOE_H) * MOE_F
             wdn = d * row_bytes(Q4_K, MOE_F) * MOE_H
             ops = 2 * T * MOE_K * MOE_H * MOE_F
-            gu_bytes = wgu + 4 * T * (MOE_H + MOE_K * MOE_F + MOE_K)
-            launches.append(Launch(f"T{T}", gu_bytes, ops, lambda E=E, I=I: be.mul_mat_id(E["gate"], xb, I, yg),
-                                   weight_bytes=wgu))
-            launches.append(Launch(f"T{T}", gu_bytes, ops, lambda E=E, I=I: be.mul_mat_id(E["up"], xb, I, yu),
-                                   weight_bytes=wgu))
+            # gate and up read the same rows and ids (TextModel::experts): one MUL_MAT_ID group, one prep
+            gu_bytes = 2 * wgu + 4 * T * (MOE_H + 2 * MOE_K * MOE_F + MOE_K)
+            launches.append(Launch(f"T{T}", gu_bytes, 2 * ops,
+                                   lambda E=E, I=I: be.mul_mat_id_group([E["gate"], E["up"]], xb, I, [yg, yu]),
+                                   weight_bytes=2 * wgu))
             launches.append(Launch(f"T{T}", wdn + 4 * T * (MOE_K * MOE_F + MOE_K * MOE_H + MOE_K), ops,
                                    lambda E=E, I=I: be.mul_mat_id(E["down"], xa, I, yd), weight_bytes=wdn))
             wbytes += d * per_expert

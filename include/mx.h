@@ -184,6 +184,13 @@ MX_API int mx_get_rows(mx_backend *be, const mx_tensor *src0, const mx_tensor *i
 MX_API int mx_mul_mat(mx_backend *be, const mx_tensor *src0, const mx_tensor *src1, const mx_tensor *dst);
 MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids,
                          const mx_tensor *dst);
+/* Several MUL_MAT_ID nodes that read the same b and ids, as a backend's graph_compute may fuse them: the gate and up
+ * experts of a MoE FFN (src/families/drama3/text-model.cpp:208-209, TextModel::experts). Each dst[i] = as[i] routed by
+ * ids over b, exactly as n separate mx_mul_mat_id calls compute it; one prep launch (bucketing, the rows'
+ * quantization) serves all n, and Q4_K experts take one grouped launch for all of them. 1..4 products whose experts
+ * share type and shape and whose dst share shape and strides. */
+MX_API int mx_mul_mat_id_group(mx_backend *be, int n, const mx_tensor *const *as, const mx_tensor *b,
+                               const mx_tensor *ids, const mx_tensor *const *dst);
 /* MUL_MAT_ID that allocates nothing. No counterpart in speech.cpp or ggml's backend interface: for callers that
  * cannot allocate device memory -- code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
  * The same products as mx_mul_mat_id, on the same kernels and with the same results, but its scratch (the bucketing

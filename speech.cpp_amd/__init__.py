@@ -41,7 +41,7 @@ EXPORTS = [
     "mx_backend_get_option", "mx_last_error", "mx_buft_alignment",
     "mx_buft_max_size", "mx_tensor_alloc_size", "mx_buffer_alloc", "mx_buffer_free", "mx_buffer_clear",
     "mx_tensor_set", "mx_tensor_get", "mx_tensor_memset", "mx_tensor_copy", "mx_supports_op", "mx_get_rows",
-    "mx_mul_mat", "mx_mul_mat_id", "mx_mul_mat_group", "mx_argmax", "mx_quantize_act", "mx_graph_begin", "mx_graph_end",
+    "mx_mul_mat", "mx_mul_mat_id", "mx_mul_mat_id_group", "mx_mul_mat_group", "mx_argmax", "mx_quantize_act", "mx_graph_begin", "mx_graph_end",
     "mx_graph_launch", "mx_graph_free", "mx_event_new", "mx_event_record", "mx_event_synchronize",
     "mx_event_elapsed_ms", "mx_event_free", "mx_quantize_chunk", "mx_fill_normal_rows", "mx_quantize_normal_rows",
     "mx_gguf_open", "mx_gguf_close", "mx_gguf_data_offset", "mx_gguf_n_tensors", "mx_gguf_get_tensor",
@@ -143,6 +143,7 @@ def lib():
         "mx_mul_mat": ([vp, P, P, P], i32),
         "mx_mul_mat_id": ([vp, P, P, P, P], i32),
         "mx_mul_mat_group": ([vp, i32, ctypes.POINTER(P), P, ctypes.POINTER(P)], i32),
+        "mx_mul_mat_id_group": ([vp, i32, ctypes.POINTER(P), P, P, ctypes.POINTER(P)], i32),
         "mx_quantize_act": ([vp, i32, i32, vp, i64, i64, sz, vp], i32),
         "mx_peak_read": ([vp, vp, sz, i32, i32, i32], i32),
         "mx_peak_mfma": ([vp, i32, i32, i32], i32),
@@ -394,6 +395,13 @@ class Backend:
 
     def mul_mat_id(self, as_: Tensor, b: Tensor, ids: Tensor, dst: Tensor) -> None:
         check(lib().mx_mul_mat_id(self.h, as_.ref(), b.ref(), ids.ref(), dst.ref()))
+
+    def mul_mat_id_group(self, as_list, b: Tensor, ids: Tensor, dsts) -> None:
+        """n MUL_MAT_IDs sharing b and ids (gate and up experts) with one prep launch."""
+        P = ctypes.POINTER(MxTensor)
+        w = (P * len(as_list))(*[ctypes.pointer(t.desc) for t in as_list])
+        y = (P * len(dsts))(*[ctypes.pointer(d.desc) for d in dsts])
+        check(lib().mx_mul_mat_id_group(self.h, len(as_list), w, b.ref(), ids.ref(), y))
 
     def mul_mat_id_noalloc(self, as_: Tensor, b: Tensor, ids: Tensor, dst: Tensor) -> None:
         """MUL_MAT_ID on the GPU's static scratch: allocates nothing (mx_mul_mat_id_noalloc)."""

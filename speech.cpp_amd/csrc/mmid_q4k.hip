@@ -288,7 +288,8 @@ __device__ __forceinline__ void mq_prologue(const MqLane &c, MqCursor &k, int nc
 
 // One workgroup's share with NG 16-row tiles (NG = 1 when the chunk has at most 16 pairs).
 template <typename Map, int S, int NG>
-__device__ __forceinline__ void mq_run(const MulMatIdArgs &a, MqLane &c, uint8_t *smem, int p0, int cnt, int ncb) {
+__device__ __forceinline__ void mq_run(const MulMatIdArgs &a, MqLane &c, uint8_t *smem, int p0, int cnt, int ncb,
+                                       float *dst) {
     const unsigned n_ids = (unsigned)a.n_ids;
     // lane fr carries row 16 g + fr of tile g (rows past the chunk repeat its last pair; their sums are dropped)
     int pair[NG];
@@ -335,7 +336,7 @@ __device__ __forceinline__ void mq_run(const MulMatIdArgs &a, MqLane &c, uint8_t
                 const unsigned pi = (unsigned)__shfl(pair[g], row, 64);  // lane `row` holds that row's pair
                 if (16 * g + row < cnt && col <= c.nmax) {
                     const unsigned t = pi / n_ids, s = pi - t * n_ids;
-                    float *y = (float *)((uint8_t *)a.dst + (int64_t)s * a.dst_nb1 + (int64_t)t * a.dst_nb2);
+                    float *y = (float *)((uint8_t *)dst + (int64_t)s * a.dst_nb1 + (int64_t)t * a.dst_nb2);
                     y[col] = acc[g][i];
                 }
                 acc[g][i] = 0.f;
@@ -348,9 +349,9 @@ __device__ __forceinline__ void mq_run(const MulMatIdArgs &a, MqLane &c, uint8_t
     mq_wait_vm<0>();  // no copy may still be landing in LDS when the workgroup ends
 }
 
-// Grid: one workgroup per CU. The work is ntiles x nblk units (a chunk and one block of MQ_COLS columns); workgroup b
-// takes the contiguous units [b U / G, (b + 1) U / G), chunk by chunk, so every CU gets the same number of column
-// blocks to within one. Within a unit wave w owns columns 16 w .. 16 w + 15 of the block and streams super-blocks
+// Grid: one workgroup per CU. The work is nprob x ntiles x nblk units (a product, a chunk and one block of MQ_COLS
+// columns); workgroup b takes the contiguous units [b U / G, (b + 1) U / G), chunk by chunk, so every CU gets the
+// same number of column blocks to within one. Within a unit wave w owns columns 16 w .. 16 w + 15 of the block and streams super-blocks
 // 0 .. nsb - 1 (nsb <= MQ_KSEG); a block's sums are written when its last super-block is done. NGMAX = 1: the host
 // cut the pairs into chunks of at most 16.
 template <int NGMAX, int S>
@@ -360,10 +361,15 @@ __global__ __launch_bounds__(64 * MQ_W) void k_mmid_q4k(MulMatIdArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int N = (int)a.N;
     const int nblk = (N + MQ_COLS - 1) / MQ_COLS;
-    const int64_t units = (int64_t)a.ntiles[0] * nblk;
+    const int64_t per = (int64_t)a.ntiles[0] * nblk;  // units of one product
+    const int64_t units = per * a.nprob;
     const int u1 = (int)((blockIdx.x + 1) * units / gridDim.x);
     for (int u = (int)(blockIdx.x * units / gridDim.x); u < u1;) {
-        const int chunk = u / nblk, cb0 = u - chunk * nblk, ncb = min(nblk - cb0, u1 - u);
+        const int pr = (int)(u / per), ur = u - pr * (int)per;
+        const int chunk = ur / nblk, cb0 = ur - chunk * nblk, ncb = min(nblk - cb0, u1 - u);
+        // uniform selection keeps the kernel-argument arrays out of private memory
+        const WPlanes w = pr == 0 ? a.wg[0] : (pr == 1 ? a.wg[1] : (pr == 2 ? a.wg[2] : a.wg[3]));
+        float *dst = pr == 0 ? a.dstg[0] : (pr == 1 ? a.dstg[1] : (pr == 2 ? a.dstg[2] : a.dstg[3]));
         const int p0 = a.tiles[3 * chunk], cnt = a.tiles[3 * chunk + 1], e = a.tiles[3 * chunk + 2];
         MqLane c;
         c.lane = threadIdx.x & 63;
@@ -379,15 +385,15 @@ __global__ __launch_bounds__(64 * MQ_W) void k_mmid_q4k(MulMatIdArgs a) {
         c.nmax = N - 1;
         c.col0 = cb0 * MQ_COLS + wave * 16 + c.fr;
         c.scol0 = cb0 * MQ_COLS + wave * 16 + (c.lane >> 2);
-        c.qe = a.w.p0 + eblk * 128 + 32 * c.grp;
+        c.qe = w.p0 + eblk * 128 + 32 * c.grp;
         const int sw = c.lane & 3;
         c.sstride = sw < 3 ? 12 : 4;
-        c.se = sw < 3 ? a.w.p1 + eblk * 12 + 4 * sw : a.w.p2 + eblk * 4;
+        c.se = sw < 3 ? w.p1 + eblk * 12 + 4 * sw : w.p2 + eblk * 4;
         c.ring = smem + wave * S * MQ_STAGE;
         c.ring_lds = (uint32_t)(uintptr_t)(mq_lds *)c.ring;
         c.a_lds = (uint32_t)(uintptr_t)(mq_lds *)(smem + Map::RING);
-        if (NGMAX > 1 && cnt > 16) mq_run<Map, S, NGMAX>(a, c, smem, p0, cnt, ncb);
-        else mq_run<Map, S, 1>(a, c, smem, p0, cnt, ncb);
+        if (NGMAX > 1 && cnt > 16) mq_run<Map, S, NGMAX>(a, c, smem, p0, cnt, ncb, dst);
+        else mq_run<Map, S, 1>(a, c, smem, p0, cnt, ncb, dst);
         u += ncb;
         __syncthreads();  // every wave is done with this chunk's activation operands before the next one's land
     }

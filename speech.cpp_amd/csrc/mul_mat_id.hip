@@ -309,16 +309,24 @@ static hipError_t launch_typed(const MulMatIdArgs &a, hipStream_t s) {
     if (TYPE == MX_TYPE_Q4_K && grouped && mmid_q4k_supported(a)) return launch_mmid_q4k(a, s);
     const unsigned gy = (unsigned)(npairs < a.E ? npairs : a.E);
     const size_t lds = act_lds_bytes(TYPE, a.K, MAX_COLS);
-    // lanes per row: the fewest whose chunks per lane fit the preload (as the mat-vec picks them)
+    // lanes per row: the fewest whose chunks per lane fit the preload (as the mat-vec picks them); one launch per
+    // product, all reading the one prep's tables and rows
     const int64_t nchunks = a.K / chunk_elems<TYPE>();
-    if (nchunks <= 16 * MMID_PRELOAD) {
-        hipLaunchKernelGGL((k_mmid_experts<TYPE, 16>), dim3((unsigned)((a.N + 15) / 16), gy), dim3(256), lds, s, a);
-    } else if (nchunks <= 32 * MMID_PRELOAD) {
-        hipLaunchKernelGGL((k_mmid_experts<TYPE, 32>), dim3((unsigned)((a.N + 7) / 8), gy), dim3(256), lds, s, a);
-    } else {
-        hipLaunchKernelGGL((k_mmid_experts<TYPE, 64>), dim3((unsigned)((a.N + 3) / 4), gy), dim3(256), lds, s, a);
+    MulMatIdArgs b = a;
+    for (int p = 0; p < a.nprob; p++) {
+        b.w = a.wg[p];
+        b.dst = a.dstg[p];
+        if (nchunks <= 16 * MMID_PRELOAD) {
+            hipLaunchKernelGGL((k_mmid_experts<TYPE, 16>), dim3((unsigned)((a.N + 15) / 16), gy), dim3(256), lds, s, b);
+        } else if (nchunks <= 32 * MMID_PRELOAD) {
+            hipLaunchKernelGGL((k_mmid_experts<TYPE, 32>), dim3((unsigned)((a.N + 7) / 8), gy), dim3(256), lds, s, b);
+        } else {
+            hipLaunchKernelGGL((k_mmid_experts<TYPE, 64>), dim3((unsigned)((a.N + 3) / 4), gy), dim3(256), lds, s, b);
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
     }
-    return hipGetLastError();
+    return hipSuccess;
 }
 
 // Up to a.matvec_pairs (token, slot) pairs (16 unless a backend's option says otherwise) run as one mat-vec launch
@@ -341,12 +349,14 @@ static hipError_t launch_matvec_ids(const MulMatIdArgs &a, hipStream_t s) {
     m.x_b3 = a.b_nb2 / 4;
     m.y_b2 = a.dst_nb1 / 4;
     m.y_b3 = a.dst_nb2 / 4;
-    m.nprob = 1;
-    m.prob[0].w = a.w;
-    m.prob[0].N = a.N;
-    m.prob[0].row0 = 0;
-    m.prob[0].y = a.dst;
-    m.prob[0].y_col_stride = 0;
+    m.nprob = a.nprob;  // the products share x and ids: one launch
+    for (int p = 0; p < a.nprob; p++) {
+        m.prob[p].w = a.wg[p];
+        m.prob[p].N = a.N;
+        m.prob[p].row0 = 0;
+        m.prob[p].y = a.dstg[p];
+        m.prob[p].y_col_stride = 0;
+    }
     m.ids = a.ids;
     m.ids_nb0 = a.ids_nb0;
     m.ids_nb1 = a.ids_nb1;

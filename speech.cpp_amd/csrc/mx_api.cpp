@@ -933,6 +933,9 @@ static void mmid_args(mx_backend *be, const mx_tensor *as, const mx_tensor *b, c
     a.dst = (float *)dst->data;
     a.dst_nb1 = (int64_t)dst->nb[1];
     a.dst_nb2 = (int64_t)dst->nb[2];
+    a.nprob = 1;
+    a.wg[0] = a.w;
+    a.dstg[0] = a.dst;
     a.generic = be->opt.mmid_kernel;
     a.chunk = mx::mmid_chunk_for(a.n_ids * a.T, a.E, be->opt.mmid_chunk);
     a.matvec_pairs = be->opt.mmid_matvec_pairs;
@@ -953,6 +956,33 @@ MX_API int mx_mul_mat_id(mx_backend *be, const mx_tensor *as, const mx_tensor *b
     if ((rc = ensure_scratch(be, need))) return rc;
     mx::mul_mat_id_scratch(&a, be->scratch);
     HIP_OK(mx::launch_mul_mat_id(a, be->stream), "MUL_MAT_ID launch");
+    return MX_SUCCESS;
+}
+
+MX_API int mx_mul_mat_id_group(mx_backend *be, int n, const mx_tensor *const *as, const mx_tensor *b,
+                               const mx_tensor *ids, const mx_tensor *const *dst) {
+    int rc = check_be(be);
+    if (rc) return rc;
+    if (n <= 0 || n > 4 || !as || !dst) return fail(MX_INVALID, "MUL_MAT_ID group: 1 to 4 products");
+    for (int i = 0; i < n; i++) {
+        if (!mx_supports_op(MX_OP_MUL_MAT_ID, as[i], b, ids, dst[i]))
+            return fail(MX_UNSUPPORTED, "MUL_MAT_ID group member %d: unsupported types, shapes or strides", i);
+        if (as[i]->type != as[0]->type || !same_shape(as[i], as[0]) || !same_layout(dst[i], dst[0]))
+            return fail(MX_UNSUPPORTED, "MUL_MAT_ID group members must share the expert type and shape, and dst's "
+                                        "shape and strides");
+    }
+    mx::MulMatIdArgs a;
+    mmid_args(be, as[0], b, ids, dst[0], a);
+    if (a.n_ids * a.T == 0) return MX_SUCCESS;
+    a.nprob = n;
+    for (int i = 0; i < n; i++) {
+        a.wg[i] = mx::wplanes(as[i]->data, mx::planes_of(as[i]->type, nelements(as[i])));
+        a.dstg[i] = (float *)dst[i]->data;
+    }
+    const size_t need = mx::mul_mat_id_scratch(&a, nullptr);
+    if ((rc = ensure_scratch(be, need))) return rc;
+    mx::mul_mat_id_scratch(&a, be->scratch);
+    HIP_OK(mx::launch_mul_mat_id(a, be->stream), "MUL_MAT_ID group launch");
     return MX_SUCCESS;
 }
 

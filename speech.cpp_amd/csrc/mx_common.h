@@ -266,6 +266,11 @@ struct MulMatIdArgs {
     int *err;
     int generic;               // 0 as picked, 1: the experts kernel, 2: the grouped MFMA product (Q4_K)
     int chunk;                 // pairs per chunk of an expert's pairs: MMID_CHUNK_SMALL or MMID_CHUNK
+    // products sharing b and ids (1..4): product p reads expert weights wg[p] into dstg[p] (dst's strides); the
+    // kernels that take one product at a time read w / dst, which the launcher points at each in turn
+    int nprob;
+    WPlanes wg[4];
+    float *dstg[4];
     int64_t matvec_pairs;      // up to this many pairs: one mat-vec launch, no bucketing
     int lpr;                   // mat-vec lanes per row forced, or 0
 };

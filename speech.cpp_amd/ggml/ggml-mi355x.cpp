@@ -133,7 +133,10 @@ struct NodeKey {
 // What a backend's graph_compute did, for tests and tuning: graphs computed eagerly / recorded / replayed, then the
 // fusions run as one launch -- norm into products, SwiGLU and residual around a product, a decode row's attention
 // block, a prefill block's norms + RoPE + stores (its attention separate) -- and fusions libmx declined.
-enum Count { kEager, kRecorded, kReplayed, kNormProducts, kProductOut, kAttention, kAttentionRows, kDeclined, kCounts };
+enum Count {
+    kEager, kRecorded, kReplayed, kNormProducts, kProductOut, kAttention, kAttentionRows, kDeclined, kExpertsGroup,
+    kCounts
+};
 
 struct BackendCtx {
     DeviceCtx *dev = nullptr;
@@ -403,7 +406,7 @@ struct GraphInfo {
 };
 
 // A step of the plan: one node, a group of products, or a fusion over several nodes (roles below, in graph order).
-enum class StepKind { Node, Products, NormProducts, ProductOut, Attention };
+enum class StepKind { Node, Products, NormProducts, ProductOut, Attention, Experts };
 struct Step {
     StepKind kind;
     std::vector<const ggml_tensor *> nodes;
@@ -518,6 +521,46 @@ bool match_attention(const GraphInfo &gi, int i, Step &st) {
     return true;
 }
 
+bool same_ne(const ggml_tensor *a, const ggml_tensor *b) {
+    return a->ne[0] == b->ne[0] && a->ne[1] == b->ne[1] && a->ne[2] == b->ne[2] && a->ne[3] == b->ne[3];
+}
+
+// Whether the bytes two tensors' data span, [data, data + nbytes), meet.
+bool overlaps(const ggml_tensor *a, const ggml_tensor *b) {
+    if (!a || !b || !a->data || !b->data) return false;
+    const uint8_t *a0 = (const uint8_t *)a->data, *b0 = (const uint8_t *)b->data;
+    return a0 < b0 + ggml_nbytes(b) && b0 < a0 + ggml_nbytes(a);
+}
+
+// MUL_MAT_ID at i and later MUL_MAT_IDs that read the same rows and ids with experts of the same type and shape (the
+// gate and up experts of text-model.cpp:208-209; ggml's graph order puts silu(gate) between them). Run together at
+// i: a later product reads nothing computed after i (its experts are a weight, its rows and ids are i's), and its
+// output may not share memory with any tensor a node between them reads or writes (the allocator reuses freed
+// memory in graph order). Roles: {products...}.
+bool match_experts(const GraphInfo &gi, int i, const std::vector<bool> &taken, Step &st) {
+    const ggml_tensor *a = gi.nodes[i];
+    std::vector<const ggml_tensor *> own{a};
+    for (int j = i + 1; j < (int)gi.nodes.size() && own.size() < 4; j++) {
+        const ggml_tensor *b = gi.nodes[j];
+        if (taken[j] || b->op != GGML_OP_MUL_MAT_ID || b->src[1] != a->src[1] || b->src[2] != a->src[2]) continue;
+        const ggml_tensor *wa = a->src[0], *wb = b->src[0];
+        if (wb->type != wa->type || !same_ne(wa, wb) || !same_ne(a, b)) continue;
+        if (gi.pos(wb) >= 0) continue;  // experts computed by the graph itself
+        bool clear = !overlaps(b, a->src[1]) && !overlaps(b, a->src[2]);
+        for (int k = i + 1; k < j && clear; k++) {
+            const ggml_tensor *n = gi.nodes[k];
+            clear = !overlaps(b, n);
+            for (int s = 0; s < GGML_MAX_SRC && clear; s++) clear = !overlaps(b, n->src[s]);
+        }
+        for (const ggml_tensor *o : own) clear = clear && !overlaps(b, o);
+        if (!clear) continue;
+        own.push_back(b);
+    }
+    if (own.size() < 2) return false;
+    st = Step{StepKind::Experts, own};
+    return true;
+}
+
 std::vector<Step> plan_graph(const GraphInfo &gi) {
     std::vector<Step> plan;
     std::vector<bool> taken(gi.nodes.size(), false);
@@ -528,6 +571,7 @@ std::vector<Step> plan_graph(const GraphInfo &gi) {
         bool fused = false;
         if (t->op == GGML_OP_RMS_NORM) fused = match_attention(gi, i, st) || match_norm_products(gi, i, st);
         if (!fused && (t->op == GGML_OP_GLU || t->op == GGML_OP_MUL_MAT)) fused = match_product_out(gi, i, st);
+        if (!fused && t->op == GGML_OP_MUL_MAT_ID) fused = match_experts(gi, i, taken, st);
         if (fused) {
             for (const ggml_tensor *n : st.nodes)
                 if (n) taken[gi.pos(n)] = true;
@@ -587,6 +631,26 @@ int run_step(BackendCtx *ctx, const Step &st) {
     switch (st.kind) {
         case StepKind::Node: return run_node(ctx, st.nodes[0]);
         case StepKind::Products: return run_products(ctx, st.nodes);
+        case StepKind::Experts: {
+            const int n = (int)st.nodes.size();
+            std::vector<mx_tensor> w(n), y(n);
+            std::vector<const mx_tensor *> wp(n), yp(n);
+            for (int k = 0; k < n; k++) {
+                w[k] = desc(st.nodes[k]->src[0]);
+                y[k] = desc(st.nodes[k]);
+                wp[k] = &w[k];
+                yp[k] = &y[k];
+            }
+            const mx_tensor b = desc(st.nodes[0]->src[1]), ids = desc(st.nodes[0]->src[2]);
+            const int rc = mx_mul_mat_id_group(ctx->be, n, wp.data(), &b, &ids, yp.data());
+            ctx->counts[rc == MX_UNSUPPORTED ? kDeclined : kExpertsGroup]++;
+            if (rc != MX_UNSUPPORTED) return rc;
+            for (const ggml_tensor *e : st.nodes) {
+                const int r = run_node(ctx, e);
+                if (r != MX_SUCCESS) return r;
+            }
+            return MX_SUCCESS;
+        }
         case StepKind::NormProducts: {
             const ggml_tensor *norm = st.nodes[0], *mul = st.nodes[1];
             const int n = (int)st.nodes.size() - 2;

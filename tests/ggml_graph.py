@@ -93,7 +93,7 @@ _SIGS = {
 }
 
 COUNTERS = ["eager", "recorded", "replayed", "norm_products", "product_out", "attention", "attention_rows",
-            "declined"]
+            "declined", "experts_group"]
 
 _lib = None
 
@@ -245,7 +245,7 @@ class Device:
         return self.h.ggml_backend_dev_supports_op(self.dev, t)
 
 
-STEPS = ["node", "products", "norm_products", "product_out", "attention"]
+STEPS = ["node", "products", "norm_products", "product_out", "attention", "experts"]
 
 
 def plan(g):
@@ -257,6 +257,35 @@ def plan(g):
     kinds, first = (ctypes.c_int32 * 8192)(), (ctypes.c_int32 * 8192)()
     n = f(g.graph, kinds, first, 8192)
     return [(STEPS[kinds[i]], first[i]) for i in range(n)]
+
+
+class MoeFfn:
+    """The routed experts of a Drama-3 MoE FFN as TextModel::experts builds them (text-model.cpp:207-210): gate and up
+    MUL_MAT_IDs over the same rows and chosen experts, then down over mul(silu(gate), up). Between gate and up sits a
+    node that reads gate (ggml's order puts silu(gate) there); MUL nodes, which this backend computes, stand in for
+    the silu: down reads (gate * gate) * up. Weights go in `weights`, the inputs and results in `compute`."""
+
+    def __init__(self, H, F, E, n_used, T, wtype=Q4_K):
+        g = self.g = Graph()
+        self.shape = dict(H=H, F=F, E=E, n_used=n_used, T=T, wtype=wtype)
+        self.gate_e, self.up_e, self.down_e = g.new(wtype, H, F, E), g.new(wtype, H, F, E), g.new(wtype, F, H, E)
+        self.weights = [self.gate_e, self.up_e, self.down_e]
+        n0 = len(g.tensors)
+        self.x = g.new(F32, H, T)
+        self.sel = g.new(I32, n_used, T)
+        rows = g.reshape_3d(self.x, H, 1, T)
+        self.gate = g.mul_mat_id(self.gate_e, rows, self.sel)
+        self.g2 = g.mul(self.gate, self.gate)
+        self.up = g.mul_mat_id(self.up_e, rows, self.sel)
+        self.act = g.mul(self.g2, self.up)
+        self.down = g.mul_mat_id(self.down_e, self.act, self.sel)
+        for t in (self.g2, self.up, self.down):
+            g.h.ggml_set_output(t)
+        g.expand(self.down)
+        self.compute = g.tensors[n0:]
+
+    def close(self):
+        self.g.close()
 
 
 class Qwen3Step:

@@ -98,6 +98,38 @@ def test_plan_keeps_what_the_graph_reads_back():
         st.close()
 
 
+def fake_addresses(tensors, alias=None):
+    """Distinct, aligned data addresses for a graph's own tensors (views get their source's plus offset), as a
+    placement without reuse would give them; alias = (a, b) puts b at a's address, as an allocator reusing a's memory
+    for b would. The plan reads addresses only."""
+    addr = 1 << 40
+    for t in tensors:
+        c = t.contents
+        if not c.view_src:
+            c.data = addr
+            addr += (G.libs()[0].ggml_nbytes(t) + 255) // 256 * 256 + 256
+    if alias:
+        alias[1].contents.data = alias[0].contents.data
+    for t in tensors:
+        c = t.contents
+        if c.view_src:
+            c.data = ctypes.cast(c.view_src, ctypes.POINTER(G.Tensor)).contents.data + c.view_offs
+
+
+def test_plan_of_a_moe_ffn():
+    """TextModel::experts' gate and up MUL_MAT_IDs (same rows, same chosen experts) plan as one step at gate's place,
+    the node between them after it; down stays a node. When up's output would reuse memory gate still holds for the
+    node between them (an allocator reusing gate's memory after that node), the two run as their own nodes."""
+    m = G.MoeFfn(2048, 1536, 64, 4, 16)
+    try:
+        fake_addresses(m.g.tensors)
+        assert [k for k, _ in G.plan(m.g)] == ["experts", "node", "node", "node"]
+        fake_addresses(m.g.tensors, alias=(m.gate, m.up))
+        assert [k for k, _ in G.plan(m.g)] == ["node"] * 5
+    finally:
+        m.close()
+
+
 # --------------------------------------------------------------------------------------------- on MI355X
 @pytest.fixture(scope="module")
 def device():
@@ -210,6 +242,57 @@ def test_products_graph_eager_record_replay(device):
         assert [after[c] - before[c] for c in ("eager", "recorded", "replayed")] == [2, 1, 1]
     finally:
         g.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [3, 24], ids=["matvec_path", "grouped"])
+def test_moe_ffn_graph(device, T):
+    """TextModel::experts' routed experts through graph_compute: gate and up in one MUL_MAT_ID group (one mat-vec
+    launch for 6 pairs, the grouped Q4_K product for 48), the MULs around them, down over their product; each
+    product against the oracle on the device's own inputs, twice (eager) with new routing. Then the same graph with
+    up's output placed over gate's memory (valid for the graph's own order: gate is dead once the MUL has read it)
+    runs gate and up as separate nodes, and still computes the right values."""
+    H, F, E, n_used = 1024, 256, 8, 2
+    m = G.MoeFfn(H, F, E, n_used, T)
+    try:
+        data = {k: O.quantize_chunk(O.TYPE_Q4_K, O.fill_normal(0x7B00 + i, n * E, kk, 0.0, 0.02))
+                for i, (k, n, kk) in enumerate((("gate", F, H), ("up", F, H), ("down", H, F)))}
+        device.place(m.weights, usage=1)
+        for t, k in zip(m.weights, ("gate", "up", "down")):
+            device.upload(t, data[k])
+        rng = np.random.default_rng(0x7B10 + T)
+
+        def run_and_check():
+            x = O.fill_normal(int(rng.integers(1 << 30)), T, H)
+            choice = np.stack([rng.choice(E, n_used, replace=False) for _ in range(T)]).astype(np.int32)
+            device.upload(m.x, x)
+            device.upload(m.sel, choice)
+            device.compute(m.g)
+            g2 = device.download(m.g2, np.float32, (T, n_used, F))
+            up = device.download(m.up, np.float32, (T, n_used, F))
+            gate = O.mul_mat_id(O.TYPE_Q4_K, data["gate"].reshape(E, F, -1), x.reshape(T, 1, H), choice)
+            assert rel_err(g2, gate * gate) <= 4 * TIGHT
+            assert rel_err(up, O.mul_mat_id(O.TYPE_Q4_K, data["up"].reshape(E, F, -1), x.reshape(T, 1, H), choice)) <= TIGHT
+            act = g2 * up
+            down = device.download(m.down, np.float32, (T, n_used, H))
+            assert rel_err(down, O.mul_mat_id(O.TYPE_Q4_K, data["down"].reshape(E, H, -1), act, choice)) <= TIGHT
+
+        device.place(m.compute)
+        device.init_views(m.g.tensors)
+        before = device.counters()
+        for _ in range(2):
+            run_and_check()
+        after = device.counters()
+        assert after["experts_group"] - before["experts_group"] == 2 and after["declined"] == before["declined"]
+
+        # up over gate's memory: the planner must not run up ahead of the MUL that reads gate
+        m.up.contents.data = m.gate.contents.data  # same buffer, same size: as an allocator reusing gate's memory
+        before = device.counters()
+        run_and_check()
+        after = device.counters()
+        assert after["experts_group"] == before["experts_group"]
+    finally:
+        m.close()
 
 
 def oracle_step(st, data, caches, tok, past):

@@ -324,6 +324,51 @@ def test_mul_mat_id_moe_layer_shape(mx, be, t):
     assert rel_err(y, y_ref) <= TIGHT
 
 
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("T", [2, 16, 40])
+def test_mul_mat_id_group(mx, be, t, T):
+    """Gate and up experts over the same rows and ids in one call (mx_mul_mat_id_group): each product the same bits as
+    its own mx_mul_mat_id -- one mat-vec launch for both at 2 tokens, the grouped product's two forms at 16 and 40
+    (Q4_K), one experts-kernel launch per product after a shared prep (Q8_0, Q6_K) -- and within the bar of the
+    oracle."""
+    E, K, N, n_ids = 16, 1024, 200, 4
+    seed = 0x5EED0D00 + 64 * T + t
+    wg = weights(t, E * N, K, seed).reshape(E, N, -1)
+    wu = weights(t, E * N, K, seed + 1).reshape(E, N, -1)
+    x = acts(seed + 2, T, K).reshape(T, 1, K)
+    logits = np.random.default_rng(seed).standard_normal((T, E))
+    ids = np.argsort(-logits, axis=1)[:, :n_ids].astype(np.int32)
+    Wg = be.tensor(t, (K, N, E), wg.reshape(E * N, -1))
+    Wu = be.tensor(t, (K, N, E), wu.reshape(E * N, -1))
+    Xt = be.tensor(mx.F32, (K, 1, T), x)
+    It = be.tensor(mx.I32, (n_ids, T), ids)
+    Ys = [be.tensor(mx.F32, (N, n_ids, T)) for _ in range(2)]
+    Yg = [be.tensor(mx.F32, (N, n_ids, T)) for _ in range(2)]
+    be.mul_mat_id(Wg, Xt, It, Ys[0])
+    be.mul_mat_id(Wu, Xt, It, Ys[1])
+    be.mul_mat_id_group([Wg, Wu], Xt, It, Yg)
+    be.sync()
+    for a, b, w in zip(Ys, Yg, (wg, wu)):
+        assert np.array_equal(a.numpy(), b.numpy())
+        assert rel_err(b.numpy().reshape(T, n_ids, N), O.mul_mat_id(t, w, x, ids)) <= TIGHT
+
+
+def test_mul_mat_id_group_refusals(mx, be):
+    K, N, E, T = 256, 32, 4, 3
+    W = be.tensor(mx.Q8_0, (K, N, E), weights(O.TYPE_Q8_0, E * N, K, 11))
+    W2 = be.tensor(mx.Q8_0, (K, N + 32, E), weights(O.TYPE_Q8_0, E * (N + 32), K, 12))
+    X = be.tensor(mx.F32, (K, 1, T), acts(13, T, K))
+    I = be.tensor(mx.I32, (2, T), np.array([[0, 1], [2, 3], [1, 0]], np.int32))
+    Y = [be.tensor(mx.F32, (N, 2, T)) for _ in range(2)]
+    Y2 = be.tensor(mx.F32, (N + 32, 2, T))
+    with pytest.raises(mx.MxError) as e:  # experts of another shape
+        be.mul_mat_id_group([W, W2], X, I, [Y[0], Y2])
+    assert e.value.code == mx.UNSUPPORTED
+    with pytest.raises(mx.MxError) as e:  # more than four
+        be.mul_mat_id_group([W] * 5, X, I, [Y[0]] * 5)
+    assert e.value.code == mx.INVALID
+
+
 def test_mul_mat_id_bad_expert(mx, be):
     K, N, E = 256, 32, 4
     Wt = be.tensor(mx.Q8_0, (K, N, E), weights(O.TYPE_Q8_0, E * N, K, 9))
