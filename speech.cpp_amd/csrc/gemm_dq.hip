@@ -479,7 +479,7 @@ __device__ __forceinline__ void dq_read_ab(v8h (&f)[8], v4i (&b)[2], uint32_t &s
 
 // Eight fragment reads without their wait, and the wait: dq_wait8's operands tie the registers to it, so that nothing
 // reads them before the data has landed.
-__device__ __forceinline__ void dq_issue8(v8h (&f)[16], const uint32_t (&a)[16]) {
+__device__ __forceinline__ void dq_issue8(v8h (&f)[16], const uint32_t (&a)[8]) {
     asm volatile(
         "ds_read_b128 %0, %8\n"
         "ds_read_b128 %1, %9\n"
@@ -734,40 +734,43 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     const uint32_t boffd0 = brow * L::RB + 16 * ((0 + fh) ^ ((brow >> 2) & 3));
     const uint32_t boffd1 = brow * L::RB + 16 * ((2 + fh) ^ ((brow >> 2) & 3));
 
-#pragma unroll 1
-    for (int s = 0; s < nst; s++) {
-        // this wave's copies of A(s) and of the raw weights of stage s + 1 (direct B: of stage s) have landed, and its
-        // LDS writes are done
-        if constexpr (L::DIRB) dq_wait_vm<(L::NS - 2) * L::OPS>();
-        else dq_wait_vm<(L::NS - 3) * L::OPS>();
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __syncthreads();
-        if constexpr (L::DIRB) {
-            const uint32_t at = lds + L::A + (s % L::NS) * BM * 128;
-            const uint32_t rt = lds + L::RAW + (s % L::NS) * BN * L::RB;
-            // A fragment x = kk TM + i: x < 8 in fa, the rest (TM = 4: K steps 2 and 3) in fb
-            uint32_t ad[8], ae[16];
+    if constexpr (L::DIRB) {
+        // The LDS address of every fragment read, per ring slot: the loop is unrolled over the slots, so a stage runs
+        // no address arithmetic (the registers are there to spare: two workgroups of four waves per CU).
+        static_assert(L::NS == 3, "the direct-B loop is unrolled over a three-stage ring");
+        uint32_t adS[L::NS][8], aeS[L::NS][8], bS0[L::NS], bS1[L::NS], scS[L::NS];
+#pragma unroll
+        for (int sl = 0; sl < L::NS; sl++) {
+            const uint32_t at = lds + L::A + sl * BM * 128, rt = lds + L::RAW + sl * BN * L::RB;
+#pragma unroll
+            for (int x = 0; x < 8; x++) adS[sl][x] = aeS[sl][x] = 0;
 #pragma unroll
             for (int kk = 0; kk < 4; kk++)
 #pragma unroll
-                for (int i = 0; i < TM; i++) {
+                for (int i = 0; i < TM; i++) {  // A fragment x = kk TM + i: x < 8 in fa, the rest (TM = 4) in fb
                     const int x = kk * TM + i;
-                    if (x < 8) ad[x] = at + aoff[i][kk];
-                    else ae[x - 8] = at + aoff[i][kk];
+                    if (x < 8) adS[sl][x] = at + aoff[i][kk];
+                    else aeS[sl][x - 8] = at + aoff[i][kk];
                 }
-#pragma unroll
-            for (int x = 4 * TM; x < 8; x++) ad[x] = 0;
-#pragma unroll
-            for (int x = (TM == 4 ? 8 : 0); x < 16; x++) ae[x] = 0;
+            bS0[sl] = rt + boffd0;
+            bS1[sl] = rt + boffd1;
+            scS[sl] = lds + L::SC + sl * BN * L::SB + brow * L::SB;
+        }
+        auto stage = [&](auto slot, int s) {
+            constexpr int SL = decltype(slot)::value;  // == s % L::NS
+            // this wave's copies of A(s) and of the raw weights of stage s have landed, and its LDS writes are done;
+            // then every wave's. The barrier is the bare instruction: __syncthreads' release fence would wait for
+            // every copy in flight (the next stages' too) wherever the compiler can see them pending.
+            dq_wait_vm<(L::NS - 2) * L::OPS>();
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             v8h fa[8], fb[16];
             v4i braw[2];
             uint32_t sw;
-            dq_read_ab<TM == 4 ? 2 : TM>(fa, braw, sw, ad, rt + boffd0, rt + boffd1,
-                                         lds + L::SC + (s % L::NS) * BN * L::SB + brow * L::SB);
+            dq_read_ab<TM == 4 ? 2 : TM>(fa, braw, sw, adS[SL], bS0[SL], bS1[SL], scS[SL]);
             v4i bq[4];  // K steps 2 kk2 and 2 kk2 + 1 from chunk kk2 (block kk2 of the stage)
             if constexpr (TM == 4 && MX_DQ_HALF) {
                 // K steps 2 and 3: their A fragments are read, and chunk 1 converted, while steps 0 and 1 run
-                dq_issue8(fb, ae);
+                dq_issue8(fb, aeS[SL]);
 #pragma unroll
                 for (int x = 0; x < 8; x++) asm volatile("" : "+v"(fa[x]));  // steps 0 and 1 stay behind the reads
                 dq_q8_0_16(braw[0], (uint16_t)(sw & 0xFFFF), bq[0], bq[1]);
@@ -788,7 +791,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
                                                                             __builtin_bit_cast(v8h, bq[kk]), acc[i][0],
                                                                             0, 0, 0);
             } else {
-                if constexpr (TM == 4) dq_read<8>(fb, ae);
+                if constexpr (TM == 4) {
+                    uint32_t ae16[16];
+#pragma unroll
+                    for (int x = 0; x < 16; x++) ae16[x] = x < 8 ? aeS[SL][x] : 0;
+                    dq_read<8>(fb, ae16);
+                }
                 dq_q8_0_16(braw[0], (uint16_t)(sw & 0xFFFF), bq[0], bq[1]);
                 dq_q8_0_16(braw[1], (uint16_t)(sw >> 16), bq[2], bq[3]);
 #pragma unroll
@@ -800,7 +808,25 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
                             acc[i][0], 0, 0, 0);
             }
             issue(s + L::NS - 1);
-        } else {
+        };
+        int s = 0;
+#pragma unroll 1
+        for (; s + L::NS <= nst; s += L::NS) {  // whole turns of the ring: no branch between the stages
+            stage(std::integral_constant<int, 0>{}, s);
+            stage(std::integral_constant<int, 1>{}, s + 1);
+            stage(std::integral_constant<int, 2>{}, s + 2);
+        }
+        if (s < nst) stage(std::integral_constant<int, 0>{}, s);
+        if (s + 1 < nst) stage(std::integral_constant<int, 1>{}, s + 1);
+    } else {
+#pragma unroll 1
+    for (int s = 0; s < nst; s++) {
+        // this wave's copies of A(s) and of the raw weights of stage s + 1 (direct B: of stage s) have landed, and its
+        // LDS writes are done
+        dq_wait_vm<(L::NS - 3) * L::OPS>();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+        {
         // the stage's fragments, then its MFMAs; the copies three stages ahead and the conversion of the next stage's
         // weights follow while the matrix cores work through them
         const uint32_t at = lds + L::A + (s % L::NS) * BM * 128;
@@ -828,6 +854,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
         issue(s + L::NS - 1);
         if (s + 1 < nst) convert(s + 1);
         }
+    }
     }
     dq_wait_vm<0>();  // the copies of the stages past the end
 
