@@ -1037,9 +1037,64 @@ def run_peaks(args, mx, be, threads):
     return result
 
 
+# The prefill products' shapes (M = 512 blocks of configs 3 and 4: q/k/v, attn_o, gate/up, down; and a larger M)
+VENDOR_SHAPES = ((512, 2048, 4096), (512, 2048, 2048), (512, 2048, 12288), (512, 6144, 2048), (1536, 2048, 12288),
+                 (4096, 4096, 4096))
+
+
+def run_vendor_gemm(args, mx, be, threads):
+    """The vendor library's GEMMs on plain operands at the prefill products' shapes, for scale: int8 x int8 -> int32
+    (torch._int_mm, hipBLASLt) and fp16 x fp16 -> fp16 (torch.matmul, hipBLASLt), operands resident, timed with torch
+    events on torch's stream. No per-block scales and no dequantization: what a Q8_0 product would take if it were a
+    plain int8 GEMM. Not a product path of this library; its ceiling for comparison."""
+    import torch
+    dev = "cuda"
+
+    def timed(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    rows = []
+    for M, K, N in VENDOR_SHAPES:
+        g = torch.Generator(device=dev).manual_seed(M * 7 + K * 5 + N)
+        a8 = torch.randint(-127, 128, (M, K), dtype=torch.int8, device=dev, generator=g)
+        b8 = torch.randint(-127, 128, (K, N), dtype=torch.int8, device=dev, generator=g)
+        ah = torch.randn(M, K, dtype=torch.float16, device=dev, generator=g)
+        bh = torch.randn(K, N, dtype=torch.float16, device=dev, generator=g)
+        ops = 2 * M * N * K
+        ms8 = timed(lambda: torch._int_mm(a8, b8), args.steps)
+        ms16 = timed(lambda: ah @ bh, args.steps)
+        r = {"M": M, "K": K, "N": N, "int8_us": round(ms8 * 1e3, 2), "int8_TOPs": round(ops / (ms8 * 1e-3) / 1e12, 1),
+             "int8_frac": round(ops / (ms8 * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4), "fp16_us": round(ms16 * 1e3, 2),
+             "fp16_TFLOPs": round(ops / (ms16 * 1e-3) / 1e12, 1),
+             "fp16_frac": round(ops / (ms16 * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4)}
+        rows.append(r)
+        log(f"M={M} K={K} N={N}: int8 {r['int8_us']:7.1f} us {r['int8_TOPs']:7.1f} TOP/s ({r['int8_frac']:.3f}); "
+            f"fp16 {r['fp16_us']:7.1f} us {r['fp16_TFLOPs']:7.1f} TFLOP/s ({r['fp16_frac']:.3f})")
+        del a8, b8, ah, bh
+    m512 = [r for r in rows if r["M"] == 512]
+    ops = sum(2 * r["M"] * r["N"] * r["K"] for r in m512)
+    us = sum(r["int8_us"] for r in m512)
+    result = base_result(args, round(ops / (us * 1e-6) / 1e12, 1), "TOP/s", us * 1e-3, "int8", {
+        "workload": "vendor int8 / fp16 GEMM (hipBLASLt through torch) at the prefill products' shapes",
+        "shapes": [list(s) for s in VENDOR_SHAPES]})
+    result["data"] = "synthetic (seeded uniform int8 and N(0,1) fp16 operands)"
+    result.update({"m512_block_int8_frac": round(ops / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4), "per_shape": rows})
+    return result
+
+
 WORKLOADS = {"decode": run_decode, "decode-full": run_decode_full, "matvec": run_matvec, "prefill-q4k": run_prefill_q4k, "asr-1.7b": run_asr,
-             "moe": run_moe, "peaks": run_peaks}
-DEFAULT_STEPS = {"decode": (300, 20), "decode-full": (100, 10), "matvec": (50, 5), "prefill-q4k": (20, 3), "asr-1.7b": (3, 1), "moe": (20, 3), "peaks": (5, 1)}
+             "moe": run_moe, "peaks": run_peaks, "vendor-gemm": run_vendor_gemm}
+DEFAULT_STEPS = {"decode": (300, 20), "decode-full": (100, 10), "matvec": (50, 5), "prefill-q4k": (20, 3), "asr-1.7b": (3, 1), "moe": (20, 3), "peaks": (5, 1),
+                 "vendor-gemm": (50, 3)}
 
 
 def main():
@@ -1077,6 +1132,10 @@ def main():
     if rank != 0:
         args.cpu_seconds = 0
 
+    if args.workload == "vendor-gemm":  # torch's own HIP runtime: initialised before (and without) libmx's
+        result = run_vendor_gemm(args, None, None, 1)
+        print(json.dumps(result), flush=True)
+        return
     mx = load_mx()
     if mx.device_count() < 1:
         print("no GPU visible to libmx", file=sys.stderr)
