@@ -864,11 +864,10 @@ def run_asr(args, mx, be, threads):
     # the prefill GEMM dequantizes Q8_0 weights and Q8_0-quantized activations to fp16 and accumulates in fp32 on
     # fp16 MFMA (--opt gemm_q8_0=1 selects the int8 MFMA GEMM); the decode mat-vecs use int8 dot products
     dq = be.get_option("gemm_q8_0") == 0
-    roof = (mfma_roofline("k_gemm_dq<Q8_0> (with its activation pass)", table,
-                          [l for l in table if l.startswith("prefill_M512")], FP16_PEAK_TFLOPS, "TFLOP/s") if dq else
-            mfma_roofline("k_gemm_q8_0_i8 (with its activation pass)", table,
-                          [l for l in table if l.startswith("prefill_M512")]))
-    roof["traffic"] = read_traffic("asr-1.7b") if dq else None
+    big = [l for l in table if l == f"prefill_M{max(blocks)}"]  # the largest block's products (512 rows as run)
+    roof = (mfma_roofline("k_gemm_dq<Q8_0> (with its activation pass)", table, big, FP16_PEAK_TFLOPS, "TFLOP/s")
+            if dq else mfma_roofline("k_gemm_q8_0_i8 (with its activation pass)", table, big))
+    roof["traffic"] = read_traffic("asr-1.7b") if dq and max(blocks) == 512 else None  # measured on 512-row blocks
     tops = pre_ops / (ms_pre * 1e-3) / 1e12
     tok_w = sum(L.weight_bytes for L in tok)
     result = base_result(args, round(tops, 2), "TOP/s", ms_step, "fp16" if dq else "int8", {
