@@ -413,10 +413,10 @@ def test_graph_replay_matches_eager(mx, be):
 
 # ----------------------------------------------------------------------------------------------- MUL_MAT, M > 8
 @pytest.mark.parametrize("M,N,K", [(9, 100, 1024), (64, 256, 2048), (130, 333, 1024), (512, 2048, 2048),
-                                   (100, 64, 6144), (650, 4500, 512), (300, 8100, 256)])
+                                   (100, 64, 6144), (650, 4500, 512), (300, 8100, 256), (520, 8200, 256)])
 def test_mul_mat_gemm_q8_0(mx, be, M, N, K):
-    """The last two take 128 x 128 tiles unsplit with ragged rows and columns; the last has four stages of K, one more
-    than the copy ring holds."""
+    """The last three take 128 x 128 tiles unsplit with ragged rows and columns (216, 192 and 325 workgroups: the last
+    more than the CUs); the last two have four stages of K, one more than the copy ring holds."""
     t = O.TYPE_Q8_0
     w = weights(t, N, K, 0x5EED0A00 + M + N)
     x = acts(0xAC700A00 + M, M, K)
