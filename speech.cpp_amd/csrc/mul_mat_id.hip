@@ -184,8 +184,26 @@ __global__ __launch_bounds__(256) void k_mmid_prep(MulMatIdArgs a) {
     else mmid_quant_row<TYPE>(a, (int64_t)blockIdx.x - 1);
 }
 
-// Weight chunks each lane requests before an expert's activation rows are copied to LDS (one-pass experts).
-constexpr int MMID_PRELOAD = 4;
+
+// Quantized activation row r of the scratch into LDS column col, in the layout the dots read (Q4_K: unit order, and
+// the sums of 32 from pairs of bsums).
+template <int TYPE>
+__device__ __forceinline__ void copy_act_row(const MulMatIdArgs &a, int64_t r, int col, int8_t *xq, float *xd,
+                                             int *xbs) {
+    const int K = (int)a.K;
+    const int nsc = TYPE == MX_TYPE_Q8_0 ? K / 32 : K / 256;
+    for (int k = 16 * threadIdx.x; k < K; k += 16 * 256) {
+        const int dst = TYPE == MX_TYPE_Q4_K ? q4u_xq_offset(k, K) : k;
+        *(int4 *)(xq + col * K + dst) = *(const int4 *)(a.xq + r * K + k);
+    }
+    for (int k = threadIdx.x; k < nsc; k += 256) xd[col * nsc + k] = a.xd[r * nsc + k];
+    if constexpr (TYPE == MX_TYPE_Q4_K) {
+        for (int k = threadIdx.x; k < K / 32; k += 256)
+            xbs[col * (K / 32) + k] = a.xbs[r * (K / 16) + 2 * k] + a.xbs[r * (K / 16) + 2 * k + 1];
+    } else if constexpr (TYPE != MX_TYPE_Q8_0) {
+        for (int k = threadIdx.x; k < K / 16; k += 256) xbs[col * (K / 16) + k] = a.xbs[r * (K / 16) + k];
+    }
+}
 
 // One workgroup per (block of 4 G weight rows, active expert): the expert's pairs in passes of up to NC columns, each
 // pass copying their quantized rows to LDS and streaming the rows' weights against them. An expert with at most NC
@@ -214,7 +232,7 @@ __global__ __launch_bounds__(256) void k_mmid_experts(MulMatIdArgs a) {
     const int nchunks = (int)(K / chunk_elems<TYPE>());
 
     if (cnt <= NC) {  // uniform: one pass, whose weight chunks go out before the activation copies
-        constexpr int PRE = MMID_PRELOAD;
+        constexpr int PRE = preload_of<TYPE>();  // requested before the activation rows are copied to LDS
         const int64_t prow = (int64_t)e * a.N + (has_row ? row : a.N - 1);  // rows past the end load the last row
         WChunk<TYPE> pre[PRE];
 #pragma unroll
@@ -226,11 +244,7 @@ __global__ __launch_bounds__(256) void k_mmid_experts(MulMatIdArgs a) {
             const int p = a.pairs[off + col];
             const int64_t t = p / a.n_ids, s = p % a.n_ids;
             const int64_t r = t * a.b_ne1 + (s % a.b_ne1);
-            for (int64_t k = 16 * threadIdx.x; k < K; k += 16 * 256)
-                *(int4 *)(xq + col * K + k) = *(const int4 *)(a.xq + r * K + k);
-            for (int64_t k = threadIdx.x; k < nsc; k += 256) xd[col * nsc + k] = a.xd[r * nsc + k];
-            if (TYPE != MX_TYPE_Q8_0)
-                for (int64_t k = threadIdx.x; k < K / 16; k += 256) xbs[col * (K / 16) + k] = a.xbs[r * (K / 16) + k];
+            copy_act_row<TYPE>(a, r, col, xq, xd, xbs);
         }
         __syncthreads();
         if (!has_row) return;  // whole LPR-lane groups leave together; no barrier follows
@@ -242,7 +256,7 @@ __global__ __launch_bounds__(256) void k_mmid_experts(MulMatIdArgs a) {
             const int c = sub + i * LPR;
             if (c < nchunks) dot_chunk<TYPE, NC, true>(pre[i], K, c, xq, xd, xbs, cnt, acc);
         }
-#pragma unroll 2
+#pragma unroll 1
         for (int c = sub + PRE * LPR; c < nchunks; c += LPR) chunk_dot<TYPE, NC, true>(a.w, grow, K, c, xq, xd, xbs, cnt, acc);
 #pragma unroll
         for (int c = 0; c < NC; c++) acc[c] = sum_lanes<LPR>(acc[c]);
@@ -266,18 +280,14 @@ __global__ __launch_bounds__(256) void k_mmid_experts(MulMatIdArgs a) {
             const int p = a.pairs[off + g0 + col];
             const int64_t t = p / a.n_ids, s = p % a.n_ids;
             const int64_t r = t * a.b_ne1 + (s % a.b_ne1);
-            for (int64_t k = 16 * threadIdx.x; k < K; k += 16 * 256)
-                *(int4 *)(xq + col * K + k) = *(const int4 *)(a.xq + r * K + k);
-            for (int64_t k = threadIdx.x; k < nsc; k += 256) xd[col * nsc + k] = a.xd[r * nsc + k];
-            if (TYPE != MX_TYPE_Q8_0)
-                for (int64_t k = threadIdx.x; k < K / 16; k += 256) xbs[col * (K / 16) + k] = a.xbs[r * (K / 16) + k];
+            copy_act_row<TYPE>(a, r, col, xq, xd, xbs);
         }
         __syncthreads();
         if (has_row) {
             float acc[NC];
 #pragma unroll
             for (int c = 0; c < NC; c++) acc[c] = 0.0f;
-#pragma unroll 2
+#pragma unroll 1
             for (int c = sub; c < nchunks; c += LPR) chunk_dot<TYPE, NC, true>(a.w, grow, K, c, xq, xd, xbs, ng, acc);
 #pragma unroll
             for (int c = 0; c < NC; c++) acc[c] = sum_lanes<LPR>(acc[c]);
@@ -316,9 +326,9 @@ static hipError_t launch_typed(const MulMatIdArgs &a, hipStream_t s) {
     for (int p = 0; p < a.nprob; p++) {
         b.w = a.wg[p];
         b.dst = a.dstg[p];
-        if (nchunks <= 16 * MMID_PRELOAD) {
+        if (nchunks <= 16 * preload_of<TYPE>()) {
             hipLaunchKernelGGL((k_mmid_experts<TYPE, 16>), dim3((unsigned)((a.N + 15) / 16), gy), dim3(256), lds, s, b);
-        } else if (nchunks <= 32 * MMID_PRELOAD) {
+        } else if (nchunks <= 32 * preload_of<TYPE>()) {
             hipLaunchKernelGGL((k_mmid_experts<TYPE, 32>), dim3((unsigned)((a.N + 7) / 8), gy), dim3(256), lds, s, b);
         } else {
             hipLaunchKernelGGL((k_mmid_experts<TYPE, 64>), dim3((unsigned)((a.N + 3) / 4), gy), dim3(256), lds, s, b);
@@ -369,6 +379,7 @@ static hipError_t launch_matvec_ids(const MulMatIdArgs &a, hipStream_t s) {
 
 hipError_t launch_mul_mat_id(const MulMatIdArgs &a, hipStream_t s) {
     if (a.n_ids * a.T == 0 || a.N == 0) return hipSuccess;
+    if (a.generic == 3 && mmid_small_supported(a)) return launch_mmid_small(a, s);
     if (a.n_ids * a.T <= a.matvec_pairs) return launch_matvec_ids(a, s);
     switch (a.type) {
         case MX_TYPE_Q8_0: return launch_typed<MX_TYPE_Q8_0>(a, s);

@@ -5,9 +5,15 @@
 // then times the exact integer sum. Only the order of the fp32 cross-block sum differs from the CPU.
 //
 // Activations in LDS, column c:
-//   xq[c*K + k]     int8 quants
+//   xq[c*K + k]     int8 quants (Q4_K weights: in unit order, below)
 //   xd[c*nsc + b]   fp32 scale of block b (the fp16-rounded d of Q8_0/Q8_1 for Q8_0 weights; Q8_K's fp32 d otherwise)
-//   xbs[c*K/16 + j] sum of quants 16j..16j+15 (K-quants only; Q8_K's bsums)
+//   xbs[c*K/16 + j] sum of quants 16j..16j+15 (Q5_K / Q6_K: Q8_K's bsums); Q4_K: xbs[c*K/32 + j], the sums of
+//                   quants 32j..32j+31 (a sub-block's, two bsums added)
+//
+// Q4_K is taken a unit of 128 elements at a time -- half a super-block: 64 bytes of qs, four sub-blocks and their
+// scales / mins -- so one lane unpacks the 6-bit scales of four sub-blocks at once. Its activation quants sit in LDS
+// as 16-byte pieces, piece i of unit u at byte 16 (i * K/128 + u): the lanes of a row read piece i of consecutive
+// units from consecutive 16-byte words (no bank conflicts), where units in place would be 128 bytes apart.
 #pragma once
 
 #include "mx_common.h"
@@ -23,9 +29,20 @@ __device__ __forceinline__ int dot16(int4 a, int4 b, int acc) {
     return acc;
 }
 
-// Chunks per row: a Q8_0 chunk is 16 quants (half a block); a K-quant chunk is 32 elements (16 bytes of qs / ql).
+// Chunks per row: a Q8_0 chunk is 16 quants (half a block); a Q5_K / Q6_K chunk is 32 elements (16 bytes of qs /
+// ql); a Q4_K chunk is a unit of 128 elements (64 bytes of qs).
 template <int TYPE>
-__host__ __device__ constexpr int chunk_elems() { return TYPE == MX_TYPE_Q8_0 ? 16 : 32; }
+__host__ __device__ constexpr int chunk_elems() { return TYPE == MX_TYPE_Q8_0 ? 16 : (TYPE == MX_TYPE_Q4_K ? 128 : 32); }
+// Chunks a lane loads ahead of the activation prologue (the same bytes in flight: 64 per lane).
+template <int TYPE>
+__host__ __device__ constexpr int preload_of() { return TYPE == MX_TYPE_Q4_K ? 1 : 4; }
+// ints of xbs per activation column.
+template <int TYPE>
+__host__ __device__ constexpr int64_t xbs_per_col(int64_t K) { return TYPE == MX_TYPE_Q4_K ? K / 32 : K / 16; }
+// Byte of Q4_K activation element e in its column's xq (unit order).
+__device__ __forceinline__ int q4u_xq_offset(int e, int K) {
+    return ((((e >> 4) & 7) * (K >> 7) + (e >> 7)) << 4) + (e & 15);
+}
 
 // Unpack the 6-bit scale and min of sub-blocks j and j+1 (j even) from Q4_K's 12 packed bytes held in three words
 // (ggml-quants.c get_scale_min_k4).
@@ -54,7 +71,8 @@ struct WChunk<MX_TYPE_Q8_0> {
 };
 template <>
 struct WChunk<MX_TYPE_Q4_K> {
-    int4 q;        // 32 nibbles: 16 of sub-block j, 16 of sub-block j + 1
+    int4 q[4];     // 64 qs bytes of half h of a super-block: q[0..1] sub-blocks 4h (low nibbles), 4h + 1 (high);
+                   // q[2..3] sub-blocks 4h + 2 (low), 4h + 3 (high)
     uint32_t s0, s1, s2;  // the 12 packed scale / min bytes
     uint32_t dm;   // fp16 d | fp16 dmin << 16
 };
@@ -89,9 +107,11 @@ __device__ __forceinline__ WChunk<TYPE> load_chunk(const WPlanes &w, int64_t gro
     if constexpr (TYPE == MX_TYPE_Q8_0) {
         r.q = ld_w16(w.p0 + grow * K + 16 * c);
         r.d = ld_w16b(w.p1 + (grow * (K / 32) + (c >> 1)) * 2);
-    } else if constexpr (TYPE == MX_TYPE_Q4_K) {
-        const int64_t blk = grow * (K / 256) + (c >> 3);
-        r.q = ld_w16(w.p0 + blk * 128 + 16 * (c & 7));
+    } else if constexpr (TYPE == MX_TYPE_Q4_K) {  // unit c: half c & 1 of super-block c >> 1
+        const int64_t blk = grow * (K / 256) + (c >> 1);
+        const uint8_t *qp = w.p0 + blk * 128 + 64 * (c & 1);
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.q[i] = ld_w16(qp + 16 * i);
         const uint8_t *sp = w.p1 + blk * 12;
         r.s0 = ld_w32(sp);
         r.s1 = ld_w32(sp + 4);
@@ -133,7 +153,44 @@ __device__ __forceinline__ void dot_chunk(const WChunk<TYPE> &wc, int64_t K, int
             const int s = dot16(wc.q, xv, 0);
             acc[col] += (float)s * (dw * xd[col * nblk + (c >> 1)]);
         }
-    } else if constexpr (TYPE == MX_TYPE_Q4_K || TYPE == MX_TYPE_Q5_K) {
+    } else if constexpr (TYPE == MX_TYPE_Q4_K) {
+        // unit c: half h of super-block sb, sub-blocks 4h .. 4h + 3 (get_scale_min_k4 of ggml-quants.c for all four:
+        // h = 0 takes the low six bits of bytes 0..3 / 4..7, h = 1 the nibbles of bytes 8..11 with the top two bits
+        // of bytes 0..3 / 4..7)
+        const int64_t nsb = K / 256, nu = K / 128;
+        const int sb = c >> 1;
+        const bool h = (c & 1) != 0;
+        const uint32_t SC = h ? ((wc.s2 & 0x0F0F0F0Fu) | ((wc.s0 >> 2) & 0x30303030u)) : (wc.s0 & 0x3F3F3F3Fu);
+        const uint32_t MN = h ? (((wc.s2 >> 4) & 0x0F0F0F0Fu) | ((wc.s1 >> 2) & 0x30303030u)) : (wc.s1 & 0x3F3F3F3Fu);
+        const float d = h2f((uint16_t)(wc.dm & 0xFFFF)), dmin = h2f((uint16_t)(wc.dm >> 16));
+        int4 lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int4 q = wc.q[i];
+            lo[i] = make_int4(q.x & 0x0F0F0F0F, q.y & 0x0F0F0F0F, q.z & 0x0F0F0F0F, q.w & 0x0F0F0F0F);
+            hi[i] = make_int4((q.x >> 4) & 0x0F0F0F0F, (q.y >> 4) & 0x0F0F0F0F, (q.z >> 4) & 0x0F0F0F0F,
+                              (q.w >> 4) & 0x0F0F0F0F);
+        }
+#pragma unroll
+        for (int col = 0; col < NC; col++) {
+            if (GUARD && col >= ncols) break;
+            // pieces 0..7 of the unit's 128 quants (16 each): sub-block k covers pieces 2k, 2k + 1
+            const int8_t *xc = xq + col * K + 16 * c;
+            const int4 *xp = (const int4 *)xc;
+            const int64_t pstride = nu;  // int4s between pieces i and i + 1 of a unit
+            const int d0 = dot16(lo[1], xp[1 * pstride], dot16(lo[0], xp[0], 0));
+            const int d1 = dot16(hi[1], xp[3 * pstride], dot16(hi[0], xp[2 * pstride], 0));
+            const int d2 = dot16(lo[3], xp[5 * pstride], dot16(lo[2], xp[4 * pstride], 0));
+            const int d3 = dot16(hi[3], xp[7 * pstride], dot16(hi[2], xp[6 * pstride], 0));
+            const int4 b = *(const int4 *)(xbs + col * (K / 32) + 4 * c);
+            const int isum = (int)(SC & 0xFF) * d0 + (int)((SC >> 8) & 0xFF) * d1 + (int)((SC >> 16) & 0xFF) * d2 +
+                             (int)(SC >> 24) * d3;
+            const int msum = (int)(MN & 0xFF) * b.x + (int)((MN >> 8) & 0xFF) * b.y + (int)((MN >> 16) & 0xFF) * b.z +
+                             (int)(MN >> 24) * b.w;
+            const float dx = xd[col * nsb + sb];
+            acc[col] += (d * dx) * (float)isum - (dmin * dx) * (float)msum;
+        }
+    } else if constexpr (TYPE == MX_TYPE_Q5_K) {
         const int64_t nsb = K / 256;
         const int sb = c >> 3, t = c & 7;
         const float d = h2f((uint16_t)(wc.dm & 0xFFFF)), dmin = h2f((uint16_t)(wc.dm >> 16));
@@ -212,6 +269,8 @@ __device__ __forceinline__ void chunk_dot(const WPlanes &w, int64_t grow, int64_
 __host__ __device__ inline size_t act_lds_bytes(int type, int64_t K, int ncols) {
     if (type == MX_TYPE_F16 || type == MX_TYPE_F32) return (size_t)ncols * (size_t)K * 4;  // fp32 (or fp16-rounded)
     if (type == MX_TYPE_Q8_0) return (size_t)ncols * (size_t)K + (size_t)ncols * (size_t)(K / 32) * 4;
+    if (type == MX_TYPE_Q4_K)
+        return (size_t)ncols * (size_t)K + (size_t)ncols * (size_t)(K / 256) * 4 + (size_t)ncols * (size_t)(K / 32) * 4;
     return (size_t)ncols * (size_t)K + (size_t)ncols * (size_t)(K / 256) * 4 + (size_t)ncols * (size_t)(K / 16) * 4;
 }
 
