@@ -122,8 +122,7 @@ MX_API int mx_backend_set_rounding(mx_backend *be, int rounding);
  *   MX_OPT_GEMM_SPLIT         K splits of the fp16 dequantizing GEMM, 0 (picked) .. 64
  *   MX_OPT_MATVEC_LPR         lanes per weight row of the mat-vec: 0 (picked), 16, 32, 64
  *   MX_OPT_MMID_KERNEL        MUL_MAT_ID with many pairs: 0 as picked (Q4_K: the grouped MFMA product), 1 the
- *                             experts kernel, 2 the grouped MFMA product, 3 the small-batch kernel (no bucketing
- *                             pass; up to 1024 pairs and 1024 experts, at any pair count)
+ *                             experts kernel, 2 the grouped MFMA product
  *   MX_OPT_MMID_MATVEC_PAIRS  MUL_MAT_ID runs as one mat-vec launch up to this many (token, slot) pairs (16; 0..4096)
  *   MX_OPT_MMID_CHUNK         pairs per chunk of an expert's pairs in the grouped Q4_K product: 0 as picked (16 when
  *                             the pairs average at most four per expert, else 32), 16 (one 16-row tile per chunk),

@@ -379,7 +379,6 @@ static hipError_t launch_matvec_ids(const MulMatIdArgs &a, hipStream_t s) {
 
 hipError_t launch_mul_mat_id(const MulMatIdArgs &a, hipStream_t s) {
     if (a.n_ids * a.T == 0 || a.N == 0) return hipSuccess;
-    if (a.generic == 3 && mmid_small_supported(a)) return launch_mmid_small(a, s);
     if (a.n_ids * a.T <= a.matvec_pairs) return launch_matvec_ids(a, s);
     switch (a.type) {
         case MX_TYPE_Q8_0: return launch_typed<MX_TYPE_Q8_0>(a, s);

@@ -335,7 +335,7 @@ MX_API int mx_backend_set_option(mx_backend *be, int option, int64_t value) {
             o.matvec_lpr = (int)value;
             return MX_SUCCESS;
         case MX_OPT_MMID_KERNEL:
-            if (!in({0, 1, 2, 3})) break;
+            if (!in({0, 1, 2})) break;
             o.mmid_kernel = (int)value;
             return MX_SUCCESS;
         case MX_OPT_MMID_MATVEC_PAIRS:

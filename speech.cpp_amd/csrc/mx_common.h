@@ -264,8 +264,7 @@ struct MulMatIdArgs {
     int32_t *ntiles;       // [1] tiles written by the bucket kernel
     int64_t max_tiles;
     int *err;
-    int generic;               // 0 as picked, 1: the experts kernel, 2: the grouped MFMA product (Q4_K),
-                               // 3: the small-batch kernel (no bucketing pass)
+    int generic;               // 0 as picked, 1: the experts kernel, 2: the grouped MFMA product (Q4_K)
     int chunk;                 // pairs per chunk of an expert's pairs: MMID_CHUNK_SMALL or MMID_CHUNK
     // products sharing b and ids (1..4): product p reads expert weights wg[p] into dstg[p] (dst's strides); the
     // kernels that take one product at a time read w / dst, which the launcher points at each in turn
@@ -394,13 +393,5 @@ hipError_t launch_mul_mat_id(const MulMatIdArgs &a, hipStream_t s);
 // Q4_K experts as a grouped product over chunks of up to a.chunk of an expert's pairs (16 x 16 x 64 int8 MFMA).
 bool mmid_q4k_supported(const MulMatIdArgs &a);  // Q4_K, K <= 2048
 hipError_t launch_mmid_q4k(const MulMatIdArgs &a, hipStream_t s);
-// Small batches: one launch with no scratch, each workgroup finding its expert's pairs from the ids itself (up to
-// MMID_SMALL_MAX_PAIRS pairs, MMID_SMALL_MAX_E experts; MMID_SMALL_COLS activation rows of K per pass in at most
-// MMID_SMALL_MAX_LDS bytes).
-constexpr int MMID_SMALL_MAX_PAIRS = 1024, MMID_SMALL_MAX_E = 1024, MMID_SMALL_COLS = 4, MMID_SMALL_MAX_LDS = 48 * 1024;
-constexpr int MMID_SMALL_WGS = 1536;  // workgroups a launch aims at (row blocks per workgroup follow, 1 to 8)
-constexpr int MMID_SMALL_PRE = 2;     // weight chunks each lane holds per row block
-bool mmid_small_supported(const MulMatIdArgs &a);
-hipError_t launch_mmid_small(const MulMatIdArgs &a, hipStream_t s);
 
 }  // namespace mx

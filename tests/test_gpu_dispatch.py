@@ -11,7 +11,7 @@ import pytest
 
 import oracle as O
 from helpers import rel_err
-from test_gpu_parity import NAMES, QTYPES, TIGHT, acts, check_product, mmid_case, weights
+from test_gpu_parity import NAMES, TIGHT, acts, check_product, mmid_case, weights
 
 pytestmark = pytest.mark.gpu
 
@@ -153,66 +153,10 @@ def test_mmid_every_path(mx, be, t):
         assert rel_err(y, y_ref) <= TIGHT
 
 
-@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
-def test_mmid_small_kernel(mx, be, t):
-    """The small-batch MUL_MAT_ID kernel (no bucketing pass) forced at every batch form: one token, a few tokens with
-    b broadcast and per slot, the 64-expert top-4 layer shape at 16 tokens, experts with more pairs than one pass
-    holds (four per pass) in a skewed routing, and 1024 pairs (the most it takes) over 8 experts."""
-    cases = [dict(E=8, K=512, N=96, n_ids=2, T=1, bcast=True), dict(E=8, K=512, N=96, n_ids=2, T=3, bcast=True),
-             dict(E=8, K=512, N=96, n_ids=2, T=3, bcast=False), dict(E=64, K=2048, N=136, n_ids=4, T=16, bcast=True),
-             dict(E=64, K=1536, N=200, n_ids=4, T=16, bcast=False),
-             dict(E=16, K=1024, N=200, n_ids=4, T=40, bcast=False, skew=3.0),
-             dict(E=8, K=256, N=72, n_ids=4, T=256, bcast=True)]
-    with be.options(mmid_kernel=3):
-        for i, c in enumerate(cases):
-            y, y_ref = mmid_case(mx, be, t, seed=0x5EED3700 + 16 * i + t, **c)
-            assert rel_err(y, y_ref) <= TIGHT, f"case {c}"
-
-
-@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K], ids=lambda t: NAMES[t])
-def test_mmid_small_kernel_group(mx, be, t):
-    """Gate and up in one small-batch launch (the product in grid z): the same bits as each product alone."""
-    E, K, N, n_ids, T = 16, 1024, 200, 4, 5
-    seed = 0x5EED3780 + t
-    wg = weights(t, E * N, K, seed).reshape(E, N, -1)
-    wu = weights(t, E * N, K, seed + 1).reshape(E, N, -1)
-    x = acts(seed + 2, T, K).reshape(T, 1, K)
-    ids = np.argsort(-np.random.default_rng(seed).standard_normal((T, E)), axis=1)[:, :n_ids].astype(np.int32)
-    Wg = be.tensor(t, (K, N, E), wg.reshape(E * N, -1))
-    Wu = be.tensor(t, (K, N, E), wu.reshape(E * N, -1))
-    Xt = be.tensor(mx.F32, (K, 1, T), x)
-    It = be.tensor(mx.I32, (n_ids, T), ids)
-    Ys = [be.tensor(mx.F32, (N, n_ids, T)) for _ in range(2)]
-    Yg = [be.tensor(mx.F32, (N, n_ids, T)) for _ in range(2)]
-    with be.options(mmid_kernel=3):
-        be.mul_mat_id(Wg, Xt, It, Ys[0])
-        be.mul_mat_id(Wu, Xt, It, Ys[1])
-        be.mul_mat_id_group([Wg, Wu], Xt, It, Yg)
-    be.sync()
-    for a, b, w in zip(Ys, Yg, (wg, wu)):
-        assert np.array_equal(a.numpy(), b.numpy())
-        assert rel_err(b.numpy().reshape(T, n_ids, N), O.mul_mat_id(t, w, x, ids)) <= TIGHT
-
-
-def test_mmid_small_kernel_bad_expert(mx, be):
-    """Ids outside [0, E) are left out and reported by the small-batch kernel as by the bucketing pass."""
-    K, N, E = 256, 32, 4
-    Wt = be.tensor(mx.Q8_0, (K, N, E), weights(O.TYPE_Q8_0, E * N, K, 9))
-    Xt = be.tensor(mx.F32, (K, 1, 2), acts(10, 2, K))
-    It = be.tensor(mx.I32, (2, 2), np.array([[0, 1], [3, E]], np.int32))
-    Yt = be.tensor(mx.F32, (N, 2, 2))
-    with be.options(mmid_kernel=3):
-        be.mul_mat_id(Wt, Xt, It, Yt)
-    with pytest.raises(mx.MxError) as e:
-        be.sync()
-    assert e.value.code == mx.INVALID
-    be.sync()
-
-
 # --------------------------------------------------------------------------------------- refusals
 def test_options_refused(mx, be):
     for name, bad in [("gemm_q8_0", 2), ("tile_m", 96), ("matvec_lpr", 8), ("split", -1), ("mmid_matvec_pairs", -1),
-                      ("mmid_kernel", 4), ("mmid_chunk", 8)]:
+                      ("mmid_kernel", 3), ("mmid_chunk", 8)]:
         with pytest.raises(mx.MxError) as e:
             be.set_option(name, bad)
         assert e.value.code == mx.INVALID
