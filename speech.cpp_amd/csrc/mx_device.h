@@ -103,37 +103,29 @@ __device__ __forceinline__ int quant32_lane(float4 v, int rounding, float *d_out
 // ------------------------------------------------------------------------------------------------------------------
 __device__ __forceinline__ int quant256_wave(float4 v, int lane, float *d_out, int *bsum_out) {
     const float e[4] = {v.x, v.y, v.z, v.w};
-    uint32_t best_bits = __float_as_uint(fabsf(e[0]));
-    uint32_t best_idx = 4u * lane;
-#pragma unroll
-    for (int j = 1; j < 4; j++) {
-        const uint32_t b = __float_as_uint(fabsf(e[j]));
-        if (b > best_bits) { best_bits = b; best_idx = 4u * lane + j; }
-    }
-    // Largest |x| wins; among equal |x| the smallest index (the first one ggml's strict '>' scan keeps): the key
-    // (|x| bits, ~index) is maximal exactly there. Reduced within rows of 16, then across rows into lane 63.
-    uint32_t khi = best_bits, klo = 0xFFFFFFFFu - best_idx;
-    auto take = [&](uint32_t ohi, uint32_t olo) {
-        const bool gt = ohi > khi || (ohi == khi && olo > klo);
-        khi = gt ? ohi : khi;
-        klo = gt ? olo : klo;
-    };
-    take(dpp_i<dpp::XOR1>(0, khi), dpp_i<dpp::XOR1>(0, klo));
-    take(dpp_i<dpp::XOR2>(0, khi), dpp_i<dpp::XOR2>(0, klo));
-    take(dpp_i<dpp::HALF_MIRROR>(0, khi), dpp_i<dpp::HALF_MIRROR>(0, klo));
-    take(dpp_i<dpp::MIRROR>(0, khi), dpp_i<dpp::MIRROR>(0, klo));
-    take(dpp_i<dpp::BCAST15, 0xA>(0, khi), dpp_i<dpp::BCAST15, 0xA>(0, klo));
-    take(dpp_i<dpp::BCAST31, 0xC>(0, khi), dpp_i<dpp::BCAST31, 0xC>(0, klo));
-    const uint32_t amax_bits = (uint32_t)__builtin_amdgcn_readlane((int)khi, 63);
-    const uint32_t idx = 0xFFFFFFFFu - (uint32_t)__builtin_amdgcn_readlane((int)klo, 63);
-    const uint32_t c = idx & 3u;  // every lane picks component idx%4; lane idx/4's is the block's max
-    const float mine = c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
-    const float maxv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), (int)(idx >> 2)));
-    if (amax_bits == 0) {
+    const float ax = fabsf(v.x), ay = fabsf(v.y), az = fabsf(v.z), aw = fabsf(v.w);
+    // amax: the largest |x| (fmaxf passes NaNs over, as ggml's strict '>' scan does), reduced within rows of 16, then
+    // across rows into lane 63
+    float a = fmaxf(fmaxf(ax, ay), fmaxf(az, aw));
+    a = fmaxf(a, dpp_f<dpp::XOR1>(0.0f, a));
+    a = fmaxf(a, dpp_f<dpp::XOR2>(0.0f, a));
+    a = fmaxf(a, dpp_f<dpp::HALF_MIRROR>(0.0f, a));
+    a = fmaxf(a, dpp_f<dpp::MIRROR>(0.0f, a));
+    a = fmaxf(a, dpp_f<dpp::BCAST15, 0xA>(0.0f, a));
+    a = fmaxf(a, dpp_f<dpp::BCAST31, 0xC>(0.0f, a));
+    const float amax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 63));
+    if (amax == 0.0f) {
         *d_out = 0.0f;
         *bsum_out = 0;
         return 0;
     }
+    // max: the element of the first index (4 lane + j) whose |x| is amax -- the lowest lane holding one, its lowest j
+    const uint64_t m0 = __ballot(ax == amax), m1 = __ballot(ay == amax), m2 = __ballot(az == amax),
+                   m3 = __ballot(aw == amax);
+    const int L = __builtin_ctzll(m0 | m1 | m2 | m3);
+    const int c = ((m0 >> L) & 1) ? 0 : (((m1 >> L) & 1) ? 1 : (((m2 >> L) & 1) ? 2 : 3));
+    const float mine = c == 0 ? v.x : (c == 1 ? v.y : (c == 2 ? v.z : v.w));
+    const float maxv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), L));
     const float iscale = -127.0f / maxv;
     int q[4];
 #pragma unroll
