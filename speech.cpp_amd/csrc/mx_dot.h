@@ -108,15 +108,18 @@ __device__ __forceinline__ WChunk<TYPE> load_chunk(const WPlanes &w, int64_t gro
         r.q = ld_w16(w.p0 + grow * K + 16 * c);
         r.d = ld_w16b(w.p1 + (grow * (K / 32) + (c >> 1)) * 2);
     } else if constexpr (TYPE == MX_TYPE_Q4_K) {  // unit c: half c & 1 of super-block c >> 1
+        // Plain loads: a lane reads its 64 bytes in four 16-byte loads, so each 128-byte line is met by four load
+        // instructions, and with the streaming hint a dense 61440 x 2048 product took 22.0 us against 15.4 us with
+        // plain loads (its arithmetic switched off in both).
         const int64_t blk = grow * (K / 256) + (c >> 1);
         const uint8_t *qp = w.p0 + blk * 128 + 64 * (c & 1);
 #pragma unroll
-        for (int i = 0; i < 4; i++) r.q[i] = ld_w16(qp + 16 * i);
-        const uint8_t *sp = w.p1 + blk * 12;
-        r.s0 = ld_w32(sp);
-        r.s1 = ld_w32(sp + 4);
-        r.s2 = ld_w32(sp + 8);
-        r.dm = ld_w32(w.p2 + blk * 4);
+        for (int i = 0; i < 4; i++) r.q[i] = *(const int4 *)(qp + 16 * i);
+        const uint32_t *sp = (const uint32_t *)(w.p1 + blk * 12);
+        r.s0 = sp[0];
+        r.s1 = sp[1];
+        r.s2 = sp[2];
+        r.dm = *(const uint32_t *)(w.p2 + blk * 4);
     } else if constexpr (TYPE == MX_TYPE_Q5_K) {
         const int64_t blk = grow * (K / 256) + (c >> 3);
         r.q = ld_w16(w.p0 + blk * 128 + 16 * (c & 7));
