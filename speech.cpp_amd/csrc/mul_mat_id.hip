@@ -205,6 +205,38 @@ __device__ __forceinline__ void copy_act_row(const MulMatIdArgs &a, int64_t r, i
     }
 }
 
+// Q4_K rows against the pass's activation columns one column at a time (a runtime loop: the unit's decoded codes are
+// shared, and the registers stay those of one column whatever the pass holds), each column's units summed in the
+// order the many-column dot sums them. `pre` holds the lane's first unit when `held`.
+template <int LPR>
+__device__ __forceinline__ void experts_q4k_columns(const MulMatIdArgs &a, const WChunk<MX_TYPE_Q4_K> &pre, bool held,
+                                                    int64_t grow, int64_t row, int sub, int nchunks, int first, int ng,
+                                                    const int8_t *xq, const float *xd, const int *xbs) {
+    const int64_t K = a.K;
+#pragma unroll 1
+    for (int col = 0; col < ng; col++) {
+        const int8_t *cq = xq + col * K;
+        const float *cd = xd + col * (K / 256);
+        const int *cb = xbs + col * (K / 32);
+        float acc = 0.0f;
+        int c = sub;
+        if (held) {
+            if (c < nchunks) dot_chunk<MX_TYPE_Q4_K, 1, false>(pre, K, c, cq, cd, cb, 1, &acc);
+            c += LPR;
+        }
+#pragma unroll 1
+        for (; c < nchunks; c += LPR)
+            dot_chunk<MX_TYPE_Q4_K, 1, false>(load_chunk<MX_TYPE_Q4_K>(a.w, grow, K, c), K, c, cq, cd, cb, 1, &acc);
+        acc = sum_lanes<LPR>(acc);
+        if (sub == LPR - 1) {
+            const int p = a.pairs[first + col];
+            const int64_t t = p / a.n_ids, s = p % a.n_ids;
+            float *y = (float *)((uint8_t *)a.dst + s * a.dst_nb1 + t * a.dst_nb2);
+            y[row] = acc;
+        }
+    }
+}
+
 // One workgroup per (block of 4 G weight rows, active expert): the expert's pairs in passes of up to NC columns, each
 // pass copying their quantized rows to LDS and streaming the rows' weights against them. An expert with at most NC
 // pairs (every one at small batches) runs in one pass whose weight loads go out first.
@@ -248,26 +280,31 @@ __global__ __launch_bounds__(256) void k_mmid_experts(MulMatIdArgs a) {
         }
         __syncthreads();
         if (!has_row) return;  // whole LPR-lane groups leave together; no barrier follows
-        float acc[NC];
+        if constexpr (TYPE == MX_TYPE_Q4_K) {
+            static_assert(PRE == 1, "one held Q4_K unit");
+            experts_q4k_columns<LPR>(a, pre[0], true, grow, row, sub, nchunks, off, cnt, xq, xd, xbs);
+        } else {
+            float acc[NC];
 #pragma unroll
-        for (int c = 0; c < NC; c++) acc[c] = 0.0f;
+            for (int c = 0; c < NC; c++) acc[c] = 0.0f;
 #pragma unroll
-        for (int i = 0; i < PRE; i++) {
-            const int c = sub + i * LPR;
-            if (c < nchunks) dot_chunk<TYPE, NC, true>(pre[i], K, c, xq, xd, xbs, cnt, acc);
-        }
+            for (int i = 0; i < PRE; i++) {
+                const int c = sub + i * LPR;
+                if (c < nchunks) dot_chunk<TYPE, NC, true>(pre[i], K, c, xq, xd, xbs, cnt, acc);
+            }
 #pragma unroll 1
-        for (int c = sub + PRE * LPR; c < nchunks; c += LPR) chunk_dot<TYPE, NC, true>(a.w, grow, K, c, xq, xd, xbs, cnt, acc);
+            for (int c = sub + PRE * LPR; c < nchunks; c += LPR) chunk_dot<TYPE, NC, true>(a.w, grow, K, c, xq, xd, xbs, cnt, acc);
 #pragma unroll
-        for (int c = 0; c < NC; c++) acc[c] = sum_lanes<LPR>(acc[c]);
-        if (sub == LPR - 1) {
+            for (int c = 0; c < NC; c++) acc[c] = sum_lanes<LPR>(acc[c]);
+            if (sub == LPR - 1) {
 #pragma unroll
-            for (int col = 0; col < NC; col++) {
-                if (col < cnt) {
-                    const int p = a.pairs[off + col];
-                    const int64_t t = p / a.n_ids, s = p % a.n_ids;
-                    float *y = (float *)((uint8_t *)a.dst + s * a.dst_nb1 + t * a.dst_nb2);
-                    y[row] = acc[col];
+                for (int col = 0; col < NC; col++) {
+                    if (col < cnt) {
+                        const int p = a.pairs[off + col];
+                        const int64_t t = p / a.n_ids, s = p % a.n_ids;
+                        float *y = (float *)((uint8_t *)a.dst + s * a.dst_nb1 + t * a.dst_nb2);
+                        y[row] = acc[col];
+                    }
                 }
             }
         }
@@ -283,7 +320,11 @@ __global__ __launch_bounds__(256) void k_mmid_experts(MulMatIdArgs a) {
             copy_act_row<TYPE>(a, r, col, xq, xd, xbs);
         }
         __syncthreads();
-        if (has_row) {
+        if constexpr (TYPE == MX_TYPE_Q4_K) {
+            if (has_row)
+                experts_q4k_columns<LPR>(a, WChunk<MX_TYPE_Q4_K>{}, false, grow, row, sub, nchunks, off + g0, ng, xq, xd,
+                                         xbs);
+        } else if (has_row) {
             float acc[NC];
 #pragma unroll
             for (int c = 0; c < NC; c++) acc[c] = 0.0f;
