@@ -26,6 +26,7 @@ Prints one JSON line. --gpus N > 1 exits: one GPU is measured.
 from __future__ import annotations
 
 import argparse
+import gc
 import subprocess
 import importlib.util
 import json
@@ -1096,6 +1097,33 @@ DEFAULT_STEPS = {"decode": (300, 20), "decode-full": (100, 10), "matvec": (50, 5
                  "vendor-gemm": (50, 3)}
 
 
+def other_configs(args, mx, be, threads):
+    """The other benchmark configurations, each at its default steps without a CPU sample, summarized for the default
+    line: value, unit, time per step and the dominant kernel's roofline fraction (one after another on this backend;
+    each workload's tensors are freed before the next)."""
+    out = {}
+    for w in ("matvec", "prefill-q4k", "asr-1.7b", "moe"):
+        sub = argparse.Namespace(**vars(args))
+        sub.steps, sub.warmup = DEFAULT_STEPS[w]
+        sub.cpu_seconds, sub.blocks, sub.batches = 0, None, None
+        log(f"configs: {w}")
+        r = WORKLOADS[w](sub, mx, be, threads)
+        roof = r.get("roofline") or {}
+        out[w] = {"value": r["value"], "unit": r["unit"], "ms_per_step": r["ms_per_step"],
+                  "workload": r["config"]["workload"], "roofline_frac": roof.get("frac"), "bound": roof.get("bound"),
+                  "kernel": roof.get("kernel")}
+        for k in ("hbm_frac", "decode_tok_s", "decode_hbm_frac", "prefill_ms"):
+            if k in r:
+                out[w][k] = r[k]
+        if "per_batch" in r:
+            out[w]["per_batch"] = [{"T": b["T"], "us_per_layer": b["us_per_layer"], "hbm_frac": b["hbm_frac"]}
+                                   for b in r["per_batch"]]
+        del r
+        gc.collect()
+        be.sync()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1108,6 +1136,9 @@ def main():
     ap.add_argument("--unfused", action="store_true", help="decode-full: one launch per ggml node, no fusions")
     ap.add_argument("--no-full-step", dest="full_step", action="store_false",
                     help="decode: skip timing the whole step (decode_full_tok_s) beside the products")
+    ap.add_argument("--no-configs", dest="configs", action="store_false",
+                    help="decode: skip the other configurations' summaries (matvec, prefill-q4k, asr-1.7b, moe) that "
+                         "the default line carries under 'configs'")
     ints = lambda v: [int(t) for t in v.split(",")]
     ap.add_argument("--blocks", type=ints, default=None,
                     help="asr-1.7b: prefill block rows (default 512,512,512,28; counter passes use 512,512,512)")
@@ -1148,6 +1179,8 @@ def main():
     EVICT = make_evictor(mx, be)
     threads = max(1, len(os.sched_getaffinity(0)))
     result = WORKLOADS[args.workload](args, mx, be, threads)
+    if args.workload == "decode" and args.configs:
+        result["configs"] = other_configs(args, mx, be, threads)
     be.close()
     if rank == 0:
         print(json.dumps(result), flush=True)
