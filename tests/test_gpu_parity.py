@@ -317,6 +317,15 @@ def test_mul_mat_id_chunk_edges(mx, be, t, chunk):
 
 
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+def test_mul_mat_id_long_rows(mx, be, t):
+    """K = 4096, past what the grouped Q4_K product keeps in LDS: the experts kernel by default, in one pass (20
+    tokens over 16 experts) and in several passes of eight pairs (40 tokens over 4 experts, ~20 pairs each)."""
+    for E, T, seed in ((16, 20, 0x5EED0E00), (4, 40, 0x5EED0E40)):
+        y, y_ref = mmid_case(mx, be, t, E=E, K=4096, N=72, n_ids=2, T=T, bcast=False, seed=seed + t)
+        assert rel_err(y, y_ref) <= TIGHT, f"E {E}, T {T}"
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
 def test_mul_mat_id_moe_layer_shape(mx, be, t):
     """The drama3-like layer's down product (64 experts, top-4 of 64 tokens, K = 1536, b per slot) on 520 of its
     2048 output rows."""
