@@ -205,7 +205,7 @@ __device__ __forceinline__ void dot_chunk(const WChunk<TYPE> &wc, int64_t K, int
         int4 qlo = make_int4(q.x & 0x0F0F0F0F, q.y & 0x0F0F0F0F, q.z & 0x0F0F0F0F, q.w & 0x0F0F0F0F);
         int4 qhi = make_int4((q.x >> 4) & 0x0F0F0F0F, (q.y >> 4) & 0x0F0F0F0F, (q.z >> 4) & 0x0F0F0F0F,
                              (q.w >> 4) & 0x0F0F0F0F);
-        if constexpr (TYPE == MX_TYPE_Q5_K) {  // codes 0..31: bit 4 of sub-block j sits in bit j of each qh byte
+        {  // codes 0..31: bit 4 of sub-block j sits in bit j of each qh byte
             const int4 h = wc.qh;
             qlo.x |= ((h.x >> jlo) & 0x01010101) << 4;
             qlo.y |= ((h.y >> jlo) & 0x01010101) << 4;
