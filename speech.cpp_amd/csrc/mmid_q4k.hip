@@ -39,20 +39,6 @@ __device__ __forceinline__ int mq_pk_mul(int codes, uint32_t s2) {
     return r;
 }
 
-// ggml-quants.c get_scale_min_k4 on the 12 packed scale bytes s0..s2, for sub-block j (0..7).
-__device__ __forceinline__ uint32_t mq_scale(uint32_t s0, uint32_t s2, int j) {
-    const int o = 8 * (j & 3);
-    const uint32_t lo = __builtin_amdgcn_ubfe(s0, o, 6);
-    const uint32_t up = __builtin_amdgcn_ubfe(s2, o, 4) | (__builtin_amdgcn_ubfe(s0, o + 6, 2) << 4);
-    return j < 4 ? lo : up;
-}
-__device__ __forceinline__ uint32_t mq_min(uint32_t s1, uint32_t s2, int j) {
-    const int o = 8 * (j & 3);
-    const uint32_t lo = __builtin_amdgcn_ubfe(s1, o, 6);
-    const uint32_t up = __builtin_amdgcn_ubfe(s2, o + 4, 4) | (__builtin_amdgcn_ubfe(s1, o + 6, 2) << 4);
-    return j < 4 ? lo : up;
-}
-
 constexpr int MQ_W = 8;              // waves per workgroup
 constexpr int MQ_COLS = 16 * MQ_W;   // dst columns per column block: 16 per wave
 static_assert(MMID_CHUNK == 32 && MMID_CHUNK_SMALL == 16, "a chunk is one or two 16-row MFMA tiles");
@@ -233,17 +219,21 @@ __device__ __forceinline__ void mq_step(const MqLane &c, MqCursor &k, int ncb, i
 
     const int grp = c.grp, hi = grp >> 1;
     const v4i mask = {0x0F0F0F0F, 0x0F0F0F0F, 0x0F0F0F0F, 0x0F0F0F0F};
+    // The 6-bit scales and mins of four sub-blocks at a time from the packed words (get_scale_min_k4 for j < 4 and
+    // for j >= 4): sub-blocks 0..3 in the bytes of the *_lo4 words, 4..7 in those of the *_hi4 words.
+    const uint32_t sc_lo4 = sv.x & 0x3F3F3F3Fu, sc_hi4 = (sv.z & 0x0F0F0F0Fu) | ((sv.x >> 2) & 0x30303030u);
+    const uint32_t mn4 = (grp & 1) ? (((sv.z >> 4) & 0x0F0F0F0Fu) | ((sv.y >> 2) & 0x30303030u)) : (sv.y & 0x3F3F3F3Fu);
     // mins of sub-blocks (4 grp + i) mod 8, matching the [64 h | l] halves this lane group carries
     v4h b16;
 #pragma unroll
-    for (int i = 0; i < 4; i++) b16[i] = (_Float16)(float)mq_min(sv.y, sv.z, 4 * (grp & 1) + i);
+    for (int i = 0; i < 4; i++) b16[i] = (_Float16)(float)__builtin_amdgcn_ubfe(mn4, 8 * i, 8);
     const float d = h2f((uint16_t)(sv.w & 0xFFFF)), dmin = h2f((uint16_t)(sv.w >> 16));
     v4i ih[NG], il[NG];
 #pragma unroll
     for (int g = 0; g < NG; g++) ih[g] = il[g] = (v4i){0, 0, 0, 0};
 #pragma unroll
     for (int q = 0; q < 4; q++) {  // codes scaled by the hi / lo halves of their sub-block's scale
-        const uint32_t sc = mq_scale(sv.x, sv.z, 2 * q + hi);
+        const uint32_t sc = __builtin_amdgcn_ubfe(q < 2 ? sc_lo4 : sc_hi4, 8 * (hi + 2 * (q & 1)), 8);  // j = 2 q + hi
         const uint32_t h = (sc >> 3) * 0x10001u, l = (sc & 7) * 0x10001u;
         const v4i cq = (w[q] >> (4 * hi)) & mask;
         const v4i bh = {mq_pk_mul(cq.x, h), mq_pk_mul(cq.y, h), mq_pk_mul(cq.z, h), mq_pk_mul(cq.w, h)};
