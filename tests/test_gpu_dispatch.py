@@ -112,8 +112,8 @@ def test_dq_gemm_tiny_rows(mx, be):
 
 
 # --------------------------------------------------------------------------------------- mat-vec lanes per row
-@pytest.mark.parametrize("t,K", [(O.TYPE_Q8_0, 1024), (O.TYPE_Q8_0, 3072), (O.TYPE_Q4_K, 2048), (O.TYPE_Q6_K, 3072),
-                                 (O.TYPE_Q5_K, 1536)], ids=lambda v: str(v))
+@pytest.mark.parametrize("t,K", [(O.TYPE_Q8_0, 1024), (O.TYPE_Q8_0, 3072), (O.TYPE_Q4_K, 2048), (O.TYPE_Q4_K, 2816),
+                                 (O.TYPE_Q4_K, 6144), (O.TYPE_Q6_K, 3072), (O.TYPE_Q5_K, 1536)], ids=lambda v: str(v))
 def test_matvec_every_lanes_per_row(mx, be, t, K):
     N = 333
     for M in (1, 3):
