@@ -155,6 +155,21 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int K = (int)a.K;
     const int tid = threadIdx.x;
+    // The argument block's fields on the way to the first weight load, requested together into scalar registers:
+    // left to the compiler, the branches below would each wait on a scalar load of their own, several round trips in
+    // a row before the weights could be requested.
+    const MatvecProblem p = pick_problem(a, (int)blockIdx.y);
+    {
+        const int nbatch = a.nbatch, rounding = a.rounding;
+        const int32_t *ids = a.ids;
+        const float *xa = a.x;
+        const int64_t xcs = a.x_col_stride;
+        asm volatile("" ::"s"(nbatch), "s"(rounding), "s"(ids), "s"(xa), "s"(xcs), "s"(a.K), "s"(a.x_b2), "s"(a.x_b3),
+                     "s"(p.w.p0), "s"(p.w.p1), "s"(p.N), "s"(p.row0));
+        if constexpr (TYPE != MX_TYPE_Q8_0) asm volatile("" ::"s"(p.w.p2));
+        if constexpr (TYPE == MX_TYPE_Q5_K || TYPE == MX_TYPE_Q6_K) asm volatile("" ::"s"(p.w.p3));
+        if constexpr (FUSED) asm volatile("" ::"s"(a.glu_b), "s"(a.norm_w), "s"(p.res));
+    }
     // Batch slice; a single slice (decode) takes no division.
     int i12 = 0, i13 = 0, mat = 0;
     if (a.nbatch > 1) {
@@ -196,7 +211,6 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecArgs a) {
         for (int i = 0; i < XP; i++) wr[i] = load_x4(a.norm_w, 1024 * i + 4 * tid, K);
     }
 
-    const MatvecProblem p = pick_problem(a, (int)blockIdx.y);
     constexpr int G = 64 / LPR;  // rows in flight per wave
     const int lane = tid & 63, wave = tid >> 6;
     const int sub = lane % LPR, grp = lane / LPR;
