@@ -6,13 +6,9 @@
 
 namespace mx {
 
-// One workgroup per output row, four consecutive elements per thread and step.
+// Output row (i10, i11, i12): one workgroup, four consecutive elements per thread and step.
 template <int TYPE>
-__global__ __launch_bounds__(256) void k_get_rows(GetRowsArgs a) {
-    const int64_t i = blockIdx.x;  // flat (i10, i11, i12)
-    const int64_t i10 = i % a.n_ids0;
-    const int64_t i11 = (i / a.n_ids0) % a.n_ids1;
-    const int64_t i12 = i / (a.n_ids0 * a.n_ids1);
+__device__ __forceinline__ void get_row(const GetRowsArgs &a, const int64_t i10, const int64_t i11, const int64_t i12) {
     const int32_t r = *(const int32_t *)((const uint8_t *)a.ids + i10 * a.ids_nb0 + i11 * a.ids_nb1 + i12 * a.ids_nb2);
     float *y = (float *)((uint8_t *)a.dst + i10 * a.dst_nb1 + i11 * a.dst_nb2 + i12 * a.dst_nb3);
     if (r < 0 || r >= a.R) {
@@ -86,10 +82,25 @@ __global__ __launch_bounds__(256) void k_get_rows(GetRowsArgs a) {
     }
 }
 
+// Workgroups stride over the output rows (one row at a time), four consecutive elements per thread and step. Row
+// indices are 32-bit: the number of rows is below 2^31 (checked by the caller).
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_get_rows(GetRowsArgs a) {
+    // The fields on the way to the row index and the first row load, requested together into scalar registers (left to
+    // the compiler, they came in over several round trips in a row).
+    asm volatile("" ::"s"(a.n_ids0), "s"(a.n_ids1), "s"(a.n_ids2), "s"(a.ids), "s"(a.ids_nb0), "s"(a.ids_nb1),
+                 "s"(a.ids_nb2), "s"(a.R), "s"(a.K), "s"(a.src_mat_rows1), "s"(a.src_mat_rows2), "s"(a.w.p0),
+                 "s"(a.w.p1));
+    asm volatile("" ::"s"(a.dst), "s"(a.dst_nb1), "s"(a.dst_nb2), "s"(a.dst_nb3));
+    const uint32_t n0 = (uint32_t)a.n_ids0, n1 = (uint32_t)a.n_ids1;
+    const uint32_t nrows = n0 * n1 * (uint32_t)a.n_ids2;
+    for (uint32_t i = blockIdx.x; i < nrows; i += gridDim.x) get_row<TYPE>(a, i % n0, (i / n0) % n1, i / (n0 * n1));
+}
+
 hipError_t launch_get_rows(const GetRowsArgs &a, hipStream_t s) {
     const int64_t n = a.n_ids0 * a.n_ids1 * a.n_ids2;
     if (n == 0) return hipSuccess;
-    dim3 grid((unsigned)n);
+    dim3 grid((unsigned)std::min<int64_t>(n, 65536));
     switch (a.type) {
         case MX_TYPE_Q8_0: hipLaunchKernelGGL(k_get_rows<MX_TYPE_Q8_0>, grid, dim3(256), 0, s, a); break;
         case MX_TYPE_Q4_K: hipLaunchKernelGGL(k_get_rows<MX_TYPE_Q4_K>, grid, dim3(256), 0, s, a); break;

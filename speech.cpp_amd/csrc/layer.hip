@@ -418,6 +418,15 @@ __global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a, QkvPostArgs pa) {
     __shared__ __align__(16) float qs[G][D];
     __shared__ float ps[G][64], mvs[64], hm[G], hs[G], hr[G];
     __shared__ __align__(16) float accs[PP * G * D];
+    // The fields on the way to the first loads, requested together into scalar registers (left to the compiler, they
+    // came in over several round trips in a row).
+    asm volatile("" ::"s"(a.k), "s"(a.v), "s"(a.k_nb2), "s"(a.v_nb2), "s"(a.mask), "s"(a.m_nb1), "s"(a.split_len),
+                 "s"(a.n_kv), "s"(a.k_nb1), "s"(a.v_nb1));
+    if constexpr (POST)
+        asm volatile("" ::"s"(pa.pos), "s"(pa.cache_rows), "s"(pa.q), "s"(pa.q_nb1), "s"(pa.qw), "s"(pa.k), "s"(pa.v),
+                     "s"(pa.k_nb1), "s"(pa.v_nb1), "s"(pa.kw), "s"(a.nsplit));
+    else
+        asm volatile("" ::"s"(a.q), "s"(a.q_nb1), "s"(a.q_nb2));
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t split = blockIdx.x, hk = blockIdx.y, i = blockIdx.z;
     const uint8_t *kb = (const uint8_t *)a.k + hk * a.k_nb2;

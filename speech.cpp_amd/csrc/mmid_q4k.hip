@@ -349,6 +349,12 @@ __global__ __launch_bounds__(64 * MQ_W) void k_mmid_q4k(MulMatIdArgs a) {
     using Map = MqMap<NGMAX, S>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // The argument block's fields on the way to the first weight copy, requested together into scalar registers (left
+    // to the compiler, they came in over several round trips in a row, between the tile count's and the tiles' loads).
+    asm volatile("" ::"s"(a.N), "s"(a.K), "s"(a.nprob), "s"(a.ntiles), "s"(a.tiles), "s"(a.pairs), "s"(a.n_ids),
+                 "s"(a.b_ne1), "s"(a.xq), "s"(a.x16), "s"(a.xd));
+    asm volatile("" ::"s"(a.wg[0].p0), "s"(a.wg[0].p1), "s"(a.wg[0].p2), "s"(a.dstg[0]), "s"(a.dst_nb1),
+                 "s"(a.dst_nb2));
     const int N = (int)a.N;
     const int nblk = (N + MQ_COLS - 1) / MQ_COLS;
     const int64_t per = (int64_t)a.ntiles[0] * nblk;  // units of one product

@@ -599,6 +599,7 @@ MX_API int mx_supports_op(int op, const mx_tensor *src0, const mx_tensor *src1, 
             const mx_tensor *ids = src1;
             if (!ids || ids->type != MX_TYPE_I32 || !shape_ok(ids) || ids->ne[3] != 1) return 0;
             if (src0->ne[2] != ids->ne[1] || src0->ne[3] != ids->ne[2]) return 0;
+            if (ids->ne[0] * ids->ne[1] * ids->ne[2] >= ((int64_t)1 << 31)) return 0;  // rows are indexed with 32 bits
             if (dst->ne[0] != K || dst->ne[1] != ids->ne[0] || dst->ne[2] != ids->ne[1] || dst->ne[3] != ids->ne[2]) return 0;
             return aligned16(dst->data) && dst->nb[1] % 16 == 0 && dst->nb[2] % 16 == 0 && dst->nb[3] % 16 == 0;
         }
