@@ -154,3 +154,13 @@ def test_supports_op_weight_types(mx):
     assert not ok(mx.OP_MUL_MAT, W, X, None, Y)
     W = desc_contig(mx, mx.F32, (1004, 8, 1, 1), data=0x10008)   # data not 16-byte aligned
     assert not ok(mx.OP_MUL_MAT, W, X, None, Y)
+
+
+def test_supports_op_get_rows_row_bound(mx):
+    """GET_ROWS indexes its output rows with 32 bits: 2^31 - 1 rows are accepted, 2^31 declined (host logic only)."""
+    L = mx.lib()
+    W = desc_contig(mx, mx.Q8_0, (64, 10, 1, 1))
+    for n, want in [((1 << 31) - 1, 1), (1 << 31, 0)]:
+        I = desc_contig(mx, mx.I32, (n, 1, 1, 1))
+        G = desc_contig(mx, mx.F32, (64, n, 1, 1))
+        assert L.mx_supports_op(mx.OP_GET_ROWS, W, I, None, G) == want
