@@ -80,11 +80,19 @@ __device__ void mmid_bucket(const MulMatIdArgs &a) {
     const int tid = threadIdx.x;
     const int E = (int)a.E;
     const int npairs = (int)(a.n_ids * a.T), chunk = a.chunk;
+    // a thread's first HELD pairs' experts stay in registers for the second pass (no second round trip for them)
+    constexpr int HELD = 8;
+    int held[HELD];
+    auto expert_of = [&](int p) {
+        const int t = p / (int)a.n_ids, s = p - t * (int)a.n_ids;
+        return *(const int32_t *)((const uint8_t *)a.ids + s * a.ids_nb0 + t * a.ids_nb1);
+    };
+#pragma unroll
+    for (int k = 0; k < HELD; k++) held[k] = tid + 256 * k < npairs ? expert_of(tid + 256 * k) : -1;
     for (int e = tid; e < E; e += 256) cnt[e] = 0;
     __syncthreads();
-    for (int p = tid; p < npairs; p += 256) {
-        const int t = p / (int)a.n_ids, s = p - t * (int)a.n_ids;
-        const int32_t e = *(const int32_t *)((const uint8_t *)a.ids + s * a.ids_nb0 + t * a.ids_nb1);
+    for (int p = tid, k = 0; p < npairs; p += 256, k++) {
+        const int32_t e = k < HELD ? held[k] : expert_of(p);
         if (e < 0 || e >= E) atomicOr(a.err, 2);  // ggml-cpu asserts; this pair is dropped and reported
         else atomicAdd(&cnt[e], 1);
     }
@@ -116,9 +124,8 @@ __device__ void mmid_bucket(const MulMatIdArgs &a) {
         a.ntiles[0] = total.y;
     }
     __syncthreads();
-    for (int p = tid; p < npairs; p += 256) {
-        const int t = p / (int)a.n_ids, s = p - t * (int)a.n_ids;
-        const int32_t e = *(const int32_t *)((const uint8_t *)a.ids + s * a.ids_nb0 + t * a.ids_nb1);
+    for (int p = tid, k = 0; p < npairs; p += 256, k++) {
+        const int32_t e = k < HELD ? held[k] : expert_of(p);
         if (e < 0 || e >= E) continue;
         a.pairs[atomicAdd(&cnt[e], 1)] = p;
     }
@@ -180,6 +187,9 @@ __device__ void mmid_quant_row(const MulMatIdArgs &a, int64_t r) {
 // One launch for both: workgroup 0 buckets the pairs, workgroup 1 + r quantizes activation row r.
 template <int TYPE>
 __global__ __launch_bounds__(256) void k_mmid_prep(MulMatIdArgs a) {
+    // the fields both roles start from, requested together into scalar registers
+    asm volatile("" ::"s"(a.n_ids), "s"(a.T), "s"(a.E), "s"(a.ids), "s"(a.ids_nb0), "s"(a.ids_nb1), "s"(a.chunk),
+                 "s"(a.b), "s"(a.b_ne1), "s"(a.b_nb1), "s"(a.b_nb2), "s"(a.K));
     if (blockIdx.x == 0) mmid_bucket(a);
     else mmid_quant_row<TYPE>(a, (int64_t)blockIdx.x - 1);
 }
