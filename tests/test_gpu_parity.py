@@ -157,6 +157,32 @@ def test_get_rows_index_out_of_range(mx, be):
     be.sync()  # the error word was cleared
 
 
+def test_get_rows_more_rows_than_workgroups(mx, be):
+    """140,000 output rows on a grid of at most 65,536 workgroups: each workgroup takes rows i, i + 65,536, ...; an
+    out-of-range id met on a workgroup's second row is zeroed and reported like one on its first."""
+    K, R, n = 64, 300, 140_000
+    table = weights(O.TYPE_Q8_0, R, K, 0x5EED0400)
+    ids = np.random.default_rng(11).integers(0, R, n).astype(np.int32)
+    T = be.tensor(mx.Q8_0, (K, R), table)
+    I = be.tensor(mx.I32, (n,), ids)
+    D = be.tensor(mx.F32, (K, n))
+    be.get_rows(T, I, D)
+    be.sync()
+    assert bits_equal(D.numpy().reshape(n, K), O.get_rows(O.TYPE_Q8_0, table, K, ids))
+    bad = ids.copy()
+    bad[70_000] = R
+    I2 = be.tensor(mx.I32, (n,), bad)
+    be.get_rows(T, I2, D)
+    with pytest.raises(mx.MxError) as e:
+        be.sync()
+    assert e.value.code == mx.INVALID
+    got = D.numpy().reshape(n, K)
+    assert np.all(got[70_000] == 0)
+    keep = np.arange(n) != 70_000
+    assert bits_equal(got[keep], O.get_rows(O.TYPE_Q8_0, table, K, ids[keep]))
+    be.sync()
+
+
 # ------------------------------------------------------------------------------------------------------ MUL_MAT
 def run_mul_mat(mx, be, t, w, x, K, N):
     M = x.shape[0]
