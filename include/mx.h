@@ -172,7 +172,7 @@ MX_API int mx_tensor_copy(mx_backend *be, const mx_tensor *src, const mx_tensor 
  *   MUL_MAT:     src/common/qwen3-decoder.cpp:362-364,403,406-407,410,426; src/common/graph.h:15-19
  *   MUL_MAT_ID:  src/common/graph.h:21-26 from src/families/drama3/text-model.cpp:198-221
  * Shapes follow ggml exactly:
- *   mx_get_rows(src0 [K, R, A, B] quantized, ids [n, A, B] I32) -> dst [K, n, A, B] F32
+ *   mx_get_rows(src0 [K, R, A, B] quantized, ids [n, A, B] I32) -> dst [K, n, A, B] F32 (n A B < 2^31 rows)
  *   mx_mul_mat(src0 [K, N, A, B] quantized, src1 [K, M, A*r2, B*r3] F32) -> dst [N, M, A*r2, B*r3] F32
  *   mx_mul_mat_id(as [K, N, E] quantized, b [K, 1 or k, T] F32, ids [k, T] I32) -> dst [N, k, T] F32
  * All products accumulate each block's integer sum exactly and sum across blocks in fp32, whatever the tensor's
