@@ -343,6 +343,14 @@ def test_mul_mat_id_chunk_edges(mx, be, t, chunk):
 
 
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
+def test_mul_mat_id_past_held_pairs(mx, be, t):
+    """2,400 (token, slot) pairs: the bucketing pass keeps a thread's first eight pairs' experts in registers (2,048
+    pairs over its 256 threads) and reads the rest again for its second pass."""
+    y, y_ref = mmid_case(mx, be, t, E=8, K=256, N=40, n_ids=4, T=600, bcast=True, seed=0x5EED0F00 + t)
+    assert rel_err(y, y_ref) <= TIGHT
+
+
+@pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
 def test_mul_mat_id_long_rows(mx, be, t):
     """K = 4096, past what the grouped Q4_K product keeps in LDS: the experts kernel by default, in one pass (20
     tokens over 16 experts) and in several passes of eight pairs (40 tokens over 4 experts, ~20 pairs each)."""
