@@ -540,6 +540,18 @@ def test_mul_mat_gemm_special_rows(mx, be, t):
     check_product(t, w, x, y, K)
 
 
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q5_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("K", [2048, 8192, 10240, 20480])
+def test_mul_mat_gemm_activation_pass_widths(mx, be, t, K):
+    """Rows of 2048 to 20480 elements through the activation pass before the fp16 GEMM: up to 16384 a row stays in
+    registers while its largest |d q| is found, past that it is quantized twice; special and ordinary rows."""
+    N = 64
+    w = weights(t, N, K, 0x5EED1000 + t + K)
+    x = np.concatenate([special_rows(K), acts(0xAC701000 + K, 7, K)])
+    y = run_mul_mat(mx, be, t, w, x, K, N)
+    check_product(t, w, x, y, K)
+
+
 @pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
 def test_mul_mat_gemm_kquant_batched(mx, be, t):
     """Broadcast batches: ne12 = 2 * ne02, each weight matrix serves two activation slices."""
