@@ -230,6 +230,26 @@ def test_mul_mat_config1(mx, be):
     assert l2_rel(y, y_ref) <= TIGHT
 
 
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("M", [1, 3])
+def test_mul_mat_many_row_blocks(mx, be, t, M):
+    """40,001 rows (2,501 blocks of 16, the last ragged), plain and with the fused residual ADD (bit for bit the
+    separate ADD)."""
+    K, N = 256, 40_001
+    w = weights(t, N, K, 0x5EED1100 + t + M)
+    x = acts(0xAC701100 + M, M, K)
+    y = run_mul_mat(mx, be, t, w, x, K, N)
+    assert rel_err(y, O.mul_mat(t, w, x)) <= TIGHT
+    r = acts(0xAC701180 + M, M, N)
+    W = be.tensor(t, (K, N), w)
+    X = be.tensor(mx.F32, (K, M), x)
+    R = be.tensor(mx.F32, (N, M), r)
+    be.mul_mat_fused([W], X, [R], residual=[R])
+    be.sync()
+    got = R.numpy().reshape(M, N)
+    assert bits_equal(got, (r.reshape(M, N) + y.reshape(M, N)).astype(np.float32))
+
+
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
 def test_mul_mat_x86_rounding(mx, be, t):
     K, N, M = 512, 64, 3
