@@ -12,11 +12,15 @@ model files and dumps that are not in its tree, so the oracle is pinned by:
   * for the K-quant weight quantizers on generic data: every code is the nearest point of its sub-block's grid given
     the packed scales; the packed 6-bit (Q4_K / Q5_K) and int8 (Q6_K) scales and d / dmin are the roundings of the
     sub-block fits; make_qx_quants's fit is the best of its candidate family (evaluated in float64); make_qkx2_quants
-    agrees bit for bit with an independent numpy statement and never loses to its min-max start -- each with a
-    mutation (another rmin, fewer steps, other weights, a narrower family) shown to fail.
-Parity unpinned: make_qkx2_quants's path-dependent search on generic data is fixed only by two restatements of ggml's
-published algorithm (oracle and numpy); a misreading shared by both would pass. The kernels read whatever bytes the
-quantizer wrote, so their parity does not depend on it.
+    agrees bit for bit with an independent numpy statement, never loses to its min-max start, returns the weighted
+    least-squares fit of its own codes (or the start, forced on exact-grid sub-blocks), and returns codes that are the
+    rounding onto the start's or a family member's grid with the min in effect (every search path followed in
+    float64) -- each with a mutation (another rmin, fewer steps, other weights, an unweighted fit, no min clamp,
+    truncated codes, a min that never moves, a max that moves, a narrower family) shown to fail.
+Parity unpinned (narrowly): where float32 and float64 differ by less than the float32 rounding -- a value within 2e-4
+of a rounding boundary, two candidate errors within 1e-5 -- the float64 checks follow both outcomes, so which way
+ggml's float32 loop goes there is fixed only by the two restatements (oracle and numpy). The kernels read whatever
+bytes the quantizer wrote, so their parity does not depend on it.
 """
 import json
 import pathlib
@@ -449,34 +453,43 @@ def kquant_weights(x):
     return (av + np.abs(x)).astype(np.float32)
 
 
-def qkx2_numpy(x, w, nmax, rmin, rdelta, nstep):
+def qkx2_numpy(x, w, nmax, rmin, rdelta, nstep, mutate=None):
     """make_qkx2_quants (use_mad = 0) restated in numpy from ggml's description, each candidate's codes vectorized and
     its sums taken in order in float32 (np.cumsum), as the C loop takes them: start from the min-max fit (min clamped
     to <= 0), then for is = 0..nstep round x - min with iscale = (nmax + rmin + rdelta is) / (max - min), fit the
     weighted least-squares (scale, min) of those codes (min > 0: min = 0 and the scale alone), and keep the fit whose
-    weighted squared error is smaller -- min and the span max - min follow the fit kept. Returns (scale, min, codes)."""
+    weighted squared error is smaller -- min and the span max - min follow the fit kept. Returns (scale, min, codes).
+    `mutate` plants one mistake, for the tests that must reject it: "fit_unweighted" (the fit ignores the weights),
+    "no_clamp" (a positive min is kept), "floor" (codes truncated instead of rounded), "min_fixed" (later candidates
+    keep the start's min), "max_moves" (the span's top follows the kept fit too)."""
     f32 = np.float32
     seq = lambda v: np.cumsum(v, dtype=f32)[-1]
     lo, hi = min(f32(x.min()), f32(0)), f32(x.max())
-    sum_w, sum_x = seq(w), seq(w * x)
     if hi == lo:
         return f32(0), lo, np.zeros(x.size, np.uint8)
     iscale = f32(nmax) / (hi - lo)
     scale = f32(1) / iscale
     L = np.clip(np.rint(iscale * (x - lo)), 0, nmax).astype(np.uint8)
     best = seq(w * (scale * L.astype(f32) + lo - x) ** 2)
+    lo0 = lo
+    rnd = np.floor if mutate == "floor" else np.rint
     for i in range(nstep + 1):
-        isc = (f32(rmin) + f32(rdelta) * f32(i) + f32(nmax)) / (hi - lo)
-        l = np.clip(np.rint(isc * (x - lo)), 0, nmax).astype(f32)
-        sl, sl2, sxl = seq(w * l), seq(w * l * l), seq(w * l * x)
-        D = sum_w * sl2 - sl * sl
+        base = lo0 if mutate == "min_fixed" else lo
+        isc = (f32(rmin) + f32(rdelta) * f32(i) + f32(nmax)) / (hi - base)
+        l = np.clip(rnd(isc * (x - base)), 0, nmax).astype(f32)
+        wf = np.ones_like(w) if mutate == "fit_unweighted" else w
+        sw, sx = seq(wf), seq(wf * x)
+        sl, sl2, sxl = seq(wf * l), seq(wf * l * l), seq(wf * l * x)
+        D = sw * sl2 - sl * sl
         if D > 0:
-            sc, mn = (sum_w * sxl - sum_x * sl) / D, (sl2 * sum_x - sl * sxl) / D
-            if mn > 0:
+            sc, mn = (sw * sxl - sx * sl) / D, (sl2 * sx - sl * sxl) / D
+            if mn > 0 and mutate != "no_clamp":
                 mn, sc = f32(0), sxl / sl2
             err = seq(w * (sc * l + mn - x) ** 2)
             if err < best:
                 L, best, scale, lo = l.astype(np.uint8), err, sc, mn
+                if mutate == "max_moves":
+                    hi = f32(sc * f32(nmax) + mn)
     return scale, lo, L
 
 
@@ -517,6 +530,149 @@ def test_make_qkx2_quants_matches_a_numpy_restatement(t):
                   lambda x, w: O.make_qkx2_quants(x, w, nmax, rmin, rdelta, nstep - 5),
                   lambda x, w: O.make_qkx2_quants(x, np.ones_like(w), nmax, rmin, rdelta, nstep)):
         assert len(qkx2_differs(t, xs, wrong)) >= 30
+
+
+def lsq_fit64(x, w, L):
+    """The weighted least-squares (scale, min) of x ~ scale * L + min, in float64 from the normal equations; a positive
+    min is set to 0 and the scale fitted alone (make_qkx2_quants' rule: a K-quant min is stored as -min >= 0). None when
+    the codes cannot fix two parameters (all equal)."""
+    xd, wd, ld = x.astype(np.float64), w.astype(np.float64), L.astype(np.float64)
+    sw, sl, sl2 = wd.sum(), (wd * ld).sum(), (wd * ld * ld).sum()
+    sx, sxl = (wd * xd).sum(), (wd * ld * xd).sum()
+    D = sw * sl2 - sl * sl
+    if D <= 1e-12 * sw * sl2:
+        return None
+    s, m = (sw * sxl - sx * sl) / D, (sl2 * sx - sl * sxl) / D
+    if m > 0:
+        m, s = 0.0, sxl / sl2
+    return s, m
+
+
+def grid_roundings(v, nmax, tol):
+    """Codes clip(rint(v), 0, nmax), and the variants with values lying within tol of a rounding boundary rounded the
+    other way (float32 arithmetic may land on either side where float64 is this close)."""
+    import itertools
+    base = np.clip(np.rint(v), 0, nmax)
+    near = np.nonzero(np.abs(v - np.floor(v) - 0.5) < tol)[0]
+    out = [base]
+    for r in range(1, len(near) + 1):
+        for sub in itertools.combinations(near, r):
+            L = base.copy()
+            for i in sub:
+                L[i] = np.clip(np.ceil(v[i]) if base[i] == np.floor(v[i]) else np.floor(v[i]), 0, nmax)
+            out.append(L)
+    return out
+
+
+def qkx2_paths(x, w, nmax, rmin, rdelta, nstep, tol_v=2e-4, tol_e=1e-5):
+    """Every (kind, codes) make_qkx2_quants can end with on this sub-block, from its definition evaluated in float64:
+    kind "start" (the min-max fit, no candidate better) or "fit" (the codes of the last candidate kept). Candidate is
+    rounds x - min onto iscale = (nmax + rmin + rdelta is) / (max - min) with the min of the fit kept last (the start's
+    min, min(x) clamped to <= 0, before any), and is kept when the weighted squared error of its least-squares fit is
+    below the best so far. Where float64 cannot decide how float32 arithmetic goes -- a value within tol_v of a rounding
+    boundary, two errors within tol_e of each other -- both outcomes are followed."""
+    xd, wd = x.astype(np.float64), w.astype(np.float64)
+    lo, hi = min(xd.min(), 0.0), xd.max()
+    if hi == lo:
+        return [("flat", np.zeros(x.size))]
+    states = []
+    for L in grid_roundings(nmax / (hi - lo) * (xd - lo), nmax, tol_v):
+        states.append((lo, float(np.sum(wd * ((hi - lo) / nmax * L + lo - xd) ** 2)), ("start", L)))
+    for i in range(nstep + 1):
+        new = []
+        for mp, best, src in states:
+            isc = (rmin + rdelta * i + nmax) / (hi - mp)
+            for L in grid_roundings(isc * (xd - mp), nmax, tol_v):
+                f = lsq_fit64(x, w, L)
+                if f is None:
+                    new.append((mp, best, src))
+                    continue
+                e = float(np.sum(wd * (f[0] * L + f[1] - xd) ** 2))
+                if e <= best * (1 + tol_e):
+                    new.append((f[1], e, ("fit", L)))
+                if e >= best * (1 - tol_e):
+                    new.append((mp, best, src))
+        seen, states = set(), []
+        for st in new:
+            key = (round(st[0], 12), st[2][0], st[2][1].tobytes())
+            if key not in seen:
+                seen.add(key)
+                states.append(st)
+        assert len(states) <= 512
+    return [st[2] for st in states]
+
+
+def qkx2_fit_ok(x, w, nmax, s, m, L):
+    """Property 1: the returned (scale, min) is the weighted least-squares fit of the returned codes (to float32
+    summation: 2e-5 of the scale, 2e-5 of the span for the min), or the min-max start with its own codes."""
+    lo, hi = min(float(x.min()), 0.0), float(x.max())
+    if hi == lo:
+        return float(s) == 0.0 and not L.any()
+    f32 = np.float32
+    isc0 = f32(nmax) / (f32(hi) - f32(lo))
+    L0 = np.clip(np.rint(isc0 * (x - f32(lo))), 0, nmax)
+    if np.array_equal(L, L0) and float(m) == lo and float(s) == float(f32(1) / isc0):
+        return True
+    f = lsq_fit64(x, w, L)
+    return f is not None and abs(float(s) - f[0]) <= 2e-5 * abs(f[0]) and abs(float(m) - f[1]) <= 2e-5 * (hi - lo)
+
+
+def qkx2_codes_ok(x, w, nmax, rmin, rdelta, nstep, L):
+    """Property 2: the returned codes are the clamped rounding of x - min onto the start's grid or onto one family
+    member's, iscale = (nmax + rmin + rdelta is) / (max - min), with the min in effect when that candidate ran."""
+    return any(np.array_equal(L, c) for _, c in qkx2_paths(x, w, nmax, rmin, rdelta, nstep))
+
+
+def grid_subblocks(n, nmax, seed):
+    """Sub-blocks whose values lie on a min-max grid exactly (a multiple of a power of two): the start fit is exact,
+    so no candidate can do better and make_qkx2_quants must return it."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        codes = rng.integers(0, nmax + 1, 32)
+        codes[0], codes[1] = 0, nmax
+        out.append((codes * 2.0 ** -int(rng.integers(4, 9))).astype(np.float32))
+    return out
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K], ids=["q4_K", "q5_K"])
+def test_make_qkx2_quants_fit_and_codes_properties(t):
+    """What the mathematics fixes of make_qkx2_quants, checked in float64 apart from the oracle's float32 loop:
+    (1) its (scale, min) is the weighted least-squares fit of its codes (a positive min clamped to 0 and the scale
+    refitted), or the min-max start when no candidate was better (exact-grid sub-blocks force that case);
+    (2) its codes are the start's rounding or one family member's, taken with the min of the fit kept before it.
+    Each property has mutations of the search that it rejects (planted in the numpy restatement, on the CPU). What
+    stays open without ggml: which way float32 breaks the near-ties that (2) follows both ways."""
+    nmax, rmin, rdelta, nstep = QKX2[t]
+    xs = list(subblocks(300, 32, 0x0C11 + t))
+    grid = grid_subblocks(20, nmax, 0x0C51 + t)
+    for x in xs + grid:
+        w = kquant_weights(x)
+        s, m, L = O.make_qkx2_quants(x, w, nmax, rmin, rdelta, nstep)
+        assert qkx2_fit_ok(x, w, nmax, s, m, L)
+        assert qkx2_codes_ok(x, w, nmax, rmin, rdelta, nstep, L)
+    for x in grid:
+        w = kquant_weights(x)
+        s, m, L = O.make_qkx2_quants(x, w, nmax, rmin, rdelta, nstep)
+        f32 = np.float32
+        isc0 = f32(nmax) / (f32(x.max()) - min(f32(x.min()), f32(0)))
+        assert float(s) == float(f32(1) / isc0) and float(m) == min(float(x.min()), 0.0)
+        assert np.array_equal(L, np.clip(np.rint(isc0 * (x - min(f32(x.min()), f32(0)))), 0, nmax))
+    # teeth: each planted mistake is rejected by the property it breaks, on many sub-blocks
+    def rejected(mutate, check):
+        n = 0
+        for x in xs:
+            w = kquant_weights(x)
+            s, m, L = qkx2_numpy(x, w, nmax, rmin, rdelta, nstep, mutate=mutate)
+            n += not (qkx2_fit_ok(x, w, nmax, s, m, L) if check == 1 else
+                      qkx2_codes_ok(x, w, nmax, rmin, rdelta, nstep, L))
+        return n
+    assert rejected(None, 1) == 0 and rejected(None, 2) == 0
+    assert rejected("fit_unweighted", 1) >= 100
+    assert rejected("no_clamp", 1) >= 15
+    assert rejected("floor", 2) >= 100
+    assert rejected("min_fixed", 2) >= 10
+    assert rejected("max_moves", 2) >= 10
 
 
 def qx_objective(x, l):
