@@ -162,7 +162,8 @@ MX_API int mx_tensor_set(mx_backend *be, const mx_tensor *t, const void *host, s
 MX_API int mx_tensor_get(mx_backend *be, const mx_tensor *t, void *host, size_t offset, size_t size);
 /* Sets ggml-layout bytes [offset, offset + size) of the tensor to `value`. */
 MX_API int mx_tensor_memset(mx_backend *be, const mx_tensor *t, uint8_t value, size_t offset, size_t size);
-/* Copies a whole tensor between two tensors of the same type and shape held by this device. */
+/* Copies a whole tensor between two tensors of the same type and shape held by this device; the copy has landed
+ * when the call returns (ggml's cpy_tensor contract), so work on any stream may read dst next. */
 MX_API int mx_tensor_copy(mx_backend *be, const mx_tensor *src, const mx_tensor *dst);
 
 /* ---------------------------------------------------------------------------------------------------------------
@@ -196,9 +197,10 @@ MX_API int mx_mul_mat_id_group(mx_backend *be, int n, const mx_tensor *const *as
  * The same products as mx_mul_mat_id, on the same kernels and with the same results, but its scratch (the bucketing
  * tables, the quantized activation rows, the chunk list) lives in a static device array of MX_NOALLOC_SCRATCH_BYTES
  * that each GPU holds from the first mx_backend_init on it until the process ends; the call itself calls no
- * allocator. A call needing more scratch (mx_mul_mat_id_noalloc_bytes) fails with MX_UNSUPPORTED. Every call on one
- * GPU shares that GPU's array, which keeps the last call's contents (each call writes everything it reads before
- * reading it): calls that overlap on one GPU -- two streams, two backends -- race. */
+ * allocator. A call needing more scratch (mx_mul_mat_id_noalloc_bytes; SIZE_MAX for inputs MUL_MAT_ID does not
+ * take) fails with MX_UNSUPPORTED. Every call on one GPU shares that GPU's array, which keeps the last call's contents
+ * (each call writes everything it reads before reading it): calls that overlap on one GPU -- two streams, two
+ * backends -- race. */
 #define MX_NOALLOC_SCRATCH_BYTES (16u << 20)
 MX_API size_t mx_mul_mat_id_noalloc_bytes(const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids);
 MX_API int mx_mul_mat_id_noalloc(mx_backend *be, const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids,

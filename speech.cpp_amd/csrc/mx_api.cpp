@@ -521,7 +521,10 @@ MX_API int mx_tensor_copy(mx_backend *be, const mx_tensor *src, const mx_tensor 
     const size_t n = mx::is_quantized(src->type) ? mx::planes_of(src->type, nelements(src)).total : nbytes(src);
     if (!mx::is_quantized(src->type) && (!contiguous(src) || !contiguous(dst)))
         return fail(MX_UNSUPPORTED, "only contiguous copies");
+    if ((rc = no_capture(be, "tensor_copy"))) return rc;
     HIP_OK(hipMemcpyAsync(dst->data, src->data, n, hipMemcpyDeviceToDevice, be->stream), "copy tensor");
+    // complete on return, as ggml's cpy_tensor is: a compute on another stream may read dst next
+    HIP_OK(hipStreamSynchronize(be->stream), "synchronize copy");
     return MX_SUCCESS;
 }
 
@@ -988,7 +991,11 @@ MX_API int mx_mul_mat_id_group(mx_backend *be, int n, const mx_tensor *const *as
 }
 
 MX_API size_t mx_mul_mat_id_noalloc_bytes(const mx_tensor *as, const mx_tensor *b, const mx_tensor *ids) {
-    if (!as || !b || !ids || !mx::is_quantized(as->type) || !shape_ok(as) || !shape_ok(ids)) return 0;
+    // inputs it cannot size read as needing more than any scratch holds, never as fitting
+    if (!as || !b || !ids || !mx::is_quantized(as->type) || !shape_ok(as) || !shape_ok(b) || !shape_ok(ids) ||
+        b->type != MX_TYPE_F32 || ids->type != MX_TYPE_I32 || b->ne[0] != as->ne[0] || ids->ne[1] != b->ne[2] ||
+        (b->ne[1] != 1 && b->ne[1] != ids->ne[0]))
+        return SIZE_MAX;
     mx::MulMatIdArgs a{};
     a.type = as->type;
     a.K = as->ne[0];

@@ -273,6 +273,7 @@ GGML_API struct ggml_tensor *ggml_swiglu_split(struct ggml_context *ctx, struct 
 
 // ----------------------------------------------------------------------------------------------- graphs
 GGML_API struct ggml_cgraph *ggml_new_graph(struct ggml_context *ctx);
+GGML_API struct ggml_cgraph *ggml_new_graph_custom(struct ggml_context *ctx, size_t size, bool grads);
 GGML_API void ggml_build_forward_expand(struct ggml_cgraph *cgraph, struct ggml_tensor *tensor);
 GGML_API int ggml_graph_n_nodes(struct ggml_cgraph *cgraph);
 GGML_API struct ggml_tensor *ggml_graph_node(struct ggml_cgraph *cgraph, int i);

@@ -121,14 +121,25 @@ struct TensorKey {
     uint64_t view_offs;
 };
 
-// One step of the last graph computed, to recognise a graph computed again with the same tensors: the node (with its
-// operation parameters: eps, RoPE's dims / mode / bases, attention's scale) and its first five sources.
+// One node of a graph, to recognise a graph computed again with the same tensors: the node (with its operation
+// parameters: eps, RoPE's dims / mode / bases, attention's scale), its first five sources, and how many nodes of the
+// whole graph read it (what decides the fusions it can take part in).
 struct NodeKey {
     int32_t op;
+    int32_t uses;
     int32_t op_params[GGML_MAX_OP_PARAMS / sizeof(int32_t)];
     TensorKey t[6];
     bool operator==(const NodeKey &o) const { return std::memcmp(this, &o, sizeof(NodeKey)) == 0; }
 };
+
+// A graph seen before and how often in a row it came again, with its recording once it has one.
+struct SeenGraph {
+    std::vector<NodeKey> keys;
+    int repeats = 0;
+    mx_graph *replay = nullptr;  // recorded from the third identical computation on
+    uint64_t last_use = 0;
+};
+constexpr size_t kSeenGraphs = 8;  // the graphs a backend keeps recordings of: the splits of a scheduled step
 
 // What a backend's graph_compute did, for tests and tuning: graphs computed eagerly / recorded / replayed, then the
 // fusions run as one launch -- norm into products, SwiGLU and residual around a product, a decode row's attention
@@ -141,9 +152,8 @@ enum Count {
 struct BackendCtx {
     DeviceCtx *dev = nullptr;
     mx_backend *be = nullptr;
-    std::vector<NodeKey> last;   // the previous graph's nodes
-    int repeats = 0;             // how many times in a row it came again
-    mx_graph *replay = nullptr;  // recorded from the third identical graph on
+    std::vector<SeenGraph> seen;  // at most kSeenGraphs, the least recently computed dropped first
+    uint64_t clock = 0;
     int64_t counts[kCounts] = {};
 };
 
@@ -287,7 +297,7 @@ const char *backend_get_name(ggml_backend_t backend) { return ((BackendCtx *)bac
 
 void backend_free(ggml_backend_t backend) {
     auto *ctx = (BackendCtx *)backend->context;
-    mx_graph_free(ctx->replay);
+    for (SeenGraph &g : ctx->seen) mx_graph_free(g.replay);
     mx_backend_free(ctx->be);
     delete ctx;
     delete backend;
@@ -376,13 +386,17 @@ int run_products(BackendCtx *ctx, const std::vector<const ggml_tensor *> &group)
 }
 
 // ------------------------------------------------------------------------------------------ fusions of a graph
-// What the plan of a graph knows about it: each node's position and, for each tensor, the nodes that read it.
+// What the plan of a graph knows about it: each node's position, for each tensor the nodes of this graph that read
+// it, and each node's use count over the whole graph ggml built. Under ggml_backend_sched the graph is one split (a
+// view of the whole graph's nodes, sharing its use counts): a node of a later split may read a tensor this one
+// computes, and only the whole graph's count shows it.
 struct GraphInfo {
+    ggml_cgraph *graph;
     std::vector<const ggml_tensor *> nodes;
     std::unordered_map<const ggml_tensor *, int> index;
     std::unordered_map<const ggml_tensor *, std::vector<int>> readers;
 
-    explicit GraphInfo(ggml_cgraph *cgraph) {
+    explicit GraphInfo(ggml_cgraph *cgraph) : graph(cgraph) {
         const int n = ggml_graph_n_nodes(cgraph);
         for (int i = 0; i < n; i++) {
             const ggml_tensor *t = ggml_graph_node(cgraph, i);
@@ -392,11 +406,17 @@ struct GraphInfo {
                 if (t->src[s]) readers[t->src[s]].push_back(i);
         }
     }
-    // the one node that reads t, if exactly one does and t is not a graph output (a fusion need not write t then)
+    // whether t is computed here and every node of the whole graph that reads it is among this graph's `n` readers
+    bool read_here_only(const ggml_tensor *t, size_t n) const {
+        const int i = pos(t);
+        return i >= 0 && ggml_node_get_use_count(graph, i) == (int)n;
+    }
+    // the one node that reads t, if exactly one node of the whole graph does and t is not a graph output (a fusion
+    // need not write t then)
     const ggml_tensor *sole_reader(const ggml_tensor *t) const {
         if (!t || (t->flags & GGML_TENSOR_FLAG_OUTPUT)) return nullptr;
         auto it = readers.find(t);
-        if (it == readers.end() || it->second.size() != 1) return nullptr;
+        if (it == readers.end() || it->second.size() != 1 || !read_here_only(t, 1)) return nullptr;
         return nodes[it->second[0]];
     }
     int pos(const ggml_tensor *t) const {
@@ -442,6 +462,7 @@ bool match_norm_products(const GraphInfo &gi, int i, Step &st) {
     if (mul->flags & GGML_TENSOR_FLAG_OUTPUT) return false;
     auto it = gi.readers.find(mul);
     if (it == gi.readers.end() || it->second.empty() || it->second.size() > 4) return false;
+    if (!gi.read_here_only(mul, it->second.size())) return false;
     std::vector<const ggml_tensor *> own{norm, mul};
     int last = gi.pos(mul);
     for (int r : it->second) {
@@ -534,9 +555,9 @@ bool overlaps(const ggml_tensor *a, const ggml_tensor *b) {
 
 // MUL_MAT_ID at i and later MUL_MAT_IDs that read the same rows and ids with experts of the same type and shape (the
 // gate and up experts of text-model.cpp:208-209; ggml's graph order puts silu(gate) between them). Run together at
-// i: a later product reads nothing computed after i (its experts are a weight, its rows and ids are i's), and its
-// output may not share memory with any tensor a node between them reads or writes (the allocator reuses freed
-// memory in graph order). Roles: {products...}.
+// i: a later product reads nothing computed after i (its experts are a weight, its rows and ids are i's, which no
+// node between them writes), and its output may not share memory with any tensor a node between them reads or
+// writes (the allocator reuses freed memory in graph order). Roles: {products...}.
 bool match_experts(const GraphInfo &gi, int i, const std::vector<bool> &taken, Step &st) {
     const ggml_tensor *a = gi.nodes[i];
     std::vector<const ggml_tensor *> own{a};
@@ -549,7 +570,9 @@ bool match_experts(const GraphInfo &gi, int i, const std::vector<bool> &taken, S
         bool clear = !overlaps(b, a->src[1]) && !overlaps(b, a->src[2]);
         for (int k = i + 1; k < j && clear; k++) {
             const ggml_tensor *n = gi.nodes[k];
-            clear = !overlaps(b, n);
+            // n writes neither b's output nor its rows and ids (an in-place op or a view over them), and reads no
+            // memory b writes
+            clear = !overlaps(b, n) && !overlaps(n, a->src[1]) && !overlaps(n, a->src[2]);
             for (int s = 0; s < GGML_MAX_SRC && clear; s++) clear = !overlaps(b, n->src[s]);
         }
         for (const ggml_tensor *o : own) clear = clear && !overlaps(b, o);
@@ -746,6 +769,7 @@ std::vector<NodeKey> keys_of(ggml_cgraph *cgraph) {
         NodeKey k;
         std::memset(&k, 0, sizeof k);
         k.op = (int32_t)t->op;
+        k.uses = ggml_node_get_use_count(cgraph, i);
         std::memcpy(k.op_params, t->op_params, sizeof k.op_params);
         key_of(t, k.t[0]);
         for (int s = 0; s < 5; s++) key_of(t->src[s], k.t[s + 1]);
@@ -755,45 +779,56 @@ std::vector<NodeKey> keys_of(ggml_cgraph *cgraph) {
 }
 
 // The same graph over the same tensors computed again (the kept decode-step graph, src/common/qwen3-decoder.cpp:
-// 187-208) is recorded once its scratch has its final size and replayed with one launch from then on. A graph that
-// differs in any node's op, parameters, or any tensor's type, shape, strides, address or view offset is computed
-// eagerly and the recording dropped (mx_graph_free waits for a replay still in flight). A recording libmx refuses
-// because the scratch grew since (MX_FAILED) is recorded again on the next identical graph.
+// 187-208; each split of a step ggml_backend_sched computes, src/families/drama3/text-model.cpp:91-97) is recorded
+// once its scratch has its final size and replayed with one launch from then on. Graphs are told apart by every
+// node's op, parameters and whole-graph use count and every tensor's type, shape, strides, address and view offset;
+// the backend keeps the last kSeenGraphs of them, each with its own count and recording (a dropped one is freed;
+// mx_graph_free waits for a replay still in flight). A recording libmx refuses because the scratch grew since
+// (MX_FAILED) is recorded again on the next identical computation.
 enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgraph) {
     auto *ctx = (BackendCtx *)backend->context;
     std::vector<NodeKey> keys = keys_of(cgraph);
-    if (keys == ctx->last) {
-        ctx->repeats++;
+    SeenGraph *g = nullptr;
+    for (SeenGraph &e : ctx->seen)
+        if (e.keys == keys) g = &e;
+    if (g) {
+        g->repeats++;
     } else {
-        ctx->last = std::move(keys);
-        ctx->repeats = 0;
-        mx_graph_free(ctx->replay);
-        ctx->replay = nullptr;
+        if (ctx->seen.size() >= kSeenGraphs) {
+            auto oldest = std::min_element(ctx->seen.begin(), ctx->seen.end(), [](const SeenGraph &a, const SeenGraph &b) {
+                return a.last_use < b.last_use;
+            });
+            mx_graph_free(oldest->replay);
+            ctx->seen.erase(oldest);
+        }
+        ctx->seen.push_back(SeenGraph{std::move(keys), 0, nullptr, 0});
+        g = &ctx->seen.back();
     }
-    if (ctx->replay) {
-        const int rc = mx_graph_launch(ctx->be, ctx->replay);
+    g->last_use = ++ctx->clock;
+    if (g->replay) {
+        const int rc = mx_graph_launch(ctx->be, g->replay);
         if (rc == MX_SUCCESS) {
             ctx->counts[kReplayed]++;
             return GGML_STATUS_SUCCESS;
         }
-        mx_graph_free(ctx->replay);  // recorded before the scratch grew: compute eagerly, record again next time
-        ctx->replay = nullptr;
-        ctx->repeats = 1;
+        mx_graph_free(g->replay);  // recorded before the scratch grew: compute eagerly, record again next time
+        g->replay = nullptr;
+        g->repeats = 1;
     }
-    if (ctx->repeats >= 2) {
+    if (g->repeats >= 2) {
         int rc = mx_graph_begin(ctx->be);
         if (rc == MX_SUCCESS) {
             const int run = run_nodes(ctx, cgraph);
-            mx_graph *g = nullptr;
-            rc = mx_graph_end(ctx->be, &g);
+            mx_graph *rec = nullptr;
+            rc = mx_graph_end(ctx->be, &rec);
             if (run == MX_SUCCESS && rc == MX_SUCCESS) {
-                ctx->replay = g;
+                g->replay = rec;
                 ctx->counts[kRecorded]++;
-                return to_status(mx_graph_launch(ctx->be, g));
+                return to_status(mx_graph_launch(ctx->be, rec));
             }
-            mx_graph_free(g);
+            mx_graph_free(rec);
         }
-        ctx->repeats = -1000000;  // not recordable: compute it eagerly from now on
+        g->repeats = -1000000;  // not recordable: compute it eagerly from now on
     }
     ctx->counts[kEager]++;
     return to_status(run_nodes(ctx, cgraph));
@@ -1012,7 +1047,7 @@ bool linked_ggml_matches() {
     const char *glu = ggml_glu_op_name(GGML_GLU_OP_SWIGLU);
     if (!glu || std::strcmp(glu, "SWIGLU") != 0) return differs("GLU op", "SWIGLU", glu);
     // tensors made by the linked ggml, read through this backend's view of ggml_tensor
-    ggml_init_params ip{16 * 1024, nullptr, true};
+    ggml_init_params ip{1024 * 1024, nullptr, true};
     ggml_context *ctx = ggml_init(ip);
     if (!ctx) return differs("ggml_init result", "a context", nullptr);
     bool ok = true;
@@ -1034,6 +1069,24 @@ bool linked_ggml_matches() {
              op_f32(r, 8) == 1.0f && r->src[0] == x && r->src[1] == pos && g->op == GGML_OP_GLU &&
              ggml_get_glu_op(g) == GGML_GLU_OP_SWIGLU && g->op_params[1] == 0 && g->src[1] == x;
         if (!ok) differs("operation parameters", "ggml.c's", "others");
+    }
+    if (ok) {
+        // a graph's layout and use counts, read as the fusions read them: n is read twice, m once, a not at all;
+        // a view of the last two nodes (one split of the graph) sees the same counts
+        ggml_tensor *n = ggml_rms_norm(ctx, x, 0.5f);
+        ggml_tensor *m = ggml_mul(ctx, n, n);
+        ggml_tensor *a = ggml_add(ctx, m, x);
+        ggml_cgraph *g = ggml_new_graph_custom(ctx, 16, false);
+        ok = g != nullptr;
+        if (ok) {
+            ggml_build_forward_expand(g, a);
+            ggml_cgraph v = ggml_graph_view(g, 1, 3);
+            ok = ggml_graph_n_nodes(g) == 3 && g->n_nodes == 3 && g->nodes[0] == n && g->nodes[1] == m &&
+                 g->nodes[2] == a && ggml_node_get_use_count(g, 0) == 2 && ggml_node_get_use_count(g, 1) == 1 &&
+                 ggml_node_get_use_count(g, 2) == 0 && v.n_nodes == 2 && v.nodes[0] == m &&
+                 ggml_node_get_use_count(&v, 0) == 1;
+        }
+        if (!ok) differs("graph layout or use counts", "ggml-impl.h's", "others");
     }
     ggml_free(ctx);
     return ok;

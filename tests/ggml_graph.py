@@ -26,6 +26,18 @@ class Tensor(ctypes.Structure):
                 ("extra", ctypes.c_void_p), ("padding", ctypes.c_char * 8)]
 
 
+class HashSet(ctypes.Structure):
+    _fields_ = [("size", ctypes.c_size_t), ("used", ctypes.c_void_p), ("keys", ctypes.c_void_p)]
+
+
+class CGraph(ctypes.Structure):
+    """ggml_cgraph as ggml-impl.h lays it out (a view of a graph is one by value)."""
+    _fields_ = [("size", ctypes.c_int), ("n_nodes", ctypes.c_int), ("n_leafs", ctypes.c_int),
+                ("nodes", ctypes.c_void_p), ("grads", ctypes.c_void_p), ("grad_accs", ctypes.c_void_p),
+                ("leafs", ctypes.c_void_p), ("use_counts", ctypes.c_void_p), ("visited_hash_set", HashSet),
+                ("order", ctypes.c_int)]
+
+
 class InitParams(ctypes.Structure):
     _fields_ = [("mem_size", ctypes.c_size_t), ("mem_buffer", ctypes.c_void_p), ("no_alloc", ctypes.c_bool)]
 
@@ -65,6 +77,7 @@ _SIGS = {
     "ggml_flash_attn_ext": (TP, [VP, TP, TP, TP, TP, FL, FL, FL]), "ggml_flash_attn_ext_set_prec": (None, [TP, INT]),
     "ggml_swiglu_split": (TP, [VP, TP, TP]),
     "ggml_new_graph": (VP, [VP]), "ggml_build_forward_expand": (None, [VP, TP]),
+    "ggml_graph_view": (CGraph, [VP, INT, INT]),
     "ggml_graph_n_nodes": (INT, [VP]), "ggml_graph_node": (TP, [VP, INT]),
     "ggml_host_last_log": (ctypes.c_char_p, []), "ggml_host_clear_log": (None, []),
     # backend
@@ -87,6 +100,7 @@ _SIGS = {
     "ggml_backend_tensor_copy": (None, [TP, TP]),
     "ggml_backend_name": (ctypes.c_char_p, [VP]), "ggml_backend_free": (None, [VP]),
     "ggml_backend_synchronize": (None, [VP]), "ggml_backend_graph_compute": (INT, [VP, VP]),
+    "ggml_host_graph_compute_split": (INT, [VP, VP, INT, INT]),
     "ggml_backend_supports_op": (ctypes.c_bool, [VP, TP]),
     "ggml_backend_event_new": (VP, [VP]), "ggml_backend_event_free": (None, [VP]),
     "ggml_backend_event_record": (None, [VP, VP]), "ggml_backend_event_synchronize": (None, [VP]),
@@ -166,6 +180,16 @@ class Graph:
     def nodes(self):
         return [self.h.ggml_graph_node(self.graph, i) for i in range(self.h.ggml_graph_n_nodes(self.graph))]
 
+    def index(self, t):
+        """The position of node t in the graph."""
+        addrs = [ctypes.addressof(n.contents) for n in self.nodes()]
+        return addrs.index(ctypes.addressof(t.contents))
+
+    def view(self, i0, i1):
+        """Nodes [i0, i1) as ggml_backend_sched hands a backend one split: a view sharing the graph's use counts.
+        Returns the view (a CGraph, kept by the caller while used)."""
+        return self.h.ggml_graph_view(self.graph, i0, i1)
+
 
 class Device:
     """The MI355X backend's first device, one backend (stream) on it, and its buffer type."""
@@ -241,6 +265,11 @@ class Device:
         st = self.h.ggml_backend_graph_compute(self.backend, g.graph)
         assert st == 0, (st, self.h.ggml_host_last_log())
 
+    def compute_split(self, g, i0, i1):
+        """Nodes [i0, i1) of g computed as one split of a scheduled graph."""
+        st = self.h.ggml_host_graph_compute_split(self.backend, g.graph, i0, i1)
+        assert st == 0, (st, self.h.ggml_host_last_log())
+
     def supports(self, t):
         return self.h.ggml_backend_dev_supports_op(self.dev, t)
 
@@ -249,13 +278,15 @@ STEPS = ["node", "products", "norm_products", "product_out", "attention", "exper
 
 
 def plan(g):
-    """The MI355X backend's plan of a graph (no device needed): [(step kind, index of its first node)]."""
+    """The MI355X backend's plan of a graph (no device needed): [(step kind, index of its first node)]. g: a Graph, or
+    a CGraph view of one (one split)."""
     h, b = libs()
     reg = b.ggml_backend_mi355x_reg()
     fp = h.ggml_backend_reg_get_proc_address(reg, b"ggml_backend_mi355x_plan")
     f = ctypes.CFUNCTYPE(INT, VP, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32), INT)(fp)
     kinds, first = (ctypes.c_int32 * 8192)(), (ctypes.c_int32 * 8192)()
-    n = f(g.graph, kinds, first, 8192)
+    graph = ctypes.addressof(g) if isinstance(g, CGraph) else g.graph
+    n = f(graph, kinds, first, 8192)
     return [(STEPS[kinds[i]], first[i]) for i in range(n)]
 
 

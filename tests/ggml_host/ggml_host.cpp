@@ -14,7 +14,6 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
-#include <unordered_set>
 #include <vector>
 
 #include "ggml-backend-impl.h"
@@ -35,10 +34,6 @@ struct ggml_context {
     std::vector<ggml_cgraph *> graphs;
 };
 
-struct ggml_cgraph {
-    std::vector<ggml_tensor *> nodes, leafs;
-    std::unordered_set<const ggml_tensor *> visited;
-};
 
 namespace {
 
@@ -121,14 +116,36 @@ ggml_tensor *view_tensor(ggml_context *ctx, ggml_tensor *a) {
 
 void set_f32(ggml_tensor *t, int i, float v) { std::memcpy(&t->op_params[i], &v, sizeof v); }
 
+// ggml_visit_parents: depth-first over the sources, each tensor listed once (a node or a leaf) after its sources; a
+// tensor's use count goes up once per node that names it as a source, over the whole graph.
 void visit(ggml_cgraph *g, ggml_tensor *t) {
-    if (!g->visited.insert(t).second) return;
-    for (int s = 0; s < GGML_MAX_SRC; s++)
-        if (t->src[s]) visit(g, t->src[s]);
-    if (t->op == GGML_OP_NONE && !(t->flags & GGML_TENSOR_FLAG_PARAM))
-        g->leafs.push_back(t);
-    else
-        g->nodes.push_back(t);
+    const size_t slot = ggml_hash_find(&g->visited_hash_set, t);
+    HOST_CHECK(slot != GGML_HASHSET_FULL);
+    if (ggml_bitset_get(g->visited_hash_set.used, slot)) return;
+    g->visited_hash_set.keys[slot] = t;
+    g->visited_hash_set.used[slot >> 5] |= 1u << (slot & 31);
+    g->use_counts[slot] = 0;
+    for (int s = 0; s < GGML_MAX_SRC; s++) {
+        if (!t->src[s]) continue;
+        visit(g, t->src[s]);
+        g->use_counts[ggml_hash_find(&g->visited_hash_set, t->src[s])]++;
+    }
+    if (t->op == GGML_OP_NONE && !(t->flags & GGML_TENSOR_FLAG_PARAM)) {
+        HOST_CHECK(g->n_leafs < g->size);
+        g->leafs[g->n_leafs++] = t;
+    } else {
+        HOST_CHECK(g->n_nodes < g->size);
+        g->nodes[g->n_nodes++] = t;
+    }
+}
+
+void free_graph(ggml_cgraph *g) {
+    delete[] g->nodes;
+    delete[] g->leafs;
+    delete[] g->use_counts;
+    delete[] g->visited_hash_set.used;
+    delete[] g->visited_hash_set.keys;
+    delete g;
 }
 
 ggml_backend_buffer_t buffer_of(const ggml_tensor *t) { return t->view_src ? t->view_src->buffer : t->buffer; }
@@ -200,7 +217,7 @@ void ggml_free(ggml_context *ctx) {
     if (!ctx) return;
     for (ggml_tensor *t : ctx->tensors) delete t;
     for (void *p : ctx->host_data) std::free(p);
-    for (ggml_cgraph *g : ctx->graphs) delete g;
+    for (ggml_cgraph *g : ctx->graphs) free_graph(g);
     delete ctx;
 }
 
@@ -391,16 +408,40 @@ ggml_tensor *ggml_swiglu_split(ggml_context *ctx, ggml_tensor *a, ggml_tensor *b
 }
 
 // ------------------------------------------------------------------------------------------------- graphs
-ggml_cgraph *ggml_new_graph(ggml_context *ctx) {
+ggml_cgraph *ggml_new_graph_custom(ggml_context *ctx, size_t size, bool grads) {
+    HOST_CHECK(!grads && size > 0);
     auto *g = new ggml_cgraph;
+    std::memset(g, 0, sizeof *g);
+    g->size = (int)size;
+    g->nodes = new ggml_tensor *[size]();
+    g->leafs = new ggml_tensor *[size]();
+    const size_t slots = 2 * size + 1;  // at most 2 size tensors (nodes and leafs) in an open-addressing set
+    g->use_counts = new int32_t[slots]();
+    g->visited_hash_set.size = slots;
+    g->visited_hash_set.used = new ggml_bitset_t[(slots + 31) / 32]();
+    g->visited_hash_set.keys = new ggml_tensor *[slots]();
+    g->order = GGML_CGRAPH_EVAL_ORDER_LEFT_TO_RIGHT;
     ctx->graphs.push_back(g);
     return g;
 }
+ggml_cgraph *ggml_new_graph(ggml_context *ctx) { return ggml_new_graph_custom(ctx, 16384, false); }
+ggml_cgraph ggml_graph_view(ggml_cgraph *g, int i0, int i1) {
+    HOST_CHECK(0 <= i0 && i0 <= i1 && i1 <= g->n_nodes);
+    ggml_cgraph v = *g;
+    v.size = 0;
+    v.n_nodes = i1 - i0;
+    v.n_leafs = 0;
+    v.nodes = g->nodes + i0;
+    v.grads = nullptr;
+    v.grad_accs = nullptr;
+    v.leafs = nullptr;
+    return v;
+}
 void ggml_build_forward_expand(ggml_cgraph *g, ggml_tensor *t) { visit(g, t); }
-int ggml_graph_n_nodes(ggml_cgraph *g) { return (int)g->nodes.size(); }
+int ggml_graph_n_nodes(ggml_cgraph *g) { return g->n_nodes; }
 ggml_tensor *ggml_graph_node(ggml_cgraph *g, int i) {
-    if (i < 0) i += (int)g->nodes.size();
-    HOST_CHECK(i >= 0 && i < (int)g->nodes.size());
+    if (i < 0) i += g->n_nodes;
+    HOST_CHECK(i >= 0 && i < g->n_nodes);
     return g->nodes[i];
 }
 
@@ -543,6 +584,12 @@ ggml_status ggml_backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgra
     const ggml_status st = ggml_backend_graph_compute_async(backend, cgraph);
     ggml_backend_synchronize(backend);
     return st;
+}
+// Nodes [i0, i1) of a graph computed as ggml_backend_sched computes one split of it: a view sharing the whole graph's
+// use counts, handed to the backend's graph_compute.
+ggml_status ggml_host_graph_compute_split(ggml_backend_t backend, ggml_cgraph *cgraph, int i0, int i1) {
+    ggml_cgraph view = ggml_graph_view(cgraph, i0, i1);
+    return ggml_backend_graph_compute(backend, &view);
 }
 bool ggml_backend_supports_op(ggml_backend_t backend, const ggml_tensor *op) {
     return ggml_backend_dev_supports_op(backend->device, op);

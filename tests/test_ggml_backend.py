@@ -130,6 +130,37 @@ def test_plan_of_a_moe_ffn():
         m.close()
 
 
+def router_split_graph(H, E, T, n_used, later):
+    """A Drama-3 FFN's front (text-model.cpp:198-221): the FFN norm x weight feeds the router product, and -- after the
+    router's softmax and top-k, which stay on the CPU and split the scheduled graph there -- the routed experts read
+    it again. Returns (graph, tensors by name, index of the first node of the second split)."""
+    g = G.Graph()
+    t = dict(x=g.new(G.F32, H, T), nw=g.new(G.F32, H), wr=g.new(G.Q8_0, H, E), ex=g.new(G.Q4_K, H, 256, E),
+             sel=g.new(G.I32, n_used, T))
+    t["h"] = g.mul(g.rms_norm(t["x"], 1e-6), t["nw"])
+    t["r"] = g.mul_mat(t["wr"], t["h"])
+    g.h.ggml_set_output(t["r"])
+    g.expand(t["r"])
+    if later:
+        t["e"] = g.mul_mat_id(t["ex"], g.reshape_3d(t["h"], H, 1, T), t["sel"])
+        g.h.ggml_set_output(t["e"])
+        g.expand(t["e"])
+    return g, t, g.index(t["r"]) + 1
+
+
+def test_plan_of_a_split_keeps_what_a_later_split_reads():
+    """Under ggml_backend_sched the backend computes one split of the graph at a time, a view sharing the whole graph's
+    use counts. When a later split reads the norm x weight again, the split holding the router product keeps norm and
+    weight as their own nodes (the fused product would not write them); with no later reader the same split fuses."""
+    for later, want in ((True, ["node", "node", "products"]), (False, ["norm_products"])):
+        g, t, cut = router_split_graph(2048, 8, 4, 4, later)
+        try:
+            v = g.view(0, cut)
+            assert [k for k, _ in G.plan(v)] == want
+        finally:
+            g.close()
+
+
 # --------------------------------------------------------------------------------------------- on MI355X
 @pytest.fixture(scope="module")
 def device():
@@ -176,6 +207,74 @@ def test_buffer_transfers(device):
         assert np.array_equal(got, ref)
         device.h.ggml_backend_buffer_clear(buf, 0)
         assert not device.download(a, np.uint8, w.shape).any()
+    finally:
+        g.close()
+
+
+@pytest.mark.gpu
+def test_copy_lands_before_the_next_compute(device):
+    """ggml_backend_tensor_copy between two device tensors (ModelFile's copy, model-file.cpp:153-158), then at once a
+    product reading the copy on the backend's own stream: the copy has landed when the call returns."""
+    K, N, T = 4096, 16384, 2
+    g = G.Graph()
+    try:
+        a, c = g.new(G.Q8_0, K, N), g.new(G.Q8_0, K, N)
+        n0 = len(g.tensors)
+        x = g.new(G.F32, K, T)
+        y = g.mul_mat(c, x)
+        g.h.ggml_set_output(y)
+        g.expand(y)
+        device.place([a, c], usage=1)
+        device.place(g.tensors[n0:])
+        w = O.quantize_chunk(O.TYPE_Q8_0, O.fill_normal(0x7C00, N, K, 0.0, 0.02))
+        xv = O.fill_normal(0x7C01, T, K)
+        device.upload(a, w)
+        device.upload(x, xv)
+        device.h.ggml_backend_tensor_memset(c, 0, 0, device.h.ggml_nbytes(c))
+        device.h.ggml_backend_tensor_copy(a, c)
+        device.compute(g)
+        assert rel_err(device.download(y, np.float32, (T, N)), O.mul_mat(O.TYPE_Q8_0, w, xv)) <= TIGHT
+    finally:
+        g.close()
+
+
+@pytest.mark.gpu
+def test_scheduled_splits_keep_intermediates_and_replay(device):
+    """A graph computed as two splits, as ggml_backend_sched computes Drama 3's (text-model.cpp:91-97): the first holds
+    the FFN norm x weight and the router product, the second the routed experts reading that norm x weight again.
+    The first split writes it (a later split reads it), and each split is recorded and replayed on its own: computed
+    alternately four times, each is eager twice, recorded on its third computation and replayed on its fourth."""
+    H, E, T, n_used = 2048, 8, 4, 4
+    g, t, cut = router_split_graph(H, E, T, n_used, True)
+    try:
+        n = g.h.ggml_graph_n_nodes(g.graph)
+        weights = [t["nw"], t["wr"], t["ex"]]
+        device.place(weights, usage=1)
+        device.place([u for u in g.tensors if all(ctypes.addressof(u.contents) != ctypes.addressof(w.contents)
+                                                  for w in weights)])
+        device.init_views(g.tensors)
+        nw = O.fill_normal(0x7D00, 1, H, 1.0, 0.1)[0]
+        wr = O.quantize_chunk(O.TYPE_Q8_0, O.fill_normal(0x7D01, E, H, 0.0, 0.02))
+        ex = O.quantize_chunk(O.TYPE_Q4_K, O.fill_normal(0x7D02, E * 256, H, 0.0, 0.02))
+        device.upload(t["nw"], nw)
+        device.upload(t["wr"], wr)
+        device.upload(t["ex"], ex)
+        rng = np.random.default_rng(0x7D10)
+        before = device.counters()
+        for step in range(4):
+            xv = O.fill_normal(int(rng.integers(1 << 30)), T, H)
+            sel = np.stack([rng.choice(E, n_used, replace=False) for _ in range(T)]).astype(np.int32)
+            device.upload(t["x"], xv)
+            device.upload(t["sel"], sel)
+            device.compute_split(g, 0, cut)
+            device.compute_split(g, cut, n)
+            h = O.binary("mul", O.rms_norm(xv, 1e-6), nw)
+            assert rel_err(device.download(t["r"], np.float32, (T, E)), O.mul_mat(O.TYPE_Q8_0, wr, h)) <= TIGHT
+            got = device.download(t["e"], np.float32, (T, n_used, 256))
+            want = O.mul_mat_id(O.TYPE_Q4_K, ex.reshape(E, 256, -1), h.reshape(T, 1, H), sel)
+            assert rel_err(got, want) <= TIGHT, f"step {step}"
+        after = device.counters()
+        assert [after[c] - before[c] for c in ("eager", "recorded", "replayed")] == [4, 2, 2]
     finally:
         g.close()
 
