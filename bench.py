@@ -199,6 +199,7 @@ def time_graph(be, launches, steps: int, warmup: int, use_graph: bool = True):
         be.graph_begin()
         eager()
         graph = be.graph_end()
+        log(f"step graph: {len(launches)} launches recorded as {be.graph_nodes(graph)} kernel nodes")
     step = (lambda: be.graph_launch(graph)) if graph else eager
     for _ in range(warmup):
         step()
@@ -529,6 +530,40 @@ def summarize_pmc(fetch_csv: str, write_csv: str, kernel: str) -> str:
              f"{COPY_BYTES >> 20} MiB device copy",
              f"fetch_bytes_per_launch: {fb:.0f}", f"write_bytes_per_launch: {wb:.0f}",
              f"traffic_bytes_per_launch: {fb + wb:.0f}"]
+    return "\n".join(lines)
+
+
+def summarize_busy(csv_path: str, kernel: str, clock_mhz: float) -> str:
+    """Per-dispatch time of the kernels whose name holds `kernel`, from one rocprofv3 --pmc GRBM_GUI_ACTIVE run, two
+    ways: the dispatch's own start and end timestamps, and its GPU-busy clock cycles (counted over the dispatch, summed
+    over the 8 XCDs) at the shader clock. Both carry the profiler's per-dispatch cost; the one-workgroup GET_ROWS of
+    the same run (1 KB read) measures that floor, and the 512 MB cache-flush reads (k_peak_read) check the cycle
+    scale against their known duration."""
+    import csv
+    import statistics
+    busy, span = {}, {}
+    for r in csv.DictReader(open(csv_path)):
+        if r["Counter_Name"] != "GRBM_GUI_ACTIVE":
+            continue
+        busy.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]) / 8 / clock_mhz)
+        span.setdefault(r["Kernel_Name"], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    med = statistics.median
+    lines = [f"per dispatch, us: timestamps (end - start) and GRBM_GUI_ACTIVE / 8 XCDs / {clock_mhz:.0f} MHz"]
+    floor = [name for name in busy if "k_get_rows" in name]
+    for name in sorted(busy):
+        if kernel in name or "k_peak_read" in name or "k_get_rows" in name:
+            lines.append(f"{name[:56]:56s} dispatches {len(busy[name]):5d}  timestamps median {med(span[name]):8.3f}"
+                         f"  busy median {med(busy[name]):8.3f}")
+    mv_span = [v for name in span if kernel in name for v in span[name]]
+    mv_busy = [v for name in busy if kernel in name for v in busy[name]]
+    lines.append(f"{kernel}: {len(mv_span)} dispatches, timestamps mean {statistics.mean(mv_span):.3f} us, "
+                 f"busy mean {statistics.mean(mv_busy):.3f} us")
+    if floor:
+        fs = med([v for name in floor for v in span[name]])
+        fb = med([v for name in floor for v in busy[name]])
+        lines.append(f"one-workgroup floor (k_get_rows): timestamps {fs:.3f} us, busy {fb:.3f} us")
+        lines.append(f"{kernel} above the floor: timestamps {statistics.mean(mv_span) - fs:.3f} us, "
+                     f"busy {statistics.mean(mv_busy) - fb:.3f} us")
     return "\n".join(lines)
 
 
@@ -1148,9 +1183,15 @@ def main():
                     help="a kernel choice of the backend (mx_backend_set_option), e.g. gemm_q8_0=1; repeatable")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the traffic summary of two rocprofv3 --pmc runs of --workload's benchmark and exit")
+    ap.add_argument("--summarize-busy", nargs=2, metavar=("GRBM_CSV", "CLOCK_MHZ"),
+                    help="print the per-dispatch busy time of a rocprofv3 --pmc GRBM_GUI_ACTIVE run of --workload's "
+                         "benchmark at the given shader clock and exit")
     args = ap.parse_args()
     if args.summarize_pmc:
         print(summarize_pmc(*args.summarize_pmc, TRAFFIC[args.workload][1]))
+        return
+    if args.summarize_busy:
+        print(summarize_busy(args.summarize_busy[0], TRAFFIC[args.workload][1], float(args.summarize_busy[1])))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported", file=sys.stderr)

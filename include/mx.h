@@ -360,6 +360,8 @@ MX_API int mx_peak_mfma(mx_backend *be, int kind, int workgroups, int iters);
 MX_API int mx_graph_begin(mx_backend *be);
 MX_API int mx_graph_end(mx_backend *be, mx_graph **graph);
 MX_API int mx_graph_launch(mx_backend *be, mx_graph *graph);
+/* The number of nodes (kernel launches) a recorded graph holds; 0 for a null graph. */
+MX_API size_t mx_graph_nodes(const mx_graph *graph);
 /* Waits for the graph's replays on its backend's stream, then frees it; free graphs before their backend. */
 MX_API void mx_graph_free(mx_graph *graph);
 

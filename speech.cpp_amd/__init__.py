@@ -49,7 +49,7 @@ EXPORTS = [
     "mx_gguf_get_int", "mx_gguf_get_float", "mx_gguf_get_arr", "mx_gguf_get_arr_str", "mx_gguf_load_tensor",
     "mx_rms_norm", "mx_binary", "mx_swiglu", "mx_supports_rope", "mx_rope", "mx_set_rows", "mx_supports_flash_attn_ext",
     "mx_flash_attn_ext", "mx_mul_mat_fused", "mx_qk_norm_rope_kv", "mx_attn_decode", "mx_decoder_new", "mx_decoder_free",
-    "mx_decoder_step", "mx_mul_mat_id_noalloc", "mx_mul_mat_id_noalloc_bytes", "mx_peak_read", "mx_peak_mfma",
+    "mx_decoder_step", "mx_graph_nodes", "mx_mul_mat_id_noalloc", "mx_mul_mat_id_noalloc_bytes", "mx_peak_read", "mx_peak_mfma",
 ]
 NOALLOC_SCRATCH_BYTES = 16 << 20  # MX_NOALLOC_SCRATCH_BYTES
 
@@ -189,6 +189,7 @@ def lib():
         "mx_decoder_new": ([vp, ctypes.POINTER(MxQwen3)], vp),
         "mx_decoder_free": ([vp], None),
         "mx_decoder_step": ([vp, P, P, P, P], i32),
+        "mx_graph_nodes": ([vp], sz),
         "mx_mul_mat_id_noalloc": ([vp, P, P, P, P], i32),
         "mx_mul_mat_id_noalloc_bytes": ([P, P, P], sz),
     }
@@ -497,6 +498,10 @@ class Backend:
 
     def graph_launch(self, g) -> None:
         check(lib().mx_graph_launch(self.h, ctypes.c_void_p(g)))
+
+    @staticmethod
+    def graph_nodes(g) -> int:
+        return int(lib().mx_graph_nodes(ctypes.c_void_p(g)))
 
     def graph_free(self, g) -> None:
         lib().mx_graph_free(ctypes.c_void_p(g))

@@ -431,20 +431,22 @@ MX_API int mx_gguf_load_tensor(mx_backend *be, const mx_gguf *f, int64_t i, cons
             return mx::set_error(MX_INVALID, ("the tensor " + t.name + " has another shape").c_str());
     std::unique_ptr<FILE, int (*)(FILE *)> fp(std::fopen(f->path.c_str(), "rb"), &std::fclose);
     if (!fp) return mx::set_error(MX_FAILED, ("cannot open " + f->path).c_str());
-    bool ok = seek(fp.get(), f->data_offset + t.offset);
-    std::vector<uint8_t> piece;
-    for (uint64_t done = 0; ok && done < t.nbytes;) {
-        const size_t n = (size_t)std::min<uint64_t>(kReadPiece, t.nbytes - done);
-        piece.resize(std::max(piece.size(), n));
-        ok = std::fread(piece.data(), 1, n, fp.get()) == n;
-        if (!ok) break;
-        const int rc = mx_tensor_set(be, dst, piece.data(), (size_t)done, n);
-        if (rc != MX_SUCCESS) return rc;  // its message stands
-        done += n;
+    // the tensor's bytes stream through one host buffer of at most kReadPiece bytes, each piece set at its offset
+    std::vector<uint8_t> buf((size_t)std::min<uint64_t>(kReadPiece, t.nbytes));
+    uint64_t got = 0;
+    if (seek(fp.get(), f->data_offset + t.offset)) {
+        while (got < t.nbytes) {
+            const size_t want = (size_t)std::min<uint64_t>(buf.size(), t.nbytes - got);
+            if (std::fread(buf.data(), 1, want, fp.get()) != want) break;
+            const int rc = mx_tensor_set(be, dst, buf.data(), (size_t)got, want);
+            if (rc != MX_SUCCESS) return rc;  // its message stands
+            got += want;
+        }
     }
-    if (!ok)
-        return mx::set_error(MX_FAILED, ("cannot read the tensor " + t.name + " of " + f->path +
-                                         "; the file is shorter than its header says").c_str());
+    if (got < t.nbytes)
+        return mx::set_error(MX_FAILED, (f->path + ": tensor " + t.name + " ends past the end of the file (" +
+                                         std::to_string(got) + " of its " + std::to_string(t.nbytes) +
+                                         " bytes read)").c_str());
     return MX_SUCCESS;
 }
 

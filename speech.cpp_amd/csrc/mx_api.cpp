@@ -1513,6 +1513,12 @@ MX_API int mx_graph_end(mx_backend *be, mx_graph **graph) {
     return MX_SUCCESS;
 }
 
+MX_API size_t mx_graph_nodes(const mx_graph *graph) {
+    size_t n = 0;
+    if (!graph || hipGraphGetNodes(graph->graph, nullptr, &n) != hipSuccess) return 0;
+    return n;
+}
+
 MX_API int mx_graph_launch(mx_backend *be, mx_graph *graph) {
     int rc = check_be(be);
     if (rc) return rc;

@@ -69,7 +69,8 @@ def test_products_on_loaded_weights(mx, be, tmp_path):
 
 
 def test_short_file_is_reported(mx, be, tmp_path):
-    """A file cut after it was opened: the read of ModelFile::load fails with its message, nothing aborts."""
+    """A file cut after it was opened: the load fails with a message naming the tensor and the bytes read, nothing
+    aborts."""
     path, tensors, _ = model_file(tmp_path)
     g = mx.Gguf(path)
     try:
@@ -78,7 +79,7 @@ def test_short_file_is_reported(mx, be, tmp_path):
         T = be.tensor(info["type"], info["ne"])
         with pytest.raises(mx.MxError) as e:
             mx.check(mx.lib().mx_gguf_load_tensor(be.h, g.h, len(tensors) - 1, T.ref()))
-        assert "shorter than its header says" in str(e.value)
+        assert "ends past the end of the file" in str(e.value)
         wrong = be.tensor(mx.F32, (4, 4))
         with pytest.raises(mx.MxError):
             mx.check(mx.lib().mx_gguf_load_tensor(be.h, g.h, 0, wrong.ref()))

@@ -250,6 +250,15 @@ def test_mul_mat_many_row_blocks(mx, be, t, M):
     assert bits_equal(got, (r.reshape(M, N) + y.reshape(M, N)).astype(np.float32))
 
 
+def test_mul_mat_output_head_full_shape(mx, be):
+    """The 0.6B shape's tied output head at its full size: 151,936 x 1024 Q8_0 (166 MB, 9,496 row blocks) on one
+    column, as the decode step's last product runs it."""
+    K, N = 1024, 151_936
+    w = mx.quantize_normal(O.TYPE_Q8_0, 0x5EED4100, N, K, 0.02)
+    x = acts(0xAC704100, 1, K)
+    assert rel_err(run_mul_mat(mx, be, O.TYPE_Q8_0, w, x, K, N), O.mul_mat(O.TYPE_Q8_0, w, x)) <= TIGHT
+
+
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
 def test_mul_mat_x86_rounding(mx, be, t):
     K, N, M = 512, 64, 3
@@ -414,6 +423,51 @@ def test_mul_mat_id_group(mx, be, t, T):
     for a, b, w in zip(Ys, Yg, (wg, wu)):
         assert np.array_equal(a.numpy(), b.numpy())
         assert rel_err(b.numpy().reshape(T, n_ids, N), O.mul_mat_id(t, w, x, ids)) <= TIGHT
+
+
+_MOE_FULL = {}
+
+
+def moe_full_weights(mx):
+    """The full-shape MoE layer's gate, up and down experts (Q4_K from N(0, 0.02)), quantized once per run."""
+    if not _MOE_FULL:
+        E, H, F = 64, 2048, 1536
+        _MOE_FULL["w"] = tuple(mx.quantize_normal(O.TYPE_Q4_K, 0x5EED4000 + i, E * n, k, 0.02).reshape(E, n, -1)
+                               for i, (n, k) in enumerate(((F, H), (F, H), (H, F))))
+    return _MOE_FULL["w"]
+
+
+@pytest.mark.parametrize("T", [1, 16, 256])
+def test_moe_layer_full_shape(mx, be, T):
+    """The drama3-like MoE FFN at its full shape (text-model.cpp:198-221): 64 Q4_K experts, hidden 2048, expert FFN 1536,
+    top-4 of N(0, 1) router logits per token, T = 1 / 16 / 256 tokens -- the gate and up experts as one group over the
+    shared rows (the launch the layer spends most of its time in at 256 tokens: 1,024 pairs over all 64 experts) and
+    the down experts over per-slot rows. The kernels compute every output row; every fifth row of each expert (rows in
+    every column tile) is held to the oracle on the same bytes."""
+    E, H, F, n_ids = 64, 2048, 1536, 4
+    t = O.TYPE_Q4_K
+    seed = 0x5EED4000 + T
+    wg, wu, wd = moe_full_weights(mx)
+    x = acts(seed + 3, T, H).reshape(T, 1, H)
+    logits = O.fill_normal(seed + 4, T, E)
+    ids = np.argsort(-logits, axis=1, kind="stable")[:, :n_ids].astype(np.int32)
+    Wg, Wu = be.tensor(t, (H, F, E), wg.reshape(E * F, -1)), be.tensor(t, (H, F, E), wu.reshape(E * F, -1))
+    Wd = be.tensor(t, (F, H, E), wd.reshape(E * H, -1))
+    Xt, It = be.tensor(mx.F32, (H, 1, T), x), be.tensor(mx.I32, (n_ids, T), ids)
+    Yg, Yu = be.tensor(mx.F32, (F, n_ids, T)), be.tensor(mx.F32, (F, n_ids, T))
+    be.mul_mat_id_group([Wg, Wu], Xt, It, [Yg, Yu])
+    be.sync()
+    rows = np.arange(0, F, 5)
+    for Y, w in ((Yg, wg), (Yu, wu)):
+        got = Y.numpy().reshape(T, n_ids, F)[:, :, rows]
+        assert rel_err(got, O.mul_mat_id(t, np.ascontiguousarray(w[:, rows]), x, ids)) <= TIGHT
+    act = acts(seed + 5, T * n_ids, F).reshape(T, n_ids, F)
+    At, Yd = be.tensor(mx.F32, (F, n_ids, T), act), be.tensor(mx.F32, (H, n_ids, T))
+    be.mul_mat_id(Wd, At, It, Yd)
+    be.sync()
+    rows = np.arange(0, H, 5)
+    got = Yd.numpy().reshape(T, n_ids, H)[:, :, rows]
+    assert rel_err(got, O.mul_mat_id(t, np.ascontiguousarray(wd[:, rows]), act, ids)) <= TIGHT
 
 
 def test_mul_mat_id_group_refusals(mx, be):
