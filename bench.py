@@ -185,9 +185,10 @@ def label_table(launches, per_ms):
     return out
 
 
-def time_graph(be, launches, steps: int, warmup: int, use_graph: bool = True):
-    """Runs the launches once eagerly (sizes the scratch), records them as one graph, then times `steps` replays
-    between HIP events on the backend's stream after `warmup` untimed ones. Returns ms per step."""
+def time_graph(be, launches, steps: int, warmup: int, use_graph: bool = True, rounds: int = 3):
+    """Runs the launches once eagerly (sizes the scratch), records them as one graph, then after `warmup` untimed
+    replays times `rounds` rounds of exactly `steps` replays each between HIP events on the backend's stream (the
+    device synchronized before and after each). Returns the median round's ms per step."""
     def eager():
         for L in launches:
             L.fn()
@@ -205,20 +206,24 @@ def time_graph(be, launches, steps: int, warmup: int, use_graph: bool = True):
         step()
     be.sync()
     e0, e1 = be.event(), be.event()
-    t0 = time.perf_counter()
-    be.record(e0)
-    for _ in range(steps):
-        step()
-    be.record(e1)
-    be.sync()
-    wall = time.perf_counter() - t0
-    ms = be.elapsed_ms(e0, e1)
-    log(f"timed {steps} steps: {ms:.2f} ms by events, {wall * 1e3:.2f} ms by wall clock")
+    per = []
+    for r in range(rounds):
+        be.sync()
+        t0 = time.perf_counter()
+        be.record(e0)
+        for _ in range(steps):
+            step()
+        be.record(e1)
+        be.sync()
+        wall = time.perf_counter() - t0
+        ms = be.elapsed_ms(e0, e1)
+        per.append(ms / steps)
+        log(f"round {r + 1}: timed {steps} steps: {ms:.2f} ms by events, {wall * 1e3:.2f} ms by wall clock")
     be.event_free(e0)
     be.event_free(e1)
     if graph:
         be.graph_free(graph)
-    return ms / steps
+    return sorted(per)[len(per) // 2]
 
 
 def hbm_roofline(kernel, table, labels):
@@ -293,16 +298,24 @@ def cpu_result(many, one):
     return out
 
 
-def timed_sample(fn, seconds: float):
-    """Runs fn once untimed, then repeatedly for about `seconds`; returns (runs, elapsed s)."""
+def timed_sample(fn, seconds: float, rounds: int = 3):
+    """Runs fn once untimed, then in `rounds` timed rounds of about seconds / rounds each; returns (runs, elapsed s) of
+    the round with the median rate (every round's rate is logged)."""
     fn()
-    n, t0 = 0, time.perf_counter()
-    while True:
-        fn()
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            return n, el
+    out = []
+    for _ in range(rounds):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds / rounds:
+                break
+        out.append((n / el, n, el))
+    out.sort()
+    log("cpu sample rounds: " + ", ".join(f"{r:.4g}/s" for r, _, _ in out) + " (median reported)")
+    _, n, el = out[len(out) // 2]
+    return n, el
 
 
 # ---------------------------------------------------------------------------------------------- decoder shapes
@@ -496,7 +509,7 @@ def cpu_decode(dec, seconds, threads=None):
     n, el = timed_sample(token, seconds)
     return {"value": round(n / el, 2), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{n} full decode tokens (1 GET_ROWS + 197 Q8_0 mat-vecs, 633 MB of weights each) after one "
-                      f"untimed token, {el:.1f} s, int8 dots, src1 quantized once per product, rows split "
+                      f"untimed token, {el:.1f} s (the median of three rounds), int8 dots, src1 quantized once per product, rows split "
                       f"across {threads} threads"}
 
 
@@ -715,8 +728,9 @@ def run_decode_full(args, mx, be, threads):
 
 
 def cpu_decode_full(dec, st, seconds, nq, nkv, hd, threads=None):
-    """The full step on the host: the port's mat-vecs on the physical cores, the scalar oracle's norms, RoPE and
-    flash attention (ggml-cpu's loop) on one thread, over host copies of the same weights and caches."""
+    """The full step on the host: the port's mat-vecs and flash attention (ggml-cpu's loop, its (row, head) pairs over
+    the threads) on the physical cores, the oracle's norms, RoPE and SwiGLU over the step's small vectors on one
+    thread, over host copies of the same weights and caches."""
     O = load_oracle()
     threads = threads or O.physical_cores()
     H, n_kv, kv_dim = dec.hidden, st["n_kv"], nkv * hd
@@ -742,7 +756,8 @@ def cpu_decode_full(dec, st, seconds, nq, nkv, hd, threads=None):
             # SET_ROWS: the new position's keys and values into the f16 caches
             caches[l]["k"][:, KV_PAST] = k.reshape(nkv, hd).astype(np.float16).view(np.uint16)
             caches[l]["v"][:, KV_PAST] = v.reshape(nkv, hd).astype(np.float16).view(np.uint16)
-            att = O.flash_attn_ext(q.transpose(1, 0, 2), caches[l]["k"], caches[l]["v"], mask, 1.0 / np.sqrt(hd))
+            att = O.cpu_fast_flash_attn_ext(q.transpose(1, 0, 2), caches[l]["k"], caches[l]["v"], mask,
+                                            1.0 / np.sqrt(hd), threads)
             x = O.binary("add", x, O.cpu_fast_mul_mat(O.TYPE_Q8_0, dec.host[(l, "o")], att.reshape(1, -1), threads))
             hv = O.binary("mul", O.rms_norm(x, RMS_EPS), norms[l]["ffn"])
             g, u = (O.cpu_fast_mul_mat(O.TYPE_Q8_0, dec.host[(l, n)], hv, threads) for n in ("gate", "up"))
@@ -752,9 +767,10 @@ def cpu_decode_full(dec, st, seconds, nq, nkv, hd, threads=None):
 
     n, el = timed_sample(token, seconds)
     return {"value": round(n / el, 2), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} full decode tokens after one untimed token, {el:.1f} s: mat-vecs in the port on "
-                      f"{threads} threads, norms / RoPE / SET_ROWS / flash attention (ggml-cpu's loop over 1025 "
-                      f"positions) / SwiGLU in the scalar oracle on one thread"}
+            "sample": f"{n} full decode tokens after one untimed token, {el:.1f} s (the median of three rounds): "
+                      f"mat-vecs and flash attention (ggml-cpu's loop over 1025 positions, F16C, its (row, head) "
+                      f"pairs split across threads) in the port on {threads} threads; norms / RoPE / SET_ROWS / "
+                      f"SwiGLU over 1-4 KB vectors in the oracle on one thread"}
 
 
 # ---------------------------------------------------------------------------------------------- matvec
@@ -794,7 +810,7 @@ def run_matvec(args, mx, be, threads):
                 i[0] += 1
             n, el = timed_sample(one_c, sec)
             runs.append({"value": round(n * nbytes / el / 1e9, 2), "unit": "GB/s", "cores": c, "kind": "port",
-                         "sample": f"{n} products over {MATVEC_COPIES} rotated host copies, {el:.1f} s, {c} threads"})
+                         "sample": f"{n} products over {MATVEC_COPIES} rotated host copies, {el:.1f} s (the median of three rounds), {c} threads"})
         result["cpu_baseline"] = cpu_result(runs[0], runs[1])
     return result
 
@@ -815,27 +831,19 @@ def cpu_prefill(dec, M, seconds, types, cores=None):
     O = load_oracle()
     cores = cores or O.physical_cores()
     x = {K: O.fill_normal(0xAC700300 + K, M, K) for K in {K for _, K, _ in dec.shapes}}
-    state = {"l": 0, "ops": 0}
+    ops_per_layer = sum(2 * M * K * N for _, K, N in dec.shapes)
+    state = {"l": 0}
 
     def layer():
         l = state["l"] % dec.layers_n
         for name, K, N in dec.shapes:
             O.cpu_fast_mul_mat(types[name], dec.host[(l, name)], x[K], cores)
-            state["ops"] += 2 * M * K * N
         state["l"] += 1
 
-    layer()
-    state["ops"] = 0
-    n, t0 = 0, time.perf_counter()
-    while True:
-        layer()
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {"value": round(state["ops"] / el / 1e12, 4), "unit": "TOP/s", "cores": cores, "kind": "port",
-            "sample": f"{n} layers' 7 products at M = {M} after one untimed layer, {el:.1f} s, int8 dots, "
-                      f"{cores} threads"}
+    n, el = timed_sample(layer, seconds)
+    return {"value": round(ops_per_layer * n / el / 1e12, 4), "unit": "TOP/s", "cores": cores, "kind": "port",
+            "sample": f"{n} layers' 7 products at M = {M} after one untimed layer, {el:.1f} s (the median of three "
+                      f"rounds), int8 dots, {cores} threads"}
 
 
 def run_prefill_q4k(args, mx, be, threads):
@@ -1015,7 +1023,8 @@ def run_moe(args, mx, be, threads):
             n, el = timed_sample(lambda c=c: layer(c), sec)
             runs.append({"value": round(n * wb / el / 1e9, 2), "unit": "GB/s", "cores": c, "kind": "port",
                          "sample": f"{n} MoE layers at T = {T} ({len(np.unique(ids))} distinct experts), "
-                                   f"per-expert AVX2 products over the routed rows, {el:.1f} s, {c} threads"})
+                                   f"per-expert AVX2 products over the routed rows, {el:.1f} s (the median of three rounds), "
+                                   f"{c} threads"})
         result["cpu_baseline"] = cpu_result(runs[0], runs[1])
     return result
 
@@ -1133,20 +1142,24 @@ DEFAULT_STEPS = {"decode": (300, 20), "decode-full": (100, 10), "matvec": (50, 5
 
 
 def other_configs(args, mx, be, threads):
-    """The other benchmark configurations, each at its default steps without a CPU sample, summarized for the default
-    line: value, unit, time per step and the dominant kernel's roofline fraction (one after another on this backend;
-    each workload's tensors are freed before the next)."""
+    """The other benchmark configurations, each at its default steps with a CPU sample of half the decode step's
+    length, summarized for the default line: value, unit, time per step, the dominant kernel's roofline fraction and
+    the CPU baseline (one after another on this backend; each workload's tensors are freed before the next)."""
     out = {}
     for w in ("matvec", "prefill-q4k", "asr-1.7b", "moe"):
         sub = argparse.Namespace(**vars(args))
         sub.steps, sub.warmup = DEFAULT_STEPS[w]
-        sub.cpu_seconds, sub.blocks, sub.batches = 0, None, None
+        sub.cpu_seconds, sub.blocks, sub.batches = args.cpu_seconds / 2, None, None
         log(f"configs: {w}")
         r = WORKLOADS[w](sub, mx, be, threads)
         roof = r.get("roofline") or {}
         out[w] = {"value": r["value"], "unit": r["unit"], "ms_per_step": r["ms_per_step"],
                   "workload": r["config"]["workload"], "roofline_frac": roof.get("frac"), "bound": roof.get("bound"),
                   "kernel": roof.get("kernel")}
+        if "cpu_baseline" in r:
+            c = r["cpu_baseline"]
+            out[w]["cpu_baseline"] = {k: c[k] for k in ("value", "unit", "cores", "kind", "sample", "value_1thread")
+                                      if k in c}
         for k in ("hbm_frac", "decode_tok_s", "decode_hbm_frac", "prefill_ms"):
             if k in r:
                 out[w][k] = r[k]

@@ -96,6 +96,10 @@ def fast():
         F.cpf_mul_mat.argtypes, F.cpf_mul_mat.restype = [P, P, P, ctypes.c_int], ctypes.c_int
         F.cpf_have_avx2.argtypes, F.cpf_have_avx2.restype = [], ctypes.c_int
         F.cpf_q8_0_isa.argtypes, F.cpf_q8_0_isa.restype = [], ctypes.c_int
+        vp, i64 = ctypes.c_void_p, ctypes.c_int64
+        F.cpf_flash_attn_ext.argtypes = [vp, vp, vp, vp, vp, ctypes.c_int, i64, i64, i64, i64, ctypes.c_float,
+                                         ctypes.c_int]
+        F.cpf_flash_attn_ext.restype = ctypes.c_int
         _fast = F
     return _fast
 
@@ -366,6 +370,26 @@ def cpu_fast_mul_mat(wtype: int, w: np.ndarray, x: np.ndarray, nthreads: int) ->
     if rc != 0:
         raise ValueError(f"cpf_mul_mat rc={rc}")
     return y
+
+
+def cpu_fast_flash_attn_ext(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask, scale: float,
+                            nthreads: int) -> np.ndarray:
+    """The F16C multi-threaded port of ggml-cpu's flash attention over f16 K / V (the layouts of flash_attn_ext)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    n_head, n_q, D = q.shape
+    n_kv_head, n_kv, _ = k.shape
+    out = np.zeros((n_q, n_head, D), np.float32)
+    mp = None
+    if mask is not None:
+        mask = np.ascontiguousarray(mask, dtype=np.uint16)
+        mp = _p(mask)
+    rc = fast().cpf_flash_attn_ext(_p(q), _p(k), _p(v), mp, _p(out), D, n_q, n_head, n_kv, n_kv_head, scale,
+                                   int(nthreads))
+    if rc != 0:
+        raise ValueError(f"cpf_flash_attn_ext rc={rc}")
+    return out
 
 
 def physical_cores() -> int:

@@ -191,3 +191,73 @@ int cpf_mul_mat(const orc_tensor *src0, const orc_tensor *src1, orc_tensor *dst,
     free(wq);
     return 0;
 }
+
+/* ggml_compute_forward_flash_attn_ext_f16 for F16 K / V as ggml-cpu runs it: the (q row, head) pairs split across
+ * threads; per pair q rounded to fp16, each score an F16C dot of the key row with q summed in fp32
+ * (ggml_vec_dot_f16), the online softmax, and the V accumulator kept in fp16 (ggml_vec_scale_f16 / ggml_vec_mad_f16:
+ * converted to fp32, scaled or multiply-added, converted back, eight channels at a time). Layouts as
+ * orc_flash_attn_ext: q [n_head][n_q][D], k, v [n_kv_head][n_kv][D], mask [n_q][n_kv] f16, dst [n_q][n_head][D].
+ * D a multiple of 8. Returns 0 on success. */
+AVX2 static float dot_f16_row(const uint16_t *a, const uint16_t *b, int D) {
+    __m256 acc = _mm256_setzero_ps();
+    for (int d = 0; d < D; d += 8) {
+        const __m256 x = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(a + d)));
+        const __m256 y = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(b + d)));
+        acc = _mm256_fmadd_ps(x, y, acc);
+    }
+    return hsum8(acc);
+}
+
+AVX2 static void fa_pair(const float *qr, const uint16_t *k, const uint16_t *v, const uint16_t *mr, float *out, int D,
+                         int64_t n_kv, float scale, uint16_t *qh, uint16_t *acc) {
+    for (int d = 0; d < D; d += 8)
+        _mm_storeu_si128((__m128i *)(qh + d), _mm256_cvtps_ph(_mm256_loadu_ps(qr + d), _MM_FROUND_TO_NEAREST_INT));
+    for (int d = 0; d < D; d++) acc[d] = 0;
+    float S = 0.0f, M = -INFINITY;
+    for (int64_t j = 0; j < n_kv; j++) {
+        const float mv = mr ? _cvtsh_ss(mr[j]) : 0.0f;
+        if (mv == -INFINITY) continue;
+        const float s = dot_f16_row(k + j * D, qh, D) * scale + mv;
+        float ms = 1.0f, vs = 1.0f;
+        if (s > M) {
+            const float Mold = M;
+            M = s;
+            ms = expf(Mold - M);
+            const __m256 f = _mm256_set1_ps(ms);
+            for (int d = 0; d < D; d += 8) {
+                const __m256 a = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(acc + d)));
+                _mm_storeu_si128((__m128i *)(acc + d), _mm256_cvtps_ph(_mm256_mul_ps(a, f), _MM_FROUND_TO_NEAREST_INT));
+            }
+        } else {
+            vs = expf(s - M);
+        }
+        const __m256 f = _mm256_set1_ps(vs);
+        const uint16_t *vr = v + j * D;
+        for (int d = 0; d < D; d += 8) {
+            const __m256 a = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(acc + d)));
+            const __m256 x = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(vr + d)));
+            _mm_storeu_si128((__m128i *)(acc + d), _mm256_cvtps_ph(_mm256_fmadd_ps(x, f, a), _MM_FROUND_TO_NEAREST_INT));
+        }
+        S = S * ms + vs;
+    }
+    const float inv = S == 0.0f ? 0.0f : 1.0f / S;
+    for (int d = 0; d < D; d++) out[d] = _cvtsh_ss(acc[d]) * inv;
+}
+
+int cpf_flash_attn_ext(const float *q, const uint16_t *k, const uint16_t *v, const uint16_t *mask, float *dst, int D,
+                       int64_t n_q, int64_t n_head, int64_t n_kv, int64_t n_kv_head, float scale, int nthreads) {
+    if (!cpf_have_avx2()) return -3;
+    if (n_kv_head < 1 || n_head % n_kv_head != 0 || D % 8 != 0 || D > 1024) return -1;
+    const int64_t g = n_head / n_kv_head;
+#pragma omp parallel num_threads(nthreads)
+    {
+        uint16_t qh[1024], acc[1024];
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t p = 0; p < n_q * n_head; p++) {
+            const int64_t i = p / n_head, h = p % n_head, hk = h / g;
+            fa_pair(q + (h * n_q + i) * D, k + hk * n_kv * D, v + hk * n_kv * D, mask ? mask + i * n_kv : NULL,
+                    dst + (i * n_head + h) * D, D, n_kv, scale, qh, acc);
+        }
+    }
+    return 0;
+}

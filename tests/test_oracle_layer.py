@@ -138,6 +138,19 @@ def test_flash_attn_against_float64(n_head, n_kv_head, n_q, n_kv, D, past):
     assert np.abs(cpu - ref).max() <= 1e-2 * np.abs(ref).max()
 
 
+@pytest.mark.parametrize("threads", [1, 4])
+def test_cpu_port_flash_attn_against_float64(threads):
+    """The multi-threaded F16C port timed as the whole decode step's CPU baseline (fp16 V accumulator, as ggml-cpu)
+    holds the oracle's bar against the float64 attention, at the decode step's shape (16 q heads over 8 kv heads, one
+    row, 1025 of 1088 positions visible) and with several rows."""
+    for n_head, n_kv_head, n_q, n_kv, D, past in ((16, 8, 1, 1088, 128, 1024), (4, 2, 9, 64, 64, 40)):
+        q, k, v, mask = fa_case(41 + n_q, n_head, n_kv_head, n_q, n_kv, D, past)
+        ref = attn_numpy(q, k, v, mask, 1.0 / np.sqrt(D))
+        got = O.cpu_fast_flash_attn_ext(q, k, v, mask, 1.0 / np.sqrt(D), threads)
+        assert np.abs(got - ref).max() <= 1e-2 * np.abs(ref).max()
+        assert np.abs(got - O.flash_attn_ext(q, k, v, mask, 1.0 / np.sqrt(D))).max() <= 1e-2 * np.abs(ref).max()
+
+
 def test_flash_attn_closed_forms():
     D = 64
     q, k, v, _ = fa_case(21, 2, 1, 2, 64, D)
