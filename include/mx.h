@@ -282,48 +282,6 @@ typedef struct mx_fusion {
 MX_API int mx_mul_mat_fused(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
                             const mx_tensor *const *dst, const mx_fusion *f);
 
-/* ---------------------------------------------------------------------------------------------------------------
- * One decode step of a Qwen3 decoder in one launch: no single ggml op. The whole of Qwen3Decoder::step
- * (src/common/qwen3-decoder.cpp:462-490) for one token with flash attention: GET_ROWS of the token from tok_embd, the
- * layers of Qwen3Decoder::layers (:350-410: RMS_NORM x attn_norm, q/k/v, q/k head norms, NEOX RoPE at pos, SET_ROWS of
- * the new key and value into the caches at row pos, flash attention over cache rows 0..pos with scale 1/sqrt(128) and
- * fp32 accumulation, attn_o + residual, RMS_NORM x ffn_norm, gate/up, SwiGLU, down + residual) and the outputs of
- * ::outputs (:422-438: RMS_NORM x out_norm, the output head into logits, ARGMAX into pick, the first of equal values),
- * each value as the separate entry points compute it (only the order of fp32 sums differs). For a caller that owns the
- * step, as Qwen3Decoder does with its kept TokenStep graph (:187-208): the token can be the previous step's pick, so
- * the step never waits on the host. Q8_0 weights, head size 128, 1, 2 or 4 q heads per kv head; f16 caches
- * [n_head_kv * 128, capacity] with contiguous rows. mx_decoder_new validates the model and holds its device tables
- * and the step's exchange buffers (MX_UNSUPPORTED for shapes the step kernel does not take: then the separate entry
- * points run the step). Steps on one decoder must not overlap (one stream). A timeout inside the step (its workgroups
- * not all resident) is reported by mx_backend_synchronize as MX_FAILED.
- * ------------------------------------------------------------------------------------------------------------- */
-typedef struct mx_qwen3_layer {
-    const mx_tensor *attn_norm;             /* F32 [n_embd] */
-    const mx_tensor *wq, *wk, *wv;          /* Q8_0 [n_embd, n_head * 128], [n_embd, n_head_kv * 128] x 2 */
-    const mx_tensor *q_norm, *k_norm;       /* F32 [128] */
-    const mx_tensor *wo;                    /* Q8_0 [n_head * 128, n_embd] */
-    const mx_tensor *ffn_norm;              /* F32 [n_embd] */
-    const mx_tensor *w_gate, *w_up;         /* Q8_0 [n_embd, n_ff] */
-    const mx_tensor *w_down;                /* Q8_0 [n_ff, n_embd] */
-    const mx_tensor *k_cache, *v_cache;     /* F16 [n_head_kv * 128, capacity] */
-} mx_qwen3_layer;
-
-typedef struct mx_qwen3 {
-    int32_t n_layer, n_head, n_head_kv;     /* head size 128 */
-    float rms_eps, rope_base, rope_freq_scale;
-    const mx_tensor *tok_embd;              /* Q8_0 [n_embd, n_vocab] */
-    const mx_tensor *out_norm;              /* F32 [n_embd] */
-    const mx_tensor *output;                /* Q8_0 [n_embd, n_vocab]; tok_embd when tied */
-    const mx_qwen3_layer *layers;           /* n_layer of them */
-} mx_qwen3;
-
-typedef struct mx_decoder mx_decoder;
-MX_API mx_decoder *mx_decoder_new(mx_backend *be, const mx_qwen3 *m);
-MX_API void mx_decoder_free(mx_decoder *d);
-/* token, pos: I32 [1] (device memory; token may be the pick of the previous step); logits F32 [n_vocab]; pick I32 [1]. */
-MX_API int mx_decoder_step(mx_decoder *d, const mx_tensor *token, const mx_tensor *pos, const mx_tensor *logits,
-                           const mx_tensor *pick);
-
 /* Several MUL_MAT nodes that read the same src1 (q/k/v, or gate/up) in one launch, as a backend's graph_compute
  * may fuse them. Each dst[i] = src0[i] x src1, exactly as n separate mx_mul_mat calls compute it. */
 MX_API int mx_mul_mat_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,

@@ -48,8 +48,7 @@ EXPORTS = [
     "mx_gguf_find_tensor", "mx_gguf_n_keys", "mx_gguf_key", "mx_gguf_find_key", "mx_gguf_key_type", "mx_gguf_get_str",
     "mx_gguf_get_int", "mx_gguf_get_float", "mx_gguf_get_arr", "mx_gguf_get_arr_str", "mx_gguf_load_tensor",
     "mx_rms_norm", "mx_binary", "mx_swiglu", "mx_supports_rope", "mx_rope", "mx_set_rows", "mx_supports_flash_attn_ext",
-    "mx_flash_attn_ext", "mx_mul_mat_fused", "mx_qk_norm_rope_kv", "mx_attn_decode", "mx_decoder_new", "mx_decoder_free",
-    "mx_decoder_step", "mx_graph_nodes", "mx_mul_mat_id_noalloc", "mx_mul_mat_id_noalloc_bytes", "mx_peak_read", "mx_peak_mfma",
+    "mx_flash_attn_ext", "mx_mul_mat_fused", "mx_qk_norm_rope_kv", "mx_attn_decode", "mx_graph_nodes", "mx_mul_mat_id_noalloc", "mx_mul_mat_id_noalloc_bytes", "mx_peak_read", "mx_peak_mfma",
 ]
 NOALLOC_SCRATCH_BYTES = 16 << 20  # MX_NOALLOC_SCRATCH_BYTES
 
@@ -69,17 +68,6 @@ class MxFusion(ctypes.Structure):
 
 
 _P = ctypes.POINTER(MxTensor)
-
-
-class MxQwen3Layer(ctypes.Structure):
-    _fields_ = [(n, _P) for n in ("attn_norm", "wq", "wk", "wv", "q_norm", "k_norm", "wo", "ffn_norm", "w_gate", "w_up",
-                                  "w_down", "k_cache", "v_cache")]
-
-
-class MxQwen3(ctypes.Structure):
-    _fields_ = [("n_layer", ctypes.c_int32), ("n_head", ctypes.c_int32), ("n_head_kv", ctypes.c_int32),
-                ("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float), ("rope_freq_scale", ctypes.c_float),
-                ("tok_embd", _P), ("out_norm", _P), ("output", _P), ("layers", ctypes.POINTER(MxQwen3Layer))]
 
 
 class GgufTensorInfo(ctypes.Structure):
@@ -186,9 +174,6 @@ def lib():
         "mx_mul_mat_fused": ([vp, i32, ctypes.POINTER(P), P, ctypes.POINTER(P), ctypes.POINTER(MxFusion)], i32),
         "mx_qk_norm_rope_kv": ([vp, P, P, P, P, P, P, P, P, P, f32, i32, i32, f32, f32, f32, f32], i32),
         "mx_attn_decode": ([vp, P, P, P, P, P, P, P, P, P, P, P, P, f32, i32, i32, f32, f32, f32, f32, f32], i32),
-        "mx_decoder_new": ([vp, ctypes.POINTER(MxQwen3)], vp),
-        "mx_decoder_free": ([vp], None),
-        "mx_decoder_step": ([vp, P, P, P, P], i32),
         "mx_graph_nodes": ([vp], sz),
         "mx_mul_mat_id_noalloc": ([vp, P, P, P, P], i32),
         "mx_mul_mat_id_noalloc_bytes": ([P, P, P], sz),
@@ -481,12 +466,6 @@ class Backend:
         r = lambda t: t.ref() if t is not None else None  # noqa: E731
         return bool(lib().mx_supports_op(op, r(src0), r(src1), r(src2), r(dst)))
 
-    def decoder(self, layers, tok_embd, out_norm, output, n_head: int, n_head_kv: int, eps: float, rope_base: float,
-                rope_freq_scale: float = 1.0) -> "Decoder":
-        """A Qwen3 decoder for the one-launch decode step (mx_decoder_new). layers: dicts of Tensors keyed by
-        mx_qwen3_layer's field names."""
-        return Decoder(self, layers, tok_embd, out_norm, output, n_head, n_head_kv, eps, rope_base, rope_freq_scale)
-
     # graphs and events
     def graph_begin(self) -> None:
         check(lib().mx_graph_begin(self.h))
@@ -525,43 +504,6 @@ class Backend:
     @staticmethod
     def event_free(e) -> None:
         lib().mx_event_free(ctypes.c_void_p(e))
-
-
-class Decoder:
-    """mx_decoder: a validated Qwen3 model on a backend, stepped one token per launch (mx_decoder_step). Holds the
-    Tensors it was built from, whose device memory the step reads."""
-
-    def __init__(self, be, layers, tok_embd, out_norm, output, n_head, n_head_kv, eps, rope_base, rope_freq_scale):
-        self.be = be
-        self._keep = [layers, tok_embd, out_norm, output]
-        self._layers = (MxQwen3Layer * len(layers))()
-        for i, d in enumerate(layers):
-            for name, _ in MxQwen3Layer._fields_:
-                setattr(self._layers[i], name, ctypes.pointer(d[name].desc))
-        m = MxQwen3()
-        m.n_layer, m.n_head, m.n_head_kv = len(layers), n_head, n_head_kv
-        m.rms_eps, m.rope_base, m.rope_freq_scale = eps, rope_base, rope_freq_scale
-        m.tok_embd, m.out_norm, m.output = (ctypes.pointer(tok_embd.desc), ctypes.pointer(out_norm.desc),
-                                            ctypes.pointer(output.desc))
-        m.layers = self._layers
-        self.h = lib().mx_decoder_new(be.h, ctypes.byref(m))
-        if not self.h:
-            msg = lib().mx_last_error().decode(errors="replace")
-            raise MxError(UNSUPPORTED if "decode step:" in msg else FAILED, msg)
-
-    def step(self, token, pos, logits, pick) -> None:
-        check(lib().mx_decoder_step(self.h, token.ref(), pos.ref(), logits.ref(), pick.ref()))
-
-    def free(self) -> None:
-        if self.h:
-            lib().mx_decoder_free(self.h)
-            self.h = None
-
-    def __del__(self):
-        try:
-            self.free()
-        except Exception:
-            pass
 
 
 def device_count() -> int:

@@ -43,15 +43,6 @@ struct mx_event {
     hipEvent_t ev = nullptr;
 };
 
-struct mx_decoder {
-    mx_backend *be = nullptr;
-    mx::DecArgs args{};
-    mx::DecLayer *layers = nullptr;  // device table
-    uint64_t *ll = nullptr;          // exchange words
-    uint32_t *epoch = nullptr;
-    int grid = 0;
-};
-
 namespace {
 
 thread_local std::string g_error;
@@ -386,9 +377,6 @@ MX_API int mx_backend_synchronize(mx_backend *be) {
     if (flag) {
         const int zero = 0;
         HIP_OK(hipMemcpy(be->err, &zero, sizeof zero, hipMemcpyHostToDevice), "clear error word");
-        if (flag & 8)
-            return fail(MX_FAILED, "a decode step's workgroup waited past its limit for a phase's input (the step's "
-                                   "workgroups were not all resident on the device); the step's outputs are not valid");
         return fail(MX_INVALID, "%s%s%s", (flag & 1) ? "GET_ROWS met a row index out of range; its rows are zero. " : "",
                     (flag & 2) ? "MUL_MAT_ID met an expert index out of range; its pairs were skipped. " : "",
                     (flag & 4) ? "SET_ROWS met a row index out of range; those rows were not written." : "");
@@ -1310,175 +1298,6 @@ MX_API int mx_quantize_act(mx_backend *be, int type, int rounding, const float *
     if ((type == MX_TYPE_Q8_K) && ((uintptr_t)out & 3)) return fail(MX_INVALID, "Q8_K output must be 4-byte aligned");
     HIP_OK(mx::launch_quantize_act(type, rounding, x, k, nrows, (int64_t)(x_row_stride / 4), out, be->stream),
            "quantize launch");
-    return MX_SUCCESS;
-}
-
-// ------------------------------------------------------------------------------------------------ decode step
-static bool q8_matrix(const mx_tensor *t, int64_t K, int64_t N) {
-    return weight_ok(t) && t->type == MX_TYPE_Q8_0 && t->ne[0] == K && t->ne[1] == N && t->ne[2] == 1 && t->ne[3] == 1;
-}
-static bool f32_vec(const mx_tensor *t, int64_t n) {
-    return t && t->type == MX_TYPE_F32 && contiguous(t) && nelements(t) == n && t->data && aligned16(t->data);
-}
-
-// The one-launch step's first run on MI355X ended in a GPU fault whose cause is not found (its address arithmetic
-// checks clean on the CPU); until it is, the step is refused here and callers run the separate entry points.
-constexpr bool kDecodeStepEnabled = false;
-
-MX_API mx_decoder *mx_decoder_new(mx_backend *be, const mx_qwen3 *m) {
-    auto refuse = [](int code, const char *why) -> mx_decoder * {
-        fail(code, "decode step: %s", why);
-        return nullptr;
-    };
-    if (check_be(be)) return nullptr;
-    if (!kDecodeStepEnabled)
-        return refuse(MX_UNSUPPORTED, "switched off: its first run faulted the GPU and the cause is not found; "
-                                      "run the step with the separate entry points");
-    if (!m || !m->layers || !m->tok_embd || !m->out_norm || !m->output) return refuse(MX_INVALID, "null model fields");
-    const int L = m->n_layer, nq = m->n_head, nkv = m->n_head_kv;
-    if (L < 1 || L > 170) return refuse(MX_UNSUPPORTED, "1 to 170 layers");
-    if (nq < 1 || nkv < 1 || nq % nkv != 0) return refuse(MX_INVALID, "n_head must be a multiple of n_head_kv");
-    const int gqa = nq / nkv;
-    if (gqa != 1 && gqa != 2 && gqa != 4) return refuse(MX_UNSUPPORTED, "1, 2 or 4 q heads per kv head");
-    const int64_t H = m->tok_embd->ne[0], V = m->tok_embd->ne[1], Q = (int64_t)nq * 128, KV = (int64_t)nkv * 128;
-    const mx_qwen3_layer &l0 = m->layers[0];
-    if (!l0.w_gate) return refuse(MX_INVALID, "null layer tensors");
-    const int64_t F = l0.w_gate->ne[1];
-    if (H % 1024 != 0 || H > mx::DEC_KMAX || Q % 256 != 0 || Q > mx::DEC_KMAX || F % 256 != 0 || F > mx::DEC_KMAX ||
-        V < 1 || V >= ((int64_t)1 << 30))
-        return refuse(MX_UNSUPPORTED, "n_embd a multiple of 1024, q width and n_ff multiples of 256, all up to 4096");
-    if (!q8_matrix(m->tok_embd, H, V) || !q8_matrix(m->output, H, V) || !f32_vec(m->out_norm, H))
-        return refuse(MX_UNSUPPORTED, "Q8_0 token embedding and output head [n_embd, n_vocab], F32 out_norm");
-    int64_t cap = -1;
-    for (int l = 0; l < L; l++) {
-        const mx_qwen3_layer &y = m->layers[l];
-        if (!q8_matrix(y.wq, H, Q) || !q8_matrix(y.wk, H, KV) || !q8_matrix(y.wv, H, KV) || !q8_matrix(y.wo, Q, H) ||
-            !q8_matrix(y.w_gate, H, F) || !q8_matrix(y.w_up, H, F) || !q8_matrix(y.w_down, F, H))
-            return refuse(MX_UNSUPPORTED, "every layer's products Q8_0 of the model's shapes");
-        if (!f32_vec(y.attn_norm, H) || !f32_vec(y.ffn_norm, H) || !f32_vec(y.q_norm, 128) || !f32_vec(y.k_norm, 128))
-            return refuse(MX_UNSUPPORTED, "F32 norm weights, 16-byte aligned");
-        for (const mx_tensor *c : {y.k_cache, y.v_cache}) {
-            if (!c || c->type != MX_TYPE_F16 || !contiguous(c) || c->ne[0] != KV || c->ne[2] != 1 || c->ne[3] != 1 ||
-                !c->data || !aligned16(c->data))
-                return refuse(MX_UNSUPPORTED, "F16 caches [n_head_kv * 128, capacity] with contiguous rows");
-            if (cap < 0) cap = c->ne[1];
-            if (c->ne[1] != cap) return refuse(MX_UNSUPPORTED, "every cache of the same capacity");
-        }
-    }
-    hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, be->device) != hipSuccess) return refuse(MX_FAILED, "device properties");
-    const int G = prop.multiProcessorCount;
-    if (G < nkv || G > mx::DEC_THREADS) return refuse(MX_UNSUPPORTED, "the device's CU count against the kv heads");
-    mx::DecArgs a{};
-    a.n_layer = L;
-    a.H = (int)H;
-    a.nq = nq;
-    a.nkv = nkv;
-    a.gqa = gqa;
-    a.F = (int)F;
-    a.V = (int)V;
-    a.Q = (int)Q;
-    a.KV = (int)KV;
-    a.S = std::min(64, G / nkv);
-    auto per = [&](int64_t n) { return (int)((n + G - 1) / G); };
-    a.r_qkv = per(Q + 2 * KV);
-    a.r_o = per(H);
-    a.r_f = per(F);
-    a.r_d = per(H);
-    a.r_m = per(Q);
-    a.r_v = per(V);
-    const bool fits = (int64_t)a.r_qkv * (H + H / 16) <= mx::DEC_SLOT && (int64_t)a.r_o * (Q + Q / 16) <= mx::DEC_SLOT &&
-                      (int64_t)2 * a.r_f * (H + H / 16) <= mx::DEC_SLOT && (int64_t)a.r_d * (F + F / 16) <= mx::DEC_SLOT &&
-                      a.r_o <= 32 && a.r_d <= 32 && a.r_m <= 8 && 128 % a.r_m == 0;
-    if (!fits) return refuse(MX_UNSUPPORTED, "a phase's rows per CU exceed the step's LDS slots");
-    a.cache_rows = cap;
-    a.eps = m->rms_eps;
-    a.theta_scale = powf(m->rope_base, -2.0f / 128.0f);  // as ggml-cpu forms it
-    a.freq_scale = m->rope_freq_scale;
-    a.scale = 1.0f / std::sqrt(128.0f);                  // 1 / sqrt(head_dim), qwen3-decoder.cpp:386
-    a.spin_limit = 200000;
-    auto q8 = [](const mx_tensor *t) {
-        const mx::WPlanes w = mx::wplanes(t->data, mx::planes_of(t->type, nelements(t)));
-        return mx::Q8p{w.p0, w.p1};
-    };
-    a.emb = q8(m->tok_embd);
-    a.out = q8(m->output);
-    a.out_norm = (const float *)m->out_norm->data;
-
-    std::unique_ptr<mx_decoder> d(new mx_decoder());
-    d->be = be;
-    d->grid = G;
-    std::vector<mx::DecLayer> host(L);
-    for (int l = 0; l < L; l++) {
-        const mx_qwen3_layer &y = m->layers[l];
-        mx::DecLayer &h = host[l];
-        h.wq = q8(y.wq);
-        h.wk = q8(y.wk);
-        h.wv = q8(y.wv);
-        h.wo = q8(y.wo);
-        h.wg = q8(y.w_gate);
-        h.wu = q8(y.w_up);
-        h.wd = q8(y.w_down);
-        h.attn_norm = (const float *)y.attn_norm->data;
-        h.ffn_norm = (const float *)y.ffn_norm->data;
-        h.q_norm = (const float *)y.q_norm->data;
-        h.k_norm = (const float *)y.k_norm->data;
-        h.kc = (uint16_t *)y.k_cache->data;
-        h.vc = (uint16_t *)y.v_cache->data;
-    }
-    const size_t words = mx::decode_ll_words(a, G);
-    bool ok = hipMalloc(&d->layers, sizeof(mx::DecLayer) * L) == hipSuccess &&
-              hipMalloc(&d->ll, words * 8) == hipSuccess && hipMalloc(&d->epoch, 256) == hipSuccess &&
-              hipMemcpy(d->layers, host.data(), sizeof(mx::DecLayer) * L, hipMemcpyHostToDevice) == hipSuccess &&
-              hipMemset(d->ll, 0, words * 8) == hipSuccess && hipMemset(d->epoch, 0, 256) == hipSuccess &&
-              hipDeviceSynchronize() == hipSuccess;
-    if (!ok) {
-        mx_decoder_free(d.release());
-        return refuse(MX_ALLOC_FAILED, "cannot allocate the step's tables and exchange buffers");
-    }
-    a.layers = d->layers;
-    a.ll = d->ll;
-    a.epoch = d->epoch;
-    a.err = be->err;
-    d->args = a;
-    return d.release();
-}
-
-MX_API void mx_decoder_free(mx_decoder *d) {
-    if (!d) return;
-    if (d->be) {
-        (void)hipSetDevice(d->be->device);
-        (void)hipStreamSynchronize(d->be->stream);
-    }
-    if (d->layers) (void)hipFree(d->layers);
-    if (d->ll) (void)hipFree(d->ll);
-    if (d->epoch) (void)hipFree(d->epoch);
-    delete d;
-}
-
-MX_API int mx_decoder_step(mx_decoder *d, const mx_tensor *token, const mx_tensor *pos, const mx_tensor *logits,
-                           const mx_tensor *pick) {
-    if (!d) return fail(MX_INVALID, "null decoder");
-    mx_backend *be = d->be;
-    int rc = check_be(be);
-    if (rc) return rc;
-    auto i32 = [](const mx_tensor *t) {
-        return t && t->type == MX_TYPE_I32 && t->data && ((uintptr_t)t->data & 3) == 0 && nelements(t) >= 1;
-    };
-    if (!i32(token) || !i32(pos) || !i32(pick)) return fail(MX_INVALID, "decode step: token, pos and pick are I32 [1]");
-    if (!logits || logits->type != MX_TYPE_F32 || !contiguous(logits) || nelements(logits) < d->args.V ||
-        !logits->data || ((uintptr_t)logits->data & 3))
-        return fail(MX_INVALID, "decode step: logits F32 [n_vocab], contiguous");
-    mx::DecArgs a = d->args;
-    a.token = (const int32_t *)token->data;
-    a.pos = (const int32_t *)pos->data;
-    a.logits = (float *)logits->data;
-    a.pick = (int32_t *)pick->data;
-    a.rounding = be->rounding;
-    // eager: a cooperative launch (every workgroup resident, or the launch fails); recorded into a graph: a plain one
-    // (the grid is one workgroup per CU with most of a CU's LDS, so the workgroups are resident all the same, and the
-    // step's waits are bounded if they were not)
-    HIP_OK(mx::launch_decode_step(a, d->grid, !be->capturing, be->stream), "decode step launch");
     return MX_SUCCESS;
 }
 

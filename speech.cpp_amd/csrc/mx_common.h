@@ -343,45 +343,6 @@ hipError_t launch_peak_mfma(int kind, int workgroups, int iters, int *sink, hipS
 hipError_t launch_argmax(const float *src, int64_t ne0, int64_t nrows, int64_t nb1, int32_t *dst, int64_t dst_nb0,
                          void *scratch, hipStream_t s);
 
-// ------------------------------------------------------------------------------------------------------------------
-// One decode step of a Qwen3 decoder in one persistent launch (decode.hip): one workgroup per CU, the dependent phases
-// of a layer exchanged through tagged words in `ll`. Weights Q8_0 in the planar layout (p0 codes, p1 fp16 scales).
-// ------------------------------------------------------------------------------------------------------------------
-struct Q8p {
-    const uint8_t *q, *d;  // codes plane, fp16 scales plane
-};
-struct DecLayer {
-    Q8p wq, wk, wv, wo, wg, wu, wd;
-    const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
-    uint16_t *kc, *vc;  // f16 caches: position j's row at kc + j * kv_dim (kv head h at channel 128 h)
-};
-struct DecArgs {
-    const DecLayer *layers;
-    int n_layer, H, nq, nkv, gqa, F, V;     // head size 128
-    int Q, KV;                               // nq * 128, nkv * 128
-    int S;                                   // attention splits per kv head (S * nkv workgroups attend)
-    int r_qkv, r_o, r_f, r_d, r_m, r_v;      // rows per workgroup: q/k/v, attn_o, gate/up pairs, down, merge, head
-    Q8p emb, out;                            // token embedding (GET_ROWS) and the output head (may be the same)
-    const float *out_norm;
-    const int32_t *token, *pos;
-    float *logits;
-    int32_t *pick;
-    int64_t cache_rows;
-    float eps, theta_scale, freq_scale, scale;
-    int rounding;
-    uint64_t *ll;                            // exchange words (ll_words of them, zeroed once)
-    uint32_t *epoch;                         // step counter: tags of this step's words
-    int *err;
-    int spin_limit;
-};
-constexpr int DEC_THREADS = 512;
-constexpr int DEC_SLOT = 32 * 1024;          // bytes of one weight slot in LDS (three of them)
-constexpr int DEC_KMAX = 4096;               // longest product input the step's LDS holds
-constexpr int DEC_HMAX = 4096;
-size_t decode_lds_bytes();
-size_t decode_ll_words(const DecArgs &a, int grid);
-hipError_t launch_decode_step(const DecArgs &a, int grid, bool cooperative, hipStream_t s);
-
 // Pairs per chunk of one expert's (token, slot) pairs: two 16-row MFMA tiles that share each expanded weight fragment,
 // or one tile (few pairs per expert: no second tile's operands to stage, and a lighter kernel form).
 constexpr int MMID_CHUNK = 32, MMID_CHUNK_SMALL = 16;

@@ -1,5 +1,5 @@
-// Device helpers shared by the decoder-layer kernels (layer.hip) and the one-launch decode step (decode.hip): wave64
-// reductions and the per-head q / k norm + NEOX RoPE of head size 128. Include after `#pragma clang fp contract(off)`:
+// Device helpers of the decoder-layer kernels (layer.hip): wave64 reductions and the per-head q / k norm + NEOX RoPE
+// of head size 128. Include after `#pragma clang fp contract(off)`:
 // these expressions must round exactly as ggml-cpu forms them (no fused multiply-adds unless written as fmaf).
 #pragma once
 

@@ -1,4 +1,6 @@
-"""The one-launch decode step (mx_decoder_new / mx_decoder_step: Qwen3Decoder::step as one persistent launch) against
+"""Skipped: the one-launch decode step these tests held (mx_decoder_new / mx_decoder_step: Qwen3Decoder::step as one
+persistent launch) was taken out of the library after its first GPU run faulted with no cause shown. They checked it
+against
 the oracle's chain of the same ops (GET_ROWS, per layer RMS_NORM x weight, q/k/v, q/k norms, NEOX RoPE, SET_ROWS into
 the f16 caches, exact flash attention over positions 0..p, attn_o + residual, RMS_NORM, gate/up, SwiGLU, down +
 residual; final norm, output head, ARGMAX), on the 0.6B shape's layers (hidden 1024, 16 q / 8 kv heads of 128, FFN
@@ -11,8 +13,8 @@ import pytest
 import oracle as O
 
 pytestmark = [pytest.mark.gpu,
-              pytest.mark.skip(reason="the one-launch decode step is switched off: its first run faulted the GPU and "
-                                      "the cause is not found (mx_decoder_new refuses it)")]
+              pytest.mark.skip(reason="the one-launch decode step was taken out of the library: its first run faulted "
+                                      "the GPU and the cause was not found")]
 
 Q8 = O.TYPE_Q8_0
 H, F, NQ, NKV, HD, V, EPS, THETA = 1024, 3072, 16, 8, 128, 5000, 1e-6, 1e6
