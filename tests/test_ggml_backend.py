@@ -161,6 +161,32 @@ def test_plan_of_a_split_keeps_what_a_later_split_reads():
             g.close()
 
 
+def test_plan_of_a_decode_split_with_readers_beyond_it():
+    """A decode step whose intermediates a node after it reads (as a later split of a scheduled graph would): the
+    product a fusion would leave unwritten (layer 0's down product before its residual ADD, layer 1's q/k/v group's
+    norm x weight) is then computed as its own node in the step's split, counted over the whole graph; the other
+    layers' fusions stay."""
+    base = G.Qwen3Step(2, 1024, 2048, 8, 4, 128, 1000, 256, 1, 128)
+    st = G.Qwen3Step(2, 1024, 2048, 8, 4, 128, 1000, 256, 1, 128)
+    try:
+        n = st.g.h.ggml_graph_n_nodes(st.g.graph)
+        extra = st.g.add(st.taps[0]["dn"], st.taps[0]["dn"])  # a later reader of layer 0's down product
+        extra2 = st.g.mul(st.taps[1]["h"], st.taps[1]["h"])  # and of layer 1's attention norm x weight
+        st.g.h.ggml_set_output(extra)
+        st.g.h.ggml_set_output(extra2)
+        st.g.expand(extra)
+        st.g.expand(extra2)
+        assert st.g.h.ggml_graph_n_nodes(st.g.graph) == n + 2
+        want = [k for k, _ in G.plan(base.g)]
+        got = [k for k, _ in G.plan(st.g.view(0, n))]  # the step's own nodes, as one split
+        assert want.count("product_out") == 4 and got.count("product_out") == 3
+        assert want.count("norm_products") == 5 and got.count("norm_products") == 4
+        assert got.count("attention") == want.count("attention") == 2
+    finally:
+        st.close()
+        base.close()
+
+
 # --------------------------------------------------------------------------------------------- on MI355X
 @pytest.fixture(scope="module")
 def device():
