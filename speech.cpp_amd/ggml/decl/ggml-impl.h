@@ -60,8 +60,9 @@ struct ggml_cgraph {
     enum ggml_cgraph_eval_order order;
 };
 
-// Nodes [i0, i1) of a graph, sharing its use counts and hash set (what ggml_backend_sched computes a split as).
-GGML_API struct ggml_cgraph ggml_graph_view(struct ggml_cgraph *cgraph, int i0, int i1);
+// Nodes [i0, i1) of a graph, sharing its use counts and hash set (what ggml_backend_sched computes a split as). The
+// backend does not call it (ggml-base need not export it); the test host provides it.
+struct ggml_cgraph ggml_graph_view(struct ggml_cgraph *cgraph, int i0, int i1);
 
 // How many sources, over the whole graph the node came from, name node node_idx (0 for a tensor no node reads).
 static inline int ggml_node_get_use_count(const struct ggml_cgraph *cgraph, int node_idx) {
