@@ -51,6 +51,11 @@ typedef __attribute__((address_space(3))) void dq_lds;
 #define MX_DQ_HALF 1  // Q8_0 128 x 32 waves: the second half of a stage's A reads overlaps the first half's MFMAs
 #endif
 constexpr int DQ_KS = 64;  // K per stage
+#ifndef MX_DQ_SKINNY_WG
+// workgroups the 32 x 128 tile aims for, splitting K (M = 28, N = 2048, K = 6144: 16 splits 17.5 us, 24 splits 19.8;
+// the K = 2048 products of the same block move by under 1 % between 256 and 512)
+#define MX_DQ_SKINNY_WG 256
+#endif
 #ifndef MX_DQ_NS_DIRB
 #define MX_DQ_NS_DIRB 3  // ring stages of the direct-B (Q8_0) tiles: 76 KB at 128 x 128, two workgroups per CU
 #endif
@@ -937,8 +942,11 @@ struct DqPlan {
 // (few rows: a short prefill block), K is split so that about 512 workgroups stream the weights, each over at least
 // four stages (a backend's split option overrides it); the split's reduce pass costs more than it saves on the large
 // tiles. A forced tile the kernel lacks gives bm = 0 (refused by the launch).
-DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o) {
+DqPlan dq_plan(int type, int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o) {
     DqPlan pl{64, 64, 1, 0};
+    // Q8_0 with direct B also has a 32 x 128 tile of four 32 x 32 waves, for blocks of at most 32 rows (the last,
+    // short block of a prompt): half the activation rows of a 64-row tile, so half its fragment reads and MFMAs
+    const bool skinny_ok = type == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B && MX_DQ_Q8_WGM128 == 1;
     int64_t wg128 = 0;
     for (int i = 0; i < nprob; i++) {
         wg128 += (N[i] + 127) / 128;
@@ -953,9 +961,16 @@ DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K, const Options 
     // 1024, N = 2048: 35.0 against 40.0), a group of them 128 (the ASR q/k/v group of widths 2048 + 1024 + 1024 at
     // M = 512 is faster on 128 x 128)
     if (wg128 >= (nprob == 1 ? 192 : 128) || split128) pl.bm = pl.bn = 128;
+    if (skinny_ok && M <= 32) {
+        pl.bm = 32;
+        pl.bn = 128;
+    }
     if (o.tile_m || o.tile_n) {
         const int tm = o.tile_m, tn = o.tile_n;
-        if ((tm == 64 || tm == 128) && (tn == 64 || tn == 128) && !(tm == 64 && tn == 128)) {
+        if (skinny_ok && tm == 32 && tn == 128) {
+            pl.bm = 32;
+            pl.bn = 128;
+        } else if ((tm == 64 || tm == 128) && (tn == 64 || tn == 128) && !(tm == 64 && tn == 128)) {
             pl.bm = tm;
             pl.bn = tn;
         } else {
@@ -968,6 +983,7 @@ DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K, const Options 
     tiles *= (M + pl.bm - 1) / pl.bm;
     int64_t want = tiles < 256 && pl.bn == 64 ? (512 + tiles - 1) / tiles : 1;
     if (split128 && pl.bm == 128 && pl.bn == 128) want = (256 + tiles - 1) / tiles;
+    if (pl.bm == 32) want = (MX_DQ_SKINNY_WG + tiles - 1) / tiles;
     const int forced = o.split;
     if (forced > 0) want = forced;
     want = std::min<int64_t>(want, std::max<int64_t>(1, forced > 0 ? nst : nst / 4));
@@ -982,8 +998,8 @@ DqPlan dq_plan(int nprob, const int64_t *N, int64_t M, int64_t K, const Options 
 static size_t dq_rs_offset(int64_t M, int64_t K) { return (gemm_dq_act_bytes(M, K) + 255) / 256 * 256; }
 static size_t dq_ws_offset(int64_t M, int64_t K) { return dq_rs_offset(M, K) + ((size_t)M * 4 + 255) / 256 * 256; }
 
-size_t gemm_dq_scratch_bytes(int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o) {
-    const DqPlan pl = dq_plan(nprob, N, M, K, o);
+size_t gemm_dq_scratch_bytes(int type, int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o) {
+    const DqPlan pl = dq_plan(type, nprob, N, M, K, o);
     size_t b = dq_ws_offset(M, K);
     if (pl.nsplit > 1) b += (size_t)pl.nsplit * (size_t)M * (size_t)pl.ntot * 4;
     return b;
@@ -1025,7 +1041,9 @@ static hipError_t launch_dq_type(const DqArgs &a, const DqPlan &pl, int maxN, hi
     if constexpr (WT == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B && MX_DQ_Q8_WGM128 == 1) {
         // direct B: four waves of 128 x 32, so every B fragment is converted by one wave only
         if (pl.bm == 128 && pl.bn == 128) return launch_dq<WT, 128, 128, 1, 4>(a, maxN, s);
+        if (pl.bm == 32) return launch_dq<WT, 32, 128, 1, 4>(a, maxN, s);
     }
+    if (pl.bm == 32) return hipErrorInvalidValue;
     if (pl.bm == 128 && pl.bn == 128) return launch_dq<WT, 128, 128, 2, MX_DQ_WGN128>(a, maxN, s);
     if (pl.bm == 128) return launch_dq<WT, 128, 64, 4, 2>(a, maxN, s);
     return launch_dq<WT, 64, 64, 2, 2>(a, maxN, s);
@@ -1034,7 +1052,7 @@ static hipError_t launch_dq_type(const DqArgs &a, const DqPlan &pl, int maxN, hi
 hipError_t launch_gemm_dq(int type, int nprob, const WPlanes *w, const int64_t *N, float *const *y,
                           const int64_t *ldy, int64_t M, int64_t K, void *scratch, const Options &o, hipStream_t s) {
     if (nprob < 1 || nprob > 4 || !gemm_dq_supported(type, M, K)) return hipErrorInvalidValue;
-    const DqPlan pl = dq_plan(nprob, N, M, K, o);
+    const DqPlan pl = dq_plan(type, nprob, N, M, K, o);
     if (pl.bm == 0) return hipErrorInvalidValue;
     DqArgs a{};
     int64_t maxN = 0;

@@ -314,7 +314,7 @@ MX_API int mx_backend_set_option(mx_backend *be, int option, int64_t value) {
             return MX_SUCCESS;
         case MX_OPT_GEMM_TILE_M:
         case MX_OPT_GEMM_TILE_N:
-            if (!in({0, 64, 128})) break;
+            if (!in({0, 64, 128}) && !(option == MX_OPT_GEMM_TILE_M && value == 32)) break;
             (option == MX_OPT_GEMM_TILE_M ? o.tile_m : o.tile_n) = (int)value;
             return MX_SUCCESS;
         case MX_OPT_GEMM_SPLIT:
@@ -756,7 +756,7 @@ static int gemm_dq_group(mx_backend *be, int n, const mx_tensor *const *src0, co
     const int64_t K = w0->ne[0], M = src1->ne[1];
     int64_t Ns[4];
     for (int i = 0; i < n; i++) Ns[i] = src0[i]->ne[1];
-    int rc = ensure_scratch(be, mx::gemm_dq_scratch_bytes(n, Ns, M, K, be->opt));
+    int rc = ensure_scratch(be, mx::gemm_dq_scratch_bytes(w0->type, n, Ns, M, K, be->opt));
     if (rc) return rc;
     const int64_t r2 = src1->ne[2] / w0->ne[2], r3 = src1->ne[3] / w0->ne[3];
     for (int64_t i13 = 0; i13 < src1->ne[3]; i13++)

@@ -214,7 +214,7 @@ inline bool gemm_supported(int type, int64_t K) { return type == MX_TYPE_Q8_0 &&
 // gemm_dq_scratch_bytes is the scratch both need (for the tile and split `o` forces, or those picked).
 bool gemm_dq_supported(int type, int64_t M, int64_t K);
 size_t gemm_dq_act_bytes(int64_t M, int64_t K);
-size_t gemm_dq_scratch_bytes(int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o);
+size_t gemm_dq_scratch_bytes(int type, int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o);
 hipError_t launch_gemm_dq_act(int type, int rounding, const float *x, int64_t x_stride, int64_t M, int64_t K,
                               void *scratch, hipStream_t s);
 hipError_t launch_gemm_dq(int type, int nprob, const WPlanes *w, const int64_t *N, float *const *y,
