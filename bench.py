@@ -43,10 +43,11 @@ HBM_PEAK_GBPS = 8000.0
 INT8_PEAK_TOPS = 5000.0   # dense int8 MFMA, MI355X
 FP16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, MI355X
 
-Q8_0, Q4_K, Q6_K = 8, 12, 14
-BLCK = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
-TSIZE = {Q8_0: 34, Q4_K: 144, Q6_K: 210}
-NAME = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+BLCK = {Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+TSIZE = {Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+NAME = {Q8_0: "Q8_0", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
+TYPE_OF = {v: k for k, v in NAME.items()}
 
 
 def row_bytes(t: int, k: int) -> int:
@@ -948,13 +949,14 @@ def router_ids(T, seed):
 
 def run_moe(args, mx, be, threads):
     t0 = time.time()
+    WT = TYPE_OF[args.moe_weights]  # Q4_K as the configuration names it; the other types measure their own paths
     specs = [("gate", MOE_H, MOE_F), ("up", MOE_H, MOE_F), ("down", MOE_F, MOE_H)]
     host = {}
     for i, (name, K, N) in enumerate(specs):
-        host[name] = mx.quantize_normal(Q4_K, weight_seed(5, 0, i), MOE_E * N, K, 0.02, nthreads=threads)
-    layers = [{name: be.tensor(Q4_K, (K, N, MOE_E), host[name]) for name, K, N in specs} for _ in range(MOE_LAYERS)]
+        host[name] = mx.quantize_normal(WT, weight_seed(5, 0, i), MOE_E * N, K, 0.02, nthreads=threads)
+    layers = [{name: be.tensor(WT, (K, N, MOE_E), host[name]) for name, K, N in specs} for _ in range(MOE_LAYERS)]
     log(f"expert weights generated and uploaded ({MOE_LAYERS} layer copies) in {time.time() - t0:.1f} s")
-    per_expert = sum(row_bytes(Q4_K, K) * N for _, K, N in specs)
+    per_expert = sum(row_bytes(WT, K) * N for _, K, N in specs)
     per_batch, all_launches, ms_total = [], [], 0.0
     for T in args.batches or MOE_BATCHES:
         launches, wbytes, distinct = [], 0, []
@@ -968,8 +970,8 @@ def run_moe(args, mx, be, threads):
             d = len(np.unique(ids))
             distinct.append(d)
             I = be.tensor(mx.I32, (MOE_K, T), ids)
-            wgu = d * row_bytes(Q4_K, MOE_H) * MOE_F
-            wdn = d * row_bytes(Q4_K, MOE_F) * MOE_H
+            wgu = d * row_bytes(WT, MOE_H) * MOE_F
+            wdn = d * row_bytes(WT, MOE_F) * MOE_H
             ops = 2 * T * MOE_K * MOE_H * MOE_F
             # gate and up read the same rows and ids (TextModel::experts): one MUL_MAT_ID group, one prep
             gu_bytes = 2 * wgu + 4 * T * (MOE_H + 2 * MOE_K * MOE_F + MOE_K)
@@ -992,14 +994,16 @@ def run_moe(args, mx, be, threads):
     total_b = sum(L.nbytes for _, ls, _ in all_launches for L in ls)
     gbps = total_b / (ms_total * 1e-3) / 1e9
     T_dom, l_dom, ms_dom = all_launches[-1]
-    roof = step_hbm_roofline(f"k_mmid_q4k at T = {T_dom} (with its bucket and Q8_K pass)", l_dom, ms_dom)
-    roof["traffic"] = read_traffic("moe")
+    kern = (f"k_mmid_q4k at T = {T_dom} (with its bucket and Q8_K pass)" if WT == Q4_K else
+            f"k_gemm_dq over expert chunks at T = {T_dom} (with its bucket and fp16 row pass)")
+    roof = step_hbm_roofline(kern, l_dom, ms_dom)
+    roof["traffic"] = read_traffic("moe") if WT == Q4_K else None
     result = base_result(args, round(gbps, 1), "GB/s", ms_total, "int8", {
         "workload": "drama3-like MoE FFN layer via MUL_MAT_ID, token batches 1, 16, 256", "experts": MOE_E,
-        "top_k": MOE_K, "hidden": MOE_H, "expert_ffn": MOE_F, "weights": "Q4_K", "layer_copies": MOE_LAYERS,
+        "top_k": MOE_K, "hidden": MOE_H, "expert_ffn": MOE_F, "weights": args.moe_weights, "layer_copies": MOE_LAYERS,
         "graph": not args.no_graph})
     result.update({"hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "per_batch": per_batch, "roofline": roof})
-    if args.cpu_seconds > 0:
+    if args.cpu_seconds > 0 and WT != Q5_K:  # the CPU port has no Q5_K dot
         O = load_oracle()
         cores = O.physical_cores()
         T = 16
@@ -1012,10 +1016,10 @@ def run_moe(args, mx, be, threads):
             for name in ("gate", "up"):
                 for e in np.unique(ids):
                     rows = np.nonzero((ids == e).any(axis=1))[0]
-                    O.cpu_fast_mul_mat(O.TYPE_Q4_K, hw[name][e], xb[rows], c)
+                    O.cpu_fast_mul_mat(WT, hw[name][e], xb[rows], c)
             for e in np.unique(ids):
                 t_idx, s_idx = np.nonzero(ids == e)
-                O.cpu_fast_mul_mat(O.TYPE_Q4_K, hw["down"][e], xa[t_idx, s_idx], c)
+                O.cpu_fast_mul_mat(WT, hw["down"][e], xa[t_idx, s_idx], c)
 
         wb = len(np.unique(ids)) * per_expert
         runs = []
@@ -1150,6 +1154,7 @@ def other_configs(args, mx, be, threads):
         sub = argparse.Namespace(**vars(args))
         sub.steps, sub.warmup = DEFAULT_STEPS[w]
         sub.cpu_seconds, sub.blocks, sub.batches = args.cpu_seconds / 2, None, None
+        sub.moe_weights = "Q4_K"  # the configuration's experts
         log(f"configs: {w}")
         r = WORKLOADS[w](sub, mx, be, threads)
         roof = r.get("roofline") or {}
@@ -1190,6 +1195,8 @@ def main():
     ints = lambda v: [int(t) for t in v.split(",")]
     ap.add_argument("--blocks", type=ints, default=None,
                     help="asr-1.7b: prefill block rows (default 512,512,512,28; counter passes use 512,512,512)")
+    ap.add_argument("--moe-weights", choices=sorted(TYPE_OF), default="Q4_K",
+                    help="moe: the experts' type (default Q4_K, as the configuration names it)")
     ap.add_argument("--batches", type=ints, default=None,
                     help="moe: token batches (default 1,16,256; counter passes use 256)")
     ap.add_argument("--opt", action="append", default=[], metavar="NAME=VALUE",

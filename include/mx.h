@@ -118,11 +118,14 @@ MX_API int mx_backend_set_rounding(mx_backend *be, int rounding);
  *   MX_OPT_GEMM_Q8_0          Q8_0 at M > 8: 0 the fp16 dequantizing GEMM, 1 the int8 MFMA GEMM (K % 128 == 0)
  *   MX_OPT_GEMM_KQUANT        Q4_K / Q6_K at M > 8: 0 as picked (scale-split int8 for Q4_K, fp16 dequantizing for
  *                             Q6_K), 1 the VALU-scaled int8 GEMM
- *   MX_OPT_GEMM_TILE_M / _N   the GEMM's tile, 0 / 64 / 128 each (0 0: picked per product)
+ *   MX_OPT_GEMM_TILE_M / _N   the GEMM's tile, 0 / 64 / 128 each, or 32 x 128 (0 0: picked per product); for the
+ *                             fp16 GEMM over MUL_MAT_ID's expert chunks 32 x 128, 32 x 64 or 64 x 64
  *   MX_OPT_GEMM_SPLIT         K splits of the fp16 dequantizing GEMM, 0 (picked) .. 64
  *   MX_OPT_MATVEC_LPR         lanes per weight row of the mat-vec: 0 (picked), 16, 32, 64
- *   MX_OPT_MMID_KERNEL        MUL_MAT_ID with many pairs: 0 as picked (Q4_K: the grouped MFMA product), 1 the
- *                             experts kernel, 2 the grouped MFMA product
+ *   MX_OPT_MMID_KERNEL        MUL_MAT_ID with many pairs: 0 as picked (Q4_K: the grouped int8 MFMA product; Q8_0,
+ *                             Q5_K, Q6_K: the fp16 dequantizing GEMM over chunks of each expert's pairs from one /
+ *                             six pairs per expert on average, else the experts kernel), 1 the experts kernel, 2 the
+ *                             grouped product (Q4_K int8, the other types the fp16 GEMM over the chunks)
  *   MX_OPT_MMID_MATVEC_PAIRS  MUL_MAT_ID runs as one mat-vec launch up to this many (token, slot) pairs (16; 0..4096)
  *   MX_OPT_MMID_CHUNK         pairs per chunk of an expert's pairs in the grouped Q4_K product: 0 as picked (16 when
  *                             the pairs average at most four per expert, else 32), 16 (one 16-row tile per chunk),

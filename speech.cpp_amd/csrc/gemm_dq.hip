@@ -24,6 +24,7 @@
 #include "mx_common.h"
 #include "mx_device.h"
 #include "mx_dot.h"
+#include "mx_dq_act.h"
 
 #include <algorithm>
 #include <type_traits>
@@ -63,7 +64,7 @@ constexpr int DQ_KS = 64;  // K per stage
 // LDS map of a BM x BN workgroup of NW waves. Row-major fp16 tiles of 64 halves (128 bytes) per row; the 16-byte
 // chunk c of row r sits at chunk c ^ ((r ^ (r >> 3)) & 7): any 8 consecutive rows an MFMA fragment read touches use 8
 // different chunks (all 32 banks of a 128-byte cycle), and 16 consecutive rows cover all 64 banks of a 256-byte one.
-template <int WT, int BM, int BN, int NW>
+template <int WT, int BM, int BN, int NW, bool RT = false>
 struct DqLds {
     static constexpr bool K6 = WT == MX_TYPE_Q6_K, K5 = WT == MX_TYPE_Q5_K;
     // Q8_0 with direct B: each wave converts its B fragments from the raw codes, so there is no fp16 weight tile
@@ -93,7 +94,8 @@ struct DqLds {
                                                                          : 0;
     static constexpr int JUNK = DD + NS * BN * DB;      // [wave][JB] where copies beyond a tile's need land
     static constexpr int RS = JUNK + NW * JB;           // [BM] the tile rows' 2^-e
-    static constexpr int SIZE = RS + BM * 4;
+    static constexpr int YO = RS + BM * 4;              // routed experts: [BM] each tile row's output offset (floats)
+    static constexpr int SIZE = YO + (RT ? BM * 8 : 0);
     static_assert(SIZE <= 160 * 1024, "LDS");
 };
 
@@ -114,6 +116,14 @@ struct DqArgs {
     int ntot;            // sum of the problems' N: columns of the split partials
     int col0[4];         // first partial column of each problem
     float *ws;           // nsplit > 1: [nsplit][M][ntot] partial sums, added in split order by k_dq_reduce
+    // Routed experts (MUL_MAT_ID; the kernel's RT form, one split): grid.y runs over chunks of one expert's (token,
+    // slot) pairs -- tiles[3 c] the chunk's first index into pairs, tiles[3 c + 1] its count (<= BM), tiles[3 c + 2]
+    // the expert, ntiles[0] the chunks there are. Row i of a chunk is pair p = pairs[first + i] = t n_ids + s: its
+    // activation row is xh row t b_ne1 + s % b_ne1, its weights rows expert N .. of each problem's planes, its output
+    // row y + s y_nb1 + t y_nb2 (floats).
+    const int32_t *tiles, *ntiles, *pairs;
+    int n_ids, b_ne1;
+    int64_t y_nb1, y_nb2;
 };
 
 __device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(dq_lds *)p; }
@@ -123,156 +133,22 @@ __device__ __forceinline__ void dq_wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
 }
 
-// The fp16 activation values of a row carry a power-of-two scale 2^e, e chosen so that the row's largest |d q| lands
-// in [2^14, 2^15): clear of fp16's overflow (65504) and of its subnormals, where ggml's fp32 sums lose nothing. The
-// GEMM multiplies its sums by rs[m] = 2^-e. Both scalings are exact, so a row that fp16 already holds in its normal
-// range gives the same bits as unscaled values would. e is at most 126, so rs stays a normal float: a row whose
-// largest |d q| is below 2^-112 (possible with Q8_K's fp32 d) lands lower than 2^14 but still in fp16's normal range
-// down to 2^-140.
-__device__ __forceinline__ int dq_row_exp(float amax) {
-    if (amax == 0.0f) return 0;
-    int E = (int)((__float_as_uint(amax) >> 23) & 0xFF);  // amax in [2^(E-127), 2^(E-126))
-    if (E == 0) E = 1;
-    const int e = 141 - E;
-    return e < -126 ? -126 : (e > 126 ? 126 : e);  // 2^-e stays a normal float (2^-127 would be subnormal)
-}
-__device__ __forceinline__ float dq_pow2(int e) { return __uint_as_float((uint32_t)(e + 127) << 23); }
-
 constexpr int DQ_ACT_NT = 1024;  // threads of an activation-pass workgroup (one row)
 
-__device__ __forceinline__ float dq_block_max(float v, float *red) {  // over a DQ_ACT_NT-thread workgroup
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float r = red[0];
-#pragma unroll
-    for (int w = 1; w < DQ_ACT_NT / 64; w++) r = fmaxf(r, red[w]);
-    return r;
-}
-
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-
-constexpr int DQ_ACT_REG = 4;  // 4-element pieces per thread an activation row keeps in registers (K <= 16384)
-constexpr int DQ_ACT_CH = 4 * DQ_ACT_NT;  // elements per pass of the workgroup
-
-__device__ __forceinline__ float4 dq_ld4(const float *xr, int e, int K) {
-    return e < K ? *(const float4 *)(xr + e) : make_float4(0.f, 0.f, 0.f, 0.f);
-}
-
-// d q of four packed codes, each exact in fp32 for Q8_0's fp16 d (11 + 7 bits); for Q8_K's fp32 d the product ggml's
-// dequantize_row_q8_K forms
-__device__ __forceinline__ float4 dq_vals(int q, float d) {
-    return make_float4(d * (float)(int8_t)(q & 0xFF), d * (float)(int8_t)((q >> 8) & 0xFF),
-                       d * (float)(int8_t)((q >> 16) & 0xFF), d * (float)(int8_t)((q >> 24) & 0xFF));
-}
-__device__ __forceinline__ float dq_amax4(float4 p) { return fmaxf(fmaxf(fabsf(p.x), fabsf(p.y)), fmaxf(fabsf(p.z), fabsf(p.w))); }
-__device__ __forceinline__ v4h dq_h4(float4 p, float sc) {
-    return v4h{(_Float16)(p.x * sc), (_Float16)(p.y * sc), (_Float16)(p.z * sc), (_Float16)(p.w * sc)};
-}
-
-// Activation row m (one workgroup) -> Q8_0 blocks (ggml's quantize_row_q8_0, d rounded to fp16 as the dot reads it)
-// -> fp16(2^e d q): d q is exact in fp32 and so is its scaling; one rounding to fp16. The row is quantized once, its
-// codes kept in registers while the workgroup finds the row's largest |d q| (rows longer than DQ_ACT_REG * DQ_ACT_CH
-// are quantized twice).
+// Activation row m (one workgroup) -> Q8_0 blocks -> fp16(2^e d q) (mx_dq_act.h).
 __global__ __launch_bounds__(DQ_ACT_NT) void k_dq_act_q8_0(const float *x, int64_t x_stride, int K, int rounding,
                                                             _Float16 *xh, float *rs) {
     __shared__ float red[DQ_ACT_NT / 64];
     const int64_t m = blockIdx.x;
-    const int t4 = 4 * threadIdx.x;
-    const float *xr = x + m * x_stride;
-    _Float16 *out = xh + m * K;
-    float amax = 0.0f;
-    if (K <= DQ_ACT_REG * DQ_ACT_CH) {
-        float4 v[DQ_ACT_REG];
-        int q[DQ_ACT_REG];
-        float dh[DQ_ACT_REG];
-#pragma unroll
-        for (int c = 0; c < DQ_ACT_REG; c++) v[c] = dq_ld4(xr, DQ_ACT_CH * c + t4, K);
-#pragma unroll
-        for (int c = 0; c < DQ_ACT_REG; c++)
-            if (DQ_ACT_CH * c < K) {  // uniform: every lane joins the 8-lane block reductions
-                float d;
-                int sum;
-                q[c] = quant32_lane(v[c], rounding, &d, &sum);
-                dh[c] = h2f(f2h(d));
-                amax = fmaxf(amax, dq_amax4(dq_vals(q[c], dh[c])));
-            }
-        const int ex = dq_row_exp(dq_block_max(amax, red));
-        if (threadIdx.x == 0) rs[m] = dq_pow2(-ex);
-        const float sc = dq_pow2(ex);
-#pragma unroll
-        for (int c = 0; c < DQ_ACT_REG; c++)
-            if (DQ_ACT_CH * c + t4 < K) *(v4h *)(out + DQ_ACT_CH * c + t4) = dq_h4(dq_vals(q[c], dh[c]), sc);
-        return;
-    }
-    for (int c = 0; c < K; c += DQ_ACT_CH) {
-        float d;
-        int sum;
-        const int q = quant32_lane(dq_ld4(xr, c + t4, K), rounding, &d, &sum);
-        amax = fmaxf(amax, dq_amax4(dq_vals(q, h2f(f2h(d)))));
-    }
-    const int ex = dq_row_exp(dq_block_max(amax, red));
-    if (threadIdx.x == 0) rs[m] = dq_pow2(-ex);
-    for (int c = 0; c < K; c += DQ_ACT_CH) {
-        float d;
-        int sum;
-        const int q = quant32_lane(dq_ld4(xr, c + t4, K), rounding, &d, &sum);
-        if (c + t4 < K) *(v4h *)(out + c + t4) = dq_h4(dq_vals(q, h2f(f2h(d))), dq_pow2(ex));
-    }
+    dq_act_row_q8_0<DQ_ACT_NT>(x + m * x_stride, K, rounding, xh + m * K, rs + m, red);
 }
 
-// Activation row m -> Q8_K blocks (ggml's quantize_row_q8_K_ref, the pairing of Q6_K weights) -> fp16(2^e fp32(d q)),
-// the product ggml's dequantize_row_q8_K forms, scaled and rounded once more. Wave w takes blocks w, w + 16, ...
+// Activation row m -> Q8_K blocks (the pairing of Q5_K / Q6_K weights) -> fp16(2^e fp32(d q)) (mx_dq_act.h).
 __global__ __launch_bounds__(DQ_ACT_NT) void k_dq_act_q8k(const float *x, int64_t x_stride, int K, _Float16 *xh,
                                                            float *rs) {
-    constexpr int NWV = DQ_ACT_NT / 64;
-    __shared__ float red[NWV];
+    __shared__ float red[DQ_ACT_NT / 64];
     const int64_t m = blockIdx.x;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nsb = K / 256;
-    const float *xr = x + m * x_stride;
-    _Float16 *out = xh + m * K;
-    float amax = 0.0f;
-    if (nsb <= NWV * DQ_ACT_REG) {
-        float4 v[DQ_ACT_REG];
-        int q[DQ_ACT_REG];
-        float dq[DQ_ACT_REG];
-#pragma unroll
-        for (int i = 0; i < DQ_ACT_REG; i++) {
-            const int sb = wave + NWV * i;
-            v[i] = sb < nsb ? *(const float4 *)(xr + sb * 256 + 4 * lane) : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int i = 0; i < DQ_ACT_REG; i++)
-            if (wave + NWV * i < nsb) {  // wave-uniform
-                int bs16;
-                q[i] = quant256_wave(v[i], lane, &dq[i], &bs16);
-                amax = fmaxf(amax, dq_amax4(dq_vals(q[i], dq[i])));
-            }
-        const int ex = dq_row_exp(dq_block_max(amax, red));
-        if (threadIdx.x == 0) rs[m] = dq_pow2(-ex);
-        const float sc = dq_pow2(ex);
-#pragma unroll
-        for (int i = 0; i < DQ_ACT_REG; i++) {
-            const int sb = wave + NWV * i;
-            if (sb < nsb) *(v4h *)(out + sb * 256 + 4 * lane) = dq_h4(dq_vals(q[i], dq[i]), sc);
-        }
-        return;
-    }
-    for (int sb = wave; sb < nsb; sb += NWV) {
-        float d;
-        int bs16;
-        const int q = quant256_wave(*(const float4 *)(xr + sb * 256 + 4 * lane), lane, &d, &bs16);
-        amax = fmaxf(amax, dq_amax4(dq_vals(q, d)));
-    }
-    const int ex = dq_row_exp(dq_block_max(amax, red));
-    if (threadIdx.x == 0) rs[m] = dq_pow2(-ex);
-    for (int sb = wave; sb < nsb; sb += NWV) {
-        float d;
-        int bs16;
-        const int q = quant256_wave(*(const float4 *)(xr + sb * 256 + 4 * lane), lane, &d, &bs16);
-        *(v4h *)(out + sb * 256 + 4 * lane) = dq_h4(dq_vals(q, d), dq_pow2(ex));
-    }
+    dq_act_row_q8k<DQ_ACT_NT>(x + m * x_stride, K, xh + m * K, rs + m, red);
 }
 
 // Four signed bytes -> four exact fp16 values: (0x64 << 8 | (b ^ 0x80)) is the fp16 of 1152 + b, and 1152 is
@@ -505,10 +381,10 @@ __device__ __forceinline__ void dq_wait8(v8h (&f)[16]) {
                  : "memory");
 }
 
-template <int WT, int BM, int BN, int WGM, int WGN>
+template <int WT, int BM, int BN, int WGM, int WGN, bool RT>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     constexpr int NW = WGM * WGN, NT = 64 * NW;
-    using L = DqLds<WT, BM, BN, NW>;
+    using L = DqLds<WT, BM, BN, NW, RT>;
     constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
     constexpr int NF = (TM + TN) * 4;  // fragments of the stage's four K steps, read together
     static_assert(L::DIRB ? TN == 1 && (TM == 1 || TM == 2 || TM == 4) : NF == 8 || NF == 12 || NF == 16,
@@ -518,8 +394,36 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     const DqProblem p = pi == 0 ? a.prob[0] : (pi == 1 ? a.prob[1] : (pi == 2 ? a.prob[2] : a.prob[3]));
     const int n0 = blockIdx.x * BN;
     if (n0 >= p.N) return;  // uniform: a problem narrower than the grid
-    const int m0 = blockIdx.y * BM;
+    const int m0 = RT ? 0 : blockIdx.y * BM;
     const int M = a.M, N = p.N, K = a.K, nblk = K / 32;
+    int mrows = 0, first = 0;  // routed: the chunk's pairs and its first index into pairs
+    int64_t wrow0 = 0;         // routed: the expert's first row in the weight planes
+    if constexpr (RT) {
+        const int c = blockIdx.y;
+        if (c >= a.ntiles[0]) return;  // uniform: past the chunks the bucketing wrote
+        first = a.tiles[3 * c];
+        mrows = a.tiles[3 * c + 1];
+        wrow0 = (int64_t)a.tiles[3 * c + 2] * N;
+    }
+    // the (token, slot) pair of routed tile row i, clamped to the chunk's last (the lambdas capture plain values: a
+    // reference to the argument block would move it to private memory)
+    const int32_t *pairs = a.pairs;
+    const int n_ids = a.n_ids, b_ne1 = a.b_ne1;
+    auto pair_of = [=](int i, int &t, int &s) {
+        const int pr = pairs[first + min(i, mrows - 1)];
+        t = pr / n_ids;
+        s = pr - t * n_ids;
+    };
+    // the activation row of tile row i, clamped to the tile's (routed: the chunk's) last
+    auto arow = [=](int i) -> int64_t {
+        if constexpr (RT) {
+            int t, s;
+            pair_of(i, t, s);
+            return (int64_t)t * b_ne1 + s % b_ne1;
+        } else {
+            return min(m0 + i, M - 1);
+        }
+    };
     // this workgroup's stages: [sb, sb + nst) of K / 64 (the host makes every split non-empty)
     const int per = (K / DQ_KS + a.nsplit - 1) / a.nsplit, sb = split * per;
     const int nst = min(K / DQ_KS - sb, per);
@@ -540,7 +444,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
 #pragma unroll
     for (int jj = 0; jj < L::PA; jj++) {
         const int j = wave * L::PA + jj, row = 8 * min(j, L::NA - 1) + (lane >> 3);
-        asrc[jj] = a.xh + (int64_t)min(m0 + row, M - 1) * K + sb * DQ_KS + 8 * ((lane & 7) ^ dq_swz(row));
+        asrc[jj] = a.xh + arow(row) * K + sb * DQ_KS + 8 * ((lane & 7) ^ dq_swz(row));
         adst[jj] = j < L::NA ? L::A + j * 1024 : L::JUNK + wave * L::JB;
     }
     const uint8_t *csrc[L::PC];
@@ -549,7 +453,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     for (int jj = 0; jj < L::PC; jj++) {
         constexpr int LR = L::RB / 16;  // lanes per code row
         const int j = wave * L::PC + jj, row = (64 / LR) * min(j, L::NC - 1) + lane / LR;
-        const int64_t grow = min(n0 + row, N - 1);
+        const int64_t grow = wrow0 + min(n0 + row, N - 1);
         // direct B: row r's chunk c lands at chunk c ^ ((r >> 2) & 3), so the 16 rows a fragment read's lane group
         // touches cover all 64 banks
         const int cc = L::DIRB ? (lane % LR) ^ ((row >> 2) & 3) : lane % LR;
@@ -561,7 +465,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
 #pragma unroll
     for (int jj = 0; jj < L::PH; jj++) {
         const int j = wave * L::PH + jj, row = 32 * min(j, L::NH - 1) + (lane >> 1);
-        hsrc[jj] = p.w.p1 + (int64_t)min(n0 + row, N - 1) * nsb * (L::K5 ? 32 : 64) + 16 * (lane & 1);
+        hsrc[jj] = p.w.p1 + (wrow0 + min(n0 + row, N - 1)) * nsb * (L::K5 ? 32 : 64) + 16 * (lane & 1);
         hdst[jj] = j < L::NH ? L::QH + j * 1024 : L::JUNK + wave * L::JB;
     }
     const uint8_t *ssrc[L::PS];
@@ -570,10 +474,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     for (int jj = 0; jj < L::PS; jj++) {
         const int j = wave * L::PS + jj, wd = 64 * min(j, L::NS4 - 1) + lane;  // scale word wd of the stage
         if constexpr (L::K5) {  // word c of row wd / 3's 12 bytes
-            const int64_t grow = min(n0 + wd / 3, N - 1);
+            const int64_t grow = wrow0 + min(n0 + wd / 3, N - 1);
             ssrc[jj] = p.w.p2 + grow * nsb * 12 + 4 * (wd % 3);
         } else {
-            const int64_t grow = min(n0 + wd, N - 1);
+            const int64_t grow = wrow0 + min(n0 + wd, N - 1);
             ssrc[jj] = L::K6 ? p.w.p2 + grow * nsb * 16 : p.w.p1 + grow * nblk * 2 + sb * 4;
         }
         sdst[jj] = j < L::NS4 ? L::SC + j * 256 : L::JUNK + wave * L::JB;
@@ -583,7 +487,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
 #pragma unroll
     for (int jj = 0; jj < L::PD; jj++) {
         const int j = wave * L::PD + jj, row = 64 * min(j, L::ND - 1) + lane;
-        dsb[jj] = (int64_t)min(n0 + row, N - 1) * nsb;
+        dsb[jj] = (wrow0 + min(n0 + row, N - 1)) * nsb;
         ddst[jj] = j < L::ND ? L::DD + j * 256 : L::JUNK + wave * L::JB;
     }
 
@@ -684,7 +588,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
                     : "=&v"(l0), "=&v"(h0), "=&v"(sw), "=&v"(dw)
                     : "v"(raw), "v"(qh), "v"(sc), "v"(dd)
                     : "memory");
-                const int64_t e = (int64_t)min(n0 + row, N - 1) * nsb + (g >> 2);
+                const int64_t e = (wrow0 + min(n0 + row, N - 1)) * nsb + (g >> 2);
                 dq_q6_k_16(l0, h0, (g & 1) * 4 + (q >> 1) * 2, (g & 1) * 4, (int8_t)(sw >> (8 * q)),
                            (uint16_t)((e & 1) ? dw >> 16 : dw & 0xFFFF), o[0], o[1]);
             }
@@ -723,16 +627,32 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-    const float rs_row = a.rs[min(m0 + (tid < BM ? tid : 0), M - 1)];  // requested ahead of the copies
+    // the tile rows' 2^-e (routed: and output offsets), requested ahead of the copies
+    float rs_row;
+    int64_t yo_row = 0;
+    if constexpr (RT) {
+        int t, s;
+        pair_of(tid < BM ? tid : 0, t, s);
+        rs_row = a.rs[(int64_t)t * b_ne1 + s % b_ne1];
+        yo_row = s * a.y_nb1 + t * a.y_nb2;
+    } else {
+        rs_row = a.rs[min(m0 + (tid < BM ? tid : 0), M - 1)];
+    }
 #pragma unroll
     for (int t = 0; t < L::NS - 1; t++) issue(t);
     if constexpr (!L::DIRB) {
         dq_wait_vm<(L::NS - 2) * L::OPS>();  // stage 0 landed (this wave's copies)
-        if (tid < BM) *(float *)(smem + L::RS + 4 * tid) = rs_row;  // the tile rows' 2^-e, read by the epilogue
+        if (tid < BM) {  // read by the epilogue
+            *(float *)(smem + L::RS + 4 * tid) = rs_row;
+            if constexpr (RT) *(int64_t *)(smem + L::YO + 8 * tid) = yo_row;
+        }
         __syncthreads();
         convert(0);
     } else {
-        if (tid < BM) *(float *)(smem + L::RS + 4 * tid) = rs_row;  // visible after the loop's first barrier
+        if (tid < BM) {  // visible after the loop's first barrier
+            *(float *)(smem + L::RS + 4 * tid) = rs_row;
+            if constexpr (RT) *(int64_t *)(smem + L::YO + 8 * tid) = yo_row;
+        }
     }
     // direct B: this lane's raw chunk 2 kk2 + fh of row wn + fr, swizzled as the copies placed it, and its scale word
     const int brow = wn + fr;
@@ -871,6 +791,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
         ldy = a.ntot;
     }
     const float *rsl = (const float *)(smem + L::RS);  // the rows' 2^-e
+    const int64_t *yol = (const int64_t *)(smem + L::YO);  // routed: the rows' output offsets
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -879,8 +800,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             if (n >= N) continue;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);
-                if (m < M) y[(int64_t)m * ldy + n] = acc[i][j][r] * rsl[m - m0];
+                const int ml = wm + 32 * i + 8 * (r >> 2) + 4 * fh + (r & 3);  // row within the tile
+                if constexpr (RT) {
+                    if (ml < mrows) y[yol[ml] + n] = acc[i][j][r] * rsl[ml];
+                } else {
+                    const int m = m0 + ml;
+                    if (m < M) y[(int64_t)m * ldy + n] = acc[i][j][r] * rsl[ml];
+                }
             }
         }
 }
@@ -1021,18 +947,20 @@ hipError_t launch_gemm_dq_act(int type, int rounding, const float *x, int64_t x_
     return hipGetLastError();
 }
 
-template <int WT, int BM, int BN, int WGM, int WGN>
-static hipError_t launch_dq(const DqArgs &a, int maxN, hipStream_t s) {
-    using L = DqLds<WT, BM, BN, WGM * WGN>;
+// gy: the routed form's chunk slots (grid.y); the dense form covers M.
+template <int WT, int BM, int BN, int WGM, int WGN, bool RT = false>
+static hipError_t launch_dq(const DqArgs &a, int maxN, hipStream_t s, int gy = 0) {
+    using L = DqLds<WT, BM, BN, WGM * WGN, RT>;
     static bool attr = false;
     if (!attr) {
-        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm_dq<WT, BM, BN, WGM, WGN>,
+        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm_dq<WT, BM, BN, WGM, WGN, RT>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, L::SIZE);
         if (e != hipSuccess) return e;
         attr = true;
     }
-    const dim3 grid((unsigned)((maxN + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM), (unsigned)(a.nprob * a.nsplit));
-    hipLaunchKernelGGL((k_gemm_dq<WT, BM, BN, WGM, WGN>), grid, dim3(64 * WGM * WGN), L::SIZE, s, a);
+    const dim3 grid((unsigned)((maxN + BN - 1) / BN), (unsigned)(RT ? gy : (a.M + BM - 1) / BM),
+                    (unsigned)(a.nprob * a.nsplit));
+    hipLaunchKernelGGL((k_gemm_dq<WT, BM, BN, WGM, WGN, RT>), grid, dim3(64 * WGM * WGN), L::SIZE, s, a);
     return hipGetLastError();
 }
 
@@ -1081,6 +1009,65 @@ hipError_t launch_gemm_dq(int type, int nprob, const WPlanes *w, const int64_t *
     if (v4) hipLaunchKernelGGL(k_dq_reduce<4>, dim3((unsigned)((pl.ntot / 4 + 255) / 256), (unsigned)M), dim3(256), 0, s, a);
     else hipLaunchKernelGGL(k_dq_reduce<1>, dim3((unsigned)((pl.ntot + 255) / 256), (unsigned)M), dim3(256), 0, s, a);
     return hipGetLastError();
+}
+
+template <int WT>
+static hipError_t dq_routed(const DqArgs &a, int tile, int maxN, int gy, hipStream_t s) {
+    switch (tile) {
+        case 32128: return launch_dq<WT, 32, 128, 1, 4, true>(a, maxN, s, gy);
+        case 32064: return launch_dq<WT, 32, 64, 1, 2, true>(a, maxN, s, gy);
+        case 64064: return launch_dq<WT, 64, 64, 2, 2, true>(a, maxN, s, gy);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// The routed form's tile: Q8_0 32 x 128, the K-quants 64 x 64, unless a backend's tile option forces one the form has
+// (32 x 128, 32 x 64 or 64 x 64; 0 x 0 if it has not). Its rows are a chunk's.
+static void dq_routed_tile(const MulMatIdArgs &m, int &bm, int &bn) {
+    bm = m.type == MX_TYPE_Q8_0 ? 32 : 64;
+    bn = m.type == MX_TYPE_Q8_0 ? 128 : 64;
+    if (m.tile_m || m.tile_n) {
+        const bool ok = (m.tile_m == 32 && (m.tile_n == 128 || m.tile_n == 64)) || (m.tile_m == 64 && m.tile_n == 64);
+        bm = ok ? m.tile_m : 0;
+        bn = ok ? m.tile_n : 0;
+    }
+}
+
+int mmid_dq_chunk(const MulMatIdArgs &m) {
+    int bm, bn;
+    dq_routed_tile(m, bm, bn);
+    return bm;
+}
+
+hipError_t launch_gemm_dq_routed(const MulMatIdArgs &m, hipStream_t s) {
+    int bm, bn;
+    dq_routed_tile(m, bm, bn);
+    if (m.nprob < 1 || m.nprob > 4 || bm == 0 || m.chunk != bm || !gemm_dq_supported(m.type, MAX_COLS + 1, m.K))
+        return hipErrorInvalidValue;
+    if (m.N == 0) return hipSuccess;
+    DqArgs a{};
+    for (int i = 0; i < m.nprob; i++) a.prob[i] = DqProblem{m.wg[i], (int)m.N, m.dstg[i], 0};
+    a.M = 0;  // rows come from the chunks
+    a.K = (int)m.K;
+    a.xh = m.xh;
+    a.rs = m.rs;
+    a.nprob = m.nprob;
+    a.nsplit = 1;
+    a.tiles = m.tiles;
+    a.ntiles = m.ntiles;
+    a.pairs = m.pairs;
+    a.n_ids = (int)m.n_ids;
+    a.b_ne1 = (int)m.b_ne1;
+    a.y_nb1 = m.dst_nb1 / 4;
+    a.y_nb2 = m.dst_nb2 / 4;
+    const int gy = (int)m.max_tiles, maxN = (int)m.N;
+    const int tile = bm * 1000 + bn;
+    switch (m.type) {
+        case MX_TYPE_Q8_0: return dq_routed<MX_TYPE_Q8_0>(a, tile, maxN, gy, s);
+        case MX_TYPE_Q6_K: return dq_routed<MX_TYPE_Q6_K>(a, tile, maxN, gy, s);
+        case MX_TYPE_Q5_K: return dq_routed<MX_TYPE_Q5_K>(a, tile, maxN, gy, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace mx

@@ -6,11 +6,14 @@
 //      expert (the matrix_row_counts / matrix_rows of ggml-cpu.c ggml_compute_forward_mul_mat_id) and cuts each
 //      expert's pairs into chunks; the other workgroups quantize every activation row once (ggml-cpu quantizes src1
 //      once, before the experts run).
-//   2. experts: Q4_K experts run as a grouped MFMA product over the chunks (mmid_q4k.hip); the other types stream
-//      each touched expert's weights once per 8 pairs on dot4 (k_mmid_experts below). Untouched experts cost nothing.
+//   2. experts: Q4_K experts run as a grouped MFMA product over the chunks (mmid_q4k.hip); Q8_0, Q5_K and Q6_K experts
+//      on the fp16 dequantizing GEMM's routed form, a chunk per row tile (gemm_dq.hip), or, when an option asks for it,
+//      stream each touched expert's weights once per 8 pairs on dot4 (k_mmid_experts below). Untouched experts cost
+//      nothing.
 #include "mx_common.h"
 #include "mx_device.h"
 #include "mx_dot.h"
+#include "mx_dq_act.h"
 
 #include <cstdlib>
 
@@ -36,10 +39,17 @@ size_t mul_mat_id_scratch(MulMatIdArgs *a, void *base) {
     a->offsets = (int32_t *)(b + off); off += al256((size_t)a->E * 4);
     a->active = (int32_t *)(b + off);  off += al256((size_t)(a->E + 1) * 4);
     a->pairs = (int32_t *)(b + off);   off += al256((size_t)npairs * 4);
+    // the activation rows: quantized blocks for the int8 kernels, or the fp16 GEMM's rows, in the same space (sized
+    // for the larger, whichever kernel runs)
+    const size_t rows0 = off;
     a->xq = (int8_t *)(b + off);       off += al256((size_t)nrows * (size_t)a->K);
     a->xd = (float *)(b + off);        off += al256((size_t)nrows * (size_t)nsc * 4);
     a->xbs = (int32_t *)(b + off);     off += al256(a->type == MX_TYPE_Q8_0 ? 0 : (size_t)nrows * (size_t)(a->K / 16) * 4);
     a->x16 = (_Float16 *)(b + off);    off += al256(a->type == MX_TYPE_Q4_K ? (size_t)nrows * (size_t)(a->K / 256) * 32 : 0);
+    size_t dq = rows0;
+    a->xh = (_Float16 *)(b + dq);      dq += al256((size_t)nrows * (size_t)a->K * 2);
+    a->rs = (float *)(b + dq);         dq += al256((size_t)nrows * 4);
+    off = off > dq ? off : dq;
     // chunks: sum over experts of ceil(count / chunk) <= npairs / chunk + (experts with pairs), sized for the
     // smaller chunk whichever the launch takes
     a->max_tiles = npairs / MMID_CHUNK_SMALL + (npairs < a->E ? npairs : a->E) + 1;
@@ -192,6 +202,37 @@ __global__ __launch_bounds__(256) void k_mmid_prep(MulMatIdArgs a) {
                  "s"(a.b), "s"(a.b_ne1), "s"(a.b_nb1), "s"(a.b_nb2), "s"(a.K));
     if (blockIdx.x == 0) mmid_bucket(a);
     else mmid_quant_row<TYPE>(a, (int64_t)blockIdx.x - 1);
+}
+
+// The same for the fp16 GEMM's routed form: workgroup 0 buckets the pairs into chunks of one row tile, workgroup
+// 1 + r writes activation row r as that GEMM's own rows (fp16(2^e d q) of the ggml blocks the weight's dot pairs
+// with, and 2^-e), the arithmetic of its dense activation pass.
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_mmid_prep_dq(MulMatIdArgs a) {
+    asm volatile("" ::"s"(a.n_ids), "s"(a.T), "s"(a.E), "s"(a.ids), "s"(a.ids_nb0), "s"(a.ids_nb1), "s"(a.chunk),
+                 "s"(a.b), "s"(a.b_ne1), "s"(a.b_nb1), "s"(a.b_nb2), "s"(a.K));
+    __shared__ float red[4];
+    if (blockIdx.x == 0) {
+        mmid_bucket(a);
+        return;
+    }
+    const int64_t r = (int64_t)blockIdx.x - 1, t = r / a.b_ne1, s = r % a.b_ne1;
+    const float *x = (const float *)((const uint8_t *)a.b + s * a.b_nb1 + t * a.b_nb2);
+    if constexpr (TYPE == MX_TYPE_Q8_0) dq_act_row_q8_0<256>(x, (int)a.K, a.rounding, a.xh + r * a.K, a.rs + r, red);
+    else dq_act_row_q8k<256>(x, (int)a.K, a.xh + r * a.K, a.rs + r, red);
+}
+
+// Q8_0 / Q5_K / Q6_K experts go to the fp16 dequantizing GEMM over the chunks once their pairs share each expert's
+// weights enough: measured over 64 experts of 2048 x 1536 (top-4, us per layer, the GEMM against the experts kernel),
+// Q8_0 from one pair per expert on average (16 tokens: 130 against 130; 32: 171 against 203; 256: 200 against
+// 1,235), the K-quants from six (Q6_K at 64 tokens, four per expert: 291 against 279; 128 tokens: 301 against 509;
+// 256: 302 against 983). An option forces the experts kernel (1) or the GEMM (2, wherever it takes the rows' K).
+bool mmid_dq_route(const MulMatIdArgs &a) {
+    if (a.type != MX_TYPE_Q8_0 && a.type != MX_TYPE_Q5_K && a.type != MX_TYPE_Q6_K) return false;
+    if (a.generic == 1 || !gemm_dq_supported(a.type, a.T * a.b_ne1, a.K)) return false;
+    if (a.generic == 2) return true;
+    const int64_t npairs = a.n_ids * a.T;
+    return npairs >= (a.type == MX_TYPE_Q8_0 ? 1 : 6) * a.E;
 }
 
 
@@ -360,6 +401,16 @@ __global__ __launch_bounds__(256) void k_mmid_experts(MulMatIdArgs a) {
 template <int TYPE>
 static hipError_t launch_typed(const MulMatIdArgs &a, hipStream_t s) {
     const int64_t nrows = a.T * a.b_ne1;
+    if constexpr (TYPE != MX_TYPE_Q4_K) {
+        if (mmid_dq_route(a)) {
+            MulMatIdArgs b = a;
+            b.chunk = mmid_dq_chunk(a);  // one row tile per chunk
+            hipLaunchKernelGGL(k_mmid_prep_dq<TYPE>, dim3((unsigned)(nrows + 1)), dim3(256), (size_t)a.E * 4, s, b);
+            const hipError_t err = hipGetLastError();
+            if (err != hipSuccess) return err;
+            return launch_gemm_dq_routed(b, s);
+        }
+    }
     hipLaunchKernelGGL(k_mmid_prep<TYPE>, dim3((unsigned)(nrows + 1)), dim3(256), (size_t)a.E * 4, s, a);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;

@@ -932,6 +932,8 @@ static void mmid_args(mx_backend *be, const mx_tensor *as, const mx_tensor *b, c
     a.chunk = mx::mmid_chunk_for(a.n_ids * a.T, a.E, be->opt.mmid_chunk);
     a.matvec_pairs = be->opt.mmid_matvec_pairs;
     a.lpr = be->opt.matvec_lpr;
+    a.tile_m = be->opt.tile_m;
+    a.tile_n = be->opt.tile_n;
     a.err = be->err;
 }
 

@@ -112,7 +112,7 @@ struct Options {
     int split = 0;                  // K splits of the fp16 dequantizing GEMM (0: picked)
     int matvec_lpr = 0;             // lanes per row of the mat-vec: 16, 32 or 64 (0: picked)
     int mmid_kernel = 0;            // MUL_MAT_ID with many pairs: 0 as picked, 1 the experts kernel, 2 the grouped
-                                    // MFMA product (Q4_K)
+                                    // product (Q4_K: int8 MFMA; Q8_0, Q5_K, Q6_K: the fp16 GEMM over expert chunks)
     int64_t mmid_matvec_pairs = 16; // MUL_MAT_ID runs as one mat-vec launch up to this many (token, slot) pairs
     int mmid_chunk = 0;             // pairs per chunk of the grouped Q4_K product: 16 or 32 (0: picked)
 };
@@ -260,6 +260,8 @@ struct MulMatIdArgs {
     float *xd;             // [T * b_ne1][K / blk] their scales
     int32_t *xbs;          // [T * b_ne1][K / 16] their 16-element sums (K-quants)
     _Float16 *x16;         // [T * b_ne1][K / 256][16] Q4_K: per super-block [64 h_j | l_j], bsum32_j = 64 h_j + l_j
+    _Float16 *xh;          // the fp16 GEMM's routed form: [T * b_ne1][K] rows fp16(2^e d q) (sharing xq's space)
+    float *rs;             // the fp16 GEMM's routed form: [T * b_ne1] their 2^-e
     int32_t *tiles;        // [max_tiles][3]: chunks of an expert's pairs: first (index into `pairs`), count, expert
     int32_t *ntiles;       // [1] tiles written by the bucket kernel
     int64_t max_tiles;
@@ -273,6 +275,7 @@ struct MulMatIdArgs {
     float *dstg[4];
     int64_t matvec_pairs;      // up to this many pairs: one mat-vec launch, no bucketing
     int lpr;                   // mat-vec lanes per row forced, or 0
+    int tile_m, tile_n;        // the fp16 GEMM's routed tile forced, or 0
 };
 // Row-wise ops on f32 rows (layer.hip): src / dst rows (i1, i2, i3) at byte strides, ne0 contiguous floats.
 struct RowsArgs {
@@ -354,5 +357,12 @@ hipError_t launch_mul_mat_id(const MulMatIdArgs &a, hipStream_t s);
 // Q4_K experts as a grouped product over chunks of up to a.chunk of an expert's pairs (16 x 16 x 64 int8 MFMA).
 bool mmid_q4k_supported(const MulMatIdArgs &a);  // Q4_K, K <= 2048
 hipError_t launch_mmid_q4k(const MulMatIdArgs &a, hipStream_t s);
+// Q8_0 / Q5_K / Q6_K experts on the fp16 dequantizing GEMM (gemm_dq.hip): each chunk of up to mmid_dq_chunk(type) of
+// an expert's pairs is one row tile (Q8_0: 32 x 128 tiles; Q5_K, Q6_K: 64 x 64), its rows the prep's (xh, rs) rows of
+// the pairs, gathered, its outputs scattered to dst; the chunks past a.ntiles[0] of the a.max_tiles slots leave at
+// once. mmid_dq_route is the dispatch rule that sends a MUL_MAT_ID there.
+int mmid_dq_chunk(const MulMatIdArgs &a);
+bool mmid_dq_route(const MulMatIdArgs &a);
+hipError_t launch_gemm_dq_routed(const MulMatIdArgs &a, hipStream_t s);
 
 }  // namespace mx

@@ -144,30 +144,48 @@ def test_matvec_every_lanes_per_row(mx, be, t, K):
 # --------------------------------------------------------------------------------------- MUL_MAT_ID paths
 @pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
 def test_mmid_every_path(mx, be, t):
-    """The experts kernel where the grouped Q4_K product would run, in several passes per expert (40 tokens) and in
-    its one-pass form (16 tokens); the grouped product at a small batch (one-tile chunks); the bucketed path for a
-    single token (mat-vec threshold 0); the mat-vec path for 64 pairs (threshold 64); the grouped product's chunk
-    forms where the other one would be picked."""
+    """The experts kernel where the grouped product would run (Q4_K: the int8 grouped product; Q8_0, Q6_K: the fp16
+    GEMM over each expert's chunks), in several passes per expert (40 tokens) and in its one-pass form (16 tokens);
+    the grouped product forced at a small batch; the bucketed path for a single token (mat-vec threshold 0); the
+    mat-vec path for 64 pairs (threshold 64); the Q4_K grouped product's chunk forms where the other one would be
+    picked (the fp16 GEMM keeps its one chunk size)."""
     with be.options(mmid_kernel=1):
-        y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=40, bcast=False, seed=0x5EED3600 + t)
-        assert rel_err(y, y_ref) <= TIGHT
+        y, ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=40, bcast=False, seed=0x5EED3600 + t)
+        ref.check(y)
     with be.options(mmid_kernel=2):
-        y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=16, bcast=True, seed=0x5EED3630 + t)
-        assert rel_err(y, y_ref) <= TIGHT
+        y, ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=16, bcast=True, seed=0x5EED3630 + t)
+        ref.check(y)
     with be.options(mmid_kernel=1):
-        y, y_ref = mmid_case(mx, be, t, E=64, K=2048, N=192, n_ids=4, T=16, bcast=True, seed=0x5EED3640 + t)
-        assert rel_err(y, y_ref) <= TIGHT
+        y, ref = mmid_case(mx, be, t, E=64, K=2048, N=192, n_ids=4, T=16, bcast=True, seed=0x5EED3640 + t)
+        ref.check(y)
     for chunk in (16, 32):  # the grouped product's one-tile form at 40 tokens, its two-tile form at 16
         with be.options(mmid_chunk=chunk):
-            y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=40 if chunk == 16 else 16, bcast=False,
-                                 seed=0x5EED3650 + t + chunk)
-            assert rel_err(y, y_ref) <= TIGHT, f"chunks of {chunk}"
+            y, ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=40 if chunk == 16 else 16, bcast=False,
+                               seed=0x5EED3650 + t + chunk)
+            ref.check(y, f"chunks of {chunk}")
     with be.options(mmid_matvec_pairs=0):
-        y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=1, bcast=True, seed=0x5EED3610 + t)
-        assert rel_err(y, y_ref) <= TIGHT
+        y, ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=1, bcast=True, seed=0x5EED3610 + t)
+        ref.check(y)
     with be.options(mmid_matvec_pairs=64):
-        y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=16, bcast=False, seed=0x5EED3620 + t)
-        assert rel_err(y, y_ref) <= TIGHT
+        y, ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=16, bcast=False, seed=0x5EED3620 + t)
+        ref.check(y)
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q5_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
+@pytest.mark.parametrize("tile", [(32, 128), (32, 64), (64, 64)], ids=lambda v: f"{v[0]}x{v[1]}")
+def test_mmid_dq_every_tile(mx, be, t, tile):
+    """The fp16 GEMM over expert chunks on each of its tiles (a chunk per row tile: 32 or 64 of an expert's pairs),
+    with experts of 0, 1, 31, 32, 33, 64, 65 and 100 pairs (full, ragged and several chunks), N not a multiple of the
+    column tile, b broadcast over the slots and per slot."""
+    counts = [1, 31, 0, 32, 33, 64, 65, 100]
+    ids = np.concatenate([np.full(c, e, np.int32) for e, c in enumerate(counts)])
+    np.random.default_rng(9).shuffle(ids)
+    with be.options(mmid_kernel=2, tile_m=tile[0], tile_n=tile[1]):
+        y, ref = mmid_case(mx, be, t, E=len(counts), K=1024, N=200, n_ids=1, T=len(ids), bcast=True,
+                           seed=0x5EED3700 + t, ids=ids.reshape(-1, 1))
+        ref.check(y, "b broadcast")
+        y, ref = mmid_case(mx, be, t, E=16, K=1536, N=136, n_ids=4, T=40, bcast=False, seed=0x5EED3710 + t)
+        ref.check(y, "b per slot")
 
 
 # --------------------------------------------------------------------------------------- refusals

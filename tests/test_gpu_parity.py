@@ -321,6 +321,43 @@ def test_supports_op(mx, be):
 
 
 # --------------------------------------------------------------------------------------------------- MUL_MAT_ID
+def mmid_uses_dq(t, K, npairs, E, kernel=0, matvec_pairs=16):
+    """Whether MUL_MAT_ID takes the dequantizing fp16 GEMM over chunks of each expert's pairs (its dispatch rule:
+    Q8_0 / Q5_K / Q6_K experts, more pairs than the mat-vec launch takes, on average at least one (Q8_0) or six
+    (K-quants) pairs per expert, or the GEMM forced; never when the experts kernel is forced)."""
+    if npairs <= matvec_pairs or kernel == 1 or not uses_dq(t, 9, K):
+        return False
+    return kernel == 2 or npairs >= (1 if t == O.TYPE_Q8_0 else 6) * E
+
+
+def mmid_dq_model(t, w, x, ids, K):
+    """dq_model for each expert's pairs: what the dequantizing GEMM computes for routed rows."""
+    T, n_ids = ids.shape
+    B = x.shape[1]
+    y = np.zeros((T, n_ids, w.shape[1]))
+    for e in np.unique(ids):
+        tt, ss = np.nonzero(ids == e)
+        y[tt, ss] = dq_model(O, t, w[e], x[tt, ss % B], K)
+    return y
+
+
+class MmidRef:
+    """The inputs of one MUL_MAT_ID and the bar its path is held to: the integer paths to TIGHT against the oracle;
+    the dequantizing fp16 GEMM to TOL against the oracle and to TIGHT against a model of its roundings."""
+
+    def __init__(self, t, w, x, ids, K, dq):
+        self.t, self.w, self.x, self.ids, self.K, self.dq = t, w, x, ids, K, dq
+
+    def check(self, y, what=""):
+        y_ref = O.mul_mat_id(self.t, self.w, self.x, self.ids)
+        if self.dq:
+            assert rel_err(y, y_ref) <= TOL, what
+            assert l2_rel(y, y_ref) <= TOL, what
+            assert rel_err(y, mmid_dq_model(self.t, self.w, self.x, self.ids, self.K)) <= TIGHT, what
+        else:
+            assert rel_err(y, y_ref) <= TIGHT, what
+
+
 def mmid_case(mx, be, t, E, K, N, n_ids, T, bcast, seed, skew=0.0, ids=None):
     w = weights(t, E * N, K, seed).reshape(E, N, -1)
     B = 1 if bcast else n_ids
@@ -337,23 +374,24 @@ def mmid_case(mx, be, t, E, K, N, n_ids, T, bcast, seed, skew=0.0, ids=None):
     be.mul_mat_id(Wt, Xt, It, Yt)
     be.sync()
     y = Yt.numpy().reshape(T, n_ids, N)
-    return y, O.mul_mat_id(t, w, x, ids)
+    dq = mmid_uses_dq(t, K, n_ids * T, E, be.get_option("mmid_kernel"), be.get_option("mmid_matvec_pairs"))
+    return y, MmidRef(t, w, x, ids, K, dq)
 
 
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
 @pytest.mark.parametrize("T", [1, 3, 16, 40])
 @pytest.mark.parametrize("bcast", [True, False], ids=["b_bcast", "b_per_slot"])
 def test_mul_mat_id(mx, be, t, T, bcast):
-    y, y_ref = mmid_case(mx, be, t, E=8, K=512, N=96, n_ids=2, T=T, bcast=bcast, seed=0x5EED0900 + T + t)
-    assert rel_err(y, y_ref) <= TIGHT
+    y, ref = mmid_case(mx, be, t, E=8, K=512, N=96, n_ids=2, T=T, bcast=bcast, seed=0x5EED0900 + T + t)
+    ref.check(y)
 
 
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
 @pytest.mark.parametrize("skew", [0.0, 3.0], ids=["spread", "skewed"])
 def test_mul_mat_id_many_pairs(mx, be, t, skew):
     """Experts with more than 16 pairs (several tiles, a ragged last one) and N not a multiple of the column tile."""
-    y, y_ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=70, bcast=False, seed=0x5EED0A00 + t, skew=skew)
-    assert rel_err(y, y_ref) <= TIGHT
+    y, ref = mmid_case(mx, be, t, E=16, K=1024, N=200, n_ids=4, T=70, bcast=False, seed=0x5EED0A00 + t, skew=skew)
+    ref.check(y)
 
 
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
@@ -366,34 +404,35 @@ def test_mul_mat_id_chunk_edges(mx, be, t, chunk):
     ids = np.concatenate([np.full(c, e, np.int32) for e, c in enumerate(counts)])
     np.random.default_rng(7).shuffle(ids)
     with be.options(mmid_chunk=chunk):
-        y, y_ref = mmid_case(mx, be, t, E=len(counts), K=2048, N=136, n_ids=1, T=len(ids), bcast=True,
-                             seed=0x5EED0B00 + t, ids=ids.reshape(-1, 1))
-    assert rel_err(y, y_ref) <= TIGHT
+        y, ref = mmid_case(mx, be, t, E=len(counts), K=2048, N=136, n_ids=1, T=len(ids), bcast=True,
+                           seed=0x5EED0B00 + t, ids=ids.reshape(-1, 1))
+    ref.check(y)
 
 
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
 def test_mul_mat_id_past_held_pairs(mx, be, t):
     """2,400 (token, slot) pairs: the bucketing pass keeps a thread's first eight pairs' experts in registers (2,048
     pairs over its 256 threads) and reads the rest again for its second pass."""
-    y, y_ref = mmid_case(mx, be, t, E=8, K=256, N=40, n_ids=4, T=600, bcast=True, seed=0x5EED0F00 + t)
-    assert rel_err(y, y_ref) <= TIGHT
+    y, ref = mmid_case(mx, be, t, E=8, K=256, N=40, n_ids=4, T=600, bcast=True, seed=0x5EED0F00 + t)
+    ref.check(y)
 
 
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
 def test_mul_mat_id_long_rows(mx, be, t):
-    """K = 4096, past what the grouped Q4_K product keeps in LDS: the experts kernel by default, in one pass (20
-    tokens over 16 experts) and in several passes of eight pairs (40 tokens over 4 experts, ~20 pairs each)."""
+    """K = 4096, past what the grouped Q4_K product keeps in LDS: for Q4_K the experts kernel by default, in one pass
+    (20 tokens over 16 experts) and in several passes of eight pairs (40 tokens over 4 experts, ~20 pairs each); the
+    other types on the fp16 GEMM over chunks of each expert's pairs, at the same shapes."""
     for E, T, seed in ((16, 20, 0x5EED0E00), (4, 40, 0x5EED0E40)):
-        y, y_ref = mmid_case(mx, be, t, E=E, K=4096, N=72, n_ids=2, T=T, bcast=False, seed=seed + t)
-        assert rel_err(y, y_ref) <= TIGHT, f"E {E}, T {T}"
+        y, ref = mmid_case(mx, be, t, E=E, K=4096, N=72, n_ids=2, T=T, bcast=False, seed=seed + t)
+        ref.check(y, f"E {E}, T {T}")
 
 
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
 def test_mul_mat_id_moe_layer_shape(mx, be, t):
     """The drama3-like layer's down product (64 experts, top-4 of 64 tokens, K = 1536, b per slot) on 520 of its
     2048 output rows."""
-    y, y_ref = mmid_case(mx, be, t, E=64, K=1536, N=520, n_ids=4, T=64, bcast=False, seed=0x5EED0C00 + t)
-    assert rel_err(y, y_ref) <= TIGHT
+    y, ref = mmid_case(mx, be, t, E=64, K=1536, N=520, n_ids=4, T=64, bcast=False, seed=0x5EED0C00 + t)
+    ref.check(y)
 
 
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
@@ -401,8 +440,8 @@ def test_mul_mat_id_moe_layer_shape(mx, be, t):
 def test_mul_mat_id_group(mx, be, t, T):
     """Gate and up experts over the same rows and ids in one call (mx_mul_mat_id_group): each product the same bits as
     its own mx_mul_mat_id -- one mat-vec launch for both at 2 tokens, the grouped product's two forms at 16 and 40
-    (Q4_K), one experts-kernel launch per product after a shared prep (Q8_0, Q6_K) -- and within the bar of the
-    oracle."""
+    (Q4_K), one launch of the fp16 GEMM over each expert's chunks for both products after a shared prep (Q8_0, Q5_K,
+    Q6_K) -- and within its path's bar against the oracle."""
     E, K, N, n_ids = 16, 1024, 200, 4
     seed = 0x5EED0D00 + 64 * T + t
     wg = weights(t, E * N, K, seed).reshape(E, N, -1)
@@ -420,9 +459,10 @@ def test_mul_mat_id_group(mx, be, t, T):
     be.mul_mat_id(Wu, Xt, It, Ys[1])
     be.mul_mat_id_group([Wg, Wu], Xt, It, Yg)
     be.sync()
+    dq = mmid_uses_dq(t, K, n_ids * T, E)
     for a, b, w in zip(Ys, Yg, (wg, wu)):
         assert np.array_equal(a.numpy(), b.numpy())
-        assert rel_err(b.numpy().reshape(T, n_ids, N), O.mul_mat_id(t, w, x, ids)) <= TIGHT
+        MmidRef(t, w, x, ids, K, dq).check(b.numpy().reshape(T, n_ids, N))
 
 
 _MOE_FULL = {}

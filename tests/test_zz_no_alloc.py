@@ -1,8 +1,8 @@
 """MUL_MAT_ID through the entry point that allocates nothing (mx_mul_mat_id_noalloc: its scratch a static device
 array per GPU) against mx_mul_mat_id on the same inputs: the same kernels, so the same bits, on two calls in a row
-(the second smaller, so it runs on what the first left in the shared array), for Q4_K experts (the grouped MFMA
-kernel) and Q8_0 experts (the generic kernel), and for 16 or fewer pairs (the mat-vec launch); both held to the
-oracle. Recorded into a graph -- what a caller that cannot allocate does -- and replayed with new inputs between the
+(the second smaller, so it runs on what the first left in the shared array), for Q4_K experts (the grouped int8
+MFMA kernel) and Q8_0 experts (the fp16 dequantizing GEMM over each expert's chunks), and for 16 or fewer pairs (the
+mat-vec launch); both held to the oracle at their paths' bars. Recorded into a graph -- what a caller that cannot allocate does -- and replayed with new inputs between the
 replays, each replay matches the allocating entry point. A call needing more than the array holds is refused before
 anything runs, and inputs MUL_MAT_ID does not take never size as fitting."""
 import numpy as np
@@ -10,6 +10,7 @@ import pytest
 
 import oracle as O
 from helpers import bits_equal, rel_err
+from test_gpu_parity import MmidRef, mmid_uses_dq
 
 pytestmark = pytest.mark.gpu
 
@@ -41,7 +42,7 @@ def test_mul_mat_id_noalloc_matches_the_allocating_entry_point(mx, be, t):
         ya = Ya.numpy().reshape(T, n_ids, N)
         yn = Yn.numpy().reshape(T, n_ids, N)
         assert bits_equal(yn, ya), f"T = {T}"
-        assert rel_err(yn, O.mul_mat_id(t, w, x, ids)) <= TIGHT
+        MmidRef(t, w, x, ids, K, mmid_uses_dq(t, K, n_ids * T, E)).check(yn, f"T = {T}")
 
 
 @pytest.mark.parametrize("pairs", [(24, 4), (4, 4)], ids=["grouped", "matvec"])
