@@ -124,7 +124,7 @@ MX_API int mx_backend_set_rounding(mx_backend *be, int rounding);
  *   MX_OPT_MATVEC_LPR         lanes per weight row of the mat-vec: 0 (picked), 16, 32, 64
  *   MX_OPT_MMID_KERNEL        MUL_MAT_ID with many pairs: 0 as picked (Q4_K: the grouped int8 MFMA product; Q8_0,
  *                             Q5_K, Q6_K: the fp16 dequantizing GEMM over chunks of each expert's pairs from one /
- *                             six pairs per expert on average, else the experts kernel), 1 the experts kernel, 2 the
+ *                             three pairs per expert on average, else the experts kernel), 1 the experts kernel, 2 the
  *                             grouped product (Q4_K int8, the other types the fp16 GEMM over the chunks)
  *   MX_OPT_MMID_MATVEC_PAIRS  MUL_MAT_ID runs as one mat-vec launch up to this many (token, slot) pairs (16; 0..4096)
  *   MX_OPT_MMID_CHUNK         pairs per chunk of an expert's pairs in the grouped Q4_K product: 0 as picked (16 when

@@ -45,6 +45,9 @@ typedef __attribute__((address_space(3))) void dq_lds;
 #ifndef MX_DQ_DIRECT_B
 #define MX_DQ_DIRECT_B 1  // Q8_0: B fragments converted in registers from the raw codes (0: through an fp16 LDS tile)
 #endif
+#ifndef MX_DQ_DIRECT_B6
+#define MX_DQ_DIRECT_B6 1  // Q6_K likewise, from the raw ql / qh bytes, scales and d (0: through an fp16 LDS tile)
+#endif
 #ifndef MX_DQ_Q8_WGM128
 #define MX_DQ_Q8_WGM128 1  // Q8_0 128 x 128 tiles: waves across M (1: four waves of 128 x 32; 2: eight of 64 x 32)
 #endif
@@ -67,8 +70,9 @@ constexpr int DQ_KS = 64;  // K per stage
 template <int WT, int BM, int BN, int NW, bool RT = false>
 struct DqLds {
     static constexpr bool K6 = WT == MX_TYPE_Q6_K, K5 = WT == MX_TYPE_Q5_K;
-    // Q8_0 with direct B: each wave converts its B fragments from the raw codes, so there is no fp16 weight tile
-    static constexpr bool DIRB = MX_DQ_DIRECT_B && !K6 && !K5;
+    // Q8_0 and Q6_K with direct B: each wave converts its B fragments from the raw bytes, so there is no fp16 weight
+    // tile
+    static constexpr bool DIRB = (MX_DQ_DIRECT_B && !K6 && !K5) || (MX_DQ_DIRECT_B6 && K6);
     // ring stages: the copies run NS - 1 stages ahead of the matrix cores
     static constexpr int NS = DIRB ? MX_DQ_NS_DIRB : 4;
     // raw bytes per weight row and stage: codes (Q8_0 codes, Q6_K ql, Q5_K qs), qh, scales, d
@@ -465,7 +469,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
 #pragma unroll
     for (int jj = 0; jj < L::PH; jj++) {
         const int j = wave * L::PH + jj, row = 32 * min(j, L::NH - 1) + (lane >> 1);
-        hsrc[jj] = p.w.p1 + (wrow0 + min(n0 + row, N - 1)) * nsb * (L::K5 ? 32 : 64) + 16 * (lane & 1);
+        // direct B: row r's qh chunk c lands at chunk c ^ ((r >> 3) & 1), so the 16 rows of a read's lane group
+        // cover all 64 banks
+        const int hc = L::DIRB ? (lane & 1) ^ ((row >> 3) & 1) : lane & 1;
+        hsrc[jj] = p.w.p1 + (wrow0 + min(n0 + row, N - 1)) * nsb * (L::K5 ? 32 : 64) + 16 * hc;
         hdst[jj] = j < L::NH ? L::QH + j * 1024 : L::JUNK + wave * L::JB;
     }
     const uint8_t *ssrc[L::PS];
@@ -655,15 +662,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
         }
     }
     // direct B: this lane's raw chunk 2 kk2 + fh of row wn + fr, swizzled as the copies placed it, and its scale word
+    // (Q6_K: also its qh chunk fh and d pair, and the row's first super-block index in the d plane)
     const int brow = wn + fr;
     const uint32_t boffd0 = brow * L::RB + 16 * ((0 + fh) ^ ((brow >> 2) & 3));
     const uint32_t boffd1 = brow * L::RB + 16 * ((2 + fh) ^ ((brow >> 2) & 3));
+    const uint32_t hoffd = brow * 32 + 16 * (fh ^ ((brow >> 3) & 1));
+    const int64_t erow = (wrow0 + min(n0 + brow, N - 1)) * nsb;
 
     if constexpr (L::DIRB) {
         // The LDS address of every fragment read, per ring slot: the loop is unrolled over the slots, so a stage runs
         // no address arithmetic (the registers are there to spare: two workgroups of four waves per CU).
         static_assert(L::NS == 3, "the direct-B loop is unrolled over a three-stage ring");
-        uint32_t adS[L::NS][8], aeS[L::NS][8], bS0[L::NS], bS1[L::NS], scS[L::NS];
+        uint32_t adS[L::NS][8], aeS[L::NS][8], bS0[L::NS], bS1[L::NS], scS[L::NS], hS[L::NS], dS[L::NS];
 #pragma unroll
         for (int sl = 0; sl < L::NS; sl++) {
             const uint32_t at = lds + L::A + sl * BM * 128, rt = lds + L::RAW + sl * BN * L::RB;
@@ -680,6 +690,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             bS0[sl] = rt + boffd0;
             bS1[sl] = rt + boffd1;
             scS[sl] = lds + L::SC + sl * BN * L::SB + brow * L::SB;
+            hS[sl] = lds + L::QH + sl * BN * 32 + hoffd;
+            dS[sl] = lds + L::DD + sl * BN * 4 + brow * 4;
         }
         auto stage = [&](auto slot, int s) {
             constexpr int SL = decltype(slot)::value;  // == s % L::NS
@@ -689,16 +701,30 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             dq_wait_vm<(L::NS - 2) * L::OPS>();
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             v8h fa[8], fb[16];
-            v4i braw[2];
-            uint32_t sw;
+            v4i braw[2], qh = {0, 0, 0, 0};
+            uint32_t sw, dw = 0;
+            if constexpr (L::K6)  // Q6_K's qh chunk and d pair: landed with the reads below (their wait covers these)
+                asm volatile("ds_read_b128 %0, %2\n\tds_read_b32 %1, %3" : "=&v"(qh), "=&v"(dw) : "v"(hS[SL]), "v"(dS[SL])
+                             : "memory");
             dq_read_ab<TM == 4 ? 2 : TM>(fa, braw, sw, adS[SL], bS0[SL], bS1[SL], scS[SL]);
+            if constexpr (L::K6) asm volatile("" : "+v"(qh), "+v"(dw));  // no use before that wait
+            // 16 raw values -> two K steps of B fragments: chunk kk2 of the stage (Q8_0: block kk2; Q6_K: values
+            // 32 kk2 + 16 fh .. of the quarter, sub-block 4 (g & 3) + 2 kk2 + fh, qh bits 4 (g & 1) + 2 kk2)
+            const int g = sb + s, gsh = (g & 1) * 4;
+            auto conv = [&](int kk2, v4i &o0, v4i &o1) {
+                if constexpr (L::K6) {
+                    const uint16_t d6 = ((erow + (g >> 2)) & 1) ? (uint16_t)(dw >> 16) : (uint16_t)(dw & 0xFFFF);
+                    dq_q6_k_16(braw[kk2], qh, gsh + 2 * kk2, gsh, (int8_t)(sw >> (8 * (2 * kk2 + fh))), d6, o0, o1);
+                } else
+                    dq_q8_0_16(braw[kk2], (uint16_t)(kk2 ? sw >> 16 : sw & 0xFFFF), o0, o1);
+            };
             v4i bq[4];  // K steps 2 kk2 and 2 kk2 + 1 from chunk kk2 (block kk2 of the stage)
             if constexpr (TM == 4 && MX_DQ_HALF) {
                 // K steps 2 and 3: their A fragments are read, and chunk 1 converted, while steps 0 and 1 run
                 dq_issue8(fb, aeS[SL]);
 #pragma unroll
                 for (int x = 0; x < 8; x++) asm volatile("" : "+v"(fa[x]));  // steps 0 and 1 stay behind the reads
-                dq_q8_0_16(braw[0], (uint16_t)(sw & 0xFFFF), bq[0], bq[1]);
+                conv(0, bq[0], bq[1]);
 #pragma unroll
                 for (int kk = 0; kk < 2; kk++)
 #pragma unroll
@@ -706,7 +732,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
                         acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[kk * TM + i],
                                                                             __builtin_bit_cast(v8h, bq[kk]), acc[i][0],
                                                                             0, 0, 0);
-                dq_q8_0_16(braw[1], (uint16_t)(sw >> 16), bq[2], bq[3]);
+                conv(1, bq[2], bq[3]);
                 dq_wait8(fb);
 #pragma unroll
                 for (int kk = 2; kk < 4; kk++)
@@ -722,8 +748,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
                     for (int x = 0; x < 16; x++) ae16[x] = x < 8 ? aeS[SL][x] : 0;
                     dq_read<8>(fb, ae16);
                 }
-                dq_q8_0_16(braw[0], (uint16_t)(sw & 0xFFFF), bq[0], bq[1]);
-                dq_q8_0_16(braw[1], (uint16_t)(sw >> 16), bq[2], bq[3]);
+                conv(0, bq[0], bq[1]);
+                conv(1, bq[2], bq[3]);
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++)
 #pragma unroll
@@ -872,7 +898,8 @@ DqPlan dq_plan(int type, int nprob, const int64_t *N, int64_t M, int64_t K, cons
     DqPlan pl{64, 64, 1, 0};
     // Q8_0 with direct B also has a 32 x 128 tile of four 32 x 32 waves, for blocks of at most 32 rows (the last,
     // short block of a prompt): half the activation rows of a 64-row tile, so half its fragment reads and MFMAs
-    const bool skinny_ok = type == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B && MX_DQ_Q8_WGM128 == 1;
+    const bool skinny_ok = (type == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B && MX_DQ_Q8_WGM128 == 1) ||
+                           (type == MX_TYPE_Q6_K && MX_DQ_DIRECT_B6);
     int64_t wg128 = 0;
     for (int i = 0; i < nprob; i++) {
         wg128 += (N[i] + 127) / 128;
@@ -966,7 +993,7 @@ static hipError_t launch_dq(const DqArgs &a, int maxN, hipStream_t s, int gy = 0
 
 template <int WT>
 static hipError_t launch_dq_type(const DqArgs &a, const DqPlan &pl, int maxN, hipStream_t s) {
-    if constexpr (WT == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B && MX_DQ_Q8_WGM128 == 1) {
+    if constexpr ((WT == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B && MX_DQ_Q8_WGM128 == 1) || (WT == MX_TYPE_Q6_K && MX_DQ_DIRECT_B6)) {
         // direct B: four waves of 128 x 32, so every B fragment is converted by one wave only
         if (pl.bm == 128 && pl.bn == 128) return launch_dq<WT, 128, 128, 1, 4>(a, maxN, s);
         if (pl.bm == 32) return launch_dq<WT, 32, 128, 1, 4>(a, maxN, s);
@@ -1021,11 +1048,13 @@ static hipError_t dq_routed(const DqArgs &a, int tile, int maxN, int gy, hipStre
     }
 }
 
-// The routed form's tile: Q8_0 32 x 128, the K-quants 64 x 64, unless a backend's tile option forces one the form has
+// The routed form's tile: 32 x 128 for the direct-B types (Q8_0, Q6_K; measured for Q6_K at 256 tokens over 64 experts:
+// 252 us per layer against 311 on 64 x 64), 64 x 64 for Q5_K, unless a backend's tile option forces one the form has
 // (32 x 128, 32 x 64 or 64 x 64; 0 x 0 if it has not). Its rows are a chunk's.
 static void dq_routed_tile(const MulMatIdArgs &m, int &bm, int &bn) {
-    bm = m.type == MX_TYPE_Q8_0 ? 32 : 64;
-    bn = m.type == MX_TYPE_Q8_0 ? 128 : 64;
+    const bool dirb = (m.type == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B) || (m.type == MX_TYPE_Q6_K && MX_DQ_DIRECT_B6);
+    bm = dirb ? 32 : 64;
+    bn = dirb ? 128 : 64;
     if (m.tile_m || m.tile_n) {
         const bool ok = (m.tile_m == 32 && (m.tile_n == 128 || m.tile_n == 64)) || (m.tile_m == 64 && m.tile_n == 64);
         bm = ok ? m.tile_m : 0;

@@ -225,14 +225,15 @@ __global__ __launch_bounds__(256) void k_mmid_prep_dq(MulMatIdArgs a) {
 // Q8_0 / Q5_K / Q6_K experts go to the fp16 dequantizing GEMM over the chunks once their pairs share each expert's
 // weights enough: measured over 64 experts of 2048 x 1536 (top-4, us per layer, the GEMM against the experts kernel),
 // Q8_0 from one pair per expert on average (16 tokens: 130 against 130; 32: 171 against 203; 256: 200 against
-// 1,235), the K-quants from six (Q6_K at 64 tokens, four per expert: 291 against 279; 128 tokens: 301 against 509;
-// 256: 302 against 983). An option forces the experts kernel (1) or the GEMM (2, wherever it takes the rows' K).
+// 1,235), the K-quants from three (Q6_K at 32 tokens, two per expert: 221 against 182; 64 tokens: 243 against 280;
+// 256: 252 against 983; Q5_K 278 / 233 and 308 / 373). An option forces the experts kernel (1) or the GEMM (2,
+// wherever it takes the rows' K).
 bool mmid_dq_route(const MulMatIdArgs &a) {
     if (a.type != MX_TYPE_Q8_0 && a.type != MX_TYPE_Q5_K && a.type != MX_TYPE_Q6_K) return false;
     if (a.generic == 1 || !gemm_dq_supported(a.type, a.T * a.b_ne1, a.K)) return false;
     if (a.generic == 2) return true;
     const int64_t npairs = a.n_ids * a.T;
-    return npairs >= (a.type == MX_TYPE_Q8_0 ? 1 : 6) * a.E;
+    return npairs >= (a.type == MX_TYPE_Q8_0 ? 1 : 3) * a.E;
 }
 
 

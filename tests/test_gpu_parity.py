@@ -323,11 +323,11 @@ def test_supports_op(mx, be):
 # --------------------------------------------------------------------------------------------------- MUL_MAT_ID
 def mmid_uses_dq(t, K, npairs, E, kernel=0, matvec_pairs=16):
     """Whether MUL_MAT_ID takes the dequantizing fp16 GEMM over chunks of each expert's pairs (its dispatch rule:
-    Q8_0 / Q5_K / Q6_K experts, more pairs than the mat-vec launch takes, on average at least one (Q8_0) or six
+    Q8_0 / Q5_K / Q6_K experts, more pairs than the mat-vec launch takes, on average at least one (Q8_0) or three
     (K-quants) pairs per expert, or the GEMM forced; never when the experts kernel is forced)."""
     if npairs <= matvec_pairs or kernel == 1 or not uses_dq(t, 9, K):
         return False
-    return kernel == 2 or npairs >= (1 if t == O.TYPE_Q8_0 else 6) * E
+    return kernel == 2 or npairs >= (1 if t == O.TYPE_Q8_0 else 3) * E
 
 
 def mmid_dq_model(t, w, x, ids, K):
