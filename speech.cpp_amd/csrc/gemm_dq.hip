@@ -48,6 +48,9 @@ typedef __attribute__((address_space(3))) void dq_lds;
 #ifndef MX_DQ_DIRECT_B6
 #define MX_DQ_DIRECT_B6 1  // Q6_K likewise, from the raw ql / qh bytes, scales and d (0: through an fp16 LDS tile)
 #endif
+#ifndef MX_DQ_DIRECT_B5
+#define MX_DQ_DIRECT_B5 1  // Q5_K likewise, from the raw qs / qh bytes, scales and d | dmin
+#endif
 #ifndef MX_DQ_Q8_WGM128
 #define MX_DQ_Q8_WGM128 1  // Q8_0 128 x 128 tiles: waves across M (1: four waves of 128 x 32; 2: eight of 64 x 32)
 #endif
@@ -72,7 +75,7 @@ struct DqLds {
     static constexpr bool K6 = WT == MX_TYPE_Q6_K, K5 = WT == MX_TYPE_Q5_K;
     // Q8_0 and Q6_K with direct B: each wave converts its B fragments from the raw bytes, so there is no fp16 weight
     // tile
-    static constexpr bool DIRB = (MX_DQ_DIRECT_B && !K6 && !K5) || (MX_DQ_DIRECT_B6 && K6);
+    static constexpr bool DIRB = (MX_DQ_DIRECT_B && !K6 && !K5) || (MX_DQ_DIRECT_B6 && K6) || (MX_DQ_DIRECT_B5 && K5);
     // ring stages: the copies run NS - 1 stages ahead of the matrix cores
     static constexpr int NS = DIRB ? MX_DQ_NS_DIRB : 4;
     // raw bytes per weight row and stage: codes (Q8_0 codes, Q6_K ql, Q5_K qs), qh, scales, d
@@ -458,9 +461,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
         constexpr int LR = L::RB / 16;  // lanes per code row
         const int j = wave * L::PC + jj, row = (64 / LR) * min(j, L::NC - 1) + lane / LR;
         const int64_t grow = wrow0 + min(n0 + row, N - 1);
-        // direct B: row r's chunk c lands at chunk c ^ ((r >> 2) & 3), so the 16 rows a fragment read's lane group
-        // touches cover all 64 banks
-        const int cc = L::DIRB ? (lane % LR) ^ ((row >> 2) & 3) : lane % LR;
+        // direct B: row r's chunk c lands at chunk c ^ ((r >> 2) & 3) (64-byte rows; 32-byte Q5_K rows: c ^ ((r >> 3)
+        // & 1)), so the 16 rows a fragment read's lane group touches cover all 64 banks
+        const int cc = !L::DIRB ? lane % LR : L::RB == 64 ? (lane % LR) ^ ((row >> 2) & 3) : (lane % LR) ^ ((row >> 3) & 1);
         csrc[jj] = (L::K6 || L::K5 ? p.w.p0 + grow * nsb * 128 : p.w.p0 + grow * K + sb * DQ_KS) + 16 * cc;
         cdst[jj] = j < L::NC ? L::RAW + j * 1024 : L::JUNK + wave * L::JB;
     }
@@ -664,8 +667,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     // direct B: this lane's raw chunk 2 kk2 + fh of row wn + fr, swizzled as the copies placed it, and its scale word
     // (Q6_K: also its qh chunk fh and d pair, and the row's first super-block index in the d plane)
     const int brow = wn + fr;
-    const uint32_t boffd0 = brow * L::RB + 16 * ((0 + fh) ^ ((brow >> 2) & 3));
-    const uint32_t boffd1 = brow * L::RB + 16 * ((2 + fh) ^ ((brow >> 2) & 3));
+    // (Q5_K: its one qs chunk fh serves both K-step pairs, as low and high nibbles)
+    const uint32_t boffd0 = L::RB == 64 ? brow * L::RB + 16 * ((0 + fh) ^ ((brow >> 2) & 3))
+                                        : brow * L::RB + 16 * (fh ^ ((brow >> 3) & 1));
+    const uint32_t boffd1 = L::RB == 64 ? brow * L::RB + 16 * ((2 + fh) ^ ((brow >> 2) & 3)) : boffd0;
     const uint32_t hoffd = brow * 32 + 16 * (fh ^ ((brow >> 3) & 1));
     const int64_t erow = (wrow0 + min(n0 + brow, N - 1)) * nsb;
 
@@ -691,7 +696,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             bS1[sl] = rt + boffd1;
             scS[sl] = lds + L::SC + sl * BN * L::SB + brow * L::SB;
             hS[sl] = lds + L::QH + sl * BN * 32 + hoffd;
-            dS[sl] = lds + L::DD + sl * BN * 4 + brow * 4;
+            dS[sl] = lds + L::DD + sl * BN * 4 + brow * 4;  // Q6_K: the d pair holding the row's; Q5_K: d | dmin
         }
         auto stage = [&](auto slot, int s) {
             constexpr int SL = decltype(slot)::value;  // == s % L::NS
@@ -702,19 +707,33 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             v8h fa[8], fb[16];
             v4i braw[2], qh = {0, 0, 0, 0};
-            uint32_t sw, dw = 0;
-            if constexpr (L::K6)  // Q6_K's qh chunk and d pair: landed with the reads below (their wait covers these)
+            uint32_t sw, dw = 0, s1 = 0, s2 = 0;
+            // the K-quants' qh chunk and d word (Q5_K: and scale words 1, 2): landed with the reads below, whose wait
+            // covers these
+            if constexpr (L::K6)
                 asm volatile("ds_read_b128 %0, %2\n\tds_read_b32 %1, %3" : "=&v"(qh), "=&v"(dw) : "v"(hS[SL]), "v"(dS[SL])
                              : "memory");
+            if constexpr (L::K5)
+                asm volatile("ds_read_b128 %0, %4\n\tds_read_b32 %1, %5\n\tds_read_b32 %2, %6 offset:4\n\t"
+                             "ds_read_b32 %3, %6 offset:8"
+                             : "=&v"(qh), "=&v"(dw), "=&v"(s1), "=&v"(s2)
+                             : "v"(hS[SL]), "v"(dS[SL]), "v"(scS[SL])
+                             : "memory");
             dq_read_ab<TM == 4 ? 2 : TM>(fa, braw, sw, adS[SL], bS0[SL], bS1[SL], scS[SL]);
-            if constexpr (L::K6) asm volatile("" : "+v"(qh), "+v"(dw));  // no use before that wait
+            if constexpr (L::K6 || L::K5) asm volatile("" : "+v"(qh), "+v"(dw), "+v"(s1), "+v"(s2));  // no use before that wait
             // 16 raw values -> two K steps of B fragments: chunk kk2 of the stage (Q8_0: block kk2; Q6_K: values
-            // 32 kk2 + 16 fh .. of the quarter, sub-block 4 (g & 3) + 2 kk2 + fh, qh bits 4 (g & 1) + 2 kk2)
+            // 32 kk2 + 16 fh .. of the quarter, sub-block 4 (g & 3) + 2 kk2 + fh, qh bits 4 (g & 1) + 2 kk2; Q5_K: the
+            // same values, sub-block 2 (g & 3) + kk2: qs nibble kk2, qh bit the sub-block)
             const int g = sb + s, gsh = (g & 1) * 4;
             auto conv = [&](int kk2, v4i &o0, v4i &o1) {
                 if constexpr (L::K6) {
                     const uint16_t d6 = ((erow + (g >> 2)) & 1) ? (uint16_t)(dw >> 16) : (uint16_t)(dw & 0xFFFF);
                     dq_q6_k_16(braw[kk2], qh, gsh + 2 * kk2, gsh, (int8_t)(sw >> (8 * (2 * kk2 + fh))), d6, o0, o1);
+                } else if constexpr (L::K5) {
+                    const int sub = 2 * (g & 3) + kk2;
+                    int scv, mv;
+                    q4k_scale_min(sw, s1, s2, sub, scv, mv);
+                    dq_q5_k_16(braw[0], qh, sub, 4 * kk2, scv, mv, dw, o0, o1);
                 } else
                     dq_q8_0_16(braw[kk2], (uint16_t)(kk2 ? sw >> 16 : sw & 0xFFFF), o0, o1);
             };
@@ -899,7 +918,7 @@ DqPlan dq_plan(int type, int nprob, const int64_t *N, int64_t M, int64_t K, cons
     // Q8_0 with direct B also has a 32 x 128 tile of four 32 x 32 waves, for blocks of at most 32 rows (the last,
     // short block of a prompt): half the activation rows of a 64-row tile, so half its fragment reads and MFMAs
     const bool skinny_ok = (type == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B && MX_DQ_Q8_WGM128 == 1) ||
-                           (type == MX_TYPE_Q6_K && MX_DQ_DIRECT_B6);
+                           (type == MX_TYPE_Q6_K && MX_DQ_DIRECT_B6) || (type == MX_TYPE_Q5_K && MX_DQ_DIRECT_B5);
     int64_t wg128 = 0;
     for (int i = 0; i < nprob; i++) {
         wg128 += (N[i] + 127) / 128;
@@ -993,7 +1012,8 @@ static hipError_t launch_dq(const DqArgs &a, int maxN, hipStream_t s, int gy = 0
 
 template <int WT>
 static hipError_t launch_dq_type(const DqArgs &a, const DqPlan &pl, int maxN, hipStream_t s) {
-    if constexpr ((WT == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B && MX_DQ_Q8_WGM128 == 1) || (WT == MX_TYPE_Q6_K && MX_DQ_DIRECT_B6)) {
+    if constexpr ((WT == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B && MX_DQ_Q8_WGM128 == 1) || (WT == MX_TYPE_Q6_K && MX_DQ_DIRECT_B6) ||
+                  (WT == MX_TYPE_Q5_K && MX_DQ_DIRECT_B5)) {
         // direct B: four waves of 128 x 32, so every B fragment is converted by one wave only
         if (pl.bm == 128 && pl.bn == 128) return launch_dq<WT, 128, 128, 1, 4>(a, maxN, s);
         if (pl.bm == 32) return launch_dq<WT, 32, 128, 1, 4>(a, maxN, s);
@@ -1052,7 +1072,8 @@ static hipError_t dq_routed(const DqArgs &a, int tile, int maxN, int gy, hipStre
 // 252 us per layer against 311 on 64 x 64), 64 x 64 for Q5_K, unless a backend's tile option forces one the form has
 // (32 x 128, 32 x 64 or 64 x 64; 0 x 0 if it has not). Its rows are a chunk's.
 static void dq_routed_tile(const MulMatIdArgs &m, int &bm, int &bn) {
-    const bool dirb = (m.type == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B) || (m.type == MX_TYPE_Q6_K && MX_DQ_DIRECT_B6);
+    const bool dirb = (m.type == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B) || (m.type == MX_TYPE_Q6_K && MX_DQ_DIRECT_B6) ||
+                      (m.type == MX_TYPE_Q5_K && MX_DQ_DIRECT_B5);
     bm = dirb ? 32 : 64;
     bn = dirb ? 128 : 64;
     if (m.tile_m || m.tile_n) {
