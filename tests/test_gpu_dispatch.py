@@ -99,13 +99,13 @@ def test_dq_gemm_every_tile_and_split(mx, be, t):
             check_product(t, ws[0], x, y, K, y_ref=refs[0])
 
 
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q5_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
 @pytest.mark.parametrize("M", [28, 9, 40])
-def test_dq_gemm_q8_0_short_blocks(mx, be, M):
-    """Q8_0 blocks of at most 32 rows (a prompt's last, short block: 28 rows of the 1564-row ASR prompt) take the
-    32 x 128 tile with K split so that about 512 workgroups stream the weights; it is held to the same model of the fp16
-    GEMM at its picked split and at forced ones (one split; three; a ragged N), and at 40 rows (two row tiles) when
-    forced."""
-    t = O.TYPE_Q8_0
+def test_dq_gemm_short_blocks(mx, be, t, M):
+    """Blocks of at most 32 rows (a prompt's last, short block: 28 rows of the 1564-row ASR prompt) take the 32 x 128
+    tile of the direct-B types with K split so that about 256 workgroups stream the weights; it is held to the same
+    model of the fp16 GEMM at its picked split and at forced ones (one split; three; a ragged N), and at 40 rows (two
+    row tiles) when forced."""
     for N, K in ((1000, 2048), (2048, 6144), (333, 1024)):
         ws, x, refs = case(t, M, [N], K, 0x5EED3500 + M + N)
         for split in ((0, 1, 3) if M <= 32 else (0,)):
