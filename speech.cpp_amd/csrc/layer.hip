@@ -329,11 +329,9 @@ __device__ __forceinline__ void fa_merge_head(const FaArgs &a, int64_t h, int64_
     constexpr int DL = D / 64, NB = 64 / DL;  // NB splits' channels per round of loads (64 registers)
     const int ns = a.nsplit;
     const float *part = a.part + (i * a.n_head + h) * ns * (D + 2);
-    float ms = -INFINITY, ss = 0.0f;
-    if (lane < ns) {
-        ms = part[lane * (D + 2)];
-        ss = part[lane * (D + 2) + 1];
-    }
+    // every lane loads (lanes past the splits read the last one's and then drop it): a load under a branch is waited
+    // for at the branch's join, before the first round's loads below would be issued
+    float ms = part[min(lane, ns - 1) * (D + 2)], ss = part[min(lane, ns - 1) * (D + 2) + 1];
     float v[NB][DL];
     auto gather = [&](int s0) {
 #pragma unroll
@@ -343,7 +341,12 @@ __device__ __forceinline__ void fa_merge_head(const FaArgs &a, int64_t h, int64_
             for (int c = 0; c < DL; c++) v[u][c] = part[sp * (D + 2) + 2 + DL * lane + c];
         }
     };
-    gather(0);  // the first round's loads travel with the maxima's
+    gather(0);  // the first round's loads travel with the maxima's: the asm, after them, is the maxima's first use
+    asm volatile("" : "+v"(ms), "+v"(ss)::"memory");
+    if (lane >= ns) {
+        ms = -INFINITY;
+        ss = 0.0f;
+    }
     const float M = wave_max_f(ms);
     const float w = (ms == -INFINITY) ? 0.0f : expf(ms - M);  // a split with nothing visible weighs 0
     const float S = wave_sum_f(ss * w);
@@ -371,18 +374,20 @@ __global__ __launch_bounds__(64) void k_fa_merge(FaArgs a) {
 }
 
 // One 64-position chunk of 256-byte K and V rows for 256 threads: thread t copies 16 bytes of rows t / 16 + 16 u,
-// threads 0..63 the mask of position t. Rows past j1 repeat row j1 - 1 and are masked.
+// threads 0..63 the mask of position t, kept as its f16 bits until the chunk is staged (converted at the load, its
+// wait would hold the thread until every load of the chunk had landed). Rows past j1 repeat row j1 - 1 and are
+// masked (-inf).
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));  // (HIP's uint4 class here is kept in scratch)
 struct FaStage {
     u32x4 k[4], v[4];
-    float mv;
+    uint32_t mh;
 };
 
 // NT: nontemporal loads, for a decode row, whose workgroups each read their cache chunk once (several query rows
 // read each chunk once per row, and keep the plain loads that leave it in the cache for the next).
 template <bool NT>
-__device__ __forceinline__ void fa_stage_load(FaStage &st, const FaArgs &a, const uint8_t *kb, const uint8_t *vb,
-                                              const uint16_t *mrow, int64_t base, int64_t j1, int tid) {
+__device__ __forceinline__ void fa_stage_rows(FaStage &st, const FaArgs &a, const uint8_t *kb, const uint8_t *vb,
+                                              int64_t base, int64_t j1, int tid) {
     const int lr = tid >> 4, seg = tid & 15;
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -392,8 +397,16 @@ __device__ __forceinline__ void fa_stage_load(FaStage &st, const FaArgs &a, cons
         st.k[u] = NT ? __builtin_nontemporal_load(kp) : *kp;
         st.v[u] = NT ? __builtin_nontemporal_load(vp) : *vp;
     }
-    st.mv = -INFINITY;
-    if (tid < 64 && base + tid < j1) st.mv = mrow ? h2f(mrow[base + tid]) : 0.0f;
+}
+// Every thread loads, with no branch (a branch's join would wait for the load at once): position base + (tid & 63)
+// clamped into the split, or with no mask the first bytes of the head's K rows; fa_mask_value picks the value.
+__device__ __forceinline__ void fa_stage_mask(FaStage &st, const uint16_t *mrow, const uint8_t *kb, int64_t base,
+                                              int64_t j1, int tid) {
+    st.mh = *(mrow ? mrow + min(base + (tid & 63), j1 - 1) : (const uint16_t *)kb);
+}
+__device__ __forceinline__ float fa_mask_value(const FaStage &st, const uint16_t *mrow, int64_t base, int64_t j1,
+                                               int tid) {
+    return base + tid < j1 ? (mrow ? h2f((uint16_t)st.mh) : 0.0f) : -INFINITY;
 }
 
 // Pass 1 for head size 128 and GQA groups of G = 1, 2 or 4 q heads per kv head: one 256-thread workgroup per (split,
@@ -438,31 +451,44 @@ __global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a, QkvPostArgs pa) {
     bool mine = false;  // POST: this workgroup stores (and reads from LDS) the new row p
     int64_t p = -1;
     float hx0 = 0.f, hx1 = 0.f, hw0 = 0.f, hw1 = 0.f, kx0 = 0.f, kx1 = 0.f, kw0 = 0.f, kw1 = 0.f, v0f = 0.f, v1f = 0.f;
-    if constexpr (POST) {  // the raw heads' loads go out first: the prologue works on them while the chunk loads
-        p = pa.pos[0];
+    // POST: the position, the raw heads and the first chunk go out together, before anything waits on the position.
+    // Every workgroup loads its kv head's raw key and value (768 bytes): only the one holding the new row uses them,
+    // and loading them after the position had arrived would add a dependent round trip to that workgroup.
+    // The waits for these loads are counted in loads issued after them, and where the paths into a wait issued
+    // different numbers of loads the count falls to the smallest. So every wave issues the same loads, with no branch,
+    // after its head loads: the mask (its branches) goes first, each wave loads a q head (waves past the group's heads
+    // repeat its last) and the kv head's key and value, then the chunk (a decode row's splits all hold positions).
+    FaStage st;
+    if constexpr (POST) {
+        // A scalar load (nothing writes the positions while the kernel runs), first used by the empty asm after the
+        // chunk's loads: its wait is then on the scalar counter, behind every load of the prologue.
+        int32_t p32 = *(const __attribute__((address_space(4))) int32_t *)pa.pos;
+        fa_stage_mask(st, mrow, kb, j0, j1, tid);
+        const float *x = (const float *)((const uint8_t *)pa.q + (hk * G + min(wave, G - 1)) * pa.q_nb1);
+        hx0 = x[lane];
+        hx1 = x[lane + 64];
+        hw0 = pa.qw[lane];
+        hw1 = pa.qw[lane + 64];
+        const float *xk = (const float *)((const uint8_t *)pa.k + hk * pa.k_nb1);
+        const float *xv = (const float *)((const uint8_t *)pa.v + hk * pa.v_nb1);
+        kx0 = xk[lane];
+        kx1 = xk[lane + 64];
+        kw0 = pa.kw[lane];
+        kw1 = pa.kw[lane + 64];
+        v0f = xv[lane];
+        v1f = xv[lane + 64];
+        fa_stage_rows<true>(st, a, kb, vb, j0, j1, tid);
+        asm volatile("" : "+s"(p32));
+        p = p32;
+    } else if (j0 < j1) {  // the first chunk's loads go out before q's
+        fa_stage_rows<false>(st, a, kb, vb, j0, j1, tid);
+        fa_stage_mask(st, mrow, kb, j0, j1, tid);
+    }
+    if constexpr (POST) {
         const bool bad = p < 0 || p >= pa.cache_rows;
         mine = !bad && ((p >= j0 && p < j1) || (split == a.nsplit - 1 && p >= j1));
-        if (wave < G) {
-            const float *x = (const float *)((const uint8_t *)pa.q + (hk * G + wave) * pa.q_nb1);
-            hx0 = x[lane];
-            hx1 = x[lane + 64];
-            hw0 = pa.qw[lane];
-            hw1 = pa.qw[lane + 64];
-        }
-        if (mine && wave == (G & 3)) {
-            const float *x = (const float *)((const uint8_t *)pa.k + hk * pa.k_nb1);
-            const float *v = (const float *)((const uint8_t *)pa.v + hk * pa.v_nb1);
-            kx0 = x[lane];
-            kx1 = x[lane + 64];
-            kw0 = pa.kw[lane];
-            kw1 = pa.kw[lane + 64];
-            v0f = v[lane];
-            v1f = v[lane + 64];
-        }
         if (bad && split == 0 && hk == 0 && tid == 0) atomicOr(pa.err, 4);
     }
-    FaStage st;
-    if (j0 < j1) fa_stage_load<POST>(st, a, kb, vb, mrow, j0, j1, tid);  // the first chunk's loads go out before q's
     if constexpr (!POST) {
         for (int e = tid; e < G * D; e += 256) {
             const int g = e / D, d = e % D;
@@ -477,6 +503,8 @@ __global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a, QkvPostArgs pa) {
             qs[wave][lane + 64] = h2f(f2h(o1));
         }
         if (mine && wave == (G & 3)) {  // a wave with no q head (wave 0 after its head when G = 4)
+            // v's conversion stays here: moved up to its loads, its wait would come before the chunk loads
+            asm volatile("" : "+v"(v0f), "+v"(v1f));
             float o0, o1;
             qk_norm_rope(kx0, kx1, kw0, kw1, p, pa.eps, pa.theta_scale, pa.freq_scale, lane, o0, o1);
             const uint16_t k0 = f2h(o0), k1 = f2h(o1), v0 = f2h(v0f), v1 = f2h(v1f);
@@ -512,9 +540,12 @@ __global__ __launch_bounds__(256) void k_fa_gqa(FaArgs a, QkvPostArgs pa) {
             *(u32x4 *)(Ks + (lr + 16 * t) * KS + 16 * seg) = kk;
             *(u32x4 *)(Vs + (lr + 16 * t) * 64 + 4 * seg) = vv;
         }
-        if (tid < 64) mvs[tid] = st.mv;
+        if (tid < 64) mvs[tid] = fa_mask_value(st, mrow, base, j1, tid);
         __syncthreads();
-        if (base + 64 < j1) fa_stage_load<POST>(st, a, kb, vb, mrow, base + 64, j1, tid);  // overlaps this chunk's work
+        if (base + 64 < j1) {  // overlaps this chunk's work
+            fa_stage_rows<POST>(st, a, kb, vb, base + 64, j1, tid);
+            fa_stage_mask(st, mrow, kb, base + 64, j1, tid);
+        }
         // scores
         {
             const uint8_t *kr = Ks + pos_s * KS + part_s * CPT * 2;
@@ -648,6 +679,7 @@ int fa_splits(int64_t n_q, int64_t n_head, int64_t n_kv, int64_t gqa, int D) {
     const int64_t blocks = (n_kv + 63) / 64;
     const bool grouped = fa_grouped(D, gqa);
     const int64_t units = grouped ? n_q * (n_head / gqa) : n_q * n_head;
+    if (blocks == 0 || units == 0) return 1;  // nothing to split: no positions (the rows come out zero) or no rows
     const int64_t target = grouped ? MX_FA_GROUP_WGS : 512;
     int64_t want = (target + units - 1) / units;
     want = want < 1 ? 1 : (want > blocks ? blocks : want);

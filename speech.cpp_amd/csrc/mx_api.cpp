@@ -1259,6 +1259,7 @@ MX_API int mx_attn_decode(mx_backend *be, const mx_tensor *q, const mx_tensor *k
     mx::FaArgs a{};
     if ((rc = fa_args(be, &qa, k_view, v_view, mask, dst, scale, &a))) return rc;
     if (a.gqa != 1 && a.gqa != 2 && a.gqa != 4) return fail(MX_UNSUPPORTED, "fused attention: 1, 2 or 4 q heads per kv head");
+    if (a.n_kv < 1) return fail(MX_UNSUPPORTED, "fused attention: the cache views hold no position");
     HIP_OK(mx::launch_attn_decode(a, pa, be->stream), "fused attention launch");
     return MX_SUCCESS;
 }

@@ -154,6 +154,24 @@ def test_flash_attn_ext(mx, be, n_head, n_kv_head, n_q, n_kv, cap, D, past):
         assert np.array_equal(Y.numpy().reshape(n_q, n_head, D), got)
 
 
+def test_flash_attn_no_positions_or_rows(mx, be):
+    """A K / V view of no positions: every output row is zero (ggml-cpu's S = 0 case); no query rows: nothing is
+    written. Neither reaches the split arithmetic with a zero divisor."""
+    D, n_head, n_kv_head, n_q = 128, 4, 2, 3
+    K = be.tensor(mx.F16, (n_kv_head * D, 8))
+    kh = K.view((D, 0, n_kv_head), (2, n_kv_head * D * 2, D * 2))
+    q = O.fill_normal(0x2C00, n_q * n_head, D)
+    Q = dev(mx, be, q)
+    qh = Q.view((D, n_q, n_head), (4, n_head * D * 4, D * 4))
+    Y = be.tensor(mx.F32, (D, n_head, n_q), np.full(n_q * n_head * D, 7.0, np.float32))
+    be.flash_attn_ext(qh, kh, kh, None, Y, 0.1)
+    be.sync()
+    assert not Y.numpy().any()
+    Y0 = Y.view((D, n_head, 0), (4, D * 4, n_head * D * 4))
+    be.flash_attn_ext(Q.view((D, 0, n_head), (4, n_head * D * 4, D * 4)), kh, kh, None, Y0, 0.1)
+    be.sync()
+
+
 def test_flash_attn_unsupported_forms(mx, be):
     (qh, kh, vh, M, Y), _ = fa_device(mx, be, 4, 2, 1, 64, 64, 128, 10, 0x2B00)
     L = mx.lib()
@@ -319,13 +337,14 @@ def test_fused_qk_norm_rope_kv_equals_the_separate_ops(mx, be):
     assert np.abs(qo.numpy().reshape(1, nq, hd) - ref_q).max() <= 2e-6
 
 
-@pytest.mark.parametrize("nq,nkv,p,n_kv", [
-    (16, 8, 1000, 1088),   # a 0.6B decode step: the new row inside the last split
-    (8, 8, 63, 64),        # one q head per kv head, the new row last of a single chunk
-    (16, 4, 130, 256),     # four q heads per kv head, the new row first of the third chunk
-    (16, 8, 300, 256),     # the new row past the positions read: stored, not attended
+@pytest.mark.parametrize("nq,nkv,p,n_kv,masked", [
+    (16, 8, 1000, 1088, True),   # a 0.6B decode step: the new row inside the last split
+    (8, 8, 63, 64, True),        # one q head per kv head, the new row last of a single chunk
+    (16, 4, 130, 256, True),     # four q heads per kv head, the new row first of the third chunk
+    (16, 8, 300, 256, True),     # the new row past the positions read: stored, not attended
+    (16, 8, 700, 701, False),    # no mask: every position read is visible (a ragged last chunk)
 ])
-def test_attn_decode_equals_the_separate_ops(mx, be, nq, nkv, p, n_kv):
+def test_attn_decode_equals_the_separate_ops(mx, be, nq, nkv, p, n_kv, masked):
     """mx_attn_decode gives the bits of mx_qk_norm_rope_kv followed by mx_flash_attn_ext: the output and both
     caches."""
     hd, cap, eps, theta = 128, 320 if n_kv < 320 else 1280, 1e-6, 1e6
@@ -342,7 +361,7 @@ def test_attn_decode_equals_the_separate_ops(mx, be, nq, nkv, p, n_kv):
     mask = m.astype(np.float16).view(np.uint16)
     Q, K, V, QW, KW, P = dev(mx, be, q), dev(mx, be, k), dev(mx, be, v), dev(mx, be, qw), dev(mx, be, kw), \
         dev(mx, be, pos, mx.I32)
-    M = dev(mx, be, mask, mx.F16)
+    M = dev(mx, be, mask, mx.F16) if masked else None
     qv = Q.view((hd, nq, 1), (4, hd * 4, nq * hd * 4))
     kv = K.view((hd, nkv, 1), (4, hd * 4, kv_dim * 4))
     vv = V.view((hd, nkv, 1), (4, hd * 4, kv_dim * 4))
