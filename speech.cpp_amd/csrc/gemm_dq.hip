@@ -78,15 +78,24 @@ struct DqLds {
     static constexpr bool DIRB = (MX_DQ_DIRECT_B && !K6 && !K5) || (MX_DQ_DIRECT_B6 && K6) || (MX_DQ_DIRECT_B5 && K5);
     // ring stages: the copies run NS - 1 stages ahead of the matrix cores
     static constexpr int NS = DIRB ? MX_DQ_NS_DIRB : 4;
+    // Direct B: bytes that several consecutive stages read alike take a two-slot ring of their own, indexed by
+    // g / SHP and copied once per SHP stages (g: the stage along the whole of K). Q6_K: quarters 2 j and 2 j + 1 of a
+    // super-block read the same ql and qh bytes (low and high nibbles, qh bit pairs 0-3 and 4-7) and d pair (SHP 2);
+    // Q5_K: its four quarters read the super-block's qh, 12 scale bytes and d | dmin (SHP 4). The rest (activations,
+    // Q6_K scales, Q5_K qs) keeps the NS-stage ring.
+    static constexpr bool SH_RAW = DIRB && K6, SH_QH = DIRB && (K6 || K5), SH_SC = DIRB && K5,
+                          SH_DD = DIRB && (K6 || K5), SHARED = SH_RAW || SH_QH || SH_SC || SH_DD;
+    static constexpr int SHP = K6 ? 2 : 4;
+    static constexpr int N_RAW = SH_RAW ? 2 : NS, N_QH = SH_QH ? 2 : NS, N_SC = SH_SC ? 2 : NS, N_DD = SH_DD ? 2 : NS;
     // raw bytes per weight row and stage: codes (Q8_0 codes, Q6_K ql, Q5_K qs), qh, scales, d
     static constexpr int RB = K5 ? 32 : 64, HB = K6 || K5 ? 32 : 0, SB = K5 ? 12 : 4, DB = K6 || K5 ? 4 : 0;
     static constexpr int A = 0;                            // [stage][BM][128 B] activations
     static constexpr int BH = A + NS * BM * 128;        // [2][BN][128 B] dequantized weights
     static constexpr int RAW = BH + (DIRB ? 0 : 2 * BN * 128);  // [stage][BN][RB] codes
-    static constexpr int QH = RAW + NS * BN * RB;       // [stage][BN][HB] qh bytes
-    static constexpr int SC = QH + NS * BN * HB;        // [stage][BN][SB] scales (Q8_0 two fp16, Q6_K four int8,
+    static constexpr int QH = RAW + N_RAW * BN * RB;    // [slot][BN][HB] qh bytes
+    static constexpr int SC = QH + N_QH * BN * HB;      // [slot][BN][SB] scales (Q8_0 two fp16, Q6_K four int8,
                                                            // Q5_K the 12 packed bytes)
-    static constexpr int DD = SC + NS * BN * SB;        // [stage][BN][DB] Q6_K: the fp16 d pair holding the row's;
+    static constexpr int DD = SC + N_SC * BN * SB;      // [slot][BN][DB] Q6_K: the fp16 d pair holding the row's;
                                                            // Q5_K: d | dmin
     // copy instructions per stage (64 lanes each): activation rows (16 B), code rows (16 B), qh rows (16 B), scale
     // words (4 B), d words (4 B), and per wave
@@ -95,11 +104,13 @@ struct DqLds {
     static constexpr int PA = (NA + NW - 1) / NW, PC = (NC + NW - 1) / NW, PH = (NH + NW - 1) / NW;
     static constexpr int PS = (NS4 + NW - 1) / NW, PD = (ND + NW - 1) / NW;
     static constexpr int OPS = PA + PC + PH + PS + PD;  // vector memory ops per wave and stage
+    // ... of a stage whose shared bytes an earlier stage brought
+    static constexpr int OPS1 = PA + (SH_RAW ? 0 : PC) + (SH_QH ? 0 : PH) + (SH_SC ? 0 : PS) + (SH_DD ? 0 : PD);
     // junk bytes per wave: the largest copy instruction some wave issues beyond the tile's need
     static constexpr int JB = PA * NW > NA || PC * NW > NC || PH * NW > NH ? 1024
                               : PS * NW > NS4 || PD * NW > ND            ? 256
                                                                          : 0;
-    static constexpr int JUNK = DD + NS * BN * DB;      // [wave][JB] where copies beyond a tile's need land
+    static constexpr int JUNK = DD + N_DD * BN * DB;    // [wave][JB] where copies beyond a tile's need land
     static constexpr int RS = JUNK + NW * JB;           // [BM] the tile rows' 2^-e
     static constexpr int YO = RS + BM * 4;              // routed experts: [BM] each tile row's output offset (floats)
     static constexpr int SIZE = YO + (RT ? BM * 8 : 0);
@@ -501,9 +512,15 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
         ddst[jj] = j < L::ND ? L::DD + j * 256 : L::JUNK + wave * L::JB;
     }
 
-    auto issue = [&](int t) {
+    // Returns whether stage t's shared bytes were copied too (the workgroup's first stage and every stage with
+    // g % SHP == 0 copy them; with nothing shared, always).
+    auto issue = [&](int t) -> bool {
         t = min(t, nst - 1);  // past the end: copy the last stage again into its own slot (identical bytes)
         const int slot = t % L::NS, g = sb + t;  // g: the stage's index along the whole of K
+        const bool sh = !L::SHARED || t == 0 || g % L::SHP == 0;
+        const int hslot = (g / L::SHP) & 1;
+        const int rslot = L::SH_RAW ? hslot : slot, qslot = L::SH_QH ? hslot : slot, sslot = L::SH_SC ? hslot : slot,
+                  dslot = L::SH_DD ? hslot : slot;
 #pragma unroll
         for (int jj = 0; jj < L::PA; jj++) {
             const uint32_t d = adst[jj] + (adst[jj] < (uint32_t)L::JUNK ? slot * BM * 128 : 0);
@@ -514,33 +531,42 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
         const int coff = L::K6   ? (g >> 2) * 128 + ((g >> 1) & 1) * 64
                          : L::K5 ? (g >> 2) * 128 + (g & 3) * 32
                                  : t * DQ_KS;
+        if (!L::SH_RAW || sh) {
 #pragma unroll
-        for (int jj = 0; jj < L::PC; jj++) {
-            const uint32_t d = cdst[jj] + (cdst[jj] < (uint32_t)L::JUNK ? slot * BN * L::RB : 0);
-            __builtin_amdgcn_global_load_lds((const void *)(csrc[jj] + coff), (dq_lds *)(smem + d), 16, 0, 0);
+            for (int jj = 0; jj < L::PC; jj++) {
+                const uint32_t d = cdst[jj] + (cdst[jj] < (uint32_t)L::JUNK ? rslot * BN * L::RB : 0);
+                __builtin_amdgcn_global_load_lds((const void *)(csrc[jj] + coff), (dq_lds *)(smem + d), 16, 0, 0);
+            }
         }
+        if (!L::SH_QH || sh) {
 #pragma unroll
-        for (int jj = 0; jj < L::PH; jj++) {
-            const uint32_t d = hdst[jj] + (hdst[jj] < (uint32_t)L::JUNK ? slot * BN * L::HB : 0);
-            const int hoff = L::K5 ? (g >> 2) * 32 : (g >> 2) * 64 + ((g >> 1) & 1) * 32;
-            __builtin_amdgcn_global_load_lds((const void *)(hsrc[jj] + hoff), (dq_lds *)(smem + d), 16, 0, 0);
+            for (int jj = 0; jj < L::PH; jj++) {
+                const uint32_t d = hdst[jj] + (hdst[jj] < (uint32_t)L::JUNK ? qslot * BN * L::HB : 0);
+                const int hoff = L::K5 ? (g >> 2) * 32 : (g >> 2) * 64 + ((g >> 1) & 1) * 32;
+                __builtin_amdgcn_global_load_lds((const void *)(hsrc[jj] + hoff), (dq_lds *)(smem + d), 16, 0, 0);
+            }
         }
         const int soff = L::K6 ? (g >> 2) * 16 + (g & 3) * 4 : L::K5 ? (g >> 2) * 12 : t * 4;
+        if (!L::SH_SC || sh) {
 #pragma unroll
-        for (int jj = 0; jj < L::PS; jj++) {
-            const uint32_t d = sdst[jj] + (sdst[jj] < (uint32_t)L::JUNK ? slot * BN * L::SB : 0);
-            __builtin_amdgcn_global_load_lds((const void *)(ssrc[jj] + soff), (dq_lds *)(smem + d), 4, 0, 0);
+            for (int jj = 0; jj < L::PS; jj++) {
+                const uint32_t d = sdst[jj] + (sdst[jj] < (uint32_t)L::JUNK ? sslot * BN * L::SB : 0);
+                __builtin_amdgcn_global_load_lds((const void *)(ssrc[jj] + soff), (dq_lds *)(smem + d), 4, 0, 0);
+            }
         }
         // d: the 4-byte-aligned pair of fp16 d holding this row's (which half: convert). When the plane holds an odd
         // number of d, the last pair runs 2 bytes past them -- inside the plane's padding to 256 bytes, which an odd
         // count of 2-byte values never fills exactly.
+        if (!L::SH_DD || sh) {
 #pragma unroll
-        for (int jj = 0; jj < L::PD; jj++) {
-            const uint32_t d = ddst[jj] + (ddst[jj] < (uint32_t)L::JUNK ? slot * BN * 4 : 0);
-            const int64_t e = dsb[jj] + (g >> 2);
-            const uint8_t *src = L::K5 ? p.w.p3 + e * 4 : p.w.p3 + (e >> 1) * 4;
-            __builtin_amdgcn_global_load_lds((const void *)src, (dq_lds *)(smem + d), 4, 0, 0);
+            for (int jj = 0; jj < L::PD; jj++) {
+                const uint32_t d = ddst[jj] + (ddst[jj] < (uint32_t)L::JUNK ? dslot * BN * 4 : 0);
+                const int64_t e = dsb[jj] + (g >> 2);
+                const uint8_t *src = L::K5 ? p.w.p3 + e * 4 : p.w.p3 + (e >> 1) * 4;
+                __builtin_amdgcn_global_load_lds((const void *)src, (dq_lds *)(smem + d), 4, 0, 0);
+            }
         }
+        return sh;
     };
 
     // Conversion of stage t's raw weights into fp16 tile buffer t & 1, in units of 16 codes: unit u is quarter u & 3
@@ -648,8 +674,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     } else {
         rs_row = a.rs[min(m0 + (tid < BM ? tid : 0), M - 1)];
     }
+    bool plast = true;  // whether the latest issue copied the shared bytes too (the ops a stage's wait leaves in flight)
 #pragma unroll
-    for (int t = 0; t < L::NS - 1; t++) issue(t);
+    for (int t = 0; t < L::NS - 1; t++) plast = issue(t);
     if constexpr (!L::DIRB) {
         dq_wait_vm<(L::NS - 2) * L::OPS>();  // stage 0 landed (this wave's copies)
         if (tid < BM) {  // read by the epilogue
@@ -681,7 +708,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
         uint32_t adS[L::NS][8], aeS[L::NS][8], bS0[L::NS], bS1[L::NS], scS[L::NS], hS[L::NS], dS[L::NS];
 #pragma unroll
         for (int sl = 0; sl < L::NS; sl++) {
-            const uint32_t at = lds + L::A + sl * BM * 128, rt = lds + L::RAW + sl * BN * L::RB;
+            [[maybe_unused]] const uint32_t at = lds + L::A + sl * BM * 128, rt = lds + L::RAW + sl * BN * L::RB;
 #pragma unroll
             for (int x = 0; x < 8; x++) adS[sl][x] = aeS[sl][x] = 0;
 #pragma unroll
@@ -692,34 +719,49 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
                     if (x < 8) adS[sl][x] = at + aoff[i][kk];
                     else aeS[sl][x - 8] = at + aoff[i][kk];
                 }
-            bS0[sl] = rt + boffd0;
-            bS1[sl] = rt + boffd1;
-            scS[sl] = lds + L::SC + sl * BN * L::SB + brow * L::SB;
-            hS[sl] = lds + L::QH + sl * BN * 32 + hoffd;
-            dS[sl] = lds + L::DD + sl * BN * 4 + brow * 4;  // Q6_K: the d pair holding the row's; Q5_K: d | dmin
+            // (shared bytes: two slots, by g / SHP, below)
+            if constexpr (!L::SH_RAW) {
+                bS0[sl] = rt + boffd0;
+                bS1[sl] = rt + boffd1;
+            }
+            if constexpr (!L::SH_SC) scS[sl] = lds + L::SC + sl * BN * L::SB + brow * L::SB;
+            if constexpr (!L::SH_QH) hS[sl] = lds + L::QH + sl * BN * 32 + hoffd;
+            if constexpr (!L::SH_DD) dS[sl] = lds + L::DD + sl * BN * 4 + brow * 4;  // Q6_K: the row's d pair; Q5_K: d | dmin
         }
+        [[maybe_unused]] const uint32_t pb0 = lds + L::RAW + boffd0, pb1 = lds + L::RAW + boffd1,
+                                        ph = lds + L::QH + hoffd, pdd = lds + L::DD + brow * 4,
+                                        psc = lds + L::SC + brow * L::SB;
         auto stage = [&](auto slot, int s) {
             constexpr int SL = decltype(slot)::value;  // == s % L::NS
             // this wave's copies of A(s) and of the raw weights of stage s have landed, and its LDS writes are done;
             // then every wave's. The barrier is the bare instruction: __syncthreads' release fence would wait for
             // every copy in flight (the next stages' too) wherever the compiler can see them pending.
-            dq_wait_vm<(L::NS - 2) * L::OPS>();
+            // (the latest issue, of stage s + 1, copied the shared bytes too or not)
+            if (L::SHARED && !plast) dq_wait_vm<(L::NS - 2) * L::OPS1>();
+            else dq_wait_vm<(L::NS - 2) * L::OPS>();
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            // this stage's code, qh, scale and d addresses
+            const uint32_t hsl = (uint32_t)((sb + s) / L::SHP) & 1u;  // the shared bytes' slot
+            const uint32_t b0 = L::SH_RAW ? pb0 + hsl * (BN * L::RB) : bS0[SL];
+            const uint32_t b1 = L::SH_RAW ? pb1 + hsl * (BN * L::RB) : bS1[SL];
+            const uint32_t hh = L::SH_QH ? ph + hsl * (BN * 32) : hS[SL];
+            const uint32_t dd = L::SH_DD ? pdd + hsl * (BN * 4) : dS[SL];
+            const uint32_t ss = L::SH_SC ? psc + hsl * (BN * L::SB) : scS[SL];
             v8h fa[8], fb[16];
             v4i braw[2], qh = {0, 0, 0, 0};
             uint32_t sw, dw = 0, s1 = 0, s2 = 0;
             // the K-quants' qh chunk and d word (Q5_K: and scale words 1, 2): landed with the reads below, whose wait
             // covers these
             if constexpr (L::K6)
-                asm volatile("ds_read_b128 %0, %2\n\tds_read_b32 %1, %3" : "=&v"(qh), "=&v"(dw) : "v"(hS[SL]), "v"(dS[SL])
+                asm volatile("ds_read_b128 %0, %2\n\tds_read_b32 %1, %3" : "=&v"(qh), "=&v"(dw) : "v"(hh), "v"(dd)
                              : "memory");
             if constexpr (L::K5)
                 asm volatile("ds_read_b128 %0, %4\n\tds_read_b32 %1, %5\n\tds_read_b32 %2, %6 offset:4\n\t"
                              "ds_read_b32 %3, %6 offset:8"
                              : "=&v"(qh), "=&v"(dw), "=&v"(s1), "=&v"(s2)
-                             : "v"(hS[SL]), "v"(dS[SL]), "v"(scS[SL])
+                             : "v"(hh), "v"(dd), "v"(ss)
                              : "memory");
-            dq_read_ab<TM == 4 ? 2 : TM>(fa, braw, sw, adS[SL], bS0[SL], bS1[SL], scS[SL]);
+            dq_read_ab<TM == 4 ? 2 : TM>(fa, braw, sw, adS[SL], b0, b1, ss);
             if constexpr (L::K6 || L::K5) asm volatile("" : "+v"(qh), "+v"(dw), "+v"(s1), "+v"(s2));  // no use before that wait
             // 16 raw values -> two K steps of B fragments: chunk kk2 of the stage (Q8_0: block kk2; Q6_K: values
             // 32 kk2 + 16 fh .. of the quarter, sub-block 4 (g & 3) + 2 kk2 + fh, qh bits 4 (g & 1) + 2 kk2; Q5_K: the
@@ -777,7 +819,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
                             kk * TM + i < 8 ? fa[kk * TM + i] : fb[kk * TM + i - 8], __builtin_bit_cast(v8h, bq[kk]),
                             acc[i][0], 0, 0, 0);
             }
-            issue(s + L::NS - 1);
+            plast = issue(s + L::NS - 1);
         };
         int s = 0;
 #pragma unroll 1
