@@ -96,18 +96,20 @@ template <int NMT_, int WM_, int WN_>
 struct Q4gT {
     static constexpr int NMT = NMT_, WM = WM_, WN = WN_;
     static constexpr int BM = 32 * NMT * WM, BN = 32 * WN, NW = WM * WN, NT = 64 * NW;
-    // operand stage
-    static constexpr int A = 0;                     // int8 quants, BM rows of 256 (swizzled)
-    static constexpr int B = A + BM * 256;          // packed codes, BN rows of 128 (swizzled)
-    static constexpr int BSC = B + BN * 128;        // [sub-block j][column]: (hi, hi), (lo, lo) u16 pairs, 8 B
-    static constexpr int OP = BSC + 8 * BN * 8;
+    // operand rings: activation quants (two slots), weight codes (three: their copies run two super-blocks ahead,
+    // the activations', from the L2 mostly, one), scale splats (two)
+    static constexpr int A = 0;                     // in an A slot: int8 quants, BM rows of 256 (swizzled)
+    static constexpr int B = 0;                     // in a B slot: packed codes, BN rows of 128 (swizzled)
+    static constexpr int BSC = 0;                   // in a splat slot: [sub-block j][column]: (hi, hi), (lo, lo) u16
+    static constexpr int SA = BM * 256, SB = BN * 128, SS = 8 * BN * 8;  // slot sizes
+    static constexpr int RA = 0, RB = RA + 2 * SA, RS = RB + 3 * SB, RE = RS + 2 * SS;  // ring bases
     // epilogue stage
     static constexpr int A16 = 0;                   // fp16 [64 h | l], 32 B per row (swizzled halves)
     static constexpr int ADX = A16 + BM * 32;       // fp32 d per row
     static constexpr int BMN = ADX + BM * 4;        // per column 8 fp16 mins
     static constexpr int BD = BMN + BN * 16;        // per column fp32 d, dmin
     static constexpr int EP = BD + BN * 8;
-    static constexpr int LDS = 2 * OP + 3 * EP;
+    static constexpr int LDS = RE + 3 * EP;
     // global -> LDS copy instructions per stage (64 lanes each), and per wave
     static constexpr int NA = BM / 4, NB = BN / 8, NA16 = BM / 32, NDX = BM / 64;
     static constexpr int QA = NA / NW, QB = NB / NW;
@@ -116,6 +118,28 @@ struct Q4gT {
     static_assert(TPC == 2 || TPC == 4, "two or four threads per weight column");
     static_assert(LDS <= 160 * 1024, "LDS of one workgroup");
 };
+
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+// A buffer descriptor for raw dword loads: base, no stride, `bytes` records (reads past them return zeros), format
+// word as the buffer-resource builtin makes it for these loads.
+__device__ __forceinline__ v4u q4g_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    return v4u{(uint32_t)b, (uint32_t)(b >> 32), bytes, 0x00020000u};
+}
+__device__ __forceinline__ uint32_t q4g_lds(const void *p) { return (uint32_t)(uintptr_t)(const lds_void *)p; }
+
+// Buffer-to-LDS copies (each lane's 16 or 4 bytes land at m0 + 16 or 4 x lane) issued through asm: issued as the
+// builtin, the compiler counts them as LDS stores that every later LDS read may alias, and waits for all of them
+// (the next stage's and the one after) before the first fragment read of a step. Their waits are counted here.
+__device__ __forceinline__ void q4g_dma16(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void q4g_dma4(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
+                 : "memory", "m0");
+}
 
 // One workgroup's global -> LDS copies through buffer loads (buffer_load_dword* ... lds): a per-lane byte offset
 // fixed for the whole K loop and a per-stage uniform offset (sb times the per-block stride of each source: 256 B of
@@ -126,15 +150,15 @@ struct Q4gT {
 template <class Q>
 struct Q4gDma {
     uint32_t a[Q::QA], b[Q::QB], a16, dx;
-    __amdgpu_buffer_rsrc_t ra, rb, r16, rdx;
+    v4u ra, rb, r16, rdx;
 
     __device__ __forceinline__ void init(int wave, const int8_t *xq, const _Float16 *x16, const float *xd,
                                          const uint8_t *qs, int m0, int n0, int M, int N, int K, int nsb) {
         const int lane = threadIdx.x & 63;
-        ra = __builtin_amdgcn_make_buffer_rsrc((void *)xq, (short)0, M * K, 0x00020000);
-        rb = __builtin_amdgcn_make_buffer_rsrc((void *)qs, (short)0, N * nsb * 128, 0x00020000);
-        r16 = __builtin_amdgcn_make_buffer_rsrc((void *)x16, (short)0, M * nsb * 32, 0x00020000);
-        rdx = __builtin_amdgcn_make_buffer_rsrc((void *)xd, (short)0, M * nsb * 4, 0x00020000);
+        ra = q4g_rsrc(xq, (uint32_t)(M * K));
+        rb = q4g_rsrc(qs, (uint32_t)(N * nsb * 128));
+        r16 = q4g_rsrc(x16, (uint32_t)(M * nsb * 32));
+        rdx = q4g_rsrc(xd, (uint32_t)(M * nsb * 4));
 #pragma unroll
         for (int q = 0; q < Q::QA; q++) {
             const int r = 4 * (wave * Q::QA + q) + (lane >> 4), cs = lane & 15;
@@ -152,22 +176,17 @@ struct Q4gDma {
         dx = (uint32_t)min(m0 + 64 * min(wave, Q::NDX - 1) + lane, M - 1) * (uint32_t)nsb * 4u;
     }
 
-    // wave is uniform (readfirstlane), so every LDS destination is a scalar.
-    __device__ __forceinline__ void issue(uint8_t *op, uint8_t *ep, int wave, int sb) const {
+    // wave is uniform (readfirstlane), so every LDS destination is a scalar. The weight codes of a super-block (QB
+    // instructions per wave) are issued on their own, last of a step's copies.
+    __device__ __forceinline__ void issue_b(uint8_t *opb, int wave, int sb) const {
 #pragma unroll
-        for (int q = 0; q < Q::QA; q++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(op + Q::A + 1024 * (wave * Q::QA + q)), 16,
-                                                     a[q], sb * 256, 0, 0);
+        for (int q = 0; q < Q::QB; q++) q4g_dma16(rb, q4g_lds(opb + Q::B + 1024 * (wave * Q::QB + q)), b[q], sb * 128);
+    }
+    __device__ __forceinline__ void issue_a(uint8_t *opa, uint8_t *ep, int wave, int sb) const {
 #pragma unroll
-        for (int q = 0; q < Q::QB; q++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)(op + Q::B + 1024 * (wave * Q::QB + q)), 16,
-                                                     b[q], sb * 128, 0, 0);
-        if (wave < Q::NA16)  // uniform
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r16, (lds_void *)(ep + Q::A16 + 1024 * wave), 16, a16,
-                                                     sb * 32, 0, 0);
-        if (wave < Q::NDX)  // uniform
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rdx, (lds_void *)(ep + Q::ADX + 256 * wave), 4, dx, sb * 4,
-                                                     0, 0);
+        for (int q = 0; q < Q::QA; q++) q4g_dma16(ra, q4g_lds(opa + Q::A + 1024 * (wave * Q::QA + q)), a[q], sb * 256);
+        if (wave < Q::NA16) q4g_dma16(r16, q4g_lds(ep + Q::A16 + 1024 * wave), a16, sb * 32);  // uniform
+        if (wave < Q::NDX) q4g_dma4(rdx, q4g_lds(ep + Q::ADX + 256 * wave), dx, sb * 4);        // uniform
     }
 };
 
@@ -176,14 +195,17 @@ struct Q4gDma {
 struct Q4gScales {
     uint32_t s0, s1, s2, dm;
 
+    // Issued through asm, like the copies, so that the compiler inserts no wait for them: `landed` (after the
+    // explicit vmcnt wait that covers them) is their first use.
     __device__ __forceinline__ void load(const uint8_t *scp, const uint8_t *dmp, uint32_t blk0, int sb) {
-        const uint32_t blk = blk0 + (uint32_t)sb;
-        const uint32_t *s = (const uint32_t *)(scp + blk * 12u);
-        s0 = s[0];
-        s1 = s[1];
-        s2 = s[2];
-        dm = *(const uint32_t *)(dmp + blk * 4u);
+        const uint32_t blk = blk0 + (uint32_t)sb;  // scalar bases, 32-bit lane offsets
+        asm volatile("global_load_dword %0, %4, %5\n\tglobal_load_dword %1, %4, %5 offset:4\n\t"
+                     "global_load_dword %2, %4, %5 offset:8\n\tglobal_load_dword %3, %6, %7"
+                     : "=&v"(s0), "=&v"(s1), "=&v"(s2), "=&v"(dm)
+                     : "v"(blk * 12u), "s"(scp), "v"(blk * 4u), "s"(dmp)
+                     : "memory");
     }
+    __device__ __forceinline__ void landed() { asm volatile("" : "+v"(s0), "+v"(s1), "+v"(s2), "+v"(dm)); }
 
     __device__ static __forceinline__ uint32_t byte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
         const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
@@ -192,10 +214,10 @@ struct Q4gScales {
 
     // ggml-quants.c get_scale_min_k4: scale splats into the operand stage, mins, d and dmin into the epilogue stage.
     template <class Q>
-    __device__ __forceinline__ void store(uint8_t *op, uint8_t *ep) const {
+    __device__ __forceinline__ void store(uint8_t *ops, uint8_t *ep) const {
         constexpr int PER = 8 / Q::TPC;
         const int t = threadIdx.x, n = t / Q::TPC, q = t % Q::TPC;
-        uint32_t *bsc = (uint32_t *)(op + Q::BSC + n * 8);
+        uint32_t *bsc = (uint32_t *)(ops + Q::BSC + n * 8);
         _Float16 *bmn = (_Float16 *)(ep + Q::BMN + n * 16);
 #pragma unroll
         for (int h = 0; h < PER; h++) {
@@ -294,23 +316,23 @@ struct Q4gBFrag {
 };
 
 template <class Q>
-__device__ __forceinline__ Q4gWFrag q4g_load_w(const Q4gWave &w, const uint8_t *op, int pr) {
+__device__ __forceinline__ Q4gWFrag q4g_load_w(const Q4gWave &w, const uint8_t *opb, const uint8_t *ops, int pr) {
     Q4gWFrag f;
-    f.pk = *(const v4i *)(op + Q::B + b_slot(w.br, 2 * pr + w.hf));
-    const uint2 *bsc = (const uint2 *)(op + Q::BSC + w.br * 8);
+    f.pk = *(const v4i *)(opb + Q::B + b_slot(w.br, 2 * pr + w.hf));
+    const uint2 *bsc = (const uint2 *)(ops + Q::BSC + w.br * 8);
     f.hl[0] = bsc[(2 * pr) * Q::BN];
     f.hl[1] = bsc[(2 * pr + 1) * Q::BN];
     return f;
 }
 
 template <class Q>
-__device__ __forceinline__ Q4gAFrag<Q> q4g_load_a(const Q4gWave &w, const uint8_t *op, int pr) {
+__device__ __forceinline__ Q4gAFrag<Q> q4g_load_a(const Q4gWave &w, const uint8_t *opa, int pr) {
     Q4gAFrag<Q> f;
 #pragma unroll
     for (int h = 0; h < 2; h++)
 #pragma unroll
         for (int t = 0; t < Q::NMT; t++)
-            f.a[h][t] = *(const v4i *)(op + Q::A + a_slot(w.wm + 32 * t + w.fr, 2 * (2 * pr + h) + w.hf));
+            f.a[h][t] = *(const v4i *)(opa + Q::A + a_slot(w.wm + 32 * t + w.fr, 2 * (2 * pr + h) + w.hf));
     return f;
 }
 
@@ -345,34 +367,39 @@ __device__ __forceinline__ void q4g_epilogue(const Q4gWave &w, const uint8_t *ep
     e.apply(I, acc);
 }
 
-// Iteration sb of one wave: start the copies of super-block sb + 1, then sb's MFMAs into `I` ({A_hi, A_lo} per tile)
-// and a float epilogue: an early wave (the first half of the workgroup) runs the epilogue of sb after its MFMAs, a
-// late wave runs the epilogue of sb - 1 before them. The two waves sharing a SIMD are one early and one late, so that
-// one's MFMAs meet the other's epilogue between any two barriers; the three-stage epilogue ring keeps sb - 1's
-// inputs in LDS for the late wave. Then the scales of sb + 1 and the stage barrier.
+// Iteration sb of one wave: start the copies of super-block sb + 1 (activations, epilogue inputs, scales) and of the
+// weight codes of sb + 2, then sb's MFMAs into `I` ({A_hi, A_lo} per tile) and a float epilogue: an early wave (the
+// first half of the workgroup) runs the epilogue of sb after its MFMAs, a late wave runs the epilogue of sb - 1 before
+// them. The two waves sharing a SIMD are one early and one late, so that one's MFMAs meet the other's epilogue between
+// any two barriers; the three-stage epilogue ring keeps sb - 1's inputs in LDS for the late wave. Then the scales of
+// sb + 1 and the stage barrier, which waits for everything but the codes of sb + 2.
 template <class Q>
 __device__ __forceinline__ void q4g_step(const Q4gWave &w, bool late, const Q4gDma<Q> &dma, Q4gScales &sc,
                                          const uint8_t *scp, const uint8_t *dmp, uint32_t scblk, int sb, int nsb,
                                          v16i (&I)[2 * Q::NMT], float (&acc)[Q::NMT][16]) {
-    uint8_t *op = w.smem + (sb & 1) * Q::OP;
-    uint8_t *opn = w.smem + ((sb + 1) & 1) * Q::OP;
-    uint8_t *epbase = w.smem + 2 * Q::OP;
-    const int e = sb % 3;
-    uint8_t *epn = epbase + (e == 2 ? 0 : e + 1) * Q::EP;
+    const int e = sb % 3, en = e == 2 ? 0 : e + 1, ep2 = e == 0 ? 2 : e - 1;  // sb, sb + 1 and sb - 1 (= sb + 2) mod 3
+    const uint8_t *opa = w.smem + Q::RA + (sb & 1) * Q::SA, *opb = w.smem + Q::RB + e * Q::SB;
+    const uint8_t *ops = w.smem + Q::RS + (sb & 1) * Q::SS;
+    uint8_t *opan = w.smem + Q::RA + ((sb + 1) & 1) * Q::SA, *opbn2 = w.smem + Q::RB + ep2 * Q::SB;
+    uint8_t *opsn = w.smem + Q::RS + ((sb + 1) & 1) * Q::SS;
+    uint8_t *epbase = w.smem + Q::RE;
+    uint8_t *epn = epbase + en * Q::EP;
     const uint8_t *epc = epbase + e * Q::EP;
-    const uint8_t *epp = epbase + (e == 0 ? 2 : e - 1) * Q::EP;
-    const int sbn = min(sb + 1, nsb - 1);  // the last iteration copies its own stage again into idle buffers
-    dma.issue(opn, epn, w.wave, sbn);
-    sc.load(scp, dmp, scblk, sbn);
+    const uint8_t *epp = epbase + ep2 * Q::EP;
+    // past the end, copies repeat the last super-block into slots no later step reads
+    dma.issue_a(opan, epn, w.wave, min(sb + 1, nsb - 1));
+    sc.load(scp, dmp, scblk, min(sb + 1, nsb - 1));
+    asm volatile("" ::: "memory");  // the codes go out last: the stage barrier leaves only them in flight
+    dma.issue_b(opbn2, w.wave, min(sb + 2, nsb - 1));
 
     // Software pipeline over the four sub-block pairs: weight bytes read two pairs ahead, activation fragments and
     // the scaling one pair ahead, so no MFMA waits on LDS or on the VALU that prepares its operand.
     Q4gWFrag wf[3];
     Q4gAFrag<Q> af[2];
     Q4gBFrag bf[2];
-    wf[0] = q4g_load_w<Q>(w, op, 0);
-    wf[1] = q4g_load_w<Q>(w, op, 1);
-    af[0] = q4g_load_a<Q>(w, op, 0);
+    wf[0] = q4g_load_w<Q>(w, opb, ops, 0);
+    wf[1] = q4g_load_w<Q>(w, opb, ops, 1);
+    af[0] = q4g_load_a<Q>(w, opa, 0);
     Q4gEpi<Q> ep;
     ep.load(w, late ? epp : epc);
     bf[0] = q4g_scale(wf[0]);
@@ -382,18 +409,22 @@ __device__ __forceinline__ void q4g_step(const Q4gWave &w, bool late, const Q4gD
     for (int i = 0; i < 2 * Q::NMT; i++) I[i] = zero16;
 #pragma unroll
     for (int pr = 0; pr < 4; pr++) {
-        if (pr + 2 < 4) wf[(pr + 2) % 3] = q4g_load_w<Q>(w, op, pr + 2);
+        if (pr + 2 < 4) wf[(pr + 2) % 3] = q4g_load_w<Q>(w, opb, ops, pr + 2);
         if (pr + 1 < 4) {
-            af[(pr + 1) & 1] = q4g_load_a<Q>(w, op, pr + 1);
+            af[(pr + 1) & 1] = q4g_load_a<Q>(w, opa, pr + 1);
             bf[(pr + 1) & 1] = q4g_scale(wf[(pr + 1) % 3]);
         }
         q4g_mfma<Q>(af[pr & 1], bf[pr & 1], I);
     }
     if (!late) ep.apply(I, acc);
 
-    sc.store<Q>(opn, epn);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies into the next stages have landed
-    __syncthreads();
+    // this wave's copies and scale loads of sb + 1 have landed (the codes of sb + 2, its last QB copies, may not)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(Q::QB) : "memory");
+    sc.landed();
+    sc.store<Q>(opsn, epn);
+    // and its LDS writes are done; then every wave's. The barrier is the bare instruction: __syncthreads' release fence
+    // would wait for the codes of sb + 2 too.
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 template <class Q>
@@ -424,10 +455,14 @@ __global__ __launch_bounds__(Q::NT) void k_gemm_q4k(Q4gArgs a) {
     dma.init(w.wave, a.xq, a.x16, a.xd, qs, m0, n0, M, N, (int)a.K, nsb);
     const uint32_t scblk = (uint32_t)min(n0 + tid / Q::TPC, N - 1) * (uint32_t)nsb;
     Q4gScales sc;
-    uint8_t *ep0 = smem + 2 * Q::OP;
-    dma.issue(smem, ep0, w.wave, 0);
+    uint8_t *ep0 = smem + Q::RE;
+    dma.issue_a(smem + Q::RA, ep0, w.wave, 0);
+    dma.issue_b(smem + Q::RB, w.wave, 0);
     sc.load(scp, dmp, scblk, 0);
-    sc.store<Q>(smem, ep0);
+    dma.issue_b(smem + Q::RB + Q::SB, w.wave, min(1, nsb - 1));
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(Q::QB) : "memory");  // all but the codes of super-block 1
+    sc.landed();
+    sc.store<Q>(smem + Q::RS, ep0);
     {
         // Epilogue stage 2 (the "previous" one of iteration 0) starts as zeros: iteration 0 runs its epilogue with zero
         // accumulators, which adds exactly 0.
@@ -435,8 +470,7 @@ __global__ __launch_bounds__(Q::NT) void k_gemm_q4k(Q4gArgs a) {
         const v4i z4 = {0, 0, 0, 0};
         for (int o = 16 * tid; o < Q::EP; o += 16 * Q::NT) *(v4i *)(ep2 + o) = z4;
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     const v16i zero16 = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     v16i I[2 * Q::NMT];
