@@ -84,7 +84,7 @@ struct Q4gProblem {
 };
 struct Q4gArgs {
     Q4gProblem prob[4];
-    int M, nsb;
+    int nprob, M, nsb;
     int64_t K;
     const int8_t *xq;
     const float *xd;
@@ -430,16 +430,29 @@ __device__ __forceinline__ void q4g_step(const Q4gWave &w, bool late, const Q4gD
 template <class Q>
 __global__ __launch_bounds__(Q::NT) void k_gemm_q4k(Q4gArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int z = blockIdx.z;
+    // The grid is one dimension of the problems' tiles, problem after problem, each (N_z / BN) x (M / BM) with n
+    // fastest: no workgroup of a narrower problem's missing columns (a grid of the widest problem's width per problem
+    // launched those, and the launch ran as if it had that many more workgroups). A column's M tiles stay a multiple
+    // of the column count apart, which keeps them on one XCD when that count is a multiple of 8.
+    const int MT = (a.M + Q::BM - 1) / Q::BM;
+    int t = blockIdx.x, z = 0;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const int Ni = i == 0 ? a.prob[0].N : (i == 1 ? a.prob[1].N : a.prob[2].N);
+        const int ti = (Ni + Q::BN - 1) / Q::BN * MT;
+        if (z == i && i + 1 < a.nprob && t >= ti) {
+            t -= ti;
+            z = i + 1;
+        }
+    }
     const uint8_t *qs = z == 0 ? a.prob[0].qs : (z == 1 ? a.prob[1].qs : (z == 2 ? a.prob[2].qs : a.prob[3].qs));
     const uint8_t *scp = z == 0 ? a.prob[0].sc : (z == 1 ? a.prob[1].sc : (z == 2 ? a.prob[2].sc : a.prob[3].sc));
     const uint8_t *dmp = z == 0 ? a.prob[0].dm : (z == 1 ? a.prob[1].dm : (z == 2 ? a.prob[2].dm : a.prob[3].dm));
     float *y = z == 0 ? a.prob[0].y : (z == 1 ? a.prob[1].y : (z == 2 ? a.prob[2].y : a.prob[3].y));
     const int N = z == 0 ? a.prob[0].N : (z == 1 ? a.prob[1].N : (z == 2 ? a.prob[2].N : a.prob[3].N));
     const int64_t ldy = z == 0 ? a.prob[0].ldy : (z == 1 ? a.prob[1].ldy : (z == 2 ? a.prob[2].ldy : a.prob[3].ldy));
-    const int n0 = blockIdx.x * Q::BN;
-    if (n0 >= N) return;  // uniform: a problem narrower than the grid
-    const int m0 = blockIdx.y * Q::BM;
+    const int ntz = (N + Q::BN - 1) / Q::BN;
+    const int n0 = (t % ntz) * Q::BN, m0 = (t / ntz) * Q::BM;
     const int M = a.M, nsb = a.nsb;
     const int tid = threadIdx.x, lane = tid & 63;
 
@@ -530,7 +543,7 @@ hipError_t launch_gemm_q4k_quant(const float *x, int64_t x_stride, int64_t M, in
 }
 
 template <class Q>
-static hipError_t launch_q4g(const Q4gArgs &a, int nprob, int maxN, hipStream_t s) {
+static hipError_t launch_q4g(const Q4gArgs &a, hipStream_t s) {
     static bool configured = false;
     if (!configured) {
         const hipError_t e = hipFuncSetAttribute((const void *)k_gemm_q4k<Q>, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -538,8 +551,10 @@ static hipError_t launch_q4g(const Q4gArgs &a, int nprob, int maxN, hipStream_t 
         if (e != hipSuccess) return e;
         configured = true;
     }
-    const dim3 grid((unsigned)((maxN + Q::BN - 1) / Q::BN), (unsigned)((a.M + Q::BM - 1) / Q::BM), (unsigned)nprob);
-    hipLaunchKernelGGL(k_gemm_q4k<Q>, grid, dim3(Q::NT), Q::LDS, s, a);
+    int64_t tiles = 0;
+    for (int i = 0; i < a.nprob; i++)
+        tiles += (int64_t)((a.prob[i].N + Q::BN - 1) / Q::BN) * ((a.M + Q::BM - 1) / Q::BM);
+    hipLaunchKernelGGL(k_gemm_q4k<Q>, dim3((unsigned)tiles), dim3(Q::NT), Q::LDS, s, a);
     return hipGetLastError();
 }
 
@@ -550,31 +565,35 @@ hipError_t launch_gemm_q4k(int nprob, const WPlanes *w, const int64_t *N, float 
     if ((uint64_t)M * (uint64_t)K >= (1ull << 31)) return hipErrorInvalidValue;
     const Q4gScratch sp = q4g_scratch(scratch, M, K);
     Q4gArgs a{};
-    int64_t maxN = 0;
     for (int i = 0; i < nprob; i++) {
         if (N[i] <= 0 || (uint64_t)N[i] * (uint64_t)K / 2 >= (1ull << 31)) return hipErrorInvalidValue;
         a.prob[i] = Q4gProblem{w[i].p0, w[i].p1, w[i].p2, y[i], ldy[i], (int)N[i]};
-        maxN = N[i] > maxN ? N[i] : maxN;
     }
+    a.nprob = nprob;
     a.M = (int)M;
     a.nsb = (int)(K / 256);
     a.K = K;
     a.xq = sp.xq;
     a.xd = sp.xd;
     a.x16 = sp.x16;
-    // Tile: 128 x 128 (eight waves, two per SIMD) when that gives at least 128 workgroups, else 128 x 64 (four).
-    // Measured at M = 512: q/k/v (N = 4096) on 128 workgroups of 128 x 128 takes 29.7 us against 43.3 us on 256 of
-    // 128 x 64; attn_o (N = 2048) on 64 of 128 x 128 takes 29.0 us against 24.8 us on 128 of 128 x 64.
-    // A backend's tile option forces 128 x 128 or 128 x 64; any other forced pair is refused.
+    // Tile: 128 x 128 (eight waves, two per SIMD, each with two 32 x 32 tiles) when that gives a workgroup to every
+    // CU, else 64 x 128 (eight waves of one 32 x 32 tile: twice the workgroups). Measured at M = 512, weights cold,
+    // with the activation pass: N = 4096 28.7 us on 128 workgroups of 128 x 128, 22.5 us on 256 of 64 x 128, 22.9 on
+    // 256 of 128 x 64 (four waves); N = 2048 27.1 / 20.7 / 22.0 us; N = 12288 51.0 us on 384 of 128 x 128, 53.8 on
+    // 768 of 64 x 128.
+    // A backend's tile option forces 128 x 128, 64 x 128 or 128 x 64; any other forced pair is refused.
     int64_t wg_big = 0;
     for (int i = 0; i < nprob; i++) wg_big += (N[i] + 127) / 128 * ((M + 127) / 128);
-    bool big = wg_big >= 128;
+    int tile = wg_big >= 256 ? 0 : 1;  // 0: 128 x 128, 1: 64 x 128, 2: 128 x 64
     if (o.tile_m || o.tile_n) {
-        if (o.tile_m != 128 || (o.tile_n != 128 && o.tile_n != 64)) return hipErrorInvalidValue;
-        big = o.tile_n == 128;
+        if (o.tile_m == 128 && o.tile_n == 128) tile = 0;
+        else if (o.tile_m == 64 && o.tile_n == 128) tile = 1;
+        else if (o.tile_m == 128 && o.tile_n == 64) tile = 2;
+        else return hipErrorInvalidValue;
     }
-    if (big) return launch_q4g<Q4gT<2, 2, 4>>(a, nprob, (int)maxN, s);
-    return launch_q4g<Q4gT<2, 2, 2>>(a, nprob, (int)maxN, s);
+    if (tile == 0) return launch_q4g<Q4gT<2, 2, 4>>(a, s);
+    if (tile == 1) return launch_q4g<Q4gT<1, 2, 4>>(a, s);
+    return launch_q4g<Q4gT<2, 2, 2>>(a, s);
 }
 
 }  // namespace mx
