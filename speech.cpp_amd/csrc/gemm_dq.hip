@@ -130,7 +130,7 @@ struct DqArgs {
     int M, K;
     const _Float16 *xh;  // [M][K] fp16(2^e_m d q) of the quantized activations
     const float *rs;     // [M] 2^-e_m, applied to each row's sums
-    int nprob, nsplit;   // grid.z = nprob * nsplit: problem z % nprob, K split z / nprob
+    int nprob, nsplit;   // dense: grid.x runs over the splits' tiles (below); routed: grid.z = nprob
     int ntot;            // sum of the problems' N: columns of the split partials
     int col0[4];         // first partial column of each problem
     float *ws;           // nsplit > 1: [nsplit][M][ntot] partial sums, added in split order by k_dq_reduce
@@ -408,11 +408,39 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     static_assert(L::DIRB ? TN == 1 && (TM == 1 || TM == 2 || TM == 4) : NF == 8 || NF == 12 || NF == 16,
                   "wave tiles of 32 x 32, 64 x 32 or 64 x 64; direct B: 32, 64 or 128 x 32");
     extern __shared__ __align__(16) uint8_t smem[];
-    const int z = blockIdx.z, pi = z % a.nprob, split = z / a.nprob;
+    // Dense: grid.x runs over split after split, each the problems' tiles problem after problem, (N_p / BN) x (M / BM)
+    // with n fastest; no workgroup of a narrower problem's missing columns is launched (a grid of the widest problem's
+    // width per problem launched those, and the launch ran as if it had that many more workgroups). Routed: grid.x the
+    // column tiles, grid.y the chunks, grid.z the problems.
+    int pi = 0, split = 0, n0, m0 = 0;
+    if constexpr (RT) {
+        pi = blockIdx.z % a.nprob;  // (one split)
+        split = blockIdx.z / a.nprob;
+        n0 = blockIdx.x * BN;
+    } else {
+        const int MT = (a.M + BM - 1) / BM;
+        int per = 0;  // tiles of one split
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (i < a.nprob) per += (a.prob[i].N + BN - 1) / BN * MT;
+        int t = blockIdx.x;
+        split = t / per;
+        t -= split * per;
+#pragma unroll
+        for (int i = 0; i < 3; i++) {
+            const int ti = (a.prob[i].N + BN - 1) / BN * MT;
+            if (pi == i && i + 1 < a.nprob && t >= ti) {
+                t -= ti;
+                pi = i + 1;
+            }
+        }
+        const int Np = pi == 0 ? a.prob[0].N : (pi == 1 ? a.prob[1].N : (pi == 2 ? a.prob[2].N : a.prob[3].N));
+        const int ntp = (Np + BN - 1) / BN;
+        n0 = (t % ntp) * BN;
+        m0 = (t / ntp) * BM;
+    }
     const DqProblem p = pi == 0 ? a.prob[0] : (pi == 1 ? a.prob[1] : (pi == 2 ? a.prob[2] : a.prob[3]));
-    const int n0 = blockIdx.x * BN;
-    if (n0 >= p.N) return;  // uniform: a problem narrower than the grid
-    const int m0 = RT ? 0 : blockIdx.y * BM;
+    if (n0 >= p.N) return;  // routed: uniform, a problem narrower than the grid
     const int M = a.M, N = p.N, K = a.K, nblk = K / 32;
     int mrows = 0, first = 0;  // routed: the chunk's pairs and its first index into pairs
     int64_t wrow0 = 0;         // routed: the expert's first row in the weight planes
@@ -971,10 +999,13 @@ DqPlan dq_plan(int type, int nprob, const int64_t *N, int64_t M, int64_t K, cons
     // long products (K >= 4096) whose 128 x 128 grid is smaller still keep the large tile and split K instead (at
     // M = 512, N = 2048, K = 6144: four splits of 24 stages and the reduce beat 256 tiles of 64 x 64)
     const bool split128 = wg128 >= 32 && wg128 < 128 && nst >= 64;
-    // a single product needs 192 workgroups of 128 x 128 (M = 512, N = 4096: 31.3 us on 64 x 64 tiles against 37.0; M =
-    // 1024, N = 2048: 35.0 against 40.0), a group of them 128 (the ASR q/k/v group of widths 2048 + 1024 + 1024 at
-    // M = 512 is faster on 128 x 128)
-    if (wg128 >= (nprob == 1 ? 192 : 128) || split128) pl.bm = pl.bn = 128;
+    // 128 x 128 from 192 workgroups of it, else 128 x 64 when that gives 256 (wg128 >= 128), else 64 x 64. Measured
+    // at M = 512, K = 2048, Q8_0, weights cold, with the activation pass (us on 64 x 64 / 128 x 64 / 128 x 128): N =
+    // 4096 30.5 / 30.3 / 33.2; N = 2048 21.9 / 27.6 / 29.4; N = 12288 70.7 / 62.0 / 47.3; the ASR q/k/v group 2048 +
+    // 1024 + 1024 32.1 / 30.0 / 33.7 (a group's grid holds only its problems' own tiles, so it runs as a product of
+    // its summed width)
+    if (wg128 >= 192 || split128) pl.bm = pl.bn = 128;
+    else if (wg128 >= 128 && M >= 128) pl.bm = 128;
     if (skinny_ok && M <= 32) {
         pl.bm = 32;
         pl.bn = 128;
@@ -1046,8 +1077,10 @@ static hipError_t launch_dq(const DqArgs &a, int maxN, hipStream_t s, int gy = 0
         if (e != hipSuccess) return e;
         attr = true;
     }
-    const dim3 grid((unsigned)((maxN + BN - 1) / BN), (unsigned)(RT ? gy : (a.M + BM - 1) / BM),
-                    (unsigned)(a.nprob * a.nsplit));
+    int64_t tiles = 0;  // dense: every split's tiles of every problem
+    for (int i = 0; i < a.nprob; i++) tiles += (int64_t)((a.prob[i].N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
+    const dim3 grid = RT ? dim3((unsigned)((maxN + BN - 1) / BN), (unsigned)gy, (unsigned)a.nprob)
+                         : dim3((unsigned)(tiles * a.nsplit));
     hipLaunchKernelGGL((k_gemm_dq<WT, BM, BN, WGM, WGN, RT>), grid, dim3(64 * WGM * WGN), L::SIZE, s, a);
     return hipGetLastError();
 }
