@@ -577,22 +577,24 @@ hipError_t launch_gemm_q4k(int nprob, const WPlanes *w, const int64_t *N, float 
     a.xd = sp.xd;
     a.x16 = sp.x16;
     // Tile: 128 x 128 (eight waves, two per SIMD, each with two 32 x 32 tiles) when that gives a workgroup to every
-    // CU, else 64 x 128 (eight waves of one 32 x 32 tile: twice the workgroups). Measured at M = 512, weights cold,
-    // with the activation pass: N = 4096 28.7 us on 128 workgroups of 128 x 128, 22.5 us on 256 of 64 x 128, 22.9 on
-    // 256 of 128 x 64 (four waves); N = 2048 27.1 / 20.7 / 22.0 us; N = 12288 51.0 us on 384 of 128 x 128, 53.8 on
-    // 768 of 64 x 128.
-    // A backend's tile option forces 128 x 128, 64 x 128 or 128 x 64; any other forced pair is refused.
+    // CU, else 64 x 64 (four waves of one 32 x 32 tile; 75 KB of LDS, two workgroups per CU). Measured at M = 512, K =
+    // 2048, weights cold, with the activation pass (us on 128 x 128 / 64 x 64 / 64 x 128 eight-wave / 128 x 64
+    // four-wave): N = 4096 28.7 / 22.7 / 22.4-22.5 / 22.9; N = 2048 27.1 / 16.6 / 20.7 / 21.8; N = 12288 51.0-53.9 /
+    // 51.9 / 52.9-53.8 / 55.1-55.4.
+    // A backend's tile option forces 128 x 128, 64 x 64, 64 x 128 or 128 x 64; any other forced pair is refused.
     int64_t wg_big = 0;
     for (int i = 0; i < nprob; i++) wg_big += (N[i] + 127) / 128 * ((M + 127) / 128);
-    int tile = wg_big >= 256 ? 0 : 1;  // 0: 128 x 128, 1: 64 x 128, 2: 128 x 64
+    int tile = wg_big >= 256 ? 0 : 3;  // 0: 128 x 128, 1: 64 x 128, 2: 128 x 64, 3: 64 x 64
     if (o.tile_m || o.tile_n) {
         if (o.tile_m == 128 && o.tile_n == 128) tile = 0;
         else if (o.tile_m == 64 && o.tile_n == 128) tile = 1;
         else if (o.tile_m == 128 && o.tile_n == 64) tile = 2;
+        else if (o.tile_m == 64 && o.tile_n == 64) tile = 3;
         else return hipErrorInvalidValue;
     }
     if (tile == 0) return launch_q4g<Q4gT<2, 2, 4>>(a, s);
     if (tile == 1) return launch_q4g<Q4gT<1, 2, 4>>(a, s);
+    if (tile == 3) return launch_q4g<Q4gT<1, 2, 2>>(a, s);
     return launch_q4g<Q4gT<2, 2, 2>>(a, s);
 }
 

@@ -1,5 +1,5 @@
 """Every kernel the products' dispatcher can pick, reached in one process: by the shapes that pick it by default
-(config 3's Q4_K prefill groups on the 128 x 128 and 64 x 128 eight-wave tiles) and by a backend's options
+(config 3's Q4_K prefill groups on the 128 x 128 eight-wave and 64 x 64 four-wave tiles) and by a backend's options
 (mx_backend_set_option: the int8 Q8_0 GEMM, the VALU-scaled int8 K-quant GEMM, each GEMM tile, forced K splits, the
 mat-vec's lanes per row, the MUL_MAT_ID experts kernel or grouped product and its mat-vec threshold), each held to the oracle at the
 parity bars of test_gpu_parity.py. Also the graph rule that a graph recorded before the backend's scratch grew is
@@ -38,9 +38,9 @@ def case(t, M, Ns, K, seed):
 
 
 # --------------------------------------------------------------------------------------- Q4_K prefill (config 3)
-# (M, widths, K): config 3's q/k/v group (128 workgroups of 128 x 128, so 256 of 64 x 128 by default), its gate/up
-# group (384 of 128 x 128 by default), attn_o (64 of 128 x 128, so 128 of 64 x 128) and a ragged product (192 of
-# 128 x 128, so 64 x 128 tiles with partial rows and columns).
+# (M, widths, K): config 3's q/k/v group (128 workgroups of 128 x 128, so 512 of 64 x 64 by default), its gate/up
+# group (384 of 128 x 128 by default), attn_o (64 of 128 x 128, so 256 of 64 x 64) and a ragged product (192 of
+# 128 x 128, so 64 x 64 tiles with partial rows and columns).
 Q4K_SHAPES = {"qkv": (512, [2048, 1024, 1024], 2048), "gate_up": (512, [6144, 6144], 2048),
               "attn_o": (512, [2048], 2048), "ragged": (300, [8100], 256)}
 
@@ -50,7 +50,7 @@ def test_q4k_gemm_config3_every_tile(mx, be, shape):
     M, Ns, K = Q4K_SHAPES[shape]
     t = O.TYPE_Q4_K
     ws, x, refs = case(t, M, Ns, K, 0x5EED3000 + len(Ns) * 100 + M)
-    for tile in [(0, 0), (128, 128), (128, 64), (64, 128)]:
+    for tile in [(0, 0), (128, 128), (128, 64), (64, 128), (64, 64)]:
         with be.options(tile_m=tile[0], tile_n=tile[1]):
             ys = run_products(mx, be, t, ws, Ns, x, K)
         for w, y, r in zip(ws, ys, refs):
@@ -205,10 +205,10 @@ def test_options_refused(mx, be):
         with pytest.raises(mx.MxError) as e:
             run_products(mx, be, t, ws, [N], x, K)
         assert e.value.code == mx.UNSUPPORTED
-    t, K = O.TYPE_Q4_K, 1024  # a 64 x 64 tile the Q4_K GEMM lacks
+    t, K = O.TYPE_Q4_K, 1024  # a 32 x 128 tile the Q4_K GEMM lacks
     ws = [weights(t, N, K, 0x5EED3701)]
     x = acts(0xAC703701, M, K)
-    with be.options(tile_m=64, tile_n=64):
+    with be.options(tile_m=32, tile_n=128):
         with pytest.raises(mx.MxError) as e:
             run_products(mx, be, t, ws, [N], x, K)
         assert e.value.code == mx.FAILED
