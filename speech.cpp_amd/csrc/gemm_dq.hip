@@ -985,10 +985,11 @@ struct DqPlan {
 // tiles. A forced tile the kernel lacks gives bm = 0 (refused by the launch).
 DqPlan dq_plan(int type, int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o) {
     DqPlan pl{64, 64, 1, 0};
-    // Q8_0 with direct B also has a 32 x 128 tile of four 32 x 32 waves, for blocks of at most 32 rows (the last,
-    // short block of a prompt): half the activation rows of a 64-row tile, so half its fragment reads and MFMAs
-    const bool skinny_ok = (type == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B && MX_DQ_Q8_WGM128 == 1) ||
-                           (type == MX_TYPE_Q6_K && MX_DQ_DIRECT_B6) || (type == MX_TYPE_Q5_K && MX_DQ_DIRECT_B5);
+    // The direct-B types also have a 32 x 128 tile of four 32 x 32 waves, for blocks of at most 32 rows (the last,
+    // short block of a prompt: half the activation rows of a 64-row tile, so half its fragment reads and MFMAs), and
+    // a 64 x 128 one of four 64 x 32 waves
+    const bool dirb = (type == MX_TYPE_Q8_0 && MX_DQ_DIRECT_B && MX_DQ_Q8_WGM128 == 1) ||
+                      (type == MX_TYPE_Q6_K && MX_DQ_DIRECT_B6) || (type == MX_TYPE_Q5_K && MX_DQ_DIRECT_B5);
     int64_t wg128 = 0;
     for (int i = 0; i < nprob; i++) {
         wg128 += (N[i] + 127) / 128;
@@ -999,21 +1000,25 @@ DqPlan dq_plan(int type, int nprob, const int64_t *N, int64_t M, int64_t K, cons
     // long products (K >= 4096) whose 128 x 128 grid is smaller still keep the large tile and split K instead (at
     // M = 512, N = 2048, K = 6144: four splits of 24 stages and the reduce beat 256 tiles of 64 x 64)
     const bool split128 = wg128 >= 32 && wg128 < 128 && nst >= 64;
-    // 128 x 128 from 192 workgroups of it, else 128 x 64 when that gives 256 (wg128 >= 128), else 64 x 64. Measured
-    // at M = 512, K = 2048, Q8_0, weights cold, with the activation pass (us on 64 x 64 / 128 x 64 / 128 x 128): N =
-    // 4096 30.5 / 30.3 / 33.2; N = 2048 21.9 / 27.6 / 29.4; N = 12288 70.7 / 62.0 / 47.3; the ASR q/k/v group 2048 +
-    // 1024 + 1024 32.1 / 30.0 / 33.7 (a group's grid holds only its problems' own tiles, so it runs as a product of
-    // its summed width)
+    // 128 x 128 from 192 workgroups of it, else, when half-height or half-width tiles give 256 (wg128 >= 128), 64 x 128
+    // (direct B: four waves of 64 x 32) or 128 x 64 (the others), else 64 x 64. Measured at M = 512, K = 2048, weights
+    // cold, with the activation pass (us on 64 x 64 / 64 x 128 / 128 x 64 / 128 x 128): Q8_0 N = 4096 29.9 / 29.1 /
+    // 29.1 / 32.8; N = 2048 21.4 / 24.0 / 27.1 / 29.2; N = 12288 73.8 / 57.5 / 64.1 / 49.1; the ASR q/k/v group 2048 +
+    // 1024 + 1024 32.0 / 29.7 / 29.7 / 33.3 (a group's grid holds only its problems' own tiles, so it runs as a product
+    // of its summed width); Q6_K N = 4096 39.2 / 33.7 / 39.4 / 39.8, N = 2048 28.2 / 31.4 / 31.6 / 38.2
     if (wg128 >= 192 || split128) pl.bm = pl.bn = 128;
-    else if (wg128 >= 128 && M >= 128) pl.bm = 128;
-    if (skinny_ok && M <= 32) {
+    else if (wg128 >= 128 && M >= 128) {
+        pl.bm = dirb ? 64 : 128;
+        pl.bn = dirb ? 128 : 64;
+    }
+    if (dirb && M <= 32) {
         pl.bm = 32;
         pl.bn = 128;
     }
     if (o.tile_m || o.tile_n) {
         const int tm = o.tile_m, tn = o.tile_n;
-        if (skinny_ok && tm == 32 && tn == 128) {
-            pl.bm = 32;
+        if (dirb && (tm == 32 || tm == 64) && tn == 128) {  // the direct-B types' 32 x 128 and 64 x 128
+            pl.bm = tm;
             pl.bn = 128;
         } else if ((tm == 64 || tm == 128) && (tn == 64 || tn == 128) && !(tm == 64 && tn == 128)) {
             pl.bm = tm;
@@ -1091,9 +1096,10 @@ static hipError_t launch_dq_type(const DqArgs &a, const DqPlan &pl, int maxN, hi
                   (WT == MX_TYPE_Q5_K && MX_DQ_DIRECT_B5)) {
         // direct B: four waves of 128 x 32, so every B fragment is converted by one wave only
         if (pl.bm == 128 && pl.bn == 128) return launch_dq<WT, 128, 128, 1, 4>(a, maxN, s);
+        if (pl.bm == 64 && pl.bn == 128) return launch_dq<WT, 64, 128, 1, 4>(a, maxN, s);
         if (pl.bm == 32) return launch_dq<WT, 32, 128, 1, 4>(a, maxN, s);
     }
-    if (pl.bm == 32) return hipErrorInvalidValue;
+    if (pl.bm == 32 || (pl.bm == 64 && pl.bn == 128)) return hipErrorInvalidValue;
     if (pl.bm == 128 && pl.bn == 128) return launch_dq<WT, 128, 128, 2, MX_DQ_WGN128>(a, maxN, s);
     if (pl.bm == 128) return launch_dq<WT, 128, 64, 4, 2>(a, maxN, s);
     return launch_dq<WT, 64, 64, 2, 2>(a, maxN, s);

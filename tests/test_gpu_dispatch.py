@@ -92,7 +92,7 @@ def test_kquant_int8_gemm(mx, be, t, M, Ns, K):
 def test_dq_gemm_every_tile_and_split(mx, be, t):
     M, N, K = 300, 1000, 2048
     ws, x, refs = case(t, M, [N], K, 0x5EED3300 + t)
-    for tile in [(64, 64), (128, 64), (128, 128)]:
+    for tile in [(64, 64), (128, 64), (128, 128), (64, 128)]:  # 64 x 128: the direct-B tile of four 64 x 32 waves
         for split in (1, 3):
             with be.options(tile_m=tile[0], tile_n=tile[1], split=split):
                 y = run_products(mx, be, t, ws, [N], x, K)[0]
