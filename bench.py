@@ -423,7 +423,7 @@ COPY_BYTES = 256 << 20  # the plain copy the counters are calibrated on
 TRAFFIC = {"decode": ("k_matvec_q8_0_qwen3-0.6b_decode.traffic.txt", "k_matvec"),
            "matvec": ("k_matvec_q8_0_3072x1024_rotated.traffic.txt", "k_matvec"),
            "prefill-q4k": ("k_gemm_q4k_qwen3-1.7b_prefill.traffic.txt", "k_gemm_q4k<"),
-           "asr-1.7b": ("k_gemm_dq_q8_0_qwen3-asr-1.7b_prefill.traffic.txt", "k_gemm_dq<8,"),
+           "asr-1.7b": ("k_gemm_q8_0_i8_qwen3-asr-1.7b_prefill.traffic.txt", "k_gemm_q8_0_i8<"),
            "moe": ("k_mmid_q4k_drama3_moe.traffic.txt", "k_mmid_q4k")}
 
 
@@ -906,13 +906,13 @@ def run_asr(args, mx, be, threads):
     ms_tok = time_graph(be, tok, max(1, args.steps) * ASR_DECODE_TOKENS, args.warmup, not args.no_graph)
     ms_step = ms_pre + ASR_DECODE_TOKENS * ms_tok
     table = label_table(pre + tok, per_label_pass(be, pre + tok, reps=3, use_graph=not args.no_graph))
-    # the prefill GEMM dequantizes Q8_0 weights and Q8_0-quantized activations to fp16 and accumulates in fp32 on
-    # fp16 MFMA (--opt gemm_q8_0=1 selects the int8 MFMA GEMM); the decode mat-vecs use int8 dot products
-    dq = be.get_option("gemm_q8_0") == 0
+    # the prefill GEMM multiplies Q8_0 weights and Q8_0-quantized activations on int8 MFMA, block by block (--opt
+    # gemm_q8_0=2 selects the fp16 dequantizing GEMM instead); the decode mat-vecs use int8 dot products
+    dq = be.get_option("gemm_q8_0") == 2
     big = [l for l in table if l == f"prefill_M{max(blocks)}"]  # the largest block's products (512 rows as run)
     roof = (mfma_roofline("k_gemm_dq<Q8_0> (with its activation pass)", table, big, FP16_PEAK_TFLOPS, "TFLOP/s")
             if dq else mfma_roofline("k_gemm_q8_0_i8 (with its activation pass)", table, big))
-    roof["traffic"] = read_traffic("asr-1.7b") if dq and max(blocks) == 512 else None  # measured on 512-row blocks
+    roof["traffic"] = read_traffic("asr-1.7b") if not dq and max(blocks) == 512 else None  # measured on 512-row blocks
     tops = pre_ops / (ms_pre * 1e-3) / 1e12
     tok_w = sum(L.weight_bytes for L in tok)
     result = base_result(args, round(tops, 2), "TOP/s", ms_step, "fp16" if dq else "int8", {
@@ -1200,7 +1200,7 @@ def main():
     ap.add_argument("--batches", type=ints, default=None,
                     help="moe: token batches (default 1,16,256; counter passes use 256)")
     ap.add_argument("--opt", action="append", default=[], metavar="NAME=VALUE",
-                    help="a kernel choice of the backend (mx_backend_set_option), e.g. gemm_q8_0=1; repeatable")
+                    help="a kernel choice of the backend (mx_backend_set_option), e.g. gemm_q8_0=2; repeatable")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the traffic summary of two rocprofv3 --pmc runs of --workload's benchmark and exit")
     ap.add_argument("--summarize-busy", nargs=2, metavar=("GRBM_CSV", "CLOCK_MHZ"),

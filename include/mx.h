@@ -115,14 +115,15 @@ MX_API int mx_backend_set_rounding(mx_backend *be, int rounding);
  * product it covers to one kernel, so a test can reach each kernel the dispatcher may pick, in one process. A product
  * the forced kernel cannot compute fails with MX_UNSUPPORTED (or MX_FAILED for a tile the kernel lacks) instead of
  * going elsewhere. Values outside those listed are refused with MX_INVALID.
- *   MX_OPT_GEMM_Q8_0          Q8_0 at M > 8: 0 the fp16 dequantizing GEMM, 1 the int8 MFMA GEMM (K % 128 == 0)
+ *   MX_OPT_GEMM_Q8_0          Q8_0 at M > 8: 0 as picked (the int8 MFMA GEMM where K % 128 == 0, else the fp16
+ *                             dequantizing GEMM where K % 64 == 0), 1 the int8 MFMA GEMM, 2 the fp16 dequantizing GEMM
  *   MX_OPT_GEMM_KQUANT        Q4_K / Q6_K at M > 8: 0 as picked (scale-split int8 for Q4_K, fp16 dequantizing for
  *                             Q6_K), 1 the VALU-scaled int8 GEMM
  *   MX_OPT_GEMM_TILE_M / _N   the GEMM's tile (0 0: picked per product): the Q4_K GEMM 128 x 128, 64 x 128, 128 x 64
  *                             or 64 x 64; the fp16 dequantizing GEMM 128 x 128, 128 x 64 or 64 x 64, and for Q8_0,
  *                             Q5_K and Q6_K also 64 x 128 and 32 x 128; the int8 Q8_0 GEMM 64 x 64, 64 x 128 or
  *                             128 x 128; the fp16 GEMM over MUL_MAT_ID's expert chunks 32 x 128, 32 x 64 or 64 x 64
- *   MX_OPT_GEMM_SPLIT         K splits of the fp16 dequantizing GEMM, 0 (picked) .. 64
+ *   MX_OPT_GEMM_SPLIT         K splits of the fp16 dequantizing GEMM and the int8 Q8_0 GEMM, 0 (picked) .. 64
  *   MX_OPT_MATVEC_LPR         lanes per weight row of the mat-vec: 0 (picked), 16, 32, 64
  *   MX_OPT_MMID_KERNEL        MUL_MAT_ID with many pairs: 0 as picked (Q4_K: the grouped int8 MFMA product; Q8_0,
  *                             Q5_K, Q6_K: the fp16 dequantizing GEMM over chunks of each expert's pairs from one /

@@ -3,8 +3,9 @@
 //
 // Activations are quantized once into scratch (k_gemm_quant), then each workgroup computes a BM x BN tile of Y:
 // 4 waves in a 2 x 2 arrangement, each owning (BM/2) x (BN/2) of the tile as 32 x 32 MFMA tiles. K advances in
-// stages of 128 staged through LDS (rows padded so 16-byte fragment reads spread over the banks); the next stage's
-// global loads are issued before the current stage's MFMAs run.
+// stages of 128 through a ring of NS stages in LDS, filled by buffer-to-LDS copies (no registers between global
+// memory and LDS): NS - 1 stages are in flight while one is computed, which a grid of one workgroup per CU needs to
+// cover the memory latency (one stage ahead, each 128-wide stage cost a round trip).
 //
 // Per 32-element block and 32 x 32 tile: one v_mfma_i32_32x32x32_i8 (the integer sums, exact), one
 // v_mfma_f32_32x32x8_f16 whose only non-zero k is dx (x) dw -- the outer product of the two fp16 scales, exact in
@@ -12,6 +13,7 @@
 #include "mx_common.h"
 #include "mx_device.h"
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -24,11 +26,14 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 constexpr int KS = 128;       // K per LDS stage
-constexpr int LROW = KS + 16; // padded LDS row (bytes)
+#ifndef MX_I8_NS64
+#define MX_I8_NS64 4          // ring stages of the 64 x 64 tile
+#endif
 
-// Activation rows -> int8 quants [M][K], fp32 block scales [M][K/32] (the fp16-rounded d, for Q8_0 weights).
+// Activation rows -> int8 quants [M][K], fp16 block scales [M][K/32] (d rounded to fp16, as the Q8_0 the weights
+// pair with stores it).
 __global__ __launch_bounds__(256) void k_gemm_quant_q8(const float *x, int64_t x_stride, int64_t K, int rounding,
-                                                       int8_t *xq, float *xd) {
+                                                       int8_t *xq, uint16_t *xd) {
     const int64_t m = blockIdx.y;
     const int64_t e = (int64_t)blockIdx.x * 1024 + 4 * threadIdx.x;
     const bool valid = e < K;
@@ -39,101 +44,43 @@ __global__ __launch_bounds__(256) void k_gemm_quant_q8(const float *x, int64_t x
     const int q = quant32_lane(v, rounding, &d, &sum);
     if (valid) {
         *(int *)(xq + m * K + e) = q;
-        if ((threadIdx.x & 7) == 0) xd[m * (K / 32) + e / 32] = h2f(f2h(d));
+        if ((threadIdx.x & 7) == 0) xd[m * (K / 32) + e / 32] = f2h(d);
     }
 }
 
-struct GemmArgs {
+struct GemmProblem {
     WPlanes w;
-    int64_t M, N, K;
-    const int8_t *xq;
-    const float *xd;
+    int64_t N;
     float *y;
     int64_t ldy;     // floats between consecutive m rows of Y
 };
-
-// One K stage of the workgroup's tiles in flight from global memory: 16 bytes of int8 quants per thread and pass
-// (8 threads cover a 128-byte row), plus the four fp16 block scales of one activation row and one weight row.
-template <int BM, int BN>
-struct Stage {
-    static constexpr int XP = BM * 8 / 256, WP = BN * 8 / 256;
-    v4i xr[XP], wr[WP];  // native vectors: HIP's int4 is a union type whose copies defeat register promotion
-    float dx[4];         // activation scales (fp16 values held in fp32), converted only when stored to LDS
-    uint32_t dw01, dw23;
+// Up to four weights sharing the activations. The grid is one dimension: split after split, problem after problem,
+// (N_p / BN) x (M / BM) tiles with n fastest. Split s covers the K stages [s per, (s + 1) per); with nsplit > 1 each
+// split writes its partial sums to ws ([nsplit][M][ntot], problem p at columns col0[p] ..) and k_gemm_reduce adds
+// them in split order.
+struct GemmArgs {
+    GemmProblem prob[4];
+    int nprob, nsplit;
+    int64_t M, K;
+    const int8_t *xq;
+    const uint16_t *xd;  // fp16 bits
+    int64_t ntot, col0[4];
+    float *ws;
 };
 
-// Per-thread source rows of the staging loads, clamped to the matrix once; a stage adds its K offset.
-template <int BM, int BN>
-struct StageSrc {
-    const int8_t *x[Stage<BM, BN>::XP];
-    const int8_t *w[Stage<BM, BN>::WP];
-    const float *dx;       // this thread's activation row of block scales
-    const uint16_t *dw;    // this thread's weight row of block scales
-};
-
-template <int BM, int BN>
-__device__ __forceinline__ StageSrc<BM, BN> stage_src(const GemmArgs &a, int64_t m0, int64_t n0, int tid) {
-    StageSrc<BM, BN> src;
-    const int64_t K = a.K, nblk = K / 32;
-    const int srow = tid >> 3, scol = (tid & 7) * 16;
-#pragma unroll
-    for (int p = 0; p < Stage<BM, BN>::XP; p++) {
-        int64_t m = m0 + srow + 32 * p;
-        m = m < a.M ? m : a.M - 1;
-        src.x[p] = a.xq + m * K + scol;
-    }
-#pragma unroll
-    for (int p = 0; p < Stage<BM, BN>::WP; p++) {
-        int64_t n = n0 + srow + 32 * p;
-        n = n < a.N ? n : a.N - 1;
-        src.w[p] = (const int8_t *)a.w.p0 + n * K + scol;
-    }
-    int64_t m = m0 + (tid & (BM - 1));
-    m = m < a.M ? m : a.M - 1;
-    src.dx = a.xd + m * nblk;
-    int64_t n = n0 + (tid & (BN - 1));
-    n = n < a.N ? n : a.N - 1;
-    src.dw = (const uint16_t *)a.w.p1 + n * nblk;
-    return src;
+template <class T>
+__device__ __forceinline__ T pick4(int i, T v0, T v1, T v2, T v3) {
+    return i == 0 ? v0 : (i == 1 ? v1 : (i == 2 ? v2 : v3));
 }
-
-template <int BM, int BN>
-__device__ __forceinline__ void load_stage(Stage<BM, BN> &st, const StageSrc<BM, BN> &src, int k0) {
-#pragma unroll
-    for (int p = 0; p < Stage<BM, BN>::XP; p++) st.xr[p] = *(const v4i *)(src.x[p] + k0);
-#pragma unroll
-    for (int p = 0; p < Stage<BM, BN>::WP; p++) st.wr[p] = *(const v4i *)(src.w[p] + k0);
-    // Every thread loads (rows clamped): no branch around the loads, so none of them is waited for here.
-    const float4 f = *(const float4 *)(src.dx + k0 / 32);
-    st.dx[0] = f.x;
-    st.dx[1] = f.y;
-    st.dx[2] = f.z;
-    st.dx[3] = f.w;
-    const uint32_t *p = (const uint32_t *)(src.dw + k0 / 32);
-    st.dw01 = p[0];
-    st.dw23 = p[1];
-}
-
-template <int BM, int BN>
-__device__ __forceinline__ void store_stage(const Stage<BM, BN> &st, int8_t *xs, int8_t *ws, uint16_t *dxs,
-                                            uint16_t *dws, int tid) {
-    const int srow = tid >> 3, scol = (tid & 7) * 16;
-#pragma unroll
-    for (int p = 0; p < Stage<BM, BN>::XP; p++) *(v4i *)(xs + (srow + 32 * p) * LROW + scol) = st.xr[p];
-#pragma unroll
-    for (int p = 0; p < Stage<BM, BN>::WP; p++) *(v4i *)(ws + (srow + 32 * p) * LROW + scol) = st.wr[p];
-    if (tid < BM) {
-        // the scales are fp16 values held in fp32: converting back is exact
-#pragma unroll
-        for (int b = 0; b < 4; b++) dxs[b * BM + tid] = f2h(st.dx[b]);
-    }
-    if (tid >= 128 && tid < 128 + BN) {
-        const int n = tid - 128;
-        dws[0 * BN + n] = (uint16_t)(st.dw01 & 0xFFFF);
-        dws[1 * BN + n] = (uint16_t)(st.dw01 >> 16);
-        dws[2 * BN + n] = (uint16_t)(st.dw23 & 0xFFFF);
-        dws[3 * BN + n] = (uint16_t)(st.dw23 >> 16);
-    }
+// Problem pi's fields one by one (selecting the whole struct by a run-time index copies the arguments to scratch).
+__device__ __forceinline__ GemmProblem problem(const GemmArgs &a, int pi) {
+    GemmProblem p{};
+    p.w.p0 = pick4(pi, a.prob[0].w.p0, a.prob[1].w.p0, a.prob[2].w.p0, a.prob[3].w.p0);
+    p.w.p1 = pick4(pi, a.prob[0].w.p1, a.prob[1].w.p1, a.prob[2].w.p1, a.prob[3].w.p1);
+    p.N = pick4(pi, a.prob[0].N, a.prob[1].N, a.prob[2].N, a.prob[3].N);
+    p.y = pick4(pi, a.prob[0].y, a.prob[1].y, a.prob[2].y, a.prob[3].y);
+    p.ldy = pick4(pi, a.prob[0].ldy, a.prob[1].ldy, a.prob[2].ldy, a.prob[3].ldy);
+    return p;
 }
 
 __device__ __forceinline__ _Float16 as_half(uint16_t b) {
@@ -142,22 +89,141 @@ __device__ __forceinline__ _Float16 as_half(uint16_t b) {
     return h;
 }
 
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void i8_lds_void;
+
+// The LDS ring: NS stages, each of A (BM rows of 128 quants), B (BN rows), and the four fp16 block scales of each
+// activation row (DX) and weight row (DW). Quant rows are stored as 8 chunks of 16 bytes, chunk c of row r at slot
+// c ^ i8_swz(r): the 16 rows one fragment read visits at a time fall on 16 distinct 16-byte bank groups.
+template <int BM, int BN>
+struct I8Lds {
+    static constexpr int NS = BM == 64 && BN == 64 ? MX_I8_NS64 : 3;
+    static constexpr int SA = BM * KS, SB = BN * KS, SDX = BM * 8, SDW = BN * 8;  // slot sizes (bytes)
+    static constexpr int A = 0, B = A + NS * SA, DX = B + NS * SB, DW = DX + NS * SDX, SIZE = DW + NS * SDW;
+    // copies per stage and wave: 16-byte ones of 8 quant rows each; 4-byte ones of 32 scale rows each, shared by the
+    // waves (a wave past the last scale copy repeats it: the same bytes to the same place)
+    static constexpr int QA = BM / 32, QB = BN / 32, NDX = BM / 32, NSC = (BM + BN) / 32, QS = (NSC + 3) / 4;
+    static constexpr int OPS = QA + QB + QS;
+    static_assert(SIZE <= 80 * 1024 || (BM == 128 && BN == 128), "two workgroups per CU");
+};
+
+__device__ __forceinline__ int i8_swz(int r) { return (r >> 1) & 7; }
+
+__device__ __forceinline__ v4u i8_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    return v4u{(uint32_t)b, (uint32_t)(b >> 32), bytes, 0x00020000u};
+}
+
+// Buffer-to-LDS copies (each lane's 16 or 4 bytes land at m0 + 16 or 4 x lane), issued through asm so that the
+// compiler does not count them as LDS stores that every later LDS read may alias (it would wait for all of them);
+// their waits are the explicit ones below.
+__device__ __forceinline__ void i8_dma16(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void i8_dma4(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
+                 : "memory", "m0");
+}
+template <int n>
+__device__ __forceinline__ void i8_wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+}
+
+// One wave's copies of a stage: per-lane byte offsets fixed for the whole K loop (rows past M or N clamped to the
+// last row), a per-stage uniform offset (k0 bytes of quants, k0 / 16 bytes of scales per row).
+template <int BM, int BN>
+struct I8Dma {
+    using L = I8Lds<BM, BN>;
+    uint32_t a[L::QA], b[L::QB], s[L::QS], ls[L::QS];
+    v4u ra, rb, rs[L::QS];
+    uint32_t la, lb;  // LDS offsets of this wave's first A and B copy in a slot
+
+    __device__ __forceinline__ void init(int wave, const GemmArgs &g, const GemmProblem &pb, int64_t m0, int64_t n0) {
+        const int lane = threadIdx.x & 63;
+        const uint32_t K = (uint32_t)g.K, nblk = K / 32, M = (uint32_t)g.M, N = (uint32_t)pb.N;
+        ra = i8_rsrc(g.xq, M * K);
+        rb = i8_rsrc(pb.w.p0, N * K);
+        const v4u rdx = i8_rsrc(g.xd, M * nblk * 2), rdw = i8_rsrc(pb.w.p1, N * nblk * 2);
+#pragma unroll
+        for (int q = 0; q < L::QA; q++) {
+            const int r = 8 * (wave * L::QA + q) + (lane >> 3);
+            a[q] = (uint32_t)min<int64_t>(m0 + r, M - 1) * K + 16u * (uint32_t)((lane & 7) ^ i8_swz(r));
+        }
+#pragma unroll
+        for (int q = 0; q < L::QB; q++) {
+            const int r = 8 * (wave * L::QB + q) + (lane >> 3);
+            b[q] = (uint32_t)min<int64_t>(n0 + r, N - 1) * K + 16u * (uint32_t)((lane & 7) ^ i8_swz(r));
+        }
+        la = (uint32_t)(wave * L::QA) * 1024u;
+        lb = (uint32_t)(wave * L::QB) * 1024u;
+#pragma unroll
+        for (int u = 0; u < L::QS; u++) {
+            const int j = min(wave * L::QS + u, L::NSC - 1);  // scale copy j: DX rows 32 j .., then DW rows
+            const bool isx = j < L::NDX;
+            const int r = 32 * (isx ? j : j - L::NDX) + (lane >> 1);
+            const int64_t row = isx ? min<int64_t>(m0 + r, M - 1) : min<int64_t>(n0 + r, N - 1);
+            s[u] = (uint32_t)row * nblk * 2u + 4u * (uint32_t)(lane & 1);
+            rs[u] = isx ? rdx : rdw;
+            ls[u] = isx ? (uint32_t)(L::DX + 256 * j) : (uint32_t)(L::DW + 256 * (j - L::NDX));
+        }
+    }
+
+    // stage k0 into ring slot `slot` (lds: the ring's LDS address)
+    __device__ __forceinline__ void issue(uint32_t lds, int slot, int k0) const {
+        const uint32_t sa = lds + L::A + slot * L::SA + la, sb = lds + L::B + slot * L::SB + lb;
+#pragma unroll
+        for (int q = 0; q < L::QA; q++) i8_dma16(ra, sa + 1024u * q, a[q], (uint32_t)k0);
+#pragma unroll
+        for (int q = 0; q < L::QB; q++) i8_dma16(rb, sb + 1024u * q, b[q], (uint32_t)k0);
+#pragma unroll
+        for (int u = 0; u < L::QS; u++) {
+            const uint32_t sl = ls[u] < (uint32_t)L::DW ? (uint32_t)(slot * L::SDX) : (uint32_t)(slot * L::SDW);
+            i8_dma4(rs[u], lds + ls[u] + sl, s[u], (uint32_t)(k0 / 16));
+        }
+    }
+};
+
 // 32 x 32 accumulator layout of the 32x32 MFMAs: lane l, register r holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32).
 template <int BM, int BN>
-__global__ __launch_bounds__(256) void k_gemm_q8_0_i8(GemmArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemm_q8_0_i8(GemmArgs a) {
+    using L = I8Lds<BM, BN>;
     constexpr int WM = BM / 2, WN = BN / 2;   // wave tile
     constexpr int TM = WM / 32, TN = WN / 32; // MFMA tiles per wave
-    __shared__ __align__(16) int8_t xs[BM * LROW];
-    __shared__ __align__(16) int8_t ws[BN * LROW];
-    __shared__ uint16_t dxs[KS / 32 * BM];   // fp16 bits, [block][m]
-    __shared__ uint16_t dws[KS / 32 * BN];   // fp16 bits, [block][n]
+    extern __shared__ __align__(16) uint8_t smem[];
+    const uint32_t lds = (uint32_t)(uintptr_t)(i8_lds_void *)smem;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t MT = (a.M + BM - 1) / BM;
+    int64_t per = 0;  // tiles of one split
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (i < a.nprob) per += (a.prob[i].N + BN - 1) / BN * MT;
+    int64_t t = blockIdx.x;
+    const int split = (int)(t / per);
+    t -= split * per;
+    int pi = 0;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const int64_t ti = (a.prob[i].N + BN - 1) / BN * MT;
+        if (pi == i && i + 1 < a.nprob && t >= ti) {
+            t -= ti;
+            pi = i + 1;
+        }
+    }
+    const GemmProblem pb = problem(a, pi);
+    const int64_t ntp = (pb.N + BN - 1) / BN;
+    const int64_t m0 = (t / ntp) * BM, n0 = (t % ntp) * BN;
     const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
-    const int K = (int)a.K;
-    Stage<BM, BN> st;
-    const StageSrc<BM, BN> src = stage_src<BM, BN>(a, m0, n0, tid);
+    const int nst = (int)(a.K / KS), sper = (nst + a.nsplit - 1) / a.nsplit;
+    const int kb0 = split * sper * KS, nloc = min(nst - split * sper, sper);  // this split's stages (never none)
+
+    I8Dma<BM, BN> dma;
+    dma.init(wave, a, pb, m0, n0);
+#pragma unroll
+    for (int s = 0; s < L::NS - 1; s++)
+        if (s < nloc) dma.issue(lds, s, kb0 + s * KS);
 
     float acc[TM][TN][16];
 #pragma unroll
@@ -167,96 +233,255 @@ __global__ __launch_bounds__(256) void k_gemm_q8_0_i8(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-    const int fr = lane & 31, fk = (lane >> 5) * 16;  // fragment row and k offset of this lane
-    load_stage<BM, BN>(st, src, 0);
-    for (int k0 = 0; k0 < K; k0 += KS) {
-        __syncthreads();  // the previous stage's fragments have been read
-        store_stage<BM, BN>(st, xs, ws, dxs, dws, tid);
-        __syncthreads();
-        // the next stage's loads are in flight while this stage computes (the last stage reloads itself: no branch,
-        // so the staging stays in registers)
-        load_stage<BM, BN>(st, src, k0 + KS < K ? k0 + KS : k0);
-#pragma unroll 1
-        for (int kb = 0; kb < KS / 32; kb++) {
-            v4i af[TM], bf[TN];
+    // this lane's fragment offsets in a slot: row wm + 32 i + fr (A) or wn + 32 j + fr (B), chunk 2 kb + fh
+    const int fr = lane & 31, fh = lane >> 5;
+    uint32_t aoff[TM][4], boff[TN][4], dxo[TM], dwo[TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const int r = wm + 32 * i + fr;
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) aoff[i][kb] = (uint32_t)(r * KS + 16 * ((2 * kb + fh) ^ i8_swz(r)));
+        dxo[i] = (uint32_t)(r * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int r = wn + 32 * j + fr;
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) boff[j][kb] = (uint32_t)(r * KS + 16 * ((2 * kb + fh) ^ i8_swz(r)));
+        dwo[j] = (uint32_t)(r * 8);
+    }
+    const _Float16 hz = (_Float16)0.0f;
+
+    for (int s = 0; s < nloc; s++) {
+        // this wave's copies of stage s have landed (those of the stages after it that were issued may not), then
+        // every wave's, and every wave has read the slot the next copies overwrite. The barrier is the bare
+        // instruction: __syncthreads' release fence would wait for the copies still in flight too.
+        const int rem = nloc - 1 - s;  // stages issued after s: min(rem, NS - 2)
+        if (rem >= L::NS - 2) i8_wait_vm<(L::NS - 2) * L::OPS>();
+        else if (L::NS > 3 && rem == 1) i8_wait_vm<L::OPS>();
+        else i8_wait_vm<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (s + L::NS - 1 < nloc) dma.issue(lds, (s + L::NS - 1) % L::NS, kb0 + (s + L::NS - 1) * KS);
+        const int slot = s % L::NS;
+        const uint8_t *sa = smem + L::A + slot * L::SA, *sb = smem + L::B + slot * L::SB;
+        const uint8_t *sdx = smem + L::DX + slot * L::SDX, *sdw = smem + L::DW + slot * L::SDW;
+        // every fragment and scale of the stage first, so the reads overlap each other and the MFMAs that follow
+        v4i af[4][TM], bf[4][TN];
+        uint2 dx4[TM], dw4[TN];  // the row's (column's) four fp16 block scales
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            dx4[i] = *(const uint2 *)(sdx + dxo[i]);
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) af[kb][i] = *(const v4i *)(sa + aoff[i][kb]);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            dw4[j] = *(const uint2 *)(sdw + dwo[j]);
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) bf[kb][j] = *(const v4i *)(sb + boff[j][kb]);
+        }
+        // block kb's integer sums and scale products; with few tiles per wave, block kb + 1's MFMAs are issued
+        // before block kb's conversions and fmas, so the matrix cores and the VALU overlap within the wave
+        constexpr int PD = TM * TN <= 2 ? 2 : 1;
+        v16i S[PD][TM][TN];
+        v16f C[PD][TM][TN];
+        auto mfma = [&](int kb, int d) {
             v4h as[TM], bs[TN];
 #pragma unroll
             for (int i = 0; i < TM; i++) {
-                af[i] = *(const v4i *)(xs + (wm + 32 * i + fr) * LROW + kb * 32 + fk);
-                const _Float16 s = lane < 32 ? as_half(dxs[kb * BM + wm + 32 * i + fr]) : (_Float16)0.0f;
-                as[i] = v4h{s, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+                const uint32_t w = kb < 2 ? dx4[i].x : dx4[i].y;
+                as[i] = v4h{fh ? hz : as_half((uint16_t)(kb & 1 ? w >> 16 : w & 0xFFFF)), hz, hz, hz};
             }
 #pragma unroll
             for (int j = 0; j < TN; j++) {
-                bf[j] = *(const v4i *)(ws + (wn + 32 * j + fr) * LROW + kb * 32 + fk);
-                const _Float16 s = lane < 32 ? as_half(dws[kb * BN + wn + 32 * j + fr]) : (_Float16)0.0f;
-                bs[j] = v4h{s, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+                const uint32_t w = kb < 2 ? dw4[j].x : dw4[j].y;
+                bs[j] = v4h{fh ? hz : as_half((uint16_t)(kb & 1 ? w >> 16 : w & 0xFFFF)), hz, hz, hz};
             }
+            const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+            const v16f fz = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-                    v16f fz = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-                    const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], zero, 0, 0, 0);
-                    const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(as[i], bs[j], fz, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float)S[r], sc[r], acc[i][j][r]);
+                    S[d][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[kb][i], bf[kb][j], zero, 0, 0, 0);
+                    C[d][i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(as[i], bs[j], fz, 0, 0, 0);
                 }
+        };
+        auto fold = [&](int d) {
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float)S[d][i][j][r], C[d][i][j][r], acc[i][j][r]);
+        };
+        mfma(0, 0);
+#pragma unroll
+        for (int kb = 0; kb < KS / 32; kb++) {
+            if (PD == 2 && kb + 1 < KS / 32) mfma(kb + 1, (kb + 1) % PD);
+            fold(kb % PD);
+            if (PD == 1 && kb + 1 < KS / 32) mfma(kb + 1, 0);
         }
     }
 
+    float *y = pb.y;
+    int64_t ldy = pb.ldy;
+    if (a.nsplit > 1) {  // this split's partial sums
+        y = a.ws + (int64_t)split * a.M * a.ntot + pick4(pi, a.col0[0], a.col0[1], a.col0[2], a.col0[3]);
+        ldy = a.ntot;
+    }
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             const int64_t n = n0 + wn + 32 * j + fr;
-            if (n >= a.N) continue;
+            if (n >= pb.N) continue;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int64_t m = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m < a.M) a.y[m * a.ldy + n] = acc[i][j][r];
+                if (m < a.M) y[m * ldy + n] = acc[i][j][r];
             }
         }
+}
+
+// y[m][col] = the nsplit partials of (m, col) added in split order (split 0 first); one thread per column.
+__global__ __launch_bounds__(256) void k_gemm_reduce(GemmArgs a) {
+    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+    if (c >= a.ntot) return;
+    const int64_t plane = a.M * a.ntot;
+    const float *ws = a.ws + m * a.ntot + c;
+    float v[8], sum = 0.0f;
+    for (int s0 = 0; s0 < a.nsplit; s0 += 8) {  // eight partials' loads in flight at a time
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (s0 + u < a.nsplit) v[u] = ws[(s0 + u) * plane];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (s0 + u < a.nsplit) sum += v[u];
+    }
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < 4; i++) pi += i < a.nprob && c >= a.col0[i];
+    const GemmProblem p = problem(a, pi);
+    p.y[m * p.ldy + (c - pick4(pi, a.col0[0], a.col0[1], a.col0[2], a.col0[3]))] = sum;
 }
 
 // ------------------------------------------------------------------------------------------------------------------
 // Host side.
 // ------------------------------------------------------------------------------------------------------------------
-size_t gemm_act_bytes(int64_t M, int64_t K) { return (size_t)M * (size_t)K; }
+// scratch: [xq: M K int8][xd: M K/32 fp16][partials: nsplit M ntot floats], each part 256-byte aligned
+static size_t gemm_xd_offset(int64_t M, int64_t K) { return ((size_t)M * (size_t)K + 255) / 256 * 256; }
+static size_t gemm_ws_offset(int64_t M, int64_t K) {
+    return gemm_xd_offset(M, K) + ((size_t)M * (size_t)(K / 32) * 2 + 255) / 256 * 256;
+}
 
 hipError_t launch_gemm_quant(int type, int rounding, const float *x, int64_t x_stride, int64_t M, int64_t K,
-                             void *xq, float *xd, hipStream_t s) {
+                             void *scratch, hipStream_t s) {
     if (type != MX_TYPE_Q8_0) return hipErrorInvalidValue;
+    int8_t *xq = (int8_t *)scratch;
+    uint16_t *xd = (uint16_t *)((uint8_t *)scratch + gemm_xd_offset(M, K));
     const dim3 grid((unsigned)((K + 1023) / 1024), (unsigned)M);
-    hipLaunchKernelGGL(k_gemm_quant_q8, grid, dim3(256), 0, s, x, x_stride, K, rounding, (int8_t *)xq, xd);
+    hipLaunchKernelGGL(k_gemm_quant_q8, grid, dim3(256), 0, s, x, x_stride, K, rounding, xq, xd);
     return hipGetLastError();
 }
 
-// Tile: 64 x 128 when the grid still gives about four workgroups per CU, else 64 x 64. A backend's tile option
-// (tile_m x tile_n: 64 x 64, 64 x 128 or 128 x 128) overrides it; any other forced pair is refused.
-static bool pick_tile(int64_t M, int64_t N, const Options &o, int &bm, int &bn) {
-    bm = 64;
-    bn = ((M + 63) / 64) * ((N + 127) / 128) >= 1024 ? 128 : 64;
-    if (o.tile_m || o.tile_n) {
-        if (!((o.tile_m == 64 && (o.tile_n == 64 || o.tile_n == 128)) || (o.tile_m == 128 && o.tile_n == 128)))
-            return false;
-        bm = o.tile_m;
-        bn = o.tile_n;
+namespace {
+struct GemmPlan {
+    int bm = 64, bn = 64, nsplit = 1;
+    int64_t ntot = 0;
+};
+
+// Tile: 64 x 128 when that tile gives 512 workgroups, else 64 x 64. A backend's tile option (tile_m x tile_n: 64 x 64,
+// 64 x 128 or 128 x 128) overrides it; any other forced pair is refused (bm = 0). K is split, into as many splits as
+// bring the grid to about 256 workgroups (each of at least four 128-wide stages), where the tiles are fewer than 256
+// and either K is long (32 stages or more) or the tiles number at most 64: elsewhere the partial sums' traffic (8
+// bytes per split, row and column) and the reduce cost more than the wider grid gains. A forced split count (1 ..
+// 64, at most one per stage) overrides that. Measured at K = 2048 (q/k/v 2048 + 1024 + 1024, N = 2048, gate/up
+// 2 x 6144) and K = 6144 (down, N = 2048), weights cold, best split (us): down M = 33 8 splits 14.3 (one: 32.9);
+// M = 130 4 splits 24.2 (33.2); M = 256 2 splits 28.5 (35.5); M = 512 one 37.4 (2 splits 41.8); N = 2048 at M = 33
+// 4 splits 11.1 (14.1), at M = 130 one 14.5 (2 splits 14.9), M = 256 one 15.0 (17.3); gate/up at M = 33 one 16.5
+// (2 splits 21.8).
+GemmPlan gemm_plan(int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o) {
+    GemmPlan pl;
+    int64_t t128 = 0;
+    for (int i = 0; i < nprob; i++) {
+        t128 += (N[i] + 127) / 128;
+        pl.ntot += N[i];
     }
-    return true;
+    t128 *= (M + 63) / 64;
+    if (t128 >= 512) pl.bn = 128;
+    if (o.tile_m || o.tile_n) {
+        if (!((o.tile_m == 64 && (o.tile_n == 64 || o.tile_n == 128)) || (o.tile_m == 128 && o.tile_n == 128))) {
+            pl.bm = 0;
+            return pl;
+        }
+        pl.bm = o.tile_m;
+        pl.bn = o.tile_n;
+    }
+    int64_t tiles = 0;
+    for (int i = 0; i < nprob; i++) tiles += (N[i] + pl.bn - 1) / pl.bn;
+    tiles *= (M + pl.bm - 1) / pl.bm;
+    const int64_t nst = K / KS;
+    int64_t want = tiles > 0 && tiles < 256 && (nst >= 32 || tiles <= 64) ? (256 + tiles - 1) / tiles : 1;
+    want = std::min<int64_t>(want, std::max<int64_t>(1, nst / 4));
+    if (o.split > 0) want = std::min<int64_t>(o.split, nst);
+    const int64_t per = (nst + want - 1) / want;  // stages per split; no split is left empty
+    pl.nsplit = (int)((nst + per - 1) / per);
+    return pl;
+}
+}  // namespace
+
+template <int BM, int BN>
+static hipError_t launch_i8(dim3 grid, const GemmArgs &a, hipStream_t s) {
+    constexpr int bytes = I8Lds<BM, BN>::SIZE;
+    static bool attr = false;
+    if (!attr) {
+        const hipError_t e = hipFuncSetAttribute((const void *)k_gemm_q8_0_i8<BM, BN>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_gemm_q8_0_i8<BM, BN>), grid, dim3(256), bytes, s, a);
+    return hipGetLastError();
 }
 
-hipError_t launch_gemm(int type, const WPlanes &w, int64_t M, int64_t N, int64_t K, const void *xq, const float *xd,
-                       float *y, int64_t ldy, const Options &o, hipStream_t s) {
-    if (type != MX_TYPE_Q8_0 || K % KS != 0) return hipErrorInvalidValue;
-    int bm, bn;
-    if (!pick_tile(M, N, o, bm, bn)) return hipErrorInvalidValue;
-    GemmArgs a{w, M, N, K, (const int8_t *)xq, xd, y, ldy};
-    const dim3 grid((unsigned)((N + bn - 1) / bn), (unsigned)((M + bm - 1) / bm));
-    if (bm == 128 && bn == 128) hipLaunchKernelGGL((k_gemm_q8_0_i8<128, 128>), grid, dim3(256), 0, s, a);
-    else if (bm == 64 && bn == 128) hipLaunchKernelGGL((k_gemm_q8_0_i8<64, 128>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((k_gemm_q8_0_i8<64, 64>), grid, dim3(256), 0, s, a);
+size_t gemm_scratch_bytes(int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o) {
+    const GemmPlan pl = gemm_plan(nprob, N, M, K, o);
+    size_t b = gemm_ws_offset(M, K);
+    if (pl.nsplit > 1) b += (size_t)pl.nsplit * (size_t)M * (size_t)pl.ntot * 4;
+    return b;
+}
+
+hipError_t launch_gemm(int type, int nprob, const WPlanes *w, const int64_t *N, float *const *y, const int64_t *ldy,
+                       int64_t M, int64_t K, void *scratch, const Options &o, hipStream_t s) {
+    if (type != MX_TYPE_Q8_0 || K % KS != 0 || nprob < 1 || nprob > 4 || M * K >= ((int64_t)1 << 31))
+        return hipErrorInvalidValue;
+    const GemmPlan pl = gemm_plan(nprob, N, M, K, o);
+    if (pl.bm == 0) return hipErrorInvalidValue;
+    GemmArgs a{};
+    int64_t tiles = 0;
+    for (int i = 0; i < nprob; i++) {
+        if (N[i] * K >= ((int64_t)1 << 31)) return hipErrorInvalidValue;  // the copies' 32-bit byte offsets
+        a.prob[i] = GemmProblem{w[i], N[i], y[i], ldy[i]};
+        a.col0[i] = i == 0 ? 0 : a.col0[i - 1] + N[i - 1];
+        tiles += (N[i] + pl.bn - 1) / pl.bn;
+    }
+    tiles *= (M + pl.bm - 1) / pl.bm;
+    if (tiles == 0) return hipSuccess;
+    a.nprob = nprob;
+    a.nsplit = pl.nsplit;
+    a.M = M;
+    a.K = K;
+    a.xq = (const int8_t *)scratch;
+    a.xd = (const uint16_t *)((const uint8_t *)scratch + gemm_xd_offset(M, K));
+    a.ntot = pl.ntot;
+    a.ws = (float *)((uint8_t *)scratch + gemm_ws_offset(M, K));
+    const dim3 grid((unsigned)(tiles * pl.nsplit));
+    hipError_t e = pl.bm == 128  ? launch_i8<128, 128>(grid, a, s)
+                   : pl.bn == 128 ? launch_i8<64, 128>(grid, a, s)
+                                  : launch_i8<64, 64>(grid, a, s);
+    if (e != hipSuccess || pl.nsplit == 1) return e;
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((pl.ntot + 255) / 256), (unsigned)M), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

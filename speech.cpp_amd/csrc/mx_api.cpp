@@ -305,7 +305,7 @@ MX_API int mx_backend_set_option(mx_backend *be, int option, int64_t value) {
     };
     switch (option) {
         case MX_OPT_GEMM_Q8_0:
-            if (!in({0, 1})) break;
+            if (!in({0, 1, 2})) break;
             o.gemm_q8_0 = (int)value;
             return MX_SUCCESS;
         case MX_OPT_GEMM_KQUANT:
@@ -666,32 +666,33 @@ static mx::WPlanes matrix_planes(const mx_tensor *w, int64_t mat) {
     return p;
 }
 
-// M > 8: quantize src1 once into scratch, then one MFMA GEMM per weight; batch slices one after another.
+// M > 8 on Q8_0 weights (int8 MFMA): per batch slice, src1 quantized once into scratch, then one launch over every
+// weight sharing it (plus the reduce when K is split).
 static int gemm_group(mx_backend *be, int n, const mx_tensor *const *src0, const mx_tensor *src1,
                       const mx_tensor *const *dst) {
     const mx_tensor *w0 = src0[0];
     const int64_t K = w0->ne[0], M = src1->ne[1];
-    const size_t xq_bytes = mx::align_up(mx::gemm_act_bytes(M, K), 256);
-    const size_t xd_bytes = mx::align_up((uint64_t)M * (uint64_t)(K / 32) * 4, 256);
-    int rc = ensure_scratch(be, xq_bytes + xd_bytes);
+    int64_t Ns[4];
+    for (int i = 0; i < n; i++) Ns[i] = src0[i]->ne[1];
+    int rc = ensure_scratch(be, mx::gemm_scratch_bytes(n, Ns, M, K, be->opt));
     if (rc) return rc;
-    void *xq = be->scratch;
-    float *xd = (float *)((uint8_t *)be->scratch + xq_bytes);
     const int64_t r2 = src1->ne[2] / w0->ne[2], r3 = src1->ne[3] / w0->ne[3];
     for (int64_t i13 = 0; i13 < src1->ne[3]; i13++)
         for (int64_t i12 = 0; i12 < src1->ne[2]; i12++) {
             const float *x = (const float *)((const uint8_t *)src1->data + i12 * src1->nb[2] + i13 * src1->nb[3]);
-            HIP_OK(mx::launch_gemm_quant(w0->type, be->rounding, x, (int64_t)(src1->nb[1] / 4), M, K, xq, xd,
+            HIP_OK(mx::launch_gemm_quant(w0->type, be->rounding, x, (int64_t)(src1->nb[1] / 4), M, K, be->scratch,
                                          be->stream),
                    "GEMM activation quantization");
+            mx::WPlanes w[4];
+            int64_t N[4], ldy[4];
+            float *y[4];
             for (int i = 0; i < n; i++) {
-                const int64_t N = src0[i]->ne[1];
-                const mx::WPlanes w = matrix_planes(src0[i], i12 / r2 + (i13 / r3) * src0[i]->ne[2]);
-                float *y = (float *)((uint8_t *)dst[i]->data + i12 * dst[i]->nb[2] + i13 * dst[i]->nb[3]);
-                HIP_OK(mx::launch_gemm(src0[i]->type, w, M, N, K, xq, xd, y, (int64_t)(dst[i]->nb[1] / 4), be->opt,
-                                       be->stream),
-                       "GEMM launch");
+                w[i] = matrix_planes(src0[i], i12 / r2 + (i13 / r3) * src0[i]->ne[2]);
+                N[i] = src0[i]->ne[1];
+                y[i] = (float *)((uint8_t *)dst[i]->data + i12 * dst[i]->nb[2] + i13 * dst[i]->nb[3]);
+                ldy[i] = (int64_t)(dst[i]->nb[1] / 4);
             }
+            HIP_OK(mx::launch_gemm(w0->type, n, w, N, y, ldy, M, K, be->scratch, be->opt, be->stream), "GEMM launch");
         }
     return MX_SUCCESS;
 }
@@ -813,16 +814,18 @@ static int matvec_group(mx_backend *be, int n, const mx_tensor *const *src0, con
         const mx::Options &o = be->opt;
         bool fits = true;  // every weight's rows within 32-bit element offsets
         for (int i = 0; i < n; i++) fits = fits && src0[i]->ne[1] * a.K < ((int64_t)1 << 31);
-        if (a.type == MX_TYPE_Q8_0 && o.gemm_q8_0 == 1) {
-            if (!mx::gemm_supported(a.type, a.K)) return fail(MX_UNSUPPORTED, "int8 Q8_0 GEMM: K must be a multiple of 128");
-            return gemm_group(be, n, src0, src1, dst);
+        if (a.type == MX_TYPE_Q8_0 && o.gemm_q8_0 != 2) {  // the int8 GEMM: picked wherever it can take the product
+            if (fits && mx::gemm_supported(a.type, M, a.K)) return gemm_group(be, n, src0, src1, dst);
+            if (o.gemm_q8_0 == 1)
+                return fail(MX_UNSUPPORTED, "int8 Q8_0 GEMM: K must be a multiple of 128 (and M K, N K below 2^31)");
         }
+        if (a.type == MX_TYPE_Q8_0 && o.gemm_q8_0 == 2 && !(fits && mx::gemm_dq_supported(a.type, M, a.K)))
+            return fail(MX_UNSUPPORTED, "fp16 Q8_0 GEMM: K must be a multiple of 64 (and M K, N K below 2^31)");
         if ((a.type == MX_TYPE_Q4_K || a.type == MX_TYPE_Q6_K) && o.gemm_kquant == 1) {
             if (!mx::gemm_kq_supported(a.type, a.K)) return fail(MX_UNSUPPORTED, "int8 K-quant GEMM: K % 256");
             return gemm_kq_group(be, n, src0, src1, dst);
         }
         if (fits && mx::gemm_dq_supported(a.type, M, a.K)) return gemm_dq_group(be, n, src0, src1, dst);
-        if (mx::gemm_supported(a.type, a.K)) return gemm_group(be, n, src0, src1, dst);
         if (a.type == MX_TYPE_Q4_K && a.K % 256 == 0) return gemm_q4k_group(be, n, src0, src1, dst);
         if (mx::gemm_kq_supported(a.type, a.K)) return gemm_kq_group(be, n, src0, src1, dst);
     }

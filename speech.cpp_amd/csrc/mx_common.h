@@ -106,10 +106,10 @@ inline WPlanes wplanes(const void *base, const Planes &pl) {
 // choice reaches one kernel so that every kernel the dispatcher can pick is testable in one process.
 // ------------------------------------------------------------------------------------------------------------------
 struct Options {
-    int gemm_q8_0 = 0;              // Q8_0 at M > 8: 0 the fp16 dequantizing GEMM, 1 the int8 MFMA GEMM
+    int gemm_q8_0 = 0;              // Q8_0 at M > 8: 0 picked (int8 MFMA), 1 int8 MFMA, 2 fp16 dequantizing
     int gemm_kquant = 0;            // Q4_K / Q6_K at M > 8: 0 as picked, 1 the VALU-scaled int8 GEMM (k_gemm_kq)
     int tile_m = 0, tile_n = 0;     // GEMM tile (0: picked per product)
-    int split = 0;                  // K splits of the fp16 dequantizing GEMM (0: picked)
+    int split = 0;                  // K splits of the prefill GEMMs that split K (0: picked)
     int matvec_lpr = 0;             // lanes per row of the mat-vec: 16, 32 or 64 (0: picked)
     int mmid_kernel = 0;            // MUL_MAT_ID with many pairs: 0 as picked, 1 the experts kernel, 2 the grouped
                                     // product (Q4_K: int8 MFMA; Q8_0, Q5_K, Q6_K: the fp16 GEMM over expert chunks)
@@ -199,14 +199,19 @@ hipError_t launch_matvec(const MatvecArgs &a, hipStream_t s);
 // F16, K % 4 == 0 for F32; no ids mode).
 hipError_t launch_matvec_f(const MatvecArgs &a, hipStream_t s);
 
-// Prefill GEMM on int8 MFMA (Q8_0, M > 8): activations quantized once into scratch (gemm_act_bytes of int8 quants,
-// plus M * K/32 fp32 block scales), then MFMA tiles. A forced tile the kernel lacks is refused (hipErrorInvalidValue).
-size_t gemm_act_bytes(int64_t M, int64_t K);
+// Prefill GEMM on int8 MFMA (Q8_0, M > 8): launch_gemm_quant writes the activations as Q8_0 (int8 quants and fp32
+// block scales) at the start of `scratch`, launch_gemm runs up to four weights sharing them in one launch (plus a
+// reduce launch when K is split; the partial sums follow the activations in scratch). gemm_scratch_bytes is the
+// scratch both need (for the tile and split `o` forces, or those picked). A forced tile the kernel lacks is refused
+// (hipErrorInvalidValue).
+size_t gemm_scratch_bytes(int nprob, const int64_t *N, int64_t M, int64_t K, const Options &o);
 hipError_t launch_gemm_quant(int type, int rounding, const float *x, int64_t x_stride, int64_t M, int64_t K,
-                             void *xq, float *xd, hipStream_t s);
-hipError_t launch_gemm(int type, const WPlanes &w, int64_t M, int64_t N, int64_t K, const void *xq, const float *xd,
-                       float *y, int64_t ldy, const Options &o, hipStream_t s);
-inline bool gemm_supported(int type, int64_t K) { return type == MX_TYPE_Q8_0 && K % 128 == 0; }
+                             void *scratch, hipStream_t s);
+hipError_t launch_gemm(int type, int nprob, const WPlanes *w, const int64_t *N, float *const *y, const int64_t *ldy,
+                       int64_t M, int64_t K, void *scratch, const Options &o, hipStream_t s);
+inline bool gemm_supported(int type, int64_t M, int64_t K) {
+    return type == MX_TYPE_Q8_0 && K % 128 == 0 && M * K < ((int64_t)1 << 31);
+}
 
 // Prefill GEMM on the fp16 matrix cores over dequantized tiles (Q8_0 weights): launch_gemm_dq_act writes the
 // activations' quantized values as fp16 at the start of `scratch`, launch_gemm_dq runs up to four weights sharing

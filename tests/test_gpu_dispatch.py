@@ -1,8 +1,8 @@
 """Every kernel the products' dispatcher can pick, reached in one process: by the shapes that pick it by default
 (config 3's Q4_K prefill groups on the 128 x 128 eight-wave and 64 x 64 four-wave tiles) and by a backend's options
-(mx_backend_set_option: the int8 Q8_0 GEMM, the VALU-scaled int8 K-quant GEMM, each GEMM tile, forced K splits, the
-mat-vec's lanes per row, the MUL_MAT_ID experts kernel or grouped product and its mat-vec threshold), each held to the oracle at the
-parity bars of test_gpu_parity.py. Also the graph rule that a graph recorded before the backend's scratch grew is
+(mx_backend_set_option: the int8 Q8_0 GEMM's tiles and K splits, the fp16 GEMM on Q8_0, the VALU-scaled int8 K-quant
+GEMM, each GEMM tile, forced K splits, the mat-vec's lanes per row, the MUL_MAT_ID experts kernel or grouped product
+and its mat-vec threshold), each held to the oracle at the parity bars of test_gpu_parity.py. Also the graph rule that a graph recorded before the backend's scratch grew is
 refused."""
 import ctypes
 
@@ -64,15 +64,16 @@ I8_SHAPES = {"qkv": (512, [2048, 1024, 1024], 2048), "down": (512, [2048], 6144)
 
 
 @pytest.mark.parametrize("shape", list(I8_SHAPES))
-def test_q8_0_int8_gemm_every_tile(mx, be, shape):
+def test_q8_0_int8_gemm_every_tile_and_split(mx, be, shape):
     M, Ns, K = I8_SHAPES[shape]
     t = O.TYPE_Q8_0
     ws, x, refs = case(t, M, Ns, K, 0x5EED3100 + M + K)
     for tile in [(0, 0), (64, 64), (64, 128), (128, 128)]:
-        with be.options(gemm_q8_0=1, tile_m=tile[0], tile_n=tile[1]):
-            ys = run_products(mx, be, t, ws, Ns, x, K)
-        for w, y, r in zip(ws, ys, refs):
-            check_product(t, w, x, y, K, int8=True, y_ref=r)
+        for split in (0, 1, 3, 64):  # 64: more than the 128-wide stages of K, so one split per stage
+            with be.options(gemm_q8_0=1, tile_m=tile[0], tile_n=tile[1], split=split):
+                ys = run_products(mx, be, t, ws, Ns, x, K)
+            for w, y, r in zip(ws, ys, refs):
+                check_product(t, w, x, y, K, int8=True, y_ref=r)
 
 
 # --------------------------------------------------------------------------------------- VALU-scaled int8 K-quants
@@ -88,15 +89,17 @@ def test_kquant_int8_gemm(mx, be, t, M, Ns, K):
 
 
 # --------------------------------------------------------------------------------------- fp16 dequantizing GEMM
+FP16_Q8 = {"gemm_q8_0": 2}  # Q8_0 products on the fp16 GEMM (the int8 one is picked where K % 128 == 0)
+
 @pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q5_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
 def test_dq_gemm_every_tile_and_split(mx, be, t):
     M, N, K = 300, 1000, 2048
     ws, x, refs = case(t, M, [N], K, 0x5EED3300 + t)
     for tile in [(64, 64), (128, 64), (128, 128), (64, 128)]:  # 64 x 128: the direct-B tile of four 64 x 32 waves
         for split in (1, 3):
-            with be.options(tile_m=tile[0], tile_n=tile[1], split=split):
+            with be.options(tile_m=tile[0], tile_n=tile[1], split=split, **FP16_Q8):
                 y = run_products(mx, be, t, ws, [N], x, K)[0]
-            check_product(t, ws[0], x, y, K, y_ref=refs[0])
+            check_product(t, ws[0], x, y, K, y_ref=refs[0], dq=True)
 
 
 @pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q5_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
@@ -109,11 +112,13 @@ def test_dq_gemm_short_blocks(mx, be, t, M):
     for N, K in ((1000, 2048), (2048, 6144), (333, 1024)):
         ws, x, refs = case(t, M, [N], K, 0x5EED3500 + M + N)
         for split in ((0, 1, 3) if M <= 32 else (0,)):
-            with be.options(tile_m=32, tile_n=128, split=split):
+            with be.options(tile_m=32, tile_n=128, split=split, **FP16_Q8):
                 y = run_products(mx, be, t, ws, [N], x, K)[0]
-            check_product(t, ws[0], x, y, K, y_ref=refs[0])
-        if M <= 32:  # picked without options
-            check_product(t, ws[0], x, run_products(mx, be, t, ws, [N], x, K)[0], K, y_ref=refs[0])
+            check_product(t, ws[0], x, y, K, y_ref=refs[0], dq=True)
+        if M <= 32:  # picked without the tile options
+            with be.options(**FP16_Q8):
+                y = run_products(mx, be, t, ws, [N], x, K)[0]
+            check_product(t, ws[0], x, y, K, y_ref=refs[0], dq=True)
 
 
 def test_dq_gemm_tiny_rows(mx, be):
@@ -190,7 +195,7 @@ def test_mmid_dq_every_tile(mx, be, t, tile):
 
 # --------------------------------------------------------------------------------------- refusals
 def test_options_refused(mx, be):
-    for name, bad in [("gemm_q8_0", 2), ("tile_m", 96), ("matvec_lpr", 8), ("split", -1), ("mmid_matvec_pairs", -1),
+    for name, bad in [("gemm_q8_0", 3), ("tile_m", 96), ("matvec_lpr", 8), ("split", -1), ("mmid_matvec_pairs", -1),
                       ("mmid_kernel", 3), ("mmid_chunk", 8)]:
         with pytest.raises(mx.MxError) as e:
             be.set_option(name, bad)

@@ -17,21 +17,27 @@ TOL = 1e-3         # the parity bar
 TIGHT = 2e-5       # what exact integer sums with an fp32 cross-block sum give
 
 
+def dq_types(t, K):
+    """Whether the dequantizing fp16 GEMM can take weights of type t and width K (Q8_0 K % 64, Q5_K / Q6_K K % 256)."""
+    return (t == O.TYPE_Q8_0 and K % 64 == 0) or (t in (O.TYPE_Q5_K, O.TYPE_Q6_K) and K % 256 == 0)
+
+
 def uses_dq(t, M, K, int8=False):
-    """Whether MUL_MAT takes the dequantizing fp16 GEMM (its dispatch rule; int8: an int8 GEMM forced by the backend's
+    """Whether MUL_MAT takes the dequantizing fp16 GEMM (its dispatch rule: past eight rows, Q5_K / Q6_K, and Q8_0
+    where K is not a multiple of 128, which the int8 Q8_0 GEMM takes; int8: an int8 GEMM forced by the backend's
     options)."""
-    return not int8 and M > 8 and ((t == O.TYPE_Q8_0 and K % 64 == 0) or
-                                   (t in (O.TYPE_Q5_K, O.TYPE_Q6_K) and K % 256 == 0))
+    return not int8 and M > 8 and dq_types(t, K) and not (t == O.TYPE_Q8_0 and K % 128 == 0)
 
 
-def check_product(t, w, x, y, K, rounding=O.ROUND_REF, int8=False, y_ref=None):
+def check_product(t, w, x, y, K, rounding=O.ROUND_REF, int8=False, y_ref=None, dq=None):
     """Parity of one product. The integer paths sum the oracle's exact per-block integers: held to TIGHT. The
     dequantizing fp16 GEMM rounds each operand to fp16 once: held to TOL against the oracle and to TIGHT against a
-    model of exactly that rounding, which a dropped or misplaced term would miss by far more."""
+    model of exactly that rounding, which a dropped or misplaced term would miss by far more. dq: whether the product
+    ran on the fp16 GEMM (None: as the dispatch rule picks)."""
     M = x.shape[0]
     if y_ref is None:
         y_ref = O.mul_mat(t, w, x, rounding=rounding)
-    if uses_dq(t, M, K, int8):
+    if uses_dq(t, M, K, int8) if dq is None else dq:
         assert rel_err(y, y_ref) <= TOL
         assert l2_rel(y, y_ref) <= TOL
         assert rel_err(y, dq_model(O, t, w, x, K, rounding)) <= TIGHT
@@ -202,7 +208,7 @@ def test_mul_mat_small_m(mx, be, t, M):
     w = weights(t, N, K, 0x5EED0400 + t)
     x = acts(0xAC700400 + M, M, K)
     y = run_mul_mat(mx, be, t, w, x, K, N)
-    if uses_dq(t, M, K):  # past eight columns Q8_0 / Q6_K take the fp16 GEMM
+    if uses_dq(t, M, K):  # past eight columns Q8_0 at K % 128 != 0 and Q6_K take the fp16 GEMM
         check_product(t, w, x, y, K)
         return
     assert rel_err(y, O.mul_mat(t, w, x)) <= TIGHT
@@ -325,7 +331,7 @@ def mmid_uses_dq(t, K, npairs, E, kernel=0, matvec_pairs=16):
     """Whether MUL_MAT_ID takes the dequantizing fp16 GEMM over chunks of each expert's pairs (its dispatch rule:
     Q8_0 / Q5_K / Q6_K experts, more pairs than the mat-vec launch takes, on average at least one (Q8_0) or three
     (K-quants) pairs per expert, or the GEMM forced; never when the experts kernel is forced)."""
-    if npairs <= matvec_pairs or kernel == 1 or not uses_dq(t, 9, K):
+    if npairs <= matvec_pairs or kernel == 1 or not dq_types(t, K):
         return False
     return kernel == 2 or npairs >= (1 if t == O.TYPE_Q8_0 else 3) * E
 
@@ -569,20 +575,28 @@ def test_graph_replay_matches_eager(mx, be):
 
 
 # ----------------------------------------------------------------------------------------------- MUL_MAT, M > 8
+Q8_PATHS = {"int8": 0, "fp16": 2}  # the Q8_0 GEMM option: as picked (the int8 GEMM), the fp16 GEMM forced
+
+
+@pytest.mark.parametrize("path", list(Q8_PATHS))
 @pytest.mark.parametrize("M,N,K", [(9, 100, 1024), (64, 256, 2048), (130, 333, 1024), (512, 2048, 2048),
                                    (100, 64, 6144), (650, 4500, 512), (300, 8100, 256), (520, 8200, 256)])
-def test_mul_mat_gemm_q8_0(mx, be, M, N, K):
-    """The last three take 128 x 128 tiles unsplit with ragged rows and columns (216, 192 and 325 workgroups: the last
-    more than the CUs); the last two have four stages of K, one more than the copy ring holds."""
+def test_mul_mat_gemm_q8_0(mx, be, M, N, K, path):
+    """Both Q8_0 GEMMs. Short blocks split K (9 and 64 rows; 100 rows over K = 6144); on the fp16 GEMM the last three
+    take 128 x 128 tiles unsplit with ragged rows and columns (216, 192 and 325 workgroups: the last more than the
+    CUs); the last two have two (K = 256) and four (K = 512) stages of K, fewer than the int8 GEMM's copy ring holds
+    and one more than the fp16 GEMM's."""
     t = O.TYPE_Q8_0
     w = weights(t, N, K, 0x5EED0A00 + M + N)
     x = acts(0xAC700A00 + M, M, K)
-    y = run_mul_mat(mx, be, t, w, x, K, N)
-    check_product(t, w, x, y, K)
+    with be.options(gemm_q8_0=Q8_PATHS[path]):
+        y = run_mul_mat(mx, be, t, w, x, K, N)
+    check_product(t, w, x, y, K, dq=path == "fp16")
 
 
-def test_mul_mat_gemm_group_q8_0_split(mx, be):
-    """A short block (28 rows) through the grouped fp16 GEMM: K is split over several workgroups per tile and the
+@pytest.mark.parametrize("path", list(Q8_PATHS))
+def test_mul_mat_gemm_group_q8_0_split(mx, be, path):
+    """A short block (28 rows) through either grouped Q8_0 GEMM: K is split over several workgroups per tile and the
     partial sums of the three products are added by one reduce pass; a second run gives the same bits."""
     t, K, M = O.TYPE_Q8_0, 2048, 28
     Ns = [200, 64, 72]
@@ -591,32 +605,36 @@ def test_mul_mat_gemm_group_q8_0_split(mx, be):
     W = [be.tensor(t, (K, n), w) for n, w in zip(Ns, ws)]
     X = be.tensor(mx.F32, (K, M), x)
     Y = [be.tensor(mx.F32, (n, M)) for n in Ns]
-    be.mul_mat_group(W, X, Y)
-    be.sync()
-    first = [yt.numpy().reshape(M, n).copy() for n, yt in zip(Ns, Y)]
-    for n, w, y in zip(Ns, ws, first):
-        check_product(t, w, x, y, K)
-    be.mul_mat_group(W, X, Y)
-    be.sync()
+    with be.options(gemm_q8_0=Q8_PATHS[path]):
+        be.mul_mat_group(W, X, Y)
+        be.sync()
+        first = [yt.numpy().reshape(M, n).copy() for n, yt in zip(Ns, Y)]
+        for n, w, y in zip(Ns, ws, first):
+            check_product(t, w, x, y, K, dq=path == "fp16")
+        be.mul_mat_group(W, X, Y)
+        be.sync()
     for n, yt, y in zip(Ns, Y, first):
         assert bits_equal(yt.numpy().reshape(M, n), y)
 
 
-@pytest.mark.parametrize("t,M,Ns,K", [(O.TYPE_Q8_0, 160, [3000], 4096), (O.TYPE_Q6_K, 160, [3000], 4096),
-                                      (O.TYPE_Q5_K, 160, [3000], 4096), (O.TYPE_Q8_0, 140, [1024, 1024], 4096)],
-                         ids=["q8_0", "q6_K", "q5_K", "q8_0_group"])
-def test_mul_mat_gemm_long_k(mx, be, t, M, Ns, K):
-    """Long products whose 128 x 128 grid is small keep the large tile and split K: ragged widths through the scalar
-    reduce, a two-weight group of widths divisible by four through the vector one."""
+@pytest.mark.parametrize("t,M,Ns,K,q8", [(O.TYPE_Q8_0, 160, [3000], 4096, 2), (O.TYPE_Q6_K, 160, [3000], 4096, 0),
+                                         (O.TYPE_Q5_K, 160, [3000], 4096, 0), (O.TYPE_Q8_0, 140, [1024, 1024], 4096, 2),
+                                         (O.TYPE_Q8_0, 160, [3000], 4096, 0), (O.TYPE_Q8_0, 140, [1024, 1024], 4096, 0)],
+                         ids=["q8_0_fp16", "q6_K", "q5_K", "q8_0_group_fp16", "q8_0_int8", "q8_0_group_int8"])
+def test_mul_mat_gemm_long_k(mx, be, t, M, Ns, K, q8):
+    """Long products whose grid is small split K. On the fp16 GEMM they keep the 128 x 128 tile: ragged widths through
+    the scalar reduce, a two-weight group of widths divisible by four through the vector one. On the int8 Q8_0 GEMM
+    (32 stages of K): two splits of 64 x 64 tiles, ragged and grouped."""
     ws = [weights(t, n, K, 0x5EED1400 + n + t) for n in Ns]
     x = acts(0xAC701400 + M, M, K)
     W = [be.tensor(t, (K, n), w) for n, w in zip(Ns, ws)]
     X = be.tensor(mx.F32, (K, M), x)
     Y = [be.tensor(mx.F32, (n, M)) for n in Ns]
-    be.mul_mat_group(W, X, Y)
-    be.sync()
+    with be.options(gemm_q8_0=q8):
+        be.mul_mat_group(W, X, Y)
+        be.sync()
     for n, w, yt in zip(Ns, ws, Y):
-        check_product(t, w, x, yt.numpy().reshape(M, n), K)
+        check_product(t, w, x, yt.numpy().reshape(M, n), K, dq=None if t != O.TYPE_Q8_0 else q8 == 2)
 
 
 def test_mul_mat_gemm_batched(mx, be):
