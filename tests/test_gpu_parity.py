@@ -578,6 +578,52 @@ def test_graph_replay_matches_eager(mx, be):
 Q8_PATHS = {"int8": 0, "fp16": 2}  # the Q8_0 GEMM option: as picked (the int8 GEMM), the fp16 GEMM forced
 
 
+# (type, Q8_0 option, rows, widths, K): the int8 Q8_0 GEMM split four ways (28 rows, a group) and on 64 x 128 tiles
+# unsplit (130 rows x 2 x 3000: 564 tiles of 64 x 128), the fp16 GEMM split (Q8_0 forced, Q6_K), the Q4_K GEMM
+GRAPH_CASES = {"q8_0_int8_split": (O.TYPE_Q8_0, 0, 28, [200, 64, 72], 2048),
+               "q8_0_int8_wide": (O.TYPE_Q8_0, 0, 130, [3000, 3000], 1024),
+               "q8_0_fp16_split": (O.TYPE_Q8_0, 2, 28, [200, 64, 72], 2048),
+               "q6_K_fp16": (O.TYPE_Q6_K, 0, 40, [1000], 4096),
+               "q4_K": (O.TYPE_Q4_K, 0, 130, [1024, 512], 2048)}
+
+
+@pytest.mark.parametrize("case", list(GRAPH_CASES))
+def test_gemm_graph_replays(mx, be, case):
+    """A prefill group recorded into a graph and replayed three times, with eager products and the outputs
+    overwritten between the replays: every replay gives the eager run's bits (the split partials and their reduce
+    included), and the eager run is held to the oracle."""
+    t, q8, M, Ns, K = GRAPH_CASES[case]
+    ws = [weights(t, n, K, 0x5EED1600 + 13 * i + t) for i, n in enumerate(Ns)]
+    x = acts(0xAC701600 + M, M, K)
+    W = [be.tensor(t, (K, n), w) for n, w in zip(Ns, ws)]
+    X = be.tensor(mx.F32, (K, M), x)
+    Y = [be.tensor(mx.F32, (n, M)) for n in Ns]
+    other_w = be.tensor(t, (K, 96), weights(t, 96, K, 0x5EED1650 + t))
+    other_y = be.tensor(mx.F32, (96, M))
+    with be.options(gemm_q8_0=q8):
+        be.mul_mat_group(W, X, Y)
+        be.sync()
+        eager = [yt.numpy().reshape(M, n).copy() for n, yt in zip(Ns, Y)]
+        for w, y in zip(ws, eager):
+            check_product(t, w, x, y, K, dq=None if t != O.TYPE_Q8_0 else q8 == 2)
+        be.mul_mat(other_w, X, other_y)  # (the scratch at its largest before the recording)
+        be.graph_begin()
+        be.mul_mat_group(W, X, Y)
+        g = be.graph_end()
+        try:
+            for rep in range(3):
+                for yt, n in zip(Y, Ns):
+                    yt.set(np.full((M, n), np.nan, np.float32))
+                be.mul_mat(other_w, X, other_y)  # eager work between the replays, on the same scratch
+                be.sync()
+                be.graph_launch(g)
+                be.sync()
+                for n, yt, y in zip(Ns, Y, eager):
+                    assert bits_equal(yt.numpy().reshape(M, n), y), f"replay {rep}"
+        finally:
+            be.graph_free(g)
+
+
 @pytest.mark.parametrize("path", list(Q8_PATHS))
 @pytest.mark.parametrize("M,N,K", [(9, 100, 1024), (64, 256, 2048), (130, 333, 1024), (512, 2048, 2048),
                                    (100, 64, 6144), (650, 4500, 512), (300, 8100, 256), (520, 8200, 256)])
