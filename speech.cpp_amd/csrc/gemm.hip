@@ -34,8 +34,8 @@ constexpr int KS = 128;       // K per LDS stage
 // pair with stores it).
 __global__ __launch_bounds__(256) void k_gemm_quant_q8(const float *x, int64_t x_stride, int64_t K, int rounding,
                                                        int8_t *xq, uint16_t *xd) {
-    const int64_t m = blockIdx.y;
-    const int64_t e = (int64_t)blockIdx.x * 1024 + 4 * threadIdx.x;
+    const int64_t m = blockIdx.x;  // rows on x: grid.y holds at most 65,535
+    const int64_t e = (int64_t)blockIdx.y * 1024 + 4 * threadIdx.x;
     const bool valid = e < K;
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (valid) v = *(const float4 *)(x + m * x_stride + e);
@@ -380,7 +380,8 @@ hipError_t launch_gemm_quant(int type, int rounding, const float *x, int64_t x_s
     if (type != MX_TYPE_Q8_0) return hipErrorInvalidValue;
     int8_t *xq = (int8_t *)scratch;
     uint16_t *xd = (uint16_t *)((uint8_t *)scratch + gemm_xd_offset(M, K));
-    const dim3 grid((unsigned)((K + 1023) / 1024), (unsigned)M);
+    if (M == 0) return hipSuccess;
+    const dim3 grid((unsigned)M, (unsigned)((K + 1023) / 1024));
     hipLaunchKernelGGL(k_gemm_quant_q8, grid, dim3(256), 0, s, x, x_stride, K, rounding, xq, xd);
     return hipGetLastError();
 }

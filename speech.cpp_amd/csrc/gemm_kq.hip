@@ -25,9 +25,9 @@ constexpr int KQROW = KQS + 16;   // padded LDS row (bytes)
 // Activation rows -> Q8_K: int8 quants [M][K], fp32 d [M][K/256], fp32 sums of 32 quants [M][K/32].
 __global__ __launch_bounds__(256) void k_gemm_quant_q8k(const float *x, int64_t x_stride, int64_t K, int8_t *xq,
                                                         float *xd, float *xs32) {
-    const int64_t m = blockIdx.y;
+    const int64_t m = blockIdx.x;  // rows on x: grid.y holds at most 65,535
     const int lane = threadIdx.x & 63;
-    const int64_t sb = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t sb = (int64_t)blockIdx.y * 4 + (threadIdx.x >> 6);
     if (sb * 256 >= K) return;  // whole wave
     const float4 v = *(const float4 *)(x + m * x_stride + sb * 256 + 4 * lane);
     float d;
@@ -254,8 +254,9 @@ static KqScratch kq_scratch(void *scratch, int64_t M, int64_t K) {
 
 hipError_t launch_gemm_kq_quant(const float *x, int64_t x_stride, int64_t M, int64_t K, void *scratch, hipStream_t s) {
     if (K % 256 != 0) return hipErrorInvalidValue;
+    if (M == 0) return hipSuccess;
     const KqScratch p = kq_scratch(scratch, M, K);
-    hipLaunchKernelGGL(k_gemm_quant_q8k, dim3((unsigned)((K / 256 + 3) / 4), (unsigned)M), dim3(256), 0, s, x, x_stride,
+    hipLaunchKernelGGL(k_gemm_quant_q8k, dim3((unsigned)M, (unsigned)((K / 256 + 3) / 4)), dim3(256), 0, s, x, x_stride,
                        K, p.xq, p.xd, p.xs32);
     return hipGetLastError();
 }

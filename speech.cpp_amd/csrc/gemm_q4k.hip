@@ -55,9 +55,9 @@ __device__ __forceinline__ int h_slot(int r, int h) { return r * 32 + 16 * (h ^ 
 // [64 h_0 .. 64 h_7, l_0 .. l_7] with bsum32_j = 64 h_j + l_j (the sums of the eight sub-blocks' quants).
 __global__ __launch_bounds__(256) void k_gemm_q4k_quant(const float *x, int64_t x_stride, int K, int8_t *xq,
                                                         float *xd, _Float16 *x16) {
-    const int64_t m = blockIdx.y;
+    const int64_t m = blockIdx.x;  // rows on x: grid.y holds at most 65,535
     const int lane = threadIdx.x & 63;
-    const int sb = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int sb = blockIdx.y * 4 + (threadIdx.x >> 6);
     const int nsb = K / 256;
     if (sb >= nsb) return;  // whole wave
     const float4 v = *(const float4 *)(x + m * x_stride + (int64_t)sb * 256 + 4 * lane);
@@ -537,7 +537,7 @@ hipError_t launch_gemm_q4k_quant(const float *x, int64_t x_stride, int64_t M, in
                                  hipStream_t s) {
     if (K % 256 != 0 || M <= 0) return hipErrorInvalidValue;
     const Q4gScratch p = q4g_scratch(scratch, M, K);
-    hipLaunchKernelGGL(k_gemm_q4k_quant, dim3((unsigned)((K / 256 + 3) / 4), (unsigned)M), dim3(256), 0, s, x,
+    hipLaunchKernelGGL(k_gemm_q4k_quant, dim3((unsigned)M, (unsigned)((K / 256 + 3) / 4)), dim3(256), 0, s, x,
                        x_stride, (int)K, p.xq, p.xd, p.x16);
     return hipGetLastError();
 }

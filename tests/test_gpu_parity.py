@@ -578,6 +578,16 @@ def test_graph_replay_matches_eager(mx, be):
 Q8_PATHS = {"int8": 0, "fp16": 2}  # the Q8_0 GEMM option: as picked (the int8 GEMM), the fp16 GEMM forced
 
 
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_K, O.TYPE_Q6_K], ids=lambda t: NAMES[t])
+def test_gemm_rows_past_grid_y(mx, be, t):
+    """66,000 rows, more than a grid's y dimension holds (65,535): the activation passes put the rows on x."""
+    M, N, K = 66000, 40, 256
+    w = weights(t, N, K, 0x5EED1700 + t)
+    x = acts(0xAC701700, M, K)
+    y = run_mul_mat(mx, be, t, w, x, K, N)
+    check_product(t, w, x, y, K)
+
+
 # (type, Q8_0 option, rows, widths, K): the int8 Q8_0 GEMM split four ways (28 rows, a group) and on 64 x 128 tiles
 # unsplit (130 rows x 2 x 3000: 564 tiles of 64 x 128), the fp16 GEMM split (Q8_0 forced, Q6_K), the Q4_K GEMM
 GRAPH_CASES = {"q8_0_int8_split": (O.TYPE_Q8_0, 0, 28, [200, 64, 72], 2048),
