@@ -4,8 +4,9 @@
 // Activations are quantized once into scratch (k_gemm_quant), then each workgroup computes a BM x BN tile of Y:
 // 4 waves in a 2 x 2 arrangement, each owning (BM/2) x (BN/2) of the tile as 32 x 32 MFMA tiles. K advances in
 // stages of 128 through a ring of NS stages in LDS, filled by buffer-to-LDS copies (no registers between global
-// memory and LDS): NS - 1 stages are in flight while one is computed, which a grid of one workgroup per CU needs to
-// cover the memory latency (one stage ahead, each 128-wide stage cost a round trip).
+// memory and LDS): NS - 1 stages are in flight while one is computed, which a grid of one or two workgroups per CU
+// needs to cover the memory latency (one stage ahead, each 128-wide stage cost a round trip). The 64 x 128 tile, picked
+// only for grids of 512 workgroups or more, keeps two stages and covers the latency with three workgroups per CU.
 //
 // Per 32-element block and 32 x 32 tile: one v_mfma_i32_32x32x32_i8 (the integer sums, exact), one
 // v_mfma_f32_32x32x8_f16 whose only non-zero k is dx (x) dw -- the outer product of the two fp16 scales, exact in
@@ -26,9 +27,18 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 constexpr int KS = 128;       // K per LDS stage
-#ifndef MX_I8_NS64
-#define MX_I8_NS64 4          // ring stages of the 64 x 64 tile
-#endif
+// Per tile: ring stages, blocks whose MFMAs a wave has in flight at once, and the waves per SIMD its registers are
+// allocated for. 64 x 64: four stages (70 KB, two workgroups per CU), block kb + 1's MFMAs issued before block kb's
+// VALU. 64 x 128: two stages (52 KB) and one block at a time (162 VGPRs), so three workgroups share a CU; measured at
+// M = 512 on the ASR gate/up group (768 workgroups) 50.7 -> 46.7 us against three stages and two blocks (212 VGPRs,
+// two workgroups per CU), while the 64 x 64 tile measured slower that way (down, K = 6144: 37.3 -> 40.8 us).
+template <int BM, int BN>
+struct I8Cfg {
+    static constexpr bool WIDE = BM == 64 && BN == 128;
+    static constexpr int NS = BM == 64 && BN == 64 ? 4 : (WIDE ? 2 : 3);
+    static constexpr int PD = BM == 64 && BN == 64 ? 2 : 1;
+    static constexpr int WPE = WIDE ? 3 : 2;
+};
 
 // Activation rows -> int8 quants [M][K], fp16 block scales [M][K/32] (d rounded to fp16, as the Q8_0 the weights
 // pair with stores it).
@@ -97,7 +107,7 @@ typedef __attribute__((address_space(3))) void i8_lds_void;
 // c ^ i8_swz(r): the 16 rows one fragment read visits at a time fall on 16 distinct 16-byte bank groups.
 template <int BM, int BN>
 struct I8Lds {
-    static constexpr int NS = BM == 64 && BN == 64 ? MX_I8_NS64 : 3;
+    static constexpr int NS = I8Cfg<BM, BN>::NS;
     static constexpr int SA = BM * KS, SB = BN * KS, SDX = BM * 8, SDW = BN * 8;  // slot sizes (bytes)
     static constexpr int A = 0, B = A + NS * SA, DX = B + NS * SB, DW = DX + NS * SDX, SIZE = DW + NS * SDW;
     // copies per stage and wave: 16-byte ones of 8 quant rows each; 4-byte ones of 32 scale rows each, shared by the
@@ -105,6 +115,7 @@ struct I8Lds {
     static constexpr int QA = BM / 32, QB = BN / 32, NDX = BM / 32, NSC = (BM + BN) / 32, QS = (NSC + 3) / 4;
     static constexpr int OPS = QA + QB + QS;
     static_assert(SIZE <= 80 * 1024 || (BM == 128 && BN == 128), "two workgroups per CU");
+    static_assert(NS >= 2, "a ring of two stages or more");
 };
 
 __device__ __forceinline__ int i8_swz(int r) { return (r >> 1) & 7; }
@@ -186,7 +197,8 @@ struct I8Dma {
 
 // 32 x 32 accumulator layout of the 32x32 MFMAs: lane l, register r holds (row 8*(r/4) + 4*(l/32) + r%4, col l%32).
 template <int BM, int BN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) void k_gemm_q8_0_i8(GemmArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, I8Cfg<BM, BN>::WPE))) void k_gemm_q8_0_i8(
+    GemmArgs a) {
     using L = I8Lds<BM, BN>;
     constexpr int WM = BM / 2, WN = BN / 2;   // wave tile
     constexpr int TM = WM / 32, TN = WN / 32; // MFMA tiles per wave
@@ -280,9 +292,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
             for (int kb = 0; kb < 4; kb++) bf[kb][j] = *(const v4i *)(sb + boff[j][kb]);
         }
-        // block kb's integer sums and scale products; with few tiles per wave, block kb + 1's MFMAs are issued
-        // before block kb's conversions and fmas, so the matrix cores and the VALU overlap within the wave
-        constexpr int PD = TM * TN <= 2 ? 2 : 1;
+        // block kb's integer sums and scale products; with PD = 2 block kb + 1's MFMAs are issued before block kb's
+        // conversions and fmas, so the matrix cores and the VALU overlap within the wave
+        constexpr int PD = I8Cfg<BM, BN>::PD;
         v16i S[PD][TM][TN];
         v16f C[PD][TM][TN];
         auto mfma = [&](int kb, int d) {
