@@ -278,6 +278,25 @@ def test_mul_mat_x86_rounding(mx, be, t):
     assert rel_err(y, O.mul_mat(t, w, x, rounding=O.ROUND_X86)) <= TIGHT
 
 
+@pytest.mark.parametrize("path", ["int8", "fp16"])
+def test_gemm_q8_0_x86_rounding(mx, be, path):
+    """The x86 activation rounding (rint of x * 127 / amax) through both Q8_0 GEMMs, 40 rows with a special row:
+    the int8 GEMM to TIGHT of the oracle under the same rounding, the fp16 one to its model of that rounding."""
+    t, K, N = O.TYPE_Q8_0, 512, 200
+    w = weights(t, N, K, 0x5EED0610)
+    x = np.concatenate([acts(0xAC700610, 39, K), special_rows(K)[2:3]])
+    be.set_rounding(mx.ROUND_X86)
+    try:
+        with be.options(gemm_q8_0=Q8_PATHS[path]):
+            y = run_mul_mat(mx, be, t, w, x, K, N)
+    finally:
+        be.set_rounding(mx.ROUND_REF)
+    check_product(t, w, x, y, K, rounding=O.ROUND_X86, dq=path == "fp16")
+    # the REF rounding gives other quants for this row set: a kernel that ignored the mode would miss
+    y_ref = O.mul_mat(t, w, x, rounding=O.ROUND_REF)
+    assert not np.array_equal(O.mul_mat(t, w, x, rounding=O.ROUND_X86), y_ref)
+
+
 @pytest.mark.parametrize("t", QTYPES, ids=lambda t: NAMES[t])
 def test_mul_mat_batched_broadcast(mx, be, t):
     # src0 [K, N, 2, 1], src1 [K, M, 4, 2]: r2 = 2, r3 = 2 (ggml broadcast of src0 over src1's batch axes)
@@ -636,12 +655,14 @@ def test_gemm_graph_replays(mx, be, case):
 
 @pytest.mark.parametrize("path", list(Q8_PATHS))
 @pytest.mark.parametrize("M,N,K", [(9, 100, 1024), (64, 256, 2048), (130, 333, 1024), (512, 2048, 2048),
-                                   (100, 64, 6144), (650, 4500, 512), (300, 8100, 256), (520, 8200, 256)])
+                                   (100, 64, 6144), (650, 4500, 512), (300, 8100, 256), (520, 8200, 256),
+                                   (200, 300, 1152)])
 def test_mul_mat_gemm_q8_0(mx, be, M, N, K, path):
-    """Both Q8_0 GEMMs. Short blocks split K (9 and 64 rows; 100 rows over K = 6144); on the fp16 GEMM the last three
-    take 128 x 128 tiles unsplit with ragged rows and columns (216, 192 and 325 workgroups: the last more than the
-    CUs); the last two have two (K = 256) and four (K = 512) stages of K, fewer than the int8 GEMM's copy ring holds
-    and one more than the fp16 GEMM's."""
+    """Both Q8_0 GEMMs. Short blocks split K (9 and 64 rows; 100 rows over K = 6144); on the fp16 GEMM three take
+    128 x 128 tiles unsplit with ragged rows and columns (216, 192 and 325 workgroups: the last more than the CUs);
+    K = 256 and 512 have two and four stages of 128, fewer than the int8 GEMM's 64 x 64 copy ring holds; K = 1152 ends
+    one 128-wide stage past a 1024-element piece of the activation pass; 520 x 8200 takes the int8 GEMM's 64 x 128
+    tile (585 of them: its two-stage ring)."""
     t = O.TYPE_Q8_0
     w = weights(t, N, K, 0x5EED0A00 + M + N)
     x = acts(0xAC700A00 + M, M, K)

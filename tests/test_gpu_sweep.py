@@ -1,6 +1,6 @@
 """A seeded sweep of product shapes across the dispatcher's boundaries, every weight type, through the C ABI on
 device 0: MUL_MAT at row counts either side of the mat-vec / GEMM switch (8 | 9) and the short-block tile (32 | 33),
-K with and without the GEMMs' multiples (Q8_0 K % 64), ragged N; MUL_MAT_ID with pair counts either side of the
+K with and without the GEMMs' multiples (Q8_0 K % 64 for the fp16 GEMM, K % 128 for the int8 one), ragged N; MUL_MAT_ID with pair counts either side of the
 mat-vec launch (16) and of the fp16 GEMM's per-expert thresholds (one pair per expert for Q8_0, three for the
 K-quants), b broadcast and per slot. Each case is held to its path's bar (test_gpu_parity.py): the integer paths to
 2e-5 of the oracle, the fp16 dequantizing GEMM to 1e-3 of it and to 2e-5 of a model of its roundings. A product of
