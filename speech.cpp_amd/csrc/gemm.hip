@@ -99,8 +99,6 @@ __device__ __forceinline__ _Float16 as_half(uint16_t b) {
     return h;
 }
 
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void i8_lds_void;
 
 // The LDS ring: NS stages, each of A (BM rows of 128 quants), B (BN rows), and the four fp16 block scales of each
 // activation row (DX) and weight row (DW). Quant rows are stored as 8 chunks of 16 bytes, chunk c of row r at slot
@@ -120,27 +118,6 @@ struct I8Lds {
 
 __device__ __forceinline__ int i8_swz(int r) { return (r >> 1) & 7; }
 
-__device__ __forceinline__ v4u i8_rsrc(const void *base, uint32_t bytes) {
-    const uint64_t b = (uint64_t)(uintptr_t)base;
-    return v4u{(uint32_t)b, (uint32_t)(b >> 32), bytes, 0x00020000u};
-}
-
-// Buffer-to-LDS copies (each lane's 16 or 4 bytes land at m0 + 16 or 4 x lane), issued through asm so that the
-// compiler does not count them as LDS stores that every later LDS read may alias (it would wait for all of them);
-// their waits are the explicit ones below.
-__device__ __forceinline__ void i8_dma16(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void i8_dma4(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
-                 : "memory", "m0");
-}
-template <int n>
-__device__ __forceinline__ void i8_wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
-}
-
 // One wave's copies of a stage: per-lane byte offsets fixed for the whole K loop (rows past M or N clamped to the
 // last row), a per-stage uniform offset (k0 bytes of quants, k0 / 16 bytes of scales per row).
 template <int BM, int BN>
@@ -153,9 +130,9 @@ struct I8Dma {
     __device__ __forceinline__ void init(int wave, const GemmArgs &g, const GemmProblem &pb, int64_t m0, int64_t n0) {
         const int lane = threadIdx.x & 63;
         const uint32_t K = (uint32_t)g.K, nblk = K / 32, M = (uint32_t)g.M, N = (uint32_t)pb.N;
-        ra = i8_rsrc(g.xq, M * K);
-        rb = i8_rsrc(pb.w.p0, N * K);
-        const v4u rdx = i8_rsrc(g.xd, M * nblk * 2), rdw = i8_rsrc(pb.w.p1, N * nblk * 2);
+        ra = buf_rsrc(g.xq, M * K);
+        rb = buf_rsrc(pb.w.p0, N * K);
+        const v4u rdx = buf_rsrc(g.xd, M * nblk * 2), rdw = buf_rsrc(pb.w.p1, N * nblk * 2);
 #pragma unroll
         for (int q = 0; q < L::QA; q++) {
             const int r = 8 * (wave * L::QA + q) + (lane >> 3);
@@ -184,13 +161,13 @@ struct I8Dma {
     __device__ __forceinline__ void issue(uint32_t lds, int slot, int k0) const {
         const uint32_t sa = lds + L::A + slot * L::SA + la, sb = lds + L::B + slot * L::SB + lb;
 #pragma unroll
-        for (int q = 0; q < L::QA; q++) i8_dma16(ra, sa + 1024u * q, a[q], (uint32_t)k0);
+        for (int q = 0; q < L::QA; q++) dma16_lds(ra, sa + 1024u * q, a[q], (uint32_t)k0);
 #pragma unroll
-        for (int q = 0; q < L::QB; q++) i8_dma16(rb, sb + 1024u * q, b[q], (uint32_t)k0);
+        for (int q = 0; q < L::QB; q++) dma16_lds(rb, sb + 1024u * q, b[q], (uint32_t)k0);
 #pragma unroll
         for (int u = 0; u < L::QS; u++) {
             const uint32_t sl = ls[u] < (uint32_t)L::DW ? (uint32_t)(slot * L::SDX) : (uint32_t)(slot * L::SDW);
-            i8_dma4(rs[u], lds + ls[u] + sl, s[u], (uint32_t)(k0 / 16));
+            dma4_lds(rs[u], lds + ls[u] + sl, s[u], (uint32_t)(k0 / 16));
         }
     }
 };
@@ -203,7 +180,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, I8Cfg<BM
     constexpr int WM = BM / 2, WN = BN / 2;   // wave tile
     constexpr int TM = WM / 32, TN = WN / 32; // MFMA tiles per wave
     extern __shared__ __align__(16) uint8_t smem[];
-    const uint32_t lds = (uint32_t)(uintptr_t)(i8_lds_void *)smem;
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_void *)smem;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -269,9 +246,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, I8Cfg<BM
         // every wave's, and every wave has read the slot the next copies overwrite. The barrier is the bare
         // instruction: __syncthreads' release fence would wait for the copies still in flight too.
         const int rem = nloc - 1 - s;  // stages issued after s: min(rem, NS - 2)
-        if (rem >= L::NS - 2) i8_wait_vm<(L::NS - 2) * L::OPS>();
-        else if (L::NS > 3 && rem == 1) i8_wait_vm<L::OPS>();
-        else i8_wait_vm<0>();
+        if (rem >= L::NS - 2) wait_vm<(L::NS - 2) * L::OPS>();
+        else if (L::NS > 3 && rem == 1) wait_vm<L::OPS>();
+        else wait_vm<0>();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         if (s + L::NS - 1 < nloc) dma.issue(lds, (s + L::NS - 1) % L::NS, kb0 + (s + L::NS - 1) * KS);
         const int slot = s % L::NS;

@@ -37,7 +37,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void dq_lds;
 
 #ifndef MX_DQ_WGN128
 #define MX_DQ_WGN128 4  // waves across N in a 128 x 128 tile (4: 64 x 32 per wave; 2: 64 x 64)
@@ -144,12 +143,6 @@ struct DqArgs {
     int64_t y_nb1, y_nb2;
 };
 
-__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(dq_lds *)p; }
-
-template <int n>
-__device__ __forceinline__ void dq_wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
-}
 
 constexpr int DQ_ACT_NT = 1024;  // threads of an activation-pass workgroup (one row)
 
@@ -552,7 +545,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
 #pragma unroll
         for (int jj = 0; jj < L::PA; jj++) {
             const uint32_t d = adst[jj] + (adst[jj] < (uint32_t)L::JUNK ? slot * BM * 128 : 0);
-            __builtin_amdgcn_global_load_lds((const void *)(asrc[jj] + t * DQ_KS), (dq_lds *)(smem + d), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(asrc[jj] + t * DQ_KS), (lds_void *)(smem + d), 16, 0, 0);
         }
         // K-quants: stage g is quarter g & 3 of super-block g >> 2. Q6_K: both quarters of a half read the half's ql
         // and qh; Q5_K: the quarter's 32 qs bytes and the super-block's 32 qh bytes
@@ -563,7 +556,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
 #pragma unroll
             for (int jj = 0; jj < L::PC; jj++) {
                 const uint32_t d = cdst[jj] + (cdst[jj] < (uint32_t)L::JUNK ? rslot * BN * L::RB : 0);
-                __builtin_amdgcn_global_load_lds((const void *)(csrc[jj] + coff), (dq_lds *)(smem + d), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void *)(csrc[jj] + coff), (lds_void *)(smem + d), 16, 0, 0);
             }
         }
         if (!L::SH_QH || sh) {
@@ -571,7 +564,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             for (int jj = 0; jj < L::PH; jj++) {
                 const uint32_t d = hdst[jj] + (hdst[jj] < (uint32_t)L::JUNK ? qslot * BN * L::HB : 0);
                 const int hoff = L::K5 ? (g >> 2) * 32 : (g >> 2) * 64 + ((g >> 1) & 1) * 32;
-                __builtin_amdgcn_global_load_lds((const void *)(hsrc[jj] + hoff), (dq_lds *)(smem + d), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void *)(hsrc[jj] + hoff), (lds_void *)(smem + d), 16, 0, 0);
             }
         }
         const int soff = L::K6 ? (g >> 2) * 16 + (g & 3) * 4 : L::K5 ? (g >> 2) * 12 : t * 4;
@@ -579,7 +572,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
 #pragma unroll
             for (int jj = 0; jj < L::PS; jj++) {
                 const uint32_t d = sdst[jj] + (sdst[jj] < (uint32_t)L::JUNK ? sslot * BN * L::SB : 0);
-                __builtin_amdgcn_global_load_lds((const void *)(ssrc[jj] + soff), (dq_lds *)(smem + d), 4, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void *)(ssrc[jj] + soff), (lds_void *)(smem + d), 4, 0, 0);
             }
         }
         // d: the 4-byte-aligned pair of fp16 d holding this row's (which half: convert). When the plane holds an odd
@@ -591,7 +584,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
                 const uint32_t d = ddst[jj] + (ddst[jj] < (uint32_t)L::JUNK ? dslot * BN * 4 : 0);
                 const int64_t e = dsb[jj] + (g >> 2);
                 const uint8_t *src = L::K5 ? p.w.p3 + e * 4 : p.w.p3 + (e >> 1) * 4;
-                __builtin_amdgcn_global_load_lds((const void *)src, (dq_lds *)(smem + d), 4, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void *)src, (lds_void *)(smem + d), 4, 0, 0);
             }
         }
         return sh;
@@ -706,7 +699,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
 #pragma unroll
     for (int t = 0; t < L::NS - 1; t++) plast = issue(t);
     if constexpr (!L::DIRB) {
-        dq_wait_vm<(L::NS - 2) * L::OPS>();  // stage 0 landed (this wave's copies)
+        wait_vm<(L::NS - 2) * L::OPS>();  // stage 0 landed (this wave's copies)
         if (tid < BM) {  // read by the epilogue
             *(float *)(smem + L::RS + 4 * tid) = rs_row;
             if constexpr (RT) *(int64_t *)(smem + L::YO + 8 * tid) = yo_row;
@@ -765,8 +758,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
             // then every wave's. The barrier is the bare instruction: __syncthreads' release fence would wait for
             // every copy in flight (the next stages' too) wherever the compiler can see them pending.
             // (the latest issue, of stage s + 1, copied the shared bytes too or not)
-            if (L::SHARED && !plast) dq_wait_vm<(L::NS - 2) * L::OPS1>();
-            else dq_wait_vm<(L::NS - 2) * L::OPS>();
+            if (L::SHARED && !plast) wait_vm<(L::NS - 2) * L::OPS1>();
+            else wait_vm<(L::NS - 2) * L::OPS>();
             asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             // this stage's code, qh, scale and d addresses
             const uint32_t hsl = (uint32_t)((sb + s) / L::SHP) & 1u;  // the shared bytes' slot
@@ -863,7 +856,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
     for (int s = 0; s < nst; s++) {
         // this wave's copies of A(s) and of the raw weights of stage s + 1 (direct B: of stage s) have landed, and its
         // LDS writes are done
-        dq_wait_vm<(L::NS - 3) * L::OPS>();
+        wait_vm<(L::NS - 3) * L::OPS>();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
         {
@@ -896,7 +889,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_dq(DqArgs a) {
         }
     }
     }
-    dq_wait_vm<0>();  // the copies of the stages past the end
+    wait_vm<0>();  // the copies of the stages past the end
 
     // 32 x 32 accumulator layout: lane l, register r holds (row 8 (r / 4) + 4 (l / 32) + r % 4, col l % 32)
     float *y = p.y;

@@ -35,7 +35,6 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
-typedef __attribute__((address_space(3))) void lds_void;
 
 // LDS rows are unpadded and 16-byte chunks are XOR-swizzled so that the MFMA fragment reads (32 rows, one chunk
 // each) meet distinct banks whether the LDS serves 128 or 256 bytes a clock (8 or 16 lanes of a ds_read_b128):
@@ -119,28 +118,6 @@ struct Q4gT {
     static_assert(LDS <= 160 * 1024, "LDS of one workgroup");
 };
 
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-
-// A buffer descriptor for raw dword loads: base, no stride, `bytes` records (reads past them return zeros), format
-// word as the buffer-resource builtin makes it for these loads.
-__device__ __forceinline__ v4u q4g_rsrc(const void *base, uint32_t bytes) {
-    const uint64_t b = (uint64_t)(uintptr_t)base;
-    return v4u{(uint32_t)b, (uint32_t)(b >> 32), bytes, 0x00020000u};
-}
-__device__ __forceinline__ uint32_t q4g_lds(const void *p) { return (uint32_t)(uintptr_t)(const lds_void *)p; }
-
-// Buffer-to-LDS copies (each lane's 16 or 4 bytes land at m0 + 16 or 4 x lane) issued through asm: issued as the
-// builtin, the compiler counts them as LDS stores that every later LDS read may alias, and waits for all of them
-// (the next stage's and the one after) before the first fragment read of a step. Their waits are counted here.
-__device__ __forceinline__ void q4g_dma16(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ void q4g_dma4(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
-                 : "memory", "m0");
-}
-
 // One workgroup's global -> LDS copies through buffer loads (buffer_load_dword* ... lds): a per-lane byte offset
 // fixed for the whole K loop and a per-stage uniform offset (sb times the per-block stride of each source: 256 B of
 // quants, 32 B of [64 h | l], 4 B of d per activation row; 128 code bytes per weight row). The waves share the
@@ -155,10 +132,10 @@ struct Q4gDma {
     __device__ __forceinline__ void init(int wave, const int8_t *xq, const _Float16 *x16, const float *xd,
                                          const uint8_t *qs, int m0, int n0, int M, int N, int K, int nsb) {
         const int lane = threadIdx.x & 63;
-        ra = q4g_rsrc(xq, (uint32_t)(M * K));
-        rb = q4g_rsrc(qs, (uint32_t)(N * nsb * 128));
-        r16 = q4g_rsrc(x16, (uint32_t)(M * nsb * 32));
-        rdx = q4g_rsrc(xd, (uint32_t)(M * nsb * 4));
+        ra = buf_rsrc(xq, (uint32_t)(M * K));
+        rb = buf_rsrc(qs, (uint32_t)(N * nsb * 128));
+        r16 = buf_rsrc(x16, (uint32_t)(M * nsb * 32));
+        rdx = buf_rsrc(xd, (uint32_t)(M * nsb * 4));
 #pragma unroll
         for (int q = 0; q < Q::QA; q++) {
             const int r = 4 * (wave * Q::QA + q) + (lane >> 4), cs = lane & 15;
@@ -180,13 +157,13 @@ struct Q4gDma {
     // instructions per wave) are issued on their own, last of a step's copies.
     __device__ __forceinline__ void issue_b(uint8_t *opb, int wave, int sb) const {
 #pragma unroll
-        for (int q = 0; q < Q::QB; q++) q4g_dma16(rb, q4g_lds(opb + Q::B + 1024 * (wave * Q::QB + q)), b[q], sb * 128);
+        for (int q = 0; q < Q::QB; q++) dma16_lds(rb, lds_addr(opb + Q::B + 1024 * (wave * Q::QB + q)), b[q], sb * 128);
     }
     __device__ __forceinline__ void issue_a(uint8_t *opa, uint8_t *ep, int wave, int sb) const {
 #pragma unroll
-        for (int q = 0; q < Q::QA; q++) q4g_dma16(ra, q4g_lds(opa + Q::A + 1024 * (wave * Q::QA + q)), a[q], sb * 256);
-        if (wave < Q::NA16) q4g_dma16(r16, q4g_lds(ep + Q::A16 + 1024 * wave), a16, sb * 32);  // uniform
-        if (wave < Q::NDX) q4g_dma4(rdx, q4g_lds(ep + Q::ADX + 256 * wave), dx, sb * 4);        // uniform
+        for (int q = 0; q < Q::QA; q++) dma16_lds(ra, lds_addr(opa + Q::A + 1024 * (wave * Q::QA + q)), a[q], sb * 256);
+        if (wave < Q::NA16) dma16_lds(r16, lds_addr(ep + Q::A16 + 1024 * wave), a16, sb * 32);  // uniform
+        if (wave < Q::NDX) dma4_lds(rdx, lds_addr(ep + Q::ADX + 256 * wave), dx, sb * 4);        // uniform
     }
 };
 

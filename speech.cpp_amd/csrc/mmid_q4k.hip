@@ -45,14 +45,7 @@ static_assert(MMID_CHUNK == 32 && MMID_CHUNK_SMALL == 16, "a chunk is one or two
 
 constexpr int MQ_STAGE = 2304;  // one stage: 16 columns x (128 code bytes + 12 scale bytes + d | dmin)
 
-typedef __attribute__((address_space(3))) void mq_lds;
 
-// Waits until at most n vector memory ops of this wave are outstanding. The memory clobber keeps the compiler from
-// moving loads and stores across it, so the LDS reads that follow see the copies it waited for.
-template <int n>
-__device__ __forceinline__ void mq_wait_vm() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
-}
 // Keeps the memory ops before it ahead of the ones after it (the wait counts depend on their issue order).
 __device__ __forceinline__ void mq_order() { asm volatile("" ::: "memory"); }
 
@@ -108,7 +101,7 @@ template <typename Map>
 __device__ __forceinline__ void mq_seg_store(const MqSeg &r, uint8_t *smem, int seg, int nsb) {
     const int g = threadIdx.x >> 8, u = threadIdx.x & 255, fr = u & 15;
     const int n = min(MQ_KSEG, nsb - MQ_KSEG * seg);
-    const uint32_t base = (uint32_t)(uintptr_t)(mq_lds *)smem;
+    const uint32_t base = (uint32_t)(uintptr_t)(lds_void *)smem;
 #pragma unroll
     for (int i = 0; i < MQ_KSEG; i++)
         if (i < n)
@@ -144,9 +137,9 @@ __device__ __forceinline__ void mq_seek(const MqLane &c, MqCursor &k, int cb) {
 template <int SLOT>
 __device__ __forceinline__ void mq_copy(const MqLane &c, MqCursor &k, int ncb) {
     uint8_t *st = c.ring + SLOT * MQ_STAGE;
-    __builtin_amdgcn_global_load_lds((const void *)(k.qcb + k.sb * 128), (mq_lds *)st, 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const void *)(k.qcb + k.sb * 128 + 16), (mq_lds *)(st + 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const void *)(k.scb + k.sb * c.sstride), (mq_lds *)(st + 2048), 4, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void *)(k.qcb + k.sb * 128), (lds_void *)st, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void *)(k.qcb + k.sb * 128 + 16), (lds_void *)(st + 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void *)(k.scb + k.sb * c.sstride), (lds_void *)(st + 2048), 4, 0, 0);
     if (k.sb + 1 < c.nsb) {
         k.sb++;
     } else if (k.cb + 1 < ncb) {
@@ -162,7 +155,7 @@ __device__ __forceinline__ void mq_copy(const MqLane &c, MqCursor &k, int ncb) {
 template <typename Map, int S, int SLOT, int NG>
 __device__ __forceinline__ void mq_step(const MqLane &c, MqCursor &k, int ncb, int sbl, float (&acc)[NG][4]) {
     mq_copy<(SLOT + S - 1) % S>(c, k, ncb);
-    mq_wait_vm<3 * (S - 1)>();
+    wait_vm<3 * (S - 1)>();
     const uint32_t st = c.ring_lds + SLOT * MQ_STAGE;
     const uint32_t aq = c.a_lds + Map::AQ - Map::RING + sbl * Map::AQ_SB + 16 * c.lane;
     const uint32_t a16 = c.a_lds + Map::A16 - Map::RING + sbl * Map::A16_SB + 32 * c.fr + 8 * c.grp;
@@ -336,7 +329,7 @@ __device__ __forceinline__ void mq_run(const MulMatIdArgs &a, MqLane &c, uint8_t
     };
 #pragma unroll 1
     for (int it = 0; it < c.nsteps; it += S) mq_turn<Map, S, 0, NG>(c, k, ncb, it, sb, acc, finish);
-    mq_wait_vm<0>();  // no copy may still be landing in LDS when the workgroup ends
+    wait_vm<0>();  // no copy may still be landing in LDS when the workgroup ends
 }
 
 // Grid: one workgroup per CU. The work is nprob x ntiles x nblk units (a product, a chunk and one block of MQ_COLS
@@ -386,8 +379,8 @@ __global__ __launch_bounds__(64 * MQ_W) void k_mmid_q4k(MulMatIdArgs a) {
         c.sstride = sw < 3 ? 12 : 4;
         c.se = sw < 3 ? w.p1 + eblk * 12 + 4 * sw : w.p2 + eblk * 4;
         c.ring = smem + wave * S * MQ_STAGE;
-        c.ring_lds = (uint32_t)(uintptr_t)(mq_lds *)c.ring;
-        c.a_lds = (uint32_t)(uintptr_t)(mq_lds *)(smem + Map::RING);
+        c.ring_lds = (uint32_t)(uintptr_t)(lds_void *)c.ring;
+        c.a_lds = (uint32_t)(uintptr_t)(lds_void *)(smem + Map::RING);
         if (NGMAX > 1 && cnt > 16) mq_run<Map, S, NGMAX>(a, c, smem, p0, cnt, ncb, dst);
         else mq_run<Map, S, 1>(a, c, smem, p0, cnt, ncb, dst);
         u += ncb;

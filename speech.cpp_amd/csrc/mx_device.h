@@ -53,6 +53,41 @@ __device__ __forceinline__ float sum_lanes(float v) {
     return v;
 }
 
+// ------------------------------------------------------------------------------------------------------------------
+// Buffer-to-LDS copies and their waits (the prefill GEMMs' and the MoE product's operand rings).
+// ------------------------------------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+// The LDS address of a pointer into the workgroup's shared memory.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) { return (uint32_t)(uintptr_t)(const lds_void *)p; }
+
+// A buffer descriptor for raw dword loads: base, no stride, `bytes` records (reads past them return zeros), format
+// word as the buffer-resource builtin makes it for these loads.
+__device__ __forceinline__ v4u buf_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    return v4u{(uint32_t)b, (uint32_t)(b >> 32), bytes, 0x00020000u};
+}
+
+// Buffer-to-LDS copies (each lane's 16 or 4 bytes land at m0 + 16 or 4 x lane), issued through asm: issued as the
+// builtin, the compiler counts them as LDS stores that every later LDS read may alias, and waits for all of them
+// (the next stages' too) before the first fragment read of a stage. Their waits are counted by the caller (wait_vm).
+__device__ __forceinline__ void dma16_lds(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void dma4_lds(v4u r, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds" ::"s"(lds), "v"(voff), "s"(r), "s"(soff)
+                 : "memory", "m0");
+}
+
+// Waits until at most n vector memory ops of this wave are outstanding. The memory clobber keeps the compiler from
+// moving loads and stores across it, so the LDS reads that follow see the copies it waited for.
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
+}
+
 __device__ __forceinline__ int pack4(int a, int b, int c, int d) {
     return (a & 0xFF) | ((b & 0xFF) << 8) | ((c & 0xFF) << 16) | ((int)((unsigned)d << 24));
 }
