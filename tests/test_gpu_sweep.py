@@ -68,3 +68,31 @@ def test_mul_mat_id_shape_sweep(mx, be, t):
         n_ids = min(n_ids, E)
         y, ref = mmid_case(mx, be, t, E=E, K=K, N=N, n_ids=n_ids, T=T, bcast=bool(b), seed=0x5EED7300 + 31 * i + t)
         ref.check(y, f"draw {i}: E {E} n_ids {n_ids} T {T} N {N} K {K} b {'broadcast' if b else 'per slot'}")
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_int8_q8_0_gemm_group_sweep(mx, be, seed):
+    """The int8 Q8_0 GEMM (the default for Q8_0 at M > 8, K % 128 == 0) over seeded groups: one to four weights of
+    ragged widths sharing the activations, M from 9 to 600, K from one 128-wide stage to 48, at the picked tile and
+    split and at a forced split; every output to TIGHT of the oracle's exact block sums."""
+    rng = np.random.default_rng(0x5EED7400 + seed)
+    t = O.TYPE_Q8_0
+    for i in range(4):
+        M = int(rng.choice([9, 17, 33, 64, 100, 200, 600]))
+        K = 128 * int(rng.choice([1, 2, 5, 8, 16, 48]))
+        Ns = [int(rng.integers(1, 700)) for _ in range(int(rng.integers(1, 5)))]
+        split = int(rng.choice([0, 0, 2, 3, 7]))
+        ws = [weights(t, n, K, 0x5EED7500 + 97 * seed + 13 * i + j) for j, n in enumerate(Ns)]
+        x = acts(0xAC707500 + 97 * seed + i, M, K)
+        W = [be.tensor(t, (K, n), w) for n, w in zip(Ns, ws)]
+        X = be.tensor(mx.F32, (K, M), x)
+        Y = [be.tensor(mx.F32, (n, M)) for n in Ns]
+        with be.options(split=split):
+            be.mul_mat_group(W, X, Y)
+            be.sync()
+        for n, w, yt in zip(Ns, ws, Y):
+            y = yt.numpy().reshape(M, n)
+            try:
+                (check_product if n >= 32 else check_narrow)(t, w, x, y, K)
+            except AssertionError as e:
+                raise AssertionError(f"draw {i}: M {M} widths {Ns} K {K} split {split}") from e
