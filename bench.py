@@ -1201,6 +1201,8 @@ def main():
                     help="moe: token batches (default 1,16,256; counter passes use 256)")
     ap.add_argument("--opt", action="append", default=[], metavar="NAME=VALUE",
                     help="a kernel choice of the backend (mx_backend_set_option), e.g. gemm_q8_0=2; repeatable")
+    ap.add_argument("--pmc-kernel", default=None,
+                    help="with --summarize-pmc: the kernel-name substring to sum (default: the workload's own)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="print the traffic summary of two rocprofv3 --pmc runs of --workload's benchmark and exit")
     ap.add_argument("--summarize-busy", nargs=2, metavar=("GRBM_CSV", "CLOCK_MHZ"),
@@ -1208,7 +1210,7 @@ def main():
                          "benchmark at the given shader clock and exit")
     args = ap.parse_args()
     if args.summarize_pmc:
-        print(summarize_pmc(*args.summarize_pmc, TRAFFIC[args.workload][1]))
+        print(summarize_pmc(*args.summarize_pmc, args.pmc_kernel or TRAFFIC[args.workload][1]))
         return
     if args.summarize_busy:
         print(summarize_busy(args.summarize_busy[0], TRAFFIC[args.workload][1], float(args.summarize_busy[1])))
